@@ -1,0 +1,251 @@
+/*
+ * kq_hip.h — C ABI of the MI355X (gfx950) backend for Kestrel-Q's
+ * quantized-weight path: GGUF block dequantization (Q4_K, Q6_K, Q8_0) fused
+ * into matrix-vector products, the MoE expert FFN and the LM head.
+ *
+ * Conventions (same as the reference library):
+ *  - every entry point returns kq_status and fills the optional
+ *    kq_diagnostic (include/kq_status.h);
+ *  - arguments are validated before any device work is enqueued and bad
+ *    arguments fail closed with the reference's status codes;
+ *  - the caller owns every buffer, including device scratch.
+ * Device pointers are plain `void *` / `float *` obtained from
+ * kq_hip_malloc (or any allocation on the context's device); packed weights
+ * are byte-identical GGUF blocks (kq_tensor_view_physical_data). Weight and
+ * activation pointers must be 16-byte aligned.
+ *
+ * Execution: work is enqueued on the context's stream. In the default
+ * synchronous mode each call waits for its work and reports device-detected
+ * failures (non-finite block scales -> KQ_STATUS_MALFORMED_QUANTIZED_DATA,
+ * non-finite inputs/results -> KQ_STATUS_NUMERIC_DOMAIN). In asynchronous
+ * mode calls return after enqueueing and kq_hip_context_synchronize reports
+ * them. Device outputs of a call that fails are unspecified (the reference
+ * stages host outputs and commits on success; device results are written in
+ * place and the status tells the caller not to use them).
+ */
+#ifndef KQ_HIP_H
+#define KQ_HIP_H
+
+#include <stdint.h>
+
+#include "kq_status.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor type ids (include/kq_gguf.h:15-23; Q6_K = 14, the GGML id). */
+#define KQ_HIP_TYPE_F32 0U
+#define KQ_HIP_TYPE_Q8_0 8U
+#define KQ_HIP_TYPE_Q4_K 12U
+#define KQ_HIP_TYPE_Q6_K 14U
+
+typedef struct kq_hip_context kq_hip_context;
+
+/* ------------------------------------------------------------------ */
+/* Context, stream and memory. The reference has no device runtime; its
+ * only device entry point is `int kq_cuda_smoke(void)` (include/kq_cuda.h:9). */
+
+kq_status kq_hip_context_create(int device, kq_hip_context **out_context,
+                                kq_diagnostic *diagnostic);
+void kq_hip_context_destroy(kq_hip_context *context);
+/* 0 = synchronous (default), 1 = asynchronous. */
+kq_status kq_hip_context_set_async(kq_hip_context *context, int async,
+                                   kq_diagnostic *diagnostic);
+/* Waits for enqueued work; reports and clears device-detected failures. */
+kq_status kq_hip_context_synchronize(kq_hip_context *context,
+                                     kq_diagnostic *diagnostic);
+/* The hipStream_t the context enqueues on (as an opaque pointer). */
+void *kq_hip_context_stream(const kq_hip_context *context);
+
+kq_status kq_hip_malloc(kq_hip_context *context, uint64_t bytes,
+                        void **out_device_ptr, kq_diagnostic *diagnostic);
+void kq_hip_free(kq_hip_context *context, void *device_ptr);
+kq_status kq_hip_upload(kq_hip_context *context, void *device_dst,
+                        const void *host_src, uint64_t bytes,
+                        kq_diagnostic *diagnostic);
+kq_status kq_hip_download(kq_hip_context *context, void *host_dst,
+                          const void *device_src, uint64_t bytes,
+                          kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* Quant geometry (host only).
+ * Replaces kq_quant_geometry_for_type / kq_quant_packed_size
+ * (include/kq_tensor_view.h:85-92, src/kq_tensor_view.c:44-108). */
+
+typedef struct kq_hip_quant_geometry {
+    uint32_t type_id;
+    uint64_t block_elements;
+    uint64_t bytes_per_block;
+} kq_hip_quant_geometry;
+
+kq_status kq_hip_quant_geometry_for_type(uint32_t type_id,
+                                         kq_hip_quant_geometry *out_geometry,
+                                         kq_diagnostic *diagnostic);
+kq_status kq_hip_quant_packed_size(uint32_t type_id, uint64_t element_count,
+                                   uint64_t *out_packed_bytes,
+                                   kq_diagnostic *diagnostic);
+/* Byte span of expert `expert_id` in a contiguous [experts][rows][cols]
+ * packed stack. Replaces the member addressing of
+ * kq_tensor_view_open_expert_member (src/kq_tensor_view.c:664-807). */
+kq_status kq_hip_expert_member_span(uint32_t type_id, uint64_t rows,
+                                    uint64_t cols, uint32_t expert_count,
+                                    uint32_t expert_id,
+                                    uint64_t *out_byte_offset,
+                                    uint64_t *out_byte_count,
+                                    kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* Numeric core. */
+
+/* Replaces kq_dequantize_blocks_f32 (include/kq_numeric.h:20-26,
+ * src/kq_numeric.c:297-359). Bit-identical decode. *output_count receives
+ * the required element count (also on KQ_STATUS_BUFFER_TOO_SMALL). */
+kq_status kq_hip_dequantize_blocks_f32(kq_hip_context *context,
+                                       uint32_t type_id,
+                                       const void *device_packed,
+                                       uint64_t packed_bytes,
+                                       float *device_output,
+                                       uint64_t output_capacity,
+                                       uint64_t *output_count,
+                                       kq_diagnostic *diagnostic);
+
+/* Replaces kq_quantized_row_dot_f32 (include/kq_numeric.h:38-44,
+ * src/kq_numeric.c:420-503): one packed row dotted with x. */
+kq_status kq_hip_quantized_row_dot_f32(kq_hip_context *context,
+                                       uint32_t type_id,
+                                       const void *device_packed,
+                                       uint64_t packed_bytes,
+                                       const float *device_activation,
+                                       uint64_t activation_count,
+                                       float *device_output,
+                                       kq_diagnostic *diagnostic);
+
+/* Replaces kq_weight_provider_linear_f32 (include/kq_weight_provider.h:56-61,
+ * src/kq_weight_provider.c:378-509), extended to `batch` activation vectors:
+ * y[b*rows + r] = row r of W (packed, rows contiguous) . x[b*columns ...].
+ * batch 1..8; columns 256, 512, 1024 or 2048. */
+kq_status kq_hip_quantized_matvec_f32(kq_hip_context *context,
+                                      uint32_t type_id,
+                                      const void *device_weights,
+                                      uint64_t rows, uint64_t columns,
+                                      const float *device_input,
+                                      uint32_t batch, float *device_output,
+                                      uint64_t output_capacity,
+                                      kq_diagnostic *diagnostic);
+
+/* Replaces kq_model_exec_greedy_argmax_f32 (include/kq_model_exec.h:200-202,
+ * src/kq_model_exec.c:566-584) for `batch` logit rows of logit_count each:
+ * first maximum, ties to the lowest id, non-finite logits rejected. */
+kq_status kq_hip_greedy_argmax_f32(kq_hip_context *context,
+                                   const float *device_logits,
+                                   uint64_t logit_count, uint32_t batch,
+                                   uint32_t *device_token_ids,
+                                   kq_diagnostic *diagnostic);
+
+/* The LM-head call plus greedy selection (src/kq_model_exec.c:830-846 and
+ * :1095-1113): logits = W_lm h for `batch` hidden states, then argmax per
+ * batch row, fused (the argmax partials come out of the matvec kernel). */
+kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *context,
+                                    uint32_t type_id,
+                                    const void *device_weights,
+                                    uint64_t vocab, uint64_t columns,
+                                    const float *device_hidden,
+                                    uint32_t batch, float *device_logits,
+                                    uint32_t *device_token_ids,
+                                    kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* MoE operator. */
+
+/* Mirrors kq_moe_dimensions (src/kq_moe_internal.h:10-17) for F32
+ * activations; configs come from kq_hip_moe_config_create, which mirrors
+ * the test-config constructor kq_moe_test_config_create
+ * (src/kq_moe.c:283-297) and its validation (src/kq_moe.c:83-140). */
+typedef struct kq_hip_moe_dimensions {
+    uint32_t hidden_size;
+    uint32_t expert_count;
+    uint32_t top_k;
+    uint32_t routed_intermediate_size;
+    uint32_t shared_intermediate_size;
+} kq_hip_moe_dimensions;
+
+typedef struct kq_hip_moe_config kq_hip_moe_config;
+
+kq_status kq_hip_moe_config_create(const kq_hip_moe_dimensions *dimensions,
+                                   kq_hip_moe_config **out_config,
+                                   kq_diagnostic *diagnostic);
+void kq_hip_moe_config_close(kq_hip_moe_config *config);
+/* Device scratch needed by route/execute for `token_count` tokens. */
+uint64_t kq_hip_moe_config_scratch_bytes(const kq_hip_moe_config *config,
+                                         uint64_t token_count);
+
+/* Mirrors kq_moe_weights_f32 (include/kq_moe.h:72-89) with a GGUF type per
+ * packed role. Routed roles are contiguous expert stacks:
+ * gate/up [experts][routed_inter][hidden], down [experts][hidden][routed_inter]
+ * (the GGUF dims [cols, rows, experts], src/kq_tensor_view.c:664-807).
+ * router [experts][hidden] and shared_gate_weight [hidden] are F32. */
+typedef struct kq_hip_moe_weights {
+    const float *router;
+    uint32_t routed_gate_type;
+    const void *routed_gate;
+    uint32_t routed_up_type;
+    const void *routed_up;
+    uint32_t routed_down_type;
+    const void *routed_down;
+    uint32_t shared_gate_type;
+    const void *shared_gate;
+    uint32_t shared_up_type;
+    const void *shared_up;
+    uint32_t shared_down_type;
+    const void *shared_down;
+    const float *shared_gate_weight;
+} kq_hip_moe_weights;
+
+/* Replaces kq_moe_route_f32 (include/kq_moe.h:128-141,
+ * src/kq_moe_qwen38.c:276-376) for token_count tokens: logits, softmax
+ * probabilities, top-k ids (bit-identical to the CPU partial selection)
+ * and renormalised weights, each [tokens][...] in device memory. */
+kq_status kq_hip_moe_route_f32(kq_hip_context *context,
+                               const kq_hip_moe_config *config,
+                               const float *device_router_weight,
+                               const float *device_shared_gate_weight,
+                               const float *device_hidden,
+                               uint64_t token_count,
+                               float *device_router_logits,
+                               float *device_router_probabilities,
+                               uint32_t *device_selected_ids,
+                               float *device_selected_weights,
+                               void *device_scratch, uint64_t scratch_bytes,
+                               kq_diagnostic *diagnostic);
+
+/* Replaces kq_moe_execute_quantized (src/kq_moe_internal.h:56-64,
+ * src/kq_moe_qwen38.c:882-901) / kq_moe_execute_f32 (include/kq_moe.h:154-166):
+ * hidden [tokens][hidden] -> output [tokens][hidden]. Optional
+ * device_selected_ids [tokens][top_k] receives the routing. */
+kq_status kq_hip_moe_execute_quantized(kq_hip_context *context,
+                                       const kq_hip_moe_config *config,
+                                       const kq_hip_moe_weights *weights,
+                                       const float *device_hidden,
+                                       uint64_t token_count,
+                                       float *device_output,
+                                       uint64_t output_capacity,
+                                       uint32_t *device_selected_ids,
+                                       void *device_scratch,
+                                       uint64_t scratch_bytes,
+                                       kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* Elementwise binary32 expf with the bits of the libm expf the reference
+ * calls (src/kq_numeric.c:628-638, :776-813). No reference entry point of
+ * its own; it exposes the device expf that the softmax uses so callers can
+ * check it. */
+kq_status kq_hip_f32_expf(kq_hip_context *context, const float *device_input,
+                          uint64_t count, float *device_output,
+                          kq_diagnostic *diagnostic);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,107 @@
+/*
+ * kq_launch.h — internal launcher interface between the C host layer
+ * (kq_hip_api.c, validation and orchestration) and the HIP kernel files.
+ * Not installed; the public boundary is include/kq_hip.h.
+ *
+ * Launchers enqueue on the given stream and return the launch status only;
+ * numeric failures found on the device are OR-ed into *status.
+ */
+#ifndef KQ_LAUNCH_H
+#define KQ_LAUNCH_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KQ_LAUNCH_F32 0u
+#define KQ_LAUNCH_Q8_0 8u
+#define KQ_LAUNCH_Q4_K 12u
+#define KQ_LAUNCH_Q6_K 14u
+
+/* dequant (kq_dequant.hip) */
+hipError_t kq_launch_dequant(uint32_t type, const void *packed, uint64_t blocks,
+                             float *out, uint32_t *status, hipStream_t stream);
+
+/* matvec / argmax (kq_matvec.hip) */
+int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t batch);
+uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols);
+hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_t cols,
+                            const float *x, uint32_t batch, float *y, uint32_t *status,
+                            float *part_v, uint32_t *part_i, hipStream_t stream);
+uint32_t kq_launch_argmax_parts(uint32_t count);
+hipError_t kq_launch_argmax(const float *logits, uint32_t count, uint32_t batch,
+                            float *part_v, uint32_t *part_i, uint32_t *ids,
+                            uint32_t *status, hipStream_t stream);
+hipError_t kq_launch_argmax_from_parts(const float *part_v, const uint32_t *part_i,
+                                       uint32_t nparts, uint32_t batch, uint32_t *ids,
+                                       hipStream_t stream);
+
+/* elementwise expf (kq_dequant.hip), used to pin the device expf */
+hipError_t kq_launch_expf(const float *in, uint64_t n, float *out, hipStream_t stream);
+
+/* MoE (kq_moe.hip) */
+typedef struct kq_launch_moe_dims {
+    uint32_t hidden;
+    uint32_t experts;
+    uint32_t top_k;
+    uint32_t inter;
+    uint32_t shared_inter;
+} kq_launch_moe_dims;
+
+typedef struct kq_launch_moe_weights {
+    const float *router;
+    uint32_t gate_type;
+    const void *gate;
+    uint32_t up_type;
+    const void *up;
+    uint32_t down_type;
+    const void *down;
+    uint32_t shared_gate_type;
+    const void *shared_gate;
+    uint32_t shared_up_type;
+    const void *shared_up;
+    uint32_t shared_down_type;
+    const void *shared_down;
+    const float *shared_gate_weight;
+} kq_launch_moe_weights;
+
+/* Device workspace carved by the host from caller scratch
+ * (kq_launch_moe_ws_bytes gives the size for a token count). */
+typedef struct kq_launch_moe_ws {
+    float *router_t;      /* router rows + shared gate row, transposed to
+                             [hidden/4][experts_padded][4]; for one token the
+                             products w*x in the same layout */
+    float *logits;        /* [tokens][experts] */
+    float *probs;         /* [tokens][experts] */
+    uint32_t *ids;        /* [tokens][top_k], descending probability */
+    float *weights;       /* [tokens][top_k] */
+    uint32_t *order;      /* [tokens][top_k]: slots sorted by ascending id */
+    float *shared_logit;  /* [tokens] */
+    float *shared_scale;  /* [tokens] */
+    float *act;           /* [tokens][top_k + 1][max(inter, shared_inter)] */
+    float *expert_out;    /* [tokens][top_k + 1][hidden] */
+} kq_launch_moe_ws;
+
+uint32_t kq_launch_moe_experts_padded(uint32_t experts);
+uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t tokens);
+void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tokens, void *base,
+                            kq_launch_moe_ws *ws);
+int kq_launch_moe_supported(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w);
+/* logits (+ shared gate logit), softmax, partial-selection top-k, weights */
+hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
+                               const float *shared_gate_weight, const float *hidden,
+                               uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t *status,
+                               hipStream_t stream);
+hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
+                                 const float *hidden, uint32_t tokens,
+                                 const kq_launch_moe_ws *ws, float *out, uint32_t *status,
+                                 hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

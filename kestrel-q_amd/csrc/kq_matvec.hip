@@ -1,0 +1,271 @@
+/*
+ * kq_matvec.hip — dequant-fused matrix-vector products y = W x for GGUF
+ * Q4_K, Q6_K and Q8_0 rows (batch 1..4, fp32 activations and outputs) and
+ * greedy argmax over the results.
+ *
+ * Restates the row loop of kq_weight_provider_linear_f32
+ * (src/kq_weight_provider.c:464-475) around kq_quantized_row_dot_f32
+ * (src/kq_numeric.c:420-503), and kq_model_exec_greedy_argmax_f32
+ * (src/kq_model_exec.c:566-584). Weights decode exactly as the reference
+ * decodes them; the row sum is a wave-parallel fp32 reduction compared by
+ * tolerance. The argmax is exact (first maximum, lowest row on ties).
+ *
+ * Each 64-lane wavefront keeps its lanes' activations in registers for the
+ * whole launch and walks RT row-groups per iteration, so RT rows of packed
+ * weights are in flight before the first multiply (kq_rowdot.h). Row sums
+ * finish with lane shuffles inside each row's lane group. For the fused LM
+ * head every wave also keeps a running (max, row) per batch column and
+ * writes one partial; a one-block kernel merges the partials.
+ */
+#include "kq_launch.h"
+#include "kq_rowdot.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRT = 4;
+/* Enough waves to cover HBM latency on the large matrices (8 blocks of 4
+ * waves per CU); smaller matrices get one row-group stride per wave. */
+constexpr int kMaxBlocks = 256 * 8;
+
+/* larger value wins, equal values keep the lower row */
+__device__ __forceinline__ void argmax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void wave_argmax(float &bv, uint32_t &bi) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, KQ_WAVE);
+        uint32_t oi = __shfl_xor(bi, o, KQ_WAVE);
+        argmax_merge(bv, bi, ov, oi);
+    }
+}
+
+template <uint32_t TYPE, uint32_t COLS, int B, int RT>
+__global__ __launch_bounds__(kThreads) void matvec_kernel(
+    const uint8_t *__restrict__ W, uint32_t rows, const float *__restrict__ x,
+    float *__restrict__ y, uint32_t *status, float *part_v, uint32_t *part_i,
+    const uint8_t *w_end) {
+    using Lane = typename kq::LaneFor<TYPE, B>::T;
+    constexpr uint32_t LPR = kq::lanes_per_row<TYPE>(COLS);
+    static_assert(LPR <= 64 && 64 % LPR == 0, "row must fit a wave");
+    constexpr uint32_t RPW = 64u / LPR;
+    constexpr uint32_t RB = kq::row_bytes<TYPE>(COLS);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
+    const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
+    const uint32_t sub = lane / LPR, l = lane % LPR;
+
+    Lane ln;
+    if (ln.init(l, x, COLS)) kq_flag(status, KQ_DEV_INPUT);
+    bool bad = false;
+    bool malformed = false;
+    float best_v[B];
+    uint32_t best_i[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        best_v[b] = -__builtin_inff();
+        best_i[b] = 0xffffffffu;
+    }
+
+    for (uint32_t row_base = wave * (RPW * RT); row_base < rows;
+         row_base += nwaves * (RPW * RT)) {
+        typename Lane::Raw raw[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
+            raw[r] = row < rows ? ln.load(W + (size_t)row * RB, w_end) : ln.zero();
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
+            float acc[B];
+            ln.dot(raw[r], acc, malformed);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float v = kq_group_sum<LPR>(acc[b]);
+                if (row < rows) {
+                    if (l == 0) y[(size_t)b * rows + row] = v;
+                    bad |= !kq_isfinite(v);
+                    argmax_merge(best_v[b], best_i[b], v, row);
+                }
+            }
+        }
+    }
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+    if (part_v != nullptr) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float v = best_v[b];
+            uint32_t i = best_i[b];
+            wave_argmax(v, i);
+            if (lane == 0) {
+                part_v[(size_t)b * nwaves + wave] = v;
+                part_i[(size_t)b * nwaves + wave] = i;
+            }
+        }
+    }
+}
+
+/* ---- argmax over rows of logits (two stages) ---- */
+__global__ __launch_bounds__(kThreads) void argmax_partial(const float *__restrict__ logits,
+                                                           uint32_t count, float *part_v,
+                                                           uint32_t *part_i, uint32_t *status) {
+    const uint32_t b = blockIdx.y;
+    const float *v = logits + (size_t)b * count;
+    const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
+    const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xffffffffu;
+    bool bad = false;
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < count; i += gridDim.x * kThreads) {
+        const float f = v[i];
+        bad |= !kq_isfinite(f);
+        argmax_merge(bv, bi, f, i);
+    }
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+    wave_argmax(bv, bi);
+    if ((threadIdx.x & 63u) == 0u) {
+        part_v[(size_t)b * nwaves + wave] = bv;
+        part_i[(size_t)b * nwaves + wave] = bi;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_final(const float *part_v,
+                                                         const uint32_t *part_i,
+                                                         uint32_t nparts, uint32_t *ids) {
+    __shared__ float sv[kThreads / 64];
+    __shared__ uint32_t si[kThreads / 64];
+    const uint32_t b = blockIdx.x;
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t i = threadIdx.x; i < nparts; i += kThreads)
+        argmax_merge(bv, bi, part_v[(size_t)b * nparts + i], part_i[(size_t)b * nparts + i]);
+    wave_argmax(bv, bi);
+    if ((threadIdx.x & 63u) == 0u) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+        ids[b] = bi;
+    }
+}
+
+int grid_for(uint32_t rows, uint32_t rows_per_wave_iter) {
+    const uint32_t waves = (rows + rows_per_wave_iter - 1u) / rows_per_wave_iter;
+    uint32_t blocks = (waves + (kThreads / 64) - 1u) / (kThreads / 64);
+    if (blocks > (uint32_t)kMaxBlocks) blocks = kMaxBlocks;
+    return blocks < 1u ? 1 : (int)blocks;
+}
+
+/* every format gives each lane 32 weights, so a row takes cols/32 lanes */
+uint32_t rows_per_iter(uint32_t cols) {
+    const uint32_t lanes = cols / 32u;
+    return (lanes >= 64u ? 1u : 64u / lanes) * kRT;
+}
+
+template <uint32_t TYPE, uint32_t COLS, int B>
+hipError_t launch_one(const uint8_t *W, uint32_t rows, const float *x, float *y, uint32_t *st,
+                      float *pv, uint32_t *pi, hipStream_t s) {
+    const uint8_t *end = W + (size_t)rows * kq::row_bytes<TYPE>(COLS);
+    hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, kRT>),
+                       dim3(grid_for(rows, rows_per_iter(COLS))), dim3(kThreads), 0, s, W,
+                       rows, x, y, st, pv, pi, end);
+    return hipGetLastError();
+}
+
+template <uint32_t TYPE, int B>
+hipError_t launch_cols(uint32_t cols, const uint8_t *W, uint32_t rows, const float *x, float *y,
+                       uint32_t *st, float *pv, uint32_t *pi, hipStream_t s) {
+    switch (cols) {
+    case 32:
+    case 64:
+    case 128:
+        /* short rows exist only for 32-element Q8_0 blocks */
+        if (TYPE != KQ_LAUNCH_Q8_0) break;
+        if (cols == 32) return launch_one<KQ_LAUNCH_Q8_0, 32u, B>(W, rows, x, y, st, pv, pi, s);
+        if (cols == 64) return launch_one<KQ_LAUNCH_Q8_0, 64u, B>(W, rows, x, y, st, pv, pi, s);
+        return launch_one<KQ_LAUNCH_Q8_0, 128u, B>(W, rows, x, y, st, pv, pi, s);
+    case 256: return launch_one<TYPE, 256u, B>(W, rows, x, y, st, pv, pi, s);
+    case 512: return launch_one<TYPE, 512u, B>(W, rows, x, y, st, pv, pi, s);
+    case 1024: return launch_one<TYPE, 1024u, B>(W, rows, x, y, st, pv, pi, s);
+    case 2048: return launch_one<TYPE, 2048u, B>(W, rows, x, y, st, pv, pi, s);
+    default: break;
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int B>
+hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t rows,
+                    const float *x, float *y, uint32_t *st, float *pv, uint32_t *pi,
+                    hipStream_t s) {
+    switch (type) {
+    case KQ_LAUNCH_Q4_K: return launch_cols<KQ_LAUNCH_Q4_K, B>(cols, W, rows, x, y, st, pv, pi, s);
+    case KQ_LAUNCH_Q6_K: return launch_cols<KQ_LAUNCH_Q6_K, B>(cols, W, rows, x, y, st, pv, pi, s);
+    case KQ_LAUNCH_Q8_0: return launch_cols<KQ_LAUNCH_Q8_0, B>(cols, W, rows, x, y, st, pv, pi, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+extern "C" int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t batch) {
+    if (batch < 1u || batch > 4u) return 0;
+    if (type != KQ_LAUNCH_Q4_K && type != KQ_LAUNCH_Q6_K && type != KQ_LAUNCH_Q8_0) return 0;
+    if (type == KQ_LAUNCH_Q8_0 && (cols == 32u || cols == 64u || cols == 128u)) return 1;
+    return cols == 256u || cols == 512u || cols == 1024u || cols == 2048u;
+}
+
+extern "C" uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols) {
+    (void)type;
+    return (uint32_t)grid_for(rows, rows_per_iter(cols)) * (kThreads / 64);
+}
+
+extern "C" hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows,
+                                       uint32_t cols, const float *x, uint32_t batch, float *y,
+                                       uint32_t *status, float *part_v, uint32_t *part_i,
+                                       hipStream_t stream) {
+    const uint8_t *w = (const uint8_t *)W;
+    switch (batch) {
+    case 1: return launch_b<1>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
+    case 2: return launch_b<2>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
+    case 3: return launch_b<3>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
+    case 4: return launch_b<4>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" uint32_t kq_launch_argmax_parts(uint32_t count) {
+    uint32_t blocks = (count + kThreads * 8u - 1u) / (kThreads * 8u);
+    if (blocks > 1024u) blocks = 1024u;
+    if (blocks < 1u) blocks = 1u;
+    return blocks * (kThreads / 64u);
+}
+
+extern "C" hipError_t kq_launch_argmax(const float *logits, uint32_t count, uint32_t batch,
+                                       float *part_v, uint32_t *part_i, uint32_t *ids,
+                                       uint32_t *status, hipStream_t stream) {
+    const uint32_t parts = kq_launch_argmax_parts(count);
+    hipLaunchKernelGGL(argmax_partial, dim3(parts / (kThreads / 64u), batch), dim3(kThreads), 0,
+                       stream, logits, count, part_v, part_i, status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(kThreads), 0, stream, part_v, part_i,
+                       parts, ids);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t kq_launch_argmax_from_parts(const float *part_v, const uint32_t *part_i,
+                                                  uint32_t nparts, uint32_t batch, uint32_t *ids,
+                                                  hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(kThreads), 0, stream, part_v, part_i,
+                       nparts, ids);
+    return hipGetLastError();
+}

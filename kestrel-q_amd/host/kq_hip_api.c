@@ -1,0 +1,683 @@
+/*
+ * kq_hip_api.c — host side of the kq_hip C ABI (include/kq_hip.h).
+ *
+ * C17. Validates every call before enqueueing device work, with the
+ * reference's status codes and order of checks (src/kq_numeric.c:297-359,
+ * :420-503; src/kq_weight_provider.c:378-437; src/kq_moe_qwen38.c:276-330,
+ * :604-660), then drives the HIP launchers of the kernel files
+ * (kestrel-q_amd/csrc/kq_launch.h) on the context's stream.
+ *
+ * Device-detected failures are OR-ed by kernels into a device status word;
+ * synchronous calls (the default) read it back after the stream drains and
+ * report it, asynchronous ones leave it for kq_hip_context_synchronize.
+ */
+#include "kq_hip.h"
+
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "kq_launch.h"
+#include "kq_status_internal.h"
+
+#define KQ_MOE_CONFIG_MAGIC 0x4b514d48u /* "KQMH" */
+#define KQ_DEV_MALFORMED 1u
+#define KQ_DEV_NUMERIC 2u
+#define KQ_DEV_INPUT 4u
+
+struct kq_hip_context {
+    int device;
+    int async;
+    hipStream_t stream;
+    uint32_t *d_status;
+    uint32_t *h_status; /* pinned */
+    float *part_v;      /* argmax partials */
+    uint32_t *part_i;
+    uint64_t part_cap;
+};
+
+struct kq_hip_moe_config {
+    uint32_t magic;
+    kq_hip_moe_dimensions dims;
+};
+
+/* ------------------------------------------------------------------ */
+
+static kq_status hip_fail(kq_diagnostic *diag, hipError_t e, const char *what) {
+    return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "%s: %s", what, hipGetErrorString(e));
+}
+
+static int ctx_ok(const kq_hip_context *c) { return c != NULL && c->stream != NULL; }
+
+static kq_status set_device(kq_hip_context *c, kq_diagnostic *diag) {
+    hipError_t e = hipSetDevice(c->device);
+    return e == hipSuccess ? KQ_STATUS_OK : hip_fail(diag, e, "hipSetDevice");
+}
+
+/* Map the device status word to the reference's codes: a non-finite input
+ * is reported first (the reference validates inputs before decoding), then a
+ * malformed block scale, then a non-finite result. */
+static kq_status device_flags(uint32_t flags, kq_diagnostic *diag) {
+    if (flags & KQ_DEV_INPUT)
+        return kq_fail(diag, KQ_STATUS_NUMERIC_DOMAIN, "non-finite input on the device path");
+    if (flags & KQ_DEV_MALFORMED)
+        return kq_fail(diag, KQ_STATUS_MALFORMED_QUANTIZED_DATA,
+                       "quantized block scale is non-finite");
+    if (flags & KQ_DEV_NUMERIC)
+        return kq_fail(diag, KQ_STATUS_NUMERIC_DOMAIN, "device computation produced a non-finite value");
+    return KQ_STATUS_OK;
+}
+
+static kq_status drain(kq_hip_context *c, kq_diagnostic *diag) {
+    hipError_t e = hipMemcpyAsync(c->h_status, c->d_status, sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(diag, e, "stream synchronize");
+    if (*c->h_status != 0u) {
+        uint32_t flags = *c->h_status;
+        *c->h_status = 0u;
+        e = hipMemsetAsync(c->d_status, 0, sizeof(uint32_t), c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return hip_fail(diag, e, "status reset");
+        return device_flags(flags, diag);
+    }
+    return KQ_STATUS_OK;
+}
+
+static kq_status finish(kq_hip_context *c, hipError_t launch, const char *what,
+                        kq_diagnostic *diag) {
+    if (launch != hipSuccess) return hip_fail(diag, launch, what);
+    if (c->async) return KQ_STATUS_OK;
+    return drain(c, diag);
+}
+
+static int ranges_overlap(const void *a, uint64_t an, const void *b, uint64_t bn) {
+    uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    if (a == NULL || b == NULL || an == 0u || bn == 0u) return 0;
+    return a0 < b0 + bn && b0 < a0 + an;
+}
+
+static int aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0u; }
+
+static int u64_mul(uint64_t a, uint64_t b, uint64_t *out) {
+    if (a != 0u && b > UINT64_MAX / a) return 0;
+    *out = a * b;
+    return 1;
+}
+
+/* ------------------------------------------------------------------ */
+/* context */
+
+kq_status kq_hip_context_create(int device, kq_hip_context **out, kq_diagnostic *diag) {
+    kq_hip_context *c;
+    hipDeviceProp_t prop;
+    hipError_t e;
+    int count = 0;
+    kq_diagnostic_clear(diag);
+    if (out == NULL) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "context output is required");
+    *out = NULL;
+    e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "no HIP device is available");
+    if (device < 0 || device >= count)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "device %d is out of range", device);
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(diag, e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE,
+                       "device %d is %s; this library is built for gfx950 only", device,
+                       prop.gcnArchName);
+    c = (kq_hip_context *)calloc(1, sizeof(*c));
+    if (c == NULL) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "context allocation failed");
+    c->device = device;
+    e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc((void **)&c->d_status, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipHostMalloc((void **)&c->h_status, sizeof(uint32_t), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMemsetAsync(c->d_status, 0, sizeof(uint32_t), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        kq_status st = hip_fail(diag, e, "context setup");
+        kq_hip_context_destroy(c);
+        return st;
+    }
+    *c->h_status = 0u;
+    *out = c;
+    return KQ_STATUS_OK;
+}
+
+void kq_hip_context_destroy(kq_hip_context *c) {
+    if (c == NULL) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->part_v) (void)hipFree(c->part_v);
+    if (c->part_i) (void)hipFree(c->part_i);
+    if (c->d_status) (void)hipFree(c->d_status);
+    if (c->h_status) (void)hipHostFree(c->h_status);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    free(c);
+}
+
+kq_status kq_hip_context_set_async(kq_hip_context *c, int async, kq_diagnostic *diag) {
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c)) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "valid context is required");
+    c->async = async ? 1 : 0;
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_context_synchronize(kq_hip_context *c, kq_diagnostic *diag) {
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c)) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "valid context is required");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return drain(c, diag);
+}
+
+void *kq_hip_context_stream(const kq_hip_context *c) {
+    return c == NULL ? NULL : (void *)c->stream;
+}
+
+kq_status kq_hip_malloc(kq_hip_context *c, uint64_t bytes, void **out, kq_diagnostic *diag) {
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || out == NULL || bytes == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "context, size and output are required");
+    *out = NULL;
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = hipMalloc(out, (size_t)bytes);
+    if (e != hipSuccess) {
+        *out = NULL;
+        return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "hipMalloc of %llu bytes failed: %s",
+                       (unsigned long long)bytes, hipGetErrorString(e));
+    }
+    return KQ_STATUS_OK;
+}
+
+void kq_hip_free(kq_hip_context *c, void *p) {
+    if (c == NULL || p == NULL) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(p);
+}
+
+kq_status kq_hip_upload(kq_hip_context *c, void *dst, const void *src, uint64_t bytes,
+                        kq_diagnostic *diag) {
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || dst == NULL || src == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "context and buffers are required");
+    if (bytes == 0u) return KQ_STATUS_OK;
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? KQ_STATUS_OK : hip_fail(diag, e, "upload");
+}
+
+kq_status kq_hip_download(kq_hip_context *c, void *dst, const void *src, uint64_t bytes,
+                          kq_diagnostic *diag) {
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || dst == NULL || src == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "context and buffers are required");
+    if (bytes == 0u) return KQ_STATUS_OK;
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? KQ_STATUS_OK : hip_fail(diag, e, "download");
+}
+
+/* ------------------------------------------------------------------ */
+/* geometry */
+
+kq_status kq_hip_quant_geometry_for_type(uint32_t type_id, kq_hip_quant_geometry *g,
+                                         kq_diagnostic *diag) {
+    kq_diagnostic_clear(diag);
+    if (g == NULL) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "output geometry is required");
+    memset(g, 0, sizeof(*g));
+    switch (type_id) {
+    case KQ_HIP_TYPE_F32: g->block_elements = 1u; g->bytes_per_block = 4u; break;
+    case KQ_HIP_TYPE_Q8_0: g->block_elements = 32u; g->bytes_per_block = 34u; break;
+    case KQ_HIP_TYPE_Q4_K: g->block_elements = 256u; g->bytes_per_block = 144u; break;
+    case KQ_HIP_TYPE_Q6_K: g->block_elements = 256u; g->bytes_per_block = 210u; break;
+    default:
+        return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
+                       "GGUF tensor type %u is unsupported", type_id);
+    }
+    g->type_id = type_id;
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_quant_packed_size(uint32_t type_id, uint64_t elements, uint64_t *out,
+                                   kq_diagnostic *diag) {
+    kq_hip_quant_geometry g;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (out == NULL) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "output byte count is required");
+    *out = 0u;
+    st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (elements == 0u || elements % g.block_elements != 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_QUANTIZED_GEOMETRY,
+                       "element count is not a non-zero whole number of quant blocks");
+    if (!u64_mul(elements / g.block_elements, g.bytes_per_block, out))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "packed byte count overflows uint64");
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_expert_member_span(uint32_t type_id, uint64_t rows, uint64_t cols,
+                                    uint32_t expert_count, uint32_t expert_id,
+                                    uint64_t *off, uint64_t *count, kq_diagnostic *diag) {
+    uint64_t elements, bytes;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (off == NULL || count == NULL || rows == 0u || cols == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "member geometry and outputs are required");
+    if (expert_id >= expert_count)
+        return kq_fail(diag, KQ_STATUS_SPAN_OUT_OF_RANGE, "expert %u is outside %u experts",
+                       expert_id, expert_count);
+    if (!u64_mul(rows, cols, &elements))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "member element count overflows");
+    st = kq_hip_quant_packed_size(type_id, elements, &bytes, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (cols % (type_id == KQ_HIP_TYPE_Q8_0 ? 32u : (type_id == KQ_HIP_TYPE_F32 ? 1u : 256u)) != 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_QUANTIZED_GEOMETRY,
+                       "member rows are not whole quant blocks");
+    if (!u64_mul(bytes, expert_id, off))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "member offset overflows");
+    *count = bytes;
+    return KQ_STATUS_OK;
+}
+
+static kq_status quant_geometry(uint32_t type_id, uint64_t *be, uint64_t *bb,
+                                kq_diagnostic *diag) {
+    kq_hip_quant_geometry g;
+    kq_status st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (type_id != KQ_HIP_TYPE_Q8_0 && type_id != KQ_HIP_TYPE_Q4_K && type_id != KQ_HIP_TYPE_Q6_K)
+        return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
+                       "device path supports Q8_0, Q4_K and Q6_K blocks");
+    *be = g.block_elements;
+    *bb = g.bytes_per_block;
+    return KQ_STATUS_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* numeric */
+
+kq_status kq_hip_dequantize_blocks_f32(kq_hip_context *c, uint32_t type_id, const void *packed,
+                                       uint64_t packed_bytes, float *output,
+                                       uint64_t capacity, uint64_t *count,
+                                       kq_diagnostic *diag) {
+    uint64_t be, bb, blocks, need, out_bytes;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || count == NULL || packed == NULL || packed_bytes == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "packed input and output count are required");
+    *count = 0u;
+    st = quant_geometry(type_id, &be, &bb, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (packed_bytes % bb != 0u)
+        return kq_fail(diag, KQ_STATUS_MALFORMED_QUANTIZED_DATA,
+                       "packed bytes are not a bounded whole-block span");
+    blocks = packed_bytes / bb;
+    if (!u64_mul(blocks, be, &need) || !u64_mul(need, sizeof(float), &out_bytes))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "decoded output count overflows");
+    *count = need;
+    if (output == NULL || capacity < need)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "decoded output capacity is too small");
+    if (ranges_overlap(packed, packed_bytes, output, out_bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "packed input and decoded output overlap");
+    if (!aligned(packed, type_id == KQ_HIP_TYPE_Q4_K ? 16u : 4u) || !aligned(output, 16u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT,
+                       "device buffers must be 16-byte (Q4_K) / 4-byte aligned, output 16-byte");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return finish(c, kq_launch_dequant(type_id, packed, blocks, output, c->d_status, c->stream),
+                  "dequant launch", diag);
+}
+
+static kq_status ensure_parts(kq_hip_context *c, uint64_t n, kq_diagnostic *diag) {
+    hipError_t e;
+    if (n <= c->part_cap) return KQ_STATUS_OK;
+    if (c->part_v) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->part_v);
+        (void)hipFree(c->part_i);
+        c->part_v = NULL;
+        c->part_i = NULL;
+        c->part_cap = 0u;
+    }
+    e = hipMalloc((void **)&c->part_v, (size_t)n * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->part_i, (size_t)n * sizeof(uint32_t));
+    if (e != hipSuccess) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "argmax partials: %s",
+                                        hipGetErrorString(e));
+    c->part_cap = n;
+    return KQ_STATUS_OK;
+}
+
+static kq_status validate_matvec(const kq_hip_context *c, uint32_t type_id, const void *w,
+                                 uint64_t rows, uint64_t cols, const float *x, uint32_t batch,
+                                 const float *y, uint64_t capacity, kq_diagnostic *diag) {
+    uint64_t be, bb, w_bytes, need;
+    kq_status st;
+    if (!ctx_ok(c) || w == NULL || x == NULL || y == NULL || rows == 0u || cols == 0u ||
+        batch == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "weights, input, output and non-zero shape are required");
+    st = quant_geometry(type_id, &be, &bb, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (cols % be != 0u)
+        return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH, "columns are not whole quant blocks");
+    if (rows > UINT32_MAX || batch > 8u)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "rows must fit 32 bits and batch be <= 8");
+    if (!kq_launch_matvec_supported(type_id, (uint32_t)cols, 1u))
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
+                       "device matvec supports 256, 512, 1024 or 2048 columns");
+    if (!u64_mul(rows, cols / be * bb, &w_bytes) || !u64_mul(rows, batch, &need))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "matrix byte count overflows");
+    if (capacity < need)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "output capacity is too small");
+    if (ranges_overlap(w, w_bytes, y, need * 4u) ||
+        ranges_overlap(x, (uint64_t)batch * cols * 4u, y, need * 4u))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "linear output overlaps an input");
+    if (!aligned(w, 16u) || !aligned(x, 16u) || !aligned(y, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT,
+                       "weights and input must be 16-byte aligned");
+    return KQ_STATUS_OK;
+}
+
+/* Enqueue y for up to 8 batch columns, in launches of at most 4. */
+static hipError_t enqueue_matvec(kq_hip_context *c, uint32_t type_id, const void *w,
+                                 uint64_t rows, uint64_t cols, const float *x, uint32_t batch,
+                                 float *y, float *pv, uint32_t *pi, uint32_t nparts) {
+    uint32_t done = 0u;
+    while (done < batch) {
+        uint32_t nb = batch - done > 4u ? 4u : batch - done;
+        hipError_t e = kq_launch_matvec(type_id, w, (uint32_t)rows, (uint32_t)cols,
+                                        x + (size_t)done * cols, nb, y + (size_t)done * rows,
+                                        c->d_status, pv ? pv + (size_t)done * nparts : NULL,
+                                        pi ? pi + (size_t)done * nparts : NULL, c->stream);
+        if (e != hipSuccess) return e;
+        done += nb;
+    }
+    return hipSuccess;
+}
+
+kq_status kq_hip_quantized_matvec_f32(kq_hip_context *c, uint32_t type_id, const void *w,
+                                      uint64_t rows, uint64_t cols, const float *x,
+                                      uint32_t batch, float *y, uint64_t capacity,
+                                      kq_diagnostic *diag) {
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    st = validate_matvec(c, type_id, w, rows, cols, x, batch, y, capacity, diag);
+    if (st != KQ_STATUS_OK) return st;
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return finish(c, enqueue_matvec(c, type_id, w, rows, cols, x, batch, y, NULL, NULL, 0u),
+                  "matvec launch", diag);
+}
+
+kq_status kq_hip_quantized_row_dot_f32(kq_hip_context *c, uint32_t type_id, const void *packed,
+                                       uint64_t packed_bytes, const float *x, uint64_t count,
+                                       float *out, kq_diagnostic *diag) {
+    uint64_t be, bb;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || packed == NULL || x == NULL || out == NULL || packed_bytes == 0u ||
+        count == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "row-dot inputs and scalar output are required");
+    st = quant_geometry(type_id, &be, &bb, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (packed_bytes % bb != 0u)
+        return kq_fail(diag, KQ_STATUS_MALFORMED_QUANTIZED_DATA,
+                       "row is not a bounded whole-block span");
+    if (packed_bytes / bb * be != count)
+        return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH,
+                       "quantized row and activation lengths differ");
+    return kq_hip_quantized_matvec_f32(c, type_id, packed, 1u, count, x, 1u, out, 1u, diag);
+}
+
+kq_status kq_hip_greedy_argmax_f32(kq_hip_context *c, const float *logits, uint64_t count,
+                                   uint32_t batch, uint32_t *ids, kq_diagnostic *diag) {
+    uint32_t parts;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || logits == NULL || ids == NULL || count == 0u || count > UINT32_MAX ||
+        batch == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "valid finite logits and selection output are required");
+    if (ranges_overlap(logits, count * batch * 4u, ids, (uint64_t)batch * 4u))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "logits and ids overlap");
+    if (!aligned(logits, 4u) || !aligned(ids, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "buffers must be 4-byte aligned");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    parts = kq_launch_argmax_parts((uint32_t)count);
+    st = ensure_parts(c, (uint64_t)parts * batch, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return finish(c, kq_launch_argmax(logits, (uint32_t)count, batch, c->part_v, c->part_i, ids,
+                                      c->d_status, c->stream),
+                  "argmax launch", diag);
+}
+
+kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const void *w,
+                                    uint64_t vocab, uint64_t cols, const float *h,
+                                    uint32_t batch, float *logits, uint32_t *ids,
+                                    kq_diagnostic *diag) {
+    uint32_t nparts;
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    st = validate_matvec(c, type_id, w, vocab, cols, h, batch, logits, vocab * batch, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (ids == NULL) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "token id output is required");
+    if (ranges_overlap(ids, (uint64_t)batch * 4u, logits, vocab * batch * 4u))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "logits and ids overlap");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    nparts = kq_launch_matvec_waves(type_id, (uint32_t)vocab, (uint32_t)cols);
+    st = ensure_parts(c, (uint64_t)nparts * batch, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = enqueue_matvec(c, type_id, w, vocab, cols, h, batch, logits, c->part_v, c->part_i, nparts);
+    if (e == hipSuccess)
+        e = kq_launch_argmax_from_parts(c->part_v, c->part_i, nparts, batch, ids, c->stream);
+    return finish(c, e, "lm head launch", diag);
+}
+
+kq_status kq_hip_f32_expf(kq_hip_context *c, const float *in, uint64_t n, float *out,
+                          kq_diagnostic *diag) {
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || in == NULL || out == NULL || n == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "input and output are required");
+    if (ranges_overlap(in, n * 4u, out, n * 4u) && in != out)
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "input and output overlap");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return finish(c, kq_launch_expf(in, n, out, c->stream), "expf launch", diag);
+}
+
+/* ------------------------------------------------------------------ */
+/* MoE */
+
+static int moe_ok(const kq_hip_moe_config *cfg) {
+    return cfg != NULL && cfg->magic == KQ_MOE_CONFIG_MAGIC;
+}
+
+static kq_launch_moe_dims launch_dims(const kq_hip_moe_config *cfg) {
+    kq_launch_moe_dims d;
+    d.hidden = cfg->dims.hidden_size;
+    d.experts = cfg->dims.expert_count;
+    d.top_k = cfg->dims.top_k;
+    d.inter = cfg->dims.routed_intermediate_size;
+    d.shared_inter = cfg->dims.shared_intermediate_size;
+    return d;
+}
+
+kq_status kq_hip_moe_config_create(const kq_hip_moe_dimensions *dims, kq_hip_moe_config **out,
+                                   kq_diagnostic *diag) {
+    kq_hip_moe_config *cfg;
+    kq_launch_moe_dims d;
+    kq_diagnostic_clear(diag);
+    if (dims == NULL || out == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "MoE dimensions and output are required");
+    *out = NULL;
+    if (dims->hidden_size == 0u || dims->expert_count == 0u || dims->top_k == 0u ||
+        dims->top_k > dims->expert_count || dims->routed_intermediate_size == 0u ||
+        dims->shared_intermediate_size == 0u)
+        return kq_fail(diag, KQ_STATUS_INCOMPATIBLE_MOE, "invalid MoE dimensions, top-k, or dtype");
+    d.hidden = dims->hidden_size;
+    d.experts = dims->expert_count;
+    d.top_k = dims->top_k;
+    d.inter = dims->routed_intermediate_size;
+    d.shared_inter = dims->shared_intermediate_size;
+    if (!kq_launch_moe_supported(&d, NULL))
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
+                       "device MoE needs hidden %% 4 == 0, experts <= 1023, top_k <= 64");
+    cfg = (kq_hip_moe_config *)calloc(1, sizeof(*cfg));
+    if (cfg == NULL) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "MoE config allocation failed");
+    cfg->magic = KQ_MOE_CONFIG_MAGIC;
+    cfg->dims = *dims;
+    *out = cfg;
+    return KQ_STATUS_OK;
+}
+
+void kq_hip_moe_config_close(kq_hip_moe_config *cfg) {
+    if (cfg == NULL) return;
+    cfg->magic = 0u;
+    free(cfg);
+}
+
+uint64_t kq_hip_moe_config_scratch_bytes(const kq_hip_moe_config *cfg, uint64_t tokens) {
+    kq_launch_moe_dims d;
+    if (!moe_ok(cfg) || tokens == 0u || tokens > UINT32_MAX) return 0u;
+    d = launch_dims(cfg);
+    return kq_launch_moe_ws_bytes(&d, (uint32_t)tokens);
+}
+
+#define KQ_MOE_MAX_TOKENS 65536u
+
+static kq_status moe_common(const kq_hip_context *c, const kq_hip_moe_config *cfg,
+                            const float *router, const float *sgw, const float *hidden,
+                            uint64_t tokens, void *scratch, uint64_t scratch_bytes,
+                            kq_diagnostic *diag) {
+    kq_launch_moe_dims d;
+    if (!ctx_ok(c) || !moe_ok(cfg) || router == NULL || sgw == NULL || hidden == NULL ||
+        scratch == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE arguments are required");
+    if (tokens == 0u || tokens > KQ_MOE_MAX_TOKENS)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "MoE token count is zero or above %u",
+                       KQ_MOE_MAX_TOKENS);
+    d = launch_dims(cfg);
+    if (scratch_bytes < kq_launch_moe_ws_bytes(&d, (uint32_t)tokens))
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "MoE device scratch is too small");
+    if (!aligned(router, 16u) || !aligned(sgw, 16u) || !aligned(hidden, 16u) ||
+        !aligned(scratch, 256u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT,
+                       "MoE weights/input need 16-byte and scratch 256-byte alignment");
+    if (ranges_overlap(hidden, tokens * d.hidden * 4u, scratch, scratch_bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "MoE input and scratch overlap");
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_moe_route_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
+                               const float *router, const float *sgw, const float *hidden,
+                               uint64_t tokens, float *logits, float *probs, uint32_t *ids,
+                               float *weights, void *scratch, uint64_t scratch_bytes,
+                               kq_diagnostic *diag) {
+    kq_launch_moe_dims d;
+    kq_launch_moe_ws ws;
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    st = moe_common(c, cfg, router, sgw, hidden, tokens, scratch, scratch_bytes, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (logits == NULL || probs == NULL || ids == NULL || weights == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE route arguments are required");
+    d = launch_dims(cfg);
+    kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(logits, ws.logits, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
+                           c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(probs, ws.probs, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
+                           c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(ids, ws.ids, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice, c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(weights, ws.weights, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice,
+                           c->stream);
+    return finish(c, e, "MoE route launch", diag);
+}
+
+kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_config *cfg,
+                                       const kq_hip_moe_weights *w, const float *hidden,
+                                       uint64_t tokens, float *out, uint64_t capacity,
+                                       uint32_t *ids, void *scratch, uint64_t scratch_bytes,
+                                       kq_diagnostic *diag) {
+    kq_launch_moe_dims d;
+    kq_launch_moe_weights lw;
+    kq_launch_moe_ws ws;
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (w == NULL || out == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE execution arguments are required");
+    st = moe_common(c, cfg, w->router, w->shared_gate_weight, hidden, tokens, scratch,
+                    scratch_bytes, diag);
+    if (st != KQ_STATUS_OK) return st;
+    d = launch_dims(cfg);
+    if (w->routed_gate == NULL || w->routed_up == NULL || w->routed_down == NULL ||
+        w->shared_gate == NULL || w->shared_up == NULL || w->shared_down == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "every MoE weight role is required");
+    if (capacity < tokens * d.hidden)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "MoE output or aligned scratch is too small");
+    if (ranges_overlap(hidden, tokens * d.hidden * 4u, out, tokens * d.hidden * 4u) ||
+        ranges_overlap(out, tokens * d.hidden * 4u, scratch, scratch_bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                       "MoE input, output, and scratch must not overlap");
+    lw.router = w->router;
+    lw.gate_type = w->routed_gate_type;
+    lw.gate = w->routed_gate;
+    lw.up_type = w->routed_up_type;
+    lw.up = w->routed_up;
+    lw.down_type = w->routed_down_type;
+    lw.down = w->routed_down;
+    lw.shared_gate_type = w->shared_gate_type;
+    lw.shared_gate = w->shared_gate;
+    lw.shared_up_type = w->shared_up_type;
+    lw.shared_up = w->shared_up;
+    lw.shared_down_type = w->shared_down_type;
+    lw.shared_down = w->shared_down;
+    lw.shared_gate_weight = w->shared_gate_weight;
+    if (!kq_launch_moe_supported(&d, &lw))
+        return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
+                       "device MoE needs Q8_0/Q4_K/Q6_K roles (gate=up types, shared like routed), "
+                       "hidden and intermediate in {256,512,1024,2048}, equal intermediates");
+    if (!aligned(w->routed_gate, 16u) || !aligned(w->routed_up, 16u) ||
+        !aligned(w->routed_down, 16u) || !aligned(w->shared_gate, 16u) ||
+        !aligned(w->shared_up, 16u) || !aligned(w->shared_down, 16u) || !aligned(out, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "MoE weights must be 16-byte aligned");
+    kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = kq_launch_moe_route(&d, w->router, w->shared_gate_weight, hidden, (uint32_t)tokens, &ws,
+                            c->d_status, c->stream);
+    if (e == hipSuccess)
+        e = kq_launch_moe_experts(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status,
+                                  c->stream);
+    if (e == hipSuccess && ids != NULL)
+        e = hipMemcpyAsync(ids, ws.ids, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice, c->stream);
+    return finish(c, e, "MoE execute launch", diag);
+}

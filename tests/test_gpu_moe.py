@@ -1,0 +1,201 @@
+"""Device parity for the MoE operator, through the C ABI, against the CPU
+oracle. Bars: router logits, probabilities, top-k ids and weights bit-exact
+(the device restates the CPU's arithmetic order); layer outputs within
+|gpu - ref| <= 1e-4 + 1e-3 * |ref|."""
+import numpy as np
+import pytest
+
+from conftest import hex_le_f32, load_golden, oracle_threads
+
+import kq_hip
+import kq_oracle
+import kq_synth as S
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+ROUTING = load_golden("moe_routing_vectors.json")
+ROLES = {"router": kq_oracle.F32, "gate": kq_oracle.Q4_K, "up": kq_oracle.Q4_K,
+         "down": kq_oracle.Q6_K, "shared_gate": kq_oracle.Q4_K, "shared_up": kq_oracle.Q4_K,
+         "shared_down": kq_oracle.Q6_K, "shared_gate_weight": kq_oracle.F32}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = kq_hip.Context(0)
+    yield c
+    c.close()
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def device_route(ctx, H, E, K, router, sgw, x):
+    T = x.shape[0]
+    cfg = kq_hip.MoeConfig(H, E, K, 256, 256)
+    n = cfg.scratch_bytes(T)
+    bufs = [ctx.upload(router), ctx.upload(sgw), ctx.upload(x), ctx.alloc(T * E * 4),
+            ctx.alloc(T * E * 4), ctx.alloc(T * K * 4), ctx.alloc(T * K * 4), ctx.alloc(n)]
+    dr, dsg, dx, dl, dp, di, dw, ds = bufs
+    ctx.moe_route(cfg, dr, dsg, dx, T, dl, dp, di, dw, ds, n)
+    out = (ctx.download(dl, np.float32, T * E).reshape(T, E),
+           ctx.download(dp, np.float32, T * E).reshape(T, E),
+           ctx.download(di, np.uint32, T * K).reshape(T, K),
+           ctx.download(dw, np.float32, T * K).reshape(T, K))
+    for b in bufs:
+        b.close()
+    cfg.close()
+    return out
+
+
+def oracle_route(H, E, K, router, x):
+    dims = dict(hidden=H, experts=E, top_k=K, inter=1, shared_inter=1)
+    res = [kq_oracle.moe_route(dims, (kq_oracle.F32, router), x[t]) for t in range(x.shape[0])]
+    return tuple(np.stack([r[i] for r in res]) for i in range(4))
+
+
+def assert_route_exact(got, want):
+    names = ("logits", "probabilities", "ids", "weights")
+    for n, g, w in zip(names, got, want):
+        assert np.array_equal(np.asarray(g).view(np.uint32), np.asarray(w).view(np.uint32)), n
+
+
+@pytest.mark.parametrize("case", ROUTING["cases"], ids=lambda c: c["id"])
+def test_tier_b_routing_vectors(ctx, case):
+    # research/operators/.../moe-routing-vectors.json: 512 experts, top-10,
+    # EXACT_DISCRETE ids; the device matches the oracle bit for bit.
+    cfg = ROUTING["config"]
+    H, E, K = cfg["hidden_size"], cfg["expert_count"], cfg["top_k"]
+    router = hex_le_f32(case["router_weight"]["le_hex"]).reshape(E, H)
+    x = hex_le_f32(case["input"]["le_hex"]).reshape(-1, H)
+    got = device_route(ctx, H, E, K, router, np.zeros(H, np.float32), x)
+    assert [list(map(int, r)) for r in got[2]] == case["expected"]["selected_expert_ids"]
+    assert_route_exact(got, oracle_route(H, E, K, router, x))
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("tokens", [1, 5])
+def test_routing_512x2048_bit_exact(ctx, seed, tokens):
+    H, E, K = 2048, 512, 10
+    router = S.normal_f32(S.stream_key(S.W_MOE, S.R_ROUTER, seed, 7), E * H, 0.02).reshape(E, H)
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, seed, tokens), tokens * H).reshape(tokens, H)
+    got = device_route(ctx, H, E, K, router, np.zeros(H, np.float32), x)
+    assert_route_exact(got, oracle_route(H, E, K, router, x))
+
+
+@pytest.mark.parametrize("pattern", ["duplicate-rows", "zero-router", "quantised-logits"])
+def test_routing_tie_heavy(ctx, pattern):
+    # Exact probability ties at and around the k-th boundary: the partial
+    # selection's eviction order decides which tied ids survive.
+    H, E, K = 64, 512, 10
+    rng = np.random.default_rng({"duplicate-rows": 1, "zero-router": 2, "quantised-logits": 3}[pattern])
+    if pattern == "duplicate-rows":
+        base = rng.standard_normal((8, H)).astype(np.float32)
+        router = base[rng.integers(0, 8, E)]
+    elif pattern == "zero-router":
+        router = np.zeros((E, H), np.float32)
+        router[rng.choice(E, 4, replace=False)] = 1.0
+    else:
+        router = (rng.integers(-2, 3, (E, H)) * 0.25).astype(np.float32)
+    x = np.ones((3, H), np.float32)
+    x[1] = rng.integers(-1, 2, H).astype(np.float32)
+    x[2, ::2] = 0.0
+    got = device_route(ctx, H, E, K, router, np.zeros(H, np.float32), x)
+    assert_route_exact(got, oracle_route(H, E, K, router, x))
+
+
+class Layer:
+    """MoE weights resident on the device plus their host copies."""
+
+    def __init__(self, ctx, workload, H, E, K, I):
+        self.H, self.E, self.K, self.I = H, E, K, I
+        self.w = S.moe_weights(workload, H, E, I, I)
+        self.bufs = {k: ctx.upload(v) for k, v in self.w.items()}
+        self.cfg = kq_hip.MoeConfig(H, E, K, I, I)
+        self.dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+
+    def run(self, ctx, x):
+        T = x.shape[0]
+        n = self.cfg.scratch_bytes(T)
+        scratch, dx = ctx.alloc(n), ctx.upload(x)
+        dout, dids = ctx.alloc(T * self.H * 4), ctx.alloc(T * self.K * 4)
+        ctx.moe_execute(self.cfg, kq_hip.moe_weights(self.bufs), dx, T, dout, dids, scratch, n)
+        out = ctx.download(dout, np.float32, T * self.H).reshape(T, self.H)
+        ids = ctx.download(dids, np.uint32, T * self.K).reshape(T, self.K)
+        for b in (scratch, dx, dout, dids):
+            b.close()
+        return out, ids
+
+    def oracle(self, x):
+        return kq_oracle.moe_execute(self.dims, {k: (t, self.w[k]) for k, t in ROLES.items()},
+                                     x, trace=True, threads=oracle_threads())
+
+
+@pytest.fixture(scope="module")
+def layer(ctx):
+    say("uploading 512-expert layer")
+    return Layer(ctx, S.W_MOE, 2048, 512, 10, 512)
+
+
+def test_moe_decode_one_token(ctx, layer):
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN), 2048)[None, :]
+    out, ids = layer.run(ctx, x)
+    ref, tr = layer.oracle(x)
+    assert np.array_equal(ids, tr["selected_ids"])
+    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("tokens", [2, 16])
+def test_moe_multi_token(ctx, layer, tokens):
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, tokens), tokens * 2048).reshape(tokens, 2048)
+    out, ids = layer.run(ctx, x)
+    ref, tr = layer.oracle(x)
+    assert np.array_equal(ids, tr["selected_ids"])
+    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+
+
+def test_moe_repeated_calls_identical(ctx, layer):
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 99), 2048)[None, :]
+    a, ia = layer.run(ctx, x)
+    b, ib = layer.run(ctx, x)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and np.array_equal(ia, ib)
+
+
+def test_moe_small_formats(ctx):
+    # Q8_0 gate/up with Q4_K down at reduced dims.
+    H, E, K, I = 512, 32, 4, 256
+    w = S.moe_weights(S.W_MOE + 7, H, E, I, I, gate_fmt="Q8_0", down_fmt="Q4_K")
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    x = S.normal_f32(S.stream_key(S.W_MOE + 7, S.R_HIDDEN), 3 * H).reshape(3, H)
+    n = cfg.scratch_bytes(3)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(3 * H * 4), ctx.alloc(3 * K * 4)
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, kq_hip.TYPE_Q8_0, kq_hip.TYPE_Q4_K), dx, 3,
+                    dout, dids, scratch, n)
+    out = ctx.download(dout, np.float32, 3 * H).reshape(3, H)
+    roles = dict(ROLES, gate=kq_oracle.Q8_0, up=kq_oracle.Q8_0, shared_gate=kq_oracle.Q8_0,
+                 shared_up=kq_oracle.Q8_0, down=kq_oracle.Q4_K, shared_down=kq_oracle.Q4_K)
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in roles.items()}, x, trace=True)
+    assert np.array_equal(ctx.download(dids, np.uint32, 3 * K).reshape(3, K), tr["selected_ids"])
+    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+
+
+def test_moe_fails_closed(ctx, layer):
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 5), 2048)[None, :].copy()
+    x[0, 3] = np.inf
+    with pytest.raises(kq_hip.KqError) as e:
+        layer.run(ctx, x)
+    assert e.value.name == "NUMERIC_DOMAIN"
+    n = layer.cfg.scratch_bytes(1)
+    scratch, dx, dout = ctx.alloc(n), ctx.upload(x), ctx.alloc(2048 * 4)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.moe_execute(layer.cfg, kq_hip.moe_weights(layer.bufs), dx, 1, dout, None, scratch,
+                        n - 256)
+    assert e.value.name == "BUFFER_TOO_SMALL"
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.moe_execute(layer.cfg, kq_hip.moe_weights(layer.bufs), dx, 1, dx, None, scratch, n)
+    assert e.value.name == "ALIASING_VIOLATION"
+    # and the layer still runs correctly afterwards
+    test_moe_decode_one_token(ctx, layer)

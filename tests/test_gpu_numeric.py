@@ -1,0 +1,248 @@
+"""Device parity for the numeric core, through the C ABI, against the CPU
+oracle on identical seeded inputs.
+
+Bars: dequantized weights bit-exact; matvec / LM-head outputs within
+|gpu - ref| <= 1e-4 + 1e-3 * |ref| (fp32 accumulation in a different order);
+argmax token ids exact; device expf bit-exact on all 2^32 inputs."""
+import numpy as np
+import pytest
+
+from conftest import bits_f32, load_golden, oracle_threads
+
+import kq_hip
+import kq_oracle
+import kq_synth as S
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+NUM = load_golden("numeric_vectors.json")
+FMTS = {"Q4_K": kq_hip.TYPE_Q4_K, "Q8_0": kq_hip.TYPE_Q8_0, "Q6_K": kq_hip.TYPE_Q6_K}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = kq_hip.Context(0)
+    yield c
+    c.close()
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def gpu_dequant(ctx, type_id, packed):
+    be, bb = kq_hip.geometry(type_id)
+    n = packed.size // bb * be
+    dp = ctx.upload(packed)
+    do = ctx.alloc(n * 4)
+    cnt = ctx.dequantize(type_id, dp, packed.size, do, n)
+    assert cnt == n
+    out = ctx.download(do, np.float32, n)
+    dp.close()
+    do.close()
+    return out
+
+
+@pytest.mark.parametrize("case", [c for c in NUM["cases"] if c["type"] in FMTS],
+                         ids=lambda c: c["id"])
+def test_dequant_golden_vectors(ctx, case):
+    packed = np.frombuffer(bytes.fromhex(case["packed_hex"]), np.uint8).copy()
+    got = gpu_dequant(ctx, FMTS[case["type"]], packed)
+    want = bits_f32(case["expected_f32_bits"])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+def test_dequant_64m_weights_bit_exact(ctx, fmt):
+    # 67,108,864 weights per format, same seeded blocks as the oracle.
+    gen, qk, bb = S.BLOCK_GEN[fmt]
+    blocks = (1 << 26) // qk
+    say(f"dequant {fmt}: {blocks} blocks")
+    packed = gen(S.stream_key(S.W_DEQUANT, S.R_WEIGHT, FMTS[fmt]), blocks).reshape(-1)
+    got = gpu_dequant(ctx, FMTS[fmt], packed)
+    want = kq_oracle.dequantize(FMTS[fmt], packed)
+    bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:5]}"
+
+
+def test_dequant_subnormal_and_edge_scales(ctx):
+    # Q4_K blocks whose d/dmin are fp16 subnormals, zero, negative zero and
+    # the largest finite half; Q6_K/Q8_0 with subnormal d.
+    blocks = S.q4k_blocks(S.stream_key(S.W_DEQUANT, 50), 64)
+    halves = np.array([0x0001, 0x03FF, 0x8001, 0x0000, 0x8000, 0x7BFF, 0xFBFF, 0x0400],
+                      np.uint16)
+    for i in range(64):
+        blocks[i, 0:2] = np.frombuffer(halves[i % 8].tobytes(), np.uint8)
+        blocks[i, 2:4] = np.frombuffer(halves[(i // 8) % 8].tobytes(), np.uint8)
+    p = blocks.reshape(-1)
+    assert np.array_equal(gpu_dequant(ctx, kq_hip.TYPE_Q4_K, p).view(np.uint32),
+                          kq_oracle.dequantize(kq_oracle.Q4_K, p).view(np.uint32))
+    q6 = S.q6k_blocks(S.stream_key(S.W_DEQUANT, 51), 8)
+    q8 = S.q8_0_blocks(S.stream_key(S.W_DEQUANT, 52), 8)
+    for i in range(8):
+        q6[i, 208:210] = np.frombuffer(halves[i].tobytes(), np.uint8)
+        q8[i, 0:2] = np.frombuffer(halves[i].tobytes(), np.uint8)
+    for t, b in ((kq_hip.TYPE_Q6_K, q6), (kq_hip.TYPE_Q8_0, q8)):
+        p = b.reshape(-1)
+        assert np.array_equal(gpu_dequant(ctx, t, p).view(np.uint32),
+                              kq_oracle.dequantize(t, p).view(np.uint32))
+
+
+def test_dequant_fails_closed(ctx):
+    q8 = S.q8_0_blocks(S.stream_key(S.W_DEQUANT, 53), 4)
+    q8[2, 0:2] = [0x00, 0x7C]  # +Inf scale
+    with pytest.raises(kq_hip.KqError) as e:
+        gpu_dequant(ctx, kq_hip.TYPE_Q8_0, q8.reshape(-1))
+    assert e.value.name == "MALFORMED_QUANTIZED_DATA"
+    dp = ctx.upload(np.zeros(144 * 2, np.uint8))
+    do = ctx.alloc(256 * 4)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.dequantize(kq_hip.TYPE_Q4_K, dp, 288, do, 256)  # room for one block only
+    assert e.value.name == "BUFFER_TOO_SMALL"
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.dequantize(kq_hip.TYPE_Q4_K, dp, 200, do, 256)  # partial block
+    assert e.value.name == "MALFORMED_QUANTIZED_DATA"
+    # the context stays usable after device-detected failures
+    ok = S.q8_0_blocks(S.stream_key(S.W_DEQUANT, 54), 2).reshape(-1)
+    assert np.array_equal(gpu_dequant(ctx, kq_hip.TYPE_Q8_0, ok).view(np.uint32),
+                          kq_oracle.dequantize(kq_oracle.Q8_0, ok).view(np.uint32))
+
+
+def test_expf_bit_exact_all_inputs(ctx):
+    # Device expf against the oracle's (which equals libm expf on every
+    # pattern, see test_oracle_numeric) over all 2^32 bit patterns.
+    chunk = 1 << 27
+    din = ctx.alloc(chunk * 4)
+    dout = ctx.alloc(chunk * 4)
+    th = oracle_threads()
+    for start in range(0, 1 << 32, chunk):
+        if start % (1 << 30) == 0:
+            say(f"expf chunk at {start:#x}")
+        x = np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        d = kq_hip.Diagnostic()
+        kq_hip.check(kq_hip.lib().kq_hip_upload(ctx._h, kq_hip.C.c_void_p(din.ptr),
+                                                x.ctypes.data, x.nbytes, kq_hip.C.byref(d)), d)
+        ctx.expf(din, chunk, dout)
+        got = ctx.download(dout, np.float32, chunk)
+        want = kq_oracle.expf_array(x, th)
+        gb, wb = got.view(np.uint32), want.view(np.uint32)
+        diff = gb != wb
+        if diff.any():
+            both_nan = np.isnan(got) & np.isnan(want)
+            diff &= ~both_nan
+        assert not diff.any(), f"expf mismatch at {x[diff][:4]}"
+
+
+def matvec_case(ctx, fmt, rows, cols, batch, key):
+    t = FMTS[fmt]
+    w = S.quant_matrix(fmt, key, rows, cols)
+    x = S.normal_f32(key ^ 0x55, batch * cols).reshape(batch, cols)
+    dw, dx = ctx.upload(w), ctx.upload(x)
+    dy = ctx.alloc(rows * batch * 4)
+    ctx.matvec(t, dw, rows, cols, dx, batch, dy)
+    got = ctx.download(dy, np.float32, rows * batch).reshape(batch, rows)
+    want = kq_oracle.matvec(t, w, rows, cols, x, threads=oracle_threads())
+    for b in (dw, dx, dy):
+        b.close()
+    return got, want
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+def test_matvec_4096x2048_batch1(ctx, fmt):
+    got, want = matvec_case(ctx, fmt, 4096, 2048, 1, S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+@pytest.mark.parametrize("rows,cols,batch", [(1, 256, 1), (7, 512, 2), (33, 1024, 3),
+                                             (4097, 2048, 4), (5, 2048, 8), (300, 256, 4)])
+def test_matvec_shapes(ctx, fmt, rows, cols, batch):
+    got, want = matvec_case(ctx, fmt, rows, cols, batch,
+                            S.stream_key(S.W_MATVEC_Q6K, rows, cols, batch))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("cols", [32, 64, 128])
+def test_matvec_q8_short_rows(ctx, cols):
+    got, want = matvec_case(ctx, "Q8_0", 130, cols, 2, S.stream_key(S.W_MATVEC_Q8_0, cols))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("case", [c for c in NUM["row_dot_cases"] if c["type"] in FMTS],
+                         ids=lambda c: c["id"])
+def test_row_dot_golden(ctx, case):
+    src = {c["id"]: c for c in NUM["cases"]}[case["source_case_id"]]
+    packed = np.frombuffer(bytes.fromhex(src["packed_hex"]), np.uint8).copy()
+    x = bits_f32(case["activation_f32_bits"])
+    dp, dx, do = ctx.upload(packed), ctx.upload(x), ctx.alloc(4)
+    ctx.row_dot(FMTS[case["type"]], dp, packed.size, dx, x.size, do)
+    got = ctx.download(do, np.float32, 1)[0]
+    want = bits_f32(case["expected_f32_bits"])[0]
+    assert abs(float(got) - float(want)) <= ATOL + RTOL * abs(float(want))
+
+
+def test_matvec_fails_closed(ctx):
+    w = S.quant_matrix("Q4_K", S.stream_key(S.W_MATVEC_Q4K, 77), 16, 512)
+    x = S.normal_f32(S.stream_key(S.W_MATVEC_Q4K, 78), 512)
+    x_bad = x.copy()
+    x_bad[100] = np.nan
+    dw, dx, dxb, dy = ctx.upload(w), ctx.upload(x), ctx.upload(x_bad), ctx.alloc(16 * 4)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q4_K, dw, 16, 512, dxb, 1, dy)
+    assert e.value.name == "NUMERIC_DOMAIN"
+    w_bad = w.copy().reshape(-1, 144)
+    w_bad[5, 0:2] = [0x00, 0xFC]  # -Inf d
+    dwb = ctx.upload(w_bad.reshape(-1))
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q4_K, dwb, 16, 512, dx, 1, dy)
+    assert e.value.name == "MALFORMED_QUANTIZED_DATA"
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q4_K, dw, 16, 512, dx, 1, dy, capacity=15)
+    assert e.value.name == "BUFFER_TOO_SMALL"
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q4_K, dw, 16, 500, dx, 1, dy)
+    assert e.value.name == "DIMENSION_MISMATCH"
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q4_K, dw, 16, 512, dw, 1, dw.ptr + 64)
+    assert e.value.name == "ALIASING_VIOLATION"
+    ctx.matvec(kq_hip.TYPE_Q4_K, dw, 16, 512, dx, 1, dy)  # still usable
+
+
+def test_argmax_exact(ctx):
+    rng = np.random.default_rng(9)
+    v = rng.standard_normal((3, 151936)).astype(np.float32)
+    v[1, 5000] = v[1, 90000] = v[1].max() + 1  # tie -> lower id
+    v[2, :] = 0.0
+    v[2, 77] = -0.0  # +0 and -0 compare equal: first occurrence wins
+    dv, di = ctx.upload(v), ctx.alloc(3 * 4)
+    ctx.argmax(dv, 151936, 3, di)
+    got = ctx.download(di, np.uint32, 3)
+    assert list(got) == [kq_oracle.argmax(v[b]) for b in range(3)] == [int(np.argmax(v[0])), 5000, 0]
+    v[0, 10] = np.inf
+    dv2 = ctx.upload(v)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.argmax(dv2, 151936, 3, di)
+    assert e.value.name == "NUMERIC_DOMAIN"
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_lm_head_q6k_151936x2048(ctx, batch):
+    V, H = 151936, 2048
+    say(f"lm head batch {batch}")
+    w = S.quant_matrix("Q6_K", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT), V, H)
+    h = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, batch), batch * H).reshape(batch, H)
+    dw, dh = ctx.upload(w), ctx.upload(h)
+    dl, di = ctx.alloc(V * batch * 4), ctx.alloc(batch * 4)
+    ctx.lm_head(kq_hip.TYPE_Q6_K, dw, V, H, dh, batch, dl, di)
+    logits = ctx.download(dl, np.float32, V * batch).reshape(batch, V)
+    ids = ctx.download(di, np.uint32, batch)
+    ref = kq_oracle.matvec(kq_oracle.Q6_K, w, V, H, h, threads=oracle_threads())
+    np.testing.assert_allclose(logits, ref, rtol=RTOL, atol=ATOL)
+    for b in range(batch):
+        # exact on the device's own logits; equal to the CPU's where the
+        # CPU top-2 margin exceeds the tolerance
+        assert ids[b] == int(np.argmax(logits[b]))
+        top2 = np.sort(ref[b])[-2:]
+        if top2[1] - top2[0] > ATOL + RTOL * abs(top2[1]):
+            assert ids[b] == kq_oracle.argmax(ref[b])
