@@ -1,0 +1,407 @@
+"""Benchmark of the MI355X quantized-weight path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME|all]
+                    [--no-cpu] [--no-graph]
+
+A step is one pass of the hot path over one batch of synthetic input with the
+weights already resident in HBM. The headline workload (value / metric) is
+the Q4_K dequant-fused matvec y = W x, W 4096 x 2048 (4,718,592 packed bytes),
+batch 1; `value` is algorithmic HBM bytes per step / time per step in GB/s.
+The same JSON line carries every other workload (Q8_0 / Q6_K matvecs,
+64M-weight dequant, 512-expert top-10 MoE decode in tokens/s, the Q6_K
+151936 x 2048 LM head with argmax at batch 1 and 4, MoE prefill T=512),
+the roofline of the headline kernel and the CPU baseline (the C oracle,
+timed on this host on a bounded sample).
+
+Timing: W untimed warmup steps, then K steps captured into a HIP graph on the
+library's stream and replayed between two HIP events on that stream, with
+device synchronisation on both sides. Weight replicas (bit-identical device
+copies at distinct addresses) rotate so that the bytes touched between two
+uses of a replica exceed 512 MB, twice the ~256 MB Infinity Cache: every
+weight read is an HBM read.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kestrel-q_amd"))
+
+import kq_hip  # noqa: E402
+import kq_synth as S  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MALL_DEFEAT_BYTES = 512 << 20
+
+# ---------------------------------------------------------------- HIP runtime
+_hip = None
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so")
+        _hip.hipEventCreate.argtypes = [C.c_void_p]
+        _hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        _hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        _hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        _hip.hipEventDestroy.argtypes = [C.c_void_p]
+        _hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        _hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.c_void_p]
+        _hip.hipGraphInstantiate.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                             C.c_size_t]
+        _hip.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        _hip.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        _hip.hipGraphDestroy.argtypes = [C.c_void_p]
+        _hip.hipStreamSynchronize.argtypes = [C.c_void_p]
+        _hip.hipDeviceSynchronize.argtypes = []
+        _hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    return _hip
+
+
+def hcheck(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with hipError {rc}")
+
+
+class Events:
+    def __init__(self):
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        hcheck(hip().hipEventCreate(C.byref(self.a)), "hipEventCreate")
+        hcheck(hip().hipEventCreate(C.byref(self.b)), "hipEventCreate")
+
+    def ms(self) -> float:
+        hcheck(hip().hipEventSynchronize(self.b), "hipEventSynchronize")
+        v = C.c_float()
+        hcheck(hip().hipEventElapsedTime(C.byref(v), self.a, self.b), "hipEventElapsedTime")
+        return v.value
+
+    def close(self):
+        hip().hipEventDestroy(self.a)
+        hip().hipEventDestroy(self.b)
+
+
+def d2d(ctx, dst, src, nbytes):
+    hcheck(hip().hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), nbytes, 3,
+                                C.c_void_p(ctx.stream)), "hipMemcpyAsync")
+
+
+def time_steps(ctx, step, warmup: int, steps: int, graph: bool) -> float:
+    """ms per step over `steps` steps; `step(i)` enqueues step i on ctx's stream."""
+    stream = C.c_void_p(ctx.stream)
+    ctx.set_async(True)
+    for i in range(warmup):
+        step(i)
+    ctx.synchronize()
+    hcheck(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+    ev = Events()
+    if graph:
+        g, ge = C.c_void_p(), C.c_void_p()
+        hcheck(hip().hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+        for i in range(steps):
+            step(warmup + i)
+        hcheck(hip().hipStreamEndCapture(stream, C.byref(g)), "hipStreamEndCapture")
+        hcheck(hip().hipGraphInstantiate(C.byref(ge), g, None, None, 0), "hipGraphInstantiate")
+        hcheck(hip().hipGraphLaunch(ge, stream), "hipGraphLaunch")  # untimed replay
+        hcheck(hip().hipStreamSynchronize(stream), "hipStreamSynchronize")
+        hcheck(hip().hipEventRecord(ev.a, stream), "hipEventRecord")
+        hcheck(hip().hipGraphLaunch(ge, stream), "hipGraphLaunch")
+        hcheck(hip().hipEventRecord(ev.b, stream), "hipEventRecord")
+        ms = ev.ms()
+        hip().hipGraphExecDestroy(ge)
+        hip().hipGraphDestroy(g)
+    else:
+        hcheck(hip().hipEventRecord(ev.a, stream), "hipEventRecord")
+        for i in range(steps):
+            step(warmup + i)
+        hcheck(hip().hipEventRecord(ev.b, stream), "hipEventRecord")
+        ms = ev.ms()
+    hcheck(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+    ev.close()
+    ctx.synchronize()  # reports any device-detected failure
+    ctx.set_async(False)
+    return ms / steps
+
+
+def replicas(ctx, host: np.ndarray, want_bytes: int, cap: int = 256):
+    """Bit-identical device copies of `host` at distinct addresses."""
+    n = max(1, min(cap, -(-want_bytes // max(1, host.nbytes))))
+    first = ctx.upload(host)
+    out = [first]
+    for _ in range(n - 1):
+        b = ctx.alloc(host.nbytes)
+        d2d(ctx, b.ptr, first.ptr, host.nbytes)
+        out.append(b)
+    ctx.synchronize()
+    return out
+
+
+# ---------------------------------------------------------------- workloads
+def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph):
+    t = kq_hip.TYPE_IDS[fmt]
+    w = S.quant_matrix(fmt, S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT), rows, cols)
+    x = S.normal_f32(S.stream_key(S.W_MATVEC_Q4K, S.R_X), batch * cols)
+    reps = replicas(ctx, w, MALL_DEFEAT_BYTES)
+    dx, dy = ctx.upload(x), ctx.alloc(rows * batch * 4)
+    ms = time_steps(ctx, lambda i: ctx.matvec(t, reps[i % len(reps)], rows, cols, dx, batch, dy),
+                    warmup, steps, graph)
+    nbytes = w.nbytes + x.nbytes + rows * batch * 4
+    for b in reps + [dx, dy]:
+        b.close()
+    return {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
+            "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "replicas": len(reps),
+            "flops_per_step": 2 * rows * cols * batch}
+
+
+def wl_dequant(ctx, fmt, warmup, steps, graph):
+    t = kq_hip.TYPE_IDS[fmt]
+    gen, qk, bb = S.BLOCK_GEN[fmt]
+    blocks = (1 << 26) // qk
+    w = gen(S.stream_key(S.W_DEQUANT, S.R_WEIGHT, t), blocks).reshape(-1)
+    reps = replicas(ctx, w, 2 * w.nbytes, cap=2)
+    n = blocks * qk
+    out = ctx.alloc(n * 4)
+    ms = time_steps(ctx, lambda i: ctx.dequantize(t, reps[i % len(reps)], w.nbytes, out, n),
+                    warmup, steps, graph)
+    nbytes = w.nbytes + n * 4
+    for b in reps + [out]:
+        b.close()
+    return {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
+            "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "weights": n}
+
+
+def moe_layer(ctx, H=2048, E=512, K=10, I=512):
+    w = S.moe_weights(S.W_MOE, H, E, I, I)
+    return w, kq_hip.MoeConfig(H, E, K, I, I)
+
+
+def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache):
+    H, E, K, I = 2048, 512, 10, 512
+    if "w" not in layer_cache:
+        layer_cache["w"], layer_cache["cfg"] = moe_layer(ctx)
+    w, cfg = layer_cache["w"], layer_cache["cfg"]
+    layer_bytes = sum(v.nbytes for v in w.values())
+    # bytes touched per decode step ~26.6 MB; rotate whole-layer replicas so
+    # a replica's router/shared/expert rows are not MALL-resident on reuse
+    touched = 4_194_304 + (K + 1) * 2_039_808 + 8192 if tokens == 1 else layer_bytes
+    nrep = max(2, min(24, -(-MALL_DEFEAT_BYTES // touched)))
+    if tokens > 1:
+        nrep = 1
+    layers = []
+    for r in range(nrep):
+        if r == 0:
+            bufs = {k: ctx.upload(v) for k, v in w.items()}
+        else:
+            bufs = {}
+            for k, v in w.items():
+                b = ctx.alloc(v.nbytes)
+                d2d(ctx, b.ptr, layers[0][k].ptr, v.nbytes)
+                bufs[k] = b
+        layers.append(bufs)
+    ctx.synchronize()
+    mw = [kq_hip.moe_weights(b) for b in layers]
+    ntok_inputs = 16
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 1000 + tokens),
+                     ntok_inputs * tokens * H).reshape(ntok_inputs, tokens * H)
+    dxs = [ctx.upload(x[j]) for j in range(ntok_inputs)]
+    n = cfg.scratch_bytes(tokens)
+    scratch = ctx.alloc(n)
+    out = ctx.alloc(tokens * H * 4)
+
+    def step(i):
+        ctx.moe_execute(cfg, mw[i % nrep], dxs[i % ntok_inputs], tokens, out, None, scratch, n)
+
+    ms = time_steps(ctx, step, warmup, steps, graph)
+    for bufs in layers:
+        for b in bufs.values():
+            b.close()
+    for b in dxs + [scratch, out]:
+        b.close()
+    if tokens == 1:
+        nbytes = touched + H * 4 * 2
+    else:
+        nbytes = layer_bytes + 2 * tokens * H * 4
+    return {"ms_per_step": ms, "tokens_per_s": tokens / ms * 1e3, "bytes_per_step": nbytes,
+            "GBps": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "layer_replicas": nrep, "tokens": tokens}
+
+
+def wl_lm_head(ctx, batch, warmup, steps, graph):
+    V, H = 151936, 2048
+    w = S.quant_matrix("Q6_K", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT), V, H)
+    h = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, batch), batch * H)
+    reps = replicas(ctx, w, MALL_DEFEAT_BYTES + w.nbytes, cap=3)
+    dh, dl, di = ctx.upload(h), ctx.alloc(V * batch * 4), ctx.alloc(batch * 4)
+    ms = time_steps(ctx, lambda i: ctx.lm_head(kq_hip.TYPE_Q6_K, reps[i % len(reps)], V, H, dh,
+                                               batch, dl, di), warmup, steps, graph)
+    nbytes = w.nbytes + h.nbytes + V * batch * 4
+    for b in reps + [dh, dl, di]:
+        b.close()
+    return {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
+            "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "tokens_per_s": batch / ms * 1e3,
+            "replicas": len(reps)}
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(threads: int, budget_s: float = 3.0) -> dict:
+    """The C oracle (restatement of the reference's scalar path, reference fp
+    flags) on this host: the headline matvec at 1 thread and `threads`
+    threads with identical per-row arithmetic, plus one MoE decode step and
+    one LM-head step."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import kq_oracle as O
+
+    def timeit(fn, budget):
+        fn()
+        ts = []
+        t_end = time.perf_counter() + budget
+        while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 50):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)), len(ts)
+
+    res = {}
+    w = S.quant_matrix("Q4_K", S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT), 4096, 2048)
+    x = S.normal_f32(S.stream_key(S.W_MATVEC_Q4K, S.R_X), 2048)[None, :]
+    nbytes = w.nbytes + x.nbytes + 4096 * 4
+    for th in sorted({1, threads}):
+        s, n = timeit(lambda: O.matvec(O.Q4_K, w, 4096, 2048, x, threads=th), budget_s)
+        res[f"q4k_matvec_{th}t"] = {"s_per_step": s, "GBps": nbytes / s / 1e9, "runs": n}
+    wts, _ = moe_layer(None)
+    roles = {"router": O.F32, "gate": O.Q4_K, "up": O.Q4_K, "down": O.Q6_K,
+             "shared_gate": O.Q4_K, "shared_up": O.Q4_K, "shared_down": O.Q6_K,
+             "shared_gate_weight": O.F32}
+    dims = dict(hidden=2048, experts=512, top_k=10, inter=512, shared_inter=512)
+    xm = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 1001), 2048)[None, :]
+    wr = {k: (t, wts[k]) for k, t in roles.items()}
+    for th in sorted({1, threads}):
+        s, n = timeit(lambda: O.moe_execute(dims, wr, xm, threads=th), budget_s)
+        res[f"moe_decode_{th}t"] = {"s_per_step": s, "tokens_per_s": 1.0 / s, "runs": n}
+    wl = S.quant_matrix("Q6_K", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT), 151936, 2048)
+    hl = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, 1), 2048)[None, :]
+    for th in sorted({1, threads}):
+        s, n = timeit(lambda: O.argmax(O.matvec(O.Q6_K, wl, 151936, 2048, hl, threads=th)[0]),
+                      budget_s if th > 1 else 0.0)
+        res[f"lm_head_b1_{th}t"] = {"s_per_step": s, "tokens_per_s": 1.0 / s, "runs": n}
+    return res
+
+
+def cpu_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------- main
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+    graph = not args.no_graph
+    K, W = args.steps, args.warmup
+    wanted = args.workload
+    work = {}
+    with kq_hip.Context(0) as ctx:
+        def run(name, fn):
+            if wanted in ("all", name) or (wanted == "headline" and name == HEADLINE):
+                print(f"[bench] {name} ...", file=sys.stderr, flush=True)
+                t0 = time.time()
+                work[name] = fn()
+                work[name]["wall_s"] = round(time.time() - t0, 2)
+                print(f"[bench] {name}: {json.dumps(work[name])}", file=sys.stderr, flush=True)
+
+        HEADLINE = "q4k_matvec_4096x2048_b1"
+        run(HEADLINE, lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph))
+        run("q8_0_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q8_0", 4096, 2048, 1, W, K, graph))
+        run("q6k_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q6_K", 4096, 2048, 1, W, K, graph))
+        for f in ("Q4_K", "Q8_0", "Q6_K"):
+            run(f"dequant_64m_{f.lower()}",
+                lambda f=f: wl_dequant(ctx, f, 3, max(5, K // 20), graph))
+        cache = {}
+        run("moe_decode_1tok", lambda: wl_moe(ctx, 1, W, K, graph, cache))
+        run("lm_head_q6k_151936x2048_b1", lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph))
+        run("lm_head_q6k_151936x2048_b4", lambda: wl_lm_head(ctx, 4, 3, max(10, K // 10), graph))
+        run("moe_prefill_512", lambda: wl_moe(ctx, 512, 1, 3, graph, cache))
+    head = work.get(HEADLINE)
+    threads = int(os.environ.get("KQ_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        t0 = time.time()
+        cpu = cpu_baseline(threads)
+        print(f"[bench] cpu baseline done in {time.time() - t0:.1f}s: {json.dumps(cpu)}",
+              file=sys.stderr, flush=True)
+    line = {
+        "metric": "quant matvec HBM GB/s (% of ~8 TB/s peak); MoE-layer decode tokens/s",
+        "value": round(head["GBps"], 2) if head else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(head["ms_per_step"], 6) if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, fp32 activations/accumulation",
+        "data": "synthetic (seeded SplitMix64 GGUF blocks, N(0,1) activations)",
+        "config": {"workload": HEADLINE, "rows": 4096, "cols": 2048, "batch": 1,
+                   "format": "Q4_K", "timing": "hip graph of K launches, hip events" if graph
+                   else "stream launches, hip events"},
+        "hbm_frac": round(head["hbm_frac"], 4) if head else None,
+        "moe_decode_tokens_per_s": round(work["moe_decode_1tok"]["tokens_per_s"], 1)
+        if "moe_decode_1tok" in work else None,
+        "roofline": None,
+        "cpu_baseline": None,
+        "workloads": work,
+    }
+    if head:
+        line["roofline"] = {"bound": "hbm", "achieved": round(head["GBps"], 2),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(head["GBps"] / HBM_PEAK_GBS, 4),
+                            "traffic": traffic_from_profiles(HEADLINE)}
+    if cpu:
+        key = f"q4k_matvec_{threads}t"
+        line["cpu_baseline"] = {"value": round(cpu[key]["GBps"], 4), "unit": "GB/s",
+                                "cores": threads, "kind": "port",
+                                "sample": "the same 4096x2048 Q4_K matvec, median of repeated "
+                                          "full runs (C oracle, reference fp flags, row-parallel "
+                                          f"OpenMP); CPU: {cpu_name()}",
+                                "runs": cpu}
+    print(json.dumps(line))
+    return 0
+
+
+def traffic_from_profiles(workload: str):
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(workload, {}).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void dequant_q8_0(const uint8_t *__restri
             const uint8_t *p = packed + blk * 34u;
             const float d = kq_f16_to_f32(*(const uint16_t *)p);
             bad |= !kq_isfinite(d);
-            const uint32_t c = kq_load4_u2a(p + 2u + 4u * (lane & 7u), end);
+            const uint32_t c = kq_load4_u2a_end(p + 2u + 4u * (lane & 7u), end);
             store4(out + blk * 32u + 4u * (lane & 7u),
                    (float)(int8_t)(c & 0xffu) * d, (float)(int8_t)((c >> 8) & 0xffu) * d,
                    (float)(int8_t)((c >> 16) & 0xffu) * d, (float)(int8_t)(c >> 24) * d);
@@ -94,7 +94,6 @@ __global__ __launch_bounds__(kThreads) void dequant_q6k(const uint8_t *__restric
     const uint32_t lane = threadIdx.x & 63u;
     const uint64_t wave = ((uint64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
     const uint64_t nwaves = ((uint64_t)gridDim.x * kThreads) >> 6;
-    const uint8_t *end = packed + blocks * 210u;
     const uint32_t n = lane >> 5, quarter = (lane >> 3) & 3u, l0 = 4u * (lane & 7u);
     const uint32_t ql_off = 64u * n + l0 + ((quarter & 1u) ? 32u : 0u);
     const uint32_t nib_shift = quarter >= 2u ? 4u : 0u;
@@ -105,8 +104,8 @@ __global__ __launch_bounds__(kThreads) void dequant_q6k(const uint8_t *__restric
         const uint8_t *p = packed + blk * 210u;
         const float d = kq_f16_to_f32(*(const uint16_t *)(p + 208u));
         bad |= !kq_isfinite(d);
-        const uint32_t ql = kq_load4_u2a(p + ql_off, end);
-        const uint32_t qh = kq_load4_u2a(p + qh_off, end);
+        const uint32_t ql = kq_load4_u2a(p + ql_off);
+        const uint32_t qh = kq_load4_u2a(p + qh_off);
         const float ds = d * (float)(int8_t)p[sc_off];
         const uint32_t c = ((ql >> nib_shift) & 0x0f0f0f0fu) |
                            (((qh >> (2u * quarter)) & 0x03030303u) << 4);

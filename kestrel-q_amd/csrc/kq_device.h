@@ -133,49 +133,107 @@ __device__ __forceinline__ void kq_k_scale(uint32_t j, uint32_t w0, uint32_t w1,
 }
 
 /*
- * Byte loads from addresses that are only 2-byte aligned (Q8_0 blocks are
- * 34 B and Q6_K blocks 210 B, so a block can start at 2 mod 4). The dwords
- * covering the span are read at 4-byte aligned addresses and re-aligned with
- * a byte funnel shift. `end` is one past the last valid byte of the buffer:
- * no dword that starts at or beyond it is read, and the final dword is
- * replaced by a 16-bit read when only two of its bytes are in bounds.
+ * Raw buffer loads: a 128-bit resource (base, byte count) in scalar
+ * registers plus a 32-bit per-lane offset, so a row walk costs one 32-bit
+ * add per row instead of 64-bit per-lane address arithmetic. Dwords whose
+ * offset lies at or beyond the byte count read as zero without touching
+ * memory. Word 3 = 0x00020000 is the raw-buffer format of the gfx9 family.
  */
-__device__ __forceinline__ uint32_t kq_ld32_guard(const uint8_t *p,
-                                                  const uint8_t *end) {
-    if (p + 4 <= end) return *(const uint32_t *)p;
-    if (p + 2 <= end) return (uint32_t)(*(const uint16_t *)p);
-    return 0u;
+struct KqBuf {
+    __amdgpu_buffer_rsrc_t r;
+};
+
+__device__ __forceinline__ KqBuf kq_buf(const void *base, uint32_t bytes) {
+    KqBuf b;
+    b.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                            0x00020000);
+    return b;
 }
 
+typedef unsigned int kq_u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int kq_u32x3 __attribute__((ext_vector_type(3)));
+typedef unsigned int kq_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 kq_ld128(KqBuf b, uint32_t voff, uint32_t soff) {
+    const kq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)voff, (int)soff, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ kq_u32x3 kq_ld96(KqBuf b, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b96(b.r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ kq_u32x2 kq_ld64(KqBuf b, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ uint32_t kq_ld32(KqBuf b, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ uint32_t kq_ld16(KqBuf b, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.r, (int)voff, (int)soff, 0);
+}
+
+/*
+ * Byte loads from addresses that are only 2-byte aligned (Q8_0 blocks are
+ * 34 B and Q6_K blocks 210 B, so a block can start at 2 mod 4). The dwords
+ * covering the span are read at 4-byte aligned addresses (the buffer start
+ * is 4-byte aligned, so a - (a & 3) never precedes it) and re-aligned with
+ * a byte funnel shift. The pointer arithmetic keeps the global address
+ * space, so these stay global (not flat) loads.
+ */
 __device__ __forceinline__ uint32_t kq_align2(uint32_t hi, uint32_t lo,
                                               uint32_t shift_bytes) {
     return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }
 
-/* 8 bytes at a 2-byte aligned address a (a < end). */
-__device__ __forceinline__ uint2 kq_load8_u2a(const uint8_t *a,
-                                              const uint8_t *end) {
-    uintptr_t ua = (uintptr_t)a;
-    const uint8_t *base = (const uint8_t *)(ua & ~(uintptr_t)3);
-    uint32_t sh = (uint32_t)(ua & 3u);
-    uint32_t d0 = *(const uint32_t *)base;
-    uint32_t d1 = *(const uint32_t *)(base + 4);
-    uint32_t d2 = sh ? kq_ld32_guard(base + 8, end) : 0u;
+/* 8 bytes at a (a even). Reads [a - (a&3), a - (a&3) + (a&3 ? 12 : 8)):
+ * at most 2 bytes past a + 8. */
+__device__ __forceinline__ uint2 kq_load8_u2a(const uint8_t *a) {
+    const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);
+    const uint32_t *base = (const uint32_t *)(a - sh);
+    const uint32_t d0 = base[0], d1 = base[1];
+    const uint32_t d2 = base[sh ? 2 : 1];
     uint2 r;
     r.x = kq_align2(d1, d0, sh);
     r.y = kq_align2(d2, d1, sh);
     return r;
 }
 
-/* 4 bytes at a 2-byte aligned address a. */
-__device__ __forceinline__ uint32_t kq_load4_u2a(const uint8_t *a,
-                                                 const uint8_t *end) {
-    uintptr_t ua = (uintptr_t)a;
-    const uint8_t *base = (const uint8_t *)(ua & ~(uintptr_t)3);
-    uint32_t sh = (uint32_t)(ua & 3u);
-    uint32_t d0 = *(const uint32_t *)base;
-    uint32_t d1 = sh ? kq_ld32_guard(base + 4, end) : 0u;
-    return kq_align2(d1, d0, sh);
+/* As kq_load8_u2a, but never reads at or past `end` (a + 8 <= end). */
+__device__ __forceinline__ uint2 kq_load8_u2a_end(const uint8_t *a, const uint8_t *end) {
+    const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);
+    const uint32_t *base = (const uint32_t *)(a - sh);
+    const uint32_t d0 = base[0], d1 = base[1];
+    uint32_t d2 = d1;
+    if (sh) {
+        if ((const uint8_t *)(base + 3) <= end)
+            d2 = base[2];
+        else
+            d2 = (uint32_t)(*(const uint16_t *)(base + 2));
+    }
+    uint2 r;
+    r.x = kq_align2(d1, d0, sh);
+    r.y = kq_align2(d2, d1, sh);
+    return r;
+}
+
+/* 4 bytes at a (a even), reading at most 2 bytes past a + 4. */
+__device__ __forceinline__ uint32_t kq_load4_u2a(const uint8_t *a) {
+    const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);
+    const uint32_t *base = (const uint32_t *)(a - sh);
+    return kq_align2(base[sh ? 1 : 0], base[0], sh);
+}
+
+/* 4 bytes at a (a even), never reading at or past end (a + 4 <= end). */
+__device__ __forceinline__ uint32_t kq_load4_u2a_end(const uint8_t *a, const uint8_t *end) {
+    const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);
+    const uint32_t *base = (const uint32_t *)(a - sh);
+    uint32_t d1 = base[0];
+    if (sh) {
+        if ((const uint8_t *)(base + 2) <= end)
+            d1 = base[1];
+        else
+            d1 = (uint32_t)(*(const uint16_t *)(base + 1));
+    }
+    return kq_align2(d1, base[0], sh);
 }
 
 /* Wave-wide sum over groups of G consecutive lanes (G power of two <= 64);
@@ -185,6 +243,93 @@ __device__ __forceinline__ float kq_group_sum(float v) {
 #pragma unroll
     for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, KQ_WAVE);
     return v;
+}
+
+/* Bitwise AND the optimiser cannot split into per-byte field extracts, so
+ * that byte-wise conversions of the result stay single v_cvt_f32_ubyteN
+ * instructions. */
+__device__ __forceinline__ uint32_t kq_and_0f(uint32_t a) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ uint32_t kq_and_f0(uint32_t a) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0xf0f0f0f0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ uint32_t kq_xor_80(uint32_t a) {
+    uint32_t r;
+    asm("v_xor_b32 %0, 0x80808080, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+/* x from lane (l ^ mask) within rows of 16, through DPP: masks 1 and 2 are
+ * quad permutes, 7 and 15 are the half-row and row mirrors. */
+template <int MASK>
+__device__ __forceinline__ float kq_dpp_pair(float x) {
+    constexpr int ctrl = MASK == 1 ? 0xB1 : MASK == 2 ? 0x4E : MASK == 7 ? 0x141 : 0x140;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xf, 0xf, false));
+}
+
+/* a(lane) + a(lane ^ 32) for lanes < 32 and b(lane ^ 32) + b(lane) for
+ * lanes >= 32, with one v_permlane32_swap (gfx950). */
+__device__ __forceinline__ float kq_fold32(float a, float b) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+/* The same across odd/even 16-lane rows (lane ^ 16), v_permlane16_swap. */
+__device__ __forceinline__ float kq_fold16(float a, float b) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+/*
+ * Transposed butterfly: every lane of a G-lane group (G = 1..64, power of
+ * two, groups aligned in the wave) holds N partial sums; afterwards the
+ * group's total of value j is held by lane j * G / N (N <= G, in v[0]) or by
+ * lane j / (N / G) in v[j % (N / G)] (N > G). Each level halves the values a
+ * lane keeps: the lane whose level bit is clear keeps the low half and
+ * receives its partner's low half, the other keeps the high half. Levels run
+ * from offset G/2 down; partners at a level differ in that level's bit and
+ * agree in every higher bit (mirrors flip the lower bits too, which only
+ * reorders lanes that later levels still combine).
+ */
+template <int G, int N, int O>
+__device__ __forceinline__ void kq_reduce_level(float *v, uint32_t lane) {
+    if constexpr (O >= 1) {
+        constexpr int n = (N * O * 2 / G) > 0 ? (N * O * 2 / G) : 1; /* values at this level */
+        if constexpr (n >= 2) {
+            constexpr int h = n / 2;
+            const bool upper = (lane & (uint32_t)O) != 0u;
+#pragma unroll
+            for (int i = 0; i < h; ++i) {
+                const float lo = v[i], hi = v[i + h];
+                if constexpr (O == 32) {
+                    v[i] = kq_fold32(lo, hi);
+                } else if constexpr (O == 16) {
+                    v[i] = kq_fold16(lo, hi);
+                } else {
+                    const float keep = upper ? hi : lo;
+                    const float send = upper ? lo : hi;
+                    v[i] = keep + kq_dpp_pair<O == 8 ? 15 : O == 4 ? 7 : O>(send);
+                }
+            }
+        } else {
+            if constexpr (O == 32)
+                v[0] = kq_fold32(v[0], v[0]);
+            else if constexpr (O == 16)
+                v[0] = kq_fold16(v[0], v[0]);
+            else
+                v[0] = v[0] + kq_dpp_pair<O == 8 ? 15 : O == 4 ? 7 : O>(v[0]);
+        }
+        kq_reduce_level<G, N, O / 2>(v, lane);
+    }
+}
+
+template <int G, int N>
+__device__ __forceinline__ void kq_group_reduce(float (&v)[N], uint32_t lane) {
+    kq_reduce_level<G, N, G / 2>(v, lane);
 }
 
 #endif

@@ -27,7 +27,7 @@ hipError_t kq_launch_dequant(uint32_t type, const void *packed, uint64_t blocks,
 
 /* matvec / argmax (kq_matvec.hip) */
 int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t batch);
-uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols);
+uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols, uint32_t batch);
 hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_t cols,
                             const float *x, uint32_t batch, float *y, uint32_t *status,
                             float *part_v, uint32_t *part_i, hipStream_t stream);

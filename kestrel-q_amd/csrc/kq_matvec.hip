@@ -11,11 +11,13 @@
  * tolerance. The argmax is exact (first maximum, lowest row on ties).
  *
  * Each 64-lane wavefront keeps its lanes' activations in registers for the
- * whole launch and walks RT row-groups per iteration, so RT rows of packed
- * weights are in flight before the first multiply (kq_rowdot.h). Row sums
- * finish with lane shuffles inside each row's lane group. For the fused LM
- * head every wave also keeps a running (max, row) per batch column and
- * writes one partial; a one-block kernel merges the partials.
+ * whole launch and walks groups of RT row passes (kq_rowdot.h): the first
+ * group's weight loads are issued before the activation loads, and each
+ * following group's loads are in flight while the current group is reduced.
+ * Row sums finish with a transposed butterfly (permlane swaps and DPP), so a
+ * group of RT*B partial sums costs a few cross-lane operations. For the
+ * fused LM head every wave also keeps a running (max, row) per batch column
+ * and writes one partial; a one-block kernel merges the partials.
  */
 #include "kq_launch.h"
 #include "kq_rowdot.h"
@@ -23,10 +25,6 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRT = 4;
-/* Enough waves to cover HBM latency on the large matrices (8 blocks of 4
- * waves per CU); smaller matrices get one row-group stride per wave. */
-constexpr int kMaxBlocks = 256 * 8;
 
 /* larger value wins, equal values keep the lower row */
 __device__ __forceinline__ void argmax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
@@ -50,20 +48,25 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     const uint8_t *__restrict__ W, uint32_t rows, const float *__restrict__ x,
     float *__restrict__ y, uint32_t *status, float *part_v, uint32_t *part_i,
     const uint8_t *w_end) {
-    using Lane = typename kq::LaneFor<TYPE, B>::T;
-    constexpr uint32_t LPR = kq::lanes_per_row<TYPE>(COLS);
-    static_assert(LPR <= 64 && 64 % LPR == 0, "row must fit a wave");
-    constexpr uint32_t RPW = 64u / LPR;
-    constexpr uint32_t RB = kq::row_bytes<TYPE>(COLS);
+    using R = kq::Rows<TYPE, COLS, B, RT>;
+    using Raw = typename R::Raw;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
     const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
-    const uint32_t sub = lane / LPR, l = lane % LPR;
+    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
+    const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
 
-    Lane ln;
-    if (ln.init(l, x, COLS)) kq_flag(status, KQ_DEV_INPUT);
-    bool bad = false;
-    bool malformed = false;
+    typename R::Lane ln;
+    ln.setup(l);
+    const KqBuf wb = kq_buf(W, rows * R::RB);
+    Raw ra[RT], rb[RT];
+    uint32_t g = wave;
+    /* the first group's weights are requested before the activations so the
+     * two memory latencies overlap */
+    if (g < ngroups) R::load_group(ln, wb, g, rows, sub, ra);
+    if (ln.load_x(x, COLS)) kq_flag(status, KQ_DEV_INPUT);
+
+    bool bad = false, malformed = false;
     float best_v[B];
     uint32_t best_i[B];
 #pragma unroll
@@ -71,42 +74,46 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
         best_v[b] = -__builtin_inff();
         best_i[b] = 0xffffffffu;
     }
-
-    for (uint32_t row_base = wave * (RPW * RT); row_base < rows;
-         row_base += nwaves * (RPW * RT)) {
-        typename Lane::Raw raw[RT];
+    auto finish = [&](const Raw (&raw)[RT], uint32_t gg) {
+        float v[R::N];
+        R::dot_group(ln, raw, l, v, malformed);
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
-            raw[r] = row < rows ? ln.load(W + (size_t)row * RB, w_end) : ln.zero();
-        }
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
-            float acc[B];
-            ln.dot(raw[r], acc, malformed);
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const float v = kq_group_sum<LPR>(acc[b]);
+        for (int j = 0; j < R::KEEP; ++j) {
+            const int idx = R::value_index(l, j);
+            if (idx >= 0) {
+                const uint32_t r = (uint32_t)idx / B, b = (uint32_t)idx % B;
+                const uint32_t row = gg * R::GROUP + r * R::RPW + sub;
                 if (row < rows) {
-                    if (l == 0) y[(size_t)b * rows + row] = v;
-                    bad |= !kq_isfinite(v);
-                    argmax_merge(best_v[b], best_i[b], v, row);
+                    y[(size_t)b * rows + row] = v[j];
+                    bad |= !kq_isfinite(v[j]);
+                    argmax_merge(best_v[b], best_i[b], v[j], row);
                 }
             }
         }
+    };
+    /* ping-pong: the next group's loads are in flight while one is reduced */
+    while (g < ngroups) {
+        uint32_t gn = g + nwaves;
+        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, rb);
+        finish(ra, g);
+        g = gn;
+        if (g >= ngroups) break;
+        gn = g + nwaves;
+        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, ra);
+        finish(rb, g);
+        g = gn;
     }
     if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
     if (part_v != nullptr) {
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            float v = best_v[b];
-            uint32_t i = best_i[b];
-            wave_argmax(v, i);
+            float bv = best_v[b];
+            uint32_t bi = best_i[b];
+            wave_argmax(bv, bi);
             if (lane == 0) {
-                part_v[(size_t)b * nwaves + wave] = v;
-                part_i[(size_t)b * nwaves + wave] = i;
+                part_v[(size_t)b * nwaves + wave] = bv;
+                part_i[(size_t)b * nwaves + wave] = bi;
             }
         }
     }
@@ -158,26 +165,46 @@ __global__ __launch_bounds__(kThreads) void argmax_final(const float *part_v,
     }
 }
 
-int grid_for(uint32_t rows, uint32_t rows_per_wave_iter) {
-    const uint32_t waves = (rows + rows_per_wave_iter - 1u) / rows_per_wave_iter;
-    uint32_t blocks = (waves + (kThreads / 64) - 1u) / (kThreads / 64);
-    if (blocks > (uint32_t)kMaxBlocks) blocks = kMaxBlocks;
-    return blocks < 1u ? 1 : (int)blocks;
+/* Row groups per wave: one group of RT passes per wave when that fills the
+ * GPU (small matrices: latency bound, every wave issues its loads at once),
+ * otherwise a grid of resident waves that stride over groups with the next
+ * group's loads in flight while the current one is reduced. */
+constexpr uint32_t kResidentWaves = 256u * 4u * 4u;
+
+uint32_t lanes_for(uint32_t cols) { return cols / 32u; }
+
+uint32_t group_rows(uint32_t cols, uint32_t rt) {
+    const uint32_t lanes = lanes_for(cols);
+    return (lanes >= 64u ? 1u : 64u / lanes) * rt;
 }
 
-/* every format gives each lane 32 weights, so a row takes cols/32 lanes */
-uint32_t rows_per_iter(uint32_t cols) {
-    const uint32_t lanes = cols / 32u;
-    return (lanes >= 64u ? 1u : 64u / lanes) * kRT;
+/* RT = 1 for matrices whose RT = 4 grid would leave the GPU under-filled */
+uint32_t pick_rt(uint32_t rows, uint32_t cols) {
+    const uint32_t groups4 = (rows + group_rows(cols, 4) - 1u) / group_rows(cols, 4);
+    return groups4 >= kResidentWaves ? 4u : 1u;
+}
+
+uint32_t waves_for(uint32_t rows, uint32_t cols, uint32_t batch) {
+    const uint32_t rt = pick_rt(rows, cols);
+    const uint32_t groups = (rows + group_rows(cols, rt) - 1u) / group_rows(cols, rt);
+    /* wide batches use more registers: fewer resident waves */
+    const uint32_t cap = batch >= 3u ? kResidentWaves / 2u : kResidentWaves;
+    uint32_t w = groups < cap ? groups : cap;
+    w = (w + (kThreads / 64u) - 1u) / (kThreads / 64u) * (kThreads / 64u);
+    return w < (kThreads / 64u) ? (kThreads / 64u) : w;
 }
 
 template <uint32_t TYPE, uint32_t COLS, int B>
 hipError_t launch_one(const uint8_t *W, uint32_t rows, const float *x, float *y, uint32_t *st,
                       float *pv, uint32_t *pi, hipStream_t s) {
-    const uint8_t *end = W + (size_t)rows * kq::row_bytes<TYPE>(COLS);
-    hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, kRT>),
-                       dim3(grid_for(rows, rows_per_iter(COLS))), dim3(kThreads), 0, s, W,
-                       rows, x, y, st, pv, pi, end);
+    const uint8_t *end = nullptr;
+    const uint32_t blocks = waves_for(rows, COLS, B) / (kThreads / 64u);
+    if (pick_rt(rows, COLS) == 4u)
+        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 4>), dim3(blocks), dim3(kThreads), 0, s,
+                           W, rows, x, y, st, pv, pi, end);
+    else
+        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 1>), dim3(blocks), dim3(kThreads), 0, s,
+                           W, rows, x, y, st, pv, pi, end);
     return hipGetLastError();
 }
 
@@ -223,9 +250,10 @@ extern "C" int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t
     return cols == 256u || cols == 512u || cols == 1024u || cols == 2048u;
 }
 
-extern "C" uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols) {
+extern "C" uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols,
+                                           uint32_t batch) {
     (void)type;
-    return (uint32_t)grid_for(rows, rows_per_iter(cols)) * (kThreads / 64);
+    return waves_for(rows, cols, batch);
 }
 
 extern "C" hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows,

@@ -303,8 +303,9 @@ __global__ __launch_bounds__(1024) void route_finish(
 }
 
 /* ---------------------- expert gate/up + SwiGLU ---------------------- */
-/* grid: x = row tiles, y = slot (0..K-1 routed by top-k position, K =
- * shared expert), z = token. act[t][slot][row] = swiglu(g, u). */
+/* grid: x = row groups, y = slot (0..K-1 routed by top-k position, K = the
+ * shared expert), z = token. act[t][slot][row] = swiglu(g, u). Each wave
+ * requests its gate and up rows before the activations (kq_rowdot.h). */
 template <uint32_t TYPE, uint32_t COLS, int RT>
 __global__ __launch_bounds__(kThreads) void expert_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
@@ -312,10 +313,8 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
     const float *__restrict__ hidden_states, const uint32_t *__restrict__ ids,
     uint32_t top_k, uint32_t inter, uint32_t shared_inter, uint32_t act_stride,
     float *__restrict__ act, uint32_t *status) {
-    using Lane = typename kq::LaneFor<TYPE, 1>::T;
-    constexpr uint32_t LPR = kq::lanes_per_row<TYPE>(COLS);
-    constexpr uint32_t RPW = 64u / LPR;
-    constexpr uint32_t RB = kq::row_bytes<TYPE>(COLS);
+    using R = kq::Rows<TYPE, COLS, 1, RT>;
+    using Raw = typename R::Raw;
     const uint32_t slot = blockIdx.y, t = blockIdx.z;
     const bool shared = slot == top_k;
     const uint32_t rows = shared ? shared_inter : inter;
@@ -325,39 +324,44 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
         U = sup;
     } else {
         const uint32_t e = ids[(size_t)t * top_k + slot];
-        G = gate + (size_t)e * inter * RB;
-        U = up + (size_t)e * inter * RB;
+        G = gate + (size_t)e * inter * R::RB;
+        U = up + (size_t)e * inter * R::RB;
     }
-    const uint8_t *g_end = G + (size_t)rows * RB, *u_end = U + (size_t)rows * RB;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
     const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
-    const uint32_t sub = lane / LPR, l = lane % LPR;
-    Lane ln;
-    if (ln.init(l, hidden_states + (size_t)t * COLS, COLS)) kq_flag(status, KQ_DEV_INPUT);
-    bool bad = false;
-    bool malformed = false;
+    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
+    const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
+    typename R::Lane ln;
+    ln.setup(l);
+    Raw rg[RT], ru[RT];
+    uint32_t g = wave;
+    const KqBuf gb = kq_buf(G, rows * R::RB), ub = kq_buf(U, rows * R::RB);
+    if (g < ngroups) {
+        R::load_group(ln, gb, g, rows, sub, rg);
+        R::load_group(ln, ub, g, rows, sub, ru);
+    }
+    if (ln.load_x(hidden_states + (size_t)t * COLS, COLS)) kq_flag(status, KQ_DEV_INPUT);
+    bool bad = false, malformed = false;
     float *out = act + ((size_t)t * (top_k + 1u) + slot) * act_stride;
-    for (uint32_t row_base = wave * (RPW * RT); row_base < rows; row_base += nwaves * (RPW * RT)) {
-        typename Lane::Raw rg[RT], ru[RT];
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
-            rg[r] = row < rows ? ln.load(G + (size_t)row * RB, g_end) : ln.zero();
-            ru[r] = row < rows ? ln.load(U + (size_t)row * RB, u_end) : ln.zero();
+    for (; g < ngroups; g += nwaves) {
+        if (g != wave) {
+            R::load_group(ln, gb, g, rows, sub, rg);
+            R::load_group(ln, ub, g, rows, sub, ru);
         }
+        float vg[R::N], vu[R::N];
+        R::dot_group(ln, rg, l, vg, malformed);
+        R::dot_group(ln, ru, l, vu, malformed);
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
-            float ag[1], au[1];
-            ln.dot(rg[r], ag, malformed);
-            ln.dot(ru[r], au, malformed);
-            const float g = kq_group_sum<LPR>(ag[0]);
-            const float u = kq_group_sum<LPR>(au[0]);
-            if (row < rows && l == 0) {
-                const float a = kq_swiglu(g, u);
-                bad |= !kq_isfinite(g) || !kq_isfinite(u) || !kq_isfinite(a);
-                out[row] = a;
+        for (int j = 0; j < R::KEEP; ++j) {
+            const int idx = R::value_index(l, j);
+            if (idx >= 0) {
+                const uint32_t row = g * R::GROUP + (uint32_t)idx * R::RPW + sub;
+                if (row < rows) {
+                    const float a = kq_swiglu(vg[j], vu[j]);
+                    bad |= !kq_isfinite(vg[j]) || !kq_isfinite(vu[j]) || !kq_isfinite(a);
+                    out[row] = a;
+                }
             }
         }
     }
@@ -366,46 +370,47 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
 }
 
 /* ------------------------------ down ------------------------------ */
-/* grid: x = row tiles over hidden, y = slot, z = token.
+/* grid: x = row groups over hidden, y = slot, z = token.
  * expert_out[t][slot][f] = Wd[f] . act[t][slot]. */
 template <uint32_t TYPE, uint32_t COLS, int RT>
 __global__ __launch_bounds__(kThreads) void expert_down(
     const uint8_t *__restrict__ down, const uint8_t *__restrict__ sdown,
     const float *__restrict__ act, const uint32_t *__restrict__ ids, uint32_t top_k,
     uint32_t hidden, uint32_t act_stride, float *__restrict__ expert_out, uint32_t *status) {
-    using Lane = typename kq::LaneFor<TYPE, 1>::T;
-    constexpr uint32_t LPR = kq::lanes_per_row<TYPE>(COLS);
-    constexpr uint32_t RPW = 64u / LPR;
-    constexpr uint32_t RB = kq::row_bytes<TYPE>(COLS);
+    using R = kq::Rows<TYPE, COLS, 1, RT>;
+    using Raw = typename R::Raw;
     const uint32_t slot = blockIdx.y, t = blockIdx.z;
     const bool shared = slot == top_k;
-    const uint8_t *D = shared ? sdown : down + (size_t)ids[(size_t)t * top_k + slot] * hidden * RB;
-    const uint8_t *d_end = D + (size_t)hidden * RB;
+    const uint8_t *D =
+        shared ? sdown : down + (size_t)ids[(size_t)t * top_k + slot] * hidden * R::RB;
+    const KqBuf db = kq_buf(D, hidden * R::RB);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
     const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
-    const uint32_t sub = lane / LPR, l = lane % LPR;
-    Lane ln;
-    bool bad = ln.init(l, act + ((size_t)t * (top_k + 1u) + slot) * act_stride, COLS);
-    bool malformed = false;
+    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
+    const uint32_t ngroups = (hidden + R::GROUP - 1u) / R::GROUP;
+    typename R::Lane ln;
+    ln.setup(l);
+    Raw rd[RT];
+    uint32_t g = wave;
+    if (g < ngroups) R::load_group(ln, db, g, hidden, sub, rd);
+    if (ln.load_x(act + ((size_t)t * (top_k + 1u) + slot) * act_stride, COLS))
+        kq_flag(status, KQ_DEV_NUMERIC);
+    bool bad = false, malformed = false;
     float *out = expert_out + ((size_t)t * (top_k + 1u) + slot) * hidden;
-    for (uint32_t row_base = wave * (RPW * RT); row_base < hidden;
-         row_base += nwaves * (RPW * RT)) {
-        typename Lane::Raw rd[RT];
+    for (; g < ngroups; g += nwaves) {
+        if (g != wave) R::load_group(ln, db, g, hidden, sub, rd);
+        float v[R::N];
+        R::dot_group(ln, rd, l, v, malformed);
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
-            rd[r] = row < hidden ? ln.load(D + (size_t)row * RB, d_end) : ln.zero();
-        }
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint32_t row = row_base + (uint32_t)r * RPW + sub;
-            float a[1];
-            ln.dot(rd[r], a, malformed);
-            const float v = kq_group_sum<LPR>(a[0]);
-            if (row < hidden && l == 0) {
-                bad |= !kq_isfinite(v);
-                out[row] = v;
+        for (int j = 0; j < R::KEEP; ++j) {
+            const int idx = R::value_index(l, j);
+            if (idx >= 0) {
+                const uint32_t row = g * R::GROUP + (uint32_t)idx * R::RPW + sub;
+                if (row < hidden) {
+                    bad |= !kq_isfinite(v[j]);
+                    out[row] = v[j];
+                }
             }
         }
     }
@@ -446,9 +451,8 @@ hipError_t launch_gateup(const kq_launch_moe_dims *d, const kq_launch_moe_weight
                          const float *hidden, uint32_t tokens, const kq_launch_moe_ws *ws,
                          uint32_t act_stride, uint32_t *status, hipStream_t s) {
     constexpr int RT = 2;
-    constexpr uint32_t LPR = kq::lanes_per_row<TYPE>(COLS);
     const uint32_t rows = d->inter > d->shared_inter ? d->inter : d->shared_inter;
-    const uint32_t rows_per_wave = (64u / LPR) * RT;
+    const uint32_t rows_per_wave = kq::Rows<TYPE, COLS, 1, RT>::GROUP;
     const uint32_t waves = (rows + rows_per_wave - 1u) / rows_per_wave;
     const uint32_t blocks = (waves + 3u) / 4u;
     hipLaunchKernelGGL((expert_gateup<TYPE, COLS, RT>), dim3(blocks, d->top_k + 1u, tokens),
@@ -463,9 +467,8 @@ template <uint32_t TYPE, uint32_t COLS>
 hipError_t launch_down(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                        uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t act_stride,
                        uint32_t *status, hipStream_t s) {
-    constexpr int RT = 4;
-    constexpr uint32_t LPR = kq::lanes_per_row<TYPE>(COLS);
-    const uint32_t rows_per_wave = (64u / LPR) * RT;
+    constexpr int RT = 2;
+    const uint32_t rows_per_wave = kq::Rows<TYPE, COLS, 1, RT>::GROUP;
     const uint32_t waves = (d->hidden + rows_per_wave - 1u) / rows_per_wave;
     const uint32_t blocks = (waves + 3u) / 4u;
     hipLaunchKernelGGL((expert_down<TYPE, COLS, RT>), dim3(blocks, d->top_k + 1u, tokens),

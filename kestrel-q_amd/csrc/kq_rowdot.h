@@ -9,7 +9,8 @@
  * src/kq_numeric.c:176-295 (Q8_0, Q4_K) and the GGML Q6_K layout; the
  * per-sub-block scale is applied once to a sum of code*x products, and the
  * block offset (Q4_K dmin*m, Q6_K -32, Q8_0 +128 bias) is taken off with a
- * precomputed activation sum.
+ * precomputed activation sum. Codes are converted with one
+ * v_cvt_f32_ubyteN per weight (the masks are opaque to the optimiser).
  */
 #ifndef KQ_ROWDOT_H
 #define KQ_ROWDOT_H
@@ -25,7 +26,7 @@ __device__ __forceinline__ bool load_x8(const float *x, uint32_t stride, uint32_
 #pragma unroll
     for (int b = 0; b < B; ++b) {
         const float4 *p = (const float4 *)(x + (size_t)b * stride + k);
-        float4 u = p[0], v = p[1];
+        const float4 u = p[0], v = p[1];
         dst[b][0] = u.x; dst[b][1] = u.y; dst[b][2] = u.z; dst[b][3] = u.w;
         dst[b][4] = v.x; dst[b][5] = v.y; dst[b][6] = v.z; dst[b][7] = v.w;
 #pragma unroll
@@ -34,7 +35,7 @@ __device__ __forceinline__ bool load_x8(const float *x, uint32_t stride, uint32_
     return bad;
 }
 
-/* 4 packed byte codes of w dotted with 4 activations, fp32 fused. */
+/* 4 byte codes of w dotted with 4 activations, fp32 fused. */
 __device__ __forceinline__ float dot4_u8(uint32_t w, const float *xv, float acc) {
     acc = fmaf((float)(w & 0xffu), xv[0], acc);
     acc = fmaf((float)((w >> 8) & 0xffu), xv[1], acc);
@@ -58,25 +59,23 @@ __device__ __forceinline__ void sum8(const float (&v)[B][8], float (&s)[B]) {
 template <int B>
 struct LaneQ4K {
     static constexpr uint32_t kBlockBytes = 144u;
-    static constexpr uint32_t kLanesPerBlock = 8u;
     struct Raw {
         uint4 hd, qs;
     };
     uint32_t off;  /* byte offset of this lane's block within the row */
     uint32_t qoff; /* offset of its 16 qs bytes within the block */
-    uint32_t gq;
+    uint32_t gq, k0;
     float xl[B][16], xh[B][16], sxl[B], sxh[B];
 
-    /* l = lane index within the row (0 .. 8*blocks-1) */
-    __device__ __forceinline__ bool init(uint32_t l, const float *x, uint32_t stride) {
+    /* l = lane index within the row: block l/8, 16-byte qs slice l%8 */
+    __device__ __forceinline__ void setup(uint32_t l) {
         const uint32_t bb = l >> 3, c = l & 7u, h = c & 1u;
         gq = c >> 1;
         off = kBlockBytes * bb;
         qoff = 16u + 32u * gq + 16u * h;
-        const uint32_t k0 = 256u * bb + 64u * gq + 16u * h;
-        return load_x(x, stride, k0);
+        k0 = 256u * bb + 64u * gq + 16u * h;
     }
-    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride, uint32_t k0) {
+    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
         float t0[B][8], t1[B][8], s0[B], s1[B];
         bool bad = load_x8<B>(x, stride, k0, t0);
         bad |= load_x8<B>(x, stride, k0 + 8u, t1);
@@ -100,10 +99,11 @@ struct LaneQ4K {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(const uint8_t *row, const uint8_t *) const {
+    /* row_off: byte offset of the row in the buffer */
+    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
         Raw r;
-        r.hd = *(const uint4 *)(row + off);
-        r.qs = *(const uint4 *)(row + off + qoff);
+        r.hd = kq_ld128(b, row_off + off, 0u);
+        r.qs = kq_ld128(b, row_off + off + qoff, 0u);
         return r;
     }
     __device__ __forceinline__ Raw zero() const {
@@ -112,7 +112,7 @@ struct LaneQ4K {
         r.qs = make_uint4(0, 0, 0, 0);
         return r;
     }
-    __device__ __forceinline__ void dot(const Raw &r, float (&acc)[B], bool &malformed) const {
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
         const float d = kq_f16_to_f32(r.hd.x & 0xffffu);
         const float dmin = kq_f16_to_f32(r.hd.x >> 16);
         malformed |= !kq_isfinite(d) || !kq_isfinite(dmin);
@@ -120,19 +120,27 @@ struct LaneQ4K {
         kq_k_scale(2u * gq, r.hd.y, r.hd.z, r.hd.w, &s0, &m0);
         kq_k_scale(2u * gq + 1u, r.hd.y, r.hd.z, r.hd.w, &s1, &m1);
         const float dl = d * (float)s0, ml = dmin * (float)m0;
-        const float dh = d * (float)s1, mh = dmin * (float)m1;
+        /* high nibbles are converted in place (16 * code): fold 1/16 into
+         * the sub-block scale (exact power of two) */
+        const float dh = d * (float)s1 * 0.0625f, mh = dmin * (float)m1;
         const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lo[w] = kq_and_0f(q[w]);
+            hi[w] = kq_and_f0(q[w]);
+        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            float lo = 0.0f, hi = 0.0f;
+            float sl = 0.0f, sh = 0.0f;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                lo = dot4_u8(q[w] & 0x0f0f0f0fu, &xl[b][4 * w], lo);
-                hi = dot4_u8((q[w] >> 4) & 0x0f0f0f0fu, &xh[b][4 * w], hi);
+                sl = dot4_u8(lo[w], &xl[b][4 * w], sl);
+                sh = dot4_u8(hi[w], &xh[b][4 * w], sh);
             }
-            float v = dl * lo;
+            float v = dl * sl;
             v = fmaf(-ml, sxl[b], v);
-            v = fmaf(dh, hi, v);
+            v = fmaf(dh, sh, v);
             v = fmaf(-mh, sxh[b], v);
             acc[b] = v;
         }
@@ -140,26 +148,34 @@ struct LaneQ4K {
 };
 
 /* ---------------- Q6_K: 210 B blocks of 256 ---------------- */
+/* Fields of 8 bytes at byte offset o (o even) are read as one 12-byte
+ * dwordx3 window at o - (o & 3) and funnel-shifted; the sub-scales of the
+ * second half (the last field of a block, ending at 208) use the window
+ * [o - 4, o + 8) when o is 4-aligned, so no window passes the block's last
+ * byte. A window may start 2 bytes before its block (inside the previous
+ * block of the same buffer). */
 template <int B>
 struct LaneQ6K {
     static constexpr uint32_t kBlockBytes = 210u;
-    static constexpr uint32_t kLanesPerBlock = 8u;
+    /* raw 12-byte windows; aligned in dot() so that issuing the next group's
+     * loads never waits for this group's data */
     struct Raw {
-        uint2 qa, qb, qh, sc;
-        uint32_t d;
+        kq_u32x3 wa, wb, wh, ws;
+        uint32_t d, sh;
     };
-    uint32_t off, n, t;
+    uint32_t off, n, t, k0;
     float xq[4][B][8], xs[4][B];
 
-    __device__ __forceinline__ bool init(uint32_t l, const float *x, uint32_t stride) {
+    /* l = lane index within the row: block l/8, half n, l-range 8t..8t+7 */
+    __device__ __forceinline__ void setup(uint32_t l) {
         const uint32_t bb = l >> 3, s = l & 7u;
         n = s >> 2;
         t = s & 3u;
         off = kBlockBytes * bb;
-        return load_x(x, stride, 256u * bb + 128u * n + 8u * t);
+        k0 = 256u * bb + 128u * n + 8u * t;
     }
     /* quarter q holds outputs k0 + 32q + 0..7 */
-    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride, uint32_t k0) {
+    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
         bool bad = false;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -168,29 +184,46 @@ struct LaneQ6K {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(const uint8_t *row, const uint8_t *end) const {
-        const uint8_t *p = row + off;
+    /* byte offset of the 12-byte window holding the 8 bytes at o */
+    __device__ static __forceinline__ uint32_t window(uint32_t o, bool last) {
+        const uint32_t sh = o & 3u;
+        return (last && sh == 0u) ? o - 4u : o - sh;
+    }
+    __device__ static __forceinline__ uint2 align8(kq_u32x3 w, uint32_t sh, bool back) {
+        uint2 r;
+        r.x = back ? w.y : kq_align2(w.y, w.x, sh);
+        r.y = back ? w.z : kq_align2(w.z, w.y, sh);
+        return r;
+    }
+    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+        const uint32_t p = row_off + off;
         Raw r;
-        r.qa = kq_load8_u2a(p + 64u * n + 8u * t, end);
-        r.qb = kq_load8_u2a(p + 64u * n + 32u + 8u * t, end);
-        r.qh = kq_load8_u2a(p + 128u + 32u * n + 8u * t, end);
-        r.sc = kq_load8_u2a(p + 192u + 8u * n, end);
-        r.d = *(const uint16_t *)(p + 208u);
+        r.sh = p & 3u; /* every field of a block shares the block's alignment */
+        r.wa = kq_ld96(b, window(p + 64u * n + 8u * t, false), 0u);
+        r.wb = kq_ld96(b, window(p + 64u * n + 32u + 8u * t, false), 0u);
+        r.wh = kq_ld96(b, window(p + 128u + 32u * n + 8u * t, false), 0u);
+        r.ws = kq_ld96(b, window(p + 192u + 8u * n, n == 1u), 0u);
+        r.d = kq_ld16(b, p + 208u, 0u);
         return r;
     }
     __device__ __forceinline__ Raw zero() const {
         Raw r;
-        r.qa = r.qb = r.qh = r.sc = make_uint2(0, 0);
+        r.wa = r.wb = r.wh = r.ws = kq_u32x3{0u, 0u, 0u};
         r.d = 0u;
+        r.sh = 0u;
         return r;
     }
-    __device__ __forceinline__ void dot(const Raw &r, float (&acc)[B], bool &malformed) const {
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
         const float d = kq_f16_to_f32(r.d);
         malformed |= !kq_isfinite(d);
-        /* quarter q uses sc[8n + (t>>1) + 2q] */
+        const uint2 qa = align8(r.wa, r.sh, false), qb = align8(r.wb, r.sh, false);
+        const uint2 qh = align8(r.wh, r.sh, false);
+        const uint2 sc = align8(r.ws, r.sh, n == 1u && r.sh == 0u);
+        /* quarter q uses sc[8n + (t>>1) + 2q]: byte (t>>1) or (t>>1)+2 of the
+         * first or second dword of sc[8n .. 8n+7] */
         const uint32_t sh = (t >> 1) * 8u;
-        const uint32_t sv[4] = {r.sc.x >> sh, r.sc.x >> (sh + 16u), r.sc.y >> sh,
-                                r.sc.y >> (sh + 16u)};
+        const uint32_t sv[4] = {sc.x >> sh, sc.x >> (sh + 16u), sc.y >> sh,
+                                sc.y >> (sh + 16u)};
         float dq[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) dq[q] = d * (float)(int8_t)(sv[q] & 0xffu);
@@ -201,9 +234,9 @@ struct LaneQ6K {
             for (int b = 0; b < B; ++b) part[q][b] = 0.0f;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            const uint32_t A = half ? r.qa.y : r.qa.x;
-            const uint32_t Bq = half ? r.qb.y : r.qb.x;
-            const uint32_t H = half ? r.qh.y : r.qh.x;
+            const uint32_t A = half ? qa.y : qa.x;
+            const uint32_t Bq = half ? qb.y : qb.x;
+            const uint32_t H = half ? qh.y : qh.x;
             const uint32_t c0 = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
             const uint32_t c1 = (Bq & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
             const uint32_t c2 = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
@@ -227,22 +260,25 @@ struct LaneQ6K {
 };
 
 /* ---------------- Q8_0: 34 B blocks of 32 ---------------- */
+/* A block at byte offset bo (even) is read as two 16-byte windows from
+ * bo - (bo & 3) plus two 16-bit loads of its last four code bytes: every
+ * read lies inside the block or the 2 bytes before it. */
 template <int B>
 struct LaneQ8 {
     static constexpr uint32_t kBlockBytes = 34u;
-    static constexpr uint32_t kLanesPerBlock = 1u;
+    /* raw windows; aligned in dot() (see LaneQ6K) */
     struct Raw {
-        uint32_t d;
-        uint32_t c[8];
+        uint4 w0, w1;
+        uint32_t t0, t1, sh;
     };
-    uint32_t off;
+    uint32_t off, k0;
     float xv[4][B][8], xsum[B];
 
-    __device__ __forceinline__ bool init(uint32_t l, const float *x, uint32_t stride) {
+    __device__ __forceinline__ void setup(uint32_t l) {
         off = kBlockBytes * l;
-        return load_x(x, stride, 32u * l);
+        k0 = 32u * l;
     }
-    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride, uint32_t k0) {
+    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
         bool bad = false;
 #pragma unroll
         for (int q = 0; q < 4; ++q) bad |= load_x8<B>(x, stride, k0 + 8u * q, xv[q]);
@@ -257,36 +293,41 @@ struct LaneQ8 {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(const uint8_t *row, const uint8_t *end) const {
-        const uint8_t *p = row + off;
+    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+        const uint32_t bo = row_off + off;
         Raw r;
-        r.d = *(const uint16_t *)p;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint2 u = kq_load8_u2a(p + 2u + 8u * j, end);
-            r.c[2 * j] = u.x;
-            r.c[2 * j + 1] = u.y;
-        }
+        r.sh = bo & 3u;
+        r.w0 = kq_ld128(b, bo - r.sh, 0u);
+        r.w1 = kq_ld128(b, bo - r.sh + 16u, 0u);
+        r.t0 = kq_ld16(b, bo + 30u, 0u);
+        r.t1 = kq_ld16(b, bo + 32u, 0u);
         return r;
     }
     __device__ __forceinline__ Raw zero() const {
         Raw r;
-        r.d = 0u;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) r.c[j] = 0x80808080u;
+        /* codes decode to the +128 bias only: a zero scale gives 0 */
+        r.w0 = make_uint4(0u, 0x80808080u, 0x80808080u, 0x80808080u);
+        r.w1 = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+        r.t0 = r.t1 = 0x8080u;
+        r.sh = 0u;
         return r;
     }
-    __device__ __forceinline__ void dot(const Raw &r, float (&acc)[B], bool &malformed) const {
-        const float d = kq_f16_to_f32(r.d);
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const uint32_t w[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+        const float d = kq_f16_to_f32(r.sh ? (w[0] >> 16) : (w[0] & 0xffffu));
         malformed |= !kq_isfinite(d);
+        /* code dword k = bytes bo+2+4k .. bo+5+4k of the block at bo */
+        uint32_t u[8];
+#pragma unroll
+        for (int k = 0; k < 7; ++k) u[k] = kq_xor_80(r.sh ? w[k + 1] : kq_align2(w[k + 1], w[k], 2u));
+        u[7] = kq_xor_80(r.t0 | (r.t1 << 16));
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             /* int8 code + 128 as an unsigned byte; the bias comes off with
              * the activation sum */
             float s = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                s = dot4_u8(r.c[j] ^ 0x80808080u, &xv[j >> 1][b][4 * (j & 1)], s);
+            for (int j = 0; j < 8; ++j) s = dot4_u8(u[j], &xv[j >> 1][b][4 * (j & 1)], s);
             acc[b] = d * fmaf(-128.0f, xsum[b], s);
         }
     }
@@ -317,6 +358,67 @@ template <uint32_t TYPE>
 __host__ __device__ constexpr uint32_t row_bytes(uint32_t cols) {
     return TYPE == 8u ? (cols / 32u) * 34u : (cols / 256u) * (TYPE == 12u ? 144u : 210u);
 }
+
+/*
+ * Row-group engine. A wave covers RPW = 64/LPR rows side by side and RT
+ * such passes per group (GROUP = RPW*RT rows). load_group issues every load
+ * of a group; groups entirely below `rows` take the unguarded path.
+ */
+template <uint32_t TYPE, uint32_t COLS, int B, int RT>
+struct Rows {
+    using Lane = typename LaneFor<TYPE, B>::T;
+    using Raw = typename Lane::Raw;
+    static constexpr uint32_t LPR = lanes_per_row<TYPE>(COLS);
+    static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "row must fit a wave");
+    static constexpr uint32_t RPW = 64u / LPR;
+    static constexpr uint32_t GROUP = RPW * RT;
+    static constexpr uint32_t RB = row_bytes<TYPE>(COLS);
+    static constexpr int NV = RT * B; /* partial sums per lane */
+    /* the butterfly halves the count at every level: pad to a power of two */
+    static constexpr int N = NV <= 1 ? 1 : NV <= 2 ? 2 : NV <= 4 ? 4 : NV <= 8 ? 8
+                             : NV <= 16 ? 16 : 32;
+    static constexpr int KEEP = N > (int)LPR ? N / (int)LPR : 1; /* after reduction */
+
+    __device__ static __forceinline__ void load_group(const Lane &ln, KqBuf W, uint32_t g,
+                                                      uint32_t rows, uint32_t sub,
+                                                      Raw (&raw)[RT]) {
+        const uint32_t row0 = g * GROUP + sub;
+        if ((g + 1u) * GROUP <= rows) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) raw[r] = ln.load(W, (row0 + (uint32_t)r * RPW) * RB);
+        } else {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const uint32_t row = row0 + (uint32_t)r * RPW;
+                raw[r] = row < rows ? ln.load(W, row * RB) : ln.zero();
+            }
+        }
+    }
+
+    /* partial dots of a group, reduced over each row's LPR lanes; on return
+     * lane l (within its row group) holds value index idx(l, j) in v[j] */
+    __device__ static __forceinline__ void dot_group(const Lane &ln, const Raw (&raw)[RT],
+                                                     uint32_t l, float (&v)[N],
+                                                     bool &malformed) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r) ln.dot(raw[r], &v[r * B], malformed);
+#pragma unroll
+        for (int i = NV; i < N; ++i) v[i] = 0.0f;
+        kq_group_reduce<(int)LPR, N>(v, l);
+    }
+
+    /* value index held in v[j] by lane l, or -1 (duplicate holder, padding) */
+    __device__ static __forceinline__ int value_index(uint32_t l, int j) {
+        int idx;
+        if constexpr (N <= (int)LPR) {
+            constexpr uint32_t span = LPR / (uint32_t)N;
+            idx = (l % span == 0u && j == 0) ? (int)(l / span) : -1;
+        } else {
+            idx = (int)l * KEEP + j;
+        }
+        return idx < NV ? idx : -1;
+    }
+};
 
 }  // namespace kq
 

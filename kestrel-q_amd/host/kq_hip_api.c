@@ -483,7 +483,8 @@ kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const v
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "logits and ids overlap");
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
-    nparts = kq_launch_matvec_waves(type_id, (uint32_t)vocab, (uint32_t)cols);
+    nparts = kq_launch_matvec_waves(type_id, (uint32_t)vocab, (uint32_t)cols,
+                                    batch > 4u ? 4u : batch);
     st = ensure_parts(c, (uint64_t)nparts * batch, diag);
     if (st != KQ_STATUS_OK) return st;
     e = enqueue_matvec(c, type_id, w, vocab, cols, h, batch, logits, c->part_v, c->part_i, nparts);

@@ -42,6 +42,31 @@ def ulp_distance(a, b):
     return np.abs(a - b)
 
 
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def assert_close(got, ref, rtol=RTOL, atol=ATOL):
+    """fp32-accumulated outputs: |got - ref| <= atol + rtol * max(|ref|, rms),
+    rms taken over each output row (last axis). A reordered fp32 sum errs in
+    proportion to the size of its terms, not of its result; the row RMS is
+    that scale at elements where the terms cancel. One wrong weight or expert
+    moves an element by ~rms/sqrt(n), far above rtol * rms."""
+    import numpy as np
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.isfinite(got).all()
+    rms = np.sqrt(np.mean(ref * ref, axis=-1, keepdims=True))
+    bound = atol + rtol * np.maximum(np.abs(ref), rms)
+    err = np.abs(got - ref)
+    bad = err > bound
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{int(bad.sum())} elements beyond tolerance, first {idx.tolist()}: "
+                             f"got {got[bad][:5]}, ref {ref[bad][:5]}, max err/bound "
+                             f"{float((err / bound).max()):.3g}")
+
+
 @pytest.fixture(scope="session")
 def oracle():
     import kq_oracle

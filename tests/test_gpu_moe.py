@@ -1,11 +1,11 @@
 """Device parity for the MoE operator, through the C ABI, against the CPU
 oracle. Bars: router logits, probabilities, top-k ids and weights bit-exact
 (the device restates the CPU's arithmetic order); layer outputs within
-|gpu - ref| <= 1e-4 + 1e-3 * |ref|."""
+|gpu - ref| <= 1e-4 + 1e-3 * max(|ref|, row rms) (conftest.assert_close)."""
 import numpy as np
 import pytest
 
-from conftest import hex_le_f32, load_golden, oracle_threads
+from conftest import assert_close, hex_le_f32, load_golden, oracle_threads
 
 import kq_hip
 import kq_oracle
@@ -143,7 +143,7 @@ def test_moe_decode_one_token(ctx, layer):
     out, ids = layer.run(ctx, x)
     ref, tr = layer.oracle(x)
     assert np.array_equal(ids, tr["selected_ids"])
-    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    assert_close(out, ref)
 
 
 @pytest.mark.parametrize("tokens", [2, 16])
@@ -152,7 +152,7 @@ def test_moe_multi_token(ctx, layer, tokens):
     out, ids = layer.run(ctx, x)
     ref, tr = layer.oracle(x)
     assert np.array_equal(ids, tr["selected_ids"])
-    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    assert_close(out, ref)
 
 
 def test_moe_repeated_calls_identical(ctx, layer):
@@ -179,7 +179,7 @@ def test_moe_small_formats(ctx):
     dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in roles.items()}, x, trace=True)
     assert np.array_equal(ctx.download(dids, np.uint32, 3 * K).reshape(3, K), tr["selected_ids"])
-    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    assert_close(out, ref)
 
 
 def test_moe_fails_closed(ctx, layer):

@@ -2,12 +2,13 @@
 oracle on identical seeded inputs.
 
 Bars: dequantized weights bit-exact; matvec / LM-head outputs within
-|gpu - ref| <= 1e-4 + 1e-3 * |ref| (fp32 accumulation in a different order);
-argmax token ids exact; device expf bit-exact on all 2^32 inputs."""
+|gpu - ref| <= 1e-4 + 1e-3 * max(|ref|, row rms) (fp32 accumulation in a
+different order, conftest.assert_close); argmax token ids exact; device expf
+bit-exact on all 2^32 inputs."""
 import numpy as np
 import pytest
 
-from conftest import bits_f32, load_golden, oracle_threads
+from conftest import assert_close, bits_f32, load_golden, oracle_threads
 
 import kq_hip
 import kq_oracle
@@ -151,7 +152,7 @@ def matvec_case(ctx, fmt, rows, cols, batch, key):
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
 def test_matvec_4096x2048_batch1(ctx, fmt):
     got, want = matvec_case(ctx, fmt, 4096, 2048, 1, S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT))
-    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    assert_close(got, want)
 
 
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
@@ -160,13 +161,13 @@ def test_matvec_4096x2048_batch1(ctx, fmt):
 def test_matvec_shapes(ctx, fmt, rows, cols, batch):
     got, want = matvec_case(ctx, fmt, rows, cols, batch,
                             S.stream_key(S.W_MATVEC_Q6K, rows, cols, batch))
-    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    assert_close(got, want)
 
 
 @pytest.mark.parametrize("cols", [32, 64, 128])
 def test_matvec_q8_short_rows(ctx, cols):
     got, want = matvec_case(ctx, "Q8_0", 130, cols, 2, S.stream_key(S.W_MATVEC_Q8_0, cols))
-    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    assert_close(got, want)
 
 
 @pytest.mark.parametrize("case", [c for c in NUM["row_dot_cases"] if c["type"] in FMTS],
@@ -238,7 +239,7 @@ def test_lm_head_q6k_151936x2048(ctx, batch):
     logits = ctx.download(dl, np.float32, V * batch).reshape(batch, V)
     ids = ctx.download(di, np.uint32, batch)
     ref = kq_oracle.matvec(kq_oracle.Q6_K, w, V, H, h, threads=oracle_threads())
-    np.testing.assert_allclose(logits, ref, rtol=RTOL, atol=ATOL)
+    assert_close(logits, ref)
     for b in range(batch):
         # exact on the device's own logits; equal to the CPU's where the
         # CPU top-2 margin exceeds the tolerance
