@@ -72,8 +72,7 @@ typedef struct kq_launch_moe_weights {
  * (kq_launch_moe_ws_bytes gives the size for a token count). */
 typedef struct kq_launch_moe_ws {
     float *router_t;      /* router rows + shared gate row, transposed to
-                             [hidden/4][experts_padded][4]; for one token the
-                             products w*x in the same layout */
+                             [hidden/4][experts_padded][4] (several tokens) */
     float *logits;        /* [tokens][experts] */
     float *probs;         /* [tokens][experts] */
     uint32_t *ids;        /* [tokens][top_k], descending probability */

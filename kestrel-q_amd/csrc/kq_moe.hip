@@ -37,15 +37,141 @@ constexpr int kThreads = 256;
 
 uint32_t pad64(uint32_t n) { return (n + 63u) & ~63u; }
 
-/* ------------------------- router transpose ------------------------- */
-/* Tile: 64 rows (experts) x 64 columns. Rows >= experts+1 are zero; row
- * `experts` is the shared gate vector. With PRODUCTS the tile is multiplied
- * by x (one token). Output [H/4][Ep][4]. */
-template <bool PRODUCTS>
+/* ------------------------- router, one token ------------------------- */
+/* One workgroup per 8 logit rows: expert rows, then the shared gate vector
+ * as row `experts`; rows past it load nothing and are discarded. Every
+ * thread issues all of its loads at once (HBM latency exceeds the chain
+ * time of a segment), then the four waves form the rounded binary32
+ * products w*x (as the CPU forms them) segment by segment and stage them in
+ * LDS as [q][row] float4, q = column / 4, with one float4 of padding per q
+ * so that every eight consecutive q of a store hit distinct banks. Lanes
+ * 0..7 of wave 0 run the left-to-right chains from LDS, one segment of 512
+ * columns behind the staging; a barrier per segment publishes it. The chain
+ * is 4 adds per q: a 2048-column router is 2048 dependent adds. */
+constexpr uint32_t kRtRows = 8;
+constexpr uint32_t kRtSegQ = 128;
+constexpr uint32_t kRtPitch = kRtRows + 1u;
+constexpr uint32_t kRtPerSeg = kRtRows * kRtSegQ / kThreads; /* float4 per thread */
+
+__device__ __forceinline__ void add4(float &acc, const float4 v) {
+    acc = acc + v.x;
+    acc = acc + v.y;
+    acc = acc + v.z;
+    acc = acc + v.w;
+}
+
+/* acc += b[0], b[pitch], ... for n float4 in order; full runs of 128 are
+ * software-pipelined so the next eight reads are in flight during the adds */
+__device__ __forceinline__ void chain_lds(const float4 *b, uint32_t pitch, uint32_t n,
+                                          float &acc) {
+    if (n == kRtSegQ) {
+        float4 va[8], vb[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) va[j] = b[j * pitch];
+#pragma unroll
+        for (uint32_t q = 0; q < kRtSegQ; q += 16u) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vb[j] = b[(q + 8u + j) * pitch];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) add4(acc, va[j]);
+            if (q + 16u < kRtSegQ) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) va[j] = b[(q + 16u + j) * pitch];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) add4(acc, vb[j]);
+        }
+    } else {
+        for (uint32_t q = 0; q < n; ++q) add4(acc, b[q * pitch]);
+    }
+}
+
+__device__ __forceinline__ float4 as_f4(const uint4 u) {
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                       __uint_as_float(u.w));
+}
+
+template <uint32_t HIDDEN>
+__global__ __launch_bounds__(kThreads) void router_decode(
+    const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
+    const float *__restrict__ x, uint32_t experts, float *__restrict__ logits,
+    float *__restrict__ shared_logit, uint32_t *status) {
+    constexpr uint32_t NQ = HIDDEN / 4u;
+    constexpr uint32_t NSEG = (NQ + kRtSegQ - 1u) / kRtSegQ;
+    __shared__ float4 buf[NSEG * kRtSegQ * kRtPitch];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t row0 = blockIdx.x * kRtRows;
+    /* thread covers column group ql of rows rsub + 2k (k < 4); rsub is
+     * uniform across a wave, so each row's buffer descriptor is scalar.
+     * Rows past the shared gate row get an empty buffer and columns past
+     * the row's end lie outside it: the buffer loads return zeros. */
+    const uint32_t ql = tid % kRtSegQ;
+    const uint32_t rsub = __builtin_amdgcn_readfirstlane(tid / kRtSegQ);
+    KqBuf rb[kRtPerSeg];
+#pragma unroll
+    for (uint32_t k = 0; k < kRtPerSeg; ++k) {
+        const uint32_t e = row0 + rsub + 2u * k;
+        rb[k] = kq_buf(e < experts ? router + (size_t)e * HIDDEN : shared_gate_weight,
+                       e <= experts ? HIDDEN * 4u : 0u);
+    }
+    const KqBuf xb = kq_buf(x, HIDDEN * 4u);
+    uint4 v[NSEG][kRtPerSeg], xr[NSEG];
+#pragma unroll
+    for (uint32_t sg = 0; sg < NSEG; ++sg) {
+        const uint32_t off = (sg * kRtSegQ + ql) * 16u;
+        xr[sg] = kq_ld128(xb, off, 0);
+#pragma unroll
+        for (uint32_t k = 0; k < kRtPerSeg; ++k) v[sg][k] = kq_ld128(rb[k], off, 0);
+    }
+    bool bad = false;
+    auto stage = [&](uint32_t sg) {
+        float4 *b = buf + (sg * kRtSegQ + ql) * kRtPitch + rsub;
+        const float4 xq = as_f4(xr[sg]);
+#pragma unroll
+        for (uint32_t k = 0; k < kRtPerSeg; ++k) {
+            const float4 w = as_f4(v[sg][k]);
+            bad |= !kq_isfinite(w.x) || !kq_isfinite(w.y) || !kq_isfinite(w.z) ||
+                   !kq_isfinite(w.w);
+            float4 p;
+            p.x = w.x * xq.x;
+            p.y = w.y * xq.y;
+            p.z = w.z * xq.z;
+            p.w = w.w * xq.w;
+            b[2u * k] = p;
+        }
+    };
+    stage(0);
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (uint32_t sg = 0; sg < NSEG; ++sg) {
+        if (tid < kRtRows) {
+            constexpr uint32_t kLast = NQ - (NSEG - 1u) * kRtSegQ;
+            chain_lds(buf + sg * kRtSegQ * kRtPitch + tid, kRtPitch,
+                      sg + 1u < NSEG ? kRtSegQ : kLast, acc);
+        }
+        if (sg + 1u < NSEG) {
+            stage(sg + 1u);
+            __syncthreads();
+        }
+    }
+    if (tid < kRtRows) {
+        const uint32_t e = row0 + tid;
+        if (e < experts)
+            logits[e] = acc;
+        else if (e == experts)
+            *shared_logit = acc;
+    }
+    if (bad) kq_flag(status, KQ_DEV_INPUT);
+}
+
+/* ---------------------- router, several tokens ---------------------- */
+/* The router matrix (plus the shared gate vector as row E) is transposed to
+ * [H/4][E_pad][4] (64x64 LDS tiles; rows past E are zero) so that step q of
+ * a wave's 64 chains reads 1 KiB contiguous. */
 __global__ __launch_bounds__(kThreads) void router_transpose(
     const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
-    const float *__restrict__ x, uint32_t experts, uint32_t hidden, uint32_t ep,
-    float *__restrict__ out, uint32_t *status) {
+    uint32_t experts, uint32_t hidden, uint32_t ep, float *__restrict__ out, uint32_t *status) {
     __shared__ float4 tile[64][17];
     const uint32_t e0 = blockIdx.x * 64u, q0 = blockIdx.y * 16u;
     const uint32_t tid = threadIdx.x;
@@ -63,13 +189,6 @@ __global__ __launch_bounds__(kThreads) void router_transpose(
                 v = *(const float4 *)(shared_gate_weight + 4u * q);
             bad |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
                    !kq_isfinite(v.w);
-            if (PRODUCTS) {
-                const float4 xv = *(const float4 *)(x + 4u * q);
-                v.x = v.x * xv.x;
-                v.y = v.y * xv.y;
-                v.z = v.z * xv.z;
-                v.w = v.w * xv.w;
-            }
         }
         tile[er][qc] = v;
     }
@@ -84,60 +203,38 @@ __global__ __launch_bounds__(kThreads) void router_transpose(
     if (bad) kq_flag(status, KQ_DEV_INPUT);
 }
 
-/* ------------------------- router chain ------------------------- */
-/* One lane per expert (and lane `experts` for the shared gate logit): the
- * CPU's left-to-right binary32 accumulation over H terms. One wave per
- * workgroup so the 64-lane chains spread over CUs. */
-template <bool PRODUCTS>
-__global__ __launch_bounds__(64) void router_chain(const float *__restrict__ src,
+/* One lane per (token, expert): p = w * x rounded, acc = acc + p, in column
+ * order. One wave per workgroup so the chains spread over CUs. */
+__global__ __launch_bounds__(64) void router_chain(const float *__restrict__ wt,
                                                    const float *__restrict__ hidden_states,
                                                    uint32_t experts, uint32_t hidden,
                                                    uint32_t ep, float *__restrict__ logits,
                                                    float *__restrict__ shared_logit) {
     const uint32_t e = blockIdx.x * 64u + threadIdx.x;
     const uint32_t t = blockIdx.y;
-    const float *x = hidden_states + (size_t)t * hidden;
-    const float4 *s = (const float4 *)src + e;
+    const float4 *x = (const float4 *)(hidden_states + (size_t)t * hidden);
+    const float4 *s = (const float4 *)wt + e;
     const uint32_t nq = hidden / 4u;
     float acc = 0.0f;
+    auto step = [&](const float4 w, const float4 xv) {
+        float p;
+        p = w.x * xv.x; acc = acc + p;
+        p = w.y * xv.y; acc = acc + p;
+        p = w.z * xv.z; acc = acc + p;
+        p = w.w * xv.w; acc = acc + p;
+    };
     uint32_t q = 0;
     for (; q + 8u <= nq; q += 8u) {
-        float4 v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = s[(size_t)(q + j) * ep];
+        float4 v[8], xv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            if (PRODUCTS) {
-                acc = acc + v[j].x;
-                acc = acc + v[j].y;
-                acc = acc + v[j].z;
-                acc = acc + v[j].w;
-            } else {
-                const float4 xv = *(const float4 *)(x + 4u * (q + j));
-                float p;
-                p = v[j].x * xv.x; acc = acc + p;
-                p = v[j].y * xv.y; acc = acc + p;
-                p = v[j].z * xv.z; acc = acc + p;
-                p = v[j].w * xv.w; acc = acc + p;
-            }
+            v[j] = s[(size_t)(q + j) * ep];
+            xv[j] = x[q + j];
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) step(v[j], xv[j]);
     }
-    for (; q < nq; ++q) {
-        const float4 v = s[(size_t)q * ep];
-        if (PRODUCTS) {
-            acc = acc + v.x;
-            acc = acc + v.y;
-            acc = acc + v.z;
-            acc = acc + v.w;
-        } else {
-            const float4 xv = *(const float4 *)(x + 4u * q);
-            float p;
-            p = v.x * xv.x; acc = acc + p;
-            p = v.y * xv.y; acc = acc + p;
-            p = v.z * xv.z; acc = acc + p;
-            p = v.w * xv.w; acc = acc + p;
-        }
-    }
+    for (; q < nq; ++q) step(s[(size_t)q * ep], x[q]);
     if (e < experts)
         logits[(size_t)t * experts + e] = acc;
     else if (e == experts)
@@ -145,61 +242,159 @@ __global__ __launch_bounds__(64) void router_chain(const float *__restrict__ src
 }
 
 /* ------------------------- route finish ------------------------- */
-__device__ __forceinline__ float block_max(float v, float *red) {
+/* Maximum over the 64 lanes of a wave, returned in every lane: DPP within
+ * 16-lane rows, then permlane swaps across rows. All lanes must be active. */
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, kq_dpp_pair<1>(v));
+    v = fmaxf(v, kq_dpp_pair<2>(v));
+    v = fmaxf(v, kq_dpp_pair<7>(v));
+    v = fmaxf(v, kq_dpp_pair<15>(v));
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+    const uint32_t lane = threadIdx.x & 63u;
+    return (uint32_t)__popcll(lane ? (m & (~0ull >> (64u - lane))) : 0ull);
+}
+
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+/* Maximum over the wave of int keys, in every lane (DPP within rows,
+ * permlane swaps across rows; all lanes active). */
+template <int CTRL>
+__device__ __forceinline__ int dpp_imax(int v) {
+    return max(v, __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ int wave_imax(int v) {
+    v = dpp_imax<0xB1>(v);  /* lane ^ 1 */
+    v = dpp_imax<0x4E>(v);  /* lane ^ 2 */
+    v = dpp_imax<0x141>(v); /* mirror within 8 */
+    v = dpp_imax<0x140>(v); /* mirror within 16 */
+    auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = max((int)r[0], (int)r[1]);
+    r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return max((int)r[0], (int)r[1]);
+}
+
+template <int S>
+__device__ __forceinline__ int tree_imax(const int *c) {
+    if constexpr (S == 1) {
+        return c[0];
+    } else {
+        return max(tree_imax<S / 2>(c), tree_imax<S / 2>(c + S / 2));
+    }
+}
+
+/* k-th largest (with multiplicity) of v[0..n-1], n <= 64 * S, in every lane
+ * of the calling wave. The values are +0 or positive (softmax numerators),
+ * so their bit patterns order as int32, and -inf (negative as int32) marks
+ * an empty slot. Each round takes the maximum of what remains, counts its
+ * copies and removes them all. */
+template <int S>
+__device__ __forceinline__ float kth_largest(const float *v, uint32_t n, uint32_t k) {
+    const uint32_t lane = threadIdx.x & 63u;
+    constexpr int kEmpty = (int)0xff800000u;
+    int c[S];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, KQ_WAVE));
-    const uint32_t w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63u) == 0u) red[w] = v;
-    __syncthreads();
-    float m = red[0];
-    for (uint32_t i = 1; i < nw; ++i) m = fmaxf(m, red[i]);
-    return m;
+    for (int s = 0; s < S; ++s) {
+        const uint32_t i = lane + 64u * s;
+        c[s] = i < n ? __float_as_int(v[i]) : kEmpty;
+    }
+    uint32_t taken = 0;
+    int m = kEmpty;
+    for (uint32_t r = 0; r < k; ++r) {
+        m = wave_imax(tree_imax<S>(c));
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const bool hit = c[s] == m;
+            cnt += (uint32_t)__popcll(__ballot(hit));
+            c[s] = hit ? kEmpty : c[s];
+        }
+        taken += cnt;
+        if (taken >= k || cnt == 0u) break;
+    }
+    return __int_as_float(m);
 }
 
-__device__ __forceinline__ uint32_t block_count(bool pred, uint32_t *cnt) {
-    const uint64_t m = __ballot(pred);
-    const uint32_t w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63u) == 0u) cnt[w] = (uint32_t)__popcll(m);
-    __syncthreads();
-    uint32_t c = 0;
-    for (uint32_t i = 0; i < nw; ++i) c += cnt[i];
-    return c;
+/* Ballot masks of up to 16 waves: count of set bits in waves before `w`
+ * and in all waves. Entries of absent waves hold 0. */
+__device__ __forceinline__ void mask_counts(const uint64_t *msk, uint32_t w, uint32_t &before,
+                                            uint32_t &total) {
+    before = 0u;
+    total = 0u;
+#pragma unroll
+    for (uint32_t i = 0; i < 16u; ++i) {
+        const uint32_t c = (uint32_t)__popcll(msk[i]);
+        before += i < w ? c : 0u;
+        total += c;
+    }
 }
 
-/* exclusive prefix count of pred over thread index (all threads) */
-__device__ __forceinline__ uint32_t block_prefix(bool pred, uint32_t *cnt) {
-    const uint64_t m = __ballot(pred);
-    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0u) cnt[w] = (uint32_t)__popcll(m);
-    __syncthreads();
-    uint32_t before = 0;
-    for (uint32_t i = 0; i < w; ++i) before += cnt[i];
-    const uint64_t below = lane ? (m & (~0ull >> (64u - lane))) : 0ull;
-    return before + (uint32_t)__popcll(below);
-}
-
-/* One workgroup per token; thread e owns expert e (blockDim = Ep <= 1024). */
+/* One workgroup per token; thread e owns expert e. The last wave (an extra
+ * all-padding wave when the block has room) runs the softmax's
+ * left-to-right sum on lane 0 while wave 0 finds the k-th largest ex.
+ *
+ * Selection runs on ex = expf(l - max): p = fl(ex / s) is non-decreasing in
+ * ex for the one divisor s, so the k-th largest p (with multiplicity) is
+ * v* = fl(ex* / s) for the k-th largest ex*. With G = {p > v*}, T = {p ==
+ * v*} and c(e) = |(G u T) n [0, e]|, the CPU's partial selection keeps G
+ * and the members e of T with c(e) <= k, less the |G n {c > k}| lowest ids
+ * among them (c(e) <= k is e <= t0 for members, t0 being the member at
+ * which the running count reaches k). */
 __global__ __launch_bounds__(1024) void route_finish(
     const float *__restrict__ logits_all, const float *__restrict__ shared_logit,
     uint32_t experts, uint32_t top_k, float *__restrict__ probs_all, uint32_t *__restrict__ ids_all,
     float *__restrict__ weights_all, uint32_t *__restrict__ order_all,
     float *__restrict__ shared_scale, uint32_t *status) {
-    __shared__ float ev[1024];
-    __shared__ float red[16];
-    __shared__ uint32_t cnt[16];
-    __shared__ uint32_t sel_id[64];
-    __shared__ float sel_p[64];
-    __shared__ float s_sum;
-    __shared__ uint32_t s_t0;
+    __shared__ __align__(16) float ev[1024];
+    __shared__ __align__(16) float wmx[16];
+    __shared__ __align__(16) uint32_t wbad[16];
+    __shared__ __align__(16) uint64_t msk[4][16];
+    __shared__ __align__(16) uint32_t sel_id[64];
+    __shared__ __align__(16) float sel_p[64];
+    __shared__ __align__(16) float sorted_p[64];
+    __shared__ float s_sum, s_exk;
     const uint32_t t = blockIdx.x, e = threadIdx.x;
+    const uint32_t lane = e & 63u, w = e >> 6, nw = blockDim.x >> 6;
+    const uint32_t sum_wave = nw - 1u;
     const bool live = e < experts;
-    const float *logits = logits_all + (size_t)t * experts;
-    float l = live ? logits[e] : -__builtin_inff();
+    const float l = live ? logits_all[(size_t)t * experts + e] : -__builtin_inff();
+    const float sl = e == 0u ? shared_logit[t] : 0.0f;
     const bool bad_in = live && !kq_isfinite(l);
-    if (block_count(bad_in, cnt) != 0u) {
+    if (e < 16u && e >= nw) {
+        wmx[e] = -__builtin_inff();
+        wbad[e] = 0u;
+        for (int r = 0; r < 4; ++r) msk[r][e] = 0ull;
+    }
+    if (e < 64u) sorted_p[e] = 0.0f;
+
+    /* max of the logits and the count of non-finite ones, one barrier */
+    {
+        const float wm = wave_max(l);
+        const uint64_t bm = __ballot(bad_in);
+        if (lane == 0u) {
+            wmx[w] = wm;
+            wbad[w] = (uint32_t)__popcll(bm);
+        }
+    }
+    __syncthreads();
+    float m = -__builtin_inff();
+    uint32_t nbad = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 16u; ++i) {
+        m = fmaxf(m, wmx[i]);
+        nbad += wbad[i];
+    }
+    if (nbad != 0u) {
         /* fail closed, but leave in-range ids for the expert kernels */
         if (e < top_k) {
             ids_all[(size_t)t * top_k + e] = e;
@@ -212,53 +407,76 @@ __global__ __launch_bounds__(1024) void route_finish(
         }
         return;
     }
-    /* softmax: exact max, expf(l - max), left-to-right sum, divide */
-    const float m = block_max(l, red);
+
     const float ex = live ? kq_expf(l - m) : 0.0f;
     ev[e] = ex;
     __syncthreads();
-    if (e == 0) {
-        float s = 0.0f;
-        for (uint32_t i = 0; i < experts; ++i) s = s + ev[i];
-        s_sum = s;
-        shared_scale[t] = kq_sigmoid(shared_logit[t]);
-        if (!kq_isfinite(s) || !(s > 0.0f)) kq_flag(status, KQ_DEV_NUMERIC);
+    /* Softmax sum, left to right. Entries past the experts hold +0, which
+     * leaves a non-negative running sum unchanged, so the sum runs over
+     * whole float4 in pipelined runs. Global stores wait until after the
+     * last barrier (a barrier waits for the wave's outstanding stores). */
+    if (w == sum_wave && lane == 0u) {
+        float sum = 0.0f;
+        const uint32_t nv = (experts + 3u) / 4u;
+        for (uint32_t i = 0; i < nv; i += kRtSegQ) {
+            const uint32_t left = nv - i;
+            chain_lds((const float4 *)ev + i, 1u, left < kRtSegQ ? left : kRtSegQ, sum);
+        }
+        s_sum = sum;
+    }
+    if (w == 0u) {
+        float exk;
+        if (experts <= 64u)
+            exk = kth_largest<1>(ev, experts, top_k);
+        else if (experts <= 128u)
+            exk = kth_largest<2>(ev, experts, top_k);
+        else if (experts <= 256u)
+            exk = kth_largest<4>(ev, experts, top_k);
+        else if (experts <= 512u)
+            exk = kth_largest<8>(ev, experts, top_k);
+        else
+            exk = kth_largest<16>(ev, experts, top_k);
+        if (lane == 0u) s_exk = exk;
     }
     __syncthreads();
-    const float p = live ? ex / s_sum : -__builtin_inff();
-    if (live) probs_all[(size_t)t * experts + e] = p;
-
-    /* v* = k-th largest probability counting multiplicity */
-    float vstar = 0.0f;
-    {
-        float cur = p;
-        uint32_t taken = 0;
-        for (uint32_t round = 0; round < top_k; ++round) {
-            const float mx = block_max(cur, red);
-            const uint32_t c = block_count(live && p == mx, cnt);
-            taken += c;
-            if (taken >= top_k) {
-                vstar = mx;
-                break;
-            }
-            if (p == mx) cur = -__builtin_inff();
-        }
-    }
+    const float s = s_sum;
+    const float p = live ? ex / s : -__builtin_inff();
+    const float vstar = s_exk / s;
     const bool in_g = live && p > vstar;
     const bool in_t = live && p == vstar;
-    /* t0: index where the running count of {p >= v*} reaches k */
-    if (e == 0) s_t0 = experts - 1u;
-    const uint32_t ge_before = block_prefix(in_g || in_t, cnt);
-    if ((in_g || in_t) && ge_before + 1u == top_k) s_t0 = e;
+    {
+        const uint64_t gm = __ballot(in_g);
+        const uint64_t tm = __ballot(in_t);
+        if (lane == 0u) {
+            msk[0][w] = gm;
+            msk[1][w] = tm;
+        }
+    }
     __syncthreads();
-    const uint32_t t0 = s_t0;
-    const uint32_t g_after = block_count(in_g && e > t0, cnt);
-    const uint32_t tie_rank = block_prefix(in_t && e <= t0, cnt);
-    const bool keep = in_g || (in_t && e <= t0 && tie_rank >= g_after);
-    const uint32_t slot = block_prefix(keep, cnt);
+    /* c(e) = members of G u T up to e; the tie candidates are the members
+     * of T with c(e) <= k, and the last k - |G| of them are kept */
+    uint32_t g_before, g_total, t_before, t_total;
+    mask_counts(msk[0], w, g_before, g_total);
+    mask_counts(msk[1], w, t_before, t_total);
+    const uint32_t g_pre = g_before + lanes_below(msk[0][w]);
+    const uint32_t t_pre = t_before + lanes_below(msk[1][w]);
+    const bool tie_cand = in_t && g_pre + t_pre + 1u <= top_k;
+    {
+        const uint64_t cm = __ballot(tie_cand);
+        if (lane == 0u) msk[2][w] = cm;
+    }
+    __syncthreads();
+    uint32_t c_before, cands;
+    mask_counts(msk[2], w, c_before, cands);
+    const uint32_t c_pre = c_before + lanes_below(msk[2][w]); /* tie candidates below e */
+    const uint32_t need = top_k > g_total ? top_k - g_total : 0u;
+    const uint32_t drop = cands > need ? cands - need : 0u;    /* lowest candidates dropped */
+    const bool keep = in_g || (tie_cand && c_pre >= drop);
+    /* ascending-id slot: G members below e plus kept candidates below e */
+    const uint32_t slot = g_pre + (c_pre > drop ? c_pre - drop : 0u);
+    const uint32_t kept = g_total + (cands < need ? cands : need);
     /* the selection has exactly k members by construction; a defect would
      * otherwise index past sel_id, so it fails closed with in-range ids */
-    const uint32_t kept = block_count(keep, cnt);
     if (kept == top_k) {
         if (keep) {
             sel_id[slot] = e;
@@ -272,33 +490,40 @@ __global__ __launch_bounds__(1024) void route_finish(
         if (e == 0) kq_flag(status, KQ_DEV_NUMERIC);
     }
     __syncthreads();
+    /* position in descending-p, ascending-id order; the position in
+     * ascending-id order (the combine order) is the compaction slot */
+    uint32_t pos = 0, my_id = 0;
+    float my_p = 0.0f;
     if (e < top_k) {
-        /* position in descending-p, ascending-id order; position in
-         * ascending-id order (the combine order) is the compaction slot */
-        const float my_p = sel_p[e];
-        const uint32_t my_id = sel_id[e];
-        uint32_t pos = 0;
-        for (uint32_t j = 0; j < top_k; ++j) {
-            const float pj = sel_p[j];
-            const uint32_t ij = sel_id[j];
-            pos += (pj > my_p || (pj == my_p && ij < my_id)) ? 1u : 0u;
+        my_p = sel_p[e];
+        my_id = sel_id[e];
+        for (uint32_t j0 = 0; j0 < top_k; j0 += 4u) {
+            const float4 pj = *(const float4 *)(sel_p + j0);
+            const uint4 ij = *(const uint4 *)(sel_id + j0);
+            const float pv[4] = {pj.x, pj.y, pj.z, pj.w};
+            const uint32_t iv[4] = {ij.x, ij.y, ij.z, ij.w};
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q)
+                pos += (j0 + q < top_k && (pv[q] > my_p || (pv[q] == my_p && iv[q] < my_id)))
+                           ? 1u : 0u;
         }
-        ids_all[(size_t)t * top_k + pos] = my_id;
-        weights_all[(size_t)t * top_k + pos] = my_p;
-        order_all[(size_t)t * top_k + e] = pos;
+        sorted_p[pos] = my_p;
     }
     __syncthreads();
-    if (e == 0) {
-        /* w = p / (left-to-right sum in top-k order) */
-        float *w = weights_all + (size_t)t * top_k;
-        float s = 0.0f;
-        for (uint32_t j = 0; j < top_k; ++j) s += w[j];
-        bool ok = kq_isfinite(s) && s > 0.0f;
-        for (uint32_t j = 0; j < top_k; ++j) {
-            w[j] /= s;
-            ok = ok && kq_isfinite(w[j]);
-        }
-        if (!ok) kq_flag(status, KQ_DEV_NUMERIC);
+    /* w = p / (left-to-right sum in top-k order); entries past k hold +0 */
+    float ws = 0.0f;
+    if (e < top_k) chain_lds((const float4 *)sorted_p, 1u, (top_k + 3u) / 4u, ws);
+    if (e < top_k) {
+        const float wgt = my_p / ws;
+        ids_all[(size_t)t * top_k + pos] = my_id;
+        weights_all[(size_t)t * top_k + pos] = wgt;
+        order_all[(size_t)t * top_k + e] = pos;
+        if (!kq_isfinite(wgt) || !kq_isfinite(ws) || !(ws > 0.0f)) kq_flag(status, KQ_DEV_NUMERIC);
+    }
+    if (live) probs_all[(size_t)t * experts + e] = p;
+    if (e == 0u) {
+        shared_scale[t] = kq_sigmoid(sl);
+        if (!kq_isfinite(s) || !(s > 0.0f)) kq_flag(status, KQ_DEV_NUMERIC);
     }
 }
 
@@ -425,21 +650,39 @@ __global__ __launch_bounds__(kThreads) void moe_combine(
     const float *__restrict__ expert_out, const float *__restrict__ weights,
     const uint32_t *__restrict__ order, const float *__restrict__ shared_scale, uint32_t top_k,
     uint32_t hidden, float *__restrict__ out, uint32_t *status) {
+    __shared__ uint32_t ord_s[64];
+    __shared__ float w_s[64];
     const uint32_t t = blockIdx.y;
     const uint32_t f = blockIdx.x * kThreads + threadIdx.x;
+    /* slots in ascending expert id with their weights, staged once so the
+     * expert-output loads below do not wait on them */
+    if (threadIdx.x < top_k) {
+        const uint32_t s = order[(size_t)t * top_k + threadIdx.x];
+        ord_s[threadIdx.x] = s;
+        w_s[threadIdx.x] = weights[(size_t)t * top_k + s];
+    }
+    __syncthreads();
     if (f >= hidden) return;
-    const float *eo = expert_out + (size_t)t * (top_k + 1u) * hidden;
-    const float *w = weights + (size_t)t * top_k;
-    const uint32_t *ord = order + (size_t)t * top_k;
+    const float *eo = expert_out + (size_t)t * (top_k + 1u) * hidden + f;
+    const float scale = shared_scale[t];
+    const float so = eo[(size_t)top_k * hidden];
     float sum = 0.0f;
     bool bad = false;
-    for (uint32_t j = 0; j < top_k; ++j) {
-        const uint32_t s = ord[j];
-        const float weighted = eo[(size_t)s * hidden + f] * w[s];
-        sum = sum + weighted;
-        bad |= !kq_isfinite(sum);
+    for (uint32_t j0 = 0; j0 < top_k; j0 += 8u) {
+        float o[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j)
+            o[j] = j0 + j < top_k ? eo[(size_t)ord_s[j0 + j] * hidden] : 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j) {
+            if (j0 + j < top_k) {
+                const float weighted = o[j] * w_s[j0 + j];
+                sum = sum + weighted;
+                bad |= !kq_isfinite(sum);
+            }
+        }
     }
-    const float gated = eo[(size_t)top_k * hidden + f] * shared_scale[t];
+    const float gated = so * scale;
     const float v = sum + gated;
     bad |= !kq_isfinite(gated) || !kq_isfinite(v);
     out[(size_t)t * hidden + f] = v;
@@ -565,29 +808,37 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
                                           uint32_t tokens, const kq_launch_moe_ws *ws,
                                           uint32_t *status, hipStream_t s) {
     const uint32_t ep = pad64(d->experts + 1u);
-    const dim3 tgrid(ep / 64u, (d->hidden / 4u + 15u) / 16u);
-    const bool products = tokens == 1u;
-    if (products)
-        hipLaunchKernelGGL((router_transpose<true>), tgrid, dim3(kThreads), 0, s, router,
-                           shared_gate_weight, hidden, d->experts, d->hidden, ep, ws->router_t,
-                           status);
-    else
-        hipLaunchKernelGGL((router_transpose<false>), tgrid, dim3(kThreads), 0, s, router,
-                           shared_gate_weight, hidden, d->experts, d->hidden, ep, ws->router_t,
-                           status);
+    const uint32_t groups = (d->experts + 1u + kRtRows - 1u) / kRtRows;
+    bool fused = tokens == 1u;
+#define KQ_ROUTER_DECODE(H)                                                                   \
+    hipLaunchKernelGGL(router_decode<H>, dim3(groups), dim3(kThreads), 0, s, router,          \
+                       shared_gate_weight, hidden, d->experts, ws->logits, ws->shared_logit, \
+                       status)
+    if (fused) {
+        switch (d->hidden) {
+        case 256: KQ_ROUTER_DECODE(256u); break;
+        case 512: KQ_ROUTER_DECODE(512u); break;
+        case 1024: KQ_ROUTER_DECODE(1024u); break;
+        case 2048: KQ_ROUTER_DECODE(2048u); break;
+        default: fused = false;
+        }
+    }
+#undef KQ_ROUTER_DECODE
+    if (!fused) {
+        /* several tokens, or a hidden size without a fused instance */
+        const dim3 tgrid(ep / 64u, (d->hidden / 4u + 15u) / 16u);
+        hipLaunchKernelGGL(router_transpose, tgrid, dim3(kThreads), 0, s, router,
+                           shared_gate_weight, d->experts, d->hidden, ep, ws->router_t, status);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(router_chain, dim3(ep / 64u, tokens), dim3(64), 0, s, ws->router_t,
+                           hidden, d->experts, d->hidden, ep, ws->logits, ws->shared_logit);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (products)
-        hipLaunchKernelGGL((router_chain<true>), dim3(ep / 64u, tokens), dim3(64), 0, s,
-                           ws->router_t, hidden, d->experts, d->hidden, ep, ws->logits,
-                           ws->shared_logit);
-    else
-        hipLaunchKernelGGL((router_chain<false>), dim3(ep / 64u, tokens), dim3(64), 0, s,
-                           ws->router_t, hidden, d->experts, d->hidden, ep, ws->logits,
-                           ws->shared_logit);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(ep), 0, s, ws->logits, ws->shared_logit,
+    uint32_t fin = 64u * ((d->experts + 63u) / 64u + 1u);
+    if (fin > 1024u) fin = 1024u;
+    hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, ws->logits, ws->shared_logit,
                        d->experts, d->top_k, ws->probs, ws->ids, ws->weights, ws->order,
                        ws->shared_scale, status);
     return hipGetLastError();
