@@ -81,7 +81,6 @@ typedef struct kq_launch_moe_ws {
     float *shared_logit;  /* [tokens] */
     float *shared_scale;  /* [tokens] */
     float *act;           /* [tokens][top_k + 1][max(inter, shared_inter)] */
-    float *expert_out;    /* [tokens][top_k + 1][hidden] */
 } kq_launch_moe_ws;
 
 uint32_t kq_launch_moe_experts_padded(uint32_t experts);

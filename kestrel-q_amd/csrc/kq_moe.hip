@@ -540,6 +540,7 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
     float *__restrict__ act, uint32_t *status) {
     using R = kq::Rows<TYPE, COLS, 1, RT>;
     using Raw = typename R::Raw;
+    __shared__ __align__(16) float xs[COLS];
     const uint32_t slot = blockIdx.y, t = blockIdx.z;
     const bool shared = slot == top_k;
     const uint32_t rows = shared ? shared_inter : inter;
@@ -566,7 +567,20 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
         R::load_group(ln, gb, g, rows, sub, rg);
         R::load_group(ln, ub, g, rows, sub, ru);
     }
-    if (ln.load_x(hidden_states + (size_t)t * COLS, COLS)) kq_flag(status, KQ_DEV_INPUT);
+    /* the token's hidden state is staged once per workgroup */
+    {
+        const float4 *src = (const float4 *)(hidden_states + (size_t)t * COLS);
+        bool badx = false;
+        for (uint32_t i = threadIdx.x; i < COLS / 4u; i += kThreads) {
+            const float4 v = src[i];
+            badx |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                    !kq_isfinite(v.w);
+            ((float4 *)xs)[i] = v;
+        }
+        if (badx) kq_flag(status, KQ_DEV_INPUT);
+    }
+    __syncthreads();
+    ln.load_x(xs, COLS);
     bool bad = false, malformed = false;
     float *out = act + ((size_t)t * (top_k + 1u) + slot) * act_stride;
     for (; g < ngroups; g += nwaves) {
@@ -594,98 +608,96 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
 }
 
-/* ------------------------------ down ------------------------------ */
-/* grid: x = row groups over hidden, y = slot, z = token.
- * expert_out[t][slot][f] = Wd[f] . act[t][slot]. */
+/* -------------------------- down + combine -------------------------- */
+/* grid: x = groups of R::GROUP output rows, y = token; one wave per slot
+ * (slots 0..K-1 routed by top-k position, slot K the shared expert; waves
+ * take further slots in steps of the wave count). Each wave reduces its
+ * slot's rows Wd[f] . act[t][slot] into LDS; after a barrier one thread per
+ * row forms the combine in the CPU's order:
+ *   routed_sum = 0; for slots in ascending expert id: routed_sum += o * w;
+ *   out = routed_sum + o_shared * sigmoid(shared logit). */
+constexpr uint32_t kMaxSlots = 65;
+
+constexpr uint32_t kDownWaves = 12;
+
 template <uint32_t TYPE, uint32_t COLS, int RT>
-__global__ __launch_bounds__(kThreads) void expert_down(
+__global__ __launch_bounds__(64 * kDownWaves) void expert_down_combine(
     const uint8_t *__restrict__ down, const uint8_t *__restrict__ sdown,
-    const float *__restrict__ act, const uint32_t *__restrict__ ids, uint32_t top_k,
-    uint32_t hidden, uint32_t act_stride, float *__restrict__ expert_out, uint32_t *status) {
+    const float *__restrict__ act, const uint32_t *__restrict__ ids,
+    const uint32_t *__restrict__ order, const float *__restrict__ weights,
+    const float *__restrict__ shared_scale, uint32_t top_k, uint32_t hidden,
+    uint32_t act_stride, float *__restrict__ out, uint32_t *status) {
     using R = kq::Rows<TYPE, COLS, 1, RT>;
     using Raw = typename R::Raw;
-    const uint32_t slot = blockIdx.y, t = blockIdx.z;
-    const bool shared = slot == top_k;
-    const uint8_t *D =
-        shared ? sdown : down + (size_t)ids[(size_t)t * top_k + slot] * hidden * R::RB;
-    const KqBuf db = kq_buf(D, hidden * R::RB);
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
-    const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
-    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
-    const uint32_t ngroups = (hidden + R::GROUP - 1u) / R::GROUP;
-    typename R::Lane ln;
-    ln.setup(l);
-    Raw rd[RT];
-    uint32_t g = wave;
-    if (g < ngroups) R::load_group(ln, db, g, hidden, sub, rd);
-    if (ln.load_x(act + ((size_t)t * (top_k + 1u) + slot) * act_stride, COLS))
-        kq_flag(status, KQ_DEV_NUMERIC);
-    bool bad = false, malformed = false;
-    float *out = expert_out + ((size_t)t * (top_k + 1u) + slot) * hidden;
-    for (; g < ngroups; g += nwaves) {
-        if (g != wave) R::load_group(ln, db, g, hidden, sub, rd);
-        float v[R::N];
-        R::dot_group(ln, rd, l, v, malformed);
-#pragma unroll
-        for (int j = 0; j < R::KEEP; ++j) {
-            const int idx = R::value_index(l, j);
-            if (idx >= 0) {
-                const uint32_t row = g * R::GROUP + (uint32_t)idx * R::RPW + sub;
-                if (row < hidden) {
-                    bad |= !kq_isfinite(v[j]);
-                    out[row] = v[j];
-                }
-            }
-        }
-    }
-    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
-    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
-}
-
-/* ------------------------------ combine ------------------------------ */
-/* routed_sum = 0; for experts in ascending id: routed_sum += o * w;
- * out = routed_sum + o_shared * sigmoid(shared logit). */
-__global__ __launch_bounds__(kThreads) void moe_combine(
-    const float *__restrict__ expert_out, const float *__restrict__ weights,
-    const uint32_t *__restrict__ order, const float *__restrict__ shared_scale, uint32_t top_k,
-    uint32_t hidden, float *__restrict__ out, uint32_t *status) {
+    __shared__ float res[kMaxSlots][R::GROUP];
     __shared__ uint32_t ord_s[64];
     __shared__ float w_s[64];
-    const uint32_t t = blockIdx.y;
-    const uint32_t f = blockIdx.x * kThreads + threadIdx.x;
-    /* slots in ascending expert id with their weights, staged once so the
-     * expert-output loads below do not wait on them */
+    const uint32_t g = blockIdx.x, t = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
+    const uint32_t nslots = top_k + 1u;
     if (threadIdx.x < top_k) {
         const uint32_t s = order[(size_t)t * top_k + threadIdx.x];
         ord_s[threadIdx.x] = s;
         w_s[threadIdx.x] = weights[(size_t)t * top_k + s];
     }
+    typename R::Lane ln;
+    ln.setup(l);
+    auto matrix = [&](uint32_t slot) {
+        const uint8_t *D = slot == top_k
+                               ? sdown
+                               : down + (size_t)ids[(size_t)t * top_k + slot] * hidden * R::RB;
+        return kq_buf(D, hidden * R::RB);
+    };
+    bool bad = false, malformed = false;
+    Raw ra[RT], rb[RT];
+    uint32_t slot = wv;
+    if (slot < nslots) R::load_group(ln, matrix(slot), g, hidden, sub, ra);
+    auto reduce = [&](const Raw (&raw)[RT], uint32_t sl) {
+        float v[R::N];
+        R::dot_group(ln, raw, l, v, malformed);
+#pragma unroll
+        for (int j = 0; j < R::KEEP; ++j) {
+            const int idx = R::value_index(l, j);
+            if (idx >= 0) res[sl][(uint32_t)idx * R::RPW + sub] = v[j];
+        }
+    };
+    /* ping-pong over this wave's slots: the next slot's rows are requested
+     * before this slot's activations */
+    while (slot < nslots) {
+        uint32_t next = slot + nwv;
+        if (next < nslots) R::load_group(ln, matrix(next), g, hidden, sub, rb);
+        bad |= ln.load_x(act + ((size_t)t * nslots + slot) * act_stride, COLS);
+        reduce(ra, slot);
+        slot = next;
+        if (slot >= nslots) break;
+        next = slot + nwv;
+        if (next < nslots) R::load_group(ln, matrix(next), g, hidden, sub, ra);
+        bad |= ln.load_x(act + ((size_t)t * nslots + slot) * act_stride, COLS);
+        reduce(rb, slot);
+        slot = next;
+    }
     __syncthreads();
-    if (f >= hidden) return;
-    const float *eo = expert_out + (size_t)t * (top_k + 1u) * hidden + f;
-    const float scale = shared_scale[t];
-    const float so = eo[(size_t)top_k * hidden];
-    float sum = 0.0f;
-    bool bad = false;
-    for (uint32_t j0 = 0; j0 < top_k; j0 += 8u) {
-        float o[8];
-#pragma unroll
-        for (uint32_t j = 0; j < 8u; ++j)
-            o[j] = j0 + j < top_k ? eo[(size_t)ord_s[j0 + j] * hidden] : 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < 8u; ++j) {
-            if (j0 + j < top_k) {
-                const float weighted = o[j] * w_s[j0 + j];
+    if (threadIdx.x < R::GROUP) {
+        const uint32_t row = g * R::GROUP + threadIdx.x;
+        if (row < hidden) {
+            float sum = 0.0f;
+            for (uint32_t j = 0; j < top_k; ++j) {
+                const uint32_t s = ord_s[j];
+                const float o = res[s][threadIdx.x];
+                bad |= !kq_isfinite(o);
+                const float weighted = o * w_s[j];
                 sum = sum + weighted;
-                bad |= !kq_isfinite(sum);
             }
+            const float so = res[top_k][threadIdx.x];
+            const float gated = so * shared_scale[t];
+            const float v = sum + gated;
+            bad |= !kq_isfinite(so) || !kq_isfinite(sum) || !kq_isfinite(gated) ||
+                   !kq_isfinite(v);
+            out[(size_t)t * hidden + row] = v;
         }
     }
-    const float gated = so * scale;
-    const float v = sum + gated;
-    bad |= !kq_isfinite(gated) || !kq_isfinite(v);
-    out[(size_t)t * hidden + f] = v;
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
 }
 
@@ -709,15 +721,16 @@ hipError_t launch_gateup(const kq_launch_moe_dims *d, const kq_launch_moe_weight
 template <uint32_t TYPE, uint32_t COLS>
 hipError_t launch_down(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                        uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t act_stride,
-                       uint32_t *status, hipStream_t s) {
+                       float *out, uint32_t *status, hipStream_t s) {
     constexpr int RT = 2;
-    const uint32_t rows_per_wave = kq::Rows<TYPE, COLS, 1, RT>::GROUP;
-    const uint32_t waves = (d->hidden + rows_per_wave - 1u) / rows_per_wave;
-    const uint32_t blocks = (waves + 3u) / 4u;
-    hipLaunchKernelGGL((expert_down<TYPE, COLS, RT>), dim3(blocks, d->top_k + 1u, tokens),
-                       dim3(kThreads), 0, s, (const uint8_t *)w->down,
-                       (const uint8_t *)w->shared_down, ws->act, ws->ids, d->top_k, d->hidden,
-                       act_stride, ws->expert_out, status);
+    const uint32_t group = kq::Rows<TYPE, COLS, 1, RT>::GROUP;
+    const uint32_t blocks = (d->hidden + group - 1u) / group;
+    uint32_t waves = d->top_k + 1u;
+    if (waves > kDownWaves) waves = kDownWaves;
+    hipLaunchKernelGGL((expert_down_combine<TYPE, COLS, RT>), dim3(blocks, tokens),
+                       dim3(64u * waves), 0, s, (const uint8_t *)w->down,
+                       (const uint8_t *)w->shared_down, ws->act, ws->ids, ws->order, ws->weights,
+                       ws->shared_scale, d->top_k, d->hidden, act_stride, out, status);
     return hipGetLastError();
 }
 
@@ -737,12 +750,12 @@ hipError_t gateup_cols(const kq_launch_moe_dims *d, const kq_launch_moe_weights 
 template <uint32_t TYPE>
 hipError_t down_cols(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                      uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t act_stride,
-                     uint32_t *status, hipStream_t s) {
+                     float *out, uint32_t *status, hipStream_t s) {
     switch (d->inter) {
-    case 256: return launch_down<TYPE, 256u>(d, w, tokens, ws, act_stride, status, s);
-    case 512: return launch_down<TYPE, 512u>(d, w, tokens, ws, act_stride, status, s);
-    case 1024: return launch_down<TYPE, 1024u>(d, w, tokens, ws, act_stride, status, s);
-    case 2048: return launch_down<TYPE, 2048u>(d, w, tokens, ws, act_stride, status, s);
+    case 256: return launch_down<TYPE, 256u>(d, w, tokens, ws, act_stride, out, status, s);
+    case 512: return launch_down<TYPE, 512u>(d, w, tokens, ws, act_stride, out, status, s);
+    case 1024: return launch_down<TYPE, 1024u>(d, w, tokens, ws, act_stride, out, status, s);
+    case 2048: return launch_down<TYPE, 2048u>(d, w, tokens, ws, act_stride, out, status, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -768,14 +781,12 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * d->top_k * 4u) * 3u;           /* ids, weights, order */
     b += align256((uint64_t)tokens * 4u) * 2u;                      /* shared logit, scale */
     b += align256((uint64_t)tokens * (d->top_k + 1u) * ai * 4u);    /* act */
-    b += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u); /* expert_out */
     return b;
 }
 
 extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tokens, void *base,
                                        kq_launch_moe_ws *ws) {
     const uint64_t ep = pad64(d->experts + 1u);
-    const uint64_t ai = d->inter > d->shared_inter ? d->inter : d->shared_inter;
     uint8_t *p = (uint8_t *)base;
     ws->router_t = (float *)p; p += align256((uint64_t)d->hidden * ep * 4u);
     ws->logits = (float *)p; p += align256((uint64_t)tokens * d->experts * 4u);
@@ -785,8 +796,7 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->order = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->shared_logit = (float *)p; p += align256((uint64_t)tokens * 4u);
     ws->shared_scale = (float *)p; p += align256((uint64_t)tokens * 4u);
-    ws->act = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * ai * 4u);
-    ws->expert_out = (float *)p;
+    ws->act = (float *)p;
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
@@ -864,14 +874,9 @@ extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
     }
     if (e != hipSuccess) return e;
     switch (w->down_type) {
-    case KQ_LAUNCH_Q4_K: e = down_cols<KQ_LAUNCH_Q4_K>(d, w, tokens, ws, act_stride, status, s); break;
-    case KQ_LAUNCH_Q6_K: e = down_cols<KQ_LAUNCH_Q6_K>(d, w, tokens, ws, act_stride, status, s); break;
-    case KQ_LAUNCH_Q8_0: e = down_cols<KQ_LAUNCH_Q8_0>(d, w, tokens, ws, act_stride, status, s); break;
+    case KQ_LAUNCH_Q4_K: return down_cols<KQ_LAUNCH_Q4_K>(d, w, tokens, ws, act_stride, out, status, s);
+    case KQ_LAUNCH_Q6_K: return down_cols<KQ_LAUNCH_Q6_K>(d, w, tokens, ws, act_stride, out, status, s);
+    case KQ_LAUNCH_Q8_0: return down_cols<KQ_LAUNCH_Q8_0>(d, w, tokens, ws, act_stride, out, status, s);
     default: return hipErrorInvalidValue;
     }
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(moe_combine, dim3((d->hidden + kThreads - 1u) / kThreads, tokens),
-                       dim3(kThreads), 0, s, ws->expert_out, ws->weights, ws->order,
-                       ws->shared_scale, d->top_k, d->hidden, out, status);
-    return hipGetLastError();
 }
