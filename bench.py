@@ -1,7 +1,7 @@
 """Benchmark of the MI355X quantized-weight path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME|all]
-                    [--no-cpu] [--no-graph]
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+                    [--workload NAME|all|headline|hbm_copy_64mb] [--no-cpu] [--no-graph]
 
 A step is one pass of the hot path over one batch of synthetic input with the
 weights already resident in HBM. The headline workload (value / metric) is
@@ -250,6 +250,17 @@ def wl_lm_head(ctx, batch, warmup, steps, graph):
             "replicas": len(reps)}
 
 
+def wl_copy(ctx, nbytes, warmup, steps, graph):
+    """Device-to-device copy of a known size: the reference point that scales
+    the FETCH_SIZE / WRITE_SIZE counters to bytes. Not part of `all`."""
+    a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    ms = time_steps(ctx, lambda i: d2d(ctx, b.ptr, a.ptr, nbytes), warmup, steps, graph)
+    for buf in (a, b):
+        buf.close()
+    return {"ms_per_step": ms, "bytes_per_step": 2 * nbytes, "GBps": 2 * nbytes / ms / 1e6,
+            "hbm_frac": 2 * nbytes / ms / 1e6 / HBM_PEAK_GBS, "copy_bytes": nbytes}
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(threads: int, budget_s: float = 3.0) -> dict:
     """The C oracle (restatement of the reference's scalar path, reference fp
@@ -344,6 +355,8 @@ def main() -> int:
         run("lm_head_q6k_151936x2048_b1", lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph))
         run("lm_head_q6k_151936x2048_b4", lambda: wl_lm_head(ctx, 4, 3, max(10, K // 10), graph))
         run("moe_prefill_512", lambda: wl_moe(ctx, 512, 1, 3, graph, cache))
+        if wanted == "hbm_copy_64mb":
+            run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))
     head = work.get(HEADLINE)
     threads = int(os.environ.get("KQ_CPU_THREADS", min(16, os.cpu_count() or 1)))
     cpu = None
