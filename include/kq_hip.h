@@ -124,7 +124,8 @@ kq_status kq_hip_quantized_row_dot_f32(kq_hip_context *context,
 /* Replaces kq_weight_provider_linear_f32 (include/kq_weight_provider.h:56-61,
  * src/kq_weight_provider.c:378-509), extended to `batch` activation vectors:
  * y[b*rows + r] = row r of W (packed, rows contiguous) . x[b*columns ...].
- * batch 1..8; columns 256, 512, 1024 or 2048. */
+ * batch 1..8; columns 256, 512, 1024 or 2048 (Q8_0 also 32, 64 or 128);
+ * the packed matrix below 4 GiB. */
 kq_status kq_hip_quantized_matvec_f32(kq_hip_context *context,
                                       uint32_t type_id,
                                       const void *device_weights,

@@ -184,37 +184,6 @@ __device__ __forceinline__ uint32_t kq_align2(uint32_t hi, uint32_t lo,
     return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }
 
-/* 8 bytes at a (a even). Reads [a - (a&3), a - (a&3) + (a&3 ? 12 : 8)):
- * at most 2 bytes past a + 8. */
-__device__ __forceinline__ uint2 kq_load8_u2a(const uint8_t *a) {
-    const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);
-    const uint32_t *base = (const uint32_t *)(a - sh);
-    const uint32_t d0 = base[0], d1 = base[1];
-    const uint32_t d2 = base[sh ? 2 : 1];
-    uint2 r;
-    r.x = kq_align2(d1, d0, sh);
-    r.y = kq_align2(d2, d1, sh);
-    return r;
-}
-
-/* As kq_load8_u2a, but never reads at or past `end` (a + 8 <= end). */
-__device__ __forceinline__ uint2 kq_load8_u2a_end(const uint8_t *a, const uint8_t *end) {
-    const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);
-    const uint32_t *base = (const uint32_t *)(a - sh);
-    const uint32_t d0 = base[0], d1 = base[1];
-    uint32_t d2 = d1;
-    if (sh) {
-        if ((const uint8_t *)(base + 3) <= end)
-            d2 = base[2];
-        else
-            d2 = (uint32_t)(*(const uint16_t *)(base + 2));
-    }
-    uint2 r;
-    r.x = kq_align2(d1, d0, sh);
-    r.y = kq_align2(d2, d1, sh);
-    return r;
-}
-
 /* 4 bytes at a (a even), reading at most 2 bytes past a + 4. */
 __device__ __forceinline__ uint32_t kq_load4_u2a(const uint8_t *a) {
     const uint32_t sh = (uint32_t)((uintptr_t)a & 3u);

@@ -28,9 +28,13 @@ hipError_t kq_launch_dequant(uint32_t type, const void *packed, uint64_t blocks,
 /* matvec / argmax (kq_matvec.hip) */
 int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t batch);
 uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols, uint32_t batch);
+/* part_v/part_i (optional): per batch column, part_stride argmax partials;
+ * the launch's waves fill the first kq_launch_matvec_waves of them and the
+ * rest get the neutral entry (-inf, UINT32_MAX). */
 hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_t cols,
                             const float *x, uint32_t batch, float *y, uint32_t *status,
-                            float *part_v, uint32_t *part_i, hipStream_t stream);
+                            float *part_v, uint32_t *part_i, uint32_t part_stride,
+                            hipStream_t stream);
 uint32_t kq_launch_argmax_parts(uint32_t count);
 hipError_t kq_launch_argmax(const float *logits, uint32_t count, uint32_t batch,
                             float *part_v, uint32_t *part_i, uint32_t *ids,

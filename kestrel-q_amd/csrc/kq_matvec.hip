@@ -47,7 +47,7 @@ template <uint32_t TYPE, uint32_t COLS, int B, int RT>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(
     const uint8_t *__restrict__ W, uint32_t rows, const float *__restrict__ x,
     float *__restrict__ y, uint32_t *status, float *part_v, uint32_t *part_i,
-    const uint8_t *w_end) {
+    uint32_t part_stride) {
     using R = kq::Rows<TYPE, COLS, B, RT>;
     using Raw = typename R::Raw;
     const uint32_t lane = threadIdx.x & 63u;
@@ -56,15 +56,28 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
     const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
 
+    __shared__ __align__(16) float xs[B * COLS];
     typename R::Lane ln;
     ln.setup(l);
     const KqBuf wb = kq_buf(W, rows * R::RB);
     Raw ra[RT], rb[RT];
     uint32_t g = wave;
     /* the first group's weights are requested before the activations so the
-     * two memory latencies overlap */
+     * two memory latencies overlap; the activations are staged once per
+     * workgroup in LDS and each lane takes its slice from there */
     if (g < ngroups) R::load_group(ln, wb, g, rows, sub, ra);
-    if (ln.load_x(x, COLS)) kq_flag(status, KQ_DEV_INPUT);
+    {
+        bool badx = false;
+        for (uint32_t i = threadIdx.x; i < B * COLS / 4u; i += kThreads) {
+            const float4 v = ((const float4 *)x)[i];
+            badx |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                    !kq_isfinite(v.w);
+            ((float4 *)xs)[i] = v;
+        }
+        if (badx) kq_flag(status, KQ_DEV_INPUT);
+    }
+    __syncthreads();
+    ln.load_x(xs, COLS);
 
     bool bad = false, malformed = false;
     float best_v[B];
@@ -112,8 +125,14 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
             uint32_t bi = best_i[b];
             wave_argmax(bv, bi);
             if (lane == 0) {
-                part_v[(size_t)b * nwaves + wave] = bv;
-                part_i[(size_t)b * nwaves + wave] = bi;
+                part_v[(size_t)b * part_stride + wave] = bv;
+                part_i[(size_t)b * part_stride + wave] = bi;
+                /* slots past this launch's waves (another launch of the same
+                 * call may have more) hold the neutral entry */
+                for (uint32_t sl = wave + nwaves; sl < part_stride; sl += nwaves) {
+                    part_v[(size_t)b * part_stride + sl] = -__builtin_inff();
+                    part_i[(size_t)b * part_stride + sl] = 0xffffffffu;
+                }
             }
         }
     }
@@ -178,52 +197,72 @@ uint32_t group_rows(uint32_t cols, uint32_t rt) {
     return (lanes >= 64u ? 1u : 64u / lanes) * rt;
 }
 
-/* RT = 1 for matrices whose RT = 4 grid would leave the GPU under-filled */
+/* RT = 2 (one group per wave) for matrices whose RT = 4 grid would leave
+ * the GPU under-filled */
 uint32_t pick_rt(uint32_t rows, uint32_t cols) {
     const uint32_t groups4 = (rows + group_rows(cols, 4) - 1u) / group_rows(cols, 4);
-    return groups4 >= kResidentWaves ? 4u : 1u;
+    return groups4 >= kResidentWaves ? 4u : 2u;
 }
 
-uint32_t waves_for(uint32_t rows, uint32_t cols, uint32_t batch) {
-    const uint32_t rt = pick_rt(rows, cols);
-    const uint32_t groups = (rows + group_rows(cols, rt) - 1u) / group_rows(cols, rt);
-    /* wide batches use more registers: fewer resident waves */
-    const uint32_t cap = batch >= 3u ? kResidentWaves / 2u : kResidentWaves;
-    uint32_t w = groups < cap ? groups : cap;
-    w = (w + (kThreads / 64u) - 1u) / (kThreads / 64u) * (kThreads / 64u);
-    return w < (kThreads / 64u) ? (kThreads / 64u) : w;
+/* workgroups of `kernel` that fit on the device at once */
+template <class K>
+uint32_t resident_blocks(K kernel) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    return (uint32_t)(per_cu * cus);
 }
 
+/* Launches one matvec, or (waves != nullptr) only reports the number of
+ * waves it would launch: one group per wave for RT = 2; for RT = 4 as many
+ * workgroups as are resident at once, striding over the groups. */
 template <uint32_t TYPE, uint32_t COLS, int B>
 hipError_t launch_one(const uint8_t *W, uint32_t rows, const float *x, float *y, uint32_t *st,
-                      float *pv, uint32_t *pi, hipStream_t s) {
-    const uint8_t *end = nullptr;
-    const uint32_t blocks = waves_for(rows, COLS, B) / (kThreads / 64u);
-    if (pick_rt(rows, COLS) == 4u)
+                      float *pv, uint32_t *pi, uint32_t ps, hipStream_t s, uint32_t *waves) {
+    constexpr uint32_t kWavesPerBlock = kThreads / 64u;
+    const uint32_t rt = pick_rt(rows, COLS);
+    const uint32_t groups = (rows + group_rows(COLS, rt) - 1u) / group_rows(COLS, rt);
+    uint32_t blocks = (groups + kWavesPerBlock - 1u) / kWavesPerBlock;
+    if (rt == 4u) {
+        static const uint32_t resident = resident_blocks(matvec_kernel<TYPE, COLS, B, 4>);
+        if (blocks > resident) blocks = resident;
+    }
+    if (blocks < 1u) blocks = 1u;
+    if (waves != nullptr) {
+        *waves = blocks * kWavesPerBlock;
+        return hipSuccess;
+    }
+    if (rt == 4u)
         hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 4>), dim3(blocks), dim3(kThreads), 0, s,
-                           W, rows, x, y, st, pv, pi, end);
+                           W, rows, x, y, st, pv, pi, ps);
     else
-        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 1>), dim3(blocks), dim3(kThreads), 0, s,
-                           W, rows, x, y, st, pv, pi, end);
+        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 2>), dim3(blocks), dim3(kThreads), 0, s,
+                           W, rows, x, y, st, pv, pi, ps);
     return hipGetLastError();
 }
 
 template <uint32_t TYPE, int B>
 hipError_t launch_cols(uint32_t cols, const uint8_t *W, uint32_t rows, const float *x, float *y,
-                       uint32_t *st, float *pv, uint32_t *pi, hipStream_t s) {
+                       uint32_t *st, float *pv, uint32_t *pi, uint32_t ps, hipStream_t s,
+                       uint32_t *wv) {
     switch (cols) {
     case 32:
     case 64:
     case 128:
         /* short rows exist only for 32-element Q8_0 blocks */
         if (TYPE != KQ_LAUNCH_Q8_0) break;
-        if (cols == 32) return launch_one<KQ_LAUNCH_Q8_0, 32u, B>(W, rows, x, y, st, pv, pi, s);
-        if (cols == 64) return launch_one<KQ_LAUNCH_Q8_0, 64u, B>(W, rows, x, y, st, pv, pi, s);
-        return launch_one<KQ_LAUNCH_Q8_0, 128u, B>(W, rows, x, y, st, pv, pi, s);
-    case 256: return launch_one<TYPE, 256u, B>(W, rows, x, y, st, pv, pi, s);
-    case 512: return launch_one<TYPE, 512u, B>(W, rows, x, y, st, pv, pi, s);
-    case 1024: return launch_one<TYPE, 1024u, B>(W, rows, x, y, st, pv, pi, s);
-    case 2048: return launch_one<TYPE, 2048u, B>(W, rows, x, y, st, pv, pi, s);
+        if (cols == 32) return launch_one<KQ_LAUNCH_Q8_0, 32u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+        if (cols == 64) return launch_one<KQ_LAUNCH_Q8_0, 64u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_one<KQ_LAUNCH_Q8_0, 128u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+    case 256: return launch_one<TYPE, 256u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+    case 512: return launch_one<TYPE, 512u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+    case 1024: return launch_one<TYPE, 1024u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+    case 2048: return launch_one<TYPE, 2048u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
     default: break;
     }
     return hipErrorInvalidValue;
@@ -232,11 +271,27 @@ hipError_t launch_cols(uint32_t cols, const uint8_t *W, uint32_t rows, const flo
 template <int B>
 hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t rows,
                     const float *x, float *y, uint32_t *st, float *pv, uint32_t *pi,
-                    hipStream_t s) {
+                    uint32_t ps, hipStream_t s, uint32_t *wv) {
     switch (type) {
-    case KQ_LAUNCH_Q4_K: return launch_cols<KQ_LAUNCH_Q4_K, B>(cols, W, rows, x, y, st, pv, pi, s);
-    case KQ_LAUNCH_Q6_K: return launch_cols<KQ_LAUNCH_Q6_K, B>(cols, W, rows, x, y, st, pv, pi, s);
-    case KQ_LAUNCH_Q8_0: return launch_cols<KQ_LAUNCH_Q8_0, B>(cols, W, rows, x, y, st, pv, pi, s);
+    case KQ_LAUNCH_Q4_K:
+        return launch_cols<KQ_LAUNCH_Q4_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+    case KQ_LAUNCH_Q6_K:
+        return launch_cols<KQ_LAUNCH_Q6_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+    case KQ_LAUNCH_Q8_0:
+        return launch_cols<KQ_LAUNCH_Q8_0, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t dispatch(uint32_t type, const void *W, uint32_t rows, uint32_t cols, const float *x,
+                    uint32_t batch, float *y, uint32_t *status, float *pv, uint32_t *pi,
+                    uint32_t ps, hipStream_t stream, uint32_t *wv) {
+    const uint8_t *w = (const uint8_t *)W;
+    switch (batch) {
+    case 1: return launch_b<1>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
+    case 2: return launch_b<2>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
+    case 3: return launch_b<3>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
+    case 4: return launch_b<4>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
     default: return hipErrorInvalidValue;
     }
 }
@@ -252,22 +307,19 @@ extern "C" int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t
 
 extern "C" uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols,
                                            uint32_t batch) {
-    (void)type;
-    return waves_for(rows, cols, batch);
+    uint32_t waves = 0u;
+    if (dispatch(type, nullptr, rows, cols, nullptr, batch, nullptr, nullptr, nullptr, nullptr,
+                 0u, nullptr, &waves) != hipSuccess)
+        return 0u;
+    return waves;
 }
 
 extern "C" hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows,
                                        uint32_t cols, const float *x, uint32_t batch, float *y,
                                        uint32_t *status, float *part_v, uint32_t *part_i,
-                                       hipStream_t stream) {
-    const uint8_t *w = (const uint8_t *)W;
-    switch (batch) {
-    case 1: return launch_b<1>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
-    case 2: return launch_b<2>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
-    case 3: return launch_b<3>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
-    case 4: return launch_b<4>(type, cols, w, rows, x, y, status, part_v, part_i, stream);
-    default: return hipErrorInvalidValue;
-    }
+                                       uint32_t part_stride, hipStream_t stream) {
+    return dispatch(type, W, rows, cols, x, batch, y, status, part_v, part_i, part_stride, stream,
+                    nullptr);
 }
 
 extern "C" uint32_t kq_launch_argmax_parts(uint32_t count) {

@@ -379,9 +379,14 @@ static kq_status validate_matvec(const kq_hip_context *c, uint32_t type_id, cons
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "rows must fit 32 bits and batch be <= 8");
     if (!kq_launch_matvec_supported(type_id, (uint32_t)cols, 1u))
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
-                       "device matvec supports 256, 512, 1024 or 2048 columns");
+                       "device matvec supports 256, 512, 1024 or 2048 columns "
+                       "(Q8_0 also 32, 64, 128)");
     if (!u64_mul(rows, cols / be * bb, &w_bytes) || !u64_mul(rows, batch, &need))
         return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "matrix byte count overflows");
+    /* the kernels address the matrix through one buffer descriptor, whose
+     * byte count is 32-bit */
+    if (w_bytes > UINT32_MAX)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "a matrix must be smaller than 4 GiB");
     if (capacity < need)
         return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "output capacity is too small");
     if (ranges_overlap(w, w_bytes, y, need * 4u) ||
@@ -403,7 +408,8 @@ static hipError_t enqueue_matvec(kq_hip_context *c, uint32_t type_id, const void
         hipError_t e = kq_launch_matvec(type_id, w, (uint32_t)rows, (uint32_t)cols,
                                         x + (size_t)done * cols, nb, y + (size_t)done * rows,
                                         c->d_status, pv ? pv + (size_t)done * nparts : NULL,
-                                        pi ? pi + (size_t)done * nparts : NULL, c->stream);
+                                        pi ? pi + (size_t)done * nparts : NULL, nparts,
+                                        c->stream);
         if (e != hipSuccess) return e;
         done += nb;
     }
@@ -483,8 +489,15 @@ kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const v
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "logits and ids overlap");
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
-    nparts = kq_launch_matvec_waves(type_id, (uint32_t)vocab, (uint32_t)cols,
-                                    batch > 4u ? 4u : batch);
+    /* partials per batch column: the most any launch of the call uses */
+    nparts = 0u;
+    for (uint32_t done = 0u; done < batch; done += 4u) {
+        const uint32_t nb = batch - done > 4u ? 4u : batch - done;
+        const uint32_t w_nb = kq_launch_matvec_waves(type_id, (uint32_t)vocab, (uint32_t)cols, nb);
+        if (w_nb > nparts) nparts = w_nb;
+    }
+    if (nparts == 0u)
+        return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "lm head: no launch configuration");
     st = ensure_parts(c, (uint64_t)nparts * batch, diag);
     if (st != KQ_STATUS_OK) return st;
     e = enqueue_matvec(c, type_id, w, vocab, cols, h, batch, logits, c->part_v, c->part_i, nparts);

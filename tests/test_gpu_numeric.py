@@ -247,3 +247,22 @@ def test_lm_head_q6k_151936x2048(ctx, batch):
         top2 = np.sort(ref[b])[-2:]
         if top2[1] - top2[0] > ATOL + RTOL * abs(top2[1]):
             assert ids[b] == kq_oracle.argmax(ref[b])
+
+
+@pytest.mark.parametrize("batch", [5, 6, 8])
+def test_lm_head_batch_spans_launches(ctx, batch):
+    # batches over 4 run as several launches whose wave counts differ; the
+    # argmax partials of every batch row must still merge to the first max
+    V, H = 40000, 2048
+    say(f"lm head {V}x{H} batch {batch}")
+    w = S.quant_matrix("Q6_K", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT, 7), V, H)
+    h = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, 70 + batch), batch * H).reshape(batch, H)
+    dw, dh = ctx.upload(w), ctx.upload(h)
+    dl, di = ctx.alloc(V * batch * 4), ctx.alloc(batch * 4)
+    ctx.lm_head(kq_hip.TYPE_Q6_K, dw, V, H, dh, batch, dl, di)
+    logits = ctx.download(dl, np.float32, V * batch).reshape(batch, V)
+    ids = ctx.download(di, np.uint32, batch)
+    ref = kq_oracle.matvec(kq_oracle.Q6_K, w, V, H, h, threads=oracle_threads())
+    assert_close(logits, ref)
+    for b in range(batch):
+        assert ids[b] == int(np.argmax(logits[b]))
