@@ -236,6 +236,27 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *context,
                                        uint64_t scratch_bytes,
                                        kq_diagnostic *diagnostic);
 
+/* The token->expert permutation that the multi-token execution runs its
+ * grouped expert GEMMs over: the (token, slot) pairs of selected_ids
+ * [tokens][top_k] (from kq_hip_moe_route_f32) stably sorted by expert id,
+ * tokens ascending within an expert. expert_offsets [experts + 1] holds
+ * each expert's first position; pair_token / pair_slot [tokens * top_k] the
+ * pair at each position. device_scratch needs tokens * top_k * 4 bytes.
+ * No entry point of the reference corresponds: it runs the tokens one by
+ * one (kq_moe_execute_common, src/kq_moe_qwen38.c:666-865); this exposes
+ * the permutation so callers can check it. An id >= expert_count fails
+ * with KQ_STATUS_INVALID_ARGUMENT. */
+kq_status kq_hip_moe_token_permutation(kq_hip_context *context,
+                                       const kq_hip_moe_config *config,
+                                       const uint32_t *device_selected_ids,
+                                       uint64_t token_count,
+                                       uint32_t *device_expert_offsets,
+                                       uint32_t *device_pair_token,
+                                       uint32_t *device_pair_slot,
+                                       void *device_scratch,
+                                       uint64_t scratch_bytes,
+                                       kq_diagnostic *diagnostic);
+
 /* ------------------------------------------------------------------ */
 /* Elementwise binary32 expf with the bits of the libm expf the reference
  * calls (src/kq_numeric.c:628-638, :776-813). No reference entry point of

@@ -17,6 +17,7 @@
 #define KQ_DEV_NUMERIC 2u    /* non-finite result -> NUMERIC_DOMAIN */
 #define KQ_DEV_INPUT 4u      /* non-finite input (checked first by the
                                 reference) -> NUMERIC_DOMAIN */
+#define KQ_DEV_RANGE 8u      /* an index input out of range -> INVALID_ARGUMENT */
 
 #define KQ_WAVE 64
 

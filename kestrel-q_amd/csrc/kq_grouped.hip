@@ -1,0 +1,757 @@
+/*
+ * kq_grouped.hip — the multi-token (prefill) MoE layer as grouped expert
+ * GEMMs on MFMA: a stable token->expert permutation, one gate/up + SwiGLU
+ * pass and one down pass per expert over all of its tokens, and the ordered
+ * combine with the sigmoid-gated shared expert.
+ *
+ * The reference runs the layer token by token (kq_moe_execute_common,
+ * src/kq_moe_qwen38.c:666-865): for each token, route, then for every
+ * selected expert in ascending id g = Wg x, u = Wu x, a = swiglu(g, u),
+ * o = Wd a, routed_sum += o * w (:722-765), and out = routed_sum +
+ * sigmoid(wsg . x) * shared(x) (:771-828). With T tokens every expert's
+ * weights would stream once per token that selects it. Here each expert's
+ * weights stream once for all of its tokens:
+ *
+ *   permute  offsets[e], and the (token, slot) pairs of expert e at
+ *            positions offsets[e].. in ascending token order (a stable
+ *            counting sort; bit-exact by construction)
+ *   gate/up  act[pos] = swiglu(Wg_e x_t, Wu_e x_t) for every position of e
+ *   down     o[pos] = Wd_e act[pos]
+ *   combine  out[t] = sum over t's slots in ascending expert id of
+ *            o[pos] * w, then + sigmoid(shared logit) * o_shared[t]
+ *
+ * GEMM numerics. Weight codes are small integers, exact in fp16, so the
+ * quantized weights enter the MFMA exactly:
+ *   Q4_K  the 6-bit sub-block scale s is folded into the code (s * q <=
+ *         945, exact) with one packed fp16 FMA that also removes the
+ *         1024 exponent bias of the byte->fp16 conversion; the super-block
+ *         scale d multiplies the fp32 accumulator once per 256 columns and
+ *         the dmin * m term is a second small MFMA against per-sub-block
+ *         activation sums;
+ *   Q6_K  the code q - 32 is exact; each 16-column sub-block is one
+ *         16x16x16 MFMA step whose fp32 result is scaled by d * sc.
+ * Activations are split per token into fp16 hi + lo (x = hi + lo to ~22
+ * bits) after an exact power-of-two scaling that puts the row's largest
+ * magnitude in [2^14, 2^15), so neither part overflows and small rows keep
+ * their precision; every MFMA accumulates in fp32. Outputs are compared
+ * with the CPU by tolerance (1e-3 relative to the row RMS, 1e-4 absolute).
+ *
+ * MFMA operands: A = activations (16 tokens x K), B = weights (K x 16
+ * rows); lane l holds token / row l % 16 and a k-group l / 16, and the
+ * result D[token][row] leaves lane l with row l % 16 of tokens
+ * 4 (l / 16) .. + 3. Which hidden columns a k-slot of a step holds is free
+ * as long as A and B agree; it is chosen per format so that each lane's
+ * weight bytes are contiguous and share one scale.
+ */
+#include "kq_launch.h"
+#include "kq_device.h"
+
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kTile = 16;          /* tokens per M-chunk, rows per N-tile */
+constexpr uint32_t kMagic = 0x64646464u; /* fp16 0x64XX = 1024 + XX */
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+/* bytes b0, b1 (sel 0x04010400) or b2, b3 (sel 0x04030402) of m as fp16
+ * 1024 + byte */
+__device__ __forceinline__ h2 bytes_lo(uint32_t m) {
+    return as_h2(__builtin_amdgcn_perm(kMagic, m, 0x04010400u));
+}
+__device__ __forceinline__ h2 bytes_hi(uint32_t m) {
+    return as_h2(__builtin_amdgcn_perm(kMagic, m, 0x04030402u));
+}
+
+__device__ __forceinline__ h2 fma2(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
+
+__device__ __forceinline__ float f16f(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
+}
+
+__device__ __forceinline__ float wave_max_abs(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, KQ_WAVE));
+    return v;
+}
+
+/* ------------------------------------------------------------------ */
+/* formats */
+
+template <uint32_t FMT>
+struct Fmt;
+
+/* Q4_K: 144 B per 256 columns (d, dmin, 12 B of 6-bit scales/mins, 128 B
+ * of nibbles; src/kq_numeric.c:223-277). Lane k-group g reads nibble group
+ * g (qs bytes 32g..32g+31: sub-blocks 2g in the low nibbles, 2g+1 in the
+ * high) of its row; step s (0..7) of a block covers hidden columns
+ * 64g + 8s .. +7, low nibbles for s < 4, high nibbles for s >= 4. */
+template <>
+struct Fmt<KQ_LAUNCH_Q4_K> {
+    static constexpr uint32_t kBytes = 144u;
+    static constexpr bool kK32 = true; /* 16x16x32 steps, b128 activation reads */
+    struct Raw {
+        uint4 hd, qa, qb;
+    };
+    __device__ static __forceinline__ Raw load(KqBuf w, uint32_t boff, uint32_t g) {
+        Raw r;
+        r.hd = kq_ld128(w, boff, 0u);
+        r.qa = kq_ld128(w, boff + 16u + 32u * g, 0u);
+        r.qb = kq_ld128(w, boff + 32u + 32u * g, 0u);
+        return r;
+    }
+};
+
+/* Q6_K: 210 B per 256 columns (ql[128], qh[64], int8 sc[16], f16 d; GGML
+ * layout). Sub-block s = 8n + 2q + h (half n, quarter q, 16-column half
+ * h) is one 16x16x16 step; lane k-group g holds its columns 4g .. 4g+3,
+ * i.e. hidden 128n + 32q + 16h + 4g .. +3, whose codes come from the ql
+ * dwords at 64n + 16h + 4g (q = 0, 2) and 64n + 32 + 16h + 4g (q = 1, 3)
+ * and the qh dword at 128 + 32n + 16h + 4g. A block at an offset of 2 mod
+ * 4 is read through aligned windows re-aligned with a byte funnel shift;
+ * no window leaves the block. */
+template <>
+struct Fmt<KQ_LAUNCH_Q6_K> {
+    static constexpr uint32_t kBytes = 210u;
+    static constexpr bool kK32 = false;
+    struct Raw {
+        kq_u32x2 w[4][3]; /* [n * 2 + h][ql A, ql B, qh] */
+        uint4 sc;         /* window over sc[16] */
+        uint32_t sc_tail, d, sh;
+    };
+    __device__ static __forceinline__ Raw load(KqBuf w, uint32_t boff, uint32_t g) {
+        Raw r;
+        r.sh = boff & 3u;
+        const uint32_t base = boff - r.sh;
+#pragma unroll
+        for (uint32_t nh = 0; nh < 4u; ++nh) {
+            const uint32_t n = nh >> 1, h = nh & 1u;
+            const uint32_t oa = 64u * n + 16u * h + 4u * g;
+            r.w[nh][0] = kq_ld64(w, base + oa, 0u);
+            r.w[nh][1] = kq_ld64(w, base + oa + 32u, 0u);
+            r.w[nh][2] = kq_ld64(w, base + 128u + 32u * n + 16u * h + 4u * g, 0u);
+        }
+        /* sc[16] at 192: [192, 208) when aligned, else [190, 210) */
+        r.sc = kq_ld128(w, base + 192u, 0u);
+        r.sc_tail = r.sh ? kq_ld32(w, base + 208u, 0u) : 0u;
+        r.d = kq_ld16(w, boff + 208u, 0u);
+        return r;
+    }
+};
+
+/* ------------------------------------------------------------------ */
+/* LDS image of one M-chunk of activations */
+
+template <uint32_t FMT, uint32_t KDIM>
+struct Stage {
+    /* row pitch in fp16: b128 reads (K32 steps) want a 16-byte skew per
+     * row, b64 reads an 8-byte one, so that 8 / 16 lanes on consecutive
+     * rows hit distinct banks */
+    static constexpr uint32_t kPitch = KDIM + (Fmt<FMT>::kK32 ? 8u : 4u);
+    static constexpr uint32_t kSub = KDIM / 32u; /* Q4_K sub-blocks per row */
+    static constexpr uint32_t kSxPitch = kSub + 8u;
+    static constexpr bool kSums = FMT == KQ_LAUNCH_Q4_K;
+    __align__(16) _Float16 xh[kTile * kPitch];
+    __align__(16) _Float16 xl[kTile * kPitch];
+    __align__(16) _Float16 sxh[kSums ? kTile * kSxPitch : 4];
+    __align__(16) _Float16 sxl[kSums ? kTile * kSxPitch : 4];
+    int sig[kTile];
+};
+
+/* Stage rows src_row[i] (or zeros where negative) of X [*, KDIM]: scale by
+ * 2^sig (largest magnitude into [2^14, 2^15)), split into fp16 hi + lo and,
+ * for Q4_K, form the 32-column sums of the scaled row times 2^-5 (so they
+ * fit fp16), also split. One wave per row; each lane holds KDIM/64
+ * consecutive columns. Returns true if a non-finite input was seen. */
+template <uint32_t FMT, uint32_t KDIM>
+__device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
+                           const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
+    using S = Stage<FMT, KDIM>;
+    constexpr uint32_t EPL = KDIM / 64u; /* 4 .. 32 */
+    constexpr uint32_t NQ = EPL / 4u;
+    bool bad = false;
+    for (uint32_t i = wave; i < kTile; i += nwaves) {
+        const int src = src_row[i];
+        const float4 *p = (const float4 *)(X + (size_t)(src < 0 ? 0 : src) * KDIM) + lane * NQ;
+        float4 v[NQ];
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; ++q) v[q] = src < 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : p[q];
+        float m = 0.0f;
+        bool nf = false;
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; ++q) {
+            nf |= !kq_isfinite(v[q].x) || !kq_isfinite(v[q].y) || !kq_isfinite(v[q].z) ||
+                  !kq_isfinite(v[q].w);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)),
+                               fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
+        }
+        bad |= nf;
+        m = wave_max_abs(m);
+        const bool any_nf = __ballot(nf) != 0ull;
+        /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) lies in [2^14, 2^15) */
+        int sig = 0;
+        if (!any_nf && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
+        float part = 0.0f;
+        _Float16 *dh = st.xh + i * S::kPitch + lane * EPL;
+        _Float16 *dl = st.xl + i * S::kPitch + lane * EPL;
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; ++q) {
+            const float a[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float xs = any_nf ? 0.0f : ldexpf(a[c], sig);
+                hi[c] = (_Float16)xs;
+                lo[c] = (_Float16)(xs - (float)hi[c]);
+                part += xs;
+            }
+            *(h4 *)(dh + 4u * q) = h4{hi[0], hi[1], hi[2], hi[3]};
+            *(h4 *)(dl + 4u * q) = h4{lo[0], lo[1], lo[2], lo[3]};
+        }
+        if constexpr (S::kSums) {
+            /* 32-column sums: EPL columns per lane, 32 / EPL lanes per sum */
+            constexpr uint32_t LPS = EPL >= 32u ? 1u : 32u / EPL;
+#pragma unroll
+            for (uint32_t o = 1; o < LPS; o <<= 1) part += __shfl_xor(part, (int)o, KQ_WAVE);
+            if (lane % LPS == 0u) {
+                const float s = part * 0.03125f;
+                const _Float16 sh = (_Float16)s;
+                const _Float16 sl = (_Float16)(s - (float)sh);
+                const uint32_t j = lane * EPL / 32u;
+                st.sxh[i * S::kSxPitch + j] = sh;
+                st.sxl[i * S::kSxPitch + j] = sl;
+            }
+        }
+        if (lane == 0u) st.sig[i] = sig;
+    }
+    return bad;
+}
+
+/* ------------------------------------------------------------------ */
+/* one 16-row N-tile of NMAT matrices (gate and up share the activation
+ * fragments of every step) against the staged 16-token chunk; acc[m] gets
+ * block b of matrix m */
+
+template <uint32_t FMT, uint32_t KDIM, int NMAT>
+struct Tile;
+
+template <uint32_t KDIM, int NMAT>
+struct Tile<KQ_LAUNCH_Q4_K, KDIM, NMAT> {
+    using F = Fmt<KQ_LAUNCH_Q4_K>;
+    using S = Stage<KQ_LAUNCH_Q4_K, KDIM>;
+    using Raw = F::Raw;
+
+    __device__ static __forceinline__ void block(const Raw (&r)[NMAT], const S &st, uint32_t b,
+                                                 uint32_t i, uint32_t g, f4 (&acc)[NMAT],
+                                                 bool &malformed) {
+        float d[NMAT], dm[NMAT];
+        h2 S0[NMAT], C0[NMAT], S1[NMAT], C1[NMAT];
+        h4 bm[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            d[m] = f16f(r[m].hd.x);
+            const float dmin = f16f(r[m].hd.x >> 16);
+            malformed |= !kq_isfinite(d[m]) || !kq_isfinite(dmin);
+            dm[m] = dmin * 32.0f; /* the activation sums carry 2^-5 */
+            /* scales of sub-blocks 2g and 2g+1 (src/kq_numeric.c:161-174) */
+            const uint32_t u = r[m].hd.y >> (16u * (g & 1u)); /* q[2(g&1)], q[2(g&1)+1] */
+            const uint32_t w = r[m].hd.w >> (16u * (g & 1u)); /* q[8+2(g&1)], q[9+2(g&1)] */
+            uint32_t s0, s1;
+            if (g < 2u) {
+                s0 = u & 63u;
+                s1 = (u >> 8) & 63u;
+            } else {
+                s0 = (w & 15u) | ((u >> 2) & 0x30u);
+                s1 = ((w >> 8) & 15u) | ((u >> 10) & 0x30u);
+            }
+            const _Float16 fs0 = (_Float16)(float)s0, fs1 = (_Float16)(float)s1;
+            S0[m] = h2{fs0, fs0};
+            C0[m] = S0[m] * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+            S1[m] = h2{fs1, fs1} * h2{(_Float16)0.0625f, (_Float16)0.0625f};
+            C1[m] = h2{fs1, fs1} * h2{(_Float16)-64.0f, (_Float16)-64.0f};
+            /* mins m_4g .. m_4g+3 for g < 2 (the min-term weights); 0 for g >= 2 */
+            const uint32_t mq =
+                g == 0u ? (r[m].hd.z & 0x3f3f3f3fu)
+                        : (((r[m].hd.w >> 4) & 0x0f0f0f0fu) | ((r[m].hd.z >> 2) & 0x30303030u));
+            const h2 one = h2{(_Float16)1.0f, (_Float16)1.0f};
+            const h2 neg = h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+            h2 mlo = fma2(bytes_lo(mq), one, neg), mhi = fma2(bytes_hi(mq), one, neg);
+            if (g >= 2u) {
+                mlo = h2{(_Float16)0.0f, (_Float16)0.0f};
+                mhi = mlo;
+            }
+            bm[m] = h4{mlo.x, mlo.y, mhi.x, mhi.y};
+        }
+        f4 q[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) q[m] = f4{0.f, 0.f, 0.f, 0.f};
+        const _Float16 *xh = st.xh + i * S::kPitch + 256u * b + 64u * g;
+        const _Float16 *xl = st.xl + i * S::kPitch + 256u * b + 64u * g;
+#pragma unroll
+        for (uint32_t s = 0; s < 8u; ++s) {
+            const h8 ah = *(const h8 *)(xh + 8u * s);
+            const h8 al = *(const h8 *)(xl + 8u * s);
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                const uint4 &qd = (s & 2u) ? r[m].qb : r[m].qa;
+                const uint32_t raw0 = (s & 1u) ? qd.z : qd.x, raw1 = (s & 1u) ? qd.w : qd.y;
+                const uint32_t m0 = s < 4u ? kq_and_0f(raw0) : kq_and_f0(raw0);
+                const uint32_t m1 = s < 4u ? kq_and_0f(raw1) : kq_and_f0(raw1);
+                const h2 Sc = s < 4u ? S0[m] : S1[m], Cc = s < 4u ? C0[m] : C1[m];
+                const h2 w0 = fma2(bytes_lo(m0), Sc, Cc), w1 = fma2(bytes_hi(m0), Sc, Cc);
+                const h2 w2 = fma2(bytes_lo(m1), Sc, Cc), w3 = fma2(bytes_hi(m1), Sc, Cc);
+                const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+                q[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, q[m], 0, 0, 0);
+                q[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, q[m], 0, 0, 0);
+            }
+            /* keep each step's fragments short-lived: without this the
+             * scheduler hoists every step's LDS reads and runs out of VGPRs */
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        /* min term: sum_j m_j * (32-column sums * 2^-5) */
+        const uint32_t so = i * S::kSxPitch + 8u * b + 4u * (g & 1u);
+        const h4 sh4 = *(const h4 *)(st.sxh + so);
+        const h4 sl4 = *(const h4 *)(st.sxl + so);
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            f4 mm = {0.f, 0.f, 0.f, 0.f};
+            mm = __builtin_amdgcn_mfma_f32_16x16x16f16(sh4, bm[m], mm, 0, 0, 0);
+            mm = __builtin_amdgcn_mfma_f32_16x16x16f16(sl4, bm[m], mm, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[m][t] = fmaf(d[m], q[m][t], fmaf(-dm[m], mm[t], acc[m][t]));
+        }
+    }
+};
+
+template <uint32_t KDIM, int NMAT>
+struct Tile<KQ_LAUNCH_Q6_K, KDIM, NMAT> {
+    using F = Fmt<KQ_LAUNCH_Q6_K>;
+    using S = Stage<KQ_LAUNCH_Q6_K, KDIM>;
+    using Raw = F::Raw;
+
+    __device__ static __forceinline__ void block(const Raw (&r)[NMAT], const S &st, uint32_t b,
+                                                 uint32_t i, uint32_t g, f4 (&acc)[NMAT],
+                                                 bool &malformed) {
+        float d[NMAT];
+        uint32_t sc[NMAT][4];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            d[m] = f16f(r[m].d);
+            malformed |= !kq_isfinite(d[m]);
+            const uint32_t sh = r[m].sh ? 2u : 0u;
+            sc[m][0] = kq_align2(r[m].sc.y, r[m].sc.x, sh);
+            sc[m][1] = kq_align2(r[m].sc.z, r[m].sc.y, sh);
+            sc[m][2] = kq_align2(r[m].sc.w, r[m].sc.z, sh);
+            sc[m][3] = kq_align2(r[m].sc_tail, r[m].sc.w, sh);
+            if (!r[m].sh) {
+                sc[m][0] = r[m].sc.x;
+                sc[m][1] = r[m].sc.y;
+                sc[m][2] = r[m].sc.z;
+                sc[m][3] = r[m].sc.w;
+            }
+        }
+        const h2 bias = h2{(_Float16)-1056.0f, (_Float16)-1056.0f}; /* 1024 + 32 */
+        const _Float16 *xh = st.xh + i * S::kPitch + 256u * b + 4u * g;
+        const _Float16 *xl = st.xl + i * S::kPitch + 256u * b + 4u * g;
+#pragma unroll
+        for (uint32_t nh = 0; nh < 4u; ++nh) {
+            const uint32_t n = nh >> 1, h = nh & 1u;
+            uint32_t c[NMAT][4];
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                const uint32_t A = kq_align2(r[m].w[nh][0].y, r[m].w[nh][0].x, r[m].sh);
+                const uint32_t B = kq_align2(r[m].w[nh][1].y, r[m].w[nh][1].x, r[m].sh);
+                const uint32_t H = kq_align2(r[m].w[nh][2].y, r[m].w[nh][2].x, r[m].sh);
+                c[m][0] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+                c[m][1] = (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+                c[m][2] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+                c[m][3] = ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t s = 8u * n + 2u * q + h;
+                const uint32_t ko = 128u * n + 32u * q + 16u * h;
+                const h4 ah = *(const h4 *)(xh + ko);
+                const h4 al = *(const h4 *)(xl + ko);
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    const h2 w0 = bytes_lo(c[m][q]) + bias, w1 = bytes_hi(c[m][q]) + bias;
+                    const h4 bw = h4{w0.x, w0.y, w1.x, w1.y};
+                    f4 t = {0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bw, t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bw, t, 0, 0, 0);
+                    const int8_t scv = (int8_t)((sc[m][s >> 2] >> (8u * (s & 3u))) & 0xffu);
+                    const float ds = d[m] * (float)scv;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc[m][k] = fmaf(ds, t[k], acc[m][k]);
+                }
+            }
+        }
+    }
+};
+
+/* ------------------------------------------------------------------ */
+/* grouped expert pass */
+
+/* Who a workgroup serves: a routed expert (its tokens at positions
+ * offsets[e] .. offsets[e+1]) or a range of 16-token chunks of the shared
+ * expert (every token, positions T*K + t). */
+struct Work {
+    uint32_t first;  /* first position (routed) or first token (shared) */
+    uint32_t count;  /* tokens */
+    bool shared;
+};
+
+__device__ __forceinline__ Work work_of(uint32_t y, const uint32_t *offsets, uint32_t experts,
+                                        uint32_t tokens, uint32_t shared_chunks) {
+    Work w;
+    if (y < experts) {
+        w.first = offsets[y];
+        w.count = offsets[y + 1u] - w.first;
+        w.shared = false;
+    } else {
+        const uint32_t t0 = (y - experts) * shared_chunks * kTile;
+        w.first = t0;
+        w.count = t0 < tokens ? min(tokens - t0, shared_chunks * kTile) : 0u;
+        w.shared = true;
+    }
+    return w;
+}
+
+/*
+ * NMAT = 2: gate and up (rows = routed/shared intermediate, KDIM = hidden),
+ *   input rows are the hidden states of the tokens, output act[pos][row] =
+ *   swiglu(g, u).
+ * NMAT = 1: down (rows = hidden, KDIM = intermediate), input rows are
+ *   act[pos], output o[pos][row].
+ * grid: x = slabs of NW * 16 rows, y = routed experts then shared chunks.
+ * Positions: routed pairs 0 .. T*K-1 (permuted order), shared token t at
+ * T*K + t.
+ */
+template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW>
+__global__ __launch_bounds__(NW * 64) void grouped_pass(
+    const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
+    const uint8_t *__restrict__ SW0, const uint8_t *__restrict__ SW1,
+    const float *__restrict__ X, const uint32_t *__restrict__ offsets,
+    const uint32_t *__restrict__ perm_tok, uint32_t experts, uint32_t tokens, uint32_t top_k,
+    uint32_t rows, uint32_t shared_chunks, float *__restrict__ out, uint32_t *status) {
+    using F = Fmt<GFMT>;
+    using S = Stage<GFMT, KDIM>;
+    using T = Tile<GFMT, KDIM, NMAT>;
+    using Raw = typename F::Raw;
+    constexpr uint32_t NB = KDIM / 256u;
+    constexpr uint32_t RB = NB * F::kBytes;
+    __shared__ S st;
+    __shared__ int src_row[kTile];
+
+    const Work wk = work_of(blockIdx.y, offsets, experts, tokens, shared_chunks);
+    if (wk.count == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t row0 = (blockIdx.x * NW + wave) * kTile;
+    const bool active = row0 < rows; /* idle waves still take part in staging */
+    const uint32_t row = row0 + j;
+    const uint32_t tk = tokens * top_k;
+    const uint32_t e = blockIdx.y;
+
+    KqBuf wb[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+        const uint8_t *base = wk.shared ? (m == 0 ? SW0 : SW1)
+                                        : (m == 0 ? W0 : W1) + (size_t)e * rows * RB;
+        wb[m] = kq_buf(base, active ? rows * RB : 0u);
+    }
+    const uint32_t roff = row * RB;
+    auto load = [&](Raw (&r)[NMAT], uint32_t b) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) r[m] = F::load(wb[m], roff + b * F::kBytes, g);
+    };
+
+    bool bad = false, badin = false, malformed = false;
+    for (uint32_t c0 = 0; c0 < wk.count; c0 += kTile) {
+        /* the first block's weights are requested before the staging */
+        Raw ra[NMAT], rb[NMAT];
+        if (active) load(ra, 0u);
+        __syncthreads(); /* the previous chunk's readers are done */
+        if (threadIdx.x < kTile) {
+            const uint32_t i = threadIdx.x;
+            int src = -1;
+            if (c0 + i < wk.count) {
+                const uint32_t p = wk.first + c0 + i;
+                if (NMAT == 2)
+                    src = (int)(wk.shared ? p : perm_tok[p]);
+                else
+                    src = (int)(wk.shared ? tk + p : p);
+            }
+            src_row[i] = src;
+        }
+        __syncthreads();
+        /* a non-finite hidden state is the caller's input; a non-finite
+         * intermediate activation is a numeric failure of the layer */
+        const bool nf = stage_rows<GFMT, KDIM>(st, X, src_row, wave, NW, lane);
+        if (NMAT == 2)
+            badin |= nf;
+        else
+            bad |= nf;
+        __syncthreads();
+        if (!active) continue;
+
+        /* ping-pong: the next block's weights are in flight while one block
+         * is decoded and multiplied */
+        f4 acc[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (uint32_t b = 0; b < NB; b += 2u) {
+            if (b + 1u < NB) load(rb, b + 1u);
+            T::block(ra, st, b, j, g, acc, malformed);
+            if (b + 1u >= NB) break;
+            if (b + 2u < NB) load(ra, b + 2u);
+            T::block(rb, st, b + 1u, j, g, acc, malformed);
+        }
+        /* D[token][row]: this lane holds row `row` of tokens 4g .. 4g+3 */
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const uint32_t i = 4u * g + t;
+            if (c0 + i >= wk.count) continue;
+            const int sg = st.sig[i];
+            const uint32_t pos = wk.shared ? tk + wk.first + c0 + i : wk.first + c0 + i;
+            float v;
+            if constexpr (NMAT == 2) {
+                const float gv = ldexpf(acc[0][t], -sg), uv = ldexpf(acc[1][t], -sg);
+                v = kq_swiglu(gv, uv);
+                bad |= !kq_isfinite(gv) || !kq_isfinite(uv);
+            } else {
+                v = ldexpf(acc[0][t], -sg);
+            }
+            bad |= !kq_isfinite(v);
+            out[(size_t)pos * rows + row] = v;
+        }
+    }
+    if (badin) kq_flag(status, KQ_DEV_INPUT);
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+}
+
+/* ------------------------------------------------------------------ */
+/* permutation: stable counting sort of (token, slot) pairs by expert id */
+
+constexpr uint32_t kPermChunk = 256; /* tokens per rank pass */
+
+__global__ __launch_bounds__(1024) void moe_permute(const uint32_t *__restrict__ ids,
+                                                    uint32_t tokens, uint32_t top_k,
+                                                    uint32_t experts, uint32_t *__restrict__ offsets,
+                                                    uint32_t *__restrict__ perm_tok,
+                                                    uint32_t *__restrict__ pos,
+                                                    uint32_t *__restrict__ pair_slot,
+                                                    uint32_t *status) {
+    __shared__ uint32_t cnt[1024];
+    __shared__ uint32_t base[1024];
+    __shared__ uint32_t bits[1024][kPermChunk / 32u];
+    __shared__ uint32_t wsum[16];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t pairs = tokens * top_k;
+    cnt[tid] = 0u;
+    __syncthreads();
+    bool bad = false;
+    for (uint32_t p = tid; p < pairs; p += 1024u) {
+        uint32_t e = ids[p];
+        if (e >= experts) {
+            bad = true;
+            e = 0u;
+        }
+        atomicAdd(&cnt[e], 1u);
+    }
+    __syncthreads();
+    /* exclusive scan of cnt[0 .. 1023] (entries past the experts are 0) */
+    {
+        const uint32_t v = cnt[tid];
+        uint32_t incl = v;
+#pragma unroll
+        for (uint32_t o = 1; o < 64u; o <<= 1) {
+            const uint32_t n = __shfl_up(incl, o, KQ_WAVE);
+            if (lane >= o) incl += n;
+        }
+        if (lane == 63u) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0u;
+        for (uint32_t w = 0; w < wave; ++w) before += wsum[w];
+        const uint32_t ex = before + incl - v;
+        base[tid] = ex;
+        if (tid < experts) offsets[tid] = ex;
+        if (tid == experts) offsets[tid] = ex; /* = pairs */
+    }
+    __syncthreads();
+    for (uint32_t t0 = 0; t0 < tokens; t0 += kPermChunk) {
+        const uint32_t nt = min(kPermChunk, tokens - t0);
+        for (uint32_t w = tid; w < 1024u * (kPermChunk / 32u); w += 1024u)
+            (&bits[0][0])[w] = 0u;
+        __syncthreads();
+        const uint32_t np = nt * top_k;
+        for (uint32_t p = tid; p < np; p += 1024u) {
+            const uint32_t lt = p / top_k;
+            uint32_t e = ids[(size_t)t0 * top_k + p];
+            e = e < experts ? e : 0u;
+            atomicOr(&bits[e][lt >> 5], 1u << (lt & 31u));
+        }
+        __syncthreads();
+        for (uint32_t p = tid; p < np; p += 1024u) {
+            const uint32_t lt = p / top_k;
+            uint32_t e = ids[(size_t)t0 * top_k + p];
+            e = e < experts ? e : 0u;
+            uint32_t r = __popc(bits[e][lt >> 5] & ((1u << (lt & 31u)) - 1u));
+            for (uint32_t w = 0; w < (lt >> 5); ++w) r += __popc(bits[e][w]);
+            const uint32_t q = base[e] + r;
+            pos[(size_t)t0 * top_k + p] = q;
+            perm_tok[q] = t0 + lt;
+            if (pair_slot != nullptr) pair_slot[q] = p - lt * top_k;
+        }
+        __syncthreads();
+        {
+            uint32_t c = 0u;
+#pragma unroll
+            for (uint32_t w = 0; w < kPermChunk / 32u; ++w) c += __popc(bits[tid][w]);
+            base[tid] += c;
+        }
+        __syncthreads();
+    }
+    if (bad) kq_flag(status, KQ_DEV_RANGE);
+}
+
+/* ------------------------------------------------------------------ */
+/* combine, in the reference's order (src/kq_moe_qwen38.c:722-765, :826) */
+
+__global__ __launch_bounds__(256) void moe_combine(
+    const float *__restrict__ o, const uint32_t *__restrict__ pos,
+    const uint32_t *__restrict__ order, const float *__restrict__ weights,
+    const float *__restrict__ shared_scale, uint32_t tokens, uint32_t top_k, uint32_t hidden,
+    float *__restrict__ out, uint32_t *status) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
+    if (n >= hidden) return;
+    const uint32_t tk = tokens * top_k;
+    bool bad = false;
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < top_k; ++j) {
+        const uint32_t s = order[(size_t)t * top_k + j];
+        const uint32_t p = pos[(size_t)t * top_k + s];
+        const float v = o[(size_t)p * hidden + n];
+        bad |= !kq_isfinite(v);
+        const float weighted = v * weights[(size_t)t * top_k + s];
+        sum = sum + weighted;
+    }
+    const float so = o[(size_t)(tk + t) * hidden + n];
+    const float gated = so * shared_scale[t];
+    const float v = sum + gated;
+    bad |= !kq_isfinite(so) || !kq_isfinite(sum) || !kq_isfinite(gated) || !kq_isfinite(v);
+    out[(size_t)t * hidden + n] = v;
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+}
+
+/* ------------------------------------------------------------------ */
+/* launchers */
+
+constexpr uint32_t kSharedChunks = 2; /* 16-token chunks per shared-expert workgroup */
+
+template <uint32_t GFMT, uint32_t KDIM, int NMAT>
+constexpr int waves_for() {
+    /* gate/up at 2048 columns keeps one 136 KiB chunk image per CU: 16 waves
+     * share it; narrower images leave room for more workgroups */
+    return NMAT == 2 ? (KDIM >= 1024u ? 16 : 8) : 8;
+}
+
+template <uint32_t GFMT, uint32_t KDIM, int NMAT>
+hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
+                       const uint8_t *SW1, const float *X, const uint32_t *offsets,
+                       const uint32_t *perm_tok, uint32_t experts, uint32_t tokens,
+                       uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
+                       hipStream_t s) {
+    constexpr int NW = waves_for<GFMT, KDIM, NMAT>();
+    const uint32_t slab = (uint32_t)NW * kTile;
+    const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
+    const dim3 grid((rows + slab - 1u) / slab, experts + sh_wgs);
+    hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW>), grid, dim3(NW * 64), 0, s, W0, W1,
+                       SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, rows,
+                       kSharedChunks, out, status);
+    return hipGetLastError();
+}
+
+template <uint32_t GFMT, int NMAT>
+hipError_t pass_cols(uint32_t kdim, const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
+                     const uint8_t *SW1, const float *X, const uint32_t *offsets,
+                     const uint32_t *perm_tok, uint32_t experts, uint32_t tokens, uint32_t top_k,
+                     uint32_t rows, float *out, uint32_t *status, hipStream_t s) {
+#define KQ_PASS(K)                                                                        \
+    launch_pass<GFMT, K, NMAT>(W0, W1, SW0, SW1, X, offsets, perm_tok, experts, tokens, \
+                               top_k, rows, out, status, s)
+    switch (kdim) {
+    case 256: return KQ_PASS(256u);
+    case 512: return KQ_PASS(512u);
+    case 1024: return KQ_PASS(1024u);
+    case 2048: return KQ_PASS(2048u);
+    default: return hipErrorInvalidValue;
+    }
+#undef KQ_PASS
+}
+
+bool down_type(uint32_t t) { return t == KQ_LAUNCH_Q4_K || t == KQ_LAUNCH_Q6_K; }
+
+bool grouped_dim(uint32_t n) { return n == 256u || n == 512u || n == 1024u || n == 2048u; }
+
+}  // namespace
+
+extern "C" int kq_launch_moe_grouped_supported(const kq_launch_moe_dims *d,
+                                               const kq_launch_moe_weights *w) {
+    /* gate/up in Q4_K (the 6-bit scales fold into exact fp16 weights); down
+     * in Q4_K or Q6_K */
+    return w->gate_type == KQ_LAUNCH_Q4_K && w->up_type == w->gate_type &&
+           w->shared_gate_type == w->gate_type && w->shared_up_type == w->gate_type &&
+           down_type(w->down_type) && w->shared_down_type == w->down_type &&
+           grouped_dim(d->hidden) && grouped_dim(d->inter) && d->inter == d->shared_inter &&
+           d->experts <= 1023u;
+}
+
+extern "C" hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens, uint32_t top_k,
+                                            uint32_t experts, uint32_t *offsets,
+                                            uint32_t *pair_token, uint32_t *pos,
+                                            uint32_t *pair_slot, uint32_t *status,
+                                            hipStream_t s) {
+    hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ids, tokens, top_k, experts,
+                       offsets, pair_token, pos, pair_slot, status);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
+                                            const kq_launch_moe_weights *w, const float *hidden,
+                                            uint32_t tokens, const kq_launch_moe_ws *ws,
+                                            float *out, uint32_t *status, hipStream_t s) {
+    hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ws->ids, tokens, d->top_k,
+                       d->experts, ws->offsets, ws->perm_tok, ws->pos, nullptr, status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint8_t *g = (const uint8_t *)w->gate, *u = (const uint8_t *)w->up;
+    const uint8_t *sg = (const uint8_t *)w->shared_gate, *su = (const uint8_t *)w->shared_up;
+    e = pass_cols<KQ_LAUNCH_Q4_K, 2>(d->hidden, g, u, sg, su, hidden, ws->offsets, ws->perm_tok,
+                                     d->experts, tokens, d->top_k, d->inter, ws->act, status, s);
+    if (e != hipSuccess) return e;
+    const uint8_t *dn = (const uint8_t *)w->down, *sd = (const uint8_t *)w->shared_down;
+    if (w->down_type == KQ_LAUNCH_Q4_K)
+        e = pass_cols<KQ_LAUNCH_Q4_K, 1>(d->inter, dn, nullptr, sd, nullptr, ws->act,
+                                         ws->offsets, ws->perm_tok, d->experts, tokens, d->top_k,
+                                         d->hidden, ws->outp, status, s);
+    else
+        e = pass_cols<KQ_LAUNCH_Q6_K, 1>(d->inter, dn, nullptr, sd, nullptr, ws->act,
+                                         ws->offsets, ws->perm_tok, d->experts, tokens, d->top_k,
+                                         d->hidden, ws->outp, status, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(moe_combine, dim3((d->hidden + 255u) / 256u, tokens), dim3(256), 0, s,
+                       ws->outp, ws->pos, ws->order, ws->weights, ws->shared_scale, tokens,
+                       d->top_k, d->hidden, out, status);
+    return hipGetLastError();
+}

@@ -84,7 +84,13 @@ typedef struct kq_launch_moe_ws {
     uint32_t *order;      /* [tokens][top_k]: slots sorted by ascending id */
     float *shared_logit;  /* [tokens] */
     float *shared_scale;  /* [tokens] */
-    float *act;           /* [tokens][top_k + 1][max(inter, shared_inter)] */
+    float *act;           /* [tokens][top_k + 1][max(inter, shared_inter)]; the grouped
+                             path uses it as [tokens * top_k + tokens][inter]: routed
+                             pairs in permuted order, then the shared expert's rows */
+    uint32_t *offsets;    /* [experts + 1]: first permuted position of each expert */
+    uint32_t *perm_tok;   /* [tokens * top_k]: token at each permuted position */
+    uint32_t *pos;        /* [tokens][top_k]: permuted position of each (token, slot) */
+    float *outp;          /* [tokens * top_k + tokens][hidden]: down outputs */
 } kq_launch_moe_ws;
 
 uint32_t kq_launch_moe_experts_padded(uint32_t experts);
@@ -97,6 +103,19 @@ hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
                                const float *shared_gate_weight, const float *hidden,
                                uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t *status,
                                hipStream_t stream);
+/* grouped multi-token path (kq_grouped.hip): stable permutation, per-expert
+ * MFMA gate/up + SwiGLU and down over all of an expert's tokens, ordered
+ * combine; needs the route results in ws */
+int kq_launch_moe_grouped_supported(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w);
+/* the permutation alone (pair_slot optional) */
+hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens, uint32_t top_k,
+                                 uint32_t experts, uint32_t *offsets, uint32_t *pair_token,
+                                 uint32_t *pos, uint32_t *pair_slot, uint32_t *status,
+                                 hipStream_t stream);
+hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
+                                 const float *hidden, uint32_t tokens,
+                                 const kq_launch_moe_ws *ws, float *out, uint32_t *status,
+                                 hipStream_t stream);
 hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                                  const float *hidden, uint32_t tokens,
                                  const kq_launch_moe_ws *ws, float *out, uint32_t *status,

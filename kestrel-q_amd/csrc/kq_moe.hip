@@ -781,12 +781,16 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * d->top_k * 4u) * 3u;           /* ids, weights, order */
     b += align256((uint64_t)tokens * 4u) * 2u;                      /* shared logit, scale */
     b += align256((uint64_t)tokens * (d->top_k + 1u) * ai * 4u);    /* act */
+    b += align256((uint64_t)(d->experts + 1u) * 4u);                 /* offsets */
+    b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
+    b += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u); /* outp */
     return b;
 }
 
 extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tokens, void *base,
                                        kq_launch_moe_ws *ws) {
     const uint64_t ep = pad64(d->experts + 1u);
+    const uint64_t ai = d->inter > d->shared_inter ? d->inter : d->shared_inter;
     uint8_t *p = (uint8_t *)base;
     ws->router_t = (float *)p; p += align256((uint64_t)d->hidden * ep * 4u);
     ws->logits = (float *)p; p += align256((uint64_t)tokens * d->experts * 4u);
@@ -796,7 +800,11 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->order = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->shared_logit = (float *)p; p += align256((uint64_t)tokens * 4u);
     ws->shared_scale = (float *)p; p += align256((uint64_t)tokens * 4u);
-    ws->act = (float *)p;
+    ws->act = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * ai * 4u);
+    ws->offsets = (uint32_t *)p; p += align256((uint64_t)(d->experts + 1u) * 4u);
+    ws->perm_tok = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
+    ws->pos = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
+    ws->outp = (float *)p;
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,

@@ -24,6 +24,7 @@
 #define KQ_DEV_MALFORMED 1u
 #define KQ_DEV_NUMERIC 2u
 #define KQ_DEV_INPUT 4u
+#define KQ_DEV_RANGE 8u
 
 struct kq_hip_context {
     int device;
@@ -58,6 +59,8 @@ static kq_status set_device(kq_hip_context *c, kq_diagnostic *diag) {
  * is reported first (the reference validates inputs before decoding), then a
  * malformed block scale, then a non-finite result. */
 static kq_status device_flags(uint32_t flags, kq_diagnostic *diag) {
+    if (flags & KQ_DEV_RANGE)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "an expert id is out of range");
     if (flags & KQ_DEV_INPUT)
         return kq_fail(diag, KQ_STATUS_NUMERIC_DOMAIN, "non-finite input on the device path");
     if (flags & KQ_DEV_MALFORMED)
@@ -578,6 +581,8 @@ uint64_t kq_hip_moe_config_scratch_bytes(const kq_hip_moe_config *cfg, uint64_t 
 }
 
 #define KQ_MOE_MAX_TOKENS 65536u
+/* token count from which the layer runs as grouped expert GEMMs */
+#define KQ_GROUPED_MIN_TOKENS 2u
 
 static kq_status moe_common(const kq_hip_context *c, const kq_hip_moe_config *cfg,
                             const float *router, const float *sgw, const float *hidden,
@@ -688,10 +693,57 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     if (st != KQ_STATUS_OK) return st;
     e = kq_launch_moe_route(&d, w->router, w->shared_gate_weight, hidden, (uint32_t)tokens, &ws,
                             c->d_status, c->stream);
-    if (e == hipSuccess)
+    /* several tokens: each expert's weights stream once for all of its
+     * tokens (grouped MFMA path); one token: the fused decode kernels */
+    if (e == hipSuccess && tokens >= KQ_GROUPED_MIN_TOKENS &&
+        kq_launch_moe_grouped_supported(&d, &lw))
+        e = kq_launch_moe_grouped(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status,
+                                  c->stream);
+    else if (e == hipSuccess)
         e = kq_launch_moe_experts(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status,
                                   c->stream);
     if (e == hipSuccess && ids != NULL)
         e = hipMemcpyAsync(ids, ws.ids, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice, c->stream);
     return finish(c, e, "MoE execute launch", diag);
+}
+
+kq_status kq_hip_moe_token_permutation(kq_hip_context *c, const kq_hip_moe_config *cfg,
+                                       const uint32_t *ids, uint64_t tokens, uint32_t *offsets,
+                                       uint32_t *pair_token, uint32_t *pair_slot, void *scratch,
+                                       uint64_t scratch_bytes, kq_diagnostic *diag) {
+    kq_launch_moe_dims d;
+    uint64_t pairs;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || !moe_ok(cfg) || ids == NULL || offsets == NULL || pair_token == NULL ||
+        pair_slot == NULL || scratch == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete permutation arguments are required");
+    if (tokens == 0u || tokens > KQ_MOE_MAX_TOKENS)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "MoE token count is zero or above %u",
+                       KQ_MOE_MAX_TOKENS);
+    d = launch_dims(cfg);
+    if (d.experts > 1023u)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "the permutation supports up to 1023 experts");
+    pairs = tokens * d.top_k;
+    if (scratch_bytes < pairs * 4u)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "permutation scratch needs %llu bytes",
+                       (unsigned long long)(pairs * 4u));
+    if (!aligned(ids, 4u) || !aligned(offsets, 4u) || !aligned(pair_token, 4u) ||
+        !aligned(pair_slot, 4u) || !aligned(scratch, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "permutation buffers need 4-byte alignment");
+    if (ranges_overlap(offsets, (d.experts + 1u) * 4u, pair_token, pairs * 4u) ||
+        ranges_overlap(offsets, (d.experts + 1u) * 4u, pair_slot, pairs * 4u) ||
+        ranges_overlap(pair_token, pairs * 4u, pair_slot, pairs * 4u) ||
+        ranges_overlap(ids, pairs * 4u, offsets, (d.experts + 1u) * 4u) ||
+        ranges_overlap(ids, pairs * 4u, pair_token, pairs * 4u) ||
+        ranges_overlap(ids, pairs * 4u, pair_slot, pairs * 4u) ||
+        ranges_overlap(scratch, pairs * 4u, ids, pairs * 4u))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "permutation buffers overlap");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return finish(c,
+                  kq_launch_moe_permute(ids, (uint32_t)tokens, d.top_k, d.experts, offsets,
+                                        pair_token, (uint32_t *)scratch, pair_slot, c->d_status,
+                                        c->stream),
+                  "permutation launch", diag);
 }

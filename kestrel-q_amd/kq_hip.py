@@ -104,6 +104,9 @@ SIGNATURES = {
     "kq_hip_moe_execute_quantized": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p,
                                                C.c_void_p, C.c_uint64, C.c_void_p]),
+    "kq_hip_moe_token_permutation": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
+                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                               C.c_uint64, C.c_void_p]),
     "kq_hip_f32_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
 }
 
@@ -313,6 +316,14 @@ class Context:
                                                  self._p(out), cap,
                                                  self._p(ids) if ids is not None else None,
                                                  self._p(scratch), scratch_bytes, C.byref(d)), d)
+
+    def moe_permutation(self, cfg: MoeConfig, ids, tokens: int, offsets, pair_token, pair_slot,
+                        scratch, scratch_bytes: int) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_moe_token_permutation(self._h, C.c_void_p(cfg.handle), self._p(ids),
+                                                 tokens, self._p(offsets), self._p(pair_token),
+                                                 self._p(pair_slot), self._p(scratch),
+                                                 scratch_bytes, C.byref(d)), d)
 
 
 def moe_weights(bufs: dict, gate_type=TYPE_Q4_K, down_type=TYPE_Q6_K) -> MoeWeights:

@@ -199,3 +199,112 @@ def test_moe_fails_closed(ctx, layer):
     assert e.value.name == "ALIASING_VIOLATION"
     # and the layer still runs correctly afterwards
     test_moe_decode_one_token(ctx, layer)
+
+
+# ---------------- multi-token (grouped expert GEMM) path ----------------
+
+def device_permutation(ctx, E, K, ids):
+    T = ids.shape[0]
+    cfg = kq_hip.MoeConfig(64, E, K, 256, 256)
+    bufs = [ctx.upload(np.ascontiguousarray(ids, np.uint32)), ctx.alloc((E + 1) * 4),
+            ctx.alloc(T * K * 4), ctx.alloc(T * K * 4), ctx.alloc(T * K * 4)]
+    di, doff, dtok, dslot, ds = bufs
+    ctx.moe_permutation(cfg, di, T, doff, dtok, dslot, ds, T * K * 4)
+    got = (ctx.download(doff, np.uint32, E + 1), ctx.download(dtok, np.uint32, T * K),
+           ctx.download(dslot, np.uint32, T * K))
+    for b in bufs:
+        b.close()
+    cfg.close()
+    return got
+
+
+@pytest.mark.parametrize("T,E,K,pattern", [(512, 512, 10, "random"), (1, 512, 10, "random"),
+                                           (300, 64, 8, "random"), (257, 16, 16, "all-same"),
+                                           (1000, 1023, 4, "skewed")])
+def test_token_permutation_bit_exact(ctx, T, E, K, pattern):
+    # The stable counting sort by expert id (tokens ascending within an
+    # expert) that the grouped path runs on; the oracle states it by
+    # definition. Token counts straddle the kernel's 256-token rank chunks.
+    rng = np.random.default_rng(T + E + K)
+    if pattern == "all-same":
+        ids = np.tile(rng.choice(E, K, replace=False), (T, 1))
+    elif pattern == "skewed":
+        ids = np.stack([rng.choice(E, K, replace=False, p=None) if t % 3 else np.arange(K)
+                        for t in range(T)])
+    else:
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)])
+    ids = ids.astype(np.uint32)
+    got = device_permutation(ctx, E, K, ids)
+    want = kq_oracle.moe_permutation(ids, E)
+    for name, g, w in zip(("offsets", "pair_token", "pair_slot"), got, want):
+        assert np.array_equal(g, w), name
+
+
+def test_token_permutation_rejects_bad_id(ctx):
+    ids = np.zeros((4, 2), np.uint32)
+    ids[2, 1] = 16
+    with pytest.raises(kq_hip.KqError) as e:
+        device_permutation(ctx, 16, 2, ids)
+    assert e.value.name == "INVALID_ARGUMENT"
+
+
+@pytest.mark.parametrize("tokens", [3, 40, 512])
+def test_moe_prefill_grouped(ctx, layer, tokens):
+    # T tokens through route -> permutation -> grouped MFMA gate/up + SwiGLU
+    # -> grouped down -> ordered combine; at 512 tokens about a dozen experts
+    # get more than 16 tokens (several M-chunks) and every expert is touched.
+    say(f"prefill tokens={tokens}")
+    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 1000 + tokens),
+                     tokens * 2048).reshape(tokens, 2048)
+    out, ids = layer.run(ctx, x)
+    ref, tr = layer.oracle(x)
+    assert np.array_equal(ids, tr["selected_ids"])
+    assert_close(out, ref)
+
+
+def test_moe_prefill_all_tokens_same_experts(ctx):
+    # A zero router makes every logit equal: the partial selection keeps ids
+    # 0..K-1 for every token, so those experts each get all T tokens (three
+    # 16-token chunks, the last partial) and the others none.
+    H, E, K, I, T = 512, 32, 4, 256, 40
+    w = S.moe_weights(S.W_MOE + 11, H, E, I, I)
+    w["router"] = np.zeros_like(w["router"])
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    x = S.normal_f32(S.stream_key(S.W_MOE + 11, S.R_HIDDEN), T * H).reshape(T, H)
+    n = cfg.scratch_bytes(T)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(T * H * 4), ctx.alloc(T * K * 4)
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs), dx, T, dout, dids, scratch, n)
+    out = ctx.download(dout, np.float32, T * H).reshape(T, H)
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in ROLES.items()}, x, trace=True)
+    ids = ctx.download(dids, np.uint32, T * K).reshape(T, K)
+    assert np.array_equal(ids, tr["selected_ids"]) and (ids == np.arange(K)).all()
+    assert_close(out, ref)
+
+
+@pytest.mark.parametrize("down_fmt", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("H,I", [(256, 512), (1024, 256), (2048, 2048)])
+def test_moe_prefill_shapes(ctx, H, I, down_fmt):
+    # Every hidden / intermediate width the grouped kernels are built for,
+    # with Q4_K and Q6_K down projections.
+    E, K, T = 24, 3, 37
+    w = S.moe_weights(S.W_MOE + H + I, H, E, I, I, down_fmt=down_fmt)
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    x = S.normal_f32(S.stream_key(S.W_MOE + H + I, S.R_HIDDEN), T * H).reshape(T, H)
+    x[5] *= 1e-30   # tiny row: the per-token power-of-two scaling keeps it
+    x[6] *= 1e6     # large row
+    n = cfg.scratch_bytes(T)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(T * H * 4), ctx.alloc(T * K * 4)
+    dt = kq_hip.TYPE_IDS[down_fmt]
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, kq_hip.TYPE_Q4_K, dt), dx, T, dout, dids,
+                    scratch, n)
+    out = ctx.download(dout, np.float32, T * H).reshape(T, H)
+    fmt = getattr(kq_oracle, down_fmt)
+    roles = dict(ROLES, down=fmt, shared_down=fmt)
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in roles.items()}, x, trace=True,
+                                    threads=oracle_threads())
+    assert np.array_equal(ctx.download(dids, np.uint32, T * K).reshape(T, K), tr["selected_ids"])
+    assert_close(out, ref)
