@@ -166,21 +166,23 @@ struct Stage {
 /* Stage rows src_row[i] (or zeros where negative) of X [*, KDIM]: scale by
  * 2^sig (largest magnitude into [2^14, 2^15)), split into fp16 hi + lo and,
  * for Q4_K, form the 32-column sums of the scaled row times 2^-5 (so they
- * fit fp16), also split. One wave per row; each lane holds KDIM/64
- * consecutive columns. Returns true if a non-finite input was seen. */
+ * fit fp16), also split. One wave per row; lane l holds the float4 column
+ * groups l, l + 64, ..., so that both the global reads and the LDS writes
+ * of a wave are contiguous (no bank conflicts). Returns true if a
+ * non-finite input was seen. */
 template <uint32_t FMT, uint32_t KDIM>
 __device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
                            const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
     using S = Stage<FMT, KDIM>;
-    constexpr uint32_t EPL = KDIM / 64u; /* 4 .. 32 */
-    constexpr uint32_t NQ = EPL / 4u;
+    constexpr uint32_t NQ = KDIM / 256u; /* float4 groups per lane: 1 .. 8 */
     bool bad = false;
     for (uint32_t i = wave; i < kTile; i += nwaves) {
         const int src = src_row[i];
-        const float4 *p = (const float4 *)(X + (size_t)(src < 0 ? 0 : src) * KDIM) + lane * NQ;
+        const float4 *p = (const float4 *)(X + (size_t)(src < 0 ? 0 : src) * KDIM) + lane;
         float4 v[NQ];
 #pragma unroll
-        for (uint32_t q = 0; q < NQ; ++q) v[q] = src < 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : p[q];
+        for (uint32_t q = 0; q < NQ; ++q)
+            v[q] = src < 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : p[64u * q];
         float m = 0.0f;
         bool nf = false;
 #pragma unroll
@@ -196,13 +198,13 @@ __device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
         /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) lies in [2^14, 2^15) */
         int sig = 0;
         if (!any_nf && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
-        float part = 0.0f;
-        _Float16 *dh = st.xh + i * S::kPitch + lane * EPL;
-        _Float16 *dl = st.xl + i * S::kPitch + lane * EPL;
+        _Float16 *dh = st.xh + i * S::kPitch + 4u * lane;
+        _Float16 *dl = st.xl + i * S::kPitch + 4u * lane;
 #pragma unroll
         for (uint32_t q = 0; q < NQ; ++q) {
             const float a[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
             _Float16 hi[4], lo[4];
+            float part = 0.0f;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const float xs = any_nf ? 0.0f : ldexpf(a[c], sig);
@@ -210,21 +212,21 @@ __device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
                 lo[c] = (_Float16)(xs - (float)hi[c]);
                 part += xs;
             }
-            *(h4 *)(dh + 4u * q) = h4{hi[0], hi[1], hi[2], hi[3]};
-            *(h4 *)(dl + 4u * q) = h4{lo[0], lo[1], lo[2], lo[3]};
-        }
-        if constexpr (S::kSums) {
-            /* 32-column sums: EPL columns per lane, 32 / EPL lanes per sum */
-            constexpr uint32_t LPS = EPL >= 32u ? 1u : 32u / EPL;
-#pragma unroll
-            for (uint32_t o = 1; o < LPS; o <<= 1) part += __shfl_xor(part, (int)o, KQ_WAVE);
-            if (lane % LPS == 0u) {
-                const float s = part * 0.03125f;
-                const _Float16 sh = (_Float16)s;
-                const _Float16 sl = (_Float16)(s - (float)sh);
-                const uint32_t j = lane * EPL / 32u;
-                st.sxh[i * S::kSxPitch + j] = sh;
-                st.sxl[i * S::kSxPitch + j] = sl;
+            *(h4 *)(dh + 256u * q) = h4{hi[0], hi[1], hi[2], hi[3]};
+            *(h4 *)(dl + 256u * q) = h4{lo[0], lo[1], lo[2], lo[3]};
+            if constexpr (S::kSums) {
+                /* 32-column sums: 8 consecutive lanes hold one */
+                part += __shfl_xor(part, 1, KQ_WAVE);
+                part += __shfl_xor(part, 2, KQ_WAVE);
+                part += __shfl_xor(part, 4, KQ_WAVE);
+                if ((lane & 7u) == 0u) {
+                    const float s = part * 0.03125f;
+                    const _Float16 sh = (_Float16)s;
+                    const _Float16 sl = (_Float16)(s - (float)sh);
+                    const uint32_t jsb = (256u * q + 4u * lane) / 32u;
+                    st.sxh[i * S::kSxPitch + jsb] = sh;
+                    st.sxl[i * S::kSxPitch + jsb] = sl;
+                }
             }
         }
         if (lane == 0u) st.sig[i] = sig;
@@ -391,6 +393,8 @@ struct Tile<KQ_LAUNCH_Q6_K, KDIM, NMAT> {
                     for (int k = 0; k < 4; ++k) acc[m][k] = fmaf(ds, t[k], acc[m][k]);
                 }
             }
+            /* as in the Q4_K tile: bound how far fragment reads are hoisted */
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 };
@@ -429,11 +433,18 @@ __device__ __forceinline__ Work work_of(uint32_t y, const uint32_t *offsets, uin
  *   swiglu(g, u).
  * NMAT = 1: down (rows = hidden, KDIM = intermediate), input rows are
  *   act[pos], output o[pos][row].
- * grid: x = slabs of NW * 16 rows, y = routed experts then shared chunks.
- * Positions: routed pairs 0 .. T*K-1 (permuted order), shared token t at
- * T*K + t.
+ * grid: x = slabs of NW * TPW * 16 rows, y = routed experts then shared
+ * chunks. Positions: routed pairs 0 .. T*K-1 (permuted order), shared token
+ * t at T*K + t.
+ *
+ * Each wave walks TPW 16-row tiles, all blocks of a tile in order, with the
+ * next block's weights (across tile boundaries) in flight while one block is
+ * multiplied. Every prefetch and every result store is issued on every
+ * path -- ones past the data use offsets outside their buffer, which the
+ * hardware drops -- so the memory counters the compiler waits on are the
+ * same on every path and a wait never drains the prefetch.
  */
-template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW>
+template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW, int TPW, int PD>
 __global__ __launch_bounds__(NW * 64) void grouped_pass(
     const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
     const uint8_t *__restrict__ SW0, const uint8_t *__restrict__ SW1,
@@ -451,32 +462,52 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
 
     const Work wk = work_of(blockIdx.y, offsets, experts, tokens, shared_chunks);
     if (wk.count == 0u) return;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    /* the wave index is uniform across the wave; saying so keeps the weight
+     * buffer descriptors in scalar registers (no per-lane waterfall) */
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t j = lane & 15u, g = lane >> 4;
-    const uint32_t row0 = (blockIdx.x * NW + wave) * kTile;
-    const bool active = row0 < rows; /* idle waves still take part in staging */
-    const uint32_t row = row0 + j;
     const uint32_t tk = tokens * top_k;
     const uint32_t e = blockIdx.y;
+    /* tile t of this wave starts at row tile_row(t); tiles past the matrix
+     * load nothing and store nothing */
+    auto tile_row = [&](uint32_t t) { return ((blockIdx.x * TPW + t) * NW + wave) * kTile; };
 
+    const uint32_t wbytes = rows * RB;
     KqBuf wb[NMAT];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
         const uint8_t *base = wk.shared ? (m == 0 ? SW0 : SW1)
                                         : (m == 0 ? W0 : W1) + (size_t)e * rows * RB;
-        wb[m] = kq_buf(base, active ? rows * RB : 0u);
+        wb[m] = kq_buf(base, wbytes);
     }
-    const uint32_t roff = row * RB;
-    auto load = [&](Raw (&r)[NMAT], uint32_t b) {
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) r[m] = F::load(wb[m], roff + b * F::kBytes, g);
+    /* byte offset of block b of tile t for this lane's row, or the buffer
+     * size (every field read from there is dropped) */
+    auto boff = [&](uint32_t t, uint32_t b) {
+        const uint32_t r0 = tile_row(t);
+        return (t < (uint32_t)TPW && r0 < rows) ? (r0 + j) * RB + b * F::kBytes : wbytes;
     };
+    auto load = [&](Raw (&r)[NMAT], uint32_t off) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) r[m] = F::load(wb[m], off, g);
+    };
+    /* results go through a buffer over this workgroup's output rows */
+    const uint32_t pos0 = wk.shared ? tk + wk.first : wk.first;
+    const uint32_t obytes = wk.count * rows * 4u;
+    const KqBuf ob = kq_buf(out + (size_t)pos0 * rows, obytes);
+
+    /* the wave's iterations are (tile, block) pairs in order; iteration
+     * `it` reads ring slot it % R, which iteration it - PD filled */
+    constexpr uint32_t NIT = (uint32_t)TPW * NB;
+    constexpr uint32_t R = (uint32_t)PD + 1u;
+    auto it_off = [&](uint32_t it) { return it < NIT ? boff(it / NB, it % NB) : wbytes; };
 
     bool bad = false, badin = false, malformed = false;
     for (uint32_t c0 = 0; c0 < wk.count; c0 += kTile) {
-        /* the first block's weights are requested before the staging */
-        Raw ra[NMAT], rb[NMAT];
-        if (active) load(ra, 0u);
+        /* the first PD blocks' weights are requested before the staging */
+        Raw ring[R][NMAT];
+#pragma unroll
+        for (uint32_t it = 0; it < (uint32_t)PD; ++it) load(ring[it], it_off(it));
         __syncthreads(); /* the previous chunk's readers are done */
         if (threadIdx.x < kTile) {
             const uint32_t i = threadIdx.x;
@@ -499,38 +530,44 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
         else
             bad |= nf;
         __syncthreads();
-        if (!active) continue;
 
-        /* ping-pong: the next block's weights are in flight while one block
-         * is decoded and multiplied */
         f4 acc[NMAT];
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
+        static_assert(NIT % R == 0u, "the ring must divide the iterations");
 #pragma unroll 1
-        for (uint32_t b = 0; b < NB; b += 2u) {
-            if (b + 1u < NB) load(rb, b + 1u);
-            T::block(ra, st, b, j, g, acc, malformed);
-            if (b + 1u >= NB) break;
-            if (b + 2u < NB) load(ra, b + 2u);
-            T::block(rb, st, b + 1u, j, g, acc, malformed);
-        }
-        /* D[token][row]: this lane holds row `row` of tokens 4g .. 4g+3 */
+        for (uint32_t it0 = 0; it0 < NIT; it0 += R) {
 #pragma unroll
-        for (uint32_t t = 0; t < 4u; ++t) {
-            const uint32_t i = 4u * g + t;
-            if (c0 + i >= wk.count) continue;
-            const int sg = st.sig[i];
-            const uint32_t pos = wk.shared ? tk + wk.first + c0 + i : wk.first + c0 + i;
-            float v;
-            if constexpr (NMAT == 2) {
-                const float gv = ldexpf(acc[0][t], -sg), uv = ldexpf(acc[1][t], -sg);
-                v = kq_swiglu(gv, uv);
-                bad |= !kq_isfinite(gv) || !kq_isfinite(uv);
-            } else {
-                v = ldexpf(acc[0][t], -sg);
+            for (uint32_t r = 0; r < R; ++r) {
+                const uint32_t it = it0 + r;
+                const uint32_t t = it / NB, b = it % NB;
+                if (b == 0u) {
+#pragma unroll
+                    for (int m = 0; m < NMAT; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
+                }
+                load(ring[(r + PD) % R], it_off(it + PD));
+                T::block(ring[r], st, b, j, g, acc, malformed);
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 1u < NB) continue;
+                /* D[token][row]: this lane holds row `row` of tokens 4g .. 4g+3 */
+                const uint32_t row = tile_row(t) + j;
+#pragma unroll
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const uint32_t i = 4u * g + q;
+                    const bool valid = c0 + i < wk.count && row < rows;
+                    const int sg = st.sig[i];
+                    float v;
+                    if constexpr (NMAT == 2) {
+                        const float gv = ldexpf(acc[0][q], -sg), uv = ldexpf(acc[1][q], -sg);
+                        v = kq_swiglu(gv, uv);
+                        bad |= valid && (!kq_isfinite(gv) || !kq_isfinite(uv));
+                    } else {
+                        v = ldexpf(acc[0][q], -sg);
+                    }
+                    bad |= valid && !kq_isfinite(v);
+                    const uint32_t off = valid ? ((c0 + i) * rows + row) * 4u : obytes;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ob.r, (int)off, 0,
+                                                          0);
+                }
             }
-            bad |= !kq_isfinite(v);
-            out[(size_t)pos * rows + row] = v;
         }
     }
     if (badin) kq_flag(status, KQ_DEV_INPUT);
@@ -659,12 +696,33 @@ __global__ __launch_bounds__(256) void moe_combine(
 
 constexpr uint32_t kSharedChunks = 2; /* 16-token chunks per shared-expert workgroup */
 
-template <uint32_t GFMT, uint32_t KDIM, int NMAT>
-constexpr int waves_for() {
-    /* gate/up at 2048 columns keeps one 136 KiB chunk image per CU: 16 waves
-     * share it; narrower images leave room for more workgroups */
-    return NMAT == 2 ? (KDIM >= 1024u ? 16 : 8) : 8;
-}
+/* Launch shape per pass: NW waves per workgroup, TPW 16-row tiles per
+ * wave, PD blocks of weights in flight ahead of the one being multiplied.
+ * The registers of a SIMD bound waves x (PD + 1) x block registers; the
+ * gate/up image (136 KiB at 2048 columns) allows one workgroup per CU. */
+#ifndef KQ_GU_NW
+#define KQ_GU_NW 16
+#define KQ_GU_TPW 1
+#define KQ_GU_PD 1
+#endif
+#ifndef KQ_DN_NW
+#define KQ_DN_NW 8
+#define KQ_DN_TPW 4
+#define KQ_DN_PD 1
+#endif
+template <uint32_t KDIM, int NMAT>
+struct Shape {
+    static constexpr int NW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_NW : 8) : KQ_DN_NW;
+    static constexpr int TPW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_TPW : 2) : KQ_DN_TPW;
+    /* the ring (PD + 1 slots) is a power of two that divides the wave's
+     * TPW * KDIM / 256 iterations */
+    static constexpr int NIT = TPW * (int)(KDIM / 256u);
+    static constexpr int WANT = (NMAT == 2 ? KQ_GU_PD : KQ_DN_PD) + 1;
+    static constexpr int RING = WANT >= 8 && NIT % 8 == 0 ? 8
+                                : WANT >= 4 && NIT % 4 == 0 ? 4
+                                : WANT >= 2 && NIT % 2 == 0 ? 2 : 1;
+    static constexpr int PD = RING > 1 ? RING - 1 : 0;
+};
 
 template <uint32_t GFMT, uint32_t KDIM, int NMAT>
 hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
@@ -672,11 +730,14 @@ hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
                        const uint32_t *perm_tok, uint32_t experts, uint32_t tokens,
                        uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
                        hipStream_t s) {
-    constexpr int NW = waves_for<GFMT, KDIM, NMAT>();
-    const uint32_t slab = (uint32_t)NW * kTile;
+    constexpr int NW = Shape<KDIM, NMAT>::NW;
+    constexpr int TPW = Shape<KDIM, NMAT>::TPW;
+    constexpr int PD = Shape<KDIM, NMAT>::PD;
+    const uint32_t slab = (uint32_t)(NW * TPW) * kTile;
     const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
     const dim3 grid((rows + slab - 1u) / slab, experts + sh_wgs);
-    hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW>), grid, dim3(NW * 64), 0, s, W0, W1,
+    hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW, TPW, PD>), grid, dim3(NW * 64), 0, s,
+                       W0, W1,
                        SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, rows,
                        kSharedChunks, out, status);
     return hipGetLastError();
