@@ -241,6 +241,91 @@ __global__ __launch_bounds__(64) void router_chain(const float *__restrict__ wt,
         shared_logit[t] = acc;
 }
 
+/* Several tokens per lane: lane e of a wave runs the chains of expert e for
+ * kChainTB consecutive tokens, so each router value it reads serves that
+ * many chains, and the waves of a workgroup (consecutive token groups, the
+ * same 64 experts) read the same router columns, which L1 then serves. The
+ * workgroup's activations are staged in LDS 256 columns at a time and read
+ * as broadcasts. Each chain is still p = w * x rounded, acc = acc + p in
+ * column order. */
+/* two chains per lane (enough independent adds to keep the VALU issuing)
+ * and two waves per workgroup: small workgroups spread the T * (E + 1)
+ * chains evenly over the CUs; the waves of one workgroup share the router
+ * columns through L1 */
+constexpr uint32_t kChainTB = 2;
+constexpr uint32_t kChainWaves = 2;
+constexpr uint32_t kChainCols = 256; /* activation columns staged per round */
+
+__global__ __launch_bounds__(64 * kChainWaves) void router_chain_tb(
+    const float *__restrict__ wt, const float *__restrict__ hidden_states, uint32_t tokens,
+    uint32_t experts, uint32_t hidden, uint32_t ep, float *__restrict__ logits,
+    float *__restrict__ shared_logit) {
+    constexpr uint32_t TPG = kChainTB * kChainWaves; /* tokens per workgroup */
+    constexpr uint32_t NQ = kChainCols / 4u;
+    __shared__ float4 xs[TPG][NQ];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t e = blockIdx.x * 64u + lane;
+    const uint32_t tg = blockIdx.y * TPG;
+    const uint32_t nq = hidden / 4u;
+    /* the 64-expert router column group, transposed: step q of lane l at
+     * (q * ep + l) * 16 bytes */
+    const KqBuf rb = kq_buf(wt + 4u * (blockIdx.x * 64u), (nq - 1u) * ep * 16u + 64u * 16u);
+    float acc[kChainTB];
+#pragma unroll
+    for (uint32_t b = 0; b < kChainTB; ++b) acc[b] = 0.0f;
+    constexpr uint32_t RUN = 8;
+    uint4 wa[RUN], wb[RUN];
+    auto fetch = [&](uint4 (&w)[RUN], uint32_t q0) {
+#pragma unroll
+        for (uint32_t k = 0; k < RUN; ++k) w[k] = kq_ld128(rb, ((q0 + k) * ep + lane) * 16u, 0u);
+    };
+    /* column q (global) of this wave's tokens from the staged round */
+    auto run = [&](const uint4 (&w)[RUN], uint32_t q0) {
+#pragma unroll
+        for (uint32_t k = 0; k < RUN; ++k) {
+            const float4 wv = as_f4(w[k]);
+            const uint32_t ql = (q0 + k) % NQ;
+#pragma unroll
+            for (uint32_t b = 0; b < kChainTB; ++b) {
+                const float4 xv = xs[wave * kChainTB + b][ql];
+                float p;
+                p = wv.x * xv.x; acc[b] = acc[b] + p;
+                p = wv.y * xv.y; acc[b] = acc[b] + p;
+                p = wv.z * xv.z; acc[b] = acc[b] + p;
+                p = wv.w * xv.w; acc[b] = acc[b] + p;
+            }
+        }
+    };
+    /* nq is a multiple of NQ (and of 2 * RUN) on this path. Every path
+     * issues the same router loads, so no wait drains the run in flight. */
+    fetch(wa, 0u);
+    for (uint32_t c = 0; c < nq; c += NQ) {
+        __syncthreads(); /* the previous round's readers are done */
+        for (uint32_t i = threadIdx.x; i < TPG * NQ; i += 64u * kChainWaves) {
+            const uint32_t tt = i / NQ, qq = i % NQ;
+            const uint32_t t = tg + tt < tokens ? tg + tt : tokens - 1u;
+            xs[tt][qq] = ((const float4 *)(hidden_states + (size_t)t * hidden))[c + qq];
+        }
+        __syncthreads();
+        for (uint32_t q = c; q < c + NQ; q += 2u * RUN) {
+            fetch(wb, q + RUN);
+            run(wa, q);
+            fetch(wa, q + 2u * RUN < nq ? q + 2u * RUN : q);
+            run(wb, q + RUN);
+        }
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < kChainTB; ++b) {
+        const uint32_t t = tg + wave * kChainTB + b;
+        if (t >= tokens) continue;
+        if (e < experts)
+            logits[(size_t)t * experts + e] = acc[b];
+        else if (e == experts)
+            shared_logit[t] = acc[b];
+    }
+}
+
 /* ------------------------- route finish ------------------------- */
 /* Maximum over the 64 lanes of a wave, returned in every lane: DPP within
  * 16-lane rows, then permlane swaps across rows. All lanes must be active. */
@@ -849,8 +934,16 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
                            shared_gate_weight, d->experts, d->hidden, ep, ws->router_t, status);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(router_chain, dim3(ep / 64u, tokens), dim3(64), 0, s, ws->router_t,
-                           hidden, d->experts, d->hidden, ep, ws->logits, ws->shared_logit);
+        if (tokens >= kChainTB * kChainWaves && d->hidden % kChainCols == 0u) {
+            const uint32_t per_wg = kChainTB * kChainWaves;
+            hipLaunchKernelGGL(router_chain_tb, dim3(ep / 64u, (tokens + per_wg - 1u) / per_wg),
+                               dim3(64 * kChainWaves), 0, s, ws->router_t, hidden, tokens,
+                               d->experts, d->hidden, ep, ws->logits, ws->shared_logit);
+        } else {
+            hipLaunchKernelGGL(router_chain, dim3(ep / 64u, tokens), dim3(64), 0, s,
+                               ws->router_t, hidden, d->experts, d->hidden, ep, ws->logits,
+                               ws->shared_logit);
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -75,8 +75,9 @@ def test_tier_b_routing_vectors(ctx, case):
 
 
 @pytest.mark.parametrize("seed", range(6))
-@pytest.mark.parametrize("tokens", [1, 5])
+@pytest.mark.parametrize("tokens", [1, 5, 37])
 def test_routing_512x2048_bit_exact(ctx, seed, tokens):
+    # 37 tokens run the several-tokens-per-lane chains, last group partial
     H, E, K = 2048, 512, 10
     router = S.normal_f32(S.stream_key(S.W_MOE, S.R_ROUTER, seed, 7), E * H, 0.02).reshape(E, H)
     x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, seed, tokens), tokens * H).reshape(tokens, H)
