@@ -44,6 +44,15 @@ __device__ __forceinline__ float kq_f16_to_f32(uint32_t h) {
     return __uint_as_float(sign | ((e + 112u) << 23) | (f << 13));
 }
 
+/* The same conversion in one v_cvt_f32_f16: exact for every finite input,
+ * subnormals included (the kernels keep fp16 denormals: float denorm mode
+ * 16/64 = 3), but a signalling NaN comes back quiet. For block scales on
+ * tolerance-compared paths, where a non-finite scale only raises
+ * MALFORMED; bit-exact decode keeps kq_f16_to_f32. */
+__device__ __forceinline__ float kq_f16_to_f32_hw(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
+}
+
 __device__ __forceinline__ bool kq_isfinite(float v) {
     return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u;
 }
@@ -131,6 +140,27 @@ __device__ __forceinline__ void kq_k_scale(uint32_t j, uint32_t w0, uint32_t w1,
         *mn = (kq_byte(w0, w1, w2, j + 4u) >> 4) |
               ((kq_byte(w0, w1, w2, j) >> 6) << 4);
     }
+}
+
+/* Scales and mins of Q4_K sub-blocks 2p and 2p+1 (p = 0..3), without
+ * branches (p differs across lanes): the same 6-bit fields as kq_k_scale
+ * (src/kq_numeric.c:161-174), from the 12 packed bytes q[0..11] in dwords
+ * w0 = q[0..3], w1 = q[4..7], w2 = q[8..11]. */
+__device__ __forceinline__ void kq_k_scale_pair(uint32_t p, uint32_t w0, uint32_t w1,
+                                                uint32_t w2, uint32_t *s0, uint32_t *m0,
+                                                uint32_t *s1, uint32_t *m1) {
+    const uint32_t sh = 16u * (p & 1u);
+    const uint32_t u = w0 >> sh; /* q[2(p&1)], q[2(p&1)+1] */
+    const uint32_t z = w1 >> sh; /* q[4+2(p&1)], q[5+2(p&1)] */
+    const uint32_t w = w2 >> sh; /* q[8+2(p&1)], q[9+2(p&1)] */
+    /* all ones for sub-blocks 0..3; a bitwise select, which the compiler
+     * keeps as v_bfi_b32 where a ?: becomes a divergent branch */
+    const uint32_t lo = 0u - (uint32_t)(p < 2u);
+    auto sel = [lo](uint32_t a, uint32_t b) { return (a & lo) | (b & ~lo); };
+    *s0 = sel(u & 63u, (w & 15u) | ((u >> 2) & 0x30u));
+    *s1 = sel((u >> 8) & 63u, ((w >> 8) & 15u) | ((u >> 10) & 0x30u));
+    *m0 = sel(z & 63u, ((w >> 4) & 15u) | ((z >> 2) & 0x30u));
+    *m1 = sel((z >> 8) & 63u, ((w >> 12) & 15u) | ((z >> 10) & 0x30u));
 }
 
 /*

@@ -51,7 +51,10 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     using R = kq::Rows<TYPE, COLS, B, RT>;
     using Raw = typename R::Raw;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
+    /* uniform across the wave: the group loop and the full-group test stay
+     * scalar branches */
+    const uint32_t wave =
+        __builtin_amdgcn_readfirstlane((blockIdx.x * kThreads + threadIdx.x) >> 6);
     const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
     const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;

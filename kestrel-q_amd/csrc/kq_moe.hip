@@ -639,7 +639,8 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
         U = up + (size_t)e * inter * R::RB;
     }
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = (blockIdx.x * kThreads + threadIdx.x) >> 6;
+    const uint32_t wave =
+        __builtin_amdgcn_readfirstlane((blockIdx.x * kThreads + threadIdx.x) >> 6);
     const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
     const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
@@ -718,7 +719,8 @@ __global__ __launch_bounds__(64 * kDownWaves) void expert_down_combine(
     __shared__ uint32_t ord_s[64];
     __shared__ float w_s[64];
     const uint32_t g = blockIdx.x, t = blockIdx.y;
-    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u, nwv = blockDim.x >> 6;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
     const uint32_t nslots = top_k + 1u;
     if (threadIdx.x < top_k) {

@@ -113,12 +113,11 @@ struct LaneQ4K {
         return r;
     }
     __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
-        const float d = kq_f16_to_f32(r.hd.x & 0xffffu);
-        const float dmin = kq_f16_to_f32(r.hd.x >> 16);
+        const float d = kq_f16_to_f32_hw(r.hd.x);
+        const float dmin = kq_f16_to_f32_hw(r.hd.x >> 16);
         malformed |= !kq_isfinite(d) || !kq_isfinite(dmin);
         uint32_t s0, m0, s1, m1;
-        kq_k_scale(2u * gq, r.hd.y, r.hd.z, r.hd.w, &s0, &m0);
-        kq_k_scale(2u * gq + 1u, r.hd.y, r.hd.z, r.hd.w, &s1, &m1);
+        kq_k_scale_pair(gq, r.hd.y, r.hd.z, r.hd.w, &s0, &m0, &s1, &m1);
         const float dl = d * (float)s0, ml = dmin * (float)m0;
         /* high nibbles are converted in place (16 * code): fold 1/16 into
          * the sub-block scale (exact power of two) */
@@ -214,7 +213,7 @@ struct LaneQ6K {
         return r;
     }
     __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
-        const float d = kq_f16_to_f32(r.d);
+        const float d = kq_f16_to_f32_hw(r.d);
         malformed |= !kq_isfinite(d);
         const uint2 qa = align8(r.wa, r.sh, false), qb = align8(r.wb, r.sh, false);
         const uint2 qh = align8(r.wh, r.sh, false);
@@ -314,7 +313,7 @@ struct LaneQ8 {
     }
     __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
         const uint32_t w[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
-        const float d = kq_f16_to_f32(r.sh ? (w[0] >> 16) : (w[0] & 0xffffu));
+        const float d = kq_f16_to_f32_hw(r.sh ? (w[0] >> 16) : w[0]);
         malformed |= !kq_isfinite(d);
         /* code dword k = bytes bo+2+4k .. bo+5+4k of the block at bo */
         uint32_t u[8];
