@@ -11,9 +11,10 @@
  * tolerance. The argmax is exact (first maximum, lowest row on ties).
  *
  * Each 64-lane wavefront keeps its lanes' activations in registers for the
- * whole launch and walks groups of RT row passes (kq_rowdot.h): the first
- * group's weight loads are issued before the activation loads, and each
- * following group's loads are in flight while the current group is reduced.
+ * whole launch and walks groups of RT row passes (kq_rowdot.h): the
+ * activation loads are issued first, then the first group's weight loads,
+ * and each following group's loads are in flight while the current group is
+ * reduced.
  * Row sums finish with a transposed butterfly (permlane swaps and DPP), so a
  * group of RT*B partial sums costs a few cross-lane operations. For the
  * fused LM head every wave also keeps a running (max, row) per batch column
@@ -59,28 +60,17 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
     const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
 
-    __shared__ __align__(16) float xs[B * COLS];
     typename R::Lane ln;
     ln.setup(l);
     const KqBuf wb = kq_buf(W, rows * R::RB);
     Raw ra[RT], rb[RT];
     uint32_t g = wave;
-    /* the first group's weights are requested before the activations so the
-     * two memory latencies overlap; the activations are staged once per
-     * workgroup in LDS and each lane takes its slice from there */
+    /* each lane loads its own activations (L2-resident after the first
+     * waves) before the first group's weights: the loads complete in order,
+     * so the activation sums are formed while the weights are in flight and
+     * nothing waits on a workgroup barrier */
+    if (ln.load_x(x, COLS)) kq_flag(status, KQ_DEV_INPUT);
     if (g < ngroups) R::load_group(ln, wb, g, rows, sub, ra);
-    {
-        bool badx = false;
-        for (uint32_t i = threadIdx.x; i < B * COLS / 4u; i += kThreads) {
-            const float4 v = ((const float4 *)x)[i];
-            badx |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
-                    !kq_isfinite(v.w);
-            ((float4 *)xs)[i] = v;
-        }
-        if (badx) kq_flag(status, KQ_DEV_INPUT);
-    }
-    __syncthreads();
-    ln.load_x(xs, COLS);
 
     bool bad = false, malformed = false;
     float best_v[B];

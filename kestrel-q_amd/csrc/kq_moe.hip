@@ -614,8 +614,9 @@ __global__ __launch_bounds__(1024) void route_finish(
 
 /* ---------------------- expert gate/up + SwiGLU ---------------------- */
 /* grid: x = row groups, y = slot (0..K-1 routed by top-k position, K = the
- * shared expert), z = token. act[t][slot][row] = swiglu(g, u). Each wave
- * requests its gate and up rows before the activations (kq_rowdot.h). */
+ * shared expert), z = token. act[t][slot][row] = swiglu(g, u). Each lane
+ * loads its slice of the token's hidden state, then requests its gate and
+ * up rows (kq_rowdot.h). */
 template <uint32_t TYPE, uint32_t COLS, int RT>
 __global__ __launch_bounds__(kThreads) void expert_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
@@ -625,7 +626,6 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
     float *__restrict__ act, uint32_t *status) {
     using R = kq::Rows<TYPE, COLS, 1, RT>;
     using Raw = typename R::Raw;
-    __shared__ __align__(16) float xs[COLS];
     const uint32_t slot = blockIdx.y, t = blockIdx.z;
     const bool shared = slot == top_k;
     const uint32_t rows = shared ? shared_inter : inter;
@@ -649,24 +649,13 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
     Raw rg[RT], ru[RT];
     uint32_t g = wave;
     const KqBuf gb = kq_buf(G, rows * R::RB), ub = kq_buf(U, rows * R::RB);
+    /* each lane loads its slice of the token's hidden state first, then its
+     * gate and up rows (the loads complete in order) */
+    if (ln.load_x(hidden_states + (size_t)t * COLS, COLS)) kq_flag(status, KQ_DEV_INPUT);
     if (g < ngroups) {
         R::load_group(ln, gb, g, rows, sub, rg);
         R::load_group(ln, ub, g, rows, sub, ru);
     }
-    /* the token's hidden state is staged once per workgroup */
-    {
-        const float4 *src = (const float4 *)(hidden_states + (size_t)t * COLS);
-        bool badx = false;
-        for (uint32_t i = threadIdx.x; i < COLS / 4u; i += kThreads) {
-            const float4 v = src[i];
-            badx |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
-                    !kq_isfinite(v.w);
-            ((float4 *)xs)[i] = v;
-        }
-        if (badx) kq_flag(status, KQ_DEV_INPUT);
-    }
-    __syncthreads();
-    ln.load_x(xs, COLS);
     bool bad = false, malformed = false;
     float *out = act + ((size_t)t * (top_k + 1u) + slot) * act_stride;
     for (; g < ngroups; g += nwaves) {
