@@ -332,4 +332,84 @@ __device__ __forceinline__ void kq_group_reduce(float (&v)[N], uint32_t lane) {
     kq_reduce_level<G, N, G / 2>(v, lane);
 }
 
+/* ---- 64-bit values across a wave (all 64 lanes active) ---- */
+
+/* x moved by one DPP control, as two 32-bit halves; lanes that the control
+ * or the row mask leaves without a source receive 0.0. */
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double kq_dpp_f64(double x) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL,
+                                                              ROW_MASK, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL,
+                                                              ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+/* Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 within rows of
+ * 16 lanes, then row 0's total into row 1 and row 2's into row 3
+ * (row_bcast:15), then rows 0-1's total into rows 2-3 (row_bcast:31). */
+__device__ __forceinline__ double kq_wave_scan_f64(double x) {
+    x += kq_dpp_f64<0x111>(x);
+    x += kq_dpp_f64<0x112>(x);
+    x += kq_dpp_f64<0x114>(x);
+    x += kq_dpp_f64<0x118>(x);
+    x += kq_dpp_f64<0x142, 0xa>(x);
+    x += kq_dpp_f64<0x143, 0xc>(x);
+    return x;
+}
+
+/* The value of lane l - 1 (0.0 in lane 0): wave_shr:1. */
+__device__ __forceinline__ double kq_wave_shr1_f64(double x) {
+    return kq_dpp_f64<0x138>(x);
+}
+
+__device__ __forceinline__ double kq_readlane_f64(double x, int lane) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+/* {x(l), x(l ^ 16)} or {x(l), x(l ^ 32)} (in either order, the same for
+ * both halves) through v_permlane16_swap / v_permlane32_swap. */
+template <int SPAN>
+__device__ __forceinline__ void kq_swap_f64(double x, double &p, double &q) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    auto rl = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                         : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    auto rh = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                         : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    p = __builtin_bit_cast(double, ((uint64_t)rh[0] << 32) | rl[0]);
+    q = __builtin_bit_cast(double, ((uint64_t)rh[1] << 32) | rl[1]);
+}
+
+/* Maximum over the wave, in every lane: quad permutes, half-row and row
+ * mirrors, then the two permlane swaps. NaN-free inputs. */
+__device__ __forceinline__ double kq_wave_max_f64(double v) {
+    v = fmax(v, kq_dpp_f64<0xB1>(v));
+    v = fmax(v, kq_dpp_f64<0x4E>(v));
+    v = fmax(v, kq_dpp_f64<0x141>(v));
+    v = fmax(v, kq_dpp_f64<0x140>(v));
+    double p, q;
+    kq_swap_f64<16>(v, p, q);
+    v = fmax(p, q);
+    kq_swap_f64<32>(v, p, q);
+    return fmax(p, q);
+}
+
+/* Sum over the wave, in every lane (the same butterfly as the maximum). */
+__device__ __forceinline__ double kq_wave_sum_f64(double v) {
+    v += kq_dpp_f64<0xB1>(v);
+    v += kq_dpp_f64<0x4E>(v);
+    v += kq_dpp_f64<0x141>(v);
+    v += kq_dpp_f64<0x140>(v);
+    double p, q;
+    kq_swap_f64<16>(v, p, q);
+    v = p + q;
+    kq_swap_f64<32>(v, p, q);
+    return p + q;
+}
+
 #endif

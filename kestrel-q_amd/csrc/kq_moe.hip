@@ -95,7 +95,9 @@ template <uint32_t HIDDEN>
 __global__ __launch_bounds__(kThreads) void router_decode(
     const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
     const float *__restrict__ x, uint32_t experts, float *__restrict__ logits,
-    float *__restrict__ shared_logit, uint32_t *status) {
+    float *__restrict__ shared_logit, uint32_t *status, const uint32_t *skip) {
+    /* the certified routing already produced the ids: nothing to do */
+    if (skip != nullptr && *skip != 0u) return;
     constexpr uint32_t NQ = HIDDEN / 4u;
     constexpr uint32_t NSEG = (NQ + kRtSegQ - 1u) / kRtSegQ;
     __shared__ float4 buf[NSEG * kRtSegQ * kRtPitch];
@@ -326,7 +328,6 @@ __global__ __launch_bounds__(64 * kChainWaves) void router_chain_tb(
     }
 }
 
-/* ------------------------- route finish ------------------------- */
 /* Maximum over the 64 lanes of a wave, returned in every lane: DPP within
  * 16-lane rows, then permlane swaps across rows. All lanes must be active. */
 __device__ __forceinline__ float wave_max(float v) {
@@ -340,6 +341,324 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+/* ---------------- certified routing for one token ---------------- */
+/*
+ * Expert ids must be the CPU's, whose logits are left-to-right binary32
+ * sums (2048 dependent adds per logit). For one token the execute path first
+ * tries to certify the selection without those chains:
+ *
+ * Bounds: for each logit row the rounded products p_i = w_i * x_i are
+ *   formed exactly as the CPU does and fp64 prefix sums give their partial
+ *   sums S_i. The CPU's sum l satisfies
+ *   |l - S_n| <= u / (1 - u) * sum_{i>=2} |l_i| (recursive summation, l_i the
+ *   CPU's own partial sums, u = 2^-24), and sum |l_i| <= sum |S_i| /
+ *   (1 - n u / (1 - u)); with n <= 2048 the bound below takes
+ *   1.001 * u * sum |S_i|, which covers both factors and the fp64 rounding.
+ *   Any non-finite product, or partial sums near the binary32 range, make
+ *   the bound infinite.
+ * Certification: with a_e = S_n and bounds b_e, the top-k by a_e is the
+ *   CPU's selection in the CPU's order if every adjacent pair in it, and
+ *   its last member against every unselected expert, is separated by more
+ *   than the two bounds plus a margin: the margin keeps the rounded
+ *   probabilities fl(fl(exp(fl(l - max))) / s) strictly ordered too, so no
+ *   tie (and no tie-break) can occur. It then writes the ids, the weights
+ *   p / sum(p) from the fp64 values (compared by tolerance like the layer
+ *   output), the ascending-id slot order and the shared gate, and sets the
+ *   flag that makes the exact router and route finish return at once;
+ *   otherwise they run and overwrite everything.
+ */
+/* Rows of router_bounds: four logit rows per workgroup of 16 waves, four
+ * waves per row, each wave a quarter of the columns. */
+constexpr uint32_t kSelRows = 4;
+constexpr uint32_t kSelParts = 4;
+
+constexpr uint32_t kMaxTopK = 64;
+constexpr uint32_t kCertCand = 64; /* candidates one wave ranks */
+
+/* hi - bhi exceeds lo + blo by more than the bounds and 16 units in the
+ * last place of the probability terms involved (m: the largest a) */
+__device__ __forceinline__ bool certify_sep(double hi, double bhi, double lo, double blo,
+                                            double m) {
+    const double margin = 0x1p-20 * (4.0 + fabs(hi - m) + fabs(lo - m));
+    return (hi - bhi) - (lo + blo) > margin;
+}
+
+__device__ __forceinline__ float rdl_f32(float v, uint32_t lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)lane));
+}
+
+/* set bits of m below this lane */
+__device__ __forceinline__ uint32_t bits_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+/*
+ * One workgroup of 16 waves (1024 threads), one thread per expert, after
+ * the bounds kernel. The top-k by a (larger
+ * first, lower id among equals) is found without sorting all experts, with
+ * keys f = (float)a (rounding is monotone):
+ *   1. each full wave (64 experts; the one partial wave when E < 64) finds
+ *      its per-th largest key, per = ceil(need / such waves),
+ *      need = min(k + 1, E) (per > 64 finds -inf);
+ *   2. t = the least of those keys: every such wave has at least `per` keys
+ *      >= t, so at least `need` experts do;
+ *   3. each wave appends its experts with f >= t to one list (an LDS
+ *      counter hands out the places) and keeps the largest a + b among its
+ *      other experts;
+ *   4. wave 0 ranks the candidates by a itself. More than 64 candidates
+ *      leaves the selection uncertified.
+ * Only wave 0 runs after the second barrier, and a lone wave pays each
+ * instruction's latency, so that part is short and free of table reads.
+ * The weights and the shared gate use the hardware exponential: they are
+ * compared by tolerance, like the layer output.
+ */
+struct CertCand {
+    double a;
+    uint32_t id, pad;
+};
+
+__device__ __forceinline__ float fast_expf(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += kq_dpp_pair<1>(v);
+    v += kq_dpp_pair<2>(v);
+    v += kq_dpp_pair<7>(v);
+    v += kq_dpp_pair<15>(v);
+    v = kq_fold16(v, v);
+    return kq_fold32(v, v);
+}
+
+__global__ __launch_bounds__(1024) void route_certify(
+    const double *__restrict__ bound, uint32_t experts, uint32_t top_k,
+    uint32_t *__restrict__ ids, float *__restrict__ weights, uint32_t *__restrict__ order,
+    float *__restrict__ shared_scale, uint32_t *__restrict__ certified) {
+    __shared__ CertCand cmp[kCertCand];
+    __shared__ double cmp_b[kCertCand];
+    __shared__ CertCand srt[kCertCand];
+    __shared__ double srt_b[kCertCand];
+    __shared__ __align__(16) float w_key[16];
+    __shared__ __align__(16) double w_rest[16];
+    __shared__ __align__(16) uint32_t w_bad[16];
+    __shared__ uint32_t s_count;
+    const uint32_t e = threadIdx.x, lane = e & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(e >> 6);
+    const double ninf = -__builtin_inf();
+    const bool live = e < experts;
+    double sh_b = 0.0;
+    if (w == 0u) sh_b = bound[2u * experts + 1u];
+    if (w == 15u) {
+        /* the shared gate from the fp64 sum; the exact route finish
+         * overwrites it when the selection is not certified */
+        const double sh_a = bound[2u * experts];
+        if (lane == 0u) *shared_scale = 1.0f / (1.0f + fast_expf(-(float)sh_a));
+    }
+    const double ar = live ? bound[2u * e] : ninf;
+    const double b = live ? bound[2u * e + 1u] : 0.0;
+    /* a NaN total comes with an infinite bound; keep it out of the maxima */
+    const double a = ar == ar ? ar : ninf;
+    const float key = (float)a;
+    const uint32_t need = top_k + 1u < experts ? top_k + 1u : experts;
+    const uint32_t ns = experts >= 64u ? experts / 64u : 1u;
+    const uint32_t per = (need + ns - 1u) / ns;
+    if (e == 0u) s_count = 0u;
+    /* 1. */
+    {
+        float m = __builtin_inff();
+        if (w < ns) {
+            float v = key;
+            for (uint32_t r = 0; r < per; ++r) {
+                m = wave_max(v);
+                const uint64_t hit = __ballot(v == m);
+                if (lane == (uint32_t)__builtin_ctzll(hit)) v = -__builtin_inff();
+            }
+        }
+        if (lane == 0u) w_key[w] = m;
+    }
+    __syncthreads();
+    /* 2. */
+    float t = w_key[0];
+#pragma unroll
+    for (uint32_t k = 1; k < 16u; ++k) t = fminf(t, w_key[k]);
+    /* 3. */
+    {
+        const bool c = live && key >= t;
+        const uint64_t cb = __ballot(c);
+        uint32_t at = 0;
+        if (lane == 0u) at = atomicAdd(&s_count, (uint32_t)__popcll(cb));
+        at = __builtin_amdgcn_readfirstlane(at) + bits_below(cb);
+        if (c && at < kCertCand) {
+            cmp[at] = CertCand{a, e, 0u};
+            cmp_b[at] = b;
+        }
+        const double rest_w = kq_wave_max_f64(live && !c ? a + b : ninf);
+        const bool bad_w = __ballot(live && !(b < __builtin_inf())) != 0ull;
+        if (lane == 0u) {
+            w_rest[w] = rest_w;
+            w_bad[w] = bad_w ? 1u : 0u;
+        }
+    }
+    __syncthreads();
+    if (w != 0u) return;
+    /* 4. */
+    const uint32_t total = s_count;
+    double rest = w_rest[0];
+    uint32_t anybad = w_bad[0];
+#pragma unroll
+    for (uint32_t k = 1; k < 16u; ++k) {
+        rest = fmax(rest, w_rest[k]);
+        anybad |= w_bad[k];
+    }
+    if (anybad != 0u || total > kCertCand || !(sh_b < __builtin_inf())) {
+        if (lane == 0u) *certified = 0u;
+        return;
+    }
+    /* places past the list hold entries that never rank above a candidate */
+    if (lane >= total) {
+        cmp[lane] = CertCand{ninf, 0xffffffffu, 0u};
+        cmp_b[lane] = 0.0;
+    }
+    const CertCand mine = cmp[lane];
+    const double mb = cmp_b[lane];
+    uint32_t rank = 0;
+    for (uint32_t j0 = 0; j0 < total; j0 += 8u) {
+        CertCand o[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8u; ++q) o[q] = cmp[(j0 + q) & (kCertCand - 1u)];
+#pragma unroll
+        for (uint32_t q = 0; q < 8u; ++q)
+            rank += (uint32_t)(o[q].a > mine.a) |
+                    ((uint32_t)(o[q].a == mine.a) & (uint32_t)(o[q].id < mine.id));
+    }
+    const bool have = lane < total;
+    if (have) {
+        srt[rank] = mine;
+        srt_b[rank] = mb;
+    }
+    rest = fmax(rest, kq_wave_max_f64(have && rank >= top_k ? mine.a + mb : ninf));
+    /* 5. adjacent selected pairs, then the last selected against the rest */
+    const uint32_t l1 = lane + 1u < top_k ? lane + 1u : 0u;
+    const CertCand s0 = srt[lane], s1 = srt[l1];
+    const double b0 = srt_b[lane], b1 = srt_b[l1];
+    const double m = kq_readlane_f64(s0.a, 0);
+    const bool pair_ok = lane + 1u >= top_k || certify_sep(s0.a, b0, s1.a, b1, m);
+    bool ok = __ballot(!pair_ok) == 0ull;
+    if (ok && rest > ninf)
+        ok = certify_sep(kq_readlane_f64(s0.a, (int)(top_k - 1u)),
+                         kq_readlane_f64(b0, (int)(top_k - 1u)), rest, 0.0, m);
+    if (lane == 0u) *certified = ok ? 1u : 0u;
+    if (!ok) return; /* the exact kernels run */
+    /* 6. weights p_r / sum of the selected p, p = exp(a - m) (the softmax
+     * denominator cancels); ascending-id rank of each slot */
+    const float ex = lane < top_k ? fast_expf((float)(s0.a - m)) : 0.0f;
+    const float psel = wave_sum_f32(ex);
+    uint32_t rk = 0;
+    for (uint32_t j = 0; j < top_k; ++j)
+        rk += (uint32_t)((uint32_t)__builtin_amdgcn_readlane((int)s0.id, (int)j) < s0.id);
+    if (lane < top_k) {
+        ids[lane] = s0.id;
+        weights[lane] = ex / psel;
+        order[rk] = lane;
+    }
+}
+
+/*
+ * Bounds of all logit rows (the shared gate vector as row E).
+ * Wave w of a workgroup takes quarter w % 4 of row 4 * blockIdx.x + w / 4;
+ * its lanes hold C consecutive columns each, so the wave's partial sums are
+ * the lane's own running sum plus a wave scan, and the row's are those plus
+ * the totals of the quarters before it.
+ */
+template <uint32_t HIDDEN>
+__global__ __launch_bounds__(1024) void router_bounds(
+    const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
+    const float *__restrict__ x, uint32_t experts, double *__restrict__ bound) {
+    constexpr uint32_t PART = HIDDEN / kSelParts;
+    constexpr uint32_t C = PART / 64u; /* 1 .. 8 */
+    __shared__ double p_tot[16], p_abs[16];
+    __shared__ uint32_t p_bad[16];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t part = w % kSelParts;
+    const uint32_t row = blockIdx.x * kSelRows + w / kSelParts;
+    const bool have = row <= experts; /* uniform over the wave */
+    float pr[C];
+    double incl = 0.0;
+    if (have) {
+        const float *wr = (row < experts ? router + (size_t)row * HIDDEN : shared_gate_weight) +
+                          part * PART + lane * C;
+        const float *xr = x + part * PART + lane * C;
+        float wv[C], xv[C];
+        if constexpr (C % 4u == 0u) {
+#pragma unroll
+            for (uint32_t q = 0; q < C / 4u; ++q) {
+                const float4 a = ((const float4 *)wr)[q], b = ((const float4 *)xr)[q];
+                wv[4u * q] = a.x, wv[4u * q + 1u] = a.y, wv[4u * q + 2u] = a.z, wv[4u * q + 3u] = a.w;
+                xv[4u * q] = b.x, xv[4u * q + 1u] = b.y, xv[4u * q + 2u] = b.z, xv[4u * q + 3u] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < C; ++i) {
+                wv[i] = wr[i];
+                xv[i] = xr[i];
+            }
+        }
+        bool bad = false;
+        double run = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < C; ++i) {
+            pr[i] = wv[i] * xv[i];
+            bad |= !kq_isfinite(pr[i]); /* also NaN or infinite w or x */
+            run += (double)pr[i];
+        }
+        incl = kq_wave_scan_f64(run);
+        const bool any_bad = __ballot(bad) != 0ull;
+        if (lane == 63u) {
+            p_tot[w] = incl;
+            p_bad[w] = any_bad ? 1u : 0u;
+        }
+    }
+    __syncthreads();
+    if (have) {
+        /* S_i of this lane's columns: earlier quarters, earlier lanes, then
+         * the lane's own products */
+        double s = kq_wave_shr1_f64(incl);
+        for (uint32_t q = 0; q < part; ++q) s += p_tot[w - part + q];
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (uint32_t i = 0; i < C; ++i) {
+            s += (double)pr[i];
+            s4[i & 3u] += fabs(s);
+        }
+        const double sabs = kq_wave_sum_f64((s4[0] + s4[1]) + (s4[2] + s4[3]));
+        if (lane == 0u) p_abs[w] = sabs;
+    }
+    __syncthreads();
+    /* thread 0 writes the workgroup's rows */
+    if (threadIdx.x == 0u) {
+        for (uint32_t r = 0; r < kSelRows; ++r) {
+            const uint32_t rr = blockIdx.x * kSelRows + r;
+            if (rr > experts) break;
+            double tot = 0.0, sab = 0.0;
+            uint32_t bad = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < kSelParts; ++q) {
+                tot += p_tot[r * kSelParts + q];
+                sab += p_abs[r * kSelParts + q];
+                bad |= p_bad[r * kSelParts + q];
+            }
+            bound[2u * rr] = tot;
+            /* partial sums near the binary32 range could overflow in the
+             * CPU's chain: only the exact path reports that */
+            bound[2u * rr + 1u] =
+                bad || !(sab < 0x1p126) ? __builtin_inf() : 1.001 * 0x1p-24 * sab;
+        }
+    }
+}
+
+/* ------------------------- route finish ------------------------- */
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     const uint32_t lane = threadIdx.x & 63u;
     return (uint32_t)__popcll(lane ? (m & (~0ull >> (64u - lane))) : 0ull);
@@ -439,7 +758,8 @@ __global__ __launch_bounds__(1024) void route_finish(
     const float *__restrict__ logits_all, const float *__restrict__ shared_logit,
     uint32_t experts, uint32_t top_k, float *__restrict__ probs_all, uint32_t *__restrict__ ids_all,
     float *__restrict__ weights_all, uint32_t *__restrict__ order_all,
-    float *__restrict__ shared_scale, uint32_t *status) {
+    float *__restrict__ shared_scale, uint32_t *status, const uint32_t *skip) {
+    if (skip != nullptr && *skip != 0u) return;
     __shared__ __align__(16) float ev[1024];
     __shared__ __align__(16) float wmx[16];
     __shared__ __align__(16) uint32_t wbad[16];
@@ -860,6 +1180,8 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)(d->experts + 1u) * 4u);                 /* offsets */
     b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
     b += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u); /* outp */
+    b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
+    b += 256u;                                                       /* certified */
     return b;
 }
 
@@ -880,7 +1202,9 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->offsets = (uint32_t *)p; p += align256((uint64_t)(d->experts + 1u) * 4u);
     ws->perm_tok = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->pos = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
-    ws->outp = (float *)p;
+    ws->outp = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u);
+    ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
+    ws->certified = (uint32_t *)p;
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
@@ -900,14 +1224,40 @@ extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
 extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
                                           const float *shared_gate_weight, const float *hidden,
                                           uint32_t tokens, const kq_launch_moe_ws *ws,
-                                          uint32_t *status, hipStream_t s) {
+                                          uint32_t *status, int certify, hipStream_t s) {
     const uint32_t ep = pad64(d->experts + 1u);
     const uint32_t groups = (d->experts + 1u + kRtRows - 1u) / kRtRows;
     bool fused = tokens == 1u;
+    /* one token, ids only needed exactly: try the certified selection first;
+     * the exact kernels below then return at once when it succeeded */
+    const uint32_t *skip = nullptr;
+    if (fused && certify && d->top_k <= kMaxTopK) {
+        const uint32_t bgroups = (d->experts + kSelRows) / kSelRows; /* E + 1 rows */
+#define KQ_ROUTER_BOUNDS(H)                                                                    \
+    hipLaunchKernelGGL(router_bounds<H>, dim3(bgroups), dim3(1024), 0, s, router,              \
+                       shared_gate_weight, hidden, d->experts, ws->bound)
+        bool have = true;
+        switch (d->hidden) {
+        case 256: KQ_ROUTER_BOUNDS(256u); break;
+        case 512: KQ_ROUTER_BOUNDS(512u); break;
+        case 1024: KQ_ROUTER_BOUNDS(1024u); break;
+        case 2048: KQ_ROUTER_BOUNDS(2048u); break;
+        default: have = false;
+        }
+#undef KQ_ROUTER_BOUNDS
+        if (have) {
+            hipLaunchKernelGGL(route_certify, dim3(1), dim3(1024), 0, s, ws->bound, d->experts,
+                               d->top_k, ws->ids, ws->weights, ws->order, ws->shared_scale,
+                               ws->certified);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            skip = ws->certified;
+        }
+    }
 #define KQ_ROUTER_DECODE(H)                                                                   \
     hipLaunchKernelGGL(router_decode<H>, dim3(groups), dim3(kThreads), 0, s, router,          \
                        shared_gate_weight, hidden, d->experts, ws->logits, ws->shared_logit, \
-                       status)
+                       status, skip)
     if (fused) {
         switch (d->hidden) {
         case 256: KQ_ROUTER_DECODE(256u); break;
@@ -942,7 +1292,7 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
     if (fin > 1024u) fin = 1024u;
     hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, ws->logits, ws->shared_logit,
                        d->experts, d->top_k, ws->probs, ws->ids, ws->weights, ws->order,
-                       ws->shared_scale, status);
+                       ws->shared_scale, status, skip);
     return hipGetLastError();
 }
 

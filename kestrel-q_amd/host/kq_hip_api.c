@@ -625,7 +625,8 @@ kq_status kq_hip_moe_route_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
     kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
-    e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, c->stream);
+    e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, 0,
+                            c->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(logits, ws.logits, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
                            c->stream);
@@ -691,8 +692,10 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
+    /* the layer needs the CPU's expert ids exactly and its weights to fp32
+     * tolerance: one token may take the certified routing */
     e = kq_launch_moe_route(&d, w->router, w->shared_gate_weight, hidden, (uint32_t)tokens, &ws,
-                            c->d_status, c->stream);
+                            c->d_status, 1, c->stream);
     /* several tokens: each expert's weights stream once for all of its
      * tokens (grouped MFMA path); one token: the fused decode kernels */
     if (e == hipSuccess && tokens >= KQ_GROUPED_MIN_TOKENS &&

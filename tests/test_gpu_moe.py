@@ -106,6 +106,19 @@ def test_routing_tie_heavy(ctx, pattern):
     assert_route_exact(got, oracle_route(H, E, K, router, x))
 
 
+def certified_flag(ctx, scratch, n):
+    # The one-token workspace ends with the certification word (its last
+    # 256-byte slot): 1 when the certified selection produced the ids.
+    return int(ctx.download(scratch.ptr + n - 256, np.uint32, 1)[0])
+
+
+def top_gaps(router, x, K):
+    # Gaps between consecutive logits among the K + 1 largest (fp64).
+    a = router.astype(np.float64) @ x.astype(np.float64)
+    top = np.sort(a)[::-1][:K + 1]
+    return -np.diff(top)
+
+
 class Layer:
     """MoE weights resident on the device plus their host copies."""
 
@@ -116,7 +129,7 @@ class Layer:
         self.cfg = kq_hip.MoeConfig(H, E, K, I, I)
         self.dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
 
-    def run(self, ctx, x):
+    def run(self, ctx, x, flag=False):
         T = x.shape[0]
         n = self.cfg.scratch_bytes(T)
         scratch, dx = ctx.alloc(n), ctx.upload(x)
@@ -124,9 +137,10 @@ class Layer:
         ctx.moe_execute(self.cfg, kq_hip.moe_weights(self.bufs), dx, T, dout, dids, scratch, n)
         out = ctx.download(dout, np.float32, T * self.H).reshape(T, self.H)
         ids = ctx.download(dids, np.uint32, T * self.K).reshape(T, self.K)
+        cert = certified_flag(ctx, scratch, n)
         for b in (scratch, dx, dout, dids):
             b.close()
-        return out, ids
+        return (out, ids, cert) if flag else (out, ids)
 
     def oracle(self, x):
         return kq_oracle.moe_execute(self.dims, {k: (t, self.w[k]) for k, t in ROLES.items()},
@@ -309,3 +323,94 @@ def test_moe_prefill_shapes(ctx, H, I, down_fmt):
                                     threads=oracle_threads())
     assert np.array_equal(ctx.download(dids, np.uint32, T * K).reshape(T, K), tr["selected_ids"])
     assert_close(out, ref)
+
+
+# ---------------- one-token execution: certified routing ----------------
+
+def test_moe_decode_many_tokens_ids_exact(ctx, layer):
+    # Each token alone: the expert ids come from the certified selection
+    # (exact product sums with a proven bound on the CPU's sequential sum)
+    # or, where the bound does not separate them, from the exact chains;
+    # either way they must be the CPU's ids, in the CPU's order.
+    # Logits ~N(0, 0.9) here carry bounds near 2e-4: tokens whose top
+    # gaps all exceed 1e-2 must take the certified selection.
+    xs = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 4242), 48 * 2048).reshape(48, 2048)
+    router = layer.w["router"].reshape(layer.E, layer.H)
+    wide = 0
+    for t in range(xs.shape[0]):
+        x = xs[t:t + 1]
+        out, ids, cert = layer.run(ctx, x, flag=True)
+        ref, tr = layer.oracle(x)
+        assert np.array_equal(ids, tr["selected_ids"]), t
+        assert_close(out, ref)
+        if top_gaps(router, x[0], layer.K).min() > 1e-2:
+            wide += 1
+            assert cert == 1, t
+    assert wide >= 8
+
+
+@pytest.mark.parametrize("H,E,K", [(512, 96, 6), (256, 40, 3), (1024, 130, 8), (512, 64, 12)])
+def test_moe_decode_certified_shapes(ctx, H, E, K):
+    # Expert counts off a multiple of 64 (a partial last wave), below 64, and
+    # a top-k that needs several keys per wave: ids and output match the
+    # CPU, and well separated logits take the certified selection.
+    I = 256
+    w = S.moe_weights(S.W_MOE + E, H, E, I, I)
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    n = cfg.scratch_bytes(1)
+    scratch, dout, dids = ctx.alloc(n), ctx.alloc(H * 4), ctx.alloc(K * 4)
+    router = w["router"].reshape(E, H)
+    xs = S.normal_f32(S.stream_key(S.W_MOE + E, S.R_HIDDEN), 6 * H).reshape(6, H)
+    wide = 0
+    for t in range(xs.shape[0]):
+        x = xs[t:t + 1]
+        dx = ctx.upload(x)
+        ctx.moe_execute(cfg, kq_hip.moe_weights(bufs), dx, 1, dout, dids, scratch, n)
+        cert = certified_flag(ctx, scratch, n)
+        ref, tr = kq_oracle.moe_execute(dims, {k: (r, w[k]) for k, r in ROLES.items()}, x,
+                                        trace=True)
+        assert np.array_equal(ctx.download(dids, np.uint32, K)[None, :], tr["selected_ids"]), t
+        assert_close(ctx.download(dout, np.float32, H)[None, :], ref)
+        if top_gaps(router, x[0], K).min() > 1e-3:
+            wide += 1
+            assert cert == 1, t
+        dx.close()
+    assert wide >= 2
+    for b in (scratch, dout, dids):
+        b.close()
+
+
+@pytest.mark.parametrize("pattern", ["zero-router", "duplicate-rows", "near-tie"])
+def test_moe_decode_ties_fall_back_to_exact_chains(ctx, pattern):
+    # Exactly tied or almost tied logits cannot be certified: the exact
+    # router and route finish must run and select as the CPU does.
+    H, E, K, I = 512, 64, 4, 256
+    w = S.moe_weights(S.W_MOE + 31, H, E, I, I)
+    rng = np.random.default_rng(7)
+    r = w["router"].reshape(E, H)
+    if pattern == "zero-router":
+        r[:] = 0.0
+    elif pattern == "duplicate-rows":
+        r[:] = r[rng.integers(0, 3, E)]
+    x = S.normal_f32(S.stream_key(S.W_MOE + 31, S.R_HIDDEN), H)[None, :]
+    if pattern == "near-tie":
+        # the last selected expert and the lowest-ranked one become copies
+        # differing by one ulp in a single weight: the pair straddles or sits
+        # on the selection boundary, closer than any bound can separate
+        order = np.argsort(-(r.astype(np.float64) @ x[0].astype(np.float64)), kind="stable")
+        j, m = order[K - 1], order[-1]
+        r[m] = r[j]
+        r[m, 17] = np.nextafter(r[j, 17], np.float32(np.inf))
+    w["router"] = np.ascontiguousarray(r.reshape(-1))
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    n = cfg.scratch_bytes(1)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(H * 4), ctx.alloc(K * 4)
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs), dx, 1, dout, dids, scratch, n)
+    assert certified_flag(ctx, scratch, n) == 0
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in ROLES.items()}, x, trace=True)
+    assert np.array_equal(ctx.download(dids, np.uint32, K)[None, :], tr["selected_ids"])
+    assert_close(ctx.download(dout, np.float32, H)[None, :], ref)
