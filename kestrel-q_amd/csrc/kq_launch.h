@@ -94,6 +94,7 @@ typedef struct kq_launch_moe_ws {
     double *bound;        /* [experts + 1][2]: exact product sums and the bound on the
                              CPU's sequential sum (certified one-token routing) */
     uint32_t *certified;  /* 1 when the certified routing produced the ids */
+    uint32_t *arrive;     /* workgroup arrivals of the one-launch exact route */
 } kq_launch_moe_ws;
 
 uint32_t kq_launch_moe_experts_padded(uint32_t experts);

@@ -91,42 +91,46 @@ __device__ __forceinline__ float4 as_f4(const uint4 u) {
                        __uint_as_float(u.w));
 }
 
+/* The chains of logit rows row0 .. row0 + 7 (the experts, then the shared
+ * gate vector as row E), computed by the workgroup's first kThreads
+ * threads; any further threads only take part in the barriers. */
 template <uint32_t HIDDEN>
-__global__ __launch_bounds__(kThreads) void router_decode(
+__device__ __forceinline__ void router_decode_rows(
     const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
     const float *__restrict__ x, uint32_t experts, float *__restrict__ logits,
-    float *__restrict__ shared_logit, uint32_t *status, const uint32_t *skip) {
-    /* the certified routing already produced the ids: nothing to do */
-    if (skip != nullptr && *skip != 0u) return;
+    float *__restrict__ shared_logit, uint32_t *status, uint32_t row0) {
     constexpr uint32_t NQ = HIDDEN / 4u;
     constexpr uint32_t NSEG = (NQ + kRtSegQ - 1u) / kRtSegQ;
     __shared__ float4 buf[NSEG * kRtSegQ * kRtPitch];
     const uint32_t tid = threadIdx.x;
-    const uint32_t row0 = blockIdx.x * kRtRows;
+    const bool active = tid < (uint32_t)kThreads; /* whole waves */
     /* thread covers column group ql of rows rsub + 2k (k < 4); rsub is
      * uniform across a wave, so each row's buffer descriptor is scalar.
      * Rows past the shared gate row get an empty buffer and columns past
      * the row's end lie outside it: the buffer loads return zeros. */
     const uint32_t ql = tid % kRtSegQ;
     const uint32_t rsub = __builtin_amdgcn_readfirstlane(tid / kRtSegQ);
-    KqBuf rb[kRtPerSeg];
-#pragma unroll
-    for (uint32_t k = 0; k < kRtPerSeg; ++k) {
-        const uint32_t e = row0 + rsub + 2u * k;
-        rb[k] = kq_buf(e < experts ? router + (size_t)e * HIDDEN : shared_gate_weight,
-                       e <= experts ? HIDDEN * 4u : 0u);
-    }
-    const KqBuf xb = kq_buf(x, HIDDEN * 4u);
     uint4 v[NSEG][kRtPerSeg], xr[NSEG];
+    if (active) {
+        KqBuf rb[kRtPerSeg];
 #pragma unroll
-    for (uint32_t sg = 0; sg < NSEG; ++sg) {
-        const uint32_t off = (sg * kRtSegQ + ql) * 16u;
-        xr[sg] = kq_ld128(xb, off, 0);
+        for (uint32_t k = 0; k < kRtPerSeg; ++k) {
+            const uint32_t e = row0 + rsub + 2u * k;
+            rb[k] = kq_buf(e < experts ? router + (size_t)e * HIDDEN : shared_gate_weight,
+                           e <= experts ? HIDDEN * 4u : 0u);
+        }
+        const KqBuf xb = kq_buf(x, HIDDEN * 4u);
 #pragma unroll
-        for (uint32_t k = 0; k < kRtPerSeg; ++k) v[sg][k] = kq_ld128(rb[k], off, 0);
+        for (uint32_t sg = 0; sg < NSEG; ++sg) {
+            const uint32_t off = (sg * kRtSegQ + ql) * 16u;
+            xr[sg] = kq_ld128(xb, off, 0);
+#pragma unroll
+            for (uint32_t k = 0; k < kRtPerSeg; ++k) v[sg][k] = kq_ld128(rb[k], off, 0);
+        }
     }
     bool bad = false;
     auto stage = [&](uint32_t sg) {
+        if (!active) return;
         float4 *b = buf + (sg * kRtSegQ + ql) * kRtPitch + rsub;
         const float4 xq = as_f4(xr[sg]);
 #pragma unroll
@@ -165,6 +169,15 @@ __global__ __launch_bounds__(kThreads) void router_decode(
             *shared_logit = acc;
     }
     if (bad) kq_flag(status, KQ_DEV_INPUT);
+}
+
+template <uint32_t HIDDEN>
+__global__ __launch_bounds__(kThreads) void router_decode(
+    const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
+    const float *__restrict__ x, uint32_t experts, float *__restrict__ logits,
+    float *__restrict__ shared_logit, uint32_t *status) {
+    router_decode_rows<HIDDEN>(router, shared_gate_weight, x, experts, logits, shared_logit,
+                               status, blockIdx.x * kRtRows);
 }
 
 /* ---------------------- router, several tokens ---------------------- */
@@ -574,7 +587,10 @@ __global__ __launch_bounds__(1024) void route_certify(
 template <uint32_t HIDDEN>
 __global__ __launch_bounds__(1024) void router_bounds(
     const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
-    const float *__restrict__ x, uint32_t experts, double *__restrict__ bound) {
+    const float *__restrict__ x, uint32_t experts, double *__restrict__ bound,
+    uint32_t *__restrict__ arrive) {
+    /* the exact fallback's arrival count starts each call at zero */
+    if (blockIdx.x == 0u && threadIdx.x == 0u) *arrive = 0u;
     constexpr uint32_t PART = HIDDEN / kSelParts;
     constexpr uint32_t C = PART / 64u; /* 1 .. 8 */
     __shared__ double p_tot[16], p_abs[16];
@@ -754,12 +770,11 @@ __device__ __forceinline__ void mask_counts(const uint64_t *msk, uint32_t w, uin
  * and the members e of T with c(e) <= k, less the |G n {c > k}| lowest ids
  * among them (c(e) <= k is e <= t0 for members, t0 being the member at
  * which the running count reaches k). */
-__global__ __launch_bounds__(1024) void route_finish(
-    const float *__restrict__ logits_all, const float *__restrict__ shared_logit,
+__device__ __forceinline__ void route_finish_body(
+    uint32_t t, const float *__restrict__ logits_all, const float *__restrict__ shared_logit,
     uint32_t experts, uint32_t top_k, float *__restrict__ probs_all, uint32_t *__restrict__ ids_all,
     float *__restrict__ weights_all, uint32_t *__restrict__ order_all,
-    float *__restrict__ shared_scale, uint32_t *status, const uint32_t *skip) {
-    if (skip != nullptr && *skip != 0u) return;
+    float *__restrict__ shared_scale, uint32_t *status) {
     __shared__ __align__(16) float ev[1024];
     __shared__ __align__(16) float wmx[16];
     __shared__ __align__(16) uint32_t wbad[16];
@@ -768,7 +783,7 @@ __global__ __launch_bounds__(1024) void route_finish(
     __shared__ __align__(16) float sel_p[64];
     __shared__ __align__(16) float sorted_p[64];
     __shared__ float s_sum, s_exk;
-    const uint32_t t = blockIdx.x, e = threadIdx.x;
+    const uint32_t e = threadIdx.x;
     const uint32_t lane = e & 63u, w = e >> 6, nw = blockDim.x >> 6;
     const uint32_t sum_wave = nw - 1u;
     const bool live = e < experts;
@@ -930,6 +945,50 @@ __global__ __launch_bounds__(1024) void route_finish(
         shared_scale[t] = kq_sigmoid(sl);
         if (!kq_isfinite(s) || !(s > 0.0f)) kq_flag(status, KQ_DEV_NUMERIC);
     }
+}
+
+__global__ __launch_bounds__(1024) void route_finish(
+    const float *__restrict__ logits_all, const float *__restrict__ shared_logit,
+    uint32_t experts, uint32_t top_k, float *__restrict__ probs_all, uint32_t *__restrict__ ids_all,
+    float *__restrict__ weights_all, uint32_t *__restrict__ order_all,
+    float *__restrict__ shared_scale, uint32_t *status) {
+    route_finish_body(blockIdx.x, logits_all, shared_logit, experts, top_k, probs_all, ids_all,
+                      weights_all, order_all, shared_scale, status);
+}
+
+/*
+ * The exact one-token route when the certified selection failed, as one
+ * launch: every workgroup runs the chains of 8 logit rows, and the
+ * workgroup that arrives last (arrive: zeroed by router_bounds earlier in
+ * the same call) runs the route finish over all of them. When the
+ * selection was certified every workgroup returns at once. The logits are
+ * written by wave 0 of each workgroup, which releases them before thread 0
+ * counts the workgroup in.
+ */
+template <uint32_t HIDDEN>
+__global__ __launch_bounds__(1024) void route_exact(
+    const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
+    const float *__restrict__ x, uint32_t experts, uint32_t top_k, float *logits,
+    float *shared_logit, float *__restrict__ probs, uint32_t *__restrict__ ids,
+    float *__restrict__ weights, uint32_t *__restrict__ order, float *__restrict__ shared_scale,
+    uint32_t *status, const uint32_t *__restrict__ certified, uint32_t *arrive) {
+    if (*certified != 0u) return;
+    __shared__ uint32_t s_last;
+    router_decode_rows<HIDDEN>(router, shared_gate_weight, x, experts, logits, shared_logit,
+                               status, blockIdx.x * kRtRows);
+    if (threadIdx.x < 64u) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        if (threadIdx.x == 0u) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = prev == gridDim.x - 1u ? 1u : 0u;
+        }
+    }
+    __syncthreads();
+    if (s_last == 0u) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    route_finish_body(0u, logits, shared_logit, experts, top_k, probs, ids, weights, order,
+                      shared_scale, status);
 }
 
 /* ---------------------- expert gate/up + SwiGLU ---------------------- */
@@ -1181,7 +1240,7 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
     b += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u); /* outp */
     b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
-    b += 256u;                                                       /* certified */
+    b += 256u;                                           /* certified flag, arrival count */
     return b;
 }
 
@@ -1205,6 +1264,7 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->outp = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u);
     ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
     ws->certified = (uint32_t *)p;
+    ws->arrive = (uint32_t *)p + 32; /* its own 128-byte line in the same slot */
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
@@ -1228,36 +1288,38 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
     const uint32_t ep = pad64(d->experts + 1u);
     const uint32_t groups = (d->experts + 1u + kRtRows - 1u) / kRtRows;
     bool fused = tokens == 1u;
-    /* one token, ids only needed exactly: try the certified selection first;
-     * the exact kernels below then return at once when it succeeded */
-    const uint32_t *skip = nullptr;
+    uint32_t fin = 64u * ((d->experts + 63u) / 64u + 1u);
+    if (fin > 1024u) fin = 1024u;
+    /* one token, ids only needed exactly: the certified selection, then the
+     * exact route as one launch that returns at once when it succeeded */
     if (fused && certify && d->top_k <= kMaxTopK) {
         const uint32_t bgroups = (d->experts + kSelRows) / kSelRows; /* E + 1 rows */
-#define KQ_ROUTER_BOUNDS(H)                                                                    \
+        const uint32_t xthreads = fin > (uint32_t)kThreads ? fin : (uint32_t)kThreads;
+#define KQ_CERTIFIED_ROUTE(H)                                                                  \
     hipLaunchKernelGGL(router_bounds<H>, dim3(bgroups), dim3(1024), 0, s, router,              \
-                       shared_gate_weight, hidden, d->experts, ws->bound)
+                       shared_gate_weight, hidden, d->experts, ws->bound, ws->arrive);         \
+    hipLaunchKernelGGL(route_certify, dim3(1), dim3(1024), 0, s, ws->bound, d->experts,        \
+                       d->top_k, ws->ids, ws->weights, ws->order, ws->shared_scale,            \
+                       ws->certified);                                                         \
+    hipLaunchKernelGGL(route_exact<H>, dim3(groups), dim3(xthreads), 0, s, router,             \
+                       shared_gate_weight, hidden, d->experts, d->top_k, ws->logits,           \
+                       ws->shared_logit, ws->probs, ws->ids, ws->weights, ws->order,           \
+                       ws->shared_scale, status, ws->certified, ws->arrive)
         bool have = true;
         switch (d->hidden) {
-        case 256: KQ_ROUTER_BOUNDS(256u); break;
-        case 512: KQ_ROUTER_BOUNDS(512u); break;
-        case 1024: KQ_ROUTER_BOUNDS(1024u); break;
-        case 2048: KQ_ROUTER_BOUNDS(2048u); break;
+        case 256: KQ_CERTIFIED_ROUTE(256u); break;
+        case 512: KQ_CERTIFIED_ROUTE(512u); break;
+        case 1024: KQ_CERTIFIED_ROUTE(1024u); break;
+        case 2048: KQ_CERTIFIED_ROUTE(2048u); break;
         default: have = false;
         }
-#undef KQ_ROUTER_BOUNDS
-        if (have) {
-            hipLaunchKernelGGL(route_certify, dim3(1), dim3(1024), 0, s, ws->bound, d->experts,
-                               d->top_k, ws->ids, ws->weights, ws->order, ws->shared_scale,
-                               ws->certified);
-            const hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            skip = ws->certified;
-        }
+#undef KQ_CERTIFIED_ROUTE
+        if (have) return hipGetLastError();
     }
 #define KQ_ROUTER_DECODE(H)                                                                   \
     hipLaunchKernelGGL(router_decode<H>, dim3(groups), dim3(kThreads), 0, s, router,          \
                        shared_gate_weight, hidden, d->experts, ws->logits, ws->shared_logit, \
-                       status, skip)
+                       status)
     if (fused) {
         switch (d->hidden) {
         case 256: KQ_ROUTER_DECODE(256u); break;
@@ -1288,11 +1350,9 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    uint32_t fin = 64u * ((d->experts + 63u) / 64u + 1u);
-    if (fin > 1024u) fin = 1024u;
     hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, ws->logits, ws->shared_logit,
                        d->experts, d->top_k, ws->probs, ws->ids, ws->weights, ws->order,
-                       ws->shared_scale, status, skip);
+                       ws->shared_scale, status);
     return hipGetLastError();
 }
 
