@@ -145,11 +145,13 @@ def replicas(ctx, host: np.ndarray, want_bytes: int, cap: int = 256):
 
 
 # ---------------------------------------------------------------- workloads
-def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph):
+def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph, warm=False):
+    """warm: one weight copy, re-read every step from the caches (a
+    single-call latency with a warm cache, not an HBM rate)."""
     t = kq_hip.TYPE_IDS[fmt]
     w = S.quant_matrix(fmt, S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT), rows, cols)
     x = S.normal_f32(S.stream_key(S.W_MATVEC_Q4K, S.R_X), batch * cols)
-    reps = replicas(ctx, w, MALL_DEFEAT_BYTES)
+    reps = replicas(ctx, w, 0 if warm else MALL_DEFEAT_BYTES, cap=1 if warm else 256)
     dx, dy = ctx.upload(x), ctx.alloc(rows * batch * 4)
     ms = time_steps(ctx, lambda i: ctx.matvec(t, reps[i % len(reps)], rows, cols, dx, batch, dy),
                     warmup, steps, graph)
@@ -347,7 +349,13 @@ def main() -> int:
         run(HEADLINE, lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph))
         run("q8_0_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q8_0", 4096, 2048, 1, W, K, graph))
         run("q6k_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q6_K", 4096, 2048, 1, W, K, graph))
-        for f in ("Q4_K", "Q8_0", "Q6_K"):
+        run("q5k_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q5_K", 4096, 2048, 1, W, K, graph))
+        run("q5_1_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q5_1", 4096, 2048, 1, W, K, graph))
+        run("iq4_nl_matvec_4096x2048_b1",
+            lambda: wl_matvec(ctx, "IQ4_NL", 4096, 2048, 1, W, K, graph))
+        run("q4k_matvec_4096x2048_b1_warm_cache",
+            lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph, warm=True))
+        for f in ("Q4_K", "Q8_0", "Q6_K", "Q5_K", "Q5_1", "IQ4_NL"):
             run(f"dequant_64m_{f.lower()}",
                 lambda f=f: wl_dequant(ctx, f, 3, max(5, K // 20), graph))
         cache = {}

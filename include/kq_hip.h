@@ -36,9 +36,13 @@ extern "C" {
 
 /* GGUF tensor type ids (include/kq_gguf.h:15-23; Q6_K = 14, the GGML id). */
 #define KQ_HIP_TYPE_F32 0U
+#define KQ_HIP_TYPE_Q5_1 7U
 #define KQ_HIP_TYPE_Q8_0 8U
 #define KQ_HIP_TYPE_Q4_K 12U
+#define KQ_HIP_TYPE_Q5_K 13U
 #define KQ_HIP_TYPE_Q6_K 14U
+#define KQ_HIP_TYPE_IQ4_NL 20U
+#define KQ_HIP_TYPE_BF16 30U
 
 typedef struct kq_hip_context kq_hip_context;
 

@@ -17,9 +17,13 @@ extern "C" {
 #endif
 
 #define KQ_LAUNCH_F32 0u
+#define KQ_LAUNCH_Q5_1 7u
 #define KQ_LAUNCH_Q8_0 8u
 #define KQ_LAUNCH_Q4_K 12u
+#define KQ_LAUNCH_Q5_K 13u
 #define KQ_LAUNCH_Q6_K 14u
+#define KQ_LAUNCH_IQ4_NL 20u
+#define KQ_LAUNCH_BF16 30u
 
 /* dequant (kq_dequant.hip) */
 hipError_t kq_launch_dequant(uint32_t type, const void *packed, uint64_t blocks,

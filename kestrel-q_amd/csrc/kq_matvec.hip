@@ -1,6 +1,6 @@
 /*
  * kq_matvec.hip — dequant-fused matrix-vector products y = W x for GGUF
- * Q4_K, Q6_K and Q8_0 rows (batch 1..4, fp32 activations and outputs) and
+ * Q4_K, Q5_K, Q6_K, Q8_0, Q5_1 and IQ4_NL rows (batch 1..4, fp32 activations and outputs) and
  * greedy argmax over the results.
  *
  * Restates the row loop of kq_weight_provider_linear_f32
@@ -247,11 +247,13 @@ hipError_t launch_cols(uint32_t cols, const uint8_t *W, uint32_t rows, const flo
     case 32:
     case 64:
     case 128:
-        /* short rows exist only for 32-element Q8_0 blocks */
-        if (TYPE != KQ_LAUNCH_Q8_0) break;
-        if (cols == 32) return launch_one<KQ_LAUNCH_Q8_0, 32u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-        if (cols == 64) return launch_one<KQ_LAUNCH_Q8_0, 64u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-        return launch_one<KQ_LAUNCH_Q8_0, 128u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+        /* short rows exist only for 32-element blocks */
+        if constexpr (kq::small_block<TYPE>()) {
+            if (cols == 32) return launch_one<TYPE, 32u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+            if (cols == 64) return launch_one<TYPE, 64u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+            return launch_one<TYPE, 128u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+        }
+        break;
     case 256: return launch_one<TYPE, 256u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
     case 512: return launch_one<TYPE, 512u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
     case 1024: return launch_one<TYPE, 1024u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
@@ -272,6 +274,12 @@ hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t row
         return launch_cols<KQ_LAUNCH_Q6_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
     case KQ_LAUNCH_Q8_0:
         return launch_cols<KQ_LAUNCH_Q8_0, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+    case KQ_LAUNCH_Q5_K:
+        return launch_cols<KQ_LAUNCH_Q5_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+    case KQ_LAUNCH_Q5_1:
+        return launch_cols<KQ_LAUNCH_Q5_1, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+    case KQ_LAUNCH_IQ4_NL:
+        return launch_cols<KQ_LAUNCH_IQ4_NL, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
     default: return hipErrorInvalidValue;
     }
 }
@@ -293,8 +301,10 @@ hipError_t dispatch(uint32_t type, const void *W, uint32_t rows, uint32_t cols, 
 
 extern "C" int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t batch) {
     if (batch < 1u || batch > 4u) return 0;
-    if (type != KQ_LAUNCH_Q4_K && type != KQ_LAUNCH_Q6_K && type != KQ_LAUNCH_Q8_0) return 0;
-    if (type == KQ_LAUNCH_Q8_0 && (cols == 32u || cols == 64u || cols == 128u)) return 1;
+    const bool small = type == KQ_LAUNCH_Q8_0 || type == KQ_LAUNCH_Q5_1 || type == KQ_LAUNCH_IQ4_NL;
+    const bool kquant = type == KQ_LAUNCH_Q4_K || type == KQ_LAUNCH_Q5_K || type == KQ_LAUNCH_Q6_K;
+    if (!small && !kquant) return 0;
+    if (small && (cols == 32u || cols == 64u || cols == 128u)) return 1;
     return cols == 256u || cols == 512u || cols == 1024u || cols == 2048u;
 }
 

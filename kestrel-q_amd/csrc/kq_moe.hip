@@ -1216,7 +1216,8 @@ hipError_t down_cols(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w
 }
 
 bool quant_type(uint32_t t) {
-    return t == KQ_LAUNCH_Q4_K || t == KQ_LAUNCH_Q6_K || t == KQ_LAUNCH_Q8_0;
+    return t == KQ_LAUNCH_Q4_K || t == KQ_LAUNCH_Q5_K || t == KQ_LAUNCH_Q6_K ||
+           t == KQ_LAUNCH_Q8_0 || t == KQ_LAUNCH_Q5_1 || t == KQ_LAUNCH_IQ4_NL;
 }
 
 bool cols_ok(uint32_t c) { return c == 256u || c == 512u || c == 1024u || c == 2048u; }
@@ -1372,6 +1373,15 @@ extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
     case KQ_LAUNCH_Q8_0:
         e = gateup_cols<KQ_LAUNCH_Q8_0>(d, w, hidden, tokens, ws, act_stride, status, s);
         break;
+    case KQ_LAUNCH_Q5_K:
+        e = gateup_cols<KQ_LAUNCH_Q5_K>(d, w, hidden, tokens, ws, act_stride, status, s);
+        break;
+    case KQ_LAUNCH_Q5_1:
+        e = gateup_cols<KQ_LAUNCH_Q5_1>(d, w, hidden, tokens, ws, act_stride, status, s);
+        break;
+    case KQ_LAUNCH_IQ4_NL:
+        e = gateup_cols<KQ_LAUNCH_IQ4_NL>(d, w, hidden, tokens, ws, act_stride, status, s);
+        break;
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
@@ -1379,6 +1389,9 @@ extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
     case KQ_LAUNCH_Q4_K: return down_cols<KQ_LAUNCH_Q4_K>(d, w, tokens, ws, act_stride, out, status, s);
     case KQ_LAUNCH_Q6_K: return down_cols<KQ_LAUNCH_Q6_K>(d, w, tokens, ws, act_stride, out, status, s);
     case KQ_LAUNCH_Q8_0: return down_cols<KQ_LAUNCH_Q8_0>(d, w, tokens, ws, act_stride, out, status, s);
+    case KQ_LAUNCH_Q5_K: return down_cols<KQ_LAUNCH_Q5_K>(d, w, tokens, ws, act_stride, out, status, s);
+    case KQ_LAUNCH_Q5_1: return down_cols<KQ_LAUNCH_Q5_1>(d, w, tokens, ws, act_stride, out, status, s);
+    case KQ_LAUNCH_IQ4_NL: return down_cols<KQ_LAUNCH_IQ4_NL>(d, w, tokens, ws, act_stride, out, status, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -6,7 +6,8 @@
  * and holds the matching activations for batch columns 0..B-1 in registers
  * (load_x), streams its slice of every row it visits (load) and returns
  * its partial dot (dot). The decode of each format follows
- * src/kq_numeric.c:176-295 (Q8_0, Q4_K) and the GGML Q6_K layout; the
+ * src/kq_numeric.c:176-295 (Q8_0, Q4_K, Q5_1, Q5_K, IQ4_NL) and the GGML
+ * Q6_K layout; the
  * per-sub-block scale is applied once to a sum of code*x products, and the
  * block offset (Q4_K dmin*m, Q6_K -32, Q8_0 +128 bias) is taken off with a
  * precomputed activation sum. Codes are converted with one
@@ -332,6 +333,271 @@ struct LaneQ8 {
     }
 };
 
+/* ---------------- Q5_K: 176 B blocks of 256 ---------------- */
+/* The Q4_K layout with a fifth code bit: d, dmin, 12 scale bytes @0,
+ * qh[32] @16, qs[128] @48 (src/kq_numeric.c:223-277). Code i of sub-block
+ * pair g is the nibble of qs[32g + i] plus 16 when bit 2g (low nibble) or
+ * 2g+1 (high nibble) of qh[i] is set; the lane mapping is LaneQ4K's, and a
+ * lane's 16 qs bytes pair with qh bytes 16h .. 16h+15. */
+template <int B>
+struct LaneQ5K {
+    static constexpr uint32_t kBlockBytes = 176u;
+    struct Raw {
+        uint4 hd, qh, qs;
+    };
+    uint32_t off, qoff, hoff;
+    uint32_t gq, k0;
+    float xl[B][16], xh[B][16], sxl[B], sxh[B];
+
+    __device__ __forceinline__ void setup(uint32_t l) {
+        const uint32_t bb = l >> 3, c = l & 7u, h = c & 1u;
+        gq = c >> 1;
+        off = kBlockBytes * bb;
+        qoff = 48u + 32u * gq + 16u * h;
+        hoff = 16u + 16u * h;
+        k0 = 256u * bb + 64u * gq + 16u * h;
+    }
+    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        float t0[B][8], t1[B][8], s0[B], s1[B];
+        bool bad = load_x8<B>(x, stride, k0, t0);
+        bad |= load_x8<B>(x, stride, k0 + 8u, t1);
+        sum8<B>(t0, s0);
+        sum8<B>(t1, s1);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { xl[b][i] = t0[b][i]; xl[b][8 + i] = t1[b][i]; }
+            sxl[b] = s0[b] + s1[b];
+        }
+        bad |= load_x8<B>(x, stride, k0 + 32u, t0);
+        bad |= load_x8<B>(x, stride, k0 + 40u, t1);
+        sum8<B>(t0, s0);
+        sum8<B>(t1, s1);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { xh[b][i] = t0[b][i]; xh[b][8 + i] = t1[b][i]; }
+            sxh[b] = s0[b] + s1[b];
+        }
+        return bad;
+    }
+    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+        Raw r;
+        r.hd = kq_ld128(b, row_off + off, 0u);
+        r.qh = kq_ld128(b, row_off + off + hoff, 0u);
+        r.qs = kq_ld128(b, row_off + off + qoff, 0u);
+        return r;
+    }
+    __device__ __forceinline__ Raw zero() const {
+        Raw r;
+        r.hd = r.qh = r.qs = make_uint4(0, 0, 0, 0);
+        return r;
+    }
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const float d = kq_f16_to_f32_hw(r.hd.x);
+        const float dmin = kq_f16_to_f32_hw(r.hd.x >> 16);
+        malformed |= !kq_isfinite(d) || !kq_isfinite(dmin);
+        uint32_t s0, m0, s1, m1;
+        kq_k_scale_pair(gq, r.hd.y, r.hd.z, r.hd.w, &s0, &m0, &s1, &m1);
+        const float dl = d * (float)s0, ml = dmin * (float)m0;
+        const float dh = d * (float)s1, mh = dmin * (float)m1;
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        const uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        const uint32_t bl = 2u * gq;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lo[w] = kq_and_0f(q[w]) | (((h[w] >> bl) & 0x01010101u) << 4);
+            hi[w] = kq_and_0f(q[w] >> 4) | (((h[w] >> (bl + 1u)) & 0x01010101u) << 4);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                sl = dot4_u8(lo[w], &xl[b][4 * w], sl);
+                sh = dot4_u8(hi[w], &xh[b][4 * w], sh);
+            }
+            float v = dl * sl;
+            v = fmaf(-ml, sxl[b], v);
+            v = fmaf(dh, sh, v);
+            v = fmaf(-mh, sxh[b], v);
+            acc[b] = v;
+        }
+    }
+};
+
+/* bit j of the low 4 bits of n into bit 8j (bits 0, 8, 16, 24) */
+__device__ __forceinline__ uint32_t spread4(uint32_t n) {
+    return ((n & 15u) * 0x00204081u) & 0x01010101u;
+}
+
+/* ---------------- Q5_1: 24 B blocks of 32 ---------------- */
+/* f16 d @0, f16 m @2, qh (u32) @4, qs[16] @8 (src/kq_numeric.c:190-209):
+ * code i = nibble | (bit i of qh) << 4, the low nibbles of qs[0..15] being
+ * codes 0..15 and the high nibbles codes 16..31; weight = code * d + m. One
+ * lane per block; blocks lie at multiples of 8 bytes. */
+template <int B>
+struct LaneQ51 {
+    static constexpr uint32_t kBlockBytes = 24u;
+    struct Raw {
+        kq_u32x2 hdr;
+        uint4 qs;
+    };
+    uint32_t off, k0;
+    float xv[4][B][8], xsum[B];
+
+    __device__ __forceinline__ void setup(uint32_t l) {
+        off = kBlockBytes * l;
+        k0 = 32u * l;
+    }
+    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        bool bad = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(x, stride, k0 + 8u * q, xv[q]);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float a = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a += xv[q][b][i];
+            xsum[b] = a;
+        }
+        return bad;
+    }
+    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+        Raw r;
+        r.hdr = kq_ld64(b, row_off + off, 0u);
+        r.qs = kq_ld128(b, row_off + off + 8u, 0u);
+        return r;
+    }
+    __device__ __forceinline__ Raw zero() const {
+        Raw r;
+        r.hdr = kq_u32x2{0u, 0u};
+        r.qs = make_uint4(0, 0, 0, 0);
+        return r;
+    }
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const float d = kq_f16_to_f32_hw(r.hdr.x);
+        const float m = kq_f16_to_f32_hw(r.hdr.x >> 16);
+        malformed |= !kq_isfinite(d) || !kq_isfinite(m);
+        const uint32_t qh = r.hdr.y;
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lo[w] = kq_and_0f(q[w]) | (spread4(qh >> (4 * w)) << 4);
+            hi[w] = kq_and_0f(q[w] >> 4) | (spread4(qh >> (16 + 4 * w)) << 4);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                s = dot4_u8(lo[w], &xv[w >> 1][b][4 * (w & 1)], s);
+                s = dot4_u8(hi[w], &xv[2 + (w >> 1)][b][4 * (w & 1)], s);
+            }
+            acc[b] = fmaf(d, s, m * xsum[b]);
+        }
+    }
+};
+
+/* ---------------- IQ4_NL: 18 B blocks of 32 ---------------- */
+/* f16 d @0, qs[16] @2 (src/kq_numeric.c:278-292): weight = d * T[nibble],
+ * T the 16-entry non-linear table; low nibbles of qs[0..15] are weights
+ * 0..15, high nibbles 16..31. The lane looks codes up in T + 128 (unsigned
+ * bytes) with v_perm_b32 and takes the bias off with the activation sum.
+ * The block at bo (even) is read as a 16-byte window from bo - (bo & 3)
+ * plus two 16-bit loads of its bytes 14..17: no read passes the block's
+ * last byte, so the last block of a buffer stays inside it. */
+constexpr uint32_t kIq4T0 = 0x3f2d1801u; /* T + 128 for codes 0..3 */
+constexpr uint32_t kIq4T1 = 0x766a5d4fu; /* 4..7 */
+constexpr uint32_t kIq4T2 = 0xa6998d81u; /* 8..11 */
+constexpr uint32_t kIq4T3 = 0xf1d9c5b5u; /* 12..15 */
+
+/* four table bytes for the four nibbles (0..15) held in the bytes of n */
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t n, uint32_t t0, uint32_t t1,
+                                               uint32_t t2, uint32_t t3) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t a = __builtin_amdgcn_perm(t1, t0, sel);
+    const uint32_t b = __builtin_amdgcn_perm(t3, t2, sel);
+    const uint32_t msk = ((n >> 3) & 0x01010101u) * 0xffu;
+    return (a & ~msk) | (b & msk);
+}
+
+template <int B>
+struct LaneIQ4NL {
+    static constexpr uint32_t kBlockBytes = 18u;
+    struct Raw {
+        uint4 w;
+        uint32_t t0, t1, sh;
+    };
+    uint32_t off, k0;
+    float xv[4][B][8], xsum[B];
+
+    __device__ __forceinline__ void setup(uint32_t l) {
+        off = kBlockBytes * l;
+        k0 = 32u * l;
+    }
+    __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        bool bad = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(x, stride, k0 + 8u * q, xv[q]);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float a = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a += xv[q][b][i];
+            xsum[b] = a;
+        }
+        return bad;
+    }
+    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+        const uint32_t bo = row_off + off;
+        Raw r;
+        r.sh = bo & 3u;
+        r.w = kq_ld128(b, bo - r.sh, 0u);
+        r.t0 = kq_ld16(b, bo + 14u, 0u);
+        r.t1 = kq_ld16(b, bo + 16u, 0u);
+        return r;
+    }
+    __device__ __forceinline__ Raw zero() const {
+        Raw r;
+        r.w = make_uint4(0, 0, 0, 0);
+        r.t0 = r.t1 = 0u;
+        r.sh = 0u;
+        return r;
+    }
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const uint32_t w[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+        const float d = kq_f16_to_f32_hw(r.sh ? (w[0] >> 16) : w[0]);
+        malformed |= !kq_isfinite(d);
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            /* qs bytes 4k .. 4k+3, i.e. block bytes 2+4k .. 5+4k; the last
+             * dword is block bytes 14..17 */
+            const uint32_t q = k == 3 ? (r.t0 | (r.t1 << 16))
+                               : r.sh ? w[k + 1] : kq_align2(w[k + 1], w[k], 2u);
+            lo[k] = iq4_lookup(q & 0x0f0f0f0fu, kIq4T0, kIq4T1, kIq4T2, kIq4T3);
+            hi[k] = iq4_lookup((q >> 4) & 0x0f0f0f0fu, kIq4T0, kIq4T1, kIq4T2, kIq4T3);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                s = dot4_u8(lo[k], &xv[k >> 1][b][4 * (k & 1)], s);
+                s = dot4_u8(hi[k], &xv[2 + (k >> 1)][b][4 * (k & 1)], s);
+            }
+            acc[b] = d * fmaf(-128.0f, xsum[b], s);
+        }
+    }
+};
+
 template <uint32_t TYPE, int B>
 struct LaneFor;
 template <int B>
@@ -346,16 +612,36 @@ template <int B>
 struct LaneFor<8u, B> {
     using T = LaneQ8<B>;
 };
+template <int B>
+struct LaneFor<13u, B> {
+    using T = LaneQ5K<B>;
+};
+template <int B>
+struct LaneFor<7u, B> {
+    using T = LaneQ51<B>;
+};
+template <int B>
+struct LaneFor<20u, B> {
+    using T = LaneIQ4NL<B>;
+};
+
+/* 32-weight blocks (Q8_0, Q5_1, IQ4_NL): one lane per block; 256-weight
+ * K-quant blocks: eight lanes per block */
+template <uint32_t TYPE>
+__host__ __device__ constexpr bool small_block() {
+    return TYPE == 8u || TYPE == 7u || TYPE == 20u;
+}
 
 /* lanes per row for a format and column count */
 template <uint32_t TYPE>
 __host__ __device__ constexpr uint32_t lanes_per_row(uint32_t cols) {
-    return TYPE == 8u ? cols / 32u : (cols / 256u) * 8u;
+    return small_block<TYPE>() ? cols / 32u : (cols / 256u) * 8u;
 }
 
 template <uint32_t TYPE>
 __host__ __device__ constexpr uint32_t row_bytes(uint32_t cols) {
-    return TYPE == 8u ? (cols / 32u) * 34u : (cols / 256u) * (TYPE == 12u ? 144u : 210u);
+    return small_block<TYPE>() ? (cols / 32u) * LaneFor<TYPE, 1>::T::kBlockBytes
+                               : (cols / 256u) * LaneFor<TYPE, 1>::T::kBlockBytes;
 }
 
 /*

@@ -246,8 +246,12 @@ kq_status kq_hip_quant_geometry_for_type(uint32_t type_id, kq_hip_quant_geometry
     memset(g, 0, sizeof(*g));
     switch (type_id) {
     case KQ_HIP_TYPE_F32: g->block_elements = 1u; g->bytes_per_block = 4u; break;
+    case KQ_HIP_TYPE_BF16: g->block_elements = 1u; g->bytes_per_block = 2u; break;
+    case KQ_HIP_TYPE_Q5_1: g->block_elements = 32u; g->bytes_per_block = 24u; break;
     case KQ_HIP_TYPE_Q8_0: g->block_elements = 32u; g->bytes_per_block = 34u; break;
+    case KQ_HIP_TYPE_IQ4_NL: g->block_elements = 32u; g->bytes_per_block = 18u; break;
     case KQ_HIP_TYPE_Q4_K: g->block_elements = 256u; g->bytes_per_block = 144u; break;
+    case KQ_HIP_TYPE_Q5_K: g->block_elements = 256u; g->bytes_per_block = 176u; break;
     case KQ_HIP_TYPE_Q6_K: g->block_elements = 256u; g->bytes_per_block = 210u; break;
     default:
         return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
@@ -278,6 +282,7 @@ kq_status kq_hip_expert_member_span(uint32_t type_id, uint64_t rows, uint64_t co
                                     uint32_t expert_count, uint32_t expert_id,
                                     uint64_t *off, uint64_t *count, kq_diagnostic *diag) {
     uint64_t elements, bytes;
+    kq_hip_quant_geometry g;
     kq_status st;
     kq_diagnostic_clear(diag);
     if (off == NULL || count == NULL || rows == 0u || cols == 0u)
@@ -289,7 +294,9 @@ kq_status kq_hip_expert_member_span(uint32_t type_id, uint64_t rows, uint64_t co
         return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "member element count overflows");
     st = kq_hip_quant_packed_size(type_id, elements, &bytes, diag);
     if (st != KQ_STATUS_OK) return st;
-    if (cols % (type_id == KQ_HIP_TYPE_Q8_0 ? 32u : (type_id == KQ_HIP_TYPE_F32 ? 1u : 256u)) != 0u)
+    st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (cols % g.block_elements != 0u)
         return kq_fail(diag, KQ_STATUS_INVALID_QUANTIZED_GEOMETRY,
                        "member rows are not whole quant blocks");
     if (!u64_mul(bytes, expert_id, off))
@@ -298,17 +305,29 @@ kq_status kq_hip_expert_member_span(uint32_t type_id, uint64_t rows, uint64_t co
     return KQ_STATUS_OK;
 }
 
+/* every type with a geometry has a device decode; products need a packed
+ * quantized type */
 static kq_status quant_geometry(uint32_t type_id, uint64_t *be, uint64_t *bb,
                                 kq_diagnostic *diag) {
     kq_hip_quant_geometry g;
     kq_status st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
     if (st != KQ_STATUS_OK) return st;
-    if (type_id != KQ_HIP_TYPE_Q8_0 && type_id != KQ_HIP_TYPE_Q4_K && type_id != KQ_HIP_TYPE_Q6_K)
-        return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
-                       "device path supports Q8_0, Q4_K and Q6_K blocks");
     *be = g.block_elements;
     *bb = g.bytes_per_block;
     return KQ_STATUS_OK;
+}
+
+static int packed_quant(uint32_t type_id) {
+    return type_id != KQ_HIP_TYPE_F32 && type_id != KQ_HIP_TYPE_BF16;
+}
+
+/* base alignment the device decode needs: 16-byte block headers (K-quants
+ * whose blocks are multiples of 16 bytes), whole 32-bit words otherwise,
+ * 16-bit elements for BF16 */
+static uintptr_t packed_alignment(uint32_t type_id) {
+    if (type_id == KQ_HIP_TYPE_Q4_K || type_id == KQ_HIP_TYPE_Q5_K) return 16u;
+    if (type_id == KQ_HIP_TYPE_BF16) return 2u;
+    return 4u;
 }
 
 /* ------------------------------------------------------------------ */
@@ -337,9 +356,10 @@ kq_status kq_hip_dequantize_blocks_f32(kq_hip_context *c, uint32_t type_id, cons
         return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "decoded output capacity is too small");
     if (ranges_overlap(packed, packed_bytes, output, out_bytes))
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "packed input and decoded output overlap");
-    if (!aligned(packed, type_id == KQ_HIP_TYPE_Q4_K ? 16u : 4u) || !aligned(output, 16u))
+    if (!aligned(packed, packed_alignment(type_id)) || !aligned(output, 16u))
         return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT,
-                       "device buffers must be 16-byte (Q4_K) / 4-byte aligned, output 16-byte");
+                       "packed input must be 16-byte (Q4_K, Q5_K), 2-byte (BF16) or 4-byte "
+                       "aligned, output 16-byte");
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
     return finish(c, kq_launch_dequant(type_id, packed, blocks, output, c->d_status, c->stream),
@@ -376,6 +396,9 @@ static kq_status validate_matvec(const kq_hip_context *c, uint32_t type_id, cons
                        "weights, input, output and non-zero shape are required");
     st = quant_geometry(type_id, &be, &bb, diag);
     if (st != KQ_STATUS_OK) return st;
+    if (!packed_quant(type_id))
+        return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
+                       "device products take Q5_1, Q8_0, IQ4_NL, Q4_K, Q5_K or Q6_K weights");
     if (cols % be != 0u)
         return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH, "columns are not whole quant blocks");
     if (rows > UINT32_MAX || batch > 8u)
@@ -383,7 +406,7 @@ static kq_status validate_matvec(const kq_hip_context *c, uint32_t type_id, cons
     if (!kq_launch_matvec_supported(type_id, (uint32_t)cols, 1u))
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
                        "device matvec supports 256, 512, 1024 or 2048 columns "
-                       "(Q8_0 also 32, 64, 128)");
+                       "(32-weight formats also 32, 64, 128)");
     if (!u64_mul(rows, cols / be * bb, &w_bytes) || !u64_mul(rows, batch, &need))
         return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "matrix byte count overflows");
     /* the kernels address the matrix through one buffer descriptor, whose
@@ -683,7 +706,7 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     lw.shared_gate_weight = w->shared_gate_weight;
     if (!kq_launch_moe_supported(&d, &lw))
         return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
-                       "device MoE needs Q8_0/Q4_K/Q6_K roles (gate=up types, shared like routed), "
+                       "device MoE needs Q5_1/Q8_0/IQ4_NL/Q4_K/Q5_K/Q6_K roles (gate=up types, shared like routed), "
                        "hidden and intermediate in {256,512,1024,2048}, equal intermediates");
     if (!aligned(w->routed_gate, 16u) || !aligned(w->routed_up, 16u) ||
         !aligned(w->routed_down, 16u) || !aligned(w->shared_gate, 16u) ||

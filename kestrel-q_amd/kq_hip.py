@@ -21,8 +21,12 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("KQ_HIP_LIB", HERE / "_build" / "libkq_hip.so"))
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
-TYPE_IDS = {"F32": TYPE_F32, "Q8_0": TYPE_Q8_0, "Q4_K": TYPE_Q4_K, "Q6_K": TYPE_Q6_K}
-GEOMETRY = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210)}
+TYPE_Q5_1, TYPE_Q5_K, TYPE_IQ4_NL, TYPE_BF16 = 7, 13, 20, 30
+TYPE_IDS = {"F32": TYPE_F32, "Q8_0": TYPE_Q8_0, "Q4_K": TYPE_Q4_K, "Q6_K": TYPE_Q6_K,
+            "Q5_1": TYPE_Q5_1, "Q5_K": TYPE_Q5_K, "IQ4_NL": TYPE_IQ4_NL, "BF16": TYPE_BF16}
+GEOMETRY = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210),
+            TYPE_Q5_1: (32, 24), TYPE_Q5_K: (256, 176), TYPE_IQ4_NL: (32, 18),
+            TYPE_F32: (1, 4), TYPE_BF16: (1, 2)}
 
 STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "OUT_OF_MEMORY", 12: "UNSUPPORTED_TENSOR_TYPE",
           13: "ARITHMETIC_OVERFLOW", 14: "LIMIT_EXCEEDED", 15: "INVALID_ALIGNMENT",

@@ -10,6 +10,10 @@ CPU oracle always see identical bytes. Distributions:
   Q8_0 block (34 B):  d f16 ~U[1e-3, 2e-2], 32 int8 ~U{-127..127}
   Q6_K block (210 B): 128 B ql + 64 B qh random, 16 int8 sub-scales
                       ~U{-32..31}, d f16 ~U[1e-4, 2e-3]
+  Q5_K block (176 B): as Q4_K, plus 32 random qh bytes (the fifth code bits)
+  Q5_1 block (24 B):  d f16 ~U[1e-3, 2e-2], m f16 ~U[-1e-2, 1e-2], 4 random
+                      qh bytes, 16 random quant bytes
+  IQ4_NL block (18 B): d f16 ~U[1e-4, 2e-3], 16 random quant bytes
   activations:        N(mu, sigma) by Box-Muller in binary64, rounded to f32
 
 Uniform floats are drawn in binary32 and rounded to binary16 to nearest even.
@@ -30,6 +34,7 @@ R_WEIGHT, R_X, R_ROUTER, R_GATE, R_UP, R_DOWN, R_SHARED_GATE, R_SHARED_UP, \
     R_SHARED_DOWN, R_SHARED_GATE_W, R_HIDDEN = range(1, 12)
 
 Q4_K_BYTES, Q8_0_BYTES, Q6_K_BYTES = 144, 34, 210
+Q5_K_BYTES, Q5_1_BYTES, IQ4_NL_BYTES = 176, 24, 18
 
 
 def _mix(z: np.ndarray) -> np.ndarray:
@@ -119,9 +124,37 @@ def q6k_blocks(key: int, blocks: int) -> np.ndarray:
     return out
 
 
+def q5k_blocks(key: int, blocks: int) -> np.ndarray:
+    out = np.empty((blocks, Q5_K_BYTES), dtype=np.uint8)
+    out[:, 0:2] = _f16_bytes(uniform_f32(key ^ 1, blocks, 1e-3, 2e-2))
+    out[:, 2:4] = _f16_bytes(uniform_f32(key ^ 2, blocks, 0.0, 1e-2))
+    sm = uniform_int(key ^ 3, blocks * 16, 0, 63).reshape(blocks, 16)
+    out[:, 4:16] = pack_k_scales(sm[:, :8], sm[:, 8:])
+    out[:, 16:] = random_bytes(key ^ 4, blocks * 160).reshape(blocks, 160)
+    return out
+
+
+def q5_1_blocks(key: int, blocks: int) -> np.ndarray:
+    out = np.empty((blocks, Q5_1_BYTES), dtype=np.uint8)
+    out[:, 0:2] = _f16_bytes(uniform_f32(key ^ 1, blocks, 1e-3, 2e-2))
+    out[:, 2:4] = _f16_bytes(uniform_f32(key ^ 2, blocks, -1e-2, 1e-2))
+    out[:, 4:] = random_bytes(key ^ 3, blocks * 20).reshape(blocks, 20)
+    return out
+
+
+def iq4_nl_blocks(key: int, blocks: int) -> np.ndarray:
+    out = np.empty((blocks, IQ4_NL_BYTES), dtype=np.uint8)
+    out[:, 0:2] = _f16_bytes(uniform_f32(key ^ 1, blocks, 1e-4, 2e-3))
+    out[:, 2:] = random_bytes(key ^ 2, blocks * 16).reshape(blocks, 16)
+    return out
+
+
 BLOCK_GEN = {"Q4_K": (q4k_blocks, 256, Q4_K_BYTES),
              "Q8_0": (q8_0_blocks, 32, Q8_0_BYTES),
-             "Q6_K": (q6k_blocks, 256, Q6_K_BYTES)}
+             "Q6_K": (q6k_blocks, 256, Q6_K_BYTES),
+             "Q5_K": (q5k_blocks, 256, Q5_K_BYTES),
+             "Q5_1": (q5_1_blocks, 32, Q5_1_BYTES),
+             "IQ4_NL": (iq4_nl_blocks, 32, IQ4_NL_BYTES)}
 
 
 def quant_matrix(fmt: str, key: int, rows: int, cols: int) -> np.ndarray:

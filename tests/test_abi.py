@@ -6,7 +6,7 @@ from pathlib import Path
 
 import pytest
 
-from conftest import ROOT
+from conftest import ROOT, load_golden
 
 import kq_hip
 
@@ -42,13 +42,14 @@ def test_library_exports_every_declared_function():
 
 
 def test_geometry_matches_reference_table():
-    # src/kq_gguf.c:57-65 plus Q6_K (256, 210).
-    assert kq_hip.geometry(kq_hip.TYPE_Q8_0) == (32, 34)
-    assert kq_hip.geometry(kq_hip.TYPE_Q4_K) == (256, 144)
+    # src/kq_gguf.c:57-65 (the reference's fixture table) plus Q6_K (256, 210).
+    table = load_golden("numeric_vectors.json")["type_geometry"]
+    for name, g in table.items():
+        assert kq_hip.geometry(kq_hip.TYPE_IDS[name]) == (g["elements_per_block"],
+                                                          g["bytes_per_block"]), name
     assert kq_hip.geometry(kq_hip.TYPE_Q6_K) == (256, 210)
-    assert kq_hip.geometry(kq_hip.TYPE_F32) == (1, 4)
     with pytest.raises(kq_hip.KqError) as e:
-        kq_hip.geometry(7)  # Q5_1: not on the device path
+        kq_hip.geometry(2)  # Q4_0: no decode here
     assert e.value.name == "UNSUPPORTED_TENSOR_TYPE"
 
 

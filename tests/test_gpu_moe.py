@@ -177,24 +177,30 @@ def test_moe_repeated_calls_identical(ctx, layer):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and np.array_equal(ia, ib)
 
 
-def test_moe_small_formats(ctx):
-    # Q8_0 gate/up with Q4_K down at reduced dims.
+@pytest.mark.parametrize("gate_fmt,down_fmt,T", [("Q8_0", "Q4_K", 3), ("Q5_K", "Q5_1", 1),
+                                                  ("Q5_K", "Q5_1", 3), ("IQ4_NL", "Q8_0", 1),
+                                                  ("Q4_K", "IQ4_NL", 2), ("Q5_1", "Q5_K", 1)])
+def test_moe_small_formats(ctx, gate_fmt, down_fmt, T):
+    # Other gate/up and down formats at reduced dims, among them the
+    # reference model's own pair (Q5_K gate/up, Q5_1 routed down).
     H, E, K, I = 512, 32, 4, 256
-    w = S.moe_weights(S.W_MOE + 7, H, E, I, I, gate_fmt="Q8_0", down_fmt="Q4_K")
+    seed = S.W_MOE + 7 + kq_hip.TYPE_IDS[gate_fmt] * 64 + kq_hip.TYPE_IDS[down_fmt]
+    w = S.moe_weights(seed, H, E, I, I, gate_fmt=gate_fmt, down_fmt=down_fmt)
     bufs = {k: ctx.upload(v) for k, v in w.items()}
     cfg = kq_hip.MoeConfig(H, E, K, I, I)
-    x = S.normal_f32(S.stream_key(S.W_MOE + 7, S.R_HIDDEN), 3 * H).reshape(3, H)
-    n = cfg.scratch_bytes(3)
-    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(3 * H * 4), ctx.alloc(3 * K * 4)
-    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, kq_hip.TYPE_Q8_0, kq_hip.TYPE_Q4_K), dx, 3,
-                    dout, dids, scratch, n)
-    out = ctx.download(dout, np.float32, 3 * H).reshape(3, H)
-    roles = dict(ROLES, gate=kq_oracle.Q8_0, up=kq_oracle.Q8_0, shared_gate=kq_oracle.Q8_0,
-                 shared_up=kq_oracle.Q8_0, down=kq_oracle.Q4_K, shared_down=kq_oracle.Q4_K)
+    x = S.normal_f32(S.stream_key(seed, S.R_HIDDEN), T * H).reshape(T, H)
+    n = cfg.scratch_bytes(T)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(T * H * 4), ctx.alloc(T * K * 4)
+    gt, dt = kq_hip.TYPE_IDS[gate_fmt], kq_hip.TYPE_IDS[down_fmt]
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, gt, dt), dx, T, dout, dids, scratch, n)
+    out = ctx.download(dout, np.float32, T * H).reshape(T, H)
+    roles = dict(ROLES, gate=gt, up=gt, shared_gate=gt, shared_up=gt, down=dt, shared_down=dt)
     dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in roles.items()}, x, trace=True)
-    assert np.array_equal(ctx.download(dids, np.uint32, 3 * K).reshape(3, K), tr["selected_ids"])
+    assert np.array_equal(ctx.download(dids, np.uint32, T * K).reshape(T, K), tr["selected_ids"])
     assert_close(out, ref)
+    for b in list(bufs.values()) + [scratch, dx, dout, dids]:
+        b.close()
 
 
 def test_moe_fails_closed(ctx, layer):

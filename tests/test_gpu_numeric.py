@@ -18,7 +18,11 @@ pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 1e-3, 1e-4
 NUM = load_golden("numeric_vectors.json")
-FMTS = {"Q4_K": kq_hip.TYPE_Q4_K, "Q8_0": kq_hip.TYPE_Q8_0, "Q6_K": kq_hip.TYPE_Q6_K}
+FMTS = {"Q4_K": kq_hip.TYPE_Q4_K, "Q8_0": kq_hip.TYPE_Q8_0, "Q6_K": kq_hip.TYPE_Q6_K,
+        "Q5_K": kq_hip.TYPE_Q5_K, "Q5_1": kq_hip.TYPE_Q5_1, "IQ4_NL": kq_hip.TYPE_IQ4_NL}
+# decode-only element types (no device products)
+ELEM = {"F32": kq_hip.TYPE_F32, "BF16": kq_hip.TYPE_BF16}
+ALL_FMTS = sorted(FMTS)
 
 
 @pytest.fixture(scope="module")
@@ -45,16 +49,16 @@ def gpu_dequant(ctx, type_id, packed):
     return out
 
 
-@pytest.mark.parametrize("case", [c for c in NUM["cases"] if c["type"] in FMTS],
+@pytest.mark.parametrize("case", [c for c in NUM["cases"] if c["type"] in FMTS or c["type"] in ELEM],
                          ids=lambda c: c["id"])
 def test_dequant_golden_vectors(ctx, case):
     packed = np.frombuffer(bytes.fromhex(case["packed_hex"]), np.uint8).copy()
-    got = gpu_dequant(ctx, FMTS[case["type"]], packed)
+    got = gpu_dequant(ctx, {**FMTS, **ELEM}[case["type"]], packed)
     want = bits_f32(case["expected_f32_bits"])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+@pytest.mark.parametrize("fmt", ALL_FMTS)
 def test_dequant_64m_weights_bit_exact(ctx, fmt):
     # 67,108,864 weights per format, same seeded blocks as the oracle.
     gen, qk, bb = S.BLOCK_GEN[fmt]
@@ -149,13 +153,13 @@ def matvec_case(ctx, fmt, rows, cols, batch, key):
     return got, want
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+@pytest.mark.parametrize("fmt", ALL_FMTS)
 def test_matvec_4096x2048_batch1(ctx, fmt):
     got, want = matvec_case(ctx, fmt, 4096, 2048, 1, S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT))
     assert_close(got, want)
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+@pytest.mark.parametrize("fmt", ALL_FMTS)
 @pytest.mark.parametrize("rows,cols,batch", [(1, 256, 1), (7, 512, 2), (33, 1024, 3),
                                              (4097, 2048, 4), (5, 2048, 8), (300, 256, 4)])
 def test_matvec_shapes(ctx, fmt, rows, cols, batch):
@@ -164,10 +168,33 @@ def test_matvec_shapes(ctx, fmt, rows, cols, batch):
     assert_close(got, want)
 
 
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q5_1", "IQ4_NL"])
 @pytest.mark.parametrize("cols", [32, 64, 128])
-def test_matvec_q8_short_rows(ctx, cols):
-    got, want = matvec_case(ctx, "Q8_0", 130, cols, 2, S.stream_key(S.W_MATVEC_Q8_0, cols))
+def test_matvec_short_rows(ctx, fmt, cols):
+    # 32-weight formats: rows of one to four blocks
+    got, want = matvec_case(ctx, fmt, 130, cols, 2, S.stream_key(S.W_MATVEC_Q8_0, cols, FMTS[fmt]))
     assert_close(got, want)
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q5_1", "IQ4_NL"])
+@pytest.mark.parametrize("rows", [1, 3, 7])
+def test_matvec_last_block_of_buffer(ctx, fmt, rows):
+    # An odd number of 32-weight blocks: the buffer's last block ends off a
+    # dword boundary, where no load may reach past the buffer.
+    got, want = matvec_case(ctx, fmt, rows, 32, 1, S.stream_key(S.W_MATVEC_Q8_0, rows, FMTS[fmt]))
+    assert_close(got, want)
+
+
+@pytest.mark.parametrize("fmt", ["F32", "BF16"])
+def test_dequant_elements_bit_exact(ctx, fmt):
+    # element types decode to their own bits (F32) or bits << 16 (BF16),
+    # NaN and infinity patterns included
+    n = 1_000_003
+    raw = S.random_bytes(S.stream_key(S.W_DEQUANT, S.R_WEIGHT, ELEM[fmt]),
+                         n * (4 if fmt == "F32" else 2))
+    got = gpu_dequant(ctx, ELEM[fmt], raw)
+    want = kq_oracle.dequantize(ELEM[fmt], raw)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("case", [c for c in NUM["row_dot_cases"] if c["type"] in FMTS],
