@@ -236,13 +236,13 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache):
             "layer_replicas": nrep, "tokens": tokens}
 
 
-def wl_lm_head(ctx, batch, warmup, steps, graph):
-    V, H = 151936, 2048
-    w = S.quant_matrix("Q6_K", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT), V, H)
+def wl_lm_head(ctx, batch, warmup, steps, graph, fmt="Q6_K", V=151936, H=2048):
+    t = kq_hip.TYPE_IDS[fmt]
+    w = S.quant_matrix(fmt, S.stream_key(S.W_LM_HEAD, S.R_WEIGHT), V, H)
     h = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, batch), batch * H)
     reps = replicas(ctx, w, MALL_DEFEAT_BYTES + w.nbytes, cap=3)
     dh, dl, di = ctx.upload(h), ctx.alloc(V * batch * 4), ctx.alloc(batch * 4)
-    ms = time_steps(ctx, lambda i: ctx.lm_head(kq_hip.TYPE_Q6_K, reps[i % len(reps)], V, H, dh,
+    ms = time_steps(ctx, lambda i: ctx.lm_head(t, reps[i % len(reps)], V, H, dh,
                                                batch, dl, di), warmup, steps, graph)
     nbytes = w.nbytes + h.nbytes + V * batch * 4
     for b in reps + [dh, dl, di]:
@@ -362,6 +362,8 @@ def main() -> int:
         run("moe_decode_1tok", lambda: wl_moe(ctx, 1, W, K, graph, cache))
         run("lm_head_q6k_151936x2048_b1", lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph))
         run("lm_head_q6k_151936x2048_b4", lambda: wl_lm_head(ctx, 4, 3, max(10, K // 10), graph))
+        run("lm_head_q8_0_248320x2560_b1",
+            lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph, "Q8_0", 248320, 2560))
         run("moe_prefill_512", lambda: wl_moe(ctx, 512, 1, 3, graph, cache))
         if wanted == "hbm_copy_64mb":
             run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))

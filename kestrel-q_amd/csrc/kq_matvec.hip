@@ -44,11 +44,15 @@ __device__ __forceinline__ void wave_argmax(float &bv, uint32_t &bi) {
     }
 }
 
+/* One column segment of COLS columns: row r's segment starts at
+ * W + r * row_bytes, batch column b's activations at x + b * x_stride. With
+ * y_prev (which may be y itself) the segment's sums are added to the
+ * previous segments' ones, in segment order. */
 template <uint32_t TYPE, uint32_t COLS, int B, int RT>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(
-    const uint8_t *__restrict__ W, uint32_t rows, const float *__restrict__ x,
-    float *__restrict__ y, uint32_t *status, float *part_v, uint32_t *part_i,
-    uint32_t part_stride) {
+    const uint8_t *__restrict__ W, uint32_t rows, uint32_t row_bytes,
+    const float *__restrict__ x, uint32_t x_stride, float *y, const float *y_prev,
+    uint32_t *status, float *part_v, uint32_t *part_i, uint32_t part_stride) {
     using R = kq::Rows<TYPE, COLS, B, RT>;
     using Raw = typename R::Raw;
     const uint32_t lane = threadIdx.x & 63u;
@@ -62,15 +66,15 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
 
     typename R::Lane ln;
     ln.setup(l);
-    const KqBuf wb = kq_buf(W, rows * R::RB);
+    const KqBuf wb = kq_buf(W, (rows - 1u) * row_bytes + R::RB);
     Raw ra[RT], rb[RT];
     uint32_t g = wave;
     /* each lane loads its own activations (L2-resident after the first
      * waves) before the first group's weights: the loads complete in order,
      * so the activation sums are formed while the weights are in flight and
      * nothing waits on a workgroup barrier */
-    if (ln.load_x(x, COLS)) kq_flag(status, KQ_DEV_INPUT);
-    if (g < ngroups) R::load_group(ln, wb, g, rows, sub, ra);
+    if (ln.load_x(x, x_stride)) kq_flag(status, KQ_DEV_INPUT);
+    if (g < ngroups) R::load_group(ln, wb, g, rows, sub, ra, row_bytes);
 
     bool bad = false, malformed = false;
     float best_v[B];
@@ -90,9 +94,11 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
                 const uint32_t r = (uint32_t)idx / B, b = (uint32_t)idx % B;
                 const uint32_t row = gg * R::GROUP + r * R::RPW + sub;
                 if (row < rows) {
-                    y[(size_t)b * rows + row] = v[j];
-                    bad |= !kq_isfinite(v[j]);
-                    argmax_merge(best_v[b], best_i[b], v[j], row);
+                    float s = v[j];
+                    if (y_prev != nullptr) s = y_prev[(size_t)b * rows + row] + s;
+                    y[(size_t)b * rows + row] = s;
+                    bad |= !kq_isfinite(s);
+                    argmax_merge(best_v[b], best_i[b], s, row);
                 }
             }
         }
@@ -100,12 +106,12 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     /* ping-pong: the next group's loads are in flight while one is reduced */
     while (g < ngroups) {
         uint32_t gn = g + nwaves;
-        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, rb);
+        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, rb, row_bytes);
         finish(ra, g);
         g = gn;
         if (g >= ngroups) break;
         gn = g + nwaves;
-        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, ra);
+        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, ra, row_bytes);
         finish(rb, g);
         g = gn;
     }
@@ -211,12 +217,21 @@ uint32_t resident_blocks(K kernel) {
     return (uint32_t)(per_cu * cus);
 }
 
-/* Launches one matvec, or (waves != nullptr) only reports the number of
+/* Where a launch's column segment lies: bytes from row to row, the
+ * activations' batch stride and, after the first segment, the sums to add
+ * to (y itself). */
+struct Seg {
+    uint32_t row_bytes, x_stride;
+    const float *y_prev;
+};
+
+/* Launches one segment, or (waves != nullptr) only reports the number of
  * waves it would launch: one group per wave for RT = 2; for RT = 4 as many
  * workgroups as are resident at once, striding over the groups. */
 template <uint32_t TYPE, uint32_t COLS, int B>
-hipError_t launch_one(const uint8_t *W, uint32_t rows, const float *x, float *y, uint32_t *st,
-                      float *pv, uint32_t *pi, uint32_t ps, hipStream_t s, uint32_t *waves) {
+hipError_t launch_one(const uint8_t *W, uint32_t rows, Seg sg, const float *x, float *y,
+                      uint32_t *st, float *pv, uint32_t *pi, uint32_t ps, hipStream_t s,
+                      uint32_t *waves) {
     constexpr uint32_t kWavesPerBlock = kThreads / 64u;
     const uint32_t rt = pick_rt(rows, COLS);
     const uint32_t groups = (rows + group_rows(COLS, rt) - 1u) / group_rows(COLS, rt);
@@ -232,80 +247,132 @@ hipError_t launch_one(const uint8_t *W, uint32_t rows, const float *x, float *y,
     }
     if (rt == 4u)
         hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 4>), dim3(blocks), dim3(kThreads), 0, s,
-                           W, rows, x, y, st, pv, pi, ps);
+                           W, rows, sg.row_bytes, x, sg.x_stride, y, sg.y_prev, st, pv, pi, ps);
     else
         hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 2>), dim3(blocks), dim3(kThreads), 0, s,
-                           W, rows, x, y, st, pv, pi, ps);
+                           W, rows, sg.row_bytes, x, sg.x_stride, y, sg.y_prev, st, pv, pi, ps);
     return hipGetLastError();
 }
 
 template <uint32_t TYPE, int B>
-hipError_t launch_cols(uint32_t cols, const uint8_t *W, uint32_t rows, const float *x, float *y,
-                       uint32_t *st, float *pv, uint32_t *pi, uint32_t ps, hipStream_t s,
-                       uint32_t *wv) {
+hipError_t launch_cols(uint32_t cols, const uint8_t *W, uint32_t rows, Seg sg, const float *x,
+                       float *y, uint32_t *st, float *pv, uint32_t *pi, uint32_t ps,
+                       hipStream_t s, uint32_t *wv) {
     switch (cols) {
     case 32:
     case 64:
     case 128:
-        /* short rows exist only for 32-element blocks */
+        /* short segments exist only for 32-element blocks */
         if constexpr (kq::small_block<TYPE>()) {
-            if (cols == 32) return launch_one<TYPE, 32u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-            if (cols == 64) return launch_one<TYPE, 64u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-            return launch_one<TYPE, 128u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+            if (cols == 32) return launch_one<TYPE, 32u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+            if (cols == 64) return launch_one<TYPE, 64u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+            return launch_one<TYPE, 128u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
         }
         break;
-    case 256: return launch_one<TYPE, 256u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-    case 512: return launch_one<TYPE, 512u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-    case 1024: return launch_one<TYPE, 1024u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
-    case 2048: return launch_one<TYPE, 2048u, B>(W, rows, x, y, st, pv, pi, ps, s, wv);
+    case 256: return launch_one<TYPE, 256u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    case 512: return launch_one<TYPE, 512u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    case 1024: return launch_one<TYPE, 1024u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    case 2048: return launch_one<TYPE, 2048u, B>(W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     default: break;
     }
     return hipErrorInvalidValue;
 }
 
 template <int B>
-hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t rows,
+hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t rows, Seg sg,
                     const float *x, float *y, uint32_t *st, float *pv, uint32_t *pi,
                     uint32_t ps, hipStream_t s, uint32_t *wv) {
     switch (type) {
     case KQ_LAUNCH_Q4_K:
-        return launch_cols<KQ_LAUNCH_Q4_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_cols<KQ_LAUNCH_Q4_K, B>(cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     case KQ_LAUNCH_Q6_K:
-        return launch_cols<KQ_LAUNCH_Q6_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_cols<KQ_LAUNCH_Q6_K, B>(cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     case KQ_LAUNCH_Q8_0:
-        return launch_cols<KQ_LAUNCH_Q8_0, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_cols<KQ_LAUNCH_Q8_0, B>(cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     case KQ_LAUNCH_Q5_K:
-        return launch_cols<KQ_LAUNCH_Q5_K, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_cols<KQ_LAUNCH_Q5_K, B>(cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     case KQ_LAUNCH_Q5_1:
-        return launch_cols<KQ_LAUNCH_Q5_1, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_cols<KQ_LAUNCH_Q5_1, B>(cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     case KQ_LAUNCH_IQ4_NL:
-        return launch_cols<KQ_LAUNCH_IQ4_NL, B>(cols, W, rows, x, y, st, pv, pi, ps, s, wv);
+        return launch_cols<KQ_LAUNCH_IQ4_NL, B>(cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
     default: return hipErrorInvalidValue;
     }
 }
 
+/* block elements and bytes of the product formats (0 for others) */
+void block_geometry(uint32_t type, uint32_t &be, uint32_t &bb) {
+    switch (type) {
+    case KQ_LAUNCH_Q4_K: be = 256u; bb = 144u; return;
+    case KQ_LAUNCH_Q5_K: be = 256u; bb = 176u; return;
+    case KQ_LAUNCH_Q6_K: be = 256u; bb = 210u; return;
+    case KQ_LAUNCH_Q8_0: be = 32u; bb = 34u; return;
+    case KQ_LAUNCH_Q5_1: be = 32u; bb = 24u; return;
+    case KQ_LAUNCH_IQ4_NL: be = 32u; bb = 18u; return;
+    default: be = 0u; bb = 0u; return;
+    }
+}
+
+/* the widest segment (2048 .. 256, and 128 .. 32 for 32-element blocks)
+ * that fits in `left` columns */
+uint32_t segment_cols(uint32_t be, uint32_t left) {
+    for (uint32_t c = 2048u; c >= be && c >= 32u; c >>= 1)
+        if (c <= left) return c;
+    return 0u;
+}
+
+hipError_t launch_batch(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t rows, Seg sg,
+                        const float *x, uint32_t batch, float *y, uint32_t *st, float *pv,
+                        uint32_t *pi, uint32_t ps, hipStream_t s, uint32_t *wv) {
+    switch (batch) {
+    case 1: return launch_b<1>(type, cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    case 2: return launch_b<2>(type, cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    case 3: return launch_b<3>(type, cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    case 4: return launch_b<4>(type, cols, W, rows, sg, x, y, st, pv, pi, ps, s, wv);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+/* A row of any whole number of blocks is cut into segments of supported
+ * widths, widest first; each segment is one launch over all rows, and the
+ * ones after the first add to y. Only the last segment's launch writes the
+ * argmax partials (over the finished sums); with wv set, only that
+ * launch's wave count is reported and nothing is launched. */
 hipError_t dispatch(uint32_t type, const void *W, uint32_t rows, uint32_t cols, const float *x,
                     uint32_t batch, float *y, uint32_t *status, float *pv, uint32_t *pi,
                     uint32_t ps, hipStream_t stream, uint32_t *wv) {
+    uint32_t be, bb;
+    block_geometry(type, be, bb);
+    if (be == 0u || cols == 0u || cols % be != 0u) return hipErrorInvalidValue;
     const uint8_t *w = (const uint8_t *)W;
-    switch (batch) {
-    case 1: return launch_b<1>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
-    case 2: return launch_b<2>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
-    case 3: return launch_b<3>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
-    case 4: return launch_b<4>(type, cols, w, rows, x, y, status, pv, pi, ps, stream, wv);
-    default: return hipErrorInvalidValue;
+    const uint32_t row_bytes = cols / be * bb;
+    uint32_t off = 0u;
+    while (off < cols) {
+        const uint32_t seg = segment_cols(be, cols - off);
+        if (seg == 0u) return hipErrorInvalidValue;
+        const bool last = off + seg == cols;
+        if (wv == nullptr || last) {
+            const Seg sg{row_bytes, cols, off == 0u ? nullptr : y};
+            const hipError_t e = launch_batch(
+                type, seg, w == nullptr ? nullptr : w + off / be * bb, rows, sg,
+                x == nullptr ? nullptr : x + off, batch, y, status, last ? pv : nullptr,
+                last ? pi : nullptr, ps, stream, last ? wv : nullptr);
+            if (e != hipSuccess) return e;
+        }
+        off += seg;
     }
+    return hipSuccess;
 }
 
 }  // namespace
 
+/* at most 32 segment launches per product */
+constexpr uint32_t kMaxCols = 65536u;
+
 extern "C" int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t batch) {
     if (batch < 1u || batch > 4u) return 0;
-    const bool small = type == KQ_LAUNCH_Q8_0 || type == KQ_LAUNCH_Q5_1 || type == KQ_LAUNCH_IQ4_NL;
-    const bool kquant = type == KQ_LAUNCH_Q4_K || type == KQ_LAUNCH_Q5_K || type == KQ_LAUNCH_Q6_K;
-    if (!small && !kquant) return 0;
-    if (small && (cols == 32u || cols == 64u || cols == 128u)) return 1;
-    return cols == 256u || cols == 512u || cols == 1024u || cols == 2048u;
+    uint32_t be, bb;
+    block_geometry(type, be, bb);
+    return be != 0u && cols != 0u && cols % be == 0u && cols <= kMaxCols;
 }
 
 extern "C" uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols,

@@ -664,18 +664,20 @@ struct Rows {
                              : NV <= 16 ? 16 : 32;
     static constexpr int KEEP = N > (int)LPR ? N / (int)LPR : 1; /* after reduction */
 
+    /* stride: bytes from one row to the next (RB, or more when the rows
+     * are column segments of longer rows) */
     __device__ static __forceinline__ void load_group(const Lane &ln, KqBuf W, uint32_t g,
                                                       uint32_t rows, uint32_t sub,
-                                                      Raw (&raw)[RT]) {
+                                                      Raw (&raw)[RT], uint32_t stride = RB) {
         const uint32_t row0 = g * GROUP + sub;
         if ((g + 1u) * GROUP <= rows) {
 #pragma unroll
-            for (int r = 0; r < RT; ++r) raw[r] = ln.load(W, (row0 + (uint32_t)r * RPW) * RB);
+            for (int r = 0; r < RT; ++r) raw[r] = ln.load(W, (row0 + (uint32_t)r * RPW) * stride);
         } else {
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 const uint32_t row = row0 + (uint32_t)r * RPW;
-                raw[r] = row < rows ? ln.load(W, row * RB) : ln.zero();
+                raw[r] = row < rows ? ln.load(W, row * stride) : ln.zero();
             }
         }
     }

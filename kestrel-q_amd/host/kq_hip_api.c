@@ -403,10 +403,9 @@ static kq_status validate_matvec(const kq_hip_context *c, uint32_t type_id, cons
         return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH, "columns are not whole quant blocks");
     if (rows > UINT32_MAX || batch > 8u)
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "rows must fit 32 bits and batch be <= 8");
-    if (!kq_launch_matvec_supported(type_id, (uint32_t)cols, 1u))
+    if (cols > UINT32_MAX || !kq_launch_matvec_supported(type_id, (uint32_t)cols, 1u))
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
-                       "device matvec supports 256, 512, 1024 or 2048 columns "
-                       "(32-weight formats also 32, 64, 128)");
+                       "device matvec takes rows of at most 65536 columns");
     if (!u64_mul(rows, cols / be * bb, &w_bytes) || !u64_mul(rows, batch, &need))
         return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "matrix byte count overflows");
     /* the kernels address the matrix through one buffer descriptor, whose

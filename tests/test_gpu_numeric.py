@@ -276,6 +276,43 @@ def test_lm_head_q6k_151936x2048(ctx, batch):
             assert ids[b] == kq_oracle.argmax(ref[b])
 
 
+@pytest.mark.parametrize("fmt,rows,cols,batch", [
+    ("Q8_0", 300, 2560, 1), ("Q8_0", 257, 6144, 2), ("Q8_0", 65, 10240, 1),
+    ("Q8_0", 1000, 320, 3), ("Q8_0", 640, 640, 1), ("Q5_1", 300, 640, 2),
+    ("IQ4_NL", 300, 2560, 1), ("Q4_K", 640, 2560, 1), ("Q5_K", 640, 2560, 4),
+    ("Q6_K", 129, 6144, 1), ("Q4_K", 33, 2304, 3)])
+def test_matvec_long_rows(ctx, fmt, rows, cols, batch):
+    # Rows of the reference model's widths (hidden 2560, expert 640, the
+    # 6144- and 10240-wide GDN and hyper-connection projections, 320): the
+    # row runs as column segments of supported widths, each one launch
+    # adding to the previous segments' sums.
+    got, want = matvec_case(ctx, fmt, rows, cols, batch,
+                            S.stream_key(S.W_MATVEC_Q8_0, rows, cols, FMTS[fmt]))
+    assert_close(got, want)
+
+
+def test_lm_head_q8_0_248320x2560(ctx):
+    # The reference model's LM head (Q8_0, vocabulary 248,320, hidden 2560):
+    # two segments, the argmax taken over the finished sums.
+    V, H = 248320, 2560
+    say("lm head q8_0 248320x2560")
+    w = S.quant_matrix("Q8_0", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT, 8), V, H)
+    h = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, 8), H)[None, :]
+    dw, dh = ctx.upload(w), ctx.upload(h)
+    dl, di = ctx.alloc(V * 4), ctx.alloc(4)
+    ctx.lm_head(kq_hip.TYPE_Q8_0, dw, V, H, dh, 1, dl, di)
+    logits = ctx.download(dl, np.float32, V)[None, :]
+    ids = ctx.download(di, np.uint32, 1)
+    ref = kq_oracle.matvec(kq_oracle.Q8_0, w, V, H, h, threads=oracle_threads())
+    assert_close(logits, ref)
+    assert ids[0] == int(np.argmax(logits[0]))
+    top2 = np.sort(ref[0])[-2:]
+    if top2[1] - top2[0] > ATOL + RTOL * abs(top2[1]):
+        assert ids[0] == kq_oracle.argmax(ref[0])
+    for b in (dw, dh, dl, di):
+        b.close()
+
+
 @pytest.mark.parametrize("batch", [5, 6, 8])
 def test_lm_head_batch_spans_launches(ctx, batch):
     # batches over 4 run as several launches whose wave counts differ; the
