@@ -1,7 +1,9 @@
 /*
  * kq_hip.h — C ABI of the MI355X (gfx950) backend for Kestrel-Q's
- * quantized-weight path: GGUF block dequantization (Q4_K, Q6_K, Q8_0) fused
- * into matrix-vector products, the MoE expert FFN and the LM head.
+ * quantized-weight path: GGUF block dequantization fused into
+ * matrix-vector products, the MoE expert FFN and the LM head, fed from
+ * GGUF files. Packed formats: Q4_K, Q5_K, Q6_K, Q5_1, Q8_0, IQ4_NL; F32 and
+ * BF16 are decoded and ingested.
  *
  * Conventions (same as the reference library):
  *  - every entry point returns kq_status and fills the optional
@@ -28,6 +30,7 @@
 
 #include <stdint.h>
 
+#include "kq_gguf.h"
 #include "kq_status.h"
 
 #ifdef __cplusplus
@@ -100,6 +103,46 @@ kq_status kq_hip_expert_member_span(uint32_t type_id, uint64_t rows,
                                     kq_diagnostic *diagnostic);
 
 /* ------------------------------------------------------------------ */
+/* GGUF ingestion: packed tensor bytes from a parsed file (include/kq_gguf.h)
+ * into device memory, byte for byte. The reference reads the same bytes
+ * through kq_tensor_view_physical_data (src/kq_tensor_view.c) and its
+ * tensor span (src/kq_gguf.c:1019-1078). */
+
+/* Byte span of expert `expert_id` in a routed expert stack: the experts are
+ * the slowest (last) GGUF dimension, so the member is the tensor's
+ * element_count / dimensions[rank-1] elements at expert_id times that.
+ * Mirrors kq_tensor_view_open_expert_member (src/kq_tensor_view.c:664-807)
+ * without the semantic registry: rank below 2 fails with
+ * INVALID_QUANTIZED_GEOMETRY, an expert past the stack with
+ * SPAN_OUT_OF_RANGE, a member that is not whole blocks with
+ * NONCONTIGUOUS_TENSOR_VIEW. */
+kq_status kq_hip_gguf_expert_member(const kq_gguf_tensor *tensor,
+                                    uint32_t expert_id,
+                                    uint64_t *out_byte_offset,
+                                    uint64_t *out_byte_count,
+                                    kq_diagnostic *diagnostic);
+
+/* Copies the tensor's packed_bytes to device_dst (device_capacity bytes,
+ * else BUFFER_TOO_SMALL). The tensor must be one of gguf's descriptors
+ * (TENSOR_OWNERSHIP_MISMATCH). Synchronous; file pages are mapped a window
+ * at a time and staged through pinned host buffers. */
+kq_status kq_hip_gguf_upload_tensor(kq_hip_context *context,
+                                    const kq_gguf *gguf,
+                                    const kq_gguf_tensor *tensor,
+                                    void *device_dst,
+                                    uint64_t device_capacity,
+                                    kq_diagnostic *diagnostic);
+
+/* Copies one expert member (kq_hip_gguf_expert_member) to device_dst. */
+kq_status kq_hip_gguf_upload_expert_member(kq_hip_context *context,
+                                           const kq_gguf *gguf,
+                                           const kq_gguf_tensor *tensor,
+                                           uint32_t expert_id,
+                                           void *device_dst,
+                                           uint64_t device_capacity,
+                                           kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
 /* Numeric core. */
 
 /* Replaces kq_dequantize_blocks_f32 (include/kq_numeric.h:20-26,
@@ -128,8 +171,8 @@ kq_status kq_hip_quantized_row_dot_f32(kq_hip_context *context,
 /* Replaces kq_weight_provider_linear_f32 (include/kq_weight_provider.h:56-61,
  * src/kq_weight_provider.c:378-509), extended to `batch` activation vectors:
  * y[b*rows + r] = row r of W (packed, rows contiguous) . x[b*columns ...].
- * batch 1..8; columns 256, 512, 1024 or 2048 (Q8_0 also 32, 64 or 128);
- * the packed matrix below 4 GiB. */
+ * batch 1..8; columns any whole number of blocks up to 65536; the packed
+ * matrix below 4 GiB. */
 kq_status kq_hip_quantized_matvec_f32(kq_hip_context *context,
                                       uint32_t type_id,
                                       const void *device_weights,

@@ -8,7 +8,8 @@
  * The numeric values of the codes below are the ones the reference assigns
  * (its enum is positional; the values are restated explicitly here so a
  * caller switching from the reference library keeps the same integers).
- * Only the codes that the quantized-weight path can return are listed.
+ * Only the codes that the quantized-weight path and its GGUF ingestion can
+ * return are listed.
  * KQ_STATUS_DEVICE_FAILURE is new: the reference has no device runtime.
  */
 #ifndef KQ_STATUS_H
@@ -24,12 +25,26 @@ typedef enum kq_status {
     KQ_STATUS_OK = 0,
     KQ_STATUS_INVALID_ARGUMENT = 1,
     KQ_STATUS_OUT_OF_MEMORY = 2,
+    KQ_STATUS_FILE_OPEN_FAILED = 3,
+    KQ_STATUS_FILE_SIZE_FAILED = 4,
+    KQ_STATUS_FILE_MAP_FAILED = 5,
+    KQ_STATUS_TRUNCATED = 6,
+    KQ_STATUS_BAD_MAGIC = 7,
+    KQ_STATUS_UNSUPPORTED_VERSION = 8,
+    KQ_STATUS_MALFORMED_METADATA = 9,
+    KQ_STATUS_UNSUPPORTED_METADATA = 10,
+    KQ_STATUS_MALFORMED_TENSOR = 11,
     KQ_STATUS_UNSUPPORTED_TENSOR_TYPE = 12,
     KQ_STATUS_ARITHMETIC_OVERFLOW = 13,
     KQ_STATUS_LIMIT_EXCEEDED = 14,
     KQ_STATUS_INVALID_ALIGNMENT = 15,
     KQ_STATUS_SPAN_OUT_OF_RANGE = 16,
+    KQ_STATUS_DUPLICATE_METADATA = 17,
+    KQ_STATUS_DUPLICATE_TENSOR = 18,
+    KQ_STATUS_INCONSISTENT_DATA_SECTION = 19,
     KQ_STATUS_INVALID_QUANTIZED_GEOMETRY = 25,
+    KQ_STATUS_NONCONTIGUOUS_TENSOR_VIEW = 26,
+    KQ_STATUS_TENSOR_OWNERSHIP_MISMATCH = 28,
     KQ_STATUS_BUFFER_TOO_SMALL = 32,
     KQ_STATUS_MALFORMED_QUANTIZED_DATA = 38,
     KQ_STATUS_NUMERIC_DOMAIN = 39,

@@ -17,6 +17,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "kq_hip_internal.h"
 #include "kq_launch.h"
 #include "kq_status_internal.h"
 
@@ -35,6 +36,8 @@ struct kq_hip_context {
     float *part_v;      /* argmax partials */
     uint32_t *part_i;
     uint64_t part_cap;
+    void *stage[2];     /* pinned staging for file-backed uploads */
+    hipEvent_t stage_done[2];
 };
 
 struct kq_hip_moe_config {
@@ -157,6 +160,10 @@ void kq_hip_context_destroy(kq_hip_context *c) {
     if (c->part_i) (void)hipFree(c->part_i);
     if (c->d_status) (void)hipFree(c->d_status);
     if (c->h_status) (void)hipHostFree(c->h_status);
+    for (int k = 0; k < 2; ++k) {
+        if (c->stage[k]) (void)hipHostFree(c->stage[k]);
+        if (c->stage_done[k]) (void)hipEventDestroy(c->stage_done[k]);
+    }
     if (c->stream) (void)hipStreamDestroy(c->stream);
     free(c);
 }
@@ -219,6 +226,53 @@ kq_status kq_hip_upload(kq_hip_context *c, void *dst, const void *src, uint64_t 
     e = hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return e == hipSuccess ? KQ_STATUS_OK : hip_fail(diag, e, "upload");
+}
+
+/* Host memory that the DMA engines may not read directly (a mapped file)
+ * is copied through two pinned buffers: while one chunk's copy to the
+ * device runs, the CPU fills the other. */
+#define KQ_STAGE_BYTES ((uint64_t)16u << 20)
+
+static hipError_t ensure_stage(kq_hip_context *c) {
+    hipError_t e = hipSuccess;
+    for (int k = 0; k < 2 && e == hipSuccess; ++k) {
+        if (c->stage[k] == NULL)
+            e = hipHostMalloc(&c->stage[k], (size_t)KQ_STAGE_BYTES, hipHostMallocDefault);
+        if (e == hipSuccess && c->stage_done[k] == NULL)
+            e = hipEventCreateWithFlags(&c->stage_done[k], hipEventDisableTiming);
+    }
+    return e;
+}
+
+kq_status kqi_hip_staged_upload(kq_hip_context *c, void *dst, const void *src, uint64_t bytes,
+                                kq_diagnostic *diag) {
+    const unsigned char *from = (const unsigned char *)src;
+    int used[2] = {0, 0};
+    uint64_t at = 0u;
+    hipError_t e, s;
+    kq_status st;
+    int k = 0;
+    if (!ctx_ok(c) || dst == NULL || src == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "context and buffers are required");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = ensure_stage(c);
+    while (e == hipSuccess && at < bytes) {
+        const uint64_t n = bytes - at < KQ_STAGE_BYTES ? bytes - at : KQ_STAGE_BYTES;
+        if (used[k]) e = hipEventSynchronize(c->stage_done[k]);
+        if (e != hipSuccess) break;
+        memcpy(c->stage[k], from + at, (size_t)n);
+        e = hipMemcpyAsync((unsigned char *)dst + at, c->stage[k], (size_t)n,
+                           hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = hipEventRecord(c->stage_done[k], c->stream);
+        used[k] = 1;
+        at += n;
+        k ^= 1;
+    }
+    /* the staging buffers must be idle before another call refills them */
+    s = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = s;
+    return e == hipSuccess ? KQ_STATUS_OK : hip_fail(diag, e, "staged upload");
 }
 
 kq_status kq_hip_download(kq_hip_context *c, void *dst, const void *src, uint64_t bytes,

@@ -13,12 +13,26 @@ const char *kq_status_string(kq_status status) {
     case KQ_STATUS_OK: return "ok";
     case KQ_STATUS_INVALID_ARGUMENT: return "invalid argument";
     case KQ_STATUS_OUT_OF_MEMORY: return "out of memory";
+    case KQ_STATUS_FILE_OPEN_FAILED: return "file open failed";
+    case KQ_STATUS_FILE_SIZE_FAILED: return "file size failed";
+    case KQ_STATUS_FILE_MAP_FAILED: return "file map failed";
+    case KQ_STATUS_TRUNCATED: return "truncated";
+    case KQ_STATUS_BAD_MAGIC: return "bad magic";
+    case KQ_STATUS_UNSUPPORTED_VERSION: return "unsupported version";
+    case KQ_STATUS_MALFORMED_METADATA: return "malformed metadata";
+    case KQ_STATUS_UNSUPPORTED_METADATA: return "unsupported metadata";
+    case KQ_STATUS_MALFORMED_TENSOR: return "malformed tensor";
     case KQ_STATUS_UNSUPPORTED_TENSOR_TYPE: return "unsupported tensor type";
     case KQ_STATUS_ARITHMETIC_OVERFLOW: return "arithmetic overflow";
     case KQ_STATUS_LIMIT_EXCEEDED: return "limit exceeded";
     case KQ_STATUS_INVALID_ALIGNMENT: return "invalid alignment";
     case KQ_STATUS_SPAN_OUT_OF_RANGE: return "span out of range";
+    case KQ_STATUS_DUPLICATE_METADATA: return "duplicate metadata";
+    case KQ_STATUS_DUPLICATE_TENSOR: return "duplicate tensor";
+    case KQ_STATUS_INCONSISTENT_DATA_SECTION: return "inconsistent data section";
     case KQ_STATUS_INVALID_QUANTIZED_GEOMETRY: return "invalid quantized geometry";
+    case KQ_STATUS_NONCONTIGUOUS_TENSOR_VIEW: return "noncontiguous tensor view";
+    case KQ_STATUS_TENSOR_OWNERSHIP_MISMATCH: return "tensor ownership mismatch";
     case KQ_STATUS_BUFFER_TOO_SMALL: return "buffer too small";
     case KQ_STATUS_MALFORMED_QUANTIZED_DATA: return "malformed quantized data";
     case KQ_STATUS_NUMERIC_DOMAIN: return "numeric domain error";

@@ -28,9 +28,14 @@ GEOMETRY = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210),
             TYPE_Q5_1: (32, 24), TYPE_Q5_K: (256, 176), TYPE_IQ4_NL: (32, 18),
             TYPE_F32: (1, 4), TYPE_BF16: (1, 2)}
 
-STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "OUT_OF_MEMORY", 12: "UNSUPPORTED_TENSOR_TYPE",
+STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "OUT_OF_MEMORY", 3: "FILE_OPEN_FAILED",
+          4: "FILE_SIZE_FAILED", 5: "FILE_MAP_FAILED", 6: "TRUNCATED", 7: "BAD_MAGIC",
+          8: "UNSUPPORTED_VERSION", 9: "MALFORMED_METADATA", 10: "UNSUPPORTED_METADATA",
+          11: "MALFORMED_TENSOR", 17: "DUPLICATE_METADATA", 18: "DUPLICATE_TENSOR",
+          19: "INCONSISTENT_DATA_SECTION", 12: "UNSUPPORTED_TENSOR_TYPE",
           13: "ARITHMETIC_OVERFLOW", 14: "LIMIT_EXCEEDED", 15: "INVALID_ALIGNMENT",
-          16: "SPAN_OUT_OF_RANGE", 25: "INVALID_QUANTIZED_GEOMETRY", 32: "BUFFER_TOO_SMALL",
+          16: "SPAN_OUT_OF_RANGE", 25: "INVALID_QUANTIZED_GEOMETRY",
+          26: "NONCONTIGUOUS_TENSOR_VIEW", 28: "TENSOR_OWNERSHIP_MISMATCH", 32: "BUFFER_TOO_SMALL",
           38: "MALFORMED_QUANTIZED_DATA", 39: "NUMERIC_DOMAIN", 40: "DIMENSION_MISMATCH",
           41: "ALIASING_VIOLATION", 46: "INCOMPATIBLE_MOE", 1000: "DEVICE_FAILURE"}
 CODES = {v: k for k, v in STATUS.items()}
@@ -62,6 +67,33 @@ class MoeWeights(C.Structure):
                 ("shared_gate_weight", C.c_void_p)]
 
 
+class StringView(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("length", C.c_uint64)]
+
+    def bytes(self) -> bytes:
+        return C.string_at(self.data, self.length) if self.length else b""
+
+
+class GgufTensor(C.Structure):
+    _fields_ = [("name", StringView), ("rank", C.c_uint32), ("dimensions", C.c_uint64 * 8),
+                ("type_id", C.c_uint32), ("block_elements", C.c_uint64),
+                ("bytes_per_block", C.c_uint64), ("element_count", C.c_uint64),
+                ("relative_offset", C.c_uint64), ("data_offset", C.c_uint64),
+                ("packed_bytes", C.c_uint64)]
+
+
+class GgufMetadata(C.Structure):
+    _fields_ = [("key", StringView), ("value_type", C.c_uint32),
+                ("array_element_type", C.c_uint32), ("array_length", C.c_uint64),
+                ("scalar_value", C.c_uint64), ("string_value", StringView),
+                ("array_data", StringView)]
+
+
+class GgufTypeInfo(C.Structure):
+    _fields_ = [("type_id", C.c_uint32), ("name", C.c_char_p), ("block_elements", C.c_uint64),
+                ("bytes_per_block", C.c_uint64)]
+
+
 class KqError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"{STATUS.get(status, status)}: {message}")
@@ -69,8 +101,52 @@ class KqError(RuntimeError):
         self.name = STATUS.get(status, str(status))
 
 
-# Every function declared in include/kq_hip.h and include/kq_status.h.
+_P = C.c_void_p
+_TP = C.POINTER(GgufTensor)
+_MP = C.POINTER(GgufMetadata)
+
+# Every function declared in include/kq_hip.h, kq_gguf.h, kq_file.h and
+# kq_status.h.
 SIGNATURES = {
+    "kq_file_open_readonly": (C.c_int, [C.c_wchar_p, _P, _P]),
+    "kq_file_open_readonly_utf8": (C.c_int, [C.c_char_p, _P, _P]),
+    "kq_file_size": (C.c_uint64, [_P]),
+    "kq_file_close": (None, [_P]),
+    "kq_file_view_open": (C.c_int, [_P, C.c_uint64, C.c_uint64, _P, _P]),
+    "kq_file_view_data": (_P, [_P]),
+    "kq_file_view_offset": (C.c_uint64, [_P]),
+    "kq_file_view_length": (C.c_uint64, [_P]),
+    "kq_file_view_close": (None, [_P]),
+    "kq_gguf_open": (C.c_int, [_P, _P, _P]),
+    "kq_gguf_close": (None, [_P]),
+    "kq_gguf_version": (C.c_uint32, [_P]),
+    "kq_gguf_metadata_count": (C.c_uint64, [_P]),
+    "kq_gguf_tensor_count": (C.c_uint64, [_P]),
+    "kq_gguf_alignment": (C.c_uint64, [_P]),
+    "kq_gguf_directory_end_offset": (C.c_uint64, [_P]),
+    "kq_gguf_data_section_offset": (C.c_uint64, [_P]),
+    "kq_gguf_packed_tensor_bytes": (C.c_uint64, [_P]),
+    "kq_gguf_format_overhead_bytes": (C.c_uint64, [_P]),
+    "kq_gguf_directory_bytes_parsed": (C.c_uint64, [_P]),
+    "kq_gguf_payload_bytes_accessed": (C.c_uint64, [_P]),
+    "kq_gguf_architecture": (StringView, [_P]),
+    "kq_gguf_metadata_at": (_MP, [_P, C.c_uint64]),
+    "kq_gguf_find_metadata": (_MP, [_P, C.c_char_p]),
+    "kq_gguf_tensor_at": (_TP, [_P, C.c_uint64]),
+    "kq_gguf_find_tensor": (_TP, [_P, C.c_char_p]),
+    "kq_gguf_type_info_for": (C.POINTER(GgufTypeInfo), [C.c_uint32]),
+    "kq_string_view_equal": (C.c_int, [_P, _P]),
+    "kq_string_view_equal_cstr": (C.c_int, [_P, C.c_char_p]),
+    "kq_gguf_metadata_u16": (C.c_int, [_MP, _P]),
+    "kq_gguf_metadata_u32": (C.c_int, [_MP, _P]),
+    "kq_gguf_metadata_i32": (C.c_int, [_MP, _P]),
+    "kq_gguf_metadata_array_i32_at": (C.c_int, [_MP, C.c_uint64, _P]),
+    "kq_gguf_metadata_array_u64_at": (C.c_int, [_MP, C.c_uint64, _P]),
+    "kq_gguf_metadata_array_string_at": (C.c_int, [_MP, C.c_uint64, _P]),
+    "kq_hip_gguf_expert_member": (C.c_int, [_TP, C.c_uint32, _P, _P, _P]),
+    "kq_hip_gguf_upload_tensor": (C.c_int, [_P, _P, _TP, _P, C.c_uint64, _P]),
+    "kq_hip_gguf_upload_expert_member": (C.c_int, [_P, _P, _TP, C.c_uint32, _P, C.c_uint64,
+                                                    _P]),
     "kq_status_string": (C.c_char_p, [C.c_int]),
     "kq_diagnostic_clear": (None, [C.c_void_p]),
     "kq_hip_context_create": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
@@ -337,3 +413,149 @@ def moe_weights(bufs: dict, gate_type=TYPE_Q4_K, down_type=TYPE_Q6_K) -> MoeWeig
     return MoeWeights(P("router"), gate_type, P("gate"), gate_type, P("up"), down_type,
                       P("down"), gate_type, P("shared_gate"), gate_type, P("shared_up"),
                       down_type, P("shared_down"), P("shared_gate_weight"))
+
+
+# ---------------------------------------------------------------- GGUF files
+
+
+class File:
+    """A read-only file (include/kq_file.h); views copy their bytes out."""
+
+    def __init__(self, path, wide: bool = False):
+        h, d = C.c_void_p(), Diagnostic()
+        if wide:
+            st = lib().kq_file_open_readonly(str(path), C.byref(h), C.byref(d))
+        else:
+            st = lib().kq_file_open_readonly_utf8(os.fsencode(path), C.byref(h), C.byref(d))
+        check(st, d)
+        self.handle = h.value
+
+    @property
+    def size(self) -> int:
+        return lib().kq_file_size(C.c_void_p(self.handle))
+
+    def view(self, offset: int, length: int) -> tuple[int, int, bytes]:
+        """(offset, length, bytes) of a mapped view, closed before returning."""
+        v, d = C.c_void_p(), Diagnostic()
+        check(lib().kq_file_view_open(C.c_void_p(self.handle), offset, length, C.byref(v),
+                                      C.byref(d)), d)
+        try:
+            L = lib()
+            return (L.kq_file_view_offset(v), L.kq_file_view_length(v),
+                    C.string_at(L.kq_file_view_data(v), L.kq_file_view_length(v)))
+        finally:
+            lib().kq_file_view_close(v)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().kq_file_close(C.c_void_p(self.handle))
+        self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class Gguf:
+    """A parsed GGUF v3 file (include/kq_gguf.h). Tensor descriptors are
+    ctypes pointers into the parser's own array (they stay valid until
+    close()); upload_* copy their packed bytes to device memory."""
+
+    def __init__(self, path, wide: bool = False):
+        self.file = File(path, wide)
+        h, d = C.c_void_p(), Diagnostic()
+        st = lib().kq_gguf_open(C.c_void_p(self.file.handle), C.byref(h), C.byref(d))
+        if st != 0:
+            self.file.close()
+            check(st, d)
+        self.handle = h.value
+
+    def _g(self):
+        return C.c_void_p(self.handle)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().kq_gguf_close(self._g())
+        self.handle = None
+        self.file.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self) -> dict:
+        L, g = lib(), self._g()
+        return {"version": L.kq_gguf_version(g), "metadata_count": L.kq_gguf_metadata_count(g),
+                "tensor_count": L.kq_gguf_tensor_count(g), "alignment": L.kq_gguf_alignment(g),
+                "directory_end": L.kq_gguf_directory_end_offset(g),
+                "data_section": L.kq_gguf_data_section_offset(g),
+                "packed_bytes": L.kq_gguf_packed_tensor_bytes(g),
+                "overhead_bytes": L.kq_gguf_format_overhead_bytes(g),
+                "bytes_parsed": L.kq_gguf_directory_bytes_parsed(g),
+                "payload_bytes_accessed": L.kq_gguf_payload_bytes_accessed(g),
+                "architecture": L.kq_gguf_architecture(g).bytes().decode()}
+
+    def tensor_at(self, index: int):
+        p = lib().kq_gguf_tensor_at(self._g(), index)
+        return p if p else None
+
+    def tensor(self, name: str):
+        p = lib().kq_gguf_find_tensor(self._g(), name.encode())
+        return p if p else None
+
+    def metadata_at(self, index: int):
+        p = lib().kq_gguf_metadata_at(self._g(), index)
+        return p if p else None
+
+    def metadata(self, key: str):
+        p = lib().kq_gguf_find_metadata(self._g(), key.encode())
+        return p if p else None
+
+    @staticmethod
+    def scalar(meta, kind: str):
+        """kind: u16 / u32 / i32; None when absent or of another type."""
+        ct = {"u16": C.c_uint16, "u32": C.c_uint32, "i32": C.c_int32}[kind]
+        out = ct()
+        fn = getattr(lib(), f"kq_gguf_metadata_{kind}")
+        return out.value if meta is not None and fn(meta, C.byref(out)) else None
+
+    @staticmethod
+    def array_item(meta, kind: str, index: int):
+        """kind: i32 / u64 / string; None when out of range or of another type."""
+        if kind == "string":
+            out = StringView()
+        else:
+            out = {"i32": C.c_int32, "u64": C.c_uint64}[kind]()
+        fn = getattr(lib(), f"kq_gguf_metadata_array_{kind}_at")
+        if meta is None or not fn(meta, index, C.byref(out)):
+            return None
+        return out.bytes() if kind == "string" else out.value
+
+    def upload_tensor(self, ctx: Context, tensor, dst, capacity: int) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_gguf_upload_tensor(ctx._h, self._g(), tensor, Context._p(dst),
+                                              capacity, C.byref(d)), d)
+
+    def upload_expert(self, ctx: Context, tensor, expert_id: int, dst, capacity: int) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_gguf_upload_expert_member(ctx._h, self._g(), tensor, expert_id,
+                                                     Context._p(dst), capacity, C.byref(d)), d)
+
+
+def gguf_expert_member(tensor, expert_id: int) -> tuple[int, int]:
+    off, cnt, d = C.c_uint64(), C.c_uint64(), Diagnostic()
+    check(lib().kq_hip_gguf_expert_member(tensor, expert_id, C.byref(off), C.byref(cnt),
+                                          C.byref(d)), d)
+    return off.value, cnt.value
+
+
+def gguf_type_info(type_id: int):
+    p = lib().kq_gguf_type_info_for(type_id)
+    if not p:
+        return None
+    t = p.contents
+    return t.name.decode(), t.block_elements, t.bytes_per_block

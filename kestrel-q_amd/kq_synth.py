@@ -187,3 +187,53 @@ def moe_weights(workload: int, hidden: int, experts: int, inter: int, shared_int
                                 hidden * shared_inter // qk_d).reshape(-1)
     w["shared_gate_weight"] = normal_f32(stream_key(workload, R_SHARED_GATE_W), hidden, 0.02)
     return w
+
+
+# ------------------------------------------------------------- GGUF writer
+
+GGUF_UINT16, GGUF_UINT32, GGUF_INT32, GGUF_FLOAT32, GGUF_BOOL = 2, 4, 5, 6, 7
+GGUF_STRING, GGUF_ARRAY, GGUF_UINT64 = 8, 9, 10
+
+
+def _gguf_str(s) -> bytes:
+    b = s.encode() if isinstance(s, str) else bytes(s)
+    return len(b).to_bytes(8, "little") + b
+
+
+def _gguf_value(vtype: int, value) -> bytes:
+    if vtype == GGUF_STRING:
+        return _gguf_str(value)
+    if vtype == GGUF_ARRAY:
+        etype, items = value
+        body = b"".join(_gguf_value(etype, v) for v in items)
+        return etype.to_bytes(4, "little") + len(items).to_bytes(8, "little") + body
+    if vtype == GGUF_FLOAT32:
+        return np.float32(value).tobytes()
+    # GGUF value types 0..12: u8 i8 u16 i16 u32 i32 f32 bool str arr u64 i64 f64
+    width = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 7: 1, 10: 8, 11: 8, 12: 8}[vtype]
+    return int(value).to_bytes(width, "little", signed=vtype in (1, 3, 5, 11))
+
+
+def gguf_bytes(tensors, metadata, alignment: int = 32) -> bytes:
+    """A GGUF v3 file image. tensors: (name, type_id, dims innermost first,
+    packed payload bytes); metadata: (key, value type, value), arrays as
+    (element type, items). Payloads are placed in order at aligned offsets
+    from relative 0; a general.alignment entry is the caller's to add."""
+    out = bytearray(b"GGUF")
+    out += (3).to_bytes(4, "little") + len(tensors).to_bytes(8, "little")
+    out += len(metadata).to_bytes(8, "little")
+    for key, vtype, value in metadata:
+        out += _gguf_str(key) + vtype.to_bytes(4, "little") + _gguf_value(vtype, value)
+    rel, offsets = 0, []
+    for name, type_id, dims, payload in tensors:
+        offsets.append(rel)
+        out += _gguf_str(name) + len(dims).to_bytes(4, "little")
+        out += b"".join(int(d).to_bytes(8, "little") for d in dims)
+        out += type_id.to_bytes(4, "little") + rel.to_bytes(8, "little")
+        rel = (rel + len(payload) + alignment - 1) // alignment * alignment
+    out += bytes(-len(out) % alignment)
+    base = len(out)
+    for (_, _, _, payload), off in zip(tensors, offsets):
+        out += bytes(base + off - len(out))
+        out += bytes(payload)
+    return bytes(out)

@@ -13,8 +13,8 @@ import kq_hip
 
 def declared_functions():
     names = set()
-    for h in ("kq_hip.h", "kq_status.h"):
-        text = (ROOT / "include" / h).read_text()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = h.read_text()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"\b(kq_[a-z0-9_]+)\s*\(", text):
             names.add(m.group(1))
@@ -37,8 +37,8 @@ def test_library_exports_every_declared_function():
     assert missing == []
     # the binding declares exactly the header's functions
     assert sorted(kq_hip.SIGNATURES) == decl
-    # internal launchers stay hidden
-    assert not any(s.startswith("kq_launch") for s in exported)
+    # internal launchers and helpers stay hidden
+    assert not any(s.startswith(("kq_launch", "kqi_", "kq_fail")) for s in exported)
 
 
 def test_geometry_matches_reference_table():
@@ -90,6 +90,10 @@ def test_status_strings():
     assert lib.kq_status_string(0) == b"ok"
     assert lib.kq_status_string(38) == b"malformed quantized data"
     assert lib.kq_status_string(1000) == b"device failure"
+    # every code the binding names has its own string
+    strings = {lib.kq_status_string(code) for code in kq_hip.STATUS}
+    assert len(strings) == len(kq_hip.STATUS) and b"unknown status" not in strings
+    assert lib.kq_status_string(27) == b"unknown status"
 
 
 def _gpu_present() -> bool:
