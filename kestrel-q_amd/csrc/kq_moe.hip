@@ -110,32 +110,36 @@ __device__ __forceinline__ void router_decode_rows(
      * the row's end lie outside it: the buffer loads return zeros. */
     const uint32_t ql = tid % kRtSegQ;
     const uint32_t rsub = __builtin_amdgcn_readfirstlane(tid / kRtSegQ);
-    uint4 v[NSEG][kRtPerSeg], xr[NSEG];
+    /* at most four segments' loads are held in registers; segment sg + 4
+     * is requested once segment sg has been staged */
+    constexpr uint32_t NR = NSEG < 4u ? NSEG : 4u;
+    uint4 v[NR][kRtPerSeg], xr[NR];
+    KqBuf rb[kRtPerSeg];
+    const KqBuf xb = kq_buf(x, HIDDEN * 4u);
+    auto issue = [&](uint32_t sg) {
+        const uint32_t off = (sg * kRtSegQ + ql) * 16u, r = sg % NR;
+        xr[r] = kq_ld128(xb, off, 0);
+#pragma unroll
+        for (uint32_t k = 0; k < kRtPerSeg; ++k) v[r][k] = kq_ld128(rb[k], off, 0);
+    };
     if (active) {
-        KqBuf rb[kRtPerSeg];
 #pragma unroll
         for (uint32_t k = 0; k < kRtPerSeg; ++k) {
             const uint32_t e = row0 + rsub + 2u * k;
             rb[k] = kq_buf(e < experts ? router + (size_t)e * HIDDEN : shared_gate_weight,
                            e <= experts ? HIDDEN * 4u : 0u);
         }
-        const KqBuf xb = kq_buf(x, HIDDEN * 4u);
 #pragma unroll
-        for (uint32_t sg = 0; sg < NSEG; ++sg) {
-            const uint32_t off = (sg * kRtSegQ + ql) * 16u;
-            xr[sg] = kq_ld128(xb, off, 0);
-#pragma unroll
-            for (uint32_t k = 0; k < kRtPerSeg; ++k) v[sg][k] = kq_ld128(rb[k], off, 0);
-        }
+        for (uint32_t sg = 0; sg < NR; ++sg) issue(sg);
     }
     bool bad = false;
     auto stage = [&](uint32_t sg) {
         if (!active) return;
         float4 *b = buf + (sg * kRtSegQ + ql) * kRtPitch + rsub;
-        const float4 xq = as_f4(xr[sg]);
+        const float4 xq = as_f4(xr[sg % NR]);
 #pragma unroll
         for (uint32_t k = 0; k < kRtPerSeg; ++k) {
-            const float4 w = as_f4(v[sg][k]);
+            const float4 w = as_f4(v[sg % NR][k]);
             bad |= !kq_isfinite(w.x) || !kq_isfinite(w.y) || !kq_isfinite(w.z) ||
                    !kq_isfinite(w.w);
             float4 p;
@@ -146,8 +150,15 @@ __device__ __forceinline__ void router_decode_rows(
             b[2u * k] = p;
         }
     };
+    /* after the barrier that follows stage(sg), segment sg's registers are
+     * free: request segment sg + NR there (the barrier keeps the loads
+     * from being hoisted into the registers still in use) */
+    auto refill = [&](uint32_t sg) {
+        if (active && sg + NR < NSEG) issue(sg + NR);
+    };
     stage(0);
     __syncthreads();
+    refill(0);
     float acc = 0.0f;
 #pragma unroll
     for (uint32_t sg = 0; sg < NSEG; ++sg) {
@@ -159,6 +170,7 @@ __device__ __forceinline__ void router_decode_rows(
         if (sg + 1u < NSEG) {
             stage(sg + 1u);
             __syncthreads();
+            refill(sg + 1u);
         }
     }
     if (tid < kRtRows) {
@@ -992,30 +1004,48 @@ __global__ __launch_bounds__(1024) void route_exact(
 }
 
 /* ---------------------- expert gate/up + SwiGLU ---------------------- */
-/* grid: x = row groups, y = slot (0..K-1 routed by top-k position, K = the
- * shared expert), z = token. act[t][slot][row] = swiglu(g, u). Each lane
- * loads its slice of the token's hidden state, then requests its gate and
- * up rows (kq_rowdot.h). */
+/* Rows longer than one wave covers (or of a width the row engine has no
+ * instance for) are cut into column segments, widest first, one launch
+ * each: the first segment writes its partial gate/up dots to `part`, later
+ * ones add theirs, and the last applies SwiGLU. A shared expert whose type
+ * differs from the routed one runs as its own launch of the same kernel.
+ *
+ * Arguments common to every segment launch of one call. */
+struct GateupArgs {
+    const uint8_t *gate, *up, *sgate, *sup; /* routed stacks, shared matrices */
+    const float *x;                         /* hidden states [tokens][hidden] */
+    const uint32_t *ids;
+    uint32_t top_k, inter, shared_inter, hidden;
+    uint32_t rstride, srstride; /* full row bytes, routed and shared */
+    uint32_t act_stride;
+    float *act;   /* [tokens][top_k + 1][act_stride] */
+    float *part;  /* [tokens][top_k + 1][2][act_stride] partial dots */
+    uint32_t *status;
+};
+
+enum : uint32_t { kSegFirst = 1u, kSegLast = 2u };
+
+/* grid: x = row groups, y = slot - slot0 (slots 0..K-1 routed by top-k
+ * position, K the shared expert), z = token. This launch covers columns
+ * [col0, col0 + COLS) of every row. */
 template <uint32_t TYPE, uint32_t COLS, int RT>
-__global__ __launch_bounds__(kThreads) void expert_gateup(
-    const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
-    const uint8_t *__restrict__ sgate, const uint8_t *__restrict__ sup,
-    const float *__restrict__ hidden_states, const uint32_t *__restrict__ ids,
-    uint32_t top_k, uint32_t inter, uint32_t shared_inter, uint32_t act_stride,
-    float *__restrict__ act, uint32_t *status) {
+__global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t slot0,
+                                                          uint32_t col0, uint32_t seg) {
     using R = kq::Rows<TYPE, COLS, 1, RT>;
     using Raw = typename R::Raw;
-    const uint32_t slot = blockIdx.y, t = blockIdx.z;
-    const bool shared = slot == top_k;
-    const uint32_t rows = shared ? shared_inter : inter;
+    const uint32_t slot = blockIdx.y + slot0, t = blockIdx.z;
+    const bool shared = slot == a.top_k;
+    const uint32_t rows = shared ? a.shared_inter : a.inter;
+    const uint32_t stride = shared ? a.srstride : a.rstride;
+    const uint32_t boff = kq::row_bytes<TYPE>(col0);
     const uint8_t *G, *U;
     if (shared) {
-        G = sgate;
-        U = sup;
+        G = a.sgate;
+        U = a.sup;
     } else {
-        const uint32_t e = ids[(size_t)t * top_k + slot];
-        G = gate + (size_t)e * inter * R::RB;
-        U = up + (size_t)e * inter * R::RB;
+        const uint32_t e = a.ids[(size_t)t * a.top_k + slot];
+        G = a.gate + (size_t)e * a.inter * stride;
+        U = a.up + (size_t)e * a.inter * stride;
     }
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave =
@@ -1027,20 +1057,23 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
     ln.setup(l);
     Raw rg[RT], ru[RT];
     uint32_t g = wave;
-    const KqBuf gb = kq_buf(G, rows * R::RB), ub = kq_buf(U, rows * R::RB);
+    const KqBuf gb = kq_buf(G + boff, rows * stride - boff),
+                ub = kq_buf(U + boff, rows * stride - boff);
     /* each lane loads its slice of the token's hidden state first, then its
      * gate and up rows (the loads complete in order) */
-    if (ln.load_x(hidden_states + (size_t)t * COLS, COLS)) kq_flag(status, KQ_DEV_INPUT);
+    if (ln.load_x(a.x + (size_t)t * a.hidden + col0, COLS)) kq_flag(a.status, KQ_DEV_INPUT);
     if (g < ngroups) {
-        R::load_group(ln, gb, g, rows, sub, rg);
-        R::load_group(ln, ub, g, rows, sub, ru);
+        R::load_group(ln, gb, g, rows, sub, rg, stride);
+        R::load_group(ln, ub, g, rows, sub, ru, stride);
     }
     bool bad = false, malformed = false;
-    float *out = act + ((size_t)t * (top_k + 1u) + slot) * act_stride;
+    const size_t at = (size_t)t * (a.top_k + 1u) + slot;
+    float *out = a.act + at * a.act_stride;
+    float *pg = a.part + at * 2u * a.act_stride, *pu = pg + a.act_stride;
     for (; g < ngroups; g += nwaves) {
         if (g != wave) {
-            R::load_group(ln, gb, g, rows, sub, rg);
-            R::load_group(ln, ub, g, rows, sub, ru);
+            R::load_group(ln, gb, g, rows, sub, rg, stride);
+            R::load_group(ln, ub, g, rows, sub, ru, stride);
         }
         float vg[R::N], vu[R::N];
         R::dot_group(ln, rg, l, vg, malformed);
@@ -1051,36 +1084,59 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(
             if (idx >= 0) {
                 const uint32_t row = g * R::GROUP + (uint32_t)idx * R::RPW + sub;
                 if (row < rows) {
-                    const float a = kq_swiglu(vg[j], vu[j]);
-                    bad |= !kq_isfinite(vg[j]) || !kq_isfinite(vu[j]) || !kq_isfinite(a);
-                    out[row] = a;
+                    float gv = vg[j], uv = vu[j];
+                    if (!(seg & kSegFirst)) {
+                        gv = pg[row] + gv;
+                        uv = pu[row] + uv;
+                    }
+                    if (seg & kSegLast) {
+                        const float r = kq_swiglu(gv, uv);
+                        bad |= !kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(r);
+                        out[row] = r;
+                    } else {
+                        pg[row] = gv;
+                        pu[row] = uv;
+                    }
                 }
             }
         }
     }
-    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
-    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
 /* -------------------------- down + combine -------------------------- */
-/* grid: x = groups of R::GROUP output rows, y = token; one wave per slot
- * (slots 0..K-1 routed by top-k position, slot K the shared expert; waves
- * take further slots in steps of the wave count). Each wave reduces its
- * slot's rows Wd[f] . act[t][slot] into LDS; after a barrier one thread per
- * row forms the combine in the CPU's order:
+/* grid: x = groups of R::GROUP output rows, y = token; the launch covers
+ * slots [slot0, slot1) (0..K-1 routed by top-k position, K the shared
+ * expert), one wave per slot and further slots in steps of the wave count,
+ * and columns [col0, col0 + COLS) of the rows. Each wave reduces its slot's
+ * rows Wd[f] . act[t][slot] into LDS. Segments other than the last, and a
+ * launch that only computes the shared expert, store the sums in
+ * part[t][slot][row] (later segments add to them); the last segment of the
+ * routed launch forms the combine in the CPU's order:
  *   routed_sum = 0; for slots in ascending expert id: routed_sum += o * w;
- *   out = routed_sum + o_shared * sigmoid(shared logit). */
+ *   out = routed_sum + o_shared * sigmoid(shared logit),
+ * taking o_shared from part[t][K] when another launch computed it. */
 constexpr uint32_t kMaxSlots = 65;
 
 constexpr uint32_t kDownWaves = 12;
 
+struct DownArgs {
+    const uint8_t *down, *sdown;
+    const float *act;
+    const uint32_t *ids, *order;
+    const float *weights, *shared_scale;
+    uint32_t top_k, hidden, rstride, srstride, act_stride;
+    float *part; /* [tokens][top_k + 1][hidden] */
+    float *out;
+    uint32_t *status;
+};
+
+enum : uint32_t { kSegCombine = 4u };
+
 template <uint32_t TYPE, uint32_t COLS, int RT>
 __global__ __launch_bounds__(64 * kDownWaves) void expert_down_combine(
-    const uint8_t *__restrict__ down, const uint8_t *__restrict__ sdown,
-    const float *__restrict__ act, const uint32_t *__restrict__ ids,
-    const uint32_t *__restrict__ order, const float *__restrict__ weights,
-    const float *__restrict__ shared_scale, uint32_t top_k, uint32_t hidden,
-    uint32_t act_stride, float *__restrict__ out, uint32_t *status) {
+    DownArgs a, uint32_t slot0, uint32_t slot1, uint32_t col0, uint32_t seg) {
     using R = kq::Rows<TYPE, COLS, 1, RT>;
     using Raw = typename R::Raw;
     __shared__ float res[kMaxSlots][R::GROUP];
@@ -1090,24 +1146,29 @@ __global__ __launch_bounds__(64 * kDownWaves) void expert_down_combine(
     const uint32_t lane = threadIdx.x & 63u, nwv = blockDim.x >> 6;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
-    const uint32_t nslots = top_k + 1u;
-    if (threadIdx.x < top_k) {
-        const uint32_t s = order[(size_t)t * top_k + threadIdx.x];
+    const uint32_t top_k = a.top_k, nslots = top_k + 1u, hidden = a.hidden;
+    const uint32_t boff = kq::row_bytes<TYPE>(col0);
+    const bool combine = (seg & kSegCombine) != 0u;
+    if (combine && threadIdx.x < top_k) {
+        const uint32_t s = a.order[(size_t)t * top_k + threadIdx.x];
         ord_s[threadIdx.x] = s;
-        w_s[threadIdx.x] = weights[(size_t)t * top_k + s];
+        w_s[threadIdx.x] = a.weights[(size_t)t * top_k + s];
     }
     typename R::Lane ln;
     ln.setup(l);
     auto matrix = [&](uint32_t slot) {
-        const uint8_t *D = slot == top_k
-                               ? sdown
-                               : down + (size_t)ids[(size_t)t * top_k + slot] * hidden * R::RB;
-        return kq_buf(D, hidden * R::RB);
+        if (slot == top_k) return kq_buf(a.sdown + boff, hidden * a.srstride - boff);
+        const uint8_t *D = a.down + (size_t)a.ids[(size_t)t * top_k + slot] * hidden * a.rstride;
+        return kq_buf(D + boff, hidden * a.rstride - boff);
+    };
+    auto stride_of = [&](uint32_t slot) { return slot == top_k ? a.srstride : a.rstride; };
+    auto act_of = [&](uint32_t slot) {
+        return a.act + ((size_t)t * nslots + slot) * a.act_stride + col0;
     };
     bool bad = false, malformed = false;
     Raw ra[RT], rb[RT];
-    uint32_t slot = wv;
-    if (slot < nslots) R::load_group(ln, matrix(slot), g, hidden, sub, ra);
+    uint32_t slot = slot0 + wv;
+    if (slot < slot1) R::load_group(ln, matrix(slot), g, hidden, sub, ra, stride_of(slot));
     auto reduce = [&](const Raw (&raw)[RT], uint32_t sl) {
         float v[R::N];
         R::dot_group(ln, raw, l, v, malformed);
@@ -1119,99 +1180,179 @@ __global__ __launch_bounds__(64 * kDownWaves) void expert_down_combine(
     };
     /* ping-pong over this wave's slots: the next slot's rows are requested
      * before this slot's activations */
-    while (slot < nslots) {
+    while (slot < slot1) {
         uint32_t next = slot + nwv;
-        if (next < nslots) R::load_group(ln, matrix(next), g, hidden, sub, rb);
-        bad |= ln.load_x(act + ((size_t)t * nslots + slot) * act_stride, COLS);
+        if (next < slot1) R::load_group(ln, matrix(next), g, hidden, sub, rb, stride_of(next));
+        bad |= ln.load_x(act_of(slot), COLS);
         reduce(ra, slot);
         slot = next;
-        if (slot >= nslots) break;
+        if (slot >= slot1) break;
         next = slot + nwv;
-        if (next < nslots) R::load_group(ln, matrix(next), g, hidden, sub, ra);
-        bad |= ln.load_x(act + ((size_t)t * nslots + slot) * act_stride, COLS);
+        if (next < slot1) R::load_group(ln, matrix(next), g, hidden, sub, ra, stride_of(next));
+        bad |= ln.load_x(act_of(slot), COLS);
         reduce(rb, slot);
         slot = next;
     }
     __syncthreads();
-    if (threadIdx.x < R::GROUP) {
-        const uint32_t row = g * R::GROUP + threadIdx.x;
-        if (row < hidden) {
-            float sum = 0.0f;
-            for (uint32_t j = 0; j < top_k; ++j) {
-                const uint32_t s = ord_s[j];
-                const float o = res[s][threadIdx.x];
-                bad |= !kq_isfinite(o);
-                const float weighted = o * w_s[j];
-                sum = sum + weighted;
-            }
-            const float so = res[top_k][threadIdx.x];
-            const float gated = so * shared_scale[t];
-            const float v = sum + gated;
-            bad |= !kq_isfinite(so) || !kq_isfinite(sum) || !kq_isfinite(gated) ||
-                   !kq_isfinite(v);
-            out[(size_t)t * hidden + row] = v;
+    /* one thread per output row of the group (a group may have more rows
+     * than the launch has threads) */
+    for (uint32_t i = threadIdx.x; i < R::GROUP; i += blockDim.x) {
+        const uint32_t row = g * R::GROUP + i;
+        if (row >= hidden) break;
+        float *prow = a.part + (size_t)t * nslots * hidden + row;
+        if (!(seg & kSegFirst)) {
+            for (uint32_t s = slot0; s < slot1; ++s)
+                res[s][i] = prow[(size_t)s * hidden] + res[s][i];
         }
+        if (!combine) {
+            for (uint32_t s = slot0; s < slot1; ++s) prow[(size_t)s * hidden] = res[s][i];
+            continue;
+        }
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < top_k; ++j) {
+            const uint32_t s = ord_s[j];
+            const float o = res[s][i];
+            bad |= !kq_isfinite(o);
+            const float weighted = o * w_s[j];
+            sum = sum + weighted;
+        }
+        const float so = slot1 > top_k ? res[top_k][i] : prow[(size_t)top_k * hidden];
+        const float gated = so * a.shared_scale[t];
+        const float v = sum + gated;
+        bad |= !kq_isfinite(so) || !kq_isfinite(sum) || !kq_isfinite(gated) || !kq_isfinite(v);
+        a.out[(size_t)t * hidden + row] = v;
     }
-    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
-    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
 template <uint32_t TYPE, uint32_t COLS>
-hipError_t launch_gateup(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
-                         const float *hidden, uint32_t tokens, const kq_launch_moe_ws *ws,
-                         uint32_t act_stride, uint32_t *status, hipStream_t s) {
+hipError_t launch_gateup(const GateupArgs &a, uint32_t tokens, uint32_t slot0, uint32_t nslot,
+                         uint32_t col0, uint32_t seg, hipStream_t s) {
     constexpr int RT = 2;
-    const uint32_t rows = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+    const uint32_t both = a.inter > a.shared_inter ? a.inter : a.shared_inter;
+    const uint32_t rows = slot0 == a.top_k ? a.shared_inter
+                          : slot0 + nslot > a.top_k ? both : a.inter;
     const uint32_t rows_per_wave = kq::Rows<TYPE, COLS, 1, RT>::GROUP;
     const uint32_t waves = (rows + rows_per_wave - 1u) / rows_per_wave;
     const uint32_t blocks = (waves + 3u) / 4u;
-    hipLaunchKernelGGL((expert_gateup<TYPE, COLS, RT>), dim3(blocks, d->top_k + 1u, tokens),
-                       dim3(kThreads), 0, s, (const uint8_t *)w->gate, (const uint8_t *)w->up,
-                       (const uint8_t *)w->shared_gate, (const uint8_t *)w->shared_up, hidden,
-                       ws->ids, d->top_k, d->inter, d->shared_inter, act_stride, ws->act,
-                       status);
+    hipLaunchKernelGGL((expert_gateup<TYPE, COLS, RT>), dim3(blocks, nslot, tokens),
+                       dim3(kThreads), 0, s, a, slot0, col0, seg);
     return hipGetLastError();
 }
 
 template <uint32_t TYPE, uint32_t COLS>
-hipError_t launch_down(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
-                       uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t act_stride,
-                       float *out, uint32_t *status, hipStream_t s) {
+hipError_t launch_down(const DownArgs &a, uint32_t tokens, uint32_t slot0, uint32_t slot1,
+                       uint32_t col0, uint32_t seg, hipStream_t s) {
     constexpr int RT = 2;
     const uint32_t group = kq::Rows<TYPE, COLS, 1, RT>::GROUP;
-    const uint32_t blocks = (d->hidden + group - 1u) / group;
-    uint32_t waves = d->top_k + 1u;
+    const uint32_t blocks = (a.hidden + group - 1u) / group;
+    uint32_t waves = slot1 - slot0;
     if (waves > kDownWaves) waves = kDownWaves;
     hipLaunchKernelGGL((expert_down_combine<TYPE, COLS, RT>), dim3(blocks, tokens),
-                       dim3(64u * waves), 0, s, (const uint8_t *)w->down,
-                       (const uint8_t *)w->shared_down, ws->act, ws->ids, ws->order, ws->weights,
-                       ws->shared_scale, d->top_k, d->hidden, act_stride, out, status);
+                       dim3(64u * waves), 0, s, a, slot0, slot1, col0, seg);
     return hipGetLastError();
 }
 
-template <uint32_t TYPE>
-hipError_t gateup_cols(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
-                       const float *hidden, uint32_t tokens, const kq_launch_moe_ws *ws,
-                       uint32_t act_stride, uint32_t *status, hipStream_t s) {
-    switch (d->hidden) {
-    case 256: return launch_gateup<TYPE, 256u>(d, w, hidden, tokens, ws, act_stride, status, s);
-    case 512: return launch_gateup<TYPE, 512u>(d, w, hidden, tokens, ws, act_stride, status, s);
-    case 1024: return launch_gateup<TYPE, 1024u>(d, w, hidden, tokens, ws, act_stride, status, s);
-    case 2048: return launch_gateup<TYPE, 2048u>(d, w, hidden, tokens, ws, act_stride, status, s);
-    default: return hipErrorInvalidValue;
+/* Column segment widths with an engine instance, widest first; the 32-weight
+ * formats also take 128, 64 and 32. */
+constexpr uint32_t kSegWidths[] = {2048u, 1024u, 512u, 256u, 128u, 64u, 32u};
+
+bool small_type(uint32_t t) {
+    return t == KQ_LAUNCH_Q8_0 || t == KQ_LAUNCH_Q5_1 || t == KQ_LAUNCH_IQ4_NL;
+}
+
+/* Cuts cols into segment widths usable by every type given (0 = none);
+ * returns the count, or 0 when cols cannot be cut so. */
+uint32_t segments(uint32_t cols, uint32_t t0, uint32_t t1, uint32_t (&w)[16]) {
+    const uint32_t min = small_type(t0) && small_type(t1) ? 32u : 256u;
+    uint32_t n = 0, left = cols;
+    for (uint32_t k = 0; k < sizeof(kSegWidths) / sizeof(kSegWidths[0]) && left; ++k) {
+        if (kSegWidths[k] < min) break;
+        while (left >= kSegWidths[k] && n < 16u) {
+            w[n++] = kSegWidths[k];
+            left -= kSegWidths[k];
+        }
     }
+    return left == 0u && cols != 0u ? n : 0u;
 }
 
 template <uint32_t TYPE>
-hipError_t down_cols(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
-                     uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t act_stride,
-                     float *out, uint32_t *status, hipStream_t s) {
-    switch (d->inter) {
-    case 256: return launch_down<TYPE, 256u>(d, w, tokens, ws, act_stride, out, status, s);
-    case 512: return launch_down<TYPE, 512u>(d, w, tokens, ws, act_stride, out, status, s);
-    case 1024: return launch_down<TYPE, 1024u>(d, w, tokens, ws, act_stride, out, status, s);
-    case 2048: return launch_down<TYPE, 2048u>(d, w, tokens, ws, act_stride, out, status, s);
-    default: return hipErrorInvalidValue;
+hipError_t gateup_width(uint32_t width, const GateupArgs &a, uint32_t tokens, uint32_t slot0,
+                        uint32_t nslot, uint32_t col0, uint32_t seg, hipStream_t s) {
+    switch (width) {
+    case 2048: return launch_gateup<TYPE, 2048u>(a, tokens, slot0, nslot, col0, seg, s);
+    case 1024: return launch_gateup<TYPE, 1024u>(a, tokens, slot0, nslot, col0, seg, s);
+    case 512: return launch_gateup<TYPE, 512u>(a, tokens, slot0, nslot, col0, seg, s);
+    case 256: return launch_gateup<TYPE, 256u>(a, tokens, slot0, nslot, col0, seg, s);
+    default: break;
+    }
+    if constexpr (kq::small_block<TYPE>()) {
+        switch (width) {
+        case 128: return launch_gateup<TYPE, 128u>(a, tokens, slot0, nslot, col0, seg, s);
+        case 64: return launch_gateup<TYPE, 64u>(a, tokens, slot0, nslot, col0, seg, s);
+        case 32: return launch_gateup<TYPE, 32u>(a, tokens, slot0, nslot, col0, seg, s);
+        default: break;
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+template <uint32_t TYPE>
+hipError_t down_width(uint32_t width, const DownArgs &a, uint32_t tokens, uint32_t slot0,
+                      uint32_t slot1, uint32_t col0, uint32_t seg, hipStream_t s) {
+    switch (width) {
+    case 2048: return launch_down<TYPE, 2048u>(a, tokens, slot0, slot1, col0, seg, s);
+    case 1024: return launch_down<TYPE, 1024u>(a, tokens, slot0, slot1, col0, seg, s);
+    case 512: return launch_down<TYPE, 512u>(a, tokens, slot0, slot1, col0, seg, s);
+    case 256: return launch_down<TYPE, 256u>(a, tokens, slot0, slot1, col0, seg, s);
+    default: break;
+    }
+    if constexpr (kq::small_block<TYPE>()) {
+        switch (width) {
+        case 128: return launch_down<TYPE, 128u>(a, tokens, slot0, slot1, col0, seg, s);
+        case 64: return launch_down<TYPE, 64u>(a, tokens, slot0, slot1, col0, seg, s);
+        case 32: return launch_down<TYPE, 32u>(a, tokens, slot0, slot1, col0, seg, s);
+        default: break;
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+#define KQ_TYPE_SWITCH(TYPE_ID, CALL)                                   \
+    switch (TYPE_ID) {                                                  \
+    case KQ_LAUNCH_Q4_K: { constexpr uint32_t T_ = KQ_LAUNCH_Q4_K; return CALL; }     \
+    case KQ_LAUNCH_Q6_K: { constexpr uint32_t T_ = KQ_LAUNCH_Q6_K; return CALL; }     \
+    case KQ_LAUNCH_Q8_0: { constexpr uint32_t T_ = KQ_LAUNCH_Q8_0; return CALL; }     \
+    case KQ_LAUNCH_Q5_K: { constexpr uint32_t T_ = KQ_LAUNCH_Q5_K; return CALL; }     \
+    case KQ_LAUNCH_Q5_1: { constexpr uint32_t T_ = KQ_LAUNCH_Q5_1; return CALL; }     \
+    case KQ_LAUNCH_IQ4_NL: { constexpr uint32_t T_ = KQ_LAUNCH_IQ4_NL; return CALL; } \
+    default: return hipErrorInvalidValue;                               \
+    }
+
+hipError_t gateup_launch(uint32_t type, uint32_t width, const GateupArgs &a, uint32_t tokens,
+                         uint32_t slot0, uint32_t nslot, uint32_t col0, uint32_t seg,
+                         hipStream_t s) {
+    KQ_TYPE_SWITCH(type, gateup_width<T_>(width, a, tokens, slot0, nslot, col0, seg, s))
+}
+
+hipError_t down_launch(uint32_t type, uint32_t width, const DownArgs &a, uint32_t tokens,
+                       uint32_t slot0, uint32_t slot1, uint32_t col0, uint32_t seg,
+                       hipStream_t s) {
+    KQ_TYPE_SWITCH(type, down_width<T_>(width, a, tokens, slot0, slot1, col0, seg, s))
+}
+
+#undef KQ_TYPE_SWITCH
+
+uint32_t row_bytes_of(uint32_t type, uint32_t cols) {
+    switch (type) {
+    case KQ_LAUNCH_Q4_K: return cols / 256u * 144u;
+    case KQ_LAUNCH_Q5_K: return cols / 256u * 176u;
+    case KQ_LAUNCH_Q6_K: return cols / 256u * 210u;
+    case KQ_LAUNCH_Q8_0: return cols / 32u * 34u;
+    case KQ_LAUNCH_Q5_1: return cols / 32u * 24u;
+    case KQ_LAUNCH_IQ4_NL: return cols / 32u * 18u;
+    default: return 0u;
     }
 }
 
@@ -1220,13 +1361,20 @@ bool quant_type(uint32_t t) {
            t == KQ_LAUNCH_Q8_0 || t == KQ_LAUNCH_Q5_1 || t == KQ_LAUNCH_IQ4_NL;
 }
 
-bool cols_ok(uint32_t c) { return c == 256u || c == 512u || c == 1024u || c == 2048u; }
 
 }  // namespace
 
 extern "C" uint32_t kq_launch_moe_experts_padded(uint32_t experts) { return pad64(experts + 1u); }
 
 static uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
+
+/* outp holds, per token and slot, the grouped path's down outputs or the
+ * per-token path's partial sums of column segments: hidden floats for
+ * down, 2 x intermediate for gate/up */
+static uint64_t outp_row(const kq_launch_moe_dims *d) {
+    const uint64_t ai = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+    return d->hidden > 2u * ai ? d->hidden : 2u * ai;
+}
 
 extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t tokens) {
     const uint64_t ep = pad64(d->experts + 1u);
@@ -1239,7 +1387,7 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * (d->top_k + 1u) * ai * 4u);    /* act */
     b += align256((uint64_t)(d->experts + 1u) * 4u);                 /* offsets */
     b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
-    b += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u); /* outp */
+    b += align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u); /* outp */
     b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
     b += 256u;                                           /* certified flag, arrival count */
     return b;
@@ -1262,7 +1410,7 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->offsets = (uint32_t *)p; p += align256((uint64_t)(d->experts + 1u) * 4u);
     ws->perm_tok = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->pos = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
-    ws->outp = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * d->hidden * 4u);
+    ws->outp = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u);
     ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
     ws->certified = (uint32_t *)p;
     ws->arrive = (uint32_t *)p + 32; /* its own 128-byte line in the same slot */
@@ -1270,16 +1418,20 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
                                        const kq_launch_moe_weights *w) {
+    uint32_t seg[16];
     if (d->hidden % 4u != 0u || d->experts + 1u > 1024u || d->top_k < 1u ||
         d->top_k > d->experts || d->top_k > 64u)
         return 0;
     if (w == nullptr) return 1;
+    if (d->inter != d->shared_inter || d->hidden > 65536u || d->inter > 65536u) return 0;
+    /* gate and up share a type (routed, and shared); each role's rows are
+     * whole blocks cut into segments that both of its types can run */
     if (!quant_type(w->gate_type) || w->up_type != w->gate_type ||
-        w->shared_gate_type != w->gate_type || w->shared_up_type != w->gate_type)
+        !quant_type(w->shared_gate_type) || w->shared_up_type != w->shared_gate_type)
         return 0;
-    if (!quant_type(w->down_type) || w->shared_down_type != w->down_type) return 0;
-    if (!cols_ok(d->hidden) || !cols_ok(d->inter) || d->inter != d->shared_inter) return 0;
-    return 1;
+    if (!quant_type(w->down_type) || !quant_type(w->shared_down_type)) return 0;
+    return segments(d->hidden, w->gate_type, w->shared_gate_type, seg) != 0u &&
+           segments(d->inter, w->down_type, w->shared_down_type, seg) != 0u;
 }
 
 extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
@@ -1312,6 +1464,7 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
         case 512: KQ_CERTIFIED_ROUTE(512u); break;
         case 1024: KQ_CERTIFIED_ROUTE(1024u); break;
         case 2048: KQ_CERTIFIED_ROUTE(2048u); break;
+        case 2560: KQ_CERTIFIED_ROUTE(2560u); break;
         default: have = false;
         }
 #undef KQ_CERTIFIED_ROUTE
@@ -1327,6 +1480,7 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
         case 512: KQ_ROUTER_DECODE(512u); break;
         case 1024: KQ_ROUTER_DECODE(1024u); break;
         case 2048: KQ_ROUTER_DECODE(2048u); break;
+        case 2560: KQ_ROUTER_DECODE(2560u); break;
         default: fused = false;
         }
     }
@@ -1361,37 +1515,66 @@ extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
                                             const kq_launch_moe_weights *w, const float *hidden,
                                             uint32_t tokens, const kq_launch_moe_ws *ws,
                                             float *out, uint32_t *status, hipStream_t s) {
-    const uint32_t act_stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
-    hipError_t e;
-    switch (w->gate_type) {
-    case KQ_LAUNCH_Q4_K:
-        e = gateup_cols<KQ_LAUNCH_Q4_K>(d, w, hidden, tokens, ws, act_stride, status, s);
-        break;
-    case KQ_LAUNCH_Q6_K:
-        e = gateup_cols<KQ_LAUNCH_Q6_K>(d, w, hidden, tokens, ws, act_stride, status, s);
-        break;
-    case KQ_LAUNCH_Q8_0:
-        e = gateup_cols<KQ_LAUNCH_Q8_0>(d, w, hidden, tokens, ws, act_stride, status, s);
-        break;
-    case KQ_LAUNCH_Q5_K:
-        e = gateup_cols<KQ_LAUNCH_Q5_K>(d, w, hidden, tokens, ws, act_stride, status, s);
-        break;
-    case KQ_LAUNCH_Q5_1:
-        e = gateup_cols<KQ_LAUNCH_Q5_1>(d, w, hidden, tokens, ws, act_stride, status, s);
-        break;
-    case KQ_LAUNCH_IQ4_NL:
-        e = gateup_cols<KQ_LAUNCH_IQ4_NL>(d, w, hidden, tokens, ws, act_stride, status, s);
-        break;
-    default: return hipErrorInvalidValue;
+    const uint32_t K = d->top_k;
+    uint32_t gw[16], dw[16];
+    const uint32_t ng = segments(d->hidden, w->gate_type, w->shared_gate_type, gw);
+    const uint32_t nd = segments(d->inter, w->down_type, w->shared_down_type, dw);
+    if (ng == 0u || nd == 0u) return hipErrorInvalidValue;
+    GateupArgs ga;
+    ga.gate = (const uint8_t *)w->gate;
+    ga.up = (const uint8_t *)w->up;
+    ga.sgate = (const uint8_t *)w->shared_gate;
+    ga.sup = (const uint8_t *)w->shared_up;
+    ga.x = hidden;
+    ga.ids = ws->ids;
+    ga.top_k = K;
+    ga.inter = d->inter;
+    ga.shared_inter = d->shared_inter;
+    ga.hidden = d->hidden;
+    ga.rstride = row_bytes_of(w->gate_type, d->hidden);
+    ga.srstride = row_bytes_of(w->shared_gate_type, d->hidden);
+    ga.act_stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+    ga.act = ws->act;
+    ga.part = ws->outp;
+    ga.status = status;
+    /* the shared expert rides in the routed launch when its type matches */
+    const bool gsame = w->shared_gate_type == w->gate_type;
+    hipError_t e = hipSuccess;
+    for (uint32_t k = 0, col = 0; k < ng && e == hipSuccess; col += gw[k], ++k) {
+        const uint32_t seg = (k == 0u ? kSegFirst : 0u) | (k + 1u == ng ? kSegLast : 0u);
+        e = gateup_launch(w->gate_type, gw[k], ga, tokens, 0u, gsame ? K + 1u : K, col, seg, s);
+        if (e == hipSuccess && !gsame)
+            e = gateup_launch(w->shared_gate_type, gw[k], ga, tokens, K, 1u, col, seg, s);
     }
     if (e != hipSuccess) return e;
-    switch (w->down_type) {
-    case KQ_LAUNCH_Q4_K: return down_cols<KQ_LAUNCH_Q4_K>(d, w, tokens, ws, act_stride, out, status, s);
-    case KQ_LAUNCH_Q6_K: return down_cols<KQ_LAUNCH_Q6_K>(d, w, tokens, ws, act_stride, out, status, s);
-    case KQ_LAUNCH_Q8_0: return down_cols<KQ_LAUNCH_Q8_0>(d, w, tokens, ws, act_stride, out, status, s);
-    case KQ_LAUNCH_Q5_K: return down_cols<KQ_LAUNCH_Q5_K>(d, w, tokens, ws, act_stride, out, status, s);
-    case KQ_LAUNCH_Q5_1: return down_cols<KQ_LAUNCH_Q5_1>(d, w, tokens, ws, act_stride, out, status, s);
-    case KQ_LAUNCH_IQ4_NL: return down_cols<KQ_LAUNCH_IQ4_NL>(d, w, tokens, ws, act_stride, out, status, s);
-    default: return hipErrorInvalidValue;
+    DownArgs da;
+    da.down = (const uint8_t *)w->down;
+    da.sdown = (const uint8_t *)w->shared_down;
+    da.act = ws->act;
+    da.ids = ws->ids;
+    da.order = ws->order;
+    da.weights = ws->weights;
+    da.shared_scale = ws->shared_scale;
+    da.top_k = K;
+    da.hidden = d->hidden;
+    da.rstride = row_bytes_of(w->down_type, d->inter);
+    da.srstride = row_bytes_of(w->shared_down_type, d->inter);
+    da.act_stride = ga.act_stride;
+    da.part = ws->outp;
+    da.out = out;
+    da.status = status;
+    const bool dsame = w->shared_down_type == w->down_type;
+    /* a shared expert of its own type is finished (into part[t][K]) before
+     * the routed launches that combine it */
+    if (!dsame) {
+        for (uint32_t k = 0, col = 0; k < nd && e == hipSuccess; col += dw[k], ++k) {
+            const uint32_t seg = (k == 0u ? kSegFirst : 0u) | (k + 1u == nd ? kSegLast : 0u);
+            e = down_launch(w->shared_down_type, dw[k], da, tokens, K, K + 1u, col, seg, s);
+        }
     }
+    for (uint32_t k = 0, col = 0; k < nd && e == hipSuccess; col += dw[k], ++k) {
+        const uint32_t seg = (k == 0u ? kSegFirst : 0u) | (k + 1u == nd ? kSegLast | kSegCombine : 0u);
+        e = down_launch(w->down_type, dw[k], da, tokens, 0u, dsame ? K + 1u : K, col, seg, s);
+    }
+    return e;
 }

@@ -759,8 +759,9 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     lw.shared_gate_weight = w->shared_gate_weight;
     if (!kq_launch_moe_supported(&d, &lw))
         return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
-                       "device MoE needs Q5_1/Q8_0/IQ4_NL/Q4_K/Q5_K/Q6_K roles (gate=up types, shared like routed), "
-                       "hidden and intermediate in {256,512,1024,2048}, equal intermediates");
+                       "device MoE needs Q5_1/Q8_0/IQ4_NL/Q4_K/Q5_K/Q6_K roles (gate and up of one "
+                       "type, routed and shared each), rows of whole blocks of every type that "
+                       "reads them, equal intermediates");
     if (!aligned(w->routed_gate, 16u) || !aligned(w->routed_up, 16u) ||
         !aligned(w->routed_down, 16u) || !aligned(w->shared_gate, 16u) ||
         !aligned(w->shared_up, 16u) || !aligned(w->shared_down, 16u) || !aligned(out, 4u))

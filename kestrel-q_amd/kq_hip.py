@@ -406,13 +406,17 @@ class Context:
                                                  scratch_bytes, C.byref(d)), d)
 
 
-def moe_weights(bufs: dict, gate_type=TYPE_Q4_K, down_type=TYPE_Q6_K) -> MoeWeights:
+def moe_weights(bufs: dict, gate_type=TYPE_Q4_K, down_type=TYPE_Q6_K,
+                shared_gate_type=None, shared_down_type=None) -> MoeWeights:
     """bufs: role -> DeviceBuffer (router, gate, up, down, shared_gate,
-    shared_up, shared_down, shared_gate_weight)."""
+    shared_up, shared_down, shared_gate_weight). The shared expert takes the
+    routed types unless given."""
     P = lambda k: C.c_void_p(bufs[k].ptr)
+    sg = gate_type if shared_gate_type is None else shared_gate_type
+    sd = down_type if shared_down_type is None else shared_down_type
     return MoeWeights(P("router"), gate_type, P("gate"), gate_type, P("up"), down_type,
-                      P("down"), gate_type, P("shared_gate"), gate_type, P("shared_up"),
-                      down_type, P("shared_down"), P("shared_gate_weight"))
+                      P("down"), sg, P("shared_gate"), sg, P("shared_up"),
+                      sd, P("shared_down"), P("shared_gate_weight"))
 
 
 # ---------------------------------------------------------------- GGUF files

@@ -165,11 +165,12 @@ def quant_matrix(fmt: str, key: int, rows: int, cols: int) -> np.ndarray:
 
 
 def moe_weights(workload: int, hidden: int, experts: int, inter: int, shared_inter: int,
-                gate_fmt: str = "Q4_K", down_fmt: str = "Q6_K") -> dict:
+                gate_fmt: str = "Q4_K", down_fmt: str = "Q6_K", shared_gate_fmt: str = None,
+                shared_down_fmt: str = None) -> dict:
     """MoE layer weights: fp32 router ~N(0,0.02), per-expert gate/up
     [inter, hidden] and down [hidden, inter] packed matrices stored back to
-    back, a shared expert of the same formats and an fp32 shared gate vector
-    ~N(0, 0.02)."""
+    back, a shared expert (of the routed formats unless given) and an fp32
+    shared gate vector ~N(0, 0.02)."""
     w = {"router": normal_f32(stream_key(workload, R_ROUTER), experts * hidden, 0.02)}
     gate_gen, qk_g, _ = BLOCK_GEN[gate_fmt]
     down_gen, qk_d, _ = BLOCK_GEN[down_fmt]
@@ -179,12 +180,14 @@ def moe_weights(workload: int, hidden: int, experts: int, inter: int, shared_int
                               .reshape(-1) for e in range(experts)])
     w["down"] = np.concatenate([down_gen(stream_key(workload, R_DOWN, e), hidden * inter // qk_d)
                                 .reshape(-1) for e in range(experts)])
-    w["shared_gate"] = gate_gen(stream_key(workload, R_SHARED_GATE),
-                                shared_inter * hidden // qk_g).reshape(-1)
-    w["shared_up"] = gate_gen(stream_key(workload, R_SHARED_UP),
-                              shared_inter * hidden // qk_g).reshape(-1)
-    w["shared_down"] = down_gen(stream_key(workload, R_SHARED_DOWN),
-                                hidden * shared_inter // qk_d).reshape(-1)
+    sg_gen, qk_sg, _ = BLOCK_GEN[shared_gate_fmt or gate_fmt]
+    sd_gen, qk_sd, _ = BLOCK_GEN[shared_down_fmt or down_fmt]
+    w["shared_gate"] = sg_gen(stream_key(workload, R_SHARED_GATE),
+                              shared_inter * hidden // qk_sg).reshape(-1)
+    w["shared_up"] = sg_gen(stream_key(workload, R_SHARED_UP),
+                            shared_inter * hidden // qk_sg).reshape(-1)
+    w["shared_down"] = sd_gen(stream_key(workload, R_SHARED_DOWN),
+                              hidden * shared_inter // qk_sd).reshape(-1)
     w["shared_gate_weight"] = normal_f32(stream_key(workload, R_SHARED_GATE_W), hidden, 0.02)
     return w
 

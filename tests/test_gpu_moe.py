@@ -420,3 +420,71 @@ def test_moe_decode_ties_fall_back_to_exact_chains(ctx, pattern):
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in ROLES.items()}, x, trace=True)
     assert np.array_equal(ctx.download(dids, np.uint32, K)[None, :], tr["selected_ids"])
     assert_close(ctx.download(dout, np.float32, H)[None, :], ref)
+
+
+def run_layer(ctx, H, E, K, I, T, gate_fmt, down_fmt, sgate_fmt, sdown_fmt, seed):
+    """One MoE call on fresh weights; returns (out, ids, ref, trace)."""
+    w = S.moe_weights(seed, H, E, I, I, gate_fmt=gate_fmt, down_fmt=down_fmt,
+                      shared_gate_fmt=sgate_fmt, shared_down_fmt=sdown_fmt)
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    x = S.normal_f32(S.stream_key(seed, S.R_HIDDEN), T * H).reshape(T, H)
+    n = cfg.scratch_bytes(T)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(T * H * 4), ctx.alloc(T * K * 4)
+    t = kq_hip.TYPE_IDS
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, t[gate_fmt], t[down_fmt], t[sgate_fmt],
+                                            t[sdown_fmt]), dx, T, dout, dids, scratch, n)
+    out = ctx.download(dout, np.float32, T * H).reshape(T, H)
+    ids = ctx.download(dids, np.uint32, T * K).reshape(T, K)
+    roles = {"router": kq_oracle.F32, "gate": t[gate_fmt], "up": t[gate_fmt],
+             "down": t[down_fmt], "shared_gate": t[sgate_fmt], "shared_up": t[sgate_fmt],
+             "shared_down": t[sdown_fmt], "shared_gate_weight": kq_oracle.F32}
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    ref, tr = kq_oracle.moe_execute(dims, {k: (r, w[k]) for k, r in roles.items()}, x, trace=True,
+                                    threads=oracle_threads())
+    for b in list(bufs.values()) + [scratch, dx, dout, dids]:
+        b.close()
+    return out, ids, ref, tr
+
+
+def test_moe_reference_model_layer(ctx):
+    # The reference model's MoE layer at full size (Qwen3.8-Flash-Next layer
+    # 0 in its GGUF): hidden 2560, 512 experts, top-10, intermediate 640,
+    # Q4_K gate/up, Q5_1 routed down, a Q8_0 shared expert. Rows are cut
+    # into column segments (2048 + 512 for gate/up, 512 + 128 for down).
+    say("reference-model layer 2560/512/10/640")
+    out, ids, ref, tr = run_layer(ctx, 2560, 512, 10, 640, 1, "Q4_K", "Q5_1", "Q8_0", "Q8_0",
+                                  S.W_MOE + 2560)
+    assert np.array_equal(ids, tr["selected_ids"])
+    assert_close(out, ref)
+
+
+@pytest.mark.parametrize("H,E,K,I,T,g,d,sg,sd", [
+    (2560, 64, 8, 640, 3, "Q4_K", "Q5_1", "Q8_0", "Q8_0"),
+    (768, 32, 4, 384, 2, "Q5_K", "Q5_1", "Q5_K", "Q5_1"),     # 512+256, 256+128
+    (640, 16, 2, 96, 1, "Q8_0", "IQ4_NL", "Q5_1", "Q8_0"),    # 512+128, 64+32
+    (1280, 16, 3, 320, 2, "Q4_K", "Q8_0", "Q6_K", "IQ4_NL"),  # 1024+256, 256+64
+    (3072, 16, 2, 256, 1, "Q6_K", "Q4_K", "Q4_K", "Q6_K"),    # 2048+1024 gate/up
+    (512, 16, 4, 256, 16, "Q4_K", "Q6_K", "Q8_0", "Q6_K"),    # mixed shared, many tokens
+], ids=["real-64e-3tok", "768x384", "640x96", "1280x320", "3072x256", "mixed-16tok"])
+def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
+    seed = S.W_MOE + 3000 + H + I + T
+    out, ids, ref, tr = run_layer(ctx, H, E, K, I, T, g, d, sg, sd, seed)
+    assert np.array_equal(ids, tr["selected_ids"])
+    assert_close(out, ref)
+
+
+def test_moe_rejects_unsplittable_rows(ctx):
+    # 640 columns of a Q4_K down row are not whole 256-weight blocks
+    H, E, K, I = 512, 16, 2, 640
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    w = S.moe_weights(S.W_MOE + 77, H, E, I, I, gate_fmt="Q8_0", down_fmt="Q8_0")
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    n = cfg.scratch_bytes(1)
+    scratch, dx, dout = ctx.alloc(n), ctx.upload(np.ones((1, H), np.float32)), ctx.alloc(H * 4)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, kq_hip.TYPE_Q8_0, kq_hip.TYPE_Q4_K), dx, 1,
+                        dout, None, scratch, n)
+    assert e.value.name == "UNSUPPORTED_TENSOR_TYPE"
+    for b in list(bufs.values()) + [scratch, dx, dout]:
+        b.close()
