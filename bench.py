@@ -180,20 +180,37 @@ def wl_dequant(ctx, fmt, warmup, steps, graph):
             "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "weights": n}
 
 
-def moe_layer(ctx, H=2048, E=512, K=10, I=512):
-    w = S.moe_weights(S.W_MOE, H, E, I, I)
-    return w, kq_hip.MoeConfig(H, E, K, I, I)
+# MoE layers measured: the configuration the headline MoE figures are quoted
+# on, and the reference model's own layer (hidden 2560, intermediate 640,
+# Q4_K gate/up, Q5_1 routed down, Q8_0 shared expert).
+MOE_LAYERS = {
+    "2048x512": dict(H=2048, E=512, K=10, I=512, gate="Q4_K", down="Q6_K", sgate="Q4_K",
+                     sdown="Q6_K", seed=S.W_MOE),
+    "2560x640": dict(H=2560, E=512, K=10, I=640, gate="Q4_K", down="Q5_1", sgate="Q8_0",
+                     sdown="Q8_0", seed=S.W_MOE + 2560),
+}
 
 
-def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache):
-    H, E, K, I = 2048, 512, 10, 512
-    if "w" not in layer_cache:
-        layer_cache["w"], layer_cache["cfg"] = moe_layer(ctx)
+def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512"):
+    L = MOE_LAYERS[layer]
+    H, E, K, I = L["H"], L["E"], L["K"], L["I"]
+    if layer_cache.get("layer") != layer:
+        layer_cache.clear()
+        layer_cache["layer"] = layer
+        layer_cache["w"] = S.moe_weights(L["seed"], H, E, I, I, gate_fmt=L["gate"],
+                                         down_fmt=L["down"], shared_gate_fmt=L["sgate"],
+                                         shared_down_fmt=L["sdown"])
+        layer_cache["cfg"] = kq_hip.MoeConfig(H, E, K, I, I)
     w, cfg = layer_cache["w"], layer_cache["cfg"]
     layer_bytes = sum(v.nbytes for v in w.values())
-    # bytes touched per decode step ~26.6 MB; rotate whole-layer replicas so
-    # a replica's router/shared/expert rows are not MALL-resident on reuse
-    touched = 4_194_304 + (K + 1) * 2_039_808 + 8192 if tokens == 1 else layer_bytes
+    # bytes one decode step reads: the router, K routed experts' gate, up and
+    # down, the shared expert and its gate vector (26.6 MB for 2048x512);
+    # whole-layer replicas rotate so that reuse does not hit the MALL
+    expert = (w["gate"].nbytes + w["up"].nbytes + w["down"].nbytes) // E
+    shared = w["shared_gate"].nbytes + w["shared_up"].nbytes + w["shared_down"].nbytes
+    touched = w["router"].nbytes + K * expert + shared + w["shared_gate_weight"].nbytes
+    if tokens > 1:
+        touched = layer_bytes
     nrep = max(2, min(24, -(-MALL_DEFEAT_BYTES // touched)))
     if tokens > 1:
         nrep = 1
@@ -209,9 +226,11 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache):
                 bufs[k] = b
         layers.append(bufs)
     ctx.synchronize()
-    mw = [kq_hip.moe_weights(b) for b in layers]
+    t = kq_hip.TYPE_IDS
+    mw = [kq_hip.moe_weights(b, t[L["gate"]], t[L["down"]], t[L["sgate"]], t[L["sdown"]])
+          for b in layers]
     ntok_inputs = 16
-    x = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 1000 + tokens),
+    x = S.normal_f32(S.stream_key(L["seed"], S.R_HIDDEN, 1000 + tokens),
                      ntok_inputs * tokens * H).reshape(ntok_inputs, tokens * H)
     dxs = [ctx.upload(x[j]) for j in range(ntok_inputs)]
     n = cfg.scratch_bytes(tokens)
@@ -227,13 +246,10 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache):
             b.close()
     for b in dxs + [scratch, out]:
         b.close()
-    if tokens == 1:
-        nbytes = touched + H * 4 * 2
-    else:
-        nbytes = layer_bytes + 2 * tokens * H * 4
+    nbytes = touched + 2 * tokens * H * 4
     return {"ms_per_step": ms, "tokens_per_s": tokens / ms * 1e3, "bytes_per_step": nbytes,
             "GBps": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-            "layer_replicas": nrep, "tokens": tokens}
+            "layer_replicas": nrep, "tokens": tokens, "layer": layer}
 
 
 def wl_lm_head(ctx, batch, warmup, steps, graph, fmt="Q6_K", V=151936, H=2048):
@@ -289,7 +305,8 @@ def cpu_baseline(threads: int, budget_s: float = 3.0) -> dict:
     for th in sorted({1, threads}):
         s, n = timeit(lambda: O.matvec(O.Q4_K, w, 4096, 2048, x, threads=th), budget_s)
         res[f"q4k_matvec_{th}t"] = {"s_per_step": s, "GBps": nbytes / s / 1e9, "runs": n}
-    wts, _ = moe_layer(None)
+    L = MOE_LAYERS["2048x512"]
+    wts = S.moe_weights(L["seed"], 2048, 512, 512, 512)
     roles = {"router": O.F32, "gate": O.Q4_K, "up": O.Q4_K, "down": O.Q6_K,
              "shared_gate": O.Q4_K, "shared_up": O.Q4_K, "shared_down": O.Q6_K,
              "shared_gate_weight": O.F32}
@@ -365,6 +382,8 @@ def main() -> int:
         run("lm_head_q8_0_248320x2560_b1",
             lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph, "Q8_0", 248320, 2560))
         run("moe_prefill_512", lambda: wl_moe(ctx, 512, 1, 3, graph, cache))
+        run("moe_decode_1tok_2560x640",
+            lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))
         if wanted == "hbm_copy_64mb":
             run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))
     head = work.get(HEADLINE)
