@@ -163,6 +163,14 @@ __device__ __forceinline__ void kq_k_scale_pair(uint32_t p, uint32_t w0, uint32_
     *m1 = sel((z >> 8) & 63u, ((w >> 12) & 15u) | ((z >> 10) & 0x30u));
 }
 
+/* Workgroup barrier that orders LDS accesses only: global loads issued
+ * before it stay in flight across it. */
+__device__ __forceinline__ void kq_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 /*
  * Raw buffer loads: a 128-bit resource (base, byte count) in scalar
  * registers plus a 32-bit per-lane offset, so a row walk costs one 32-bit

@@ -66,15 +66,23 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
 
     typename R::Lane ln;
     ln.setup(l);
-    const KqBuf wb = kq_buf(W, (rows - 1u) * row_bytes + R::RB);
+    const uint32_t wbytes = (rows - 1u) * row_bytes + R::RB;
+    const KqBuf wb = kq_buf(W, wbytes);
     Raw ra[RT], rb[RT];
     uint32_t g = wave;
-    /* each lane loads its own activations (L2-resident after the first
-     * waves) before the first group's weights: the loads complete in order,
-     * so the activation sums are formed while the weights are in flight and
-     * nothing waits on a workgroup barrier */
-    if (ln.load_x(x, x_stride)) kq_flag(status, KQ_DEV_INPUT);
-    if (g < ngroups) R::load_group(ln, wb, g, rows, sub, ra, row_bytes);
+    /* The workgroup requests its activations (once, into LDS), then every
+     * wave its first group's weights, without a branch; the activation
+     * loads complete first, are checked and written to LDS behind an
+     * LDS-only barrier while the weights are still in flight. The check is
+     * flagged at the end. */
+    using XS = kq::XStage<R, B, kThreads>;
+    __shared__ __align__(16) float4 xs[XS::NP];
+    XS stage;
+    stage.issue(x, x_stride, threadIdx.x);
+    R::load_group_oob(ln, wb, g, rows, sub, ra, row_bytes, wbytes + 64u);
+    const bool xbad = stage.commit(xs, threadIdx.x);
+    kq_lds_barrier();
+    ln.load_x(kq::XLds{xs, l, R::LPR});
 
     bool bad = false, malformed = false;
     float best_v[B];
@@ -115,6 +123,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
         finish(rb, g);
         g = gn;
     }
+    if (xbad) kq_flag(status, KQ_DEV_INPUT);
     if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
     if (part_v != nullptr) {
@@ -196,11 +205,11 @@ uint32_t group_rows(uint32_t cols, uint32_t rt) {
     return (lanes >= 64u ? 1u : 64u / lanes) * rt;
 }
 
-/* RT = 2 (one group per wave) for matrices whose RT = 4 grid would leave
+/* RT = 1 (one group per wave) for matrices whose RT = 4 grid would leave
  * the GPU under-filled */
 uint32_t pick_rt(uint32_t rows, uint32_t cols) {
     const uint32_t groups4 = (rows + group_rows(cols, 4) - 1u) / group_rows(cols, 4);
-    return groups4 >= kResidentWaves ? 4u : 2u;
+    return groups4 >= kResidentWaves ? 4u : 1u;
 }
 
 /* workgroups of `kernel` that fit on the device at once */
@@ -226,7 +235,7 @@ struct Seg {
 };
 
 /* Launches one segment, or (waves != nullptr) only reports the number of
- * waves it would launch: one group per wave for RT = 2; for RT = 4 as many
+ * waves it would launch: one group per wave for RT = 1; for RT = 4 as many
  * workgroups as are resident at once, striding over the groups. */
 template <uint32_t TYPE, uint32_t COLS, int B>
 hipError_t launch_one(const uint8_t *W, uint32_t rows, Seg sg, const float *x, float *y,
@@ -249,7 +258,7 @@ hipError_t launch_one(const uint8_t *W, uint32_t rows, Seg sg, const float *x, f
         hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 4>), dim3(blocks), dim3(kThreads), 0, s,
                            W, rows, sg.row_bytes, x, sg.x_stride, y, sg.y_prev, st, pv, pi, ps);
     else
-        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 2>), dim3(blocks), dim3(kThreads), 0, s,
+        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 1>), dim3(blocks), dim3(kThreads), 0, s,
                            W, rows, sg.row_bytes, x, sg.x_stride, y, sg.y_prev, st, pv, pi, ps);
     return hipGetLastError();
 }

@@ -1057,15 +1057,21 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t
     ln.setup(l);
     Raw rg[RT], ru[RT];
     uint32_t g = wave;
-    const KqBuf gb = kq_buf(G + boff, rows * stride - boff),
-                ub = kq_buf(U + boff, rows * stride - boff);
-    /* each lane loads its slice of the token's hidden state first, then its
-     * gate and up rows (the loads complete in order) */
-    if (ln.load_x(a.x + (size_t)t * a.hidden + col0, COLS)) kq_flag(a.status, KQ_DEV_INPUT);
-    if (g < ngroups) {
-        R::load_group(ln, gb, g, rows, sub, rg, stride);
-        R::load_group(ln, ub, g, rows, sub, ru, stride);
-    }
+    const uint32_t wbytes = rows * stride - boff;
+    const KqBuf gb = kq_buf(G + boff, wbytes), ub = kq_buf(U + boff, wbytes);
+    /* the workgroup requests the token's hidden state (once, into LDS),
+     * then every wave its first gate and up rows without a branch; the
+     * hidden state is checked and written to LDS behind an LDS-only barrier
+     * while the weights are in flight, and the check is flagged at the end */
+    using XS = kq::XStage<R, 1, kThreads>;
+    __shared__ __align__(16) float4 xs[XS::NP];
+    XS stage;
+    stage.issue(a.x + (size_t)t * a.hidden + col0, COLS, threadIdx.x);
+    R::load_group_oob(ln, gb, g, rows, sub, rg, stride, wbytes + 64u);
+    R::load_group_oob(ln, ub, g, rows, sub, ru, stride, wbytes + 64u);
+    const bool xbad = stage.commit(xs, threadIdx.x);
+    kq_lds_barrier();
+    ln.load_x(kq::XLds{xs, l, R::LPR});
     bool bad = false, malformed = false;
     const size_t at = (size_t)t * (a.top_k + 1u) + slot;
     float *out = a.act + at * a.act_stride;
@@ -1101,6 +1107,7 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t
             }
         }
     }
+    if (xbad) kq_flag(a.status, KQ_DEV_INPUT);
     if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }

@@ -20,14 +20,33 @@
 
 namespace kq {
 
-template <int B>
-__device__ __forceinline__ bool load_x8(const float *x, uint32_t stride, uint32_t k,
-                                        float (&dst)[B][8]) {
+/* Activation sources. A lane takes its 32 activations per batch column as
+ * 8 float4 chunks c = 0..7 in a fixed order (natural column k of chunk c is
+ * Lane::xk(l, c)); a source returns batch column b's chunk. */
+struct XGlobal {
+    const float *x;
+    uint32_t stride;
+    __device__ __forceinline__ float4 operator()(int b, uint32_t k, int) const {
+        return *(const float4 *)(x + (size_t)b * stride + k);
+    }
+};
+/* LDS image [b][c][lpr] of float4 (XStage): consecutive lanes read
+ * consecutive 16-byte words, lanes of one row position share a word */
+struct XLds {
+    const float4 *xs;
+    uint32_t l, lpr;
+    __device__ __forceinline__ float4 operator()(int b, uint32_t, int c) const {
+        return xs[((uint32_t)b * 8u + (uint32_t)c) * lpr + l];
+    }
+};
+
+/* chunks 2q and 2q + 1 (natural columns k .. k + 7) of every batch column */
+template <int B, class X>
+__device__ __forceinline__ bool load_x8(const X &src, uint32_t k, int q, float (&dst)[B][8]) {
     bool bad = false;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-        const float4 *p = (const float4 *)(x + (size_t)b * stride + k);
-        const float4 u = p[0], v = p[1];
+        const float4 u = src(b, k, 2 * q), v = src(b, k + 4u, 2 * q + 1);
         dst[b][0] = u.x; dst[b][1] = u.y; dst[b][2] = u.z; dst[b][3] = u.w;
         dst[b][4] = v.x; dst[b][5] = v.y; dst[b][6] = v.z; dst[b][7] = v.w;
 #pragma unroll
@@ -76,10 +95,19 @@ struct LaneQ4K {
         qoff = 16u + 32u * gq + 16u * h;
         k0 = 256u * bb + 64u * gq + 16u * h;
     }
+    /* natural column of chunk c of lane l */
+    __device__ static __forceinline__ uint32_t xk(uint32_t l, int c) {
+        const uint32_t k = 256u * (l >> 3) + 64u * ((l & 7u) >> 1) + 16u * (l & 1u);
+        return k + (c >= 4 ? 32u : 0u) + 8u * ((uint32_t)(c >> 1) & 1u) + 4u * ((uint32_t)c & 1u);
+    }
     __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        return load_x(XGlobal{x, stride});
+    }
+    template <class X>
+    __device__ __forceinline__ bool load_x(const X &src) {
         float t0[B][8], t1[B][8], s0[B], s1[B];
-        bool bad = load_x8<B>(x, stride, k0, t0);
-        bad |= load_x8<B>(x, stride, k0 + 8u, t1);
+        bool bad = load_x8<B>(src, k0, 0, t0);
+        bad |= load_x8<B>(src, k0 + 8u, 1, t1);
         sum8<B>(t0, s0);
         sum8<B>(t1, s1);
 #pragma unroll
@@ -88,8 +116,8 @@ struct LaneQ4K {
             for (int i = 0; i < 8; ++i) { xl[b][i] = t0[b][i]; xl[b][8 + i] = t1[b][i]; }
             sxl[b] = s0[b] + s1[b];
         }
-        bad |= load_x8<B>(x, stride, k0 + 32u, t0);
-        bad |= load_x8<B>(x, stride, k0 + 40u, t1);
+        bad |= load_x8<B>(src, k0 + 32u, 2, t0);
+        bad |= load_x8<B>(src, k0 + 40u, 3, t1);
         sum8<B>(t0, s0);
         sum8<B>(t1, s1);
 #pragma unroll
@@ -175,11 +203,20 @@ struct LaneQ6K {
         k0 = 256u * bb + 128u * n + 8u * t;
     }
     /* quarter q holds outputs k0 + 32q + 0..7 */
+    /* natural column of chunk c of lane l */
+    __device__ static __forceinline__ uint32_t xk(uint32_t l, int c) {
+        const uint32_t k = 256u * (l >> 3) + 128u * ((l & 7u) >> 2) + 8u * (l & 3u);
+        return k + 32u * (uint32_t)(c >> 1) + 4u * ((uint32_t)c & 1u);
+    }
     __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        return load_x(XGlobal{x, stride});
+    }
+    template <class X>
+    __device__ __forceinline__ bool load_x(const X &src) {
         bool bad = false;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            bad |= load_x8<B>(x, stride, k0 + 32u * q, xq[q]);
+            bad |= load_x8<B>(src, k0 + 32u * q, q, xq[q]);
             sum8<B>(xq[q], xs[q]);
         }
         return bad;
@@ -278,10 +315,18 @@ struct LaneQ8 {
         off = kBlockBytes * l;
         k0 = 32u * l;
     }
+    /* natural column of chunk c of lane l */
+    __device__ static __forceinline__ uint32_t xk(uint32_t l, int c) {
+        return 32u * l + 4u * (uint32_t)c;
+    }
     __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        return load_x(XGlobal{x, stride});
+    }
+    template <class X>
+    __device__ __forceinline__ bool load_x(const X &src) {
         bool bad = false;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(x, stride, k0 + 8u * q, xv[q]);
+        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(src, k0 + 8u * q, q, xv[q]);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             float a = 0.0f;
@@ -357,10 +402,19 @@ struct LaneQ5K {
         hoff = 16u + 16u * h;
         k0 = 256u * bb + 64u * gq + 16u * h;
     }
+    /* natural column of chunk c of lane l */
+    __device__ static __forceinline__ uint32_t xk(uint32_t l, int c) {
+        const uint32_t k = 256u * (l >> 3) + 64u * ((l & 7u) >> 1) + 16u * (l & 1u);
+        return k + (c >= 4 ? 32u : 0u) + 8u * ((uint32_t)(c >> 1) & 1u) + 4u * ((uint32_t)c & 1u);
+    }
     __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        return load_x(XGlobal{x, stride});
+    }
+    template <class X>
+    __device__ __forceinline__ bool load_x(const X &src) {
         float t0[B][8], t1[B][8], s0[B], s1[B];
-        bool bad = load_x8<B>(x, stride, k0, t0);
-        bad |= load_x8<B>(x, stride, k0 + 8u, t1);
+        bool bad = load_x8<B>(src, k0, 0, t0);
+        bad |= load_x8<B>(src, k0 + 8u, 1, t1);
         sum8<B>(t0, s0);
         sum8<B>(t1, s1);
 #pragma unroll
@@ -369,8 +423,8 @@ struct LaneQ5K {
             for (int i = 0; i < 8; ++i) { xl[b][i] = t0[b][i]; xl[b][8 + i] = t1[b][i]; }
             sxl[b] = s0[b] + s1[b];
         }
-        bad |= load_x8<B>(x, stride, k0 + 32u, t0);
-        bad |= load_x8<B>(x, stride, k0 + 40u, t1);
+        bad |= load_x8<B>(src, k0 + 32u, 2, t0);
+        bad |= load_x8<B>(src, k0 + 40u, 3, t1);
         sum8<B>(t0, s0);
         sum8<B>(t1, s1);
 #pragma unroll
@@ -451,10 +505,18 @@ struct LaneQ51 {
         off = kBlockBytes * l;
         k0 = 32u * l;
     }
+    /* natural column of chunk c of lane l */
+    __device__ static __forceinline__ uint32_t xk(uint32_t l, int c) {
+        return 32u * l + 4u * (uint32_t)c;
+    }
     __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        return load_x(XGlobal{x, stride});
+    }
+    template <class X>
+    __device__ __forceinline__ bool load_x(const X &src) {
         bool bad = false;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(x, stride, k0 + 8u * q, xv[q]);
+        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(src, k0 + 8u * q, q, xv[q]);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             float a = 0.0f;
@@ -540,10 +602,18 @@ struct LaneIQ4NL {
         off = kBlockBytes * l;
         k0 = 32u * l;
     }
+    /* natural column of chunk c of lane l */
+    __device__ static __forceinline__ uint32_t xk(uint32_t l, int c) {
+        return 32u * l + 4u * (uint32_t)c;
+    }
     __device__ __forceinline__ bool load_x(const float *x, uint32_t stride) {
+        return load_x(XGlobal{x, stride});
+    }
+    template <class X>
+    __device__ __forceinline__ bool load_x(const X &src) {
         bool bad = false;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(x, stride, k0 + 8u * q, xv[q]);
+        for (int q = 0; q < 4; ++q) bad |= load_x8<B>(src, k0 + 8u * q, q, xv[q]);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             float a = 0.0f;
@@ -658,6 +728,7 @@ struct Rows {
     static constexpr uint32_t RPW = 64u / LPR;
     static constexpr uint32_t GROUP = RPW * RT;
     static constexpr uint32_t RB = row_bytes<TYPE>(COLS);
+    static constexpr uint32_t kCols = COLS;
     static constexpr int NV = RT * B; /* partial sums per lane */
     /* the butterfly halves the count at every level: pad to a power of two */
     static constexpr int N = NV <= 1 ? 1 : NV <= 2 ? 2 : NV <= 4 ? 4 : NV <= 8 ? 8
@@ -679,6 +750,22 @@ struct Rows {
                 const uint32_t row = row0 + (uint32_t)r * RPW;
                 raw[r] = row < rows ? ln.load(W, row * stride) : ln.zero();
             }
+        }
+    }
+
+    /* the same loads without a branch: rows past the matrix read from
+     * `oob` (at least 64 bytes past the buffer's end, so every window of the
+     * row lies outside it), which the hardware returns as zeros, the value
+     * of zero() */
+    __device__ static __forceinline__ void load_group_oob(const Lane &ln, KqBuf W, uint32_t g,
+                                                          uint32_t rows, uint32_t sub,
+                                                          Raw (&raw)[RT], uint32_t stride,
+                                                          uint32_t oob) {
+        const uint32_t row0 = g * GROUP + sub;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint32_t row = row0 + (uint32_t)r * RPW;
+            raw[r] = ln.load(W, row < rows ? row * stride : oob);
         }
     }
 
@@ -704,6 +791,48 @@ struct Rows {
             idx = (int)l * KEEP + j;
         }
         return idx < NV ? idx : -1;
+    }
+};
+
+/* Activation staging for kernels whose waves share one set of activations
+ * (COLS columns of B batch columns at x + b * stride). The NT threads of a
+ * workgroup copy them once into the LDS image read through XLds; issue()
+ * only requests the loads, so the caller can request its weights before
+ * anything waits, and commit() checks the values and writes the image
+ * (then an LDS barrier). */
+template <class R, int B, int NT>
+struct XStage {
+    static constexpr uint32_t LPR = R::LPR;
+    static constexpr uint32_t NP = (uint32_t)B * 8u * LPR; /* float4 words */
+    static constexpr int NX = (int)((NP + (uint32_t)NT - 1u) / (uint32_t)NT);
+    kq_u32x4 v[NX];
+
+    __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid) {
+        const uint32_t bytes = ((uint32_t)(B - 1) * stride + R::kCols) * 4u;
+        const KqBuf xb = kq_buf(x, bytes);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
+            const uint32_t b = p / (8u * LPR), c = (p / LPR) & 7u, l = p % LPR;
+            const uint32_t k = R::Lane::xk(l, (int)c);
+            const uint32_t off = p < NP ? (b * stride + k) * 4u : bytes;
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(xb.r, (int)off, 0, 0);
+        }
+    }
+    __device__ __forceinline__ bool commit(float4 *xs, uint32_t tid) const {
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
+            if (NP % (uint32_t)NT == 0u || p < NP) {
+                const float4 f = make_float4(__uint_as_float(v[i].x), __uint_as_float(v[i].y),
+                                             __uint_as_float(v[i].z), __uint_as_float(v[i].w));
+                bad |= !kq_isfinite(f.x) || !kq_isfinite(f.y) || !kq_isfinite(f.z) ||
+                       !kq_isfinite(f.w);
+                xs[p] = f;
+            }
+        }
+        return bad;
     }
 };
 
