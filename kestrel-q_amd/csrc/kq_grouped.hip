@@ -136,9 +136,11 @@ struct Fmt<KQ_LAUNCH_Q6_K> {
             r.w[nh][1] = kq_ld64(w, base + oa + 32u, 0u);
             r.w[nh][2] = kq_ld64(w, base + 128u + 32u * n + 16u * h + 4u * g, 0u);
         }
-        /* sc[16] at 192: [192, 208) when aligned, else [190, 210) */
+        /* sc[16] at 192: [192, 208) when aligned, else [190, 210); the
+         * tail word is loaded on every path (a branch here would split the
+         * wave) and only used for an unaligned block */
         r.sc = kq_ld128(w, base + 192u, 0u);
-        r.sc_tail = r.sh ? kq_ld32(w, base + 208u, 0u) : 0u;
+        r.sc_tail = kq_ld32(w, base + 208u, 0u);
         r.d = kq_ld16(w, boff + 208u, 0u);
         return r;
     }
@@ -765,6 +767,280 @@ bool down_type(uint32_t t) { return t == KQ_LAUNCH_Q4_K || t == KQ_LAUNCH_Q6_K; 
 
 bool grouped_dim(uint32_t n) { return n == 256u || n == 512u || n == 1024u || n == 2048u; }
 
+/* ------------------------------------------------------------------ */
+/* Batched Q6_K matvec on MFMA: y[b] = W x[b] for 2 .. 4 activation columns
+ *
+ * The row engine keeps every lane's activations in registers, 32 per batch
+ * column; at 4 columns that leaves no room for the weights in flight. Here
+ * the columns ride on the token dimension of the same 16x16x16 steps as the
+ * grouped down pass (Tile<Q6_K>): they are staged once per workgroup as
+ * fp16 hi + lo after an exact power-of-two scaling (an LDS image of
+ * kMvCols rows), and lane l keeps row l % 16 of a 16-row tile for columns
+ * 4 (l / 16) .. + 3 -- lanes 0..15 hold every real column.
+ *
+ * Weights: the MFMA operand wants twelve scattered 4-byte pieces of a block
+ * per lane, which as global loads would touch 16 rows per instruction. So
+ * each wave streams one block of its tile's 16 rows (16 windows of 224
+ * bytes from the block's aligned start) with four contiguous 16-byte loads
+ * per lane, two blocks ahead of the one it multiplies, into a private LDS
+ * slot, and reads the operand pieces from there. The per-row fp32 sums are
+ * compared with the CPU by tolerance; the argmax partials (largest value,
+ * lowest row on ties) are exact over them. */
+
+constexpr uint32_t kMvCols = 4;      /* staged activation columns */
+constexpr int kMvWaves = 8;          /* waves per workgroup */
+constexpr uint32_t kMvMaxK = 4096u;
+constexpr uint32_t kMvWin = 224u;    /* bytes of a row's block window (>= 210 + 2) */
+constexpr uint32_t kMvPitch = 240u;  /* slot row pitch: lanes (j, g) hit distinct banks */
+constexpr uint32_t kMvSlot = kTile * kMvPitch;
+constexpr uint32_t kMvUnits = kTile * (kMvWin / 16u); /* 16-byte loads per block: 224 */
+constexpr int kMvLoads = (int)((kMvUnits + 63u) / 64u); /* per lane: 4 */
+
+__device__ __forceinline__ void mv_argmax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+/* x image pitch in fp16 (a 32-byte skew per column keeps the 16 operand
+ * reads of a step on distinct banks) */
+__host__ __device__ __forceinline__ uint32_t mv_xpitch(uint32_t nb) { return nb * 256u + 16u; }
+
+__global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
+    const uint8_t *__restrict__ W, uint32_t rows, uint32_t nb, const float *__restrict__ x,
+    uint32_t batch, float *__restrict__ y, uint32_t *status, float *part_v, uint32_t *part_i,
+    uint32_t part_stride) {
+    using F = Fmt<KQ_LAUNCH_Q6_K>;
+    extern __shared__ __align__(16) _Float16 mv_lds[];
+    const uint32_t K = nb * 256u, pitch = mv_xpitch(nb);
+    _Float16 *xh = mv_lds, *xl = mv_lds + kMvCols * pitch;
+    int *sig = (int *)(xl + kMvCols * pitch);
+    uint8_t *slots = (uint8_t *)(sig + kMvCols);
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t gw = blockIdx.x * (uint32_t)kMvWaves + wave;
+    const uint32_t nwaves = gridDim.x * (uint32_t)kMvWaves;
+    const uint32_t rb = nb * F::kBytes;
+    const uint32_t wbytes = rows * rb;
+    const KqBuf wb = kq_buf(W, wbytes);
+    const uint32_t ntiles = (rows + kTile - 1u) / kTile;
+    uint8_t *myslot = slots + wave * 2u * kMvSlot;
+
+    /* Work item it = block it % nb of tile gw + nwaves * (it / nb). Its
+     * loads: unit e = i * 64 + lane of the 224 = 16 rows x 14 covers bytes
+     * [16u, 16u + 16) of row e / 14's window (the block's start rounded
+     * down to 4 bytes); rows past the matrix, and the 32 spare units, read
+     * far past the buffer (zeros). */
+    typedef kq_u32x4 MvLd[kMvLoads];
+    auto load_item = [&](uint32_t it, MvLd &v) {
+        const uint32_t t = gw + nwaves * (it / nb), b = it % nb;
+#pragma unroll
+        for (int i = 0; i < kMvLoads; ++i) {
+            const uint32_t e = (uint32_t)i * 64u + lane;
+            const uint32_t r = e / 14u, u = e - 14u * r;
+            const uint32_t row = t * kTile + r;
+            const uint32_t o = row * rb + b * F::kBytes;
+            const uint32_t off =
+                (e < kMvUnits && t < ntiles && row < rows) ? (o & ~3u) + 16u * u : wbytes + 256u;
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(wb.r, (int)off, 0, 0);
+        }
+    };
+    auto store_item = [&](uint32_t slot, const MvLd &v) {
+#pragma unroll
+        for (int i = 0; i < kMvLoads; ++i) {
+            const uint32_t e = (uint32_t)i * 64u + lane;
+            const uint32_t r = e / 14u, u = e - 14u * r;
+            if (e < kMvUnits)
+                *(kq_u32x4 *)(myslot + slot * kMvSlot + r * kMvPitch + 16u * u) = v[i];
+        }
+    };
+
+    /* the first two items are requested before the staging */
+    MvLd va, vb;
+    load_item(0u, va);
+    load_item(1u, vb);
+
+    /* stage column i (one wave each): scale by 2^sig[i], split into hi + lo */
+    bool bad = false;
+    for (uint32_t i = wave; i < kMvCols; i += (uint32_t)kMvWaves) {
+        const bool real = i < batch;
+        float m = 0.0f;
+        bool nf = false;
+        for (uint32_t c = 4u * lane; c < K; c += 256u) {
+            const float4 v = real ? *(const float4 *)(x + (size_t)i * K + c)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            nf |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) || !kq_isfinite(v.w);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        bad |= nf;
+        m = wave_max_abs(m);
+        const bool any_nf = __ballot(nf) != 0ull;
+        int e = 0;
+        if (!any_nf && m > 0.0f) e = 15 - __builtin_amdgcn_frexp_expf(m);
+        for (uint32_t c = 4u * lane; c < K; c += 256u) {
+            const float4 v = real ? *(const float4 *)(x + (size_t)i * K + c)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float a[4] = {v.x, v.y, v.z, v.w};
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float xs = any_nf ? 0.0f : ldexpf(a[q], e);
+                hi[q] = (_Float16)xs;
+                lo[q] = (_Float16)(xs - (float)hi[q]);
+            }
+            *(h4 *)(xh + i * pitch + c) = h4{hi[0], hi[1], hi[2], hi[3]};
+            *(h4 *)(xl + i * pitch + c) = h4{lo[0], lo[1], lo[2], lo[3]};
+        }
+        if (lane == 0u) sig[i] = e;
+    }
+    store_item(0u, va);
+    load_item(2u, va);
+    kq_lds_barrier();
+    int unscale[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) unscale[k] = -sig[k];
+
+    bool malformed = false, nonfinite = false;
+    float best_v[4];
+    uint32_t best_i[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        best_v[k] = -__builtin_inff();
+        best_i[k] = 0xffffffffu;
+    }
+    /* Lane l supplies token row j = l % 16 of the A operand: rows 0..3 are
+     * the hi parts of columns 0..3, rows 4..7 their lo parts, and rows
+     * 8..15 repeat rows 0..7. Row t of a product depends on row t of A
+     * only, so one step gives the hi products to lanes 0..15 and the lo
+     * products to lanes 16..31 (both scaled and summed per row); lanes
+     * 32..63 are never used and need no zero fill. */
+    const _Float16 *xa = ((j & 4u) ? xl : xh) + (j & 3u) * pitch;
+    const h2 bias = h2{(_Float16)-1056.0f, (_Float16)-1056.0f}; /* 1024 + 32 */
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+
+    /* item it from its slot: 16 sub-block steps into acc; at the tile's
+     * last block lanes 0..15 write row t*16 + j of columns 0 .. batch-1 */
+    auto process = [&](uint32_t it, uint32_t slot) {
+        const uint32_t tt = gw + nwaves * (it / nb), bb = it % nb;
+        const uint32_t row = tt * kTile + j;
+        const uint32_t sh = (row * rb + bb * F::kBytes) & 3u;
+        const uint8_t *p = myslot + slot * kMvSlot + j * kMvPitch;
+        auto w32 = [&](uint32_t o) { return *(const uint32_t *)(p + o); };
+        const float d = (float)*(const _Float16 *)(p + sh + 208u);
+        malformed |= !kq_isfinite(d);
+        uint32_t sc[4];
+        {
+            const uint32_t s0 = w32(192u), s1 = w32(196u), s2 = w32(200u), s3 = w32(204u),
+                           s4 = w32(208u);
+            sc[0] = kq_align2(s1, s0, sh);
+            sc[1] = kq_align2(s2, s1, sh);
+            sc[2] = kq_align2(s3, s2, sh);
+            sc[3] = kq_align2(s4, s3, sh);
+        }
+        const _Float16 *pa = xa + 256u * bb + 4u * g;
+#pragma unroll
+        for (uint32_t nh = 0; nh < 4u; ++nh) {
+            const uint32_t n = nh >> 1, h = nh & 1u;
+            const uint32_t oa = 64u * n + 16u * h + 4u * g;
+            const uint32_t oq = 128u + 32u * n + 16u * h + 4u * g;
+            const uint32_t A = kq_align2(w32(oa + 4u), w32(oa), sh);
+            const uint32_t B = kq_align2(w32(oa + 36u), w32(oa + 32u), sh);
+            const uint32_t H = kq_align2(w32(oq + 4u), w32(oq), sh);
+            uint32_t c[4];
+            c[0] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+            c[1] = (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+            c[2] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+            c[3] = ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+            /* the group's four steps are independent products: all four
+             * are issued before any result is scaled, so the matrix core's
+             * latency overlaps the next products and the scaling */
+            f4 tm[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t ko = 128u * n + 32u * q + 16u * h;
+                const h4 av = *(const h4 *)(pa + ko);
+                const h2 w0 = bytes_lo(c[q]) + bias, w1 = bytes_hi(c[q]) + bias;
+                const h4 bw = h4{w0.x, w0.y, w1.x, w1.y};
+                tm[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bw, f4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                             0, 0);
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t s = 8u * n + 2u * q + h;
+                const int8_t scv = (int8_t)((sc[s >> 2] >> (8u * (s & 3u))) & 0xffu);
+                const float ds = d * (float)scv;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] = fmaf(ds, tm[q][k], acc[k]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (bb + 1u == nb) {
+            /* column k of row j = hi sum (lane j) + lo sum (lane j + 16) */
+            f4 lo;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) lo[k] = __shfl_down(acc[k], 16, KQ_WAVE);
+            if (g == 0u && row < rows) {
+#pragma unroll
+                for (uint32_t k = 0; k < 4u; ++k) {
+                    if (k < batch) {
+                        const float v = ldexpf(acc[k] + lo[k], unscale[k]);
+                        nonfinite |= !kq_isfinite(v);
+                        y[(size_t)k * rows + row] = v;
+                        mv_argmax_merge(best_v[k], best_i[k], v, row);
+                    }
+                }
+            }
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    /* Item it is multiplied from slot it % 2 while items it + 1 and it + 2
+     * are in flight (registers vb and va for even it); then it + 1 goes to
+     * the other slot and it + 3 is requested. */
+    const uint32_t nitems = ntiles > gw ? ((ntiles - gw + nwaves - 1u) / nwaves) * nb : 0u;
+    for (uint32_t it = 0u; it < nitems; it += 2u) {
+        process(it, 0u);
+        store_item(1u, vb);
+        load_item(it + 3u, vb);
+        if (it + 1u >= nitems) break;
+        process(it + 1u, 1u);
+        store_item(0u, va);
+        load_item(it + 4u, va);
+    }
+    if (bad) kq_flag(status, KQ_DEV_INPUT);
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
+    if (nonfinite) kq_flag(status, KQ_DEV_NUMERIC);
+    if (part_v != nullptr) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) {
+            float bv = best_v[k];
+            uint32_t bi = best_i[k];
+            /* lanes 16..63 hold no real column: only lanes 0..15 merge */
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o, KQ_WAVE);
+                const uint32_t oi = __shfl_xor(bi, o, KQ_WAVE);
+                mv_argmax_merge(bv, bi, ov, oi);
+            }
+            if (lane == 0u && k < batch) {
+                part_v[(size_t)k * part_stride + gw] = bv;
+                part_i[(size_t)k * part_stride + gw] = bi;
+                for (uint32_t sl = gw + nwaves; sl < part_stride; sl += nwaves) {
+                    part_v[(size_t)k * part_stride + sl] = -__builtin_inff();
+                    part_i[(size_t)k * part_stride + sl] = 0xffffffffu;
+                }
+            }
+        }
+    }
+}
+
+size_t mv_lds_bytes(uint32_t nb) {
+    return (size_t)2u * kMvCols * mv_xpitch(nb) * sizeof(_Float16) + kMvCols * sizeof(int) +
+           (size_t)kMvWaves * 2u * kMvSlot;
+}
+
 }  // namespace
 
 extern "C" int kq_launch_moe_grouped_supported(const kq_launch_moe_dims *d,
@@ -814,5 +1090,54 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     hipLaunchKernelGGL(moe_combine, dim3((d->hidden + 255u) / 256u, tokens), dim3(256), 0, s,
                        ws->outp, ws->pos, ws->order, ws->weights, ws->shared_scale, tokens,
                        d->top_k, d->hidden, out, status);
+    return hipGetLastError();
+}
+
+/* batched Q6_K matvec on MFMA: rows of 256 .. 4096 columns (whole blocks),
+ * 2 .. 4 activation columns, at least 65,536 rows (enough 16-row tiles to
+ * fill the device) */
+extern "C" int kq_launch_matvec_mfma_supported(uint32_t type, uint32_t rows, uint32_t cols,
+                                               uint32_t batch) {
+    /* block offsets, and the out-of-range offset past the last row, stay
+     * within 32 bits */
+    const uint64_t bytes = (uint64_t)rows * (cols / 256u) * 210u;
+    return type == KQ_LAUNCH_Q6_K && batch >= 2u && batch <= kMvCols && cols % 256u == 0u &&
+           cols >= 256u && cols <= kMvMaxK && rows >= 65536u && bytes <= 0xfffff000ull;
+}
+
+/* a resident grid (workgroups that fit at once), capped by the tile count */
+static uint32_t mv_blocks(uint32_t rows, uint32_t nb) {
+    static uint32_t per_cu_cache[kMvMaxK / 256u + 1u];
+    uint32_t &per = per_cu_cache[nb];
+    if (per == 0u) {
+        int dev = 0, cus = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus < 1)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_mfma_q6k, kMvWaves * 64,
+                                                         mv_lds_bytes(nb)) != hipSuccess ||
+            n < 1)
+            n = 1;
+        per = (uint32_t)(n * cus);
+    }
+    const uint32_t tiles = (rows + kTile - 1u) / kTile;
+    uint32_t blocks = (tiles + (uint32_t)kMvWaves - 1u) / (uint32_t)kMvWaves;
+    if (blocks > per) blocks = per;
+    return blocks < 1u ? 1u : blocks;
+}
+
+extern "C" uint32_t kq_launch_matvec_mfma_waves(uint32_t rows, uint32_t cols) {
+    return mv_blocks(rows, cols / 256u) * (uint32_t)kMvWaves;
+}
+
+extern "C" hipError_t kq_launch_matvec_mfma(const void *W, uint32_t rows, uint32_t cols,
+                                            const float *x, uint32_t batch, float *y,
+                                            uint32_t *status, float *part_v, uint32_t *part_i,
+                                            uint32_t part_stride, hipStream_t stream) {
+    const uint32_t nb = cols / 256u;
+    hipLaunchKernelGGL(matvec_mfma_q6k, dim3(mv_blocks(rows, nb)), dim3(kMvWaves * 64),
+                       mv_lds_bytes(nb), stream, (const uint8_t *)W, rows, nb, x, batch, y,
+                       status, part_v, part_i, part_stride);
     return hipGetLastError();
 }

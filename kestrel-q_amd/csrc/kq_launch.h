@@ -39,6 +39,13 @@ hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_
                             const float *x, uint32_t batch, float *y, uint32_t *status,
                             float *part_v, uint32_t *part_i, uint32_t part_stride,
                             hipStream_t stream);
+/* batched Q6_K matvec on MFMA (kq_grouped.hip), used by kq_launch_matvec
+ * where supported; same partials contract */
+int kq_launch_matvec_mfma_supported(uint32_t type, uint32_t rows, uint32_t cols, uint32_t batch);
+uint32_t kq_launch_matvec_mfma_waves(uint32_t rows, uint32_t cols);
+hipError_t kq_launch_matvec_mfma(const void *W, uint32_t rows, uint32_t cols, const float *x,
+                                 uint32_t batch, float *y, uint32_t *status, float *part_v,
+                                 uint32_t *part_i, uint32_t part_stride, hipStream_t stream);
 uint32_t kq_launch_argmax_parts(uint32_t count);
 hipError_t kq_launch_argmax(const float *logits, uint32_t count, uint32_t batch,
                             float *part_v, uint32_t *part_i, uint32_t *ids,

@@ -48,8 +48,8 @@ __device__ __forceinline__ void wave_argmax(float &bv, uint32_t &bi) {
  * W + r * row_bytes, batch column b's activations at x + b * x_stride. With
  * y_prev (which may be y itself) the segment's sums are added to the
  * previous segments' ones, in segment order. */
-template <uint32_t TYPE, uint32_t COLS, int B, int RT>
-__global__ __launch_bounds__(kThreads) void matvec_kernel(
+template <uint32_t TYPE, uint32_t COLS, int B, int RT, int NT>
+__global__ __launch_bounds__(NT) void matvec_kernel(
     const uint8_t *__restrict__ W, uint32_t rows, uint32_t row_bytes,
     const float *__restrict__ x, uint32_t x_stride, float *y, const float *y_prev,
     uint32_t *status, float *part_v, uint32_t *part_i, uint32_t part_stride) {
@@ -59,8 +59,8 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     /* uniform across the wave: the group loop and the full-group test stay
      * scalar branches */
     const uint32_t wave =
-        __builtin_amdgcn_readfirstlane((blockIdx.x * kThreads + threadIdx.x) >> 6);
-    const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
+        __builtin_amdgcn_readfirstlane((blockIdx.x * NT + threadIdx.x) >> 6);
+    const uint32_t nwaves = (gridDim.x * NT) >> 6;
     const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
     const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
 
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
      * loads complete first, are checked and written to LDS behind an
      * LDS-only barrier while the weights are still in flight. The check is
      * flagged at the end. */
-    using XS = kq::XStage<R, B, kThreads>;
+    using XS = kq::XStage<R, B, NT>;
     __shared__ __align__(16) float4 xs[XS::NP];
     XS stage;
     stage.issue(x, x_stride, threadIdx.x);
@@ -212,7 +212,12 @@ uint32_t pick_rt(uint32_t rows, uint32_t cols) {
     return groups4 >= kResidentWaves ? 4u : 1u;
 }
 
-/* workgroups of `kernel` that fit on the device at once */
+/* Threads per workgroup: 512 for one group per wave (the activation image
+ * is built once per 8 waves), 256 for the resident grid of RT = 4. */
+constexpr int kThreadsRt1 = 512;
+constexpr int kThreadsRt4 = 256;
+
+/* workgroups of `kernel` (kThreadsRt4 threads) that fit on the device at once */
 template <class K>
 uint32_t resident_blocks(K kernel) {
     int dev = 0, cus = 0, per_cu = 0;
@@ -220,7 +225,7 @@ uint32_t resident_blocks(K kernel) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus < 1)
         cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreadsRt4, 0) != hipSuccess ||
         per_cu < 1)
         per_cu = 1;
     return (uint32_t)(per_cu * cus);
@@ -241,25 +246,29 @@ template <uint32_t TYPE, uint32_t COLS, int B>
 hipError_t launch_one(const uint8_t *W, uint32_t rows, Seg sg, const float *x, float *y,
                       uint32_t *st, float *pv, uint32_t *pi, uint32_t ps, hipStream_t s,
                       uint32_t *waves) {
-    constexpr uint32_t kWavesPerBlock = kThreads / 64u;
     const uint32_t rt = pick_rt(rows, COLS);
+    const uint32_t threads = rt == 4u ? (uint32_t)kThreadsRt4 : (uint32_t)kThreadsRt1;
+    const uint32_t waves_per_block = threads / 64u;
     const uint32_t groups = (rows + group_rows(COLS, rt) - 1u) / group_rows(COLS, rt);
-    uint32_t blocks = (groups + kWavesPerBlock - 1u) / kWavesPerBlock;
+    uint32_t blocks = (groups + waves_per_block - 1u) / waves_per_block;
     if (rt == 4u) {
-        static const uint32_t resident = resident_blocks(matvec_kernel<TYPE, COLS, B, 4>);
+        static const uint32_t resident =
+            resident_blocks(matvec_kernel<TYPE, COLS, B, 4, kThreadsRt4>);
         if (blocks > resident) blocks = resident;
     }
     if (blocks < 1u) blocks = 1u;
     if (waves != nullptr) {
-        *waves = blocks * kWavesPerBlock;
+        *waves = blocks * waves_per_block;
         return hipSuccess;
     }
     if (rt == 4u)
-        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 4>), dim3(blocks), dim3(kThreads), 0, s,
-                           W, rows, sg.row_bytes, x, sg.x_stride, y, sg.y_prev, st, pv, pi, ps);
+        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 4, kThreadsRt4>), dim3(blocks),
+                           dim3(threads), 0, s, W, rows, sg.row_bytes, x, sg.x_stride, y,
+                           sg.y_prev, st, pv, pi, ps);
     else
-        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 1>), dim3(blocks), dim3(kThreads), 0, s,
-                           W, rows, sg.row_bytes, x, sg.x_stride, y, sg.y_prev, st, pv, pi, ps);
+        hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 1, kThreadsRt1>), dim3(blocks),
+                           dim3(threads), 0, s, W, rows, sg.row_bytes, x, sg.x_stride, y,
+                           sg.y_prev, st, pv, pi, ps);
     return hipGetLastError();
 }
 
@@ -386,6 +395,8 @@ extern "C" int kq_launch_matvec_supported(uint32_t type, uint32_t cols, uint32_t
 
 extern "C" uint32_t kq_launch_matvec_waves(uint32_t type, uint32_t rows, uint32_t cols,
                                            uint32_t batch) {
+    if (kq_launch_matvec_mfma_supported(type, rows, cols, batch))
+        return kq_launch_matvec_mfma_waves(rows, cols);
     uint32_t waves = 0u;
     if (dispatch(type, nullptr, rows, cols, nullptr, batch, nullptr, nullptr, nullptr, nullptr,
                  0u, nullptr, &waves) != hipSuccess)
@@ -397,6 +408,9 @@ extern "C" hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t ro
                                        uint32_t cols, const float *x, uint32_t batch, float *y,
                                        uint32_t *status, float *part_v, uint32_t *part_i,
                                        uint32_t part_stride, hipStream_t stream) {
+    if (kq_launch_matvec_mfma_supported(type, rows, cols, batch))
+        return kq_launch_matvec_mfma(W, rows, cols, x, batch, y, status, part_v, part_i,
+                                     part_stride, stream);
     return dispatch(type, W, rows, cols, x, batch, y, status, part_v, part_i, part_stride, stream,
                     nullptr);
 }

@@ -237,6 +237,49 @@ def test_matvec_fails_closed(ctx):
     ctx.matvec(kq_hip.TYPE_Q4_K, dw, 16, 512, dx, 1, dy)  # still usable
 
 
+@pytest.mark.parametrize("rows,cols,batch,scale", [
+    (65536, 256, 2, 1.0), (70001, 2048, 3, 1.0), (65537, 4096, 4, 1e-30),
+    (66000, 1024, 2, 1e6), (65600, 512, 4, 1.0), (65551, 2048, 4, 1.0)])
+def test_matvec_q6k_batched_mfma(ctx, rows, cols, batch, scale):
+    # Q6_K with 2..4 activation columns on at least 65,536 rows runs on
+    # MFMA (exact fp16 codes, activation columns as fp16 hi + lo after a
+    # power-of-two scaling): ragged last tiles, 1 .. 16 blocks per row, tiny
+    # and large activations (compared relative to their scale)
+    say(f"q6k mfma {rows}x{cols} batch {batch} scale {scale}")
+    key = S.stream_key(S.W_MATVEC_Q6K, rows, cols, batch)
+    w = S.quant_matrix("Q6_K", key, rows, cols)
+    x = (S.normal_f32(key ^ 0x55, batch * cols) * np.float32(scale)).reshape(batch, cols)
+    dw, dx, dy = ctx.upload(w), ctx.upload(x), ctx.alloc(rows * batch * 4)
+    ctx.matvec(kq_hip.TYPE_Q6_K, dw, rows, cols, dx, batch, dy)
+    got = ctx.download(dy, np.float32, rows * batch).reshape(batch, rows)
+    want = kq_oracle.matvec(kq_oracle.Q6_K, w, rows, cols, x, threads=oracle_threads())
+    assert_close(got.astype(np.float64) / scale, want.astype(np.float64) / scale)
+    for b in (dw, dx, dy):
+        b.close()
+
+
+def test_matvec_q6k_batched_mfma_fails_closed(ctx):
+    rows, cols = 65536, 256
+    w = S.quant_matrix("Q6_K", S.stream_key(S.W_MATVEC_Q6K, 91), rows, cols)
+    x = S.normal_f32(S.stream_key(S.W_MATVEC_Q6K, 92), 2 * cols).reshape(2, cols)
+    x_bad = x.copy()
+    x_bad[1, 17] = np.inf
+    dw, dx, dxb, dy = ctx.upload(w), ctx.upload(x), ctx.upload(x_bad), ctx.alloc(rows * 2 * 4)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q6_K, dw, rows, cols, dxb, 2, dy)
+    assert e.value.name == "NUMERIC_DOMAIN"
+    w_bad = w.copy().reshape(-1, 210)
+    w_bad[40000, 208:210] = [0x00, 0x7C]  # +Inf d
+    dwb = ctx.upload(w_bad.reshape(-1))
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.matvec(kq_hip.TYPE_Q6_K, dwb, rows, cols, dx, 2, dy)
+    assert e.value.name == "MALFORMED_QUANTIZED_DATA"
+    ctx.matvec(kq_hip.TYPE_Q6_K, dw, rows, cols, dx, 2, dy)  # still usable
+    got = ctx.download(dy, np.float32, rows * 2).reshape(2, rows)
+    assert_close(got, kq_oracle.matvec(kq_oracle.Q6_K, w, rows, cols, x,
+                                       threads=oracle_threads()))
+
+
 def test_argmax_exact(ctx):
     rng = np.random.default_rng(9)
     v = rng.standard_normal((3, 151936)).astype(np.float32)
@@ -313,11 +356,13 @@ def test_lm_head_q8_0_248320x2560(ctx):
         b.close()
 
 
-@pytest.mark.parametrize("batch", [5, 6, 8])
-def test_lm_head_batch_spans_launches(ctx, batch):
-    # batches over 4 run as several launches whose wave counts differ; the
-    # argmax partials of every batch row must still merge to the first max
-    V, H = 40000, 2048
+@pytest.mark.parametrize("V,batch", [(40000, 5), (40000, 6), (40000, 8), (65600, 5)])
+def test_lm_head_batch_spans_launches(ctx, V, batch):
+    # batches over 4 run as several launches whose wave counts differ (at
+    # 65,600 rows the first four columns run on MFMA, the fifth on the row
+    # engine); the argmax partials of every batch row must still merge to
+    # the first max
+    H = 2048
     say(f"lm head {V}x{H} batch {batch}")
     w = S.quant_matrix("Q6_K", S.stream_key(S.W_LM_HEAD, S.R_WEIGHT, 7), V, H)
     h = S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN, 70 + batch), batch * H).reshape(batch, H)
