@@ -71,6 +71,19 @@ def test_dequant_64m_weights_bit_exact(ctx, fmt):
     assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:5]}"
 
 
+@pytest.mark.parametrize("fmt", ALL_FMTS)
+def test_dequant_ragged_block_counts(ctx, fmt):
+    # Every wave takes four steps (a K-quant block or eight 32-weight
+    # blocks) at a time: counts that end inside a step, inside a group of
+    # four steps and on the buffer's last dword, each bit-exact.
+    gen, qk, bb = S.BLOCK_GEN[fmt]
+    for n in (1, 2, 3, 7, 9, 31, 33, 257, 1025):
+        packed = gen(S.stream_key(S.W_DEQUANT, 60, FMTS[fmt], n), n).reshape(-1)
+        got = gpu_dequant(ctx, FMTS[fmt], packed)
+        want = kq_oracle.dequantize(FMTS[fmt], packed)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (fmt, n)
+
+
 def test_dequant_subnormal_and_edge_scales(ctx):
     # Q4_K blocks whose d/dmin are fp16 subnormals, zero, negative zero and
     # the largest finite half; Q6_K/Q8_0 with subnormal d.
