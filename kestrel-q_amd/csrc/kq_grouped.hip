@@ -726,12 +726,24 @@ struct Shape {
     static constexpr int PD = RING > 1 ? RING - 1 : 0;
 };
 
+/* the Q6_K down pass with its weights streamed through LDS (below) */
+template <uint32_t KDIM>
+hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X,
+                           const uint32_t *offsets, uint32_t experts, uint32_t tokens,
+                           uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
+                           hipStream_t s);
+
 template <uint32_t GFMT, uint32_t KDIM, int NMAT>
 hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
                        const uint8_t *SW1, const float *X, const uint32_t *offsets,
                        const uint32_t *perm_tok, uint32_t experts, uint32_t tokens,
                        uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
                        hipStream_t s) {
+    /* (an intermediate of 2048 leaves no LDS beside its activation image
+     * for the weight slots) */
+    if constexpr (GFMT == KQ_LAUNCH_Q6_K && NMAT == 1 && KDIM <= 1024u)
+        return launch_down_q6k<KDIM>(W0, SW0, X, offsets, experts, tokens, top_k, rows, out,
+                                     status, s);
     constexpr int NW = Shape<KDIM, NMAT>::NW;
     constexpr int TPW = Shape<KDIM, NMAT>::TPW;
     constexpr int PD = Shape<KDIM, NMAT>::PD;
@@ -1039,6 +1051,169 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
 size_t mv_lds_bytes(uint32_t nb) {
     return (size_t)2u * kMvCols * mv_xpitch(nb) * sizeof(_Float16) + kMvCols * sizeof(int) +
            (size_t)kMvWaves * 2u * kMvSlot;
+}
+
+/* ------------------------------------------------------------------ */
+/* grouped Q6_K down pass with its weights streamed through LDS
+ *
+ * The same work split, staging and Tile<Q6_K> steps as grouped_pass, but
+ * the block operand pieces (twelve scattered 4-byte windows per lane) are
+ * not fetched from global memory: each wave loads one 16-row block of its
+ * tile contiguously (as matvec_mfma_q6k does) into a private LDS slot, two
+ * blocks ahead of the one it multiplies, and the Raw pieces are read from
+ * there. Offsets past the matrix read as zeros and stores past the
+ * workgroup's outputs are dropped, so no path branches around a load. */
+template <uint32_t KDIM, int NW, int TPW>
+__global__ __launch_bounds__(NW * 64) void grouped_down_q6k(
+    const uint8_t *__restrict__ W0, const uint8_t *__restrict__ SW0,
+    const float *__restrict__ X, const uint32_t *__restrict__ offsets, uint32_t experts,
+    uint32_t tokens, uint32_t top_k, uint32_t rows, uint32_t shared_chunks,
+    float *__restrict__ out, uint32_t *status) {
+    using F = Fmt<KQ_LAUNCH_Q6_K>;
+    using S = Stage<KQ_LAUNCH_Q6_K, KDIM>;
+    using T = Tile<KQ_LAUNCH_Q6_K, KDIM, 1>;
+    using Raw = F::Raw;
+    constexpr uint32_t NB = KDIM / 256u;
+    constexpr uint32_t RB = NB * F::kBytes;
+    constexpr uint32_t NIT = (uint32_t)TPW * NB;
+    static_assert(NIT % 2u == 0u, "items run in pairs");
+    __shared__ S st;
+    __shared__ int src_row[kTile];
+    __shared__ __align__(16) uint8_t slots[NW][2][kMvSlot];
+
+    const Work wk = work_of(blockIdx.y, offsets, experts, tokens, shared_chunks);
+    if (wk.count == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t tk = tokens * top_k;
+    const uint32_t e = blockIdx.y;
+    auto tile_row = [&](uint32_t t) { return ((blockIdx.x * TPW + t) * NW + wave) * kTile; };
+    const uint32_t wbytes = rows * RB;
+    const KqBuf wb = kq_buf(wk.shared ? SW0 : W0 + (size_t)e * rows * RB, wbytes);
+    const uint32_t pos0 = wk.shared ? tk + wk.first : wk.first;
+    const uint32_t obytes = wk.count * rows * 4u;
+    const KqBuf ob = kq_buf(out + (size_t)pos0 * rows, obytes);
+    uint8_t *myslot = &slots[wave][0][0];
+
+    /* item it = block it % NB of tile it / NB; unit e = i * 64 + lane of
+     * its 224 loads covers bytes [16u, 16u + 16) of row e / 14's window
+     * (the block start rounded down to 4 bytes) */
+    typedef kq_u32x4 Ld[kMvLoads];
+    auto load_item = [&](uint32_t it, Ld &v) {
+        const uint32_t t = it / NB, b = it % NB;
+#pragma unroll
+        for (int i = 0; i < kMvLoads; ++i) {
+            const uint32_t u0 = (uint32_t)i * 64u + lane;
+            const uint32_t r = u0 / 14u, u = u0 - 14u * r;
+            const uint32_t row = tile_row(t) + r;
+            const uint32_t o = row * RB + b * F::kBytes;
+            const uint32_t off = (u0 < kMvUnits && t < (uint32_t)TPW && row < rows)
+                                     ? (o & ~3u) + 16u * u
+                                     : wbytes + 256u;
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(wb.r, (int)off, 0, 0);
+        }
+    };
+    auto store_item = [&](uint32_t slot, const Ld &v) {
+#pragma unroll
+        for (int i = 0; i < kMvLoads; ++i) {
+            const uint32_t u0 = (uint32_t)i * 64u + lane;
+            const uint32_t r = u0 / 14u, u = u0 - 14u * r;
+            if (u0 < kMvUnits)
+                *(kq_u32x4 *)(myslot + slot * kMvSlot + r * kMvPitch + 16u * u) = v[i];
+        }
+    };
+    /* the pieces Fmt<Q6_K>::load would read, from this lane's row in slot */
+    auto lds_raw = [&](uint32_t slot, uint32_t t, uint32_t b) {
+        const uint32_t o = (tile_row(t) + j) * RB + b * F::kBytes;
+        const uint8_t *p = myslot + slot * kMvSlot + j * kMvPitch;
+        auto w32 = [&](uint32_t off) { return *(const uint32_t *)(p + off); };
+        Raw r;
+        r.sh = o & 3u;
+#pragma unroll
+        for (uint32_t nh = 0; nh < 4u; ++nh) {
+            const uint32_t n = nh >> 1, h = nh & 1u;
+            const uint32_t oa = 64u * n + 16u * h + 4u * g;
+            const uint32_t oq = 128u + 32u * n + 16u * h + 4u * g;
+            r.w[nh][0] = kq_u32x2{w32(oa), w32(oa + 4u)};
+            r.w[nh][1] = kq_u32x2{w32(oa + 32u), w32(oa + 36u)};
+            r.w[nh][2] = kq_u32x2{w32(oq), w32(oq + 4u)};
+        }
+        r.sc = make_uint4(w32(192u), w32(196u), w32(200u), w32(204u));
+        r.sc_tail = w32(208u);
+        r.d = *(const uint16_t *)(p + r.sh + 208u);
+        return r;
+    };
+
+    bool bad = false, malformed = false;
+    for (uint32_t c0 = 0; c0 < wk.count; c0 += kTile) {
+        Ld va, vb;
+        load_item(0u, va);
+        load_item(1u, vb);
+        __syncthreads(); /* the previous chunk's readers are done */
+        if (threadIdx.x < kTile) {
+            const uint32_t i = threadIdx.x;
+            int src = -1;
+            if (c0 + i < wk.count) {
+                const uint32_t p = wk.first + c0 + i;
+                src = (int)(wk.shared ? tk + p : p);
+            }
+            src_row[i] = src;
+        }
+        __syncthreads();
+        /* a non-finite intermediate activation is a numeric failure */
+        bad |= stage_rows<KQ_LAUNCH_Q6_K, KDIM>(st, X, src_row, wave, NW, lane);
+        __syncthreads();
+        store_item(0u, va);
+        load_item(2u, va);
+
+        f4 acc[1];
+        auto process = [&](uint32_t it, uint32_t slot) {
+            const uint32_t t = it / NB, b = it % NB;
+            if (b == 0u) acc[0] = f4{0.f, 0.f, 0.f, 0.f};
+            const Raw rr[1] = {lds_raw(slot, t, b)};
+            T::block(rr, st, b, j, g, acc, malformed);
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 1u < NB) return;
+            /* D[token][row]: this lane holds row `row` of tokens 4g .. 4g+3 */
+            const uint32_t row = tile_row(t) + j;
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t i = 4u * g + q;
+                const bool valid = c0 + i < wk.count && row < rows;
+                const float v = ldexpf(acc[0][q], -st.sig[i]);
+                bad |= valid && !kq_isfinite(v);
+                const uint32_t off = valid ? ((c0 + i) * rows + row) * 4u : obytes;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ob.r, (int)off, 0, 0);
+            }
+        };
+#pragma unroll 1
+        for (uint32_t it = 0; it < NIT; it += 2u) {
+            process(it, 0u);
+            store_item(1u, vb);
+            load_item(it + 3u, vb);
+            process(it + 1u, 1u);
+            store_item(0u, va);
+            load_item(it + 4u, va);
+        }
+    }
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+}
+
+template <uint32_t KDIM>
+hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X,
+                           const uint32_t *offsets, uint32_t experts, uint32_t tokens,
+                           uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
+                           hipStream_t s) {
+    constexpr int NW = Shape<KDIM, 1>::NW;
+    constexpr int TPW = Shape<KDIM, 1>::TPW;
+    const uint32_t slab = (uint32_t)(NW * TPW) * kTile;
+    const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
+    const dim3 grid((rows + slab - 1u) / slab, experts + sh_wgs);
+    hipLaunchKernelGGL((grouped_down_q6k<KDIM, NW, TPW>), grid, dim3(NW * 64), 0, s, W0, SW0, X,
+                       offsets, experts, tokens, top_k, rows, kSharedChunks, out, status);
+    return hipGetLastError();
 }
 
 }  // namespace
