@@ -372,16 +372,25 @@ def main() -> int:
             lambda: wl_matvec(ctx, "IQ4_NL", 4096, 2048, 1, W, K, graph))
         run("q4k_matvec_4096x2048_b1_warm_cache",
             lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph, warm=True))
+        # the same kernel family on a matrix large enough to amortise the
+        # launch and the first-load latency (151 MB per step): the rate the
+        # Q4_K row engine sustains
+        run("q4k_matvec_131072x2048_b1",
+            lambda: wl_matvec(ctx, "Q4_K", 131072, 2048, 1, 10, max(10, K // 2), graph))
         for f in ("Q4_K", "Q8_0", "Q6_K", "Q5_K", "Q5_1", "IQ4_NL"):
             run(f"dequant_64m_{f.lower()}",
-                lambda f=f: wl_dequant(ctx, f, 3, max(5, K // 20), graph))
+                lambda f=f: wl_dequant(ctx, f, 5, max(10, K // 4), graph))
         cache = {}
         run("moe_decode_1tok", lambda: wl_moe(ctx, 1, W, K, graph, cache))
-        run("lm_head_q6k_151936x2048_b1", lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph))
-        run("lm_head_q6k_151936x2048_b4", lambda: wl_lm_head(ctx, 4, 3, max(10, K // 10), graph))
+        # the large workloads run 100 / 10 timed steps (several ms): shorter
+        # timed regions read up to 10% slower per step
+        run("lm_head_q6k_151936x2048_b1",
+            lambda: wl_lm_head(ctx, 1, 10, max(10, K // 2), graph))
+        run("lm_head_q6k_151936x2048_b4",
+            lambda: wl_lm_head(ctx, 4, 10, max(10, K // 2), graph))
         run("lm_head_q8_0_248320x2560_b1",
-            lambda: wl_lm_head(ctx, 1, 3, max(10, K // 10), graph, "Q8_0", 248320, 2560))
-        run("moe_prefill_512", lambda: wl_moe(ctx, 512, 1, 3, graph, cache))
+            lambda: wl_lm_head(ctx, 1, 10, max(10, K // 2), graph, "Q8_0", 248320, 2560))
+        run("moe_prefill_512", lambda: wl_moe(ctx, 512, 2, max(3, K // 20), graph, cache))
         run("moe_decode_1tok_2560x640",
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))
         if wanted == "hbm_copy_64mb":
