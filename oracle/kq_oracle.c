@@ -834,3 +834,78 @@ int kqo_moe_permutation(const uint32_t *ids, uint64_t tokens, uint32_t top_k,
     free(cursor);
     return KQO_OK;
 }
+
+
+/* ------------------------------------------------------------------ */
+/* Gated residual around a layer block (hyper-connection read / write).
+ *
+ * Restates kq_layer_gr_read_common (src/kq_layer_qwen38.c:40-172) and
+ * kq_layer_gr_write_f32 (:196-208): per branch RMS norm; a rank-r down
+ * projection divided by the branch count and passed through SiLU; an up
+ * projection to per-element sigmoid read gates; the gate-weighted branch
+ * mix divided by the branch count; the per-branch write gate
+ * 2 * sigmoid(inject . normalized / branches). The down and up weights are
+ * F32 (the reference's F32 path: left-to-right sums of rounded products)
+ * or packed blocks (its provider path through kq_weight_provider_linear_f32,
+ * i.e. row dots); both are row dots here. All sums are left to right in
+ * binary32 (the reference's -ffp-contract=off order). */
+int kqo_gr_read(uint32_t nbranch, uint32_t hidden, uint32_t rank, float eps,
+                const float *branches, const float *norm, uint32_t down_type,
+                const void *down, uint32_t up_type, const void *up, const float *inject,
+                float *normalized, float *read_gate, float *mixed, float *rank_ws,
+                float *write_gate) {
+    const uint64_t width = (uint64_t)nbranch * hidden;
+    uint64_t i;
+    uint32_t b;
+    int st;
+    if (nbranch == 0U || hidden == 0U || rank == 0U || branches == NULL || norm == NULL ||
+        down == NULL || up == NULL || inject == NULL || normalized == NULL ||
+        read_gate == NULL || mixed == NULL || rank_ws == NULL || write_gate == NULL)
+        return KQO_INVALID_ARGUMENT;
+    for (b = 0U; b < nbranch; ++b) {
+        st = kqo_f32_rms_norm(branches + (uint64_t)b * hidden, norm + (uint64_t)b * hidden,
+                              hidden, eps, normalized + (uint64_t)b * hidden);
+        if (st != KQO_OK) return st;
+    }
+    st = kqo_matvec_f32(down_type, down, rank, width, normalized, 1U, rank_ws, 1);
+    if (st != KQO_OK) return st;
+    for (i = 0U; i < rank; ++i) rank_ws[i] /= (float)nbranch;
+    for (i = 0U; i < rank; ++i) {
+        const float s = sigmoid_scalar(rank_ws[i]);
+        rank_ws[i] *= s;
+    }
+    st = kqo_matvec_f32(up_type, up, width, rank, rank_ws, 1U, read_gate, 1);
+    if (st != KQO_OK) return st;
+    for (i = 0U; i < width; ++i) read_gate[i] = sigmoid_scalar(read_gate[i]);
+    for (i = 0U; i < hidden; ++i) {
+        float sum = 0.0f;
+        for (b = 0U; b < nbranch; ++b) {
+            const uint64_t o = (uint64_t)b * hidden + i;
+            const float p = read_gate[o] * normalized[o];
+            sum += p;
+        }
+        mixed[i] = sum / (float)nbranch;
+    }
+    for (b = 0U; b < nbranch; ++b) {
+        float sum = 0.0f;
+        for (i = 0U; i < width; ++i) {
+            const float p = inject[(uint64_t)b * width + i] * normalized[i];
+            sum += p;
+        }
+        write_gate[b] = sum;
+    }
+    for (b = 0U; b < nbranch; ++b) write_gate[b] /= (float)nbranch;
+    for (b = 0U; b < nbranch; ++b) write_gate[b] = 2.0f * sigmoid_scalar(write_gate[b]);
+    return KQO_OK;
+}
+
+void kqo_gr_write(uint32_t nbranch, uint32_t hidden, const float *branches,
+                  const float *block_output, const float *write_gate, float *out) {
+    uint32_t b, i;
+    for (b = 0U; b < nbranch; ++b)
+        for (i = 0U; i < hidden; ++i) {
+            const uint64_t o = (uint64_t)b * hidden + i;
+            const float p = block_output[i] * write_gate[b];
+            out[o] = branches[o] + p;
+        }
+}

@@ -147,6 +147,18 @@ int kqo_moe_permutation(const uint32_t *ids, uint64_t tokens, uint32_t top_k,
                         uint32_t experts, uint32_t *expert_offsets,
                         uint32_t *pair_token, uint32_t *pair_slot);
 
+/* gated residual read / write around a layer block
+ * (src/kq_layer_qwen38.c:40-208): branches [nbranch][hidden], norm
+ * [nbranch*hidden], down [rank][width] and up [width][rank] as F32 or packed
+ * rows, inject [nbranch][width] F32. */
+int kqo_gr_read(uint32_t nbranch, uint32_t hidden, uint32_t rank, float eps,
+                const float *branches, const float *norm, uint32_t down_type,
+                const void *down, uint32_t up_type, const void *up, const float *inject,
+                float *normalized, float *read_gate, float *mixed, float *rank_ws,
+                float *write_gate);
+void kqo_gr_write(uint32_t nbranch, uint32_t hidden, const float *branches,
+                  const float *block_output, const float *write_gate, float *out);
+
 #ifdef __cplusplus
 }
 #endif

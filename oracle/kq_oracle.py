@@ -83,6 +83,9 @@ def _declare(l: C.CDLL) -> None:
     l.kqo_f32_scale.argtypes = [P, U64, F, P]
     l.kqo_f32_dot.argtypes = [P, P, U64, C.POINTER(F)]
     l.kqo_f32_rms_norm.argtypes = [P, P, U64, F, P]
+    l.kqo_gr_read.argtypes = [U32, U32, U32, F, P, P, U32, P, U32, P, P, P, P, P, P, P]
+    l.kqo_gr_write.argtypes = [U32, U32, P, P, P, P]
+    l.kqo_gr_write.restype = None
     l.kqo_f32_stable_top_k.argtypes = [P, U64, U32, P, P]
     l.kqo_moe_select_top_k.argtypes = [P, U32, U32, P]
     l.kqo_moe_select_top_k.restype = None
@@ -301,6 +304,44 @@ def moe_permutation(ids: np.ndarray, experts: int):
     if st != OK:
         raise OracleError(st)
     return off, tok, slot
+
+
+def gr_read(branches: np.ndarray, hidden: int, rank: int, eps: float, norm: np.ndarray,
+            down: tuple, up: tuple, inject: np.ndarray) -> dict:
+    """Gated-residual read of one token (src/kq_layer_qwen38.c:40-172).
+
+    branches [nbranch * hidden]; down = (type, [rank][width] rows),
+    up = (type, [width][rank] rows), inject [nbranch][width] F32. Returns
+    normalized, read_gate, mixed (the block input), rank and write_gate."""
+    b = np.ascontiguousarray(branches, dtype=np.float32).reshape(-1)
+    nb = b.size // hidden
+    width = nb * hidden
+    norm = np.ascontiguousarray(norm, dtype=np.float32)
+    dt, dw = down
+    ut, uw = up
+    dw, uw = np.ascontiguousarray(dw), np.ascontiguousarray(uw)
+    inj = np.ascontiguousarray(inject, dtype=np.float32)
+    out = {"normalized": np.zeros(width, np.float32), "read_gate": np.zeros(width, np.float32),
+           "mixed": np.zeros(hidden, np.float32), "rank": np.zeros(rank, np.float32),
+           "write_gate": np.zeros(nb, np.float32)}
+    st = lib().kqo_gr_read(nb, hidden, rank, eps, _p(b), _p(norm), dt, _p(dw), ut, _p(uw),
+                           _p(inj), _p(out["normalized"]), _p(out["read_gate"]),
+                           _p(out["mixed"]), _p(out["rank"]), _p(out["write_gate"]))
+    if st != OK:
+        raise OracleError(st)
+    return out
+
+
+def gr_write(branches: np.ndarray, hidden: int, block_output: np.ndarray,
+             write_gate: np.ndarray) -> np.ndarray:
+    """out[b][i] = branches[b][i] + block_output[i] * write_gate[b]
+    (src/kq_layer_qwen38.c:196-208)."""
+    b = np.ascontiguousarray(branches, dtype=np.float32).reshape(-1)
+    bo = np.ascontiguousarray(block_output, dtype=np.float32)
+    wg = np.ascontiguousarray(write_gate, dtype=np.float32)
+    out = np.zeros_like(b)
+    lib().kqo_gr_write(b.size // hidden, hidden, _p(b), _p(bo), _p(wg), _p(out))
+    return out
 
 
 class OracleError(RuntimeError):

@@ -16,6 +16,12 @@ hex strings); the fixtures are data, not source. Provenance of each file:
                           calibrated contracts of moe-native-validation.json
   moe_routing_vectors.json research/operators/.../moe-routing-vectors.json
                           (512 experts, top-10, EXACT_DISCRETE)
+  layer_tier_a.json       research/operators/.../layer-{calibration,holdout}.json
+                          (Transformers Class-C layer input, output and the
+                          ple_output / attn_gr / mixer_output / moe_gr /
+                          moe_output checkpoints; the hyper-connection and MoE
+                          weights only) and the layer-native-validation.json
+                          contract
 """
 from __future__ import annotations
 
@@ -98,6 +104,30 @@ def moe(ref: Path) -> None:
     (OUT / "moe_tier_a.json").write_text(json.dumps(doc, indent=0, sort_keys=True))
 
 
+def layer(ref: Path) -> None:
+    base = ref / "research/operators/Qwen3.8-Flash-Next" / REV
+    contract = json.loads((base / "layer-contract.json").read_text())
+    val = json.loads((base / "layer-native-validation.json").read_text())
+    doc = {"source": [f"research/operators/Qwen3.8-Flash-Next/{REV}/layer-{c}.json"
+                      for c in ("contract", "calibration", "holdout", "native-validation")],
+           "reduced": contract["reduced"],
+           "limit_abs": max(r["limit_abs"] for r in val["records"])}
+    for corpus in ("calibration", "holdout"):
+        src = json.loads((base / f"layer-{corpus}.json").read_text())
+        cases = []
+        for c in src["cases"]:
+            w = {k: _f32_array(v) for k, v in c["weights"].items()
+                 if "hyper_connection" in k or k.startswith("mlp.")}
+            cases.append({"id": c["id"], "family": c["family"], "input": _f32_array(c["input"]),
+                          "output": _f32_array(c["output"]),
+                          "checkpoints": {k: _f32_array(v) for k, v in c["checkpoints"].items()
+                                          if k in ("ple_output", "attn_gr", "mixer_output",
+                                                   "moe_gr", "moe_output")},
+                          "weights": w})
+        doc[corpus] = cases
+    (OUT / "layer_tier_a.json").write_text(json.dumps(doc, indent=0, sort_keys=True))
+
+
 def routing(ref: Path) -> None:
     base = ref / "research/operators/Qwen3.8-Flash-Next" / REV
     src = json.loads((base / "moe-routing-vectors.json").read_text())
@@ -119,6 +149,7 @@ def main() -> None:
     primitives(ref)
     moe(ref)
     routing(ref)
+    layer(ref)
     for p in sorted(OUT.glob("*.json")):
         print(p.name, p.stat().st_size)
 
