@@ -305,6 +305,74 @@ kq_status kq_hip_moe_token_permutation(kq_hip_context *context,
                                        kq_diagnostic *diagnostic);
 
 /* ------------------------------------------------------------------ */
+/* The gated residual around a layer block: the hyper-connection read and
+ * write of src/kq_layer_qwen38.c:40-208, which src/kq_layer.c:779-813 calls
+ * around the MoE. A token's state is branch_count residual branches of
+ * hidden_size values (width = branch_count * hidden_size). */
+typedef struct kq_hip_gr_dimensions {
+    uint32_t branch_count;
+    uint32_t hidden_size;
+    uint32_t rank;
+    float rms_epsilon;
+} kq_hip_gr_dimensions;
+
+/* Mirrors kq_layer_gr_weights_f32 (src/kq_layer_internal.h) with a type for
+ * each projection: the reference's provider path reads them as packed rows
+ * (the model's blk.N.hc_ffn_down / hc_ffn_up are Q8_0). norm [width] and
+ * inject [branch_count][width] are F32; down [rank][width] and up
+ * [width][rank] are F32 (KQ_HIP_TYPE_F32, width and rank multiples of 4) or
+ * packed rows of a matvec type. */
+typedef struct kq_hip_gr_weights {
+    const float *norm;
+    uint32_t down_type;
+    const void *down;
+    uint32_t up_type;
+    const void *up;
+    const float *inject;
+} kq_hip_gr_weights;
+
+/* Device scratch of kq_hip_gr_read_f32 for `token_count` tokens. */
+uint64_t kq_hip_gr_scratch_bytes(const kq_hip_gr_dimensions *dimensions, uint64_t token_count);
+
+/* Replaces kq_layer_gr_read_f32 / kq_layer_gr_read_quantized_f32
+ * (src/kq_layer_internal.h:81-92, src/kq_layer_qwen38.c:175-194):
+ * branches [tokens][width] -> mixed [tokens][hidden] (the block input) and
+ * write_gate [tokens][branch_count]. Fails with NUMERIC_DOMAIN on a
+ * non-finite input, norm weight or result. */
+kq_status kq_hip_gr_read_f32(kq_hip_context *context, const kq_hip_gr_dimensions *dimensions,
+                             const kq_hip_gr_weights *weights, const float *device_branches,
+                             uint64_t token_count, float *device_mixed,
+                             float *device_write_gate, void *device_scratch,
+                             uint64_t scratch_bytes, kq_diagnostic *diagnostic);
+
+/* Replaces kq_layer_gr_write_f32 (src/kq_layer_internal.h:93-95,
+ * src/kq_layer_qwen38.c:196-208): output[t][b][i] = branches[t][b][i] +
+ * block_output[t][i] * write_gate[t][b], exact. output may be branches. */
+kq_status kq_hip_gr_write_f32(kq_hip_context *context, const kq_hip_gr_dimensions *dimensions,
+                              const float *device_branches, const float *device_block_output,
+                              const float *device_write_gate, uint64_t token_count,
+                              float *device_output, kq_diagnostic *diagnostic);
+
+/* Device scratch of kq_hip_moe_block_f32 for `token_count` tokens. */
+uint64_t kq_hip_moe_block_scratch_bytes(const kq_hip_gr_dimensions *dimensions,
+                                        const kq_hip_moe_config *config,
+                                        uint64_t token_count);
+
+/* The MoE step of a layer with its gated residual (src/kq_layer.c:779-813):
+ * mixed, write_gate = gr_read(branches); moe = MoE(mixed);
+ * output = gr_write(branches, moe, write_gate). branches and output are
+ * [tokens][width] and must not overlap; optional device_selected_ids
+ * [tokens][top_k] receives the routing. */
+kq_status kq_hip_moe_block_f32(kq_hip_context *context, const kq_hip_gr_dimensions *dimensions,
+                               const kq_hip_gr_weights *gr_weights,
+                               const kq_hip_moe_config *config,
+                               const kq_hip_moe_weights *moe_weights,
+                               const float *device_branches, uint64_t token_count,
+                               float *device_output, uint32_t *device_selected_ids,
+                               void *device_scratch, uint64_t scratch_bytes,
+                               kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
 /* Elementwise binary32 expf with the bits of the libm expf the reference
  * calls (src/kq_numeric.c:628-638, :776-813). No reference entry point of
  * its own; it exposes the device expf that the softmax uses so callers can

@@ -54,6 +54,22 @@ hipError_t kq_launch_argmax_from_parts(const float *part_v, const uint32_t *part
                                        uint32_t nparts, uint32_t batch, uint32_t *ids,
                                        hipStream_t stream);
 
+/* gated residual around a layer block (kq_gr.hip) */
+hipError_t kq_launch_gr_norm(const float *x, const float *norm, uint32_t tokens,
+                             uint32_t branches, uint32_t hidden, float eps, float *normalized,
+                             uint32_t *status, hipStream_t stream);
+hipError_t kq_launch_gr_rank(float *rank, uint32_t n, uint32_t branches, uint32_t *status,
+                             hipStream_t stream);
+hipError_t kq_launch_gr_mix(const float *read_raw, const float *normalized, const float *inject,
+                            uint32_t tokens, uint32_t branches, uint32_t hidden, float *mixed,
+                            float *write_gate, uint32_t *status, hipStream_t stream);
+hipError_t kq_launch_gr_write(const float *x, const float *block_output, const float *write_gate,
+                              uint32_t tokens, uint32_t branches, uint32_t hidden, float *out,
+                              uint32_t *status, hipStream_t stream);
+/* y[b][r] = W[r] . x[b] for F32 weights [rows][cols], cols % 4 == 0 */
+hipError_t kq_launch_matvec_f32w(const float *W, uint32_t rows, uint32_t cols, const float *x,
+                                 uint32_t batch, float *y, uint32_t *status, hipStream_t stream);
+
 /* elementwise expf (kq_dequant.hip), used to pin the device expf */
 hipError_t kq_launch_expf(const float *in, uint64_t n, float *out, hipStream_t stream);
 

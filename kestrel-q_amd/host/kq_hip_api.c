@@ -13,6 +13,7 @@
  */
 #include "kq_hip.h"
 
+#include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -826,4 +827,212 @@ kq_status kq_hip_moe_token_permutation(kq_hip_context *c, const kq_hip_moe_confi
                                         pair_token, (uint32_t *)scratch, pair_slot, c->d_status,
                                         c->stream),
                   "permutation launch", diag);
+}
+
+/* ------------------------------------------------------------------ */
+/* gated residual around a layer block */
+
+static uint64_t align256(uint64_t n) { return (n + 255u) & ~(uint64_t)255u; }
+
+/* scratch of a gr read: normalized [T][W], rank [T][r], read gates [T][W] */
+uint64_t kq_hip_gr_scratch_bytes(const kq_hip_gr_dimensions *d, uint64_t tokens) {
+    uint64_t w;
+    if (d == NULL) return 0u;
+    w = (uint64_t)d->branch_count * d->hidden_size;
+    return 2u * align256(tokens * w * 4u) + align256(tokens * d->rank * 4u);
+}
+
+static kq_status gr_dims_ok(const kq_hip_gr_dimensions *d, uint64_t tokens,
+                            kq_diagnostic *diag) {
+    if (d == NULL || d->branch_count == 0u || d->hidden_size == 0u || d->rank == 0u ||
+        !isfinite(d->rms_epsilon) || !(d->rms_epsilon > 0.0f))
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "gated residual needs branches, hidden, rank and a positive epsilon");
+    if (d->branch_count > 64u || tokens == 0u ||
+        tokens * d->branch_count * (uint64_t)d->hidden_size > (UINT64_C(1) << 30) ||
+        (uint64_t)d->rank * d->branch_count * d->hidden_size > (UINT64_C(1) << 31))
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
+                       "gated residual: at most 64 branches and 2^30 state values");
+    return KQ_STATUS_OK;
+}
+
+/* a projection [rows][cols] as F32 or packed rows */
+static kq_status gr_proj_ok(uint32_t type, const void *w, uint64_t cols, const char *what,
+                            kq_diagnostic *diag) {
+    if (w == NULL) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "gated residual %s is required", what);
+    if (!aligned(w, 16u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "gated residual %s must be 16-byte aligned", what);
+    if (type == KQ_HIP_TYPE_F32) {
+        if (cols % 4u != 0u)
+            return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH,
+                           "F32 gated residual %s needs rows of a multiple of 4", what);
+        return KQ_STATUS_OK;
+    }
+    if (!packed_quant(type) || !kq_launch_matvec_supported(type, (uint32_t)cols, 1u))
+        return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
+                       "gated residual %s: F32 or a matvec type with rows of whole blocks", what);
+    return KQ_STATUS_OK;
+}
+
+static hipError_t gr_project(kq_hip_context *c, uint32_t type, const void *w, uint64_t rows,
+                             uint64_t cols, const float *x, uint32_t tokens, float *y) {
+    if (type == KQ_HIP_TYPE_F32)
+        return kq_launch_matvec_f32w((const float *)w, (uint32_t)rows, (uint32_t)cols, x, tokens,
+                                     y, c->d_status, c->stream);
+    return enqueue_matvec(c, type, w, rows, cols, x, tokens, y, NULL, NULL, 0u);
+}
+
+kq_status kq_hip_gr_read_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
+                             const kq_hip_gr_weights *w, const float *x, uint64_t tokens,
+                             float *mixed, float *write_gate, void *scratch,
+                             uint64_t scratch_bytes, kq_diagnostic *diag) {
+    uint64_t W, need;
+    float *normalized, *rank, *read_raw;
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || w == NULL || x == NULL || mixed == NULL || write_gate == NULL ||
+        scratch == NULL || w->norm == NULL || w->inject == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete gated residual arguments are required");
+    st = gr_dims_ok(d, tokens, diag);
+    if (st != KQ_STATUS_OK) return st;
+    W = (uint64_t)d->branch_count * d->hidden_size;
+    st = gr_proj_ok(w->down_type, w->down, W, "down", diag);
+    if (st == KQ_STATUS_OK) st = gr_proj_ok(w->up_type, w->up, d->rank, "up", diag);
+    if (st != KQ_STATUS_OK) return st;
+    need = kq_hip_gr_scratch_bytes(d, tokens);
+    if (scratch_bytes < need)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "gated residual scratch needs %llu bytes",
+                       (unsigned long long)need);
+    if (!aligned(x, 16u) || !aligned(scratch, 256u) || !aligned(mixed, 4u) ||
+        !aligned(write_gate, 4u) || !aligned(w->norm, 4u) || !aligned(w->inject, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT,
+                       "gated residual input 16-byte, scratch 256-byte aligned");
+    if (ranges_overlap(x, tokens * W * 4u, scratch, scratch_bytes) ||
+        ranges_overlap(mixed, tokens * d->hidden_size * 4u, scratch, scratch_bytes) ||
+        ranges_overlap(write_gate, tokens * d->branch_count * 4u, scratch, scratch_bytes) ||
+        ranges_overlap(mixed, tokens * d->hidden_size * 4u, write_gate,
+                       tokens * d->branch_count * 4u) ||
+        ranges_overlap(x, tokens * W * 4u, mixed, tokens * d->hidden_size * 4u) ||
+        ranges_overlap(x, tokens * W * 4u, write_gate, tokens * d->branch_count * 4u))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                       "gated residual input, outputs and scratch must not overlap");
+    normalized = (float *)scratch;
+    rank = (float *)((char *)scratch + align256(tokens * W * 4u));
+    read_raw = (float *)((char *)rank + align256(tokens * d->rank * 4u));
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    e = kq_launch_gr_norm(x, w->norm, (uint32_t)tokens, d->branch_count, d->hidden_size,
+                          d->rms_epsilon, normalized, c->d_status, c->stream);
+    if (e == hipSuccess)
+        e = gr_project(c, w->down_type, w->down, d->rank, W, normalized, (uint32_t)tokens, rank);
+    if (e == hipSuccess)
+        e = kq_launch_gr_rank(rank, (uint32_t)(tokens * d->rank), d->branch_count, c->d_status,
+                              c->stream);
+    if (e == hipSuccess)
+        e = gr_project(c, w->up_type, w->up, W, d->rank, rank, (uint32_t)tokens, read_raw);
+    if (e == hipSuccess)
+        e = kq_launch_gr_mix(read_raw, normalized, w->inject, (uint32_t)tokens, d->branch_count,
+                             d->hidden_size, mixed, write_gate, c->d_status, c->stream);
+    return finish(c, e, "gated residual read launch", diag);
+}
+
+kq_status kq_hip_gr_write_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
+                              const float *x, const float *block_output,
+                              const float *write_gate, uint64_t tokens, float *out,
+                              kq_diagnostic *diag) {
+    uint64_t W;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || x == NULL || block_output == NULL || write_gate == NULL || out == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete gated residual arguments are required");
+    st = gr_dims_ok(d, tokens, diag);
+    if (st != KQ_STATUS_OK) return st;
+    W = (uint64_t)d->branch_count * d->hidden_size;
+    if (!aligned(x, 4u) || !aligned(block_output, 4u) || !aligned(write_gate, 4u) ||
+        !aligned(out, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "gated residual buffers must be 4-byte aligned");
+    if ((out != x && ranges_overlap(x, tokens * W * 4u, out, tokens * W * 4u)) ||
+        ranges_overlap(block_output, tokens * d->hidden_size * 4u, out, tokens * W * 4u) ||
+        ranges_overlap(write_gate, tokens * d->branch_count * 4u, out, tokens * W * 4u))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                       "gated residual output may only be the branches themselves");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    return finish(c, kq_launch_gr_write(x, block_output, write_gate, (uint32_t)tokens,
+                                        d->branch_count, d->hidden_size, out, c->d_status,
+                                        c->stream),
+                  "gated residual write launch", diag);
+}
+
+/* scratch of the MoE block: mixed [T][H], write gates [T][B], MoE output
+ * [T][H], then the gated residual's and the MoE's own scratch */
+uint64_t kq_hip_moe_block_scratch_bytes(const kq_hip_gr_dimensions *d,
+                                        const kq_hip_moe_config *cfg, uint64_t tokens) {
+    if (d == NULL || !moe_ok(cfg)) return 0u;
+    return 2u * align256(tokens * d->hidden_size * 4u) + align256(tokens * d->branch_count * 4u) +
+           kq_hip_gr_scratch_bytes(d, tokens) + align256(kq_hip_moe_config_scratch_bytes(cfg, tokens));
+}
+
+kq_status kq_hip_moe_block_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
+                               const kq_hip_gr_weights *gw, const kq_hip_moe_config *cfg,
+                               const kq_hip_moe_weights *mw, const float *x, uint64_t tokens,
+                               float *out, uint32_t *ids, void *scratch, uint64_t scratch_bytes,
+                               kq_diagnostic *diag) {
+    uint64_t W, need, hb, gb;
+    char *p;
+    float *mixed, *wg, *moe_out;
+    int prev;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || gw == NULL || mw == NULL || x == NULL || out == NULL || scratch == NULL ||
+        !moe_ok(cfg))
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE block arguments are required");
+    st = gr_dims_ok(d, tokens, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (cfg->dims.hidden_size != d->hidden_size)
+        return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH,
+                       "the MoE hidden size must be the gated residual's");
+    W = (uint64_t)d->branch_count * d->hidden_size;
+    need = kq_hip_moe_block_scratch_bytes(d, cfg, tokens);
+    if (scratch_bytes < need)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "MoE block scratch needs %llu bytes",
+                       (unsigned long long)need);
+    if (!aligned(scratch, 256u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "MoE block scratch must be 256-byte aligned");
+    if (ranges_overlap(x, tokens * W * 4u, out, tokens * W * 4u) ||
+        ranges_overlap(x, tokens * W * 4u, scratch, scratch_bytes) ||
+        ranges_overlap(out, tokens * W * 4u, scratch, scratch_bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                       "MoE block input, output and scratch must not overlap");
+    hb = align256(tokens * d->hidden_size * 4u);
+    gb = kq_hip_gr_scratch_bytes(d, tokens);
+    p = (char *)scratch;
+    mixed = (float *)p;
+    p += hb;
+    moe_out = (float *)p;
+    p += hb;
+    wg = (float *)p;
+    p += align256(tokens * d->branch_count * 4u);
+    /* one synchronisation for the whole step: the three stages enqueue */
+    prev = c->async;
+    c->async = 1;
+    st = kq_hip_gr_read_f32(c, d, gw, x, tokens, mixed, wg, p, gb, diag);
+    if (st == KQ_STATUS_OK)
+        st = kq_hip_moe_execute_quantized(c, cfg, mw, mixed, tokens, moe_out,
+                                          tokens * d->hidden_size, ids, p + gb,
+                                          scratch_bytes - (uint64_t)(p + gb - (char *)scratch),
+                                          diag);
+    if (st == KQ_STATUS_OK)
+        st = kq_hip_gr_write_f32(c, d, x, moe_out, wg, tokens, out, diag);
+    c->async = prev;
+    if (st != KQ_STATUS_OK) {
+        /* stages already enqueued finish before the error is returned */
+        if (!prev) {
+            kq_diagnostic ignored;
+            (void)drain(c, &ignored);
+        }
+        return st;
+    }
+    return finish(c, hipSuccess, "MoE block launch", diag);
 }

@@ -56,6 +56,16 @@ class MoeDims(C.Structure):
                 ("shared_intermediate_size", C.c_uint32)]
 
 
+class GrDims(C.Structure):
+    _fields_ = [("branch_count", C.c_uint32), ("hidden_size", C.c_uint32),
+                ("rank", C.c_uint32), ("rms_epsilon", C.c_float)]
+
+
+class GrWeights(C.Structure):
+    _fields_ = [("norm", C.c_void_p), ("down_type", C.c_uint32), ("down", C.c_void_p),
+                ("up_type", C.c_uint32), ("up", C.c_void_p), ("inject", C.c_void_p)]
+
+
 class MoeWeights(C.Structure):
     _fields_ = [("router", C.c_void_p),
                 ("routed_gate_type", C.c_uint32), ("routed_gate", C.c_void_p),
@@ -188,6 +198,16 @@ SIGNATURES = {
                                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_uint64, C.c_void_p]),
     "kq_hip_f32_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
+    "kq_hip_gr_scratch_bytes": (C.c_uint64, [C.c_void_p, C.c_uint64]),
+    "kq_hip_gr_read_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_uint64, C.c_void_p]),
+    "kq_hip_gr_write_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
+    "kq_hip_moe_block_scratch_bytes": (C.c_uint64, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "kq_hip_moe_block_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
+                                       C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
 }
 
 _lib = None
@@ -397,6 +417,28 @@ class Context:
                                                  self._p(ids) if ids is not None else None,
                                                  self._p(scratch), scratch_bytes, C.byref(d)), d)
 
+    def gr_read(self, dims: GrDims, weights: GrWeights, x, tokens: int, mixed, write_gate,
+                scratch, scratch_bytes: int) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_gr_read_f32(self._h, C.byref(dims), C.byref(weights), self._p(x),
+                                       tokens, self._p(mixed), self._p(write_gate),
+                                       self._p(scratch), scratch_bytes, C.byref(d)), d)
+
+    def gr_write(self, dims: GrDims, x, block_output, write_gate, tokens: int, out) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_gr_write_f32(self._h, C.byref(dims), self._p(x),
+                                        self._p(block_output), self._p(write_gate), tokens,
+                                        self._p(out), C.byref(d)), d)
+
+    def moe_block(self, dims: GrDims, gr: GrWeights, cfg: MoeConfig, moe: MoeWeights, x,
+                  tokens: int, out, ids, scratch, scratch_bytes: int) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_moe_block_f32(self._h, C.byref(dims), C.byref(gr),
+                                         C.c_void_p(cfg.handle), C.byref(moe), self._p(x),
+                                         tokens, self._p(out),
+                                         self._p(ids) if ids is not None else None,
+                                         self._p(scratch), scratch_bytes, C.byref(d)), d)
+
     def moe_permutation(self, cfg: MoeConfig, ids, tokens: int, offsets, pair_token, pair_slot,
                         scratch, scratch_bytes: int) -> None:
         d = Diagnostic()
@@ -563,3 +605,21 @@ def gguf_type_info(type_id: int):
         return None
     t = p.contents
     return t.name.decode(), t.block_elements, t.bytes_per_block
+
+
+def gr_dims(branches: int, hidden: int, rank: int, eps: float = 1.0e-6) -> GrDims:
+    return GrDims(branches, hidden, rank, eps)
+
+
+def gr_scratch_bytes(dims: GrDims, tokens: int) -> int:
+    return lib().kq_hip_gr_scratch_bytes(C.byref(dims), tokens)
+
+
+def moe_block_scratch_bytes(dims: GrDims, cfg: MoeConfig, tokens: int) -> int:
+    return lib().kq_hip_moe_block_scratch_bytes(C.byref(dims), C.c_void_p(cfg.handle), tokens)
+
+
+def gr_weights(bufs: dict, down_type: int, up_type: int) -> GrWeights:
+    """bufs: norm, down, up, inject -> DeviceBuffer."""
+    return GrWeights(bufs["norm"].ptr, down_type, bufs["down"].ptr, up_type, bufs["up"].ptr,
+                     bufs["inject"].ptr)
