@@ -191,7 +191,9 @@ MOE_LAYERS = {
 }
 
 
-def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512"):
+def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512", block=False):
+    """block: the MoE block (4 residual branches, hyper-connection read with
+    rank-320 Q8_0 projections, MoE, write) instead of the bare MoE."""
     L = MOE_LAYERS[layer]
     H, E, K, I = L["H"], L["E"], L["K"], L["I"]
     if layer_cache.get("layer") != layer:
@@ -211,16 +213,28 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512"):
     touched = w["router"].nbytes + K * expert + shared + w["shared_gate_weight"].nbytes
     if tokens > 1:
         touched = layer_bytes
+    allw = dict(w)
+    width = H
+    if block:
+        nb, rank = 4, 320
+        width = nb * H
+        key = lambda i: S.stream_key(L["seed"], 90, i)
+        allw.update({"gr_norm": S.normal_f32(key(1), width, 0.1),
+                     "gr_down": S.quant_matrix("Q8_0", key(2), rank, width),
+                     "gr_up": S.quant_matrix("Q8_0", key(3), width, rank),
+                     "gr_inject": S.normal_f32(key(4), nb * width, 0.01)})
+        touched += sum(v.nbytes for k, v in allw.items() if k.startswith("gr_"))
+        gdims = kq_hip.gr_dims(nb, H, rank)
     nrep = max(2, min(24, -(-MALL_DEFEAT_BYTES // touched)))
     if tokens > 1:
         nrep = 1
     layers = []
     for r in range(nrep):
         if r == 0:
-            bufs = {k: ctx.upload(v) for k, v in w.items()}
+            bufs = {k: ctx.upload(v) for k, v in allw.items()}
         else:
             bufs = {}
-            for k, v in w.items():
+            for k, v in allw.items():
                 b = ctx.alloc(v.nbytes)
                 d2d(ctx, b.ptr, layers[0][k].ptr, v.nbytes)
                 bufs[k] = b
@@ -231,14 +245,23 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512"):
           for b in layers]
     ntok_inputs = 16
     x = S.normal_f32(S.stream_key(L["seed"], S.R_HIDDEN, 1000 + tokens),
-                     ntok_inputs * tokens * H).reshape(ntok_inputs, tokens * H)
+                     ntok_inputs * tokens * width).reshape(ntok_inputs, tokens * width)
     dxs = [ctx.upload(x[j]) for j in range(ntok_inputs)]
-    n = cfg.scratch_bytes(tokens)
+    n = kq_hip.moe_block_scratch_bytes(gdims, cfg, tokens) if block else cfg.scratch_bytes(tokens)
     scratch = ctx.alloc(n)
-    out = ctx.alloc(tokens * H * 4)
+    out = ctx.alloc(tokens * width * 4)
+    if block:
+        q8 = kq_hip.TYPE_Q8_0
+        gws = [kq_hip.gr_weights({k: b["gr_" + k] for k in ("norm", "down", "up", "inject")},
+                                 q8, q8) for b in layers]
 
     def step(i):
-        ctx.moe_execute(cfg, mw[i % nrep], dxs[i % ntok_inputs], tokens, out, None, scratch, n)
+        if block:
+            ctx.moe_block(gdims, gws[i % nrep], cfg, mw[i % nrep], dxs[i % ntok_inputs], tokens,
+                          out, None, scratch, n)
+        else:
+            ctx.moe_execute(cfg, mw[i % nrep], dxs[i % ntok_inputs], tokens, out, None, scratch,
+                            n)
 
     ms = time_steps(ctx, step, warmup, steps, graph)
     for bufs in layers:
@@ -246,10 +269,10 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512"):
             b.close()
     for b in dxs + [scratch, out]:
         b.close()
-    nbytes = touched + 2 * tokens * H * 4
+    nbytes = touched + 2 * tokens * width * 4
     return {"ms_per_step": ms, "tokens_per_s": tokens / ms * 1e3, "bytes_per_step": nbytes,
             "GBps": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-            "layer_replicas": nrep, "tokens": tokens, "layer": layer}
+            "layer_replicas": nrep, "tokens": tokens, "layer": layer + ("+gr" if block else "")}
 
 
 def wl_lm_head(ctx, batch, warmup, steps, graph, fmt="Q6_K", V=151936, H=2048):
@@ -393,6 +416,8 @@ def main() -> int:
         run("moe_prefill_512", lambda: wl_moe(ctx, 512, 2, max(3, K // 20), graph, cache))
         run("moe_decode_1tok_2560x640",
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))
+        run("moe_block_decode_1tok_4x2560",
+            lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640", block=True))
         if wanted == "hbm_copy_64mb":
             run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))
     head = work.get(HEADLINE)

@@ -27,8 +27,10 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kNormThreads = 1024; /* a branch's H values in one or few loads per thread */
 
-/* sum over the workgroup (kThreads), returned to every thread */
+/* sum over the workgroup (NT threads), returned to every thread */
+template <int NT>
 __device__ __forceinline__ float block_sum(float v, float *red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, KQ_WAVE);
@@ -38,32 +40,34 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     __syncthreads();
     float s = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    for (int w = 0; w < NT / 64; ++w) s += red[w];
     return s;
 }
 
 /* grid (B, T): one workgroup per branch of a token (src/kq_numeric.c:722-775) */
-__global__ __launch_bounds__(kThreads) void gr_norm(const float *__restrict__ x,
+__global__ __launch_bounds__(kNormThreads) void gr_norm(const float *__restrict__ x,
                                                     const float *__restrict__ norm, uint32_t B,
                                                     uint32_t H, float eps,
                                                     float *__restrict__ out, uint32_t *status) {
-    __shared__ float red[kThreads / 64];
+    __shared__ float red[kNormThreads / 64];
     const uint32_t b = blockIdx.x, t = blockIdx.y;
     const size_t base = ((size_t)t * B + b) * H;
     const float *w = norm + (size_t)b * H;
     bool badin = false, bad = false;
     float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < H; i += kThreads) {
+#pragma unroll 4
+    for (uint32_t i = threadIdx.x; i < H; i += kNormThreads) {
         const float v = x[base + i];
         badin |= !kq_isfinite(v) || !kq_isfinite(w[i]);
         const float sq = v * v;
         s += sq;
     }
-    s = block_sum(s, red);
+    s = block_sum<kNormThreads>(s, red);
     const float mean = s / (float)H;
     const float inv = 1.0f / sqrtf(mean + eps);
     bad |= !kq_isfinite(inv);
-    for (uint32_t i = threadIdx.x; i < H; i += kThreads) {
+#pragma unroll 4
+    for (uint32_t i = threadIdx.x; i < H; i += kNormThreads) {
         const float nv = x[base + i] * inv;
         const float wt = 1.0f + w[i];
         const float r = nv * wt;
@@ -88,7 +92,9 @@ __global__ __launch_bounds__(kThreads) void gr_rank(float *__restrict__ v, uint3
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
 }
 
-/* grid (T): the read gates, the branch mix and the write gates of a token */
+/* grid (G + B, T), G = ceil(H / kThreads): workgroups below G mix kThreads
+ * values of the token's state each (read gates, branch mix); workgroup G + b
+ * forms write gate b from the inject dot over the whole width */
 __global__ __launch_bounds__(kThreads) void gr_mix(const float *__restrict__ read_raw,
                                                    const float *__restrict__ normalized,
                                                    const float *__restrict__ inject, uint32_t B,
@@ -96,34 +102,40 @@ __global__ __launch_bounds__(kThreads) void gr_mix(const float *__restrict__ rea
                                                    float *__restrict__ write_gate,
                                                    uint32_t *status) {
     __shared__ float red[kThreads / 64];
-    const uint32_t t = blockIdx.x;
+    const uint32_t t = blockIdx.y;
     const uint32_t W = B * H;
+    const uint32_t G = (H + kThreads - 1) / kThreads;
     const float *rr = read_raw + (size_t)t * W;
     const float *nm = normalized + (size_t)t * W;
     bool bad = false;
-    for (uint32_t i = threadIdx.x; i < H; i += kThreads) {
-        float sum = 0.0f;
-        for (uint32_t b = 0; b < B; ++b) {
-            const float g = kq_sigmoid(rr[(size_t)b * H + i]);
-            const float p = g * nm[(size_t)b * H + i];
-            sum += p;
+    if (blockIdx.x < G) {
+        const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+        if (i < H) {
+            float sum = 0.0f;
+#pragma unroll 4
+            for (uint32_t b = 0; b < B; ++b) {
+                const float g = kq_sigmoid(rr[(size_t)b * H + i]);
+                const float p = g * nm[(size_t)b * H + i];
+                sum += p;
+            }
+            const float m = sum / (float)B;
+            bad = !kq_isfinite(m);
+            mixed[(size_t)t * H + i] = m;
         }
-        const float m = sum / (float)B;
-        bad |= !kq_isfinite(m);
-        mixed[(size_t)t * H + i] = m;
-    }
-    for (uint32_t b = 0; b < B; ++b) {
+    } else {
+        const uint32_t b = blockIdx.x - G;
         const float *inj = inject + (size_t)b * W;
         float s = 0.0f;
+#pragma unroll 8
         for (uint32_t i = threadIdx.x; i < W; i += kThreads) {
             const float p = inj[i] * nm[i];
             s += p;
         }
-        s = block_sum(s, red);
+        s = block_sum<kThreads>(s, red);
         if (threadIdx.x == 0u) {
             const float g = s / (float)B;
             const float r = 2.0f * kq_sigmoid(g);
-            bad |= !kq_isfinite(r);
+            bad = !kq_isfinite(r);
             write_gate[(size_t)t * B + b] = r;
         }
     }
@@ -202,7 +214,7 @@ uint32_t grid_for(size_t n) {
 extern "C" hipError_t kq_launch_gr_norm(const float *x, const float *norm, uint32_t tokens,
                                         uint32_t branches, uint32_t hidden, float eps,
                                         float *normalized, uint32_t *status, hipStream_t s) {
-    hipLaunchKernelGGL(gr_norm, dim3(branches, tokens), dim3(kThreads), 0, s, x, norm, branches,
+    hipLaunchKernelGGL(gr_norm, dim3(branches, tokens), dim3(kNormThreads), 0, s, x, norm, branches,
                        hidden, eps, normalized, status);
     return hipGetLastError();
 }
@@ -218,7 +230,8 @@ extern "C" hipError_t kq_launch_gr_mix(const float *read_raw, const float *norma
                                        const float *inject, uint32_t tokens, uint32_t branches,
                                        uint32_t hidden, float *mixed, float *write_gate,
                                        uint32_t *status, hipStream_t s) {
-    hipLaunchKernelGGL(gr_mix, dim3(tokens), dim3(kThreads), 0, s, read_raw, normalized, inject,
+    const uint32_t groups = (hidden + kThreads - 1) / kThreads + branches;
+    hipLaunchKernelGGL(gr_mix, dim3(groups, tokens), dim3(kThreads), 0, s, read_raw, normalized, inject,
                        branches, hidden, mixed, write_gate, status);
     return hipGetLastError();
 }

@@ -848,11 +848,11 @@ static kq_status gr_dims_ok(const kq_hip_gr_dimensions *d, uint64_t tokens,
         !isfinite(d->rms_epsilon) || !(d->rms_epsilon > 0.0f))
         return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
                        "gated residual needs branches, hidden, rank and a positive epsilon");
-    if (d->branch_count > 64u || tokens == 0u ||
+    if (d->branch_count > 64u || tokens == 0u || tokens > 65535u ||
         tokens * d->branch_count * (uint64_t)d->hidden_size > (UINT64_C(1) << 30) ||
         (uint64_t)d->rank * d->branch_count * d->hidden_size > (UINT64_C(1) << 31))
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
-                       "gated residual: at most 64 branches and 2^30 state values");
+                       "gated residual: at most 64 branches, 65,535 tokens and 2^30 state values");
     return KQ_STATUS_OK;
 }
 
