@@ -203,6 +203,69 @@ __global__ __launch_bounds__(kThreads) void matvec_f32w(const float *__restrict_
     if (nonfinite) kq_flag(status, KQ_DEV_NUMERIC);
 }
 
+/* y[b][r] = W[r] . x[b] for Q8_0 rows wider than the row engine's widest
+ * segment (2048 columns), batch <= 4, in one launch: one row per wave, lane
+ * j takes blocks j, j + 64, ... (34 bytes: an f16 scale and 32 int8 codes,
+ * read as 17 halfwords), each block's d * sum(q * x) added to the lane's
+ * sum, then a wave reduction */
+template <int NB>
+__global__ __launch_bounds__(kThreads) void matvec_q8w(const uint8_t *__restrict__ Wq,
+                                                       uint32_t rows, uint32_t nblk,
+                                                       const float *__restrict__ x,
+                                                       float *__restrict__ y, uint32_t *status) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = __builtin_amdgcn_readfirstlane((blockIdx.x * kThreads + threadIdx.x) >> 6);
+    if (row >= rows) return;
+    const uint32_t cols = nblk * 32u;
+    const uint16_t *wr = (const uint16_t *)(Wq + (size_t)row * nblk * 34u);
+    float acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
+    bool badx = false, bads = false;
+    for (uint32_t k = lane; k < nblk; k += 64u) {
+        const uint16_t *h = wr + (size_t)k * 17u;
+        uint32_t q[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = h[1 + j];
+        const float d = kq_f16_to_f32(h[0]);
+        bads |= !kq_isfinite(d);
+        float part[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) part[b] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float q0 = (float)(int8_t)(q[2 * j] & 0xffu);
+            const float q1 = (float)(int8_t)(q[2 * j] >> 8);
+            const float q2 = (float)(int8_t)(q[2 * j + 1] & 0xffu);
+            const float q3 = (float)(int8_t)(q[2 * j + 1] >> 8);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float4 v = *(const float4 *)(x + (size_t)b * cols + (size_t)k * 32u + 4u * j);
+                badx |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                        !kq_isfinite(v.w);
+                part[b] = fmaf(q0, v.x, part[b]);
+                part[b] = fmaf(q1, v.y, part[b]);
+                part[b] = fmaf(q2, v.z, part[b]);
+                part[b] = fmaf(q3, v.w, part[b]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] = fmaf(d, part[b], acc[b]);
+    }
+    bool nonfinite = false;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        float s = acc[b];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, KQ_WAVE);
+        nonfinite |= !kq_isfinite(s);
+        if (lane == 0u) y[(size_t)b * rows + row] = s;
+    }
+    if (badx) kq_flag(status, KQ_DEV_INPUT);
+    if (bads) kq_flag(status, KQ_DEV_MALFORMED);
+    if (nonfinite) kq_flag(status, KQ_DEV_NUMERIC);
+}
+
 uint32_t grid_for(size_t n) {
     size_t b = (n + kThreads - 1) / kThreads;
     if (b > 4096u) b = 4096u;
@@ -259,6 +322,30 @@ extern "C" hipError_t kq_launch_matvec_f32w(const float *W, uint32_t rows, uint3
         case 2: hipLaunchKernelGGL(matvec_f32w<2>, grid, dim3(kThreads), 0, s, W, rows, cols, xb, yb, status); break;
         case 3: hipLaunchKernelGGL(matvec_f32w<3>, grid, dim3(kThreads), 0, s, W, rows, cols, xb, yb, status); break;
         default: hipLaunchKernelGGL(matvec_f32w<4>, grid, dim3(kThreads), 0, s, W, rows, cols, xb, yb, status); break;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        done += nb;
+    }
+    return hipSuccess;
+}
+
+extern "C" hipError_t kq_launch_matvec_q8w(const void *W, uint32_t rows, uint32_t cols,
+                                           const float *x, uint32_t batch, float *y,
+                                           uint32_t *status, hipStream_t s) {
+    if (cols % 32u != 0u) return hipErrorInvalidValue;
+    const uint8_t *wq = (const uint8_t *)W;
+    const uint32_t nblk = cols / 32u;
+    const dim3 grid((rows + kThreads / 64 - 1) / (kThreads / 64));
+    for (uint32_t done = 0; done < batch;) {
+        const uint32_t nb = batch - done >= 4u ? 4u : batch - done;
+        const float *xb = x + (size_t)done * cols;
+        float *yb = y + (size_t)done * rows;
+        switch (nb) {
+        case 1: hipLaunchKernelGGL(matvec_q8w<1>, grid, dim3(kThreads), 0, s, wq, rows, nblk, xb, yb, status); break;
+        case 2: hipLaunchKernelGGL(matvec_q8w<2>, grid, dim3(kThreads), 0, s, wq, rows, nblk, xb, yb, status); break;
+        case 3: hipLaunchKernelGGL(matvec_q8w<3>, grid, dim3(kThreads), 0, s, wq, rows, nblk, xb, yb, status); break;
+        default: hipLaunchKernelGGL(matvec_q8w<4>, grid, dim3(kThreads), 0, s, wq, rows, nblk, xb, yb, status); break;
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

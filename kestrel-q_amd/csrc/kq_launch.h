@@ -67,6 +67,10 @@ hipError_t kq_launch_gr_write(const float *x, const float *block_output, const f
                               uint32_t tokens, uint32_t branches, uint32_t hidden, float *out,
                               uint32_t *status, hipStream_t stream);
 /* y[b][r] = W[r] . x[b] for F32 weights [rows][cols], cols % 4 == 0 */
+/* y = W x for Q8_0 rows of more than 2048 columns in one launch (batch
+ * chunks of 4), the gated residual's rank projection */
+hipError_t kq_launch_matvec_q8w(const void *W, uint32_t rows, uint32_t cols, const float *x,
+                                uint32_t batch, float *y, uint32_t *status, hipStream_t s);
 hipError_t kq_launch_matvec_f32w(const float *W, uint32_t rows, uint32_t cols, const float *x,
                                  uint32_t batch, float *y, uint32_t *status, hipStream_t stream);
 

@@ -879,6 +879,9 @@ static hipError_t gr_project(kq_hip_context *c, uint32_t type, const void *w, ui
     if (type == KQ_HIP_TYPE_F32)
         return kq_launch_matvec_f32w((const float *)w, (uint32_t)rows, (uint32_t)cols, x, tokens,
                                      y, c->d_status, c->stream);
+    if (type == KQ_HIP_TYPE_Q8_0 && cols > 2048u)
+        return kq_launch_matvec_q8w(w, (uint32_t)rows, (uint32_t)cols, x, tokens, y,
+                                    c->d_status, c->stream);
     return enqueue_matvec(c, type, w, rows, cols, x, tokens, y, NULL, NULL, 0u);
 }
 
