@@ -232,6 +232,9 @@ def test_gated_residual_fails_closed(ctx, gr_model):
     with pytest.raises(kq_hip.KqError) as e:
         ctx.gr_read(g.dims, g.w, dx, T, dx, dg, ds, n)
     assert e.value.name == "ALIASING_VIOLATION"
+    with pytest.raises(kq_hip.KqError) as e:  # the grid's token axis; rejected before launch
+        ctx.gr_read(g.dims, g.w, dx, 65536, dm, dg, ds, n)
+    assert e.value.name == "LIMIT_EXCEEDED"
     bad = kq_hip.gr_dims(0, g.H, g.R, EPS)
     with pytest.raises(kq_hip.KqError) as e:
         ctx.gr_read(bad, g.w, dx, T, dm, dg, ds, n)
