@@ -1,11 +1,15 @@
 """Device parity for the MoE operator, through the C ABI, against the CPU
 oracle. Bars: router logits, probabilities, top-k ids and weights bit-exact
-(the device restates the CPU's arithmetic order); layer outputs within
-|gpu - ref| <= 1e-4 + 1e-3 * max(|ref|, row rms) (conftest.assert_close)."""
+(the device restates the CPU's arithmetic order); layer outputs per element
+within 1e-4 absolute or 1e-3 relative of the oracle, or of the binary64
+value of the same layer where the oracle's own fp32 sums are off by more
+(conftest.assert_close, tests/exact.py)."""
 import numpy as np
 import pytest
 
 from conftest import assert_close, hex_le_f32, load_golden, oracle_threads
+
+import exact
 
 import kq_hip
 import kq_oracle
@@ -146,6 +150,9 @@ class Layer:
         return kq_oracle.moe_execute(self.dims, {k: (t, self.w[k]) for k, t in ROLES.items()},
                                      x, trace=True, threads=oracle_threads())
 
+    def exact(self, x, ids):
+        return exact.moe(self.dims, ROLES, self.w, x, ids)
+
 
 @pytest.fixture(scope="module")
 def layer(ctx):
@@ -158,7 +165,7 @@ def test_moe_decode_one_token(ctx, layer):
     out, ids = layer.run(ctx, x)
     ref, tr = layer.oracle(x)
     assert np.array_equal(ids, tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=layer.exact(x, ids))
 
 
 @pytest.mark.parametrize("tokens", [2, 16])
@@ -167,7 +174,7 @@ def test_moe_multi_token(ctx, layer, tokens):
     out, ids = layer.run(ctx, x)
     ref, tr = layer.oracle(x)
     assert np.array_equal(ids, tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=layer.exact(x, ids))
 
 
 def test_moe_repeated_calls_identical(ctx, layer):
@@ -198,7 +205,7 @@ def test_moe_small_formats(ctx, gate_fmt, down_fmt, T):
     dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in roles.items()}, x, trace=True)
     assert np.array_equal(ctx.download(dids, np.uint32, T * K).reshape(T, K), tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=exact.moe(dims, roles, w, x, tr["selected_ids"]))
     for b in list(bufs.values()) + [scratch, dx, dout, dids]:
         b.close()
 
@@ -280,7 +287,7 @@ def test_moe_prefill_grouped(ctx, layer, tokens):
     out, ids = layer.run(ctx, x)
     ref, tr = layer.oracle(x)
     assert np.array_equal(ids, tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=layer.exact(x, ids))
 
 
 def test_moe_prefill_all_tokens_same_experts(ctx):
@@ -301,7 +308,7 @@ def test_moe_prefill_all_tokens_same_experts(ctx):
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in ROLES.items()}, x, trace=True)
     ids = ctx.download(dids, np.uint32, T * K).reshape(T, K)
     assert np.array_equal(ids, tr["selected_ids"]) and (ids == np.arange(K)).all()
-    assert_close(out, ref)
+    assert_close(out, ref, exact=exact.moe(dims, ROLES, w, x, ids))
 
 
 @pytest.mark.parametrize("down_fmt", ["Q4_K", "Q6_K"])
@@ -328,7 +335,7 @@ def test_moe_prefill_shapes(ctx, H, I, down_fmt):
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in roles.items()}, x, trace=True,
                                     threads=oracle_threads())
     assert np.array_equal(ctx.download(dids, np.uint32, T * K).reshape(T, K), tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=exact.moe(dims, roles, w, x, tr["selected_ids"]))
 
 
 # ---------------- one-token execution: certified routing ----------------
@@ -348,7 +355,7 @@ def test_moe_decode_many_tokens_ids_exact(ctx, layer):
         out, ids, cert = layer.run(ctx, x, flag=True)
         ref, tr = layer.oracle(x)
         assert np.array_equal(ids, tr["selected_ids"]), t
-        assert_close(out, ref)
+        assert_close(out, ref, exact=layer.exact(x, ids))
         if top_gaps(router, x[0], layer.K).min() > 1e-2:
             wide += 1
             assert cert == 1, t
@@ -378,7 +385,8 @@ def test_moe_decode_certified_shapes(ctx, H, E, K):
         ref, tr = kq_oracle.moe_execute(dims, {k: (r, w[k]) for k, r in ROLES.items()}, x,
                                         trace=True)
         assert np.array_equal(ctx.download(dids, np.uint32, K)[None, :], tr["selected_ids"]), t
-        assert_close(ctx.download(dout, np.float32, H)[None, :], ref)
+        assert_close(ctx.download(dout, np.float32, H)[None, :], ref,
+                     exact=exact.moe(dims, ROLES, w, x, tr["selected_ids"]))
         if top_gaps(router, x[0], K).min() > 1e-3:
             wide += 1
             assert cert == 1, t
@@ -419,7 +427,8 @@ def test_moe_decode_ties_fall_back_to_exact_chains(ctx, pattern):
     dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
     ref, tr = kq_oracle.moe_execute(dims, {k: (t, w[k]) for k, t in ROLES.items()}, x, trace=True)
     assert np.array_equal(ctx.download(dids, np.uint32, K)[None, :], tr["selected_ids"])
-    assert_close(ctx.download(dout, np.float32, H)[None, :], ref)
+    assert_close(ctx.download(dout, np.float32, H)[None, :], ref,
+                 exact=exact.moe(dims, ROLES, w, x, tr["selected_ids"]))
 
 
 def run_layer(ctx, H, E, K, I, T, gate_fmt, down_fmt, sgate_fmt, sdown_fmt, seed):
@@ -444,7 +453,7 @@ def run_layer(ctx, H, E, K, I, T, gate_fmt, down_fmt, sgate_fmt, sdown_fmt, seed
                                     threads=oracle_threads())
     for b in list(bufs.values()) + [scratch, dx, dout, dids]:
         b.close()
-    return out, ids, ref, tr
+    return out, ids, ref, tr, exact.moe(dims, roles, w, x, tr["selected_ids"])
 
 
 def test_moe_reference_model_layer(ctx):
@@ -453,10 +462,10 @@ def test_moe_reference_model_layer(ctx):
     # Q4_K gate/up, Q5_1 routed down, a Q8_0 shared expert. Rows are cut
     # into column segments (2048 + 512 for gate/up, 512 + 128 for down).
     say("reference-model layer 2560/512/10/640")
-    out, ids, ref, tr = run_layer(ctx, 2560, 512, 10, 640, 1, "Q4_K", "Q5_1", "Q8_0", "Q8_0",
-                                  S.W_MOE + 2560)
+    out, ids, ref, tr, ex = run_layer(ctx, 2560, 512, 10, 640, 1, "Q4_K", "Q5_1", "Q8_0",
+                                      "Q8_0", S.W_MOE + 2560)
     assert np.array_equal(ids, tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=ex)
 
 
 @pytest.mark.parametrize("H,E,K,I,T,g,d,sg,sd", [
@@ -469,9 +478,9 @@ def test_moe_reference_model_layer(ctx):
 ], ids=["real-64e-3tok", "768x384", "640x96", "1280x320", "3072x256", "mixed-16tok"])
 def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
     seed = S.W_MOE + 3000 + H + I + T
-    out, ids, ref, tr = run_layer(ctx, H, E, K, I, T, g, d, sg, sd, seed)
+    out, ids, ref, tr, ex = run_layer(ctx, H, E, K, I, T, g, d, sg, sd, seed)
     assert np.array_equal(ids, tr["selected_ids"])
-    assert_close(out, ref)
+    assert_close(out, ref, exact=ex)
 
 
 def test_moe_rejects_unsplittable_rows(ctx):
