@@ -203,6 +203,26 @@ kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *context,
                                     uint32_t *device_token_ids,
                                     kq_diagnostic *diagnostic);
 
+/* kq_hip_lm_head_greedy_f32 without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops): the argmax partials, which the
+ * entry point above allocates in the context on first use and grows on
+ * demand, live here in a static array of 131,072 (value, row) pairs
+ * (1 MiB) that each device holds for the life of the process. Same
+ * arguments, validation, kernels and results; a call needing more
+ * partials than the array holds (wave count of its launches x batch)
+ * fails with KQ_STATUS_LIMIT_EXCEEDED before any launch. All calls on one
+ * device share the array: calls that overlap in time on the same device
+ * (other streams or contexts) race. */
+kq_status kq_hip_lm_head_greedy_f32_noalloc(kq_hip_context *context,
+                                            uint32_t type_id,
+                                            const void *device_weights,
+                                            uint64_t vocab, uint64_t columns,
+                                            const float *device_hidden,
+                                            uint32_t batch, float *device_logits,
+                                            uint32_t *device_token_ids,
+                                            kq_diagnostic *diagnostic);
+
 /* ------------------------------------------------------------------ */
 /* MoE operator. */
 

@@ -53,6 +53,12 @@ hipError_t kq_launch_argmax(const float *logits, uint32_t count, uint32_t batch,
 hipError_t kq_launch_argmax_from_parts(const float *part_v, const uint32_t *part_i,
                                        uint32_t nparts, uint32_t batch, uint32_t *ids,
                                        hipStream_t stream);
+/* The allocation-free LM head's partials: a file-scope device array of
+ * kq_launch_noalloc_parts() (value, row) pairs per device. _init (with
+ * `device` current) returns its device address, looked up once per device;
+ * the values come first, then the row ids. */
+uint32_t kq_launch_noalloc_parts(void);
+hipError_t kq_launch_noalloc_scratch_init(int device, void **out);
 
 /* gated residual around a layer block (kq_gr.hip) */
 hipError_t kq_launch_gr_norm(const float *x, const float *norm, uint32_t tokens,

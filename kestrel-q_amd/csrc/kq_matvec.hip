@@ -20,8 +20,46 @@
  * fused LM head every wave also keeps a running (max, row) per batch column
  * and writes one partial; a one-block kernel merges the partials.
  */
+#include <mutex>
+
 #include "kq_launch.h"
 #include "kq_rowdot.h"
+
+/* Argmax partials of the allocation-free LM head
+ * (kq_hip_lm_head_greedy_f32_noalloc): kNoallocParts values, then as many
+ * row ids. Each device holds its own copy for the life of the process and
+ * every call on that device shares it. Host code reaches it only through
+ * the address hipGetSymbolAddress returns for the device
+ * (kq_launch_noalloc_scratch_init); the name itself is not a device
+ * address on the host. */
+constexpr uint32_t kNoallocParts = 1u << 17;
+static __device__ __align__(256) uint8_t scratch[kNoallocParts * 8u];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+}  // namespace
+
+extern "C" uint32_t kq_launch_noalloc_parts(void) { return kNoallocParts; }
+
+/* Looks up this device's copy of `scratch` once per device; `device` must
+ * be the current device. */
+extern "C" hipError_t kq_launch_noalloc_scratch_init(int device, void **out) {
+    if (device < 0 || device >= kMaxDevices || out == nullptr) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
 
 namespace {
 

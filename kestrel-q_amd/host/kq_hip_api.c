@@ -39,6 +39,7 @@ struct kq_hip_context {
     uint64_t part_cap;
     void *stage[2];     /* pinned staging for file-backed uploads */
     hipEvent_t stage_done[2];
+    void *noalloc;      /* this device's allocation-free LM-head partials */
 };
 
 struct kq_hip_moe_config {
@@ -143,6 +144,9 @@ kq_status kq_hip_context_create(int device, kq_hip_context **out, kq_diagnostic 
     if (e == hipSuccess) e = hipHostMalloc((void **)&c->h_status, sizeof(uint32_t), hipHostMallocDefault);
     if (e == hipSuccess) e = hipMemsetAsync(c->d_status, 0, sizeof(uint32_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    /* the device address of this device's static partials array, looked up
+     * once per device with the device current */
+    if (e == hipSuccess) e = kq_launch_noalloc_scratch_init(device, &c->noalloc);
     if (e != hipSuccess) {
         kq_status st = hip_fail(diag, e, "context setup");
         kq_hip_context_destroy(c);
@@ -554,11 +558,16 @@ kq_status kq_hip_greedy_argmax_f32(kq_hip_context *c, const float *logits, uint6
                   "argmax launch", diag);
 }
 
-kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const void *w,
-                                    uint64_t vocab, uint64_t cols, const float *h,
-                                    uint32_t batch, float *logits, uint32_t *ids,
-                                    kq_diagnostic *diag) {
+/* The LM head's validation, partial count and launches. noalloc: the
+ * partials live in the device's static array (no allocation, at most
+ * kq_launch_noalloc_parts() of them per call); otherwise in the context's
+ * partials, grown on demand. */
+static kq_status lm_head(kq_hip_context *c, uint32_t type_id, const void *w, uint64_t vocab,
+                         uint64_t cols, const float *h, uint32_t batch, float *logits,
+                         uint32_t *ids, int noalloc, kq_diagnostic *diag) {
     uint32_t nparts;
+    float *pv;
+    uint32_t *pi;
     hipError_t e;
     kq_status st;
     kq_diagnostic_clear(diag);
@@ -578,12 +587,40 @@ kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const v
     }
     if (nparts == 0u)
         return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "lm head: no launch configuration");
-    st = ensure_parts(c, (uint64_t)nparts * batch, diag);
-    if (st != KQ_STATUS_OK) return st;
-    e = enqueue_matvec(c, type_id, w, vocab, cols, h, batch, logits, c->part_v, c->part_i, nparts);
-    if (e == hipSuccess)
-        e = kq_launch_argmax_from_parts(c->part_v, c->part_i, nparts, batch, ids, c->stream);
+    if (noalloc) {
+        const uint64_t cap = kq_launch_noalloc_parts();
+        if ((uint64_t)nparts * batch > cap)
+            return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
+                           "allocation-free lm head: %llu argmax partials needed, the static "
+                           "array holds %llu (use kq_hip_lm_head_greedy_f32)",
+                           (unsigned long long)nparts * batch, (unsigned long long)cap);
+        if (c->noalloc == NULL)
+            return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "static partials were not set up");
+        pv = (float *)c->noalloc;
+        pi = (uint32_t *)((char *)c->noalloc + cap * sizeof(float));
+    } else {
+        st = ensure_parts(c, (uint64_t)nparts * batch, diag);
+        if (st != KQ_STATUS_OK) return st;
+        pv = c->part_v;
+        pi = c->part_i;
+    }
+    e = enqueue_matvec(c, type_id, w, vocab, cols, h, batch, logits, pv, pi, nparts);
+    if (e == hipSuccess) e = kq_launch_argmax_from_parts(pv, pi, nparts, batch, ids, c->stream);
     return finish(c, e, "lm head launch", diag);
+}
+
+kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const void *w,
+                                    uint64_t vocab, uint64_t cols, const float *h,
+                                    uint32_t batch, float *logits, uint32_t *ids,
+                                    kq_diagnostic *diag) {
+    return lm_head(c, type_id, w, vocab, cols, h, batch, logits, ids, 0, diag);
+}
+
+kq_status kq_hip_lm_head_greedy_f32_noalloc(kq_hip_context *c, uint32_t type_id, const void *w,
+                                            uint64_t vocab, uint64_t cols, const float *h,
+                                            uint32_t batch, float *logits, uint32_t *ids,
+                                            kq_diagnostic *diag) {
+    return lm_head(c, type_id, w, vocab, cols, h, batch, logits, ids, 1, diag);
 }
 
 kq_status kq_hip_f32_expf(kq_hip_context *c, const float *in, uint64_t n, float *out,

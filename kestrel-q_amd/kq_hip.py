@@ -184,6 +184,10 @@ SIGNATURES = {
     "kq_hip_lm_head_greedy_f32": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64,
                                             C.c_uint64, C.c_void_p, C.c_uint32, C.c_void_p,
                                             C.c_void_p, C.c_void_p]),
+    "kq_hip_lm_head_greedy_f32_noalloc": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p,
+                                                    C.c_uint64, C.c_uint64, C.c_void_p,
+                                                    C.c_uint32, C.c_void_p, C.c_void_p,
+                                                    C.c_void_p]),
     "kq_hip_moe_config_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "kq_hip_moe_config_close": (None, [C.c_void_p]),
     "kq_hip_moe_config_scratch_bytes": (C.c_uint64, [C.c_void_p, C.c_uint64]),
@@ -387,11 +391,13 @@ class Context:
         check(lib().kq_hip_greedy_argmax_f32(self._h, self._p(logits), count, batch,
                                              self._p(ids), C.byref(d)), d)
 
-    def lm_head(self, type_id: int, w, vocab: int, cols: int, h, batch: int, logits, ids) -> None:
+    def lm_head(self, type_id: int, w, vocab: int, cols: int, h, batch: int, logits, ids,
+                noalloc: bool = False) -> None:
         d = Diagnostic()
-        check(lib().kq_hip_lm_head_greedy_f32(self._h, type_id, self._p(w), vocab, cols,
-                                              self._p(h), batch, self._p(logits), self._p(ids),
-                                              C.byref(d)), d)
+        fn = lib().kq_hip_lm_head_greedy_f32_noalloc if noalloc else \
+            lib().kq_hip_lm_head_greedy_f32
+        check(fn(self._h, type_id, self._p(w), vocab, cols, self._p(h), batch, self._p(logits),
+                 self._p(ids), C.byref(d)), d)
 
     def expf(self, x, count: int, out) -> None:
         d = Diagnostic()
