@@ -159,6 +159,15 @@ int kqo_gr_read(uint32_t nbranch, uint32_t hidden, uint32_t rank, float eps,
 void kqo_gr_write(uint32_t nbranch, uint32_t hidden, const float *branches,
                   const float *block_output, const float *write_gate, float *out);
 
+/* kq_certify.c: the device's certified one-token routing restated on the
+ * CPU (ids of the certified selection, or *certified = 0), and a campaign
+ * of random and near-tie cases against kqo_moe_route_f32. */
+int kqo_route_certify(uint32_t experts, uint32_t hidden, uint32_t top_k, const float *router,
+                      const float *x, uint32_t *ids, int *certified);
+int kqo_certify_campaign(uint64_t seed, uint64_t trials, uint32_t experts, uint32_t hidden,
+                         uint32_t top_k, int mode, float sigma, double slack, int threads,
+                         uint64_t *stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,6 +93,8 @@ def _declare(l: C.CDLL) -> None:
     l.kqo_moe_execute.argtypes = [C.POINTER(MoeDims), C.POINTER(MoeWeights), P, U64, P,
                                   C.POINTER(MoeTrace), I]
     l.kqo_moe_permutation.argtypes = [P, U64, U32, U32, P, P, P]
+    l.kqo_route_certify.argtypes = [U32, U32, U32, P, P, P, C.POINTER(I)]
+    l.kqo_certify_campaign.argtypes = [U64, U64, U32, U32, U32, I, F, C.c_double, I, P]
 
 
 def _p(a: np.ndarray) -> int:
@@ -292,6 +294,41 @@ def moe_execute(dims: dict, weights: dict, hidden: np.ndarray, trace: bool = Fal
     if st != OK:
         raise OracleError(st)
     return (out, tr_arrays) if trace else out
+
+
+def route_certify(router: np.ndarray, x: np.ndarray, top_k: int):
+    """The device's certified one-token routing restated (kq_certify.c):
+    (certified, ids)."""
+    router = np.ascontiguousarray(router, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    E, H = router.shape
+    ids = np.zeros(top_k, np.uint32)
+    cert = C.c_int()
+    st = lib().kqo_route_certify(E, H, top_k, _p(router), _p(x), _p(ids), C.byref(cert))
+    if st != OK:
+        raise OracleError(st)
+    return bool(cert.value), ids
+
+
+CAMPAIGN_MODES = {"random": 0, "tie-at-boundary": 1, "tie-inside": 2, "tie-below-bound": 3}
+
+
+def certify_campaign(seed: int, trials: int, experts: int, hidden: int, top_k: int,
+                     mode: str, sigma: float = 0.02, threads: int = 1,
+                     slack: float = 1.0) -> dict:
+    """Certified selections against the exact route on generated cases
+    (kq_certify.c kqo_certify_campaign). slack < 1 scales the bounds and the
+    margin down: a planted unsound certification, which the campaign must
+    catch."""
+    st_arr = np.zeros(6, np.uint64)
+    st = lib().kqo_certify_campaign(seed, trials, experts, hidden, top_k,
+                                    CAMPAIGN_MODES[mode], sigma, slack, threads,
+                                    _p(st_arr))
+    if st != OK:
+        raise OracleError(st)
+    keys = ("trials", "certified", "certified_mismatch", "rounding_decided",
+            "first_mismatch_plus_1", "route_failures")
+    return {k: int(v) for k, v in zip(keys, st_arr)}
 
 
 def moe_permutation(ids: np.ndarray, experts: int):

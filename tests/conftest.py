@@ -129,6 +129,12 @@ def assert_close(got, ref, rtol=RTOL, atol=ATOL, exact=None, what=""):
     return rec
 
 
+def record(what: str, values: dict) -> None:
+    """A measured figure of a test (counts, rates) for the same log."""
+    TOL_RECORDS.append({"test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0],
+                        "what": what, **values})
+
+
 def pytest_sessionfinish(session, exitstatus):
     path = os.environ.get("KQ_TOL_LOG")
     if path and TOL_RECORDS:

@@ -7,7 +7,7 @@ value of the same layer where the oracle's own fp32 sums are off by more
 import numpy as np
 import pytest
 
-from conftest import assert_close, hex_le_f32, load_golden, oracle_threads
+from conftest import assert_close, hex_le_f32, load_golden, oracle_threads, record
 
 import exact
 
@@ -360,6 +360,75 @@ def test_moe_decode_many_tokens_ids_exact(ctx, layer):
             wide += 1
             assert cert == 1, t
     assert wide >= 8
+
+
+def near_tie(router, x, K, c):
+    """x nudged (least-norm, binary64) so that the K-th and (K+1)-th
+    logits by binary64 value are c times the sum of their certification
+    bounds apart (1.001 * 2^-24 * sum of |prefix sums|, as router_bounds)."""
+    r64, x64 = router.astype(np.float64), x.astype(np.float64)
+    a = r64 @ x64
+    order = np.argsort(-a, kind="stable")
+    hi, lo = order[K - 1], order[K]
+
+    def bound(e):
+        p = (router[e] * x).astype(np.float64)
+        return 1.001 * 2.0 ** -24 * np.abs(np.cumsum(p)).sum()
+    g = c * (bound(hi) + bound(lo))
+    d = r64[hi] - r64[lo]
+    return (x64 - ((a[hi] - a[lo] - g) / (d @ d)) * d).astype(np.float32)
+
+
+def test_moe_decode_campaign_10000_tokens(ctx, layer):
+    # 10,000 single-token decode calls on the 512-expert top-10 layer:
+    # 8,000 activations ~N(0,1) and 2,000 nudged so that the selection's
+    # boundary pair is c x its bounds apart, c log-uniform in [2^-6, 2^6]
+    # (straddling the certification threshold). Every call's ids must be the
+    # oracle's exact route, in order; the loop stops at the first mismatch.
+    # The device's certification flag is compared with the CPU restatement
+    # (oracle/kq_certify.c) on the nudged tokens and every tenth other one.
+    E, H, K = layer.E, layer.H, layer.K
+    router = layer.w["router"].reshape(E, H)
+    dims = dict(hidden=H, experts=E, top_k=K, inter=1, shared_inter=1)
+    n_rand, n_tie = 8000, 2000
+    xs = S.normal_f32(S.stream_key(S.W_MOE, S.R_HIDDEN, 10_000), (n_rand + n_tie) * H)
+    xs = xs.reshape(-1, H)
+    cs = 2.0 ** (-6.0 + 12.0 * (S.u64(S.stream_key(S.W_MOE, 77, 10_000), n_tie) >> np.uint64(11))
+                 .astype(np.float64) * 2.0 ** -53)
+    n = layer.cfg.scratch_bytes(1)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.alloc(H * 4), ctx.alloc(H * 4), ctx.alloc(K * 4)
+    mw = kq_hip.moe_weights(layer.bufs)
+    th = oracle_threads()
+    stats = {"certified": 0, "compared": 0, "flag_agree": 0, "tie_certified": 0}
+    for t in range(n_rand + n_tie):
+        x = xs[t] if t < n_rand else near_tie(router, xs[t], K, cs[t - n_rand])
+        x = np.ascontiguousarray(x)
+        d = kq_hip.Diagnostic()
+        kq_hip.check(kq_hip.lib().kq_hip_upload(ctx._h, kq_hip.C.c_void_p(dx.ptr), x.ctypes.data,
+                                                x.nbytes, kq_hip.C.byref(d)), d)
+        ctx.moe_execute(layer.cfg, mw, dx, 1, dout, dids, scratch, n)
+        ids = ctx.download(dids, np.uint32, K)
+        cert = certified_flag(ctx, scratch, n)
+        _, _, want, _ = kq_oracle.moe_route(dims, (kq_oracle.F32, router), x, threads=th)
+        assert np.array_equal(ids, want), (t, ids, want, cert)
+        stats["certified"] += cert
+        if t >= n_rand:
+            stats["tie_certified"] += cert
+        if t >= n_rand or t % 10 == 0:
+            c_cpu, c_ids = kq_oracle.route_certify(router, x, K)
+            stats["compared"] += 1
+            stats["flag_agree"] += int(bool(cert) == c_cpu)
+            if c_cpu:
+                assert np.array_equal(c_ids, want), t
+        if t % 2000 == 1999:
+            say(f"campaign: {t + 1} tokens, ids exact; {stats}")
+    for b in (scratch, dx, dout, dids):
+        b.close()
+    record("decode routing campaign", dict(stats, tokens=n_rand + n_tie, nudged=n_tie))
+    # random tokens nearly all certify; nudged ones split around the bound
+    assert stats["certified"] - stats["tie_certified"] >= 0.9 * n_rand
+    assert 0 < stats["tie_certified"] < n_tie
+    assert stats["flag_agree"] >= 0.99 * stats["compared"], stats
 
 
 @pytest.mark.parametrize("H,E,K", [(512, 96, 6), (256, 40, 3), (1024, 130, 8), (512, 64, 12)])
