@@ -1,7 +1,8 @@
 """Benchmark of the MI355X quantized-weight path (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
-                    [--workload NAME|all|headline|hbm_copy_64mb] [--no-cpu] [--no-graph]
+                    [--workload NAME[,NAME...]|all|headline|hbm_copy_64mb] [--no-cpu]
+                    [--graph]
 
 A step is one pass of the hot path over one batch of synthetic input with the
 weights already resident in HBM. The headline workload (value / metric) is
@@ -13,12 +14,22 @@ The same JSON line carries every other workload (Q8_0 / Q6_K matvecs,
 the roofline of the headline kernel and the CPU baseline (the C oracle,
 timed on this host on a bounded sample).
 
-Timing: W untimed warmup steps, then K steps captured into a HIP graph on the
-library's stream and replayed between two HIP events on that stream, with
-device synchronisation on both sides. Weight replicas (bit-identical device
-copies at distinct addresses) rotate so that the bytes touched between two
-uses of a replica exceed 512 MB, twice the ~256 MB Infinity Cache: every
-weight read is an HBM read.
+Timing: W untimed warmup steps and a device synchronisation; then the
+stream gets a 512 MiB device copy (which evicts the ~256 MB Infinity Cache)
+and a hold kernel of 100 us + 25 us per step, the first HIP event, the K
+steps' launches and the second event, all enqueued by the host while the
+copy and the hold run, so the events bracket the K launches running back to
+back. Device synchronisation on both sides. Weight replicas (bit-identical
+device copies at distinct addresses) rotate so that the bytes touched
+between two uses of a replica within the timed steps exceed 512 MB, twice
+the Infinity Cache: every weight read in the timed region is an HBM read,
+for any K. --graph captures the K steps in a HIP graph instead (replayed
+once untimed, then timed the same way); its replay adds about 12 us per
+timed region on this part (per step: 0.6 us at K = 20, 0.06 us at 200).
+
+Floors measured the same way (libkq_floor.so): an empty launch, and plain
+streaming reads of the headline's, the 131072 x 2048 matvec's and the LM
+head's weight bytes.
 """
 from __future__ import annotations
 
@@ -40,6 +51,7 @@ import kq_synth as S  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 512 << 20
+FLUSH_BYTES = 256 << 20  # copied between the untimed and the timed replay
 
 # ---------------------------------------------------------------- HIP runtime
 _hip = None
@@ -94,8 +106,31 @@ def d2d(ctx, dst, src, nbytes):
                                 C.c_void_p(ctx.stream)), "hipMemcpyAsync")
 
 
-def time_steps(ctx, step, warmup: int, steps: int, graph: bool) -> float:
-    """ms per step over `steps` steps; `step(i)` enqueues step i on ctx's stream."""
+_flush = {}
+
+
+def flush_mall(ctx):
+    """Device copy of FLUSH_BYTES (2 x FLUSH_BYTES touched) on ctx's stream:
+    evicts the Infinity Cache before a timed replay."""
+    if "bufs" not in _flush:
+        _flush["bufs"] = (ctx.alloc(FLUSH_BYTES), ctx.alloc(FLUSH_BYTES))
+    a, b = _flush["bufs"]
+    d2d(ctx, b.ptr, a.ptr, FLUSH_BYTES)
+
+
+def lead_in(ctx, flush: bool, steps: int) -> None:
+    """Work the device runs right before the timed region's first event, so
+    the host has enqueued the whole region before it starts: the 512 MiB
+    copy (flush) and a hold of 100 us plus 25 us per step (at most 10 ms)."""
+    if flush:
+        flush_mall(ctx)
+    hcheck(floor_lib().kq_floor_hold(min(10000, 100 + 25 * steps), C.c_void_p(ctx.stream)),
+           "kq_floor_hold")
+
+
+def time_steps(ctx, step, warmup: int, steps: int, graph: bool, flush: bool = True) -> float:
+    """ms per step over `steps` steps; `step(i)` enqueues step i on ctx's stream.
+    flush: evict the Infinity Cache before the timed steps."""
     stream = C.c_void_p(ctx.stream)
     ctx.set_async(True)
     for i in range(warmup):
@@ -112,6 +147,7 @@ def time_steps(ctx, step, warmup: int, steps: int, graph: bool) -> float:
         hcheck(hip().hipGraphInstantiate(C.byref(ge), g, None, None, 0), "hipGraphInstantiate")
         hcheck(hip().hipGraphLaunch(ge, stream), "hipGraphLaunch")  # untimed replay
         hcheck(hip().hipStreamSynchronize(stream), "hipStreamSynchronize")
+        lead_in(ctx, flush, steps)
         hcheck(hip().hipEventRecord(ev.a, stream), "hipEventRecord")
         hcheck(hip().hipGraphLaunch(ge, stream), "hipGraphLaunch")
         hcheck(hip().hipEventRecord(ev.b, stream), "hipEventRecord")
@@ -119,6 +155,7 @@ def time_steps(ctx, step, warmup: int, steps: int, graph: bool) -> float:
         hip().hipGraphExecDestroy(ge)
         hip().hipGraphDestroy(g)
     else:
+        lead_in(ctx, flush, steps)
         hcheck(hip().hipEventRecord(ev.a, stream), "hipEventRecord")
         for i in range(steps):
             step(warmup + i)
@@ -144,6 +181,15 @@ def replicas(ctx, host: np.ndarray, want_bytes: int, cap: int = 256):
     return out
 
 
+def reuse_bytes(nrep: int, nbytes: int, steps: int, warm: bool = False):
+    """Weight bytes read between two uses of one replica in the timed
+    replay (None: no replica is read twice). The copy before the replay
+    separates it from the untimed one."""
+    if warm:
+        return 0
+    return nrep * nbytes if steps > nrep else None
+
+
 # ---------------------------------------------------------------- workloads
 def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph, warm=False):
     """warm: one weight copy, re-read every step from the caches (a
@@ -154,12 +200,13 @@ def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph, warm=False):
     reps = replicas(ctx, w, 0 if warm else MALL_DEFEAT_BYTES, cap=1 if warm else 256)
     dx, dy = ctx.upload(x), ctx.alloc(rows * batch * 4)
     ms = time_steps(ctx, lambda i: ctx.matvec(t, reps[i % len(reps)], rows, cols, dx, batch, dy),
-                    warmup, steps, graph)
+                    warmup, steps, graph, flush=not warm)
     nbytes = w.nbytes + x.nbytes + rows * batch * 4
     for b in reps + [dx, dy]:
         b.close()
     return {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
             "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "replicas": len(reps),
+            "bytes_between_reuse": reuse_bytes(len(reps), w.nbytes, steps, warm),
             "flops_per_step": 2 * rows * cols * batch}
 
 
@@ -302,6 +349,52 @@ def wl_copy(ctx, nbytes, warmup, steps, graph):
             "hbm_frac": 2 * nbytes / ms / 1e6 / HBM_PEAK_GBS, "copy_bytes": nbytes}
 
 
+_floor = None
+
+
+def floor_lib():
+    global _floor
+    if _floor is None:
+        path = ROOT / "kestrel-q_amd" / "_build" / "libkq_floor.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is missing: build with __graft_entry__.build()")
+        _floor = C.CDLL(str(path))
+        _floor.kq_floor_empty.argtypes = [C.c_void_p]
+        _floor.kq_floor_hold.argtypes = [C.c_uint32, C.c_void_p]
+        _floor.kq_floor_read.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_void_p, C.c_void_p]
+    return _floor
+
+
+def wl_floor_empty(ctx, warmup, steps, graph):
+    """An empty kernel per step: the launch cost every workload pays."""
+    ms = time_steps(ctx, lambda i: hcheck(floor_lib().kq_floor_empty(C.c_void_p(ctx.stream)),
+                                          "kq_floor_empty"), warmup, steps, graph)
+    return {"ms_per_step": ms}
+
+
+def wl_floor_read(ctx, nbytes, loads, warmup, steps, graph):
+    """A plain streaming read of nbytes per step (replicas rotate as for the
+    matvecs): the fastest this size can be read in one launch, over the
+    given numbers of 16-byte loads per thread (the best one is reported)."""
+    host = np.zeros(nbytes, np.uint8)
+    reps = replicas(ctx, host, MALL_DEFEAT_BYTES, cap=256)
+    sink = ctx.alloc(4)
+    per = {}
+    for ld in loads:
+        per[ld] = time_steps(ctx, lambda i: hcheck(floor_lib().kq_floor_read(
+            C.c_void_p(reps[i % len(reps)].ptr), nbytes, ld, C.c_void_p(sink.ptr),
+            C.c_void_p(ctx.stream)), "kq_floor_read"), warmup, steps, graph)
+    for b in reps + [sink]:
+        b.close()
+    best = min(per, key=per.get)
+    ms = per[best]
+    return {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
+            "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "replicas": len(reps),
+            "loads_per_thread": best, "us_by_loads_per_thread":
+                {str(k): round(v * 1e3, 3) for k, v in per.items()},
+            "bytes_between_reuse": reuse_bytes(len(reps), nbytes, steps)}
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(threads: int, budget_s: float = 3.0) -> dict:
     """The C oracle (restatement of the reference's scalar path, reference fp
@@ -348,14 +441,37 @@ def cpu_baseline(threads: int, budget_s: float = 3.0) -> dict:
     return res
 
 
-def cpu_name() -> str:
+def host_cpus() -> dict:
+    """The host's CPUs as this process sees them: nproc, the affinity mask,
+    the cgroup CPU quota and the lscpu model. `usable` = the smaller of the
+    affinity count and the quota: threads beyond it only wait for a share."""
+    info = {"nproc": os.cpu_count() or 1}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["affinity"] = info["nproc"]
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
         pass
-    return "unknown"
+    info["cgroup_cpu_quota"] = quota
+    usable = info["affinity"]
+    if quota is not None:
+        usable = max(1, min(usable, int(quota)))
+    info["usable"] = usable
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core"):
+                info["lscpu_" + k.strip().lower().replace("(s)", "s").replace(" ", "_")] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
 
 
 # ---------------------------------------------------------------- main
@@ -366,19 +482,22 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="all")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--graph", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="stream launches (the default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         return 2
-    graph = not args.no_graph
+    graph = args.graph
     K, W = args.steps, args.warmup
     wanted = args.workload
     work = {}
     with kq_hip.Context(0) as ctx:
+        names = set(wanted.split(","))
+
         def run(name, fn):
-            if wanted in ("all", name) or (wanted == "headline" and name == HEADLINE):
+            if names & {"all", name} or ("headline" in names and name == HEADLINE):
                 print(f"[bench] {name} ...", file=sys.stderr, flush=True)
                 t0 = time.time()
                 work[name] = fn()
@@ -387,6 +506,10 @@ def main() -> int:
 
         HEADLINE = "q4k_matvec_4096x2048_b1"
         run(HEADLINE, lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph))
+        # what any launch costs, and a plain read of the headline's weight
+        # bytes in one launch
+        run("floor_empty_launch", lambda: wl_floor_empty(ctx, W, K, graph))
+        run("floor_read_4718592b", lambda: wl_floor_read(ctx, 4718592, (1, 2, 4), W, K, graph))
         run("q8_0_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q8_0", 4096, 2048, 1, W, K, graph))
         run("q6k_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q6_K", 4096, 2048, 1, W, K, graph))
         run("q5k_matvec_4096x2048_b1", lambda: wl_matvec(ctx, "Q5_K", 4096, 2048, 1, W, K, graph))
@@ -400,6 +523,10 @@ def main() -> int:
         # Q4_K row engine sustains
         run("q4k_matvec_131072x2048_b1",
             lambda: wl_matvec(ctx, "Q4_K", 131072, 2048, 1, 10, max(10, K // 2), graph))
+        run("floor_read_150994944b",
+            lambda: wl_floor_read(ctx, 150994944, (2, 4, 8), 10, max(10, K // 2), graph))
+        run("floor_read_255252480b",
+            lambda: wl_floor_read(ctx, 255252480, (2, 4, 8), 10, max(10, K // 2), graph))
         for f in ("Q4_K", "Q8_0", "Q6_K", "Q5_K", "Q5_1", "IQ4_NL"):
             run(f"dequant_64m_{f.lower()}",
                 lambda f=f: wl_dequant(ctx, f, 5, max(10, K // 4), graph))
@@ -418,10 +545,11 @@ def main() -> int:
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))
         run("moe_block_decode_1tok_4x2560",
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640", block=True))
-        if wanted == "hbm_copy_64mb":
+        if "hbm_copy_64mb" in names:
             run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))
     head = work.get(HEADLINE)
-    threads = int(os.environ.get("KQ_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    cpus = host_cpus()
+    threads = int(os.environ.get("KQ_CPU_THREADS", cpus["usable"]))
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
@@ -444,7 +572,7 @@ def main() -> int:
         "data": "synthetic (seeded SplitMix64 GGUF blocks, N(0,1) activations)",
         "config": {"workload": HEADLINE, "rows": 4096, "cols": 2048, "batch": 1,
                    "format": "Q4_K", "timing": "hip graph of K launches, hip events" if graph
-                   else "stream launches, hip events"},
+                   else "K stream launches behind a hold kernel, hip events"},
         "hbm_frac": round(head["hbm_frac"], 4) if head else None,
         "moe_decode_tokens_per_s": round(work["moe_decode_1tok"]["tokens_per_s"], 1)
         if "moe_decode_1tok" in work else None,
@@ -453,18 +581,44 @@ def main() -> int:
         "workloads": work,
     }
     if head:
+        # achieved: algorithmic bytes per launch / the launch's time from HIP
+        # events around the timed replay on the library's stream (the same
+        # figure as ms_per_step); traffic: FETCH_SIZE + WRITE_SIZE per
+        # dispatch from the committed counter runs
         line["roofline"] = {"bound": "hbm", "achieved": round(head["GBps"], 2),
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(head["GBps"] / HBM_PEAK_GBS, 4),
-                            "traffic": traffic_from_profiles(HEADLINE)}
+                            "traffic": traffic_from_profiles(HEADLINE),
+                            "kernel_us": round(head["ms_per_step"] * 1e3, 3),
+                            "time_source": "hip events around the timed replay of the K "
+                                           "launches, enqueued behind a hold kernel "
+                                           "(authoritative); "
+                                           "rocprofv3 durations in profiles/ include the "
+                                           "profiler's per-dispatch completion signal",
+                            "traffic_source": "profiles/traffic.json (rocprofv3 --pmc "
+                                              "FETCH_SIZE, WRITE_SIZE, scaled by a 64 MiB copy)"}
+        floors = {k: work[k]["ms_per_step"] * 1e3 for k in ("floor_empty_launch",
+                                                             "floor_read_4718592b") if k in work}
+        if floors:
+            line["roofline"]["floors_us"] = {k: round(v, 3) for k, v in floors.items()}
     if cpu:
         key = f"q4k_matvec_{threads}t"
         line["cpu_baseline"] = {"value": round(cpu[key]["GBps"], 4), "unit": "GB/s",
                                 "cores": threads, "kind": "port",
                                 "sample": "the same 4096x2048 Q4_K matvec, median of repeated "
                                           "full runs (C oracle, reference fp flags, row-parallel "
-                                          f"OpenMP); CPU: {cpu_name()}",
-                                "runs": cpu}
+                                          f"OpenMP over {threads} threads = the CPUs this process "
+                                          "may use); also one MoE decode step and one LM-head "
+                                          "step at 1 and that many threads",
+                                "host": cpus, "runs": cpu}
+        # GPU speed-up over the CPU baseline at `threads` threads, per case
+        sp = {}
+        for gk, ck in (("moe_decode_1tok", f"moe_decode_{threads}t"),
+                       ("lm_head_q6k_151936x2048_b1", f"lm_head_b1_{threads}t"),
+                       (HEADLINE, f"q4k_matvec_{threads}t")):
+            if gk in work and ck in cpu:
+                sp[gk] = round(cpu[ck]["s_per_step"] * 1e3 / work[gk]["ms_per_step"], 1)
+        line["cpu_baseline"]["gpu_speedup_at_cores"] = sp
     print(json.dumps(line))
     return 0
 
