@@ -290,7 +290,9 @@ kq_status kq_hip_moe_route_f32(kq_hip_context *context,
 /* Replaces kq_moe_execute_quantized (src/kq_moe_internal.h:56-64,
  * src/kq_moe_qwen38.c:882-901) / kq_moe_execute_f32 (include/kq_moe.h:154-166):
  * hidden [tokens][hidden] -> output [tokens][hidden]. Optional
- * device_selected_ids [tokens][top_k] receives the routing. */
+ * device_selected_ids [tokens][top_k] receives the routing; it must be
+ * 4-byte aligned and overlap neither the input, the output nor the scratch
+ * (ALIASING_VIOLATION). */
 kq_status kq_hip_moe_execute_quantized(kq_hip_context *context,
                                        const kq_hip_moe_config *config,
                                        const kq_hip_moe_weights *weights,
@@ -302,6 +304,108 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *context,
                                        void *device_scratch,
                                        uint64_t scratch_bytes,
                                        kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* MoE on F32 expert weights, with the reference's observers. */
+
+/* Mirrors kq_moe_weights_f32 (include/kq_moe.h:72-89): device pointers
+ * with element counts. Routed stacks gate/up [experts][routed_inter][hidden],
+ * down [experts][hidden][routed_inter]; shared gate/up [shared_inter][hidden],
+ * down [hidden][shared_inter]; router [experts][hidden]; shared gate
+ * weight [hidden]. */
+typedef struct kq_hip_moe_weights_f32 {
+    const float *router;
+    uint64_t router_count;
+    const float *routed_gate;
+    uint64_t routed_gate_count;
+    const float *routed_up;
+    uint64_t routed_up_count;
+    const float *routed_down;
+    uint64_t routed_down_count;
+    const float *shared_gate;
+    uint64_t shared_gate_count;
+    const float *shared_up;
+    uint64_t shared_up_count;
+    const float *shared_down;
+    uint64_t shared_down_count;
+    const float *shared_gate_weight;
+    uint64_t shared_gate_weight_count;
+} kq_hip_moe_weights_f32;
+
+/* The reference's checkpoint kinds, records and observers
+ * (include/kq_moe.h:13-70), same values and layouts; `values` point to
+ * host copies valid during the callback. */
+#define KQ_HIP_MOE_NO_EXPERT UINT32_MAX
+typedef enum kq_hip_moe_checkpoint_kind {
+    KQ_HIP_MOE_CHECKPOINT_ROUTER_LOGITS = 0,
+    KQ_HIP_MOE_CHECKPOINT_ROUTER_PROBABILITIES,
+    KQ_HIP_MOE_CHECKPOINT_SELECTED_WEIGHTS,
+    KQ_HIP_MOE_CHECKPOINT_ROUTED_GATE,
+    KQ_HIP_MOE_CHECKPOINT_ROUTED_UP,
+    KQ_HIP_MOE_CHECKPOINT_ROUTED_ACTIVATED,
+    KQ_HIP_MOE_CHECKPOINT_ROUTED_EXPERT_OUTPUT,
+    KQ_HIP_MOE_CHECKPOINT_ROUTED_WEIGHTED_OUTPUT,
+    KQ_HIP_MOE_CHECKPOINT_ROUTED_WEIGHTED_SUM,
+    KQ_HIP_MOE_CHECKPOINT_SHARED_GATE_PROJECTION,
+    KQ_HIP_MOE_CHECKPOINT_SHARED_UP_PROJECTION,
+    KQ_HIP_MOE_CHECKPOINT_SHARED_ACTIVATED,
+    KQ_HIP_MOE_CHECKPOINT_SHARED_OUTPUT,
+    KQ_HIP_MOE_CHECKPOINT_SHARED_SCALE_LOGIT,
+    KQ_HIP_MOE_CHECKPOINT_SHARED_SCALE,
+    KQ_HIP_MOE_CHECKPOINT_GATED_SHARED_OUTPUT,
+    KQ_HIP_MOE_CHECKPOINT_OPERATOR_OUTPUT
+} kq_hip_moe_checkpoint_kind;
+
+typedef struct kq_hip_moe_checkpoint {
+    kq_hip_moe_checkpoint_kind kind;
+    uint64_t token_index;
+    uint32_t expert_id;
+    uint32_t top_k_position;
+    uint32_t rank;
+    uint64_t dimensions[2];
+    const float *values;
+    uint64_t value_count;
+} kq_hip_moe_checkpoint;
+
+typedef void (*kq_hip_moe_checkpoint_observer)(const kq_hip_moe_checkpoint *checkpoint,
+                                               void *user_data);
+
+typedef struct kq_hip_moe_route {
+    uint64_t token_index;
+    const float *router_logits;
+    const float *router_probabilities;
+    uint64_t expert_count;
+    const uint32_t *selected_expert_ids;
+    const float *selected_weights;
+    uint32_t selected_count;
+} kq_hip_moe_route;
+
+typedef void (*kq_hip_moe_route_observer)(const kq_hip_moe_route *route, void *user_data);
+
+/* Device scratch of kq_hip_moe_execute_f32 for `token_count` tokens: every
+ * intermediate of every token (the checkpoints). */
+uint64_t kq_hip_moe_config_f32_scratch_bytes(const kq_hip_moe_config *config,
+                                             uint64_t token_count);
+
+/* Replaces kq_moe_execute_f32 (include/kq_moe.h:154-166,
+ * src/kq_moe_qwen38.c:604-880): every checkpoint bit-identical to the
+ * reference's (one device thread per output runs the reference's
+ * left-to-right binary32 sums). Any hidden size; at most 65,535 tokens and
+ * 960 experts. Weight counts must match the config (DIMENSION_MISMATCH);
+ * non-finite weights, inputs or results give NUMERIC_DOMAIN. The observers
+ * (optional) are called after the device work succeeds, synchronously, in
+ * the reference's order (per token: route, router logits, probabilities,
+ * selected weights, each selected expert in ascending id, routed sum, the
+ * shared expert's checkpoints, output); a failed call calls none. Always
+ * synchronous. */
+kq_status kq_hip_moe_execute_f32(kq_hip_context *context, const kq_hip_moe_config *config,
+                                 const kq_hip_moe_weights_f32 *weights,
+                                 const float *device_hidden, uint64_t token_count,
+                                 float *device_output, uint64_t output_capacity,
+                                 void *device_scratch, uint64_t scratch_bytes,
+                                 kq_hip_moe_route_observer route_observer,
+                                 kq_hip_moe_checkpoint_observer checkpoint_observer,
+                                 void *observer_user_data, kq_diagnostic *diagnostic);
 
 /* The token->expert permutation that the multi-token execution runs its
  * grouped expert GEMMs over: the (token, slot) pairs of selected_ids
@@ -382,7 +486,8 @@ uint64_t kq_hip_moe_block_scratch_bytes(const kq_hip_gr_dimensions *dimensions,
  * mixed, write_gate = gr_read(branches); moe = MoE(mixed);
  * output = gr_write(branches, moe, write_gate). branches and output are
  * [tokens][width] and must not overlap; optional device_selected_ids
- * [tokens][top_k] receives the routing. */
+ * [tokens][top_k] receives the routing (4-byte aligned, overlapping neither
+ * the branches, the output nor the scratch). */
 kq_status kq_hip_moe_block_f32(kq_hip_context *context, const kq_hip_gr_dimensions *dimensions,
                                const kq_hip_gr_weights *gr_weights,
                                const kq_hip_moe_config *config,

@@ -166,6 +166,39 @@ hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d, const kq_launch_mo
                                  const float *hidden, uint32_t tokens,
                                  const kq_launch_moe_ws *ws, float *out, uint32_t *status,
                                  hipStream_t stream);
+/* the exact softmax, partial-selection top-k, weights, ascending-id order
+ * and shared gate from logits [tokens][experts] and shared_logit [tokens]
+ * (experts <= 960) */
+hipError_t kq_launch_moe_route_finish(const float *logits, const float *shared_logit,
+                                      uint32_t experts, uint32_t top_k, uint32_t tokens,
+                                      float *probs, uint32_t *ids, float *weights,
+                                      uint32_t *order, float *shared_scale, uint32_t *status,
+                                      hipStream_t stream);
+
+/* MoE on F32 expert weights in the reference's order (kq_moe_f32.hip) */
+typedef struct kq_launch_moe_f32_weights {
+    const float *router;             /* [experts][hidden] */
+    const float *gate, *up, *down;   /* [E][I][H], [E][I][H], [E][H][I] */
+    const float *shared_gate, *shared_up, *shared_down; /* [S][H], [S][H], [H][S] */
+    const float *shared_gate_weight; /* [hidden] */
+} kq_launch_moe_f32_weights;
+
+/* every intermediate, per token (the checkpoint trace); Ip = max(I, S) */
+typedef struct kq_launch_moe_f32_ws {
+    float *logits, *probs;            /* [T][E] */
+    uint32_t *ids, *order;            /* [T][K] */
+    float *weights;                   /* [T][K] */
+    float *shared_logit, *shared_scale; /* [T] */
+    float *gate, *up, *act;           /* [T][K+1][Ip] (slot K: the shared expert) */
+    float *out, *weighted;            /* [T][K+1][H] */
+    float *routed_sum;                /* [T][H] */
+} kq_launch_moe_f32_ws;
+
+hipError_t kq_launch_f32_scan(const float *p, uint64_t n, uint32_t *status, hipStream_t s);
+hipError_t kq_launch_moe_f32(const kq_launch_moe_dims *d, const kq_launch_moe_f32_weights *w,
+                             const float *hidden, uint32_t tokens,
+                             const kq_launch_moe_f32_ws *ws, float *out, uint32_t *status,
+                             hipStream_t s);
 
 #ifdef __cplusplus
 }

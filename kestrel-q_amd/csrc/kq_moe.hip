@@ -1518,6 +1518,20 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
     return hipGetLastError();
 }
 
+extern "C" hipError_t kq_launch_moe_route_finish(const float *logits, const float *shared_logit,
+                                                 uint32_t experts, uint32_t top_k,
+                                                 uint32_t tokens, float *probs, uint32_t *ids,
+                                                 float *weights, uint32_t *order,
+                                                 float *shared_scale, uint32_t *status,
+                                                 hipStream_t s) {
+    const uint32_t fin = 64u * ((experts + 63u) / 64u + 1u);
+    if (fin > 1024u || top_k == 0u || top_k > experts || top_k > kMaxTopK)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, logits, shared_logit,
+                       experts, top_k, probs, ids, weights, order, shared_scale, status);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
                                             const kq_launch_moe_weights *w, const float *hidden,
                                             uint32_t tokens, const kq_launch_moe_ws *ws,

@@ -107,6 +107,8 @@ static int ranges_overlap(const void *a, uint64_t an, const void *b, uint64_t bn
 
 static int aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0u; }
 
+static uint64_t align256(uint64_t n) { return (n + 255u) & ~(uint64_t)255u; }
+
 static int u64_mul(uint64_t a, uint64_t b, uint64_t *out) {
     if (a != 0u && b > UINT64_MAX / a) return 0;
     *out = a * b;
@@ -670,9 +672,9 @@ kq_status kq_hip_moe_config_create(const kq_hip_moe_dimensions *dims, kq_hip_moe
     d.top_k = dims->top_k;
     d.inter = dims->routed_intermediate_size;
     d.shared_inter = dims->shared_intermediate_size;
-    if (!kq_launch_moe_supported(&d, NULL))
+    if (d.experts + 1u > 1024u || d.top_k > 64u)
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
-                       "device MoE needs hidden %% 4 == 0, experts <= 1023, top_k <= 64");
+                       "device MoE takes at most 1023 experts and top_k <= 64");
     cfg = (kq_hip_moe_config *)calloc(1, sizeof(*cfg));
     if (cfg == NULL) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "MoE config allocation failed");
     cfg->magic = KQ_MOE_CONFIG_MAGIC;
@@ -710,6 +712,10 @@ static kq_status moe_common(const kq_hip_context *c, const kq_hip_moe_config *cf
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "MoE token count is zero or above %u",
                        KQ_MOE_MAX_TOKENS);
     d = launch_dims(cfg);
+    if (!kq_launch_moe_supported(&d, NULL))
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
+                       "the packed-weight MoE and the route need hidden %% 4 == 0 "
+                       "(kq_hip_moe_execute_f32 takes any hidden size)");
     if (scratch_bytes < kq_launch_moe_ws_bytes(&d, (uint32_t)tokens))
         return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "MoE device scratch is too small");
     if (!aligned(router, 16u) || !aligned(sgw, 16u) || !aligned(hidden, 16u) ||
@@ -781,6 +787,16 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
         ranges_overlap(out, tokens * d.hidden * 4u, scratch, scratch_bytes))
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
                        "MoE input, output, and scratch must not overlap");
+    if (ids != NULL) {
+        const uint64_t ib = tokens * d.top_k * 4u;
+        if (!aligned(ids, 4u))
+            return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "selected ids need 4-byte alignment");
+        if (ranges_overlap(ids, ib, hidden, tokens * d.hidden * 4u) ||
+            ranges_overlap(ids, ib, out, tokens * d.hidden * 4u) ||
+            ranges_overlap(ids, ib, scratch, scratch_bytes))
+            return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                           "selected ids overlap the MoE input, output or scratch");
+    }
     lw.router = w->router;
     lw.gate_type = w->routed_gate_type;
     lw.gate = w->routed_gate;
@@ -823,6 +839,253 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     if (e == hipSuccess && ids != NULL)
         e = hipMemcpyAsync(ids, ws.ids, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice, c->stream);
     return finish(c, e, "MoE execute launch", diag);
+}
+
+/* ------------------------------------------------------------------ */
+/* MoE on F32 weights (kq_moe_f32.hip) */
+
+#define KQ_F32_MOE_MAX_TOKENS 65535u
+
+static void f32_ws_carve(const kq_launch_moe_dims *d, uint64_t t, void *base,
+                         kq_launch_moe_f32_ws *ws, uint64_t *bytes) {
+    const uint64_t ip = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+    const uint64_t slots = t * (d->top_k + 1u);
+    uint8_t *p = (uint8_t *)base;
+    uint64_t off = 0u;
+#define TAKE(field, type, n)                                  \
+    do {                                                      \
+        if (ws) ws->field = (type *)(void *)(p + off);        \
+        off += align256((uint64_t)(n) * 4u);                  \
+    } while (0)
+    TAKE(logits, float, t * d->experts);
+    TAKE(probs, float, t * d->experts);
+    TAKE(ids, uint32_t, t * d->top_k);
+    TAKE(order, uint32_t, t * d->top_k);
+    TAKE(weights, float, t * d->top_k);
+    TAKE(shared_logit, float, t);
+    TAKE(shared_scale, float, t);
+    TAKE(gate, float, slots * ip);
+    TAKE(up, float, slots * ip);
+    TAKE(act, float, slots * ip);
+    TAKE(out, float, slots * d->hidden);
+    TAKE(weighted, float, slots * d->hidden);
+    TAKE(routed_sum, float, t * d->hidden);
+#undef TAKE
+    if (bytes) *bytes = off;
+}
+
+uint64_t kq_hip_moe_config_f32_scratch_bytes(const kq_hip_moe_config *cfg, uint64_t tokens) {
+    kq_launch_moe_dims d;
+    uint64_t n = 0u;
+    if (!moe_ok(cfg) || tokens == 0u || tokens > KQ_F32_MOE_MAX_TOKENS) return 0u;
+    d = launch_dims(cfg);
+    f32_ws_carve(&d, tokens, NULL, NULL, &n);
+    return n;
+}
+
+/* the reference's count check per role (src/kq_moe_qwen38.c:82-126) */
+static kq_status f32_weight_counts(const kq_launch_moe_dims *d, const kq_hip_moe_weights_f32 *w,
+                                   kq_diagnostic *diag) {
+    const uint64_t routed = (uint64_t)d->inter * d->hidden * d->experts;
+    const uint64_t shared = (uint64_t)d->shared_inter * d->hidden;
+    const struct {
+        const float *p;
+        uint64_t have, want;
+        const char *what;
+    } roles[8] = {
+        {w->router, w->router_count, (uint64_t)d->experts * d->hidden, "MoE router shape/data mismatch"},
+        {w->routed_gate, w->routed_gate_count, routed, "MoE routed gate shape/data mismatch"},
+        {w->routed_up, w->routed_up_count, routed, "MoE routed up shape/data mismatch"},
+        {w->routed_down, w->routed_down_count, routed, "MoE routed down shape/data mismatch"},
+        {w->shared_gate, w->shared_gate_count, shared, "MoE shared gate shape/data mismatch"},
+        {w->shared_up, w->shared_up_count, shared, "MoE shared up shape/data mismatch"},
+        {w->shared_down, w->shared_down_count, shared, "MoE shared down shape/data mismatch"},
+        {w->shared_gate_weight, w->shared_gate_weight_count, d->hidden,
+         "MoE shared scale gate shape/data mismatch"}};
+    for (int i = 0; i < 8; ++i) {
+        if (roles[i].p == NULL) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "%s", roles[i].what);
+        if (roles[i].have != roles[i].want)
+            return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH, "%s", roles[i].what);
+    }
+    return KQ_STATUS_OK;
+}
+
+static void emit(kq_hip_moe_checkpoint_observer obs, void *user, kq_hip_moe_checkpoint_kind kind,
+                 uint64_t token, uint32_t expert, uint32_t pos, const float *v, uint64_t n) {
+    kq_hip_moe_checkpoint c;
+    memset(&c, 0, sizeof(c));
+    c.kind = kind;
+    c.token_index = token;
+    c.expert_id = expert;
+    c.top_k_position = pos;
+    c.rank = 1u;
+    c.dimensions[0] = n;
+    c.values = v;
+    c.value_count = n;
+    obs(&c, user);
+}
+
+/* The observers, in the reference's order (src/kq_moe_qwen38.c:697-863),
+ * over host copies of the device trace. */
+static kq_status f32_observe(kq_hip_context *c, const kq_launch_moe_dims *d, uint64_t T,
+                             const kq_launch_moe_f32_ws *ws, const float *y,
+                             kq_hip_moe_route_observer ro, kq_hip_moe_checkpoint_observer co,
+                             void *user, kq_diagnostic *diag) {
+    const uint64_t E = d->experts, K = d->top_k, H = d->hidden, ip =
+        d->inter > d->shared_inter ? d->inter : d->shared_inter;
+    const uint64_t slots = T * (K + 1u);
+    /* logits, probs [T][E]; weights, ids, order [T][K]; shared logit and
+     * scale [T]; routed sum and output [T][H]; gate, up, act [slots][ip];
+     * out, weighted [slots][H] */
+    const uint64_t n = T * (2u * E + 3u * K + 2u + 2u * H) + slots * (3u * ip + 2u * H);
+    float *h = (float *)malloc(n * 4u);
+    kq_status st = KQ_STATUS_OK;
+    if (h == NULL) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "observer copies: out of memory");
+    float *logits = h, *probs = logits + T * E, *wts = probs + T * E;
+    uint32_t *ids = (uint32_t *)(wts + T * K), *order = ids + T * K;
+    float *sl = (float *)(order + T * K), *ss = sl + T, *gate = ss + T, *up = gate + slots * ip;
+    float *act = up + slots * ip, *out = act + slots * ip, *wo = out + slots * H;
+    float *rsum = wo + slots * H, *yh = rsum + T * H;
+    const struct {
+        void *dst;
+        const void *src;
+        uint64_t n;
+    } cp[] = {{logits, ws->logits, T * E}, {probs, ws->probs, T * E}, {wts, ws->weights, T * K},
+              {ids, ws->ids, T * K},       {order, ws->order, T * K}, {sl, ws->shared_logit, T},
+              {ss, ws->shared_scale, T},   {gate, ws->gate, slots * ip}, {up, ws->up, slots * ip},
+              {act, ws->act, slots * ip},  {out, ws->out, slots * H}, {wo, ws->weighted, slots * H},
+              {rsum, ws->routed_sum, T * H}, {yh, y, T * H}};
+    for (size_t i = 0; i < sizeof(cp) / sizeof(cp[0]) && st == KQ_STATUS_OK; ++i)
+        st = kq_hip_download(c, cp[i].dst, cp[i].src, cp[i].n * 4u, diag);
+    for (uint64_t t = 0; t < T && st == KQ_STATUS_OK; ++t) {
+        const float *lt = logits + t * E, *pt = probs + t * E, *wt = wts + t * K;
+        const uint32_t *it = ids + t * K;
+        if (ro != NULL) {
+            kq_hip_moe_route r;
+            r.token_index = t;
+            r.router_logits = lt;
+            r.router_probabilities = pt;
+            r.expert_count = E;
+            r.selected_expert_ids = it;
+            r.selected_weights = wt;
+            r.selected_count = (uint32_t)K;
+            ro(&r, user);
+        }
+        if (co == NULL) continue;
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTER_LOGITS, t, KQ_HIP_MOE_NO_EXPERT, UINT32_MAX, lt, E);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTER_PROBABILITIES, t, KQ_HIP_MOE_NO_EXPERT,
+             UINT32_MAX, pt, E);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SELECTED_WEIGHTS, t, KQ_HIP_MOE_NO_EXPERT, UINT32_MAX,
+             wt, K);
+        /* experts in ascending id: order[j] is the top-k position of the
+         * j-th smallest selected id */
+        for (uint64_t j = 0; j < K; ++j) {
+            const uint32_t k = order[t * K + j];
+            const uint64_t sl_i = t * (K + 1u) + k;
+            const uint32_t e = it[k];
+            emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTED_GATE, t, e, k, gate + sl_i * ip, d->inter);
+            emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTED_UP, t, e, k, up + sl_i * ip, d->inter);
+            emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTED_ACTIVATED, t, e, k, act + sl_i * ip,
+                 d->inter);
+            emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTED_EXPERT_OUTPUT, t, e, k, out + sl_i * H, H);
+            emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTED_WEIGHTED_OUTPUT, t, e, k, wo + sl_i * H, H);
+        }
+        const uint64_t sh = t * (K + 1u) + K;
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_ROUTED_WEIGHTED_SUM, t, KQ_HIP_MOE_NO_EXPERT,
+             UINT32_MAX, rsum + t * H, H);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SHARED_GATE_PROJECTION, t, KQ_HIP_MOE_NO_EXPERT,
+             UINT32_MAX, gate + sh * ip, d->shared_inter);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SHARED_UP_PROJECTION, t, KQ_HIP_MOE_NO_EXPERT,
+             UINT32_MAX, up + sh * ip, d->shared_inter);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SHARED_ACTIVATED, t, KQ_HIP_MOE_NO_EXPERT, UINT32_MAX,
+             act + sh * ip, d->shared_inter);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SHARED_OUTPUT, t, KQ_HIP_MOE_NO_EXPERT, UINT32_MAX,
+             out + sh * H, H);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SHARED_SCALE_LOGIT, t, KQ_HIP_MOE_NO_EXPERT,
+             UINT32_MAX, sl + t, 1u);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_SHARED_SCALE, t, KQ_HIP_MOE_NO_EXPERT, UINT32_MAX,
+             ss + t, 1u);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_GATED_SHARED_OUTPUT, t, KQ_HIP_MOE_NO_EXPERT,
+             UINT32_MAX, wo + sh * H, H);
+        emit(co, user, KQ_HIP_MOE_CHECKPOINT_OPERATOR_OUTPUT, t, KQ_HIP_MOE_NO_EXPERT, UINT32_MAX,
+             yh + t * H, H);
+    }
+    free(h);
+    return st;
+}
+
+kq_status kq_hip_moe_execute_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
+                                 const kq_hip_moe_weights_f32 *w, const float *hidden,
+                                 uint64_t tokens, float *out, uint64_t capacity, void *scratch,
+                                 uint64_t scratch_bytes, kq_hip_moe_route_observer ro,
+                                 kq_hip_moe_checkpoint_observer co, void *user,
+                                 kq_diagnostic *diag) {
+    kq_launch_moe_dims d;
+    kq_launch_moe_f32_ws ws;
+    kq_launch_moe_f32_weights lw;
+    uint64_t need = 0u, vals, vbytes;
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || !moe_ok(cfg) || w == NULL || hidden == NULL || out == NULL ||
+        scratch == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE execution arguments are required");
+    d = launch_dims(cfg);
+    if (tokens == 0u || tokens > KQ_F32_MOE_MAX_TOKENS || !u64_mul(tokens, d.hidden, &vals) ||
+        !u64_mul(vals, 4u, &vbytes))
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
+                       "MoE token count is zero, above 65,535 or overflows");
+    if (d.experts > 960u)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "F32 MoE execution takes at most 960 experts");
+    f32_ws_carve(&d, tokens, NULL, NULL, &need);
+    if (capacity < vals || scratch_bytes < need || !aligned(scratch, 256u))
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "MoE output or aligned scratch is too small");
+    st = f32_weight_counts(&d, w, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (!aligned(hidden, 4u) || !aligned(out, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "MoE input and output need 4-byte alignment");
+    if (ranges_overlap(hidden, vbytes, out, vbytes) ||
+        ranges_overlap(hidden, vbytes, scratch, scratch_bytes) ||
+        ranges_overlap(out, vbytes, scratch, scratch_bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                       "MoE input, output, and scratch must not overlap");
+    {
+        const float *wp[8] = {w->router, w->routed_gate, w->routed_up, w->routed_down,
+                              w->shared_gate, w->shared_up, w->shared_down, w->shared_gate_weight};
+        const uint64_t wn[8] = {w->router_count, w->routed_gate_count, w->routed_up_count,
+                                w->routed_down_count, w->shared_gate_count, w->shared_up_count,
+                                w->shared_down_count, w->shared_gate_weight_count};
+        for (int i = 0; i < 8; ++i) {
+            if (!aligned(wp[i], 4u))
+                return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "MoE weights need 4-byte alignment");
+            if (ranges_overlap(wp[i], wn[i] * 4u, out, vbytes) ||
+                ranges_overlap(wp[i], wn[i] * 4u, scratch, scratch_bytes))
+                return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                               "MoE weights must not overlap writable execution buffers");
+        }
+        st = set_device(c, diag);
+        if (st != KQ_STATUS_OK) return st;
+        /* the reference validates the input, then every weight, for finiteness */
+        e = kq_launch_f32_scan(hidden, vals, c->d_status, c->stream);
+        for (int i = 0; i < 8 && e == hipSuccess; ++i)
+            e = kq_launch_f32_scan(wp[i], wn[i], c->d_status, c->stream);
+    }
+    f32_ws_carve(&d, tokens, scratch, &ws, NULL);
+    lw.router = w->router;
+    lw.gate = w->routed_gate;
+    lw.up = w->routed_up;
+    lw.down = w->routed_down;
+    lw.shared_gate = w->shared_gate;
+    lw.shared_up = w->shared_up;
+    lw.shared_down = w->shared_down;
+    lw.shared_gate_weight = w->shared_gate_weight;
+    if (e == hipSuccess)
+        e = kq_launch_moe_f32(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status, c->stream);
+    if (e != hipSuccess) return hip_fail(diag, e, "F32 MoE launch");
+    st = drain(c, diag); /* always synchronous: the observers read the results */
+    if (st != KQ_STATUS_OK) return st;
+    if (ro == NULL && co == NULL) return KQ_STATUS_OK;
+    return f32_observe(c, &d, tokens, &ws, out, ro, co, user, diag);
 }
 
 kq_status kq_hip_moe_token_permutation(kq_hip_context *c, const kq_hip_moe_config *cfg,
@@ -869,8 +1132,6 @@ kq_status kq_hip_moe_token_permutation(kq_hip_context *c, const kq_hip_moe_confi
 /* ------------------------------------------------------------------ */
 /* gated residual around a layer block */
 
-static uint64_t align256(uint64_t n) { return (n + 255u) & ~(uint64_t)255u; }
-
 /* scratch of a gr read: normalized [T][W], rank [T][r], read gates [T][W] */
 uint64_t kq_hip_gr_scratch_bytes(const kq_hip_gr_dimensions *d, uint64_t tokens) {
     uint64_t w;
@@ -887,9 +1148,11 @@ static kq_status gr_dims_ok(const kq_hip_gr_dimensions *d, uint64_t tokens,
                        "gated residual needs branches, hidden, rank and a positive epsilon");
     if (d->branch_count > 64u || tokens == 0u || tokens > 65535u ||
         tokens * d->branch_count * (uint64_t)d->hidden_size > (UINT64_C(1) << 30) ||
-        (uint64_t)d->rank * d->branch_count * d->hidden_size > (UINT64_C(1) << 31))
+        (uint64_t)d->rank * d->branch_count * d->hidden_size > (UINT64_C(1) << 31) ||
+        tokens * (uint64_t)d->rank > (UINT64_C(1) << 30))
         return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
-                       "gated residual: at most 64 branches, 65,535 tokens and 2^30 state values");
+                       "gated residual: at most 64 branches, 65,535 tokens, 2^30 state values "
+                       "and 2^30 rank values");
     return KQ_STATUS_OK;
 }
 
@@ -1045,6 +1308,16 @@ kq_status kq_hip_moe_block_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
         ranges_overlap(out, tokens * W * 4u, scratch, scratch_bytes))
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
                        "MoE block input, output and scratch must not overlap");
+    if (ids != NULL) {
+        const uint64_t ib = tokens * cfg->dims.top_k * 4u;
+        if (!aligned(ids, 4u))
+            return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "selected ids need 4-byte alignment");
+        if (ranges_overlap(ids, ib, x, tokens * W * 4u) ||
+            ranges_overlap(ids, ib, out, tokens * W * 4u) ||
+            ranges_overlap(ids, ib, scratch, scratch_bytes))
+            return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                           "selected ids overlap the MoE block input, output or scratch");
+    }
     hb = align256(tokens * d->hidden_size * 4u);
     gb = kq_hip_gr_scratch_bytes(d, tokens);
     p = (char *)scratch;

@@ -77,6 +77,38 @@ class MoeWeights(C.Structure):
                 ("shared_gate_weight", C.c_void_p)]
 
 
+class MoeWeightsF32(C.Structure):
+    _fields_ = [(n, t) for role in ("router", "routed_gate", "routed_up", "routed_down",
+                                    "shared_gate", "shared_up", "shared_down",
+                                    "shared_gate_weight")
+                for n, t in ((role, C.c_void_p), (role + "_count", C.c_uint64))]
+
+
+class MoeCheckpoint(C.Structure):
+    _fields_ = [("kind", C.c_int), ("token_index", C.c_uint64), ("expert_id", C.c_uint32),
+                ("top_k_position", C.c_uint32), ("rank", C.c_uint32),
+                ("dimensions", C.c_uint64 * 2), ("values", C.POINTER(C.c_float)),
+                ("value_count", C.c_uint64)]
+
+
+class MoeRoute(C.Structure):
+    _fields_ = [("token_index", C.c_uint64), ("router_logits", C.POINTER(C.c_float)),
+                ("router_probabilities", C.POINTER(C.c_float)), ("expert_count", C.c_uint64),
+                ("selected_expert_ids", C.POINTER(C.c_uint32)),
+                ("selected_weights", C.POINTER(C.c_float)), ("selected_count", C.c_uint32)]
+
+
+CHECKPOINT_OBSERVER = C.CFUNCTYPE(None, C.POINTER(MoeCheckpoint), C.c_void_p)
+ROUTE_OBSERVER = C.CFUNCTYPE(None, C.POINTER(MoeRoute), C.c_void_p)
+# kq_hip_moe_checkpoint_kind, in enum order
+CHECKPOINT_KINDS = ("router_logits", "router_probabilities", "selected_weights", "routed_gate",
+                    "routed_up", "routed_activated", "routed_expert_output",
+                    "routed_weighted_output", "routed_weighted_sum", "shared_gate_projection",
+                    "shared_up_projection", "shared_activated", "shared_output",
+                    "shared_scale_logit", "shared_scale", "gated_shared_output",
+                    "operator_output")
+
+
 class StringView(C.Structure):
     _fields_ = [("data", C.c_void_p), ("length", C.c_uint64)]
 
@@ -198,6 +230,11 @@ SIGNATURES = {
     "kq_hip_moe_execute_quantized": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p,
                                                C.c_void_p, C.c_uint64, C.c_void_p]),
+    "kq_hip_moe_config_f32_scratch_bytes": (C.c_uint64, [C.c_void_p, C.c_uint64]),
+    "kq_hip_moe_execute_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                         C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p,
+                                         C.c_uint64, ROUTE_OBSERVER, CHECKPOINT_OBSERVER,
+                                         C.c_void_p, C.c_void_p]),
     "kq_hip_moe_token_permutation": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
                                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_uint64, C.c_void_p]),
@@ -288,6 +325,9 @@ class MoeConfig:
 
     def scratch_bytes(self, tokens: int) -> int:
         return lib().kq_hip_moe_config_scratch_bytes(C.c_void_p(self.handle), tokens)
+
+    def f32_scratch_bytes(self, tokens: int) -> int:
+        return lib().kq_hip_moe_config_f32_scratch_bytes(C.c_void_p(self.handle), tokens)
 
     def close(self) -> None:
         if self.handle:
@@ -423,6 +463,41 @@ class Context:
                                                  self._p(ids) if ids is not None else None,
                                                  self._p(scratch), scratch_bytes, C.byref(d)), d)
 
+    def moe_execute_f32(self, cfg: MoeConfig, weights: MoeWeightsF32, hidden, tokens: int, out,
+                        scratch, scratch_bytes: int, capacity: int | None = None,
+                        observe: bool = False):
+        """F32 weights in the reference's order. observe: collect the route
+        observer's and checkpoint observer's calls, in call order, as
+        ("route", dict) / ("checkpoint", dict) with copied values."""
+        d = Diagnostic()
+        cap = tokens * cfg.hidden if capacity is None else capacity
+        seen = []
+
+        def on_route(r, _u):
+            r = r.contents
+            n, k = r.expert_count, r.selected_count
+            seen.append(("route", {
+                "token": r.token_index,
+                "logits": np.ctypeslib.as_array(r.router_logits, (n,)).copy(),
+                "probs": np.ctypeslib.as_array(r.router_probabilities, (n,)).copy(),
+                "ids": np.ctypeslib.as_array(r.selected_expert_ids, (k,)).copy(),
+                "weights": np.ctypeslib.as_array(r.selected_weights, (k,)).copy()}))
+
+        def on_ckpt(c, _u):
+            c = c.contents
+            seen.append(("checkpoint", {
+                "kind": CHECKPOINT_KINDS[c.kind], "token": c.token_index,
+                "expert": c.expert_id, "position": c.top_k_position, "rank": c.rank,
+                "dims": (c.dimensions[0], c.dimensions[1]),
+                "values": np.ctypeslib.as_array(c.values, (c.value_count,)).copy()}))
+        ro = ROUTE_OBSERVER(on_route) if observe else ROUTE_OBSERVER()
+        co = CHECKPOINT_OBSERVER(on_ckpt) if observe else CHECKPOINT_OBSERVER()
+        check(lib().kq_hip_moe_execute_f32(self._h, C.c_void_p(cfg.handle), C.byref(weights),
+                                           self._p(hidden), tokens, self._p(out), cap,
+                                           self._p(scratch), scratch_bytes, ro, co, None,
+                                           C.byref(d)), d)
+        return seen
+
     def gr_read(self, dims: GrDims, weights: GrWeights, x, tokens: int, mixed, write_gate,
                 scratch, scratch_bytes: int) -> None:
         d = Diagnostic()
@@ -465,6 +540,18 @@ def moe_weights(bufs: dict, gate_type=TYPE_Q4_K, down_type=TYPE_Q6_K,
     return MoeWeights(P("router"), gate_type, P("gate"), gate_type, P("up"), down_type,
                       P("down"), sg, P("shared_gate"), sg, P("shared_up"),
                       sd, P("shared_down"), P("shared_gate_weight"))
+
+
+def moe_weights_f32(bufs: dict, counts: dict) -> MoeWeightsF32:
+    """bufs: role -> DeviceBuffer, counts: role -> element count, roles as
+    kq_hip_moe_weights_f32 (router, routed_gate, routed_up, routed_down,
+    shared_gate, shared_up, shared_down, shared_gate_weight)."""
+    w = MoeWeightsF32()
+    for role in ("router", "routed_gate", "routed_up", "routed_down", "shared_gate",
+                 "shared_up", "shared_down", "shared_gate_weight"):
+        setattr(w, role, bufs[role].ptr if bufs.get(role) is not None else None)
+        setattr(w, role + "_count", counts[role])
+    return w
 
 
 # ---------------------------------------------------------------- GGUF files

@@ -258,6 +258,12 @@ def test_gated_residual_fails_closed(ctx, gr_model):
     with pytest.raises(kq_hip.KqError) as e:  # the grid's token axis; rejected before launch
         ctx.gr_read(g.dims, g.w, dx, 65536, dm, dg, ds, n)
     assert e.value.name == "LIMIT_EXCEEDED"
+    # tokens x rank above 2^30 (the rank step's element count) is refused
+    # before any launch
+    big = kq_hip.gr_dims(1, 4, 65536, EPS)
+    with pytest.raises(kq_hip.KqError) as e:
+        ctx.gr_read(big, g.w, dx, 16385, dm, dg, ds, n)
+    assert e.value.name == "LIMIT_EXCEEDED"
     bad = kq_hip.gr_dims(0, g.H, g.R, EPS)
     with pytest.raises(kq_hip.KqError) as e:
         ctx.gr_read(bad, g.w, dx, T, dm, dg, ds, n)

@@ -225,6 +225,14 @@ def test_moe_fails_closed(ctx, layer):
     with pytest.raises(kq_hip.KqError) as e:
         ctx.moe_execute(layer.cfg, kq_hip.moe_weights(layer.bufs), dx, 1, dx, None, scratch, n)
     assert e.value.name == "ALIASING_VIOLATION"
+    with pytest.raises(kq_hip.KqError) as e:  # ids written into the scratch
+        ctx.moe_execute(layer.cfg, kq_hip.moe_weights(layer.bufs), dx, 1, dout, scratch.ptr + 512,
+                        scratch, n)
+    assert e.value.name == "ALIASING_VIOLATION"
+    with pytest.raises(kq_hip.KqError) as e:  # ids over the output
+        ctx.moe_execute(layer.cfg, kq_hip.moe_weights(layer.bufs), dx, 1, dout, dout.ptr + 64,
+                        scratch, n)
+    assert e.value.name == "ALIASING_VIOLATION"
     # and the layer still runs correctly afterwards
     test_moe_decode_one_token(ctx, layer)
 
