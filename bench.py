@@ -527,6 +527,11 @@ def main() -> int:
             lambda: wl_floor_read(ctx, 150994944, (2, 4, 8), 10, max(10, K // 2), graph))
         run("floor_read_255252480b",
             lambda: wl_floor_read(ctx, 255252480, (2, 4, 8), 10, max(10, K // 2), graph))
+        # the reference model's GDN projections (Q8_0), on their canonical
+        # copies (kq_hip_gdn_canonicalize): attn_qkv, attn_gate, ssm_out
+        for nm, r, c in (("qkv", 10240, 2560), ("gate", 6144, 2560), ("out", 2560, 6144)):
+            run(f"gdn_{nm}_q8_0_{r}x{c}_b1",
+                lambda r=r, c=c: wl_matvec(ctx, "Q8_0", r, c, 1, W, K, graph))
         for f in ("Q4_K", "Q8_0", "Q6_K", "Q5_K", "Q5_1", "IQ4_NL"):
             run(f"dequant_64m_{f.lower()}",
                 lambda f=f: wl_dequant(ctx, f, 5, max(10, K // 4), graph))

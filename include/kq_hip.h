@@ -142,6 +142,121 @@ kq_status kq_hip_gguf_upload_expert_member(kq_hip_context *context,
                                            uint64_t device_capacity,
                                            kq_diagnostic *diagnostic);
 
+/* Logical element ranges to whole blocks (host only). Replaces
+ * kq_quant_element_to_block / kq_quant_range_to_blocks
+ * (include/kq_tensor_view.h:93-104, src/kq_tensor_view.c:110-215), same
+ * checks and statuses. */
+typedef struct kq_hip_quant_block_span {
+    uint64_t requested_element_offset;
+    uint64_t requested_element_count;
+    uint64_t first_block;
+    uint64_t block_count;
+    uint64_t physical_byte_offset;
+    uint64_t physical_byte_length;
+    uint64_t leading_elements;
+    uint64_t trailing_elements;
+} kq_hip_quant_block_span;
+
+kq_status kq_hip_quant_element_to_block(uint32_t type_id, uint64_t total_elements,
+                                        uint64_t element_index, uint64_t *out_block_index,
+                                        uint64_t *out_element_in_block,
+                                        kq_diagnostic *diagnostic);
+kq_status kq_hip_quant_range_to_blocks(uint32_t type_id, uint64_t total_elements,
+                                       uint64_t element_offset, uint64_t element_count,
+                                       kq_hip_quant_block_span *out_span,
+                                       kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* Device tensor views: the packed blocks of one tensor (or expert member,
+ * or span) in device memory, with the layout facts the reference's
+ * kq_tensor_view_info carries for the numeric path (include/kq_tensor_view.h:
+ * 26-31, 52-80). */
+typedef enum kq_hip_tensor_layout {
+    KQ_HIP_LAYOUT_CANONICAL_CONTIGUOUS = 0,
+    KQ_HIP_LAYOUT_TRANSFORMED_PHYSICAL,
+    KQ_HIP_LAYOUT_SPLIT_SEGMENT,
+    KQ_HIP_LAYOUT_FUSED_MEMBER
+} kq_hip_tensor_layout;
+
+/* kq_numeric_view_order (include/kq_numeric.h:15-18) */
+typedef enum kq_hip_view_order {
+    KQ_HIP_PHYSICAL_ORDER = 0,
+    KQ_HIP_REQUIRE_CANONICAL_ORDER
+} kq_hip_view_order;
+
+typedef struct kq_hip_tensor_view {
+    uint32_t type_id;
+    uint32_t layout;               /* kq_hip_tensor_layout */
+    uint64_t block_elements;
+    uint64_t bytes_per_block;
+    uint64_t block_count;
+    uint32_t canonical_contiguous; /* 1: blocks in canonical element order */
+    uint32_t reserved;
+    const void *device_data;       /* the view's first block */
+    uint64_t mapped_bytes;         /* bytes of device_data the view covers */
+} kq_hip_tensor_view;
+
+/* A view of `bytes` packed bytes at device_data (whole blocks, else
+ * MALFORMED_QUANTIZED_DATA). A canonical-contiguous layout sets
+ * canonical_contiguous; TRANSFORMED_PHYSICAL (the GDN tensors as stored)
+ * and SPLIT_SEGMENT do not. */
+kq_status kq_hip_tensor_view_init(uint32_t type_id, const void *device_data, uint64_t bytes,
+                                  uint32_t layout, kq_hip_tensor_view *out_view,
+                                  kq_diagnostic *diagnostic);
+
+/* Replaces kq_dequantize_view_blocks_f32 (include/kq_numeric.h:28-36,
+ * src/kq_numeric.c:361-418): blocks [relative_first_block, + block_count)
+ * of the view, bit-identical decode. KQ_HIP_REQUIRE_CANONICAL_ORDER on a
+ * view that is not canonical-contiguous (or is transformed or a split
+ * segment) fails with TENSOR_LAYOUT_MISMATCH; a range past the view with
+ * SPAN_OUT_OF_RANGE; a view without data or geometry with
+ * TENSOR_OWNERSHIP_MISMATCH. */
+kq_status kq_hip_dequantize_view_blocks_f32(kq_hip_context *context,
+                                            const kq_hip_tensor_view *view,
+                                            uint64_t relative_first_block,
+                                            uint64_t block_count, uint32_t order,
+                                            float *device_output, uint64_t output_capacity,
+                                            uint64_t *output_count,
+                                            kq_diagnostic *diagnostic);
+
+/* ------------------------------------------------------------------ */
+/* GDN row and column layouts. The model stores the value-head rows of
+ * attn_qkv, attn_gate, ssm_alpha, ssm_beta and ssm_conv1d, and the columns
+ * of ssm_out, tiled by repeat; the reference reorders them at every linear
+ * (physical_row_for, grouped_to_tiled, the GDN_OUT activation permutation:
+ * src/kq_weight_provider.c:205-248, :438-451). */
+typedef enum kq_hip_gdn_layout {
+    KQ_HIP_GDN_NONE = 0,
+    KQ_HIP_GDN_QKV,   /* rows: 4096 q/k rows, then 6144 value rows (width 128) */
+    KQ_HIP_GDN_GATE,  /* rows: 6144 (width 128) */
+    KQ_HIP_GDN_ALPHA, /* rows: 48 (width 1) */
+    KQ_HIP_GDN_BETA,  /* rows: 48 (width 1) */
+    KQ_HIP_GDN_CONV,  /* rows: as QKV */
+    KQ_HIP_GDN_OUT    /* columns: 6144 (width 128) */
+} kq_hip_gdn_layout;
+
+/* The physical row (column) holding canonical row (column) `index` of a
+ * matrix of `rows` x `columns` in a GDN layout (host only): the reference's
+ * physical_row_for / grouped_to_tiled. A geometry the layout does not map
+ * onto itself fails with TENSOR_LAYOUT_MISMATCH. */
+kq_status kq_hip_gdn_physical_row(uint32_t gdn_layout, uint64_t rows, uint64_t canonical_row,
+                                  uint64_t *out_physical_row, kq_diagnostic *diagnostic);
+kq_status kq_hip_gdn_physical_column(uint32_t gdn_layout, uint64_t columns,
+                                     uint64_t canonical_column, uint64_t *out_physical_column,
+                                     kq_diagnostic *diagnostic);
+
+/* Writes the canonical-order copy of a packed matrix stored in a GDN
+ * layout: row r of the copy is physical row physical_row(r); for GDN_OUT
+ * each row's 128-column units move whole (32-element block formats and
+ * F32 / BF16; K-quants give UNSUPPORTED_TENSOR_TYPE). The ordinary matvec on
+ * the copy then equals the reference's provider linear on the stored
+ * tensor (src/kq_weight_provider.c:438-475). Synchronous unless the
+ * context is asynchronous. */
+kq_status kq_hip_gdn_canonicalize(kq_hip_context *context, uint32_t gdn_layout,
+                                  uint32_t type_id, const void *device_physical, uint64_t rows,
+                                  uint64_t columns, void *device_canonical,
+                                  uint64_t canonical_capacity, kq_diagnostic *diagnostic);
+
 /* ------------------------------------------------------------------ */
 /* Numeric core. */
 

@@ -44,13 +44,17 @@ typedef enum kq_status {
     KQ_STATUS_INCONSISTENT_DATA_SECTION = 19,
     KQ_STATUS_INVALID_QUANTIZED_GEOMETRY = 25,
     KQ_STATUS_NONCONTIGUOUS_TENSOR_VIEW = 26,
+    KQ_STATUS_TENSOR_LAYOUT_MISMATCH = 27,
     KQ_STATUS_TENSOR_OWNERSHIP_MISMATCH = 28,
+    KQ_STATUS_INVALID_TOKEN_ID = 31,
     KQ_STATUS_BUFFER_TOO_SMALL = 32,
     KQ_STATUS_MALFORMED_QUANTIZED_DATA = 38,
     KQ_STATUS_NUMERIC_DOMAIN = 39,
     KQ_STATUS_DIMENSION_MISMATCH = 40,
     KQ_STATUS_ALIASING_VIOLATION = 41,
     KQ_STATUS_INCOMPATIBLE_MOE = 46,
+    KQ_STATUS_INCOMPATIBLE_SAMPLING = 54,
+    KQ_STATUS_INVALID_RNG_STATE = 55,
     /* Extension: a HIP runtime call failed (launch, copy, sync, graph). */
     KQ_STATUS_DEVICE_FAILURE = 1000
 } kq_status;

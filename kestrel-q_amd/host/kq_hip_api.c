@@ -40,6 +40,9 @@ struct kq_hip_context {
     void *stage[2];     /* pinned staging for file-backed uploads */
     hipEvent_t stage_done[2];
     void *noalloc;      /* this device's allocation-free LM-head partials */
+    void *stage_dev;    /* aligned device copy of a view span that starts off
+                           the decoder's alignment, grown on demand */
+    uint64_t stage_dev_cap;
 };
 
 struct kq_hip_moe_config {
@@ -165,6 +168,7 @@ void kq_hip_context_destroy(kq_hip_context *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->part_v) (void)hipFree(c->part_v);
     if (c->part_i) (void)hipFree(c->part_i);
+    if (c->stage_dev) (void)hipFree(c->stage_dev);
     if (c->d_status) (void)hipFree(c->d_status);
     if (c->h_status) (void)hipHostFree(c->h_status);
     for (int k = 0; k < 2; ++k) {
@@ -425,6 +429,254 @@ kq_status kq_hip_dequantize_blocks_f32(kq_hip_context *c, uint32_t type_id, cons
     if (st != KQ_STATUS_OK) return st;
     return finish(c, kq_launch_dequant(type_id, packed, blocks, output, c->d_status, c->stream),
                   "dequant launch", diag);
+}
+
+/* ------------------------------------------------------------------ */
+/* element ranges, tensor views */
+
+kq_status kq_hip_quant_element_to_block(uint32_t type_id, uint64_t total, uint64_t index,
+                                        uint64_t *block, uint64_t *within, kq_diagnostic *diag) {
+    kq_hip_quant_geometry g;
+    uint64_t ignored;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (block == NULL || within == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "block index and intra-block outputs are required");
+    *block = 0u;
+    *within = 0u;
+    st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
+    if (st == KQ_STATUS_OK) st = kq_hip_quant_packed_size(type_id, total, &ignored, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (index >= total)
+        return kq_fail(diag, KQ_STATUS_SPAN_OUT_OF_RANGE, "logical element index is outside the tensor");
+    *block = index / g.block_elements;
+    *within = index % g.block_elements;
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_quant_range_to_blocks(uint32_t type_id, uint64_t total, uint64_t offset,
+                                       uint64_t count, kq_hip_quant_block_span *span,
+                                       kq_diagnostic *diag) {
+    kq_hip_quant_geometry g;
+    uint64_t ignored, end, last, first_el, end_el;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (span == NULL || count == 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "non-zero logical range and output span are required");
+    memset(span, 0, sizeof(*span));
+    st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
+    if (st == KQ_STATUS_OK) st = kq_hip_quant_packed_size(type_id, total, &ignored, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (offset > UINT64_MAX - count)
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "logical element range overflows uint64");
+    end = offset + count;
+    if (offset >= total || end > total)
+        return kq_fail(diag, KQ_STATUS_SPAN_OUT_OF_RANGE, "logical element range is outside the tensor");
+    span->requested_element_offset = offset;
+    span->requested_element_count = count;
+    span->first_block = offset / g.block_elements;
+    last = (end - 1u) / g.block_elements + 1u;
+    span->block_count = last - span->first_block;
+    if (!u64_mul(span->first_block, g.bytes_per_block, &span->physical_byte_offset) ||
+        !u64_mul(span->block_count, g.bytes_per_block, &span->physical_byte_length) ||
+        !u64_mul(span->first_block, g.block_elements, &first_el) ||
+        !u64_mul(last, g.block_elements, &end_el))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW,
+                       "quantized block span arithmetic overflows uint64");
+    span->leading_elements = offset - first_el;
+    span->trailing_elements = end_el - end;
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_tensor_view_init(uint32_t type_id, const void *data, uint64_t bytes,
+                                  uint32_t layout, kq_hip_tensor_view *view,
+                                  kq_diagnostic *diag) {
+    kq_hip_quant_geometry g;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (view == NULL || data == NULL || bytes == 0u || layout > KQ_HIP_LAYOUT_FUSED_MEMBER)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "device data, size, layout and view are required");
+    memset(view, 0, sizeof(*view));
+    st = kq_hip_quant_geometry_for_type(type_id, &g, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (bytes % g.bytes_per_block != 0u)
+        return kq_fail(diag, KQ_STATUS_MALFORMED_QUANTIZED_DATA, "a view covers whole blocks");
+    view->type_id = type_id;
+    view->layout = layout;
+    view->block_elements = g.block_elements;
+    view->bytes_per_block = g.bytes_per_block;
+    view->block_count = bytes / g.bytes_per_block;
+    view->canonical_contiguous = layout == KQ_HIP_LAYOUT_CANONICAL_CONTIGUOUS ||
+                                 layout == KQ_HIP_LAYOUT_FUSED_MEMBER;
+    view->device_data = data;
+    view->mapped_bytes = bytes;
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_dequantize_view_blocks_f32(kq_hip_context *c, const kq_hip_tensor_view *v,
+                                            uint64_t first, uint64_t count, uint32_t order,
+                                            float *out, uint64_t capacity, uint64_t *out_count,
+                                            kq_diagnostic *diag) {
+    kq_hip_quant_geometry g;
+    uint64_t end, off, bytes;
+    const char *src;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (v == NULL || out_count == NULL || count == 0u ||
+        (order != KQ_HIP_PHYSICAL_ORDER && order != KQ_HIP_REQUIRE_CANONICAL_ORDER))
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "valid tensor view, block range and order are required");
+    *out_count = 0u;
+    if (v->device_data == NULL || v->bytes_per_block == 0u || v->block_elements == 0u ||
+        kq_hip_quant_geometry_for_type(v->type_id, &g, NULL) != KQ_STATUS_OK ||
+        g.bytes_per_block != v->bytes_per_block || g.block_elements != v->block_elements)
+        return kq_fail(diag, KQ_STATUS_TENSOR_OWNERSHIP_MISMATCH,
+                       "tensor view is not live or structurally valid");
+    if (order == KQ_HIP_REQUIRE_CANONICAL_ORDER &&
+        (v->canonical_contiguous == 0u || v->layout == KQ_HIP_LAYOUT_TRANSFORMED_PHYSICAL ||
+         v->layout == KQ_HIP_LAYOUT_SPLIT_SEGMENT))
+        return kq_fail(diag, KQ_STATUS_TENSOR_LAYOUT_MISMATCH,
+                       "view does not provide canonical-contiguous order");
+    if (first > UINT64_MAX - count || (end = first + count) > v->block_count ||
+        !u64_mul(first, v->bytes_per_block, &off) || !u64_mul(count, v->bytes_per_block, &bytes) ||
+        off > v->mapped_bytes || bytes > v->mapped_bytes - off)
+        return kq_fail(diag, KQ_STATUS_SPAN_OUT_OF_RANGE, "requested decode blocks are outside the view");
+    src = (const char *)v->device_data + off;
+    if (!aligned(src, packed_alignment(v->type_id)) && ctx_ok(c)) {
+        /* a span that starts off the decoder's alignment (odd blocks of the
+         * 34-, 18- and 210-byte formats) is decoded from an aligned copy */
+        hipError_t e;
+        st = set_device(c, diag);
+        if (st != KQ_STATUS_OK) return st;
+        if (c->stage_dev_cap < bytes) {
+            if (c->stage_dev) {
+                (void)hipStreamSynchronize(c->stream);
+                (void)hipFree(c->stage_dev);
+                c->stage_dev = NULL;
+                c->stage_dev_cap = 0u;
+            }
+            e = hipMalloc(&c->stage_dev, (size_t)bytes);
+            if (e != hipSuccess) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "view staging: %s",
+                                                 hipGetErrorString(e));
+            c->stage_dev_cap = bytes;
+        }
+        e = hipMemcpyAsync(c->stage_dev, src, (size_t)bytes, hipMemcpyDeviceToDevice, c->stream);
+        if (e != hipSuccess) return hip_fail(diag, e, "view staging copy");
+        src = (const char *)c->stage_dev;
+    }
+    return kq_hip_dequantize_blocks_f32(c, v->type_id, src, bytes, out, capacity, out_count, diag);
+}
+
+/* ------------------------------------------------------------------ */
+/* GDN layouts */
+
+#define KQ_GDN_QK_ROWS 4096u     /* 2 x 16 key heads x 128 */
+#define KQ_GDN_UNITS 48u         /* 16 key heads x 3 value repeats */
+
+/* rows (or columns) the layout maps onto themselves, its identity prefix
+ * and unit width; 0 when the layout moves rows (columns) otherwise */
+static int gdn_geometry(uint32_t layout, int columns, uint64_t *n, uint64_t *prefix,
+                        uint64_t *width) {
+    *prefix = 0u;
+    switch (layout) {
+    case KQ_HIP_GDN_QKV:
+    case KQ_HIP_GDN_CONV: *prefix = KQ_GDN_QK_ROWS; *width = 128u; break;
+    case KQ_HIP_GDN_GATE: *width = 128u; break;
+    case KQ_HIP_GDN_ALPHA:
+    case KQ_HIP_GDN_BETA: *width = 1u; break;
+    case KQ_HIP_GDN_OUT: *width = 128u; break;
+    default: return 0;
+    }
+    if ((layout == KQ_HIP_GDN_OUT) != (columns != 0)) return 0;
+    *n = *prefix + KQ_GDN_UNITS * *width;
+    return 1;
+}
+
+static uint64_t grouped_to_tiled(uint64_t c, uint64_t w) {
+    const uint64_t group = c / (3u * w), within = c % (3u * w);
+    return (within / w * 16u + group) * w + within % w;
+}
+
+static kq_status gdn_index(uint32_t layout, int columns, uint64_t n, uint64_t index,
+                           uint64_t *out, kq_diagnostic *diag) {
+    uint64_t want, prefix, width;
+    kq_diagnostic_clear(diag);
+    if (out == NULL || layout > KQ_HIP_GDN_OUT)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "a GDN layout and an output are required");
+    if (index >= n) return kq_fail(diag, KQ_STATUS_SPAN_OUT_OF_RANGE, "index is outside the matrix");
+    if (layout == KQ_HIP_GDN_NONE || !gdn_geometry(layout, columns, &want, &prefix, &width)) {
+        *out = index; /* rows of GDN_OUT and columns of the row layouts stay */
+        return KQ_STATUS_OK;
+    }
+    if (n != want)
+        return kq_fail(diag, KQ_STATUS_TENSOR_LAYOUT_MISMATCH,
+                       "this GDN layout maps %llu %s onto themselves, not %llu",
+                       (unsigned long long)want, columns ? "columns" : "rows",
+                       (unsigned long long)n);
+    *out = index < prefix ? index : prefix + grouped_to_tiled(index - prefix, width);
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_gdn_physical_row(uint32_t layout, uint64_t rows, uint64_t row, uint64_t *out,
+                                  kq_diagnostic *diag) {
+    return gdn_index(layout, 0, rows, row, out, diag);
+}
+
+kq_status kq_hip_gdn_physical_column(uint32_t layout, uint64_t cols, uint64_t col,
+                                     uint64_t *out, kq_diagnostic *diag) {
+    return gdn_index(layout, 1, cols, col, out, diag);
+}
+
+kq_status kq_hip_gdn_canonicalize(kq_hip_context *c, uint32_t layout, uint32_t type_id,
+                                  const void *phys, uint64_t rows, uint64_t cols, void *canon,
+                                  uint64_t capacity, kq_diagnostic *diag) {
+    uint64_t be, bb, row_bytes, bytes, n, prefix, width, units, unit_bytes;
+    const int columns = layout == KQ_HIP_GDN_OUT;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || phys == NULL || canon == NULL || rows == 0u || cols == 0u ||
+        layout > KQ_HIP_GDN_OUT)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT,
+                       "a GDN layout, both matrices and a non-zero shape are required");
+    st = quant_geometry(type_id, &be, &bb, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (cols % be != 0u)
+        return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH, "columns are not whole quant blocks");
+    row_bytes = cols / be * bb;
+    if (!u64_mul(rows, row_bytes, &bytes))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "matrix byte count overflows");
+    if (layout != KQ_HIP_GDN_NONE) {
+        gdn_geometry(layout, columns, &n, &prefix, &width);
+        if ((columns ? cols : rows) != n)
+            return kq_fail(diag, KQ_STATUS_TENSOR_LAYOUT_MISMATCH,
+                           "this GDN layout maps %llu %s onto themselves, not %llu",
+                           (unsigned long long)n, columns ? "columns" : "rows",
+                           (unsigned long long)(columns ? cols : rows));
+        if (columns && 128u % be != 0u)
+            return kq_fail(diag, KQ_STATUS_UNSUPPORTED_TENSOR_TYPE,
+                           "GDN_OUT moves 128-column units: blocks of at most 128 elements");
+    }
+    if (capacity < bytes)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL, "the canonical copy needs %llu bytes",
+                       (unsigned long long)bytes);
+    if (ranges_overlap(phys, bytes, canon, bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "the two matrices overlap");
+    if (!aligned(phys, 2u) || !aligned(canon, 2u) || bb % 2u != 0u)
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "matrices must be 2-byte aligned");
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    if (layout == KQ_HIP_GDN_NONE)
+        return finish(c, hipMemcpyAsync(canon, phys, (size_t)bytes, hipMemcpyDeviceToDevice,
+                                        c->stream), "canonical copy", diag);
+    units = columns ? rows * KQ_GDN_UNITS : rows;
+    unit_bytes = columns ? 128u / be * bb : row_bytes;
+    if (units > 0x7fffffffu || unit_bytes > 0x7fffffffu)
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "matrix too large for one gather");
+    return finish(c, kq_launch_gdn_gather(phys, canon, units, (uint32_t)unit_bytes, columns, prefix,
+                                          (uint32_t)width, KQ_GDN_UNITS, c->stream),
+                  "GDN gather launch", diag);
 }
 
 static kq_status ensure_parts(kq_hip_context *c, uint64_t n, kq_diagnostic *diag) {

@@ -32,13 +32,17 @@ const char *kq_status_string(kq_status status) {
     case KQ_STATUS_INCONSISTENT_DATA_SECTION: return "inconsistent data section";
     case KQ_STATUS_INVALID_QUANTIZED_GEOMETRY: return "invalid quantized geometry";
     case KQ_STATUS_NONCONTIGUOUS_TENSOR_VIEW: return "noncontiguous tensor view";
+    case KQ_STATUS_TENSOR_LAYOUT_MISMATCH: return "tensor layout mismatch";
     case KQ_STATUS_TENSOR_OWNERSHIP_MISMATCH: return "tensor ownership mismatch";
+    case KQ_STATUS_INVALID_TOKEN_ID: return "invalid token id";
     case KQ_STATUS_BUFFER_TOO_SMALL: return "buffer too small";
     case KQ_STATUS_MALFORMED_QUANTIZED_DATA: return "malformed quantized data";
     case KQ_STATUS_NUMERIC_DOMAIN: return "numeric domain error";
     case KQ_STATUS_DIMENSION_MISMATCH: return "dimension mismatch";
     case KQ_STATUS_ALIASING_VIOLATION: return "aliasing violation";
     case KQ_STATUS_INCOMPATIBLE_MOE: return "incompatible MoE";
+    case KQ_STATUS_INCOMPATIBLE_SAMPLING: return "incompatible sampling";
+    case KQ_STATUS_INVALID_RNG_STATE: return "invalid RNG state";
     case KQ_STATUS_DEVICE_FAILURE: return "device failure";
     default: return "unknown status";
     }

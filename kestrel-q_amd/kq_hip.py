@@ -35,9 +35,11 @@ STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "OUT_OF_MEMORY", 3: "FILE_OPEN_FAIL
           19: "INCONSISTENT_DATA_SECTION", 12: "UNSUPPORTED_TENSOR_TYPE",
           13: "ARITHMETIC_OVERFLOW", 14: "LIMIT_EXCEEDED", 15: "INVALID_ALIGNMENT",
           16: "SPAN_OUT_OF_RANGE", 25: "INVALID_QUANTIZED_GEOMETRY",
-          26: "NONCONTIGUOUS_TENSOR_VIEW", 28: "TENSOR_OWNERSHIP_MISMATCH", 32: "BUFFER_TOO_SMALL",
+          26: "NONCONTIGUOUS_TENSOR_VIEW", 27: "TENSOR_LAYOUT_MISMATCH",
+          28: "TENSOR_OWNERSHIP_MISMATCH", 31: "INVALID_TOKEN_ID", 32: "BUFFER_TOO_SMALL",
           38: "MALFORMED_QUANTIZED_DATA", 39: "NUMERIC_DOMAIN", 40: "DIMENSION_MISMATCH",
-          41: "ALIASING_VIOLATION", 46: "INCOMPATIBLE_MOE", 1000: "DEVICE_FAILURE"}
+          41: "ALIASING_VIOLATION", 46: "INCOMPATIBLE_MOE", 54: "INCOMPATIBLE_SAMPLING",
+          55: "INVALID_RNG_STATE", 1000: "DEVICE_FAILURE"}
 CODES = {v: k for k, v in STATUS.items()}
 
 
@@ -107,6 +109,25 @@ CHECKPOINT_KINDS = ("router_logits", "router_probabilities", "selected_weights",
                     "shared_up_projection", "shared_activated", "shared_output",
                     "shared_scale_logit", "shared_scale", "gated_shared_output",
                     "operator_output")
+
+
+class QuantBlockSpan(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "requested_element_offset", "requested_element_count", "first_block", "block_count",
+        "physical_byte_offset", "physical_byte_length", "leading_elements",
+        "trailing_elements")]
+
+
+class TensorView(C.Structure):
+    _fields_ = [("type_id", C.c_uint32), ("layout", C.c_uint32), ("block_elements", C.c_uint64),
+                ("bytes_per_block", C.c_uint64), ("block_count", C.c_uint64),
+                ("canonical_contiguous", C.c_uint32), ("reserved", C.c_uint32),
+                ("device_data", C.c_void_p), ("mapped_bytes", C.c_uint64)]
+
+
+LAYOUT_CANONICAL, LAYOUT_TRANSFORMED, LAYOUT_SPLIT, LAYOUT_FUSED = 0, 1, 2, 3
+PHYSICAL_ORDER, CANONICAL_ORDER = 0, 1
+GDN = {"none": 0, "qkv": 1, "gate": 2, "alpha": 3, "beta": 4, "conv": 5, "out": 6}
 
 
 class StringView(C.Structure):
@@ -204,6 +225,22 @@ SIGNATURES = {
     "kq_hip_quant_packed_size": (C.c_int, [C.c_uint32, C.c_uint64, C.c_void_p, C.c_void_p]),
     "kq_hip_expert_member_span": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint32,
                                             C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "kq_hip_quant_element_to_block": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_void_p,
+                                                C.c_void_p, C.c_void_p]),
+    "kq_hip_quant_range_to_blocks": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
+                                               C.c_void_p, C.c_void_p]),
+    "kq_hip_tensor_view_init": (C.c_int, [C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint32,
+                                          C.c_void_p, C.c_void_p]),
+    "kq_hip_dequantize_view_blocks_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64,
+                                                    C.c_uint64, C.c_uint32, C.c_void_p,
+                                                    C.c_uint64, C.c_void_p, C.c_void_p]),
+    "kq_hip_gdn_physical_row": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_void_p,
+                                          C.c_void_p]),
+    "kq_hip_gdn_physical_column": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_void_p,
+                                             C.c_void_p]),
+    "kq_hip_gdn_canonicalize": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
+                                          C.c_uint64, C.c_uint64, C.c_void_p, C.c_uint64,
+                                          C.c_void_p]),
     "kq_hip_dequantize_blocks_f32": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64,
                                                C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
     "kq_hip_quantized_row_dot_f32": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64,
@@ -283,6 +320,35 @@ def packed_size(type_id: int, elements: int) -> int:
     out, d = C.c_uint64(), Diagnostic()
     check(lib().kq_hip_quant_packed_size(type_id, elements, C.byref(out), C.byref(d)), d)
     return out.value
+
+
+def element_to_block(type_id: int, total: int, index: int) -> tuple[int, int]:
+    b, w, d = C.c_uint64(), C.c_uint64(), Diagnostic()
+    check(lib().kq_hip_quant_element_to_block(type_id, total, index, C.byref(b), C.byref(w),
+                                              C.byref(d)), d)
+    return b.value, w.value
+
+
+def range_to_blocks(type_id: int, total: int, offset: int, count: int) -> QuantBlockSpan:
+    sp, d = QuantBlockSpan(), Diagnostic()
+    check(lib().kq_hip_quant_range_to_blocks(type_id, total, offset, count, C.byref(sp),
+                                             C.byref(d)), d)
+    return sp
+
+
+def tensor_view(type_id: int, data, nbytes: int, layout: int = LAYOUT_CANONICAL) -> TensorView:
+    v, d = TensorView(), Diagnostic()
+    ptr = data.ptr if hasattr(data, "ptr") else data
+    check(lib().kq_hip_tensor_view_init(type_id, C.c_void_p(ptr), nbytes, layout, C.byref(v),
+                                        C.byref(d)), d)
+    return v
+
+
+def gdn_physical_index(layout: str, n: int, index: int, columns: bool = False) -> int:
+    o, d = C.c_uint64(), Diagnostic()
+    fn = lib().kq_hip_gdn_physical_column if columns else lib().kq_hip_gdn_physical_row
+    check(fn(GDN[layout], n, index, C.byref(o), C.byref(d)), d)
+    return o.value
 
 
 def expert_member_span(type_id, rows, cols, experts, expert_id) -> tuple[int, int]:
@@ -411,6 +477,20 @@ class Context:
                                                  packed_bytes, self._p(out), capacity,
                                                  C.byref(cnt), C.byref(d)), d)
         return cnt.value
+
+    def dequantize_view(self, view: TensorView, first: int, count: int, order: int, out,
+                        capacity: int) -> int:
+        cnt, d = C.c_uint64(), Diagnostic()
+        check(lib().kq_hip_dequantize_view_blocks_f32(self._h, C.byref(view), first, count, order,
+                                                      self._p(out), capacity, C.byref(cnt),
+                                                      C.byref(d)), d)
+        return cnt.value
+
+    def gdn_canonicalize(self, layout: str, type_id: int, phys, rows: int, cols: int, canon,
+                         capacity: int) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_gdn_canonicalize(self._h, GDN[layout], type_id, self._p(phys), rows,
+                                            cols, self._p(canon), capacity, C.byref(d)), d)
 
     def row_dot(self, type_id: int, packed, packed_bytes: int, x, count: int, out) -> None:
         d = Diagnostic()

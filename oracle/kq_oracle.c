@@ -417,6 +417,105 @@ int kqo_matvec_f32(uint32_t type_id, const void *w, uint64_t rows,
     return failed;
 }
 
+/* GDN layouts (src/kq_weight_provider.c:17-20, :205-248, :438-451): the
+ * model's value-head features are stored tiled by repeat while the
+ * canonical order groups them by key head. grouped_to_tiled maps a
+ * canonical index to its physical one with 16 key heads and 3 repeats. */
+#define KQO_GDN_KEY_HEADS 16U
+#define KQO_GDN_HEAD_WIDTH 128U
+#define KQO_GDN_VALUE_REPEAT 3U
+
+static uint64_t grouped_to_tiled(uint64_t canonical, uint64_t width) {
+    uint64_t group = canonical / (KQO_GDN_VALUE_REPEAT * width);
+    uint64_t within = canonical % (KQO_GDN_VALUE_REPEAT * width);
+    uint64_t repeat = within / width;
+    uint64_t feature = within % width;
+    return (repeat * KQO_GDN_KEY_HEADS + group) * width + feature;
+}
+
+/* physical_row_for (src/kq_weight_provider.c:231-248) */
+uint64_t kqo_gdn_physical_row(uint32_t transform, uint64_t canonical_row) {
+    const uint64_t qk = 2ULL * KQO_GDN_KEY_HEADS * KQO_GDN_HEAD_WIDTH;
+    switch (transform) {
+    case KQO_GDN_QKV:
+    case KQO_GDN_CONV:
+        return canonical_row < qk ? canonical_row
+                                  : qk + grouped_to_tiled(canonical_row - qk, KQO_GDN_HEAD_WIDTH);
+    case KQO_GDN_ALPHA:
+    case KQO_GDN_BETA:
+        return grouped_to_tiled(canonical_row, 1U);
+    case KQO_GDN_GATE:
+        return grouped_to_tiled(canonical_row, KQO_GDN_HEAD_WIDTH);
+    default:
+        return canonical_row;
+    }
+}
+
+uint64_t kqo_gdn_physical_column(uint32_t transform, uint64_t canonical_column) {
+    return transform == KQO_GDN_OUT ? grouped_to_tiled(canonical_column, KQO_GDN_HEAD_WIDTH)
+                                    : canonical_column;
+}
+
+/* The provider's linear for a GDN role (src/kq_weight_provider.c:438-475):
+ * GDN_OUT scatters the activation into physical column order first; every
+ * role dots canonical row r with physical row physical_row_for(r). A
+ * transform that leaves the geometry fails with DIMENSION_MISMATCH (the
+ * reference's TENSOR_LAYOUT_MISMATCH). */
+int kqo_gdn_linear_f32(uint32_t transform, uint32_t type_id, const void *w, uint64_t rows,
+                       uint64_t cols, const float *x, float *y, int threads) {
+    uint32_t be, bb;
+    uint64_t row_bytes;
+    float *permuted = NULL;
+    const float *act = x;
+    int failed = KQO_OK;
+    int64_t r;
+    int st = kqo_geometry(type_id, &be, &bb);
+    if (st != KQO_OK) return st;
+    if (w == NULL || x == NULL || y == NULL || rows == 0U || cols == 0U)
+        return KQO_INVALID_ARGUMENT;
+    if (cols % be != 0U) return KQO_DIMENSION_MISMATCH;
+    row_bytes = cols / be * bb;
+    if (transform == KQO_GDN_OUT) {
+        uint64_t i;
+        permuted = (float *)calloc(cols, sizeof(float));
+        if (permuted == NULL) return KQO_INVALID_ARGUMENT;
+        for (i = 0U; i < cols; ++i) {
+            uint64_t pc = kqo_gdn_physical_column(transform, i);
+            if (pc >= cols) {
+                free(permuted);
+                return KQO_DIMENSION_MISMATCH;
+            }
+            permuted[pc] = x[i];
+        }
+        act = permuted;
+    }
+    for (r = 0; r < (int64_t)rows; ++r)
+        if (kqo_gdn_physical_row(transform, (uint64_t)r) >= rows) {
+            free(permuted);
+            return KQO_DIMENSION_MISMATCH;
+        }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1) if (threads > 1)
+#else
+    (void)threads;
+#endif
+    for (r = 0; r < (int64_t)rows; ++r) {
+        const uint64_t pr = kqo_gdn_physical_row(transform, (uint64_t)r);
+        float v = 0.0f;
+        int s = kqo_row_dot_f32(type_id, (const unsigned char *)w + pr * row_bytes, row_bytes,
+                                act, cols, &v);
+        if (s != KQO_OK) {
+#ifdef _OPENMP
+#pragma omp critical
+#endif
+            failed = s;
+        }
+        y[r] = v;
+    }
+    free(permuted);
+    return failed;
+}
+
 /* src/kq_model_exec.c:566-584: first maximum (strict >), ties -> lowest id. */
 int kqo_argmax_f32(const float *logits, uint64_t count, uint32_t *id) {
     uint64_t i;

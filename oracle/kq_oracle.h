@@ -159,6 +159,22 @@ int kqo_gr_read(uint32_t nbranch, uint32_t hidden, uint32_t rank, float eps,
 void kqo_gr_write(uint32_t nbranch, uint32_t hidden, const float *branches,
                   const float *block_output, const float *write_gate, float *out);
 
+/* GDN layouts: the provider's row and column maps and its linear for the
+ * GDN roles (src/kq_weight_provider.c:205-248, :438-475). */
+enum {
+    KQO_GDN_NONE = 0,
+    KQO_GDN_QKV = 1,
+    KQO_GDN_GATE = 2,
+    KQO_GDN_ALPHA = 3,
+    KQO_GDN_BETA = 4,
+    KQO_GDN_CONV = 5,
+    KQO_GDN_OUT = 6
+};
+uint64_t kqo_gdn_physical_row(uint32_t transform, uint64_t canonical_row);
+uint64_t kqo_gdn_physical_column(uint32_t transform, uint64_t canonical_column);
+int kqo_gdn_linear_f32(uint32_t transform, uint32_t type_id, const void *w, uint64_t rows,
+                       uint64_t cols, const float *x, float *y, int threads);
+
 /* kq_certify.c: the device's certified one-token routing restated on the
  * CPU (ids of the certified selection, or *certified = 0), and a campaign
  * of random and near-tie cases against kqo_moe_route_f32. */

@@ -93,6 +93,11 @@ def _declare(l: C.CDLL) -> None:
     l.kqo_moe_execute.argtypes = [C.POINTER(MoeDims), C.POINTER(MoeWeights), P, U64, P,
                                   C.POINTER(MoeTrace), I]
     l.kqo_moe_permutation.argtypes = [P, U64, U32, U32, P, P, P]
+    l.kqo_gdn_physical_row.argtypes = [U32, U64]
+    l.kqo_gdn_physical_row.restype = U64
+    l.kqo_gdn_physical_column.argtypes = [U32, U64]
+    l.kqo_gdn_physical_column.restype = U64
+    l.kqo_gdn_linear_f32.argtypes = [U32, U32, P, U64, U64, P, P, I]
     l.kqo_route_certify.argtypes = [U32, U32, U32, P, P, P, C.POINTER(I)]
     l.kqo_certify_campaign.argtypes = [U64, U64, U32, U32, U32, I, F, C.c_double, I, P]
 
@@ -294,6 +299,31 @@ def moe_execute(dims: dict, weights: dict, hidden: np.ndarray, trace: bool = Fal
     if st != OK:
         raise OracleError(st)
     return (out, tr_arrays) if trace else out
+
+
+GDN = {"none": 0, "qkv": 1, "gate": 2, "alpha": 3, "beta": 4, "conv": 5, "out": 6}
+
+
+def gdn_physical_row(transform: str, row: int) -> int:
+    return int(lib().kqo_gdn_physical_row(GDN[transform], row))
+
+
+def gdn_physical_column(transform: str, col: int) -> int:
+    return int(lib().kqo_gdn_physical_column(GDN[transform], col))
+
+
+def gdn_linear(transform: str, type_id: int, w: np.ndarray, rows: int, cols: int,
+               x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """The provider's linear for a GDN role: physical rows, GDN_OUT's
+    activation permutation (src/kq_weight_provider.c:438-475)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(w)
+    y = np.empty(rows, np.float32)
+    st = lib().kqo_gdn_linear_f32(GDN[transform], type_id, _p(w), rows, cols, _p(x), _p(y),
+                                  threads)
+    if st != OK:
+        raise OracleError(st)
+    return y
 
 
 def route_certify(router: np.ndarray, x: np.ndarray, top_k: int):

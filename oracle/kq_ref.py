@@ -43,6 +43,14 @@ class MoeWeightsF32(C.Structure):
                 for n, t in ((role, C.c_void_p), (role + "_count", C.c_uint64))]
 
 
+class QuantBlockSpan(C.Structure):
+    # include/kq_tensor_view.h:39-48
+    _fields_ = [(n, C.c_uint64) for n in (
+        "requested_element_offset", "requested_element_count", "first_block", "block_count",
+        "physical_byte_offset", "physical_byte_length", "leading_elements",
+        "trailing_elements")]
+
+
 class RefError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"reference status {status}: {message}")
@@ -79,6 +87,8 @@ def lib() -> C.CDLL:
             "kq_moe_route_f32": [vp, vp, u64, vp, vp, u64, vp, u64, vp, u64, vp, u64, dp],
             "kq_moe_execute_f32": [vp, C.POINTER(MoeWeightsF32), vp, u64, vp, u64, vp, u64,
                                    vp, vp, vp, dp],
+            "kq_quant_element_to_block": [u32, u64, u64, C.POINTER(u64), C.POINTER(u64), dp],
+            "kq_quant_range_to_blocks": [u32, u64, u64, u64, C.POINTER(QuantBlockSpan), dp],
         }
         for name, args in sig.items():
             fn = getattr(l, name)
@@ -98,6 +108,21 @@ def _p(a: np.ndarray) -> int:
 def _check(st: int, d: Diagnostic) -> None:
     if st != 0:
         raise RefError(st, d.message.decode(errors="replace"))
+
+
+def element_to_block(type_id: int, total: int, index: int):
+    """(status, block, within) from the reference's kq_quant_element_to_block."""
+    b, w, d = C.c_uint64(), C.c_uint64(), Diagnostic()
+    st = lib().kq_quant_element_to_block(type_id, total, index, C.byref(b), C.byref(w),
+                                         C.byref(d))
+    return st, b.value, w.value
+
+
+def range_to_blocks(type_id: int, total: int, offset: int, count: int):
+    """(status, span fields) from the reference's kq_quant_range_to_blocks."""
+    sp, d = QuantBlockSpan(), Diagnostic()
+    st = lib().kq_quant_range_to_blocks(type_id, total, offset, count, C.byref(sp), C.byref(d))
+    return st, tuple(getattr(sp, n) for n, _ in QuantBlockSpan._fields_)
 
 
 def dequantize(type_id: int, packed: np.ndarray, elements: int) -> np.ndarray:

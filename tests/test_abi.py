@@ -93,7 +93,7 @@ def test_status_strings():
     # every code the binding names has its own string
     strings = {lib.kq_status_string(code) for code in kq_hip.STATUS}
     assert len(strings) == len(kq_hip.STATUS) and b"unknown status" not in strings
-    assert lib.kq_status_string(27) == b"unknown status"
+    assert lib.kq_status_string(29) == b"unknown status"  # a tokenizer code, not on this path
 
 
 def _gpu_present() -> bool:
