@@ -39,6 +39,7 @@ enum {
     KQO_INVALID_ARGUMENT = 1,
     KQO_UNSUPPORTED_TENSOR_TYPE = 12,
     KQO_ARITHMETIC_OVERFLOW = 13,
+    KQO_INVALID_TOKEN_ID = 31,
     KQO_BUFFER_TOO_SMALL = 32,
     KQO_MALFORMED_QUANTIZED_DATA = 38,
     KQO_NUMERIC_DOMAIN = 39,
@@ -174,6 +175,40 @@ uint64_t kqo_gdn_physical_row(uint32_t transform, uint64_t canonical_row);
 uint64_t kqo_gdn_physical_column(uint32_t transform, uint64_t canonical_column);
 int kqo_gdn_linear_f32(uint32_t transform, uint32_t type_id, const void *w, uint64_t rows,
                        uint64_t cols, const float *x, float *y, int threads);
+
+/* kq_sample.c: the reference's sampler (src/kq_sampling.c). The RNG
+ * record has the layout of kq_sampling_rng_state (include/kq_sampling.h). */
+typedef struct kqo_rng_state {
+    uint32_t version;
+    uint32_t reserved;
+    uint64_t seed;
+    uint64_t stream;
+    uint64_t state;
+    uint64_t increment;
+    uint64_t draws;
+    uint64_t integrity;
+} kqo_rng_state;
+
+typedef struct kqo_sample_result {
+    uint32_t selected_token_id;
+    uint32_t top_k_retained_count;
+    uint32_t retained_count;
+    uint32_t rng_word;
+    float selected_probability;
+    float maximum_probability;
+    float normalized_sum_f32;
+    uint32_t reserved;
+    double uniform_value;
+} kqo_sample_result;
+
+void kqo_rng_seed(uint64_t seed, uint64_t stream, kqo_rng_state *out);
+uint32_t kqo_rng_next(kqo_rng_state *state);
+/* one selection with the RNG word already drawn; scores_out / probs_out
+ * (optional, count each) receive the processed logits and the final
+ * probabilities (zero outside the kept set) */
+int kqo_sample_f32(float temperature, float top_p, uint32_t top_k, uint32_t canonical_count,
+                   const float *logits, uint32_t count, uint32_t word, kqo_sample_result *result,
+                   float *scores_out, float *probs_out);
 
 /* kq_certify.c: the device's certified one-token routing restated on the
  * CPU (ids of the certified selection, or *certified = 0), and a campaign

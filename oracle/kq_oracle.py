@@ -59,6 +59,21 @@ class MoeTrace(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in TRACE_FIELDS]
 
 
+class RngState(C.Structure):
+    # include/kq_sampling.h:40-49
+    _fields_ = [("version", C.c_uint32), ("reserved", C.c_uint32), ("seed", C.c_uint64),
+                ("stream", C.c_uint64), ("state", C.c_uint64), ("increment", C.c_uint64),
+                ("draws", C.c_uint64), ("integrity", C.c_uint64)]
+
+
+class SampleResult(C.Structure):
+    _fields_ = [("selected_token_id", C.c_uint32), ("top_k_retained_count", C.c_uint32),
+                ("retained_count", C.c_uint32), ("rng_word", C.c_uint32),
+                ("selected_probability", C.c_float), ("maximum_probability", C.c_float),
+                ("normalized_sum_f32", C.c_float), ("reserved", C.c_uint32),
+                ("uniform_value", C.c_double)]
+
+
 def _declare(l: C.CDLL) -> None:
     P, U32, U64, F, I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_int
     l.kqo_geometry.argtypes = [U32, C.POINTER(U32), C.POINTER(U32)]
@@ -98,6 +113,11 @@ def _declare(l: C.CDLL) -> None:
     l.kqo_gdn_physical_column.argtypes = [U32, U64]
     l.kqo_gdn_physical_column.restype = U64
     l.kqo_gdn_linear_f32.argtypes = [U32, U32, P, U64, U64, P, P, I]
+    l.kqo_rng_seed.argtypes = [U64, U64, C.POINTER(RngState)]
+    l.kqo_rng_seed.restype = None
+    l.kqo_rng_next.argtypes = [C.POINTER(RngState)]
+    l.kqo_rng_next.restype = U32
+    l.kqo_sample_f32.argtypes = [F, F, U32, U32, P, U32, U32, C.POINTER(SampleResult), P, P]
     l.kqo_route_certify.argtypes = [U32, U32, U32, P, P, P, C.POINTER(I)]
     l.kqo_certify_campaign.argtypes = [U64, U64, U32, U32, U32, I, F, C.c_double, I, P]
 
@@ -299,6 +319,28 @@ def moe_execute(dims: dict, weights: dict, hidden: np.ndarray, trace: bool = Fal
     if st != OK:
         raise OracleError(st)
     return (out, tr_arrays) if trace else out
+
+
+def rng_seed(seed: int, stream: int) -> RngState:
+    st = RngState()
+    lib().kqo_rng_seed(seed, stream, C.byref(st))
+    return st
+
+
+def rng_next(state: RngState) -> int:
+    return int(lib().kqo_rng_next(C.byref(state)))
+
+
+def sample(policy: dict, logits: np.ndarray, word: int, canonical_count: int):
+    """(status, SampleResult, scores, probabilities) of one selection with
+    the RNG word drawn."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    r = SampleResult()
+    sc = np.zeros(lg.size, np.float32)
+    pr = np.zeros(lg.size, np.float32)
+    st = lib().kqo_sample_f32(policy["temperature"], policy["top_p"], policy["top_k"],
+                              canonical_count, _p(lg), lg.size, word, C.byref(r), _p(sc), _p(pr))
+    return st, r, sc, pr
 
 
 GDN = {"none": 0, "qkv": 1, "gate": 2, "alpha": 3, "beta": 4, "conv": 5, "out": 6}

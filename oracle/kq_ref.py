@@ -245,3 +245,104 @@ class MoeConfig:
         _check(lib().kq_moe_execute_f32(self.h, C.byref(mw), _p(hidden), T, _p(out), out.size,
                                         _p(scratch), nbytes, None, None, None, C.byref(d)), d)
         return out
+
+
+class RngState(C.Structure):
+    # include/kq_sampling.h:40-49
+    _fields_ = [("version", C.c_uint32), ("reserved", C.c_uint32), ("seed", C.c_uint64),
+                ("stream", C.c_uint64), ("state", C.c_uint64), ("increment", C.c_uint64),
+                ("draws", C.c_uint64), ("integrity", C.c_uint64)]
+
+
+class SamplingPolicy(C.Structure):
+    # include/kq_sampling.h:24-31
+    _fields_ = [("version", C.c_uint32), ("flags", C.c_uint32), ("temperature", C.c_float),
+                ("top_p", C.c_float), ("top_k", C.c_uint32), ("reserved", C.c_uint32 * 3)]
+
+
+class SamplingResult(C.Structure):
+    # include/kq_sampling.h:51-63
+    _fields_ = [("selected_token_id", C.c_uint32), ("top_k_retained_count", C.c_uint32),
+                ("retained_count", C.c_uint32), ("rng_word", C.c_uint32),
+                ("selected_probability", C.c_float), ("maximum_probability", C.c_float),
+                ("normalized_sum_f32", C.c_float), ("reserved", C.c_uint32),
+                ("uniform_value", C.c_double), ("rng_draws_before", C.c_uint64),
+                ("rng_draws_after", C.c_uint64)]
+
+
+def sample(policy: dict, seed: int, stream: int, logits: np.ndarray):
+    """The reference's kq_sampling_select_f32 on a fresh RNG (seed, stream):
+    (status, SamplingResult, state after)."""
+    l = lib()
+    vp = C.c_void_p
+    l.kq_sampling_rng_seed.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(RngState),
+                                       C.POINTER(Diagnostic)]
+    l.kq_sampling_config_open_qwen38.argtypes = [C.POINTER(SamplingPolicy), C.POINTER(vp),
+                                                 C.POINTER(Diagnostic)]
+    l.kq_sampling_required_scratch_bytes.argtypes = [vp]
+    l.kq_sampling_required_scratch_bytes.restype = C.c_uint64
+    l.kq_sampling_config_close.argtypes = [vp]
+    l.kq_sampling_config_close.restype = None
+    l.kq_sampling_select_f32.argtypes = [vp, C.POINTER(RngState), vp, C.c_uint64, vp, C.c_uint64,
+                                         C.POINTER(SamplingResult), C.POINTER(Diagnostic)]
+    d = Diagnostic()
+    st = RngState()
+    _check(l.kq_sampling_rng_seed(seed, stream, C.byref(st), C.byref(d)), d)
+    pol = SamplingPolicy(1, 0, policy["temperature"], policy["top_p"], policy["top_k"])
+    cfg = vp()
+    _check(l.kq_sampling_config_open_qwen38(C.byref(pol), C.byref(cfg), C.byref(d)), d)
+    n = l.kq_sampling_required_scratch_bytes(cfg)
+    scratch = np.zeros(n, np.uint8)
+    lg = np.ascontiguousarray(logits, np.float32)
+    res = SamplingResult()
+    status = l.kq_sampling_select_f32(cfg, C.byref(st), _p(lg), lg.size, _p(scratch), n,
+                                      C.byref(res), C.byref(d))
+    l.kq_sampling_config_close(cfg)
+    return status, res, st
+
+
+class LayerDims(C.Structure):
+    # src/kq_layer_internal.h:10-17
+    _fields_ = [("layer_id", C.c_uint32), ("hidden_size", C.c_uint32),
+                ("branch_count", C.c_uint32), ("gr_rank", C.c_uint32),
+                ("rms_epsilon", C.c_float), ("family", C.c_int)]
+
+
+class LayerConfig(C.Structure):
+    # src/kq_layer_internal.h:19-31 (the fields the gated residual reads
+    # are the magic and the dimensions; the rest stay zero)
+    _fields_ = [("magic", C.c_uint32), ("model", C.c_void_p), ("dimensions", LayerDims),
+                ("owns_subconfigs", C.c_int), ("subconfigs", C.c_void_p * 5),
+                ("gr_bindings", C.c_void_p * 8), ("gr_workspace_bytes", C.c_uint64)]
+
+
+class GrWeightsF32(C.Structure):
+    # include/kq_layer.h:59-68
+    _fields_ = [("norm", C.c_void_p), ("norm_count", C.c_uint64), ("down", C.c_void_p),
+                ("down_count", C.c_uint64), ("up", C.c_void_p), ("up_count", C.c_uint64),
+                ("inject", C.c_void_p), ("inject_count", C.c_uint64)]
+
+
+def gr_read_f32(branches, hidden, rank, eps, norm, down, up, inject):
+    """The reference's kq_layer_gr_read_f32 on F32 weights (one token):
+    dict of normalized, read_gate, mixed, rank and write_gate."""
+    l = lib()
+    l.kq_layer_gr_read_f32.argtypes = [C.POINTER(LayerConfig), C.POINTER(GrWeightsF32)] + \
+        [C.c_void_p] * 6 + [C.POINTER(Diagnostic)]
+    b = np.ascontiguousarray(branches, np.float32).reshape(-1)
+    nb = b.size // hidden
+    width = nb * hidden
+    arrs = [np.ascontiguousarray(a, np.float32).reshape(-1) for a in (norm, down, up, inject)]
+    cfg = LayerConfig()
+    cfg.magic = 0x4b514c43
+    cfg.dimensions = LayerDims(0, hidden, nb, rank, eps, 0)
+    w = GrWeightsF32(_p(arrs[0]), arrs[0].size, _p(arrs[1]), arrs[1].size, _p(arrs[2]),
+                     arrs[2].size, _p(arrs[3]), arrs[3].size)
+    out = {"normalized": np.zeros(width, np.float32), "read_gate": np.zeros(width, np.float32),
+           "mixed": np.zeros(hidden, np.float32), "rank": np.zeros(rank, np.float32),
+           "write_gate": np.zeros(nb, np.float32)}
+    d = Diagnostic()
+    _check(l.kq_layer_gr_read_f32(C.byref(cfg), C.byref(w), _p(b), _p(out["normalized"]),
+                                  _p(out["read_gate"]), _p(out["mixed"]), _p(out["rank"]),
+                                  _p(out["write_gate"]), C.byref(d)), d)
+    return out

@@ -22,6 +22,13 @@ hex strings); the fixtures are data, not source. Provenance of each file:
                           moe_output checkpoints; the hyper-connection and MoE
                           weights only) and the layer-native-validation.json
                           contract
+  sampling_vectors.json   research/sampling/.../sampling-{calibration,holdout}.json
+                          (policy, seed, stream, logits as base + overrides,
+                          expected retained ids / processed logits /
+                          probabilities, selected id, RNG word and states),
+                          sampling-rng-vectors.json (PCG32 words, EXACT_BITS)
+                          and the float contract and categorical boundary
+                          words of sampling-native-validation.json
 """
 from __future__ import annotations
 
@@ -143,6 +150,24 @@ def routing(ref: Path) -> None:
     (OUT / "moe_routing_vectors.json").write_text(json.dumps(doc, indent=0, sort_keys=True))
 
 
+def sampling(ref: Path) -> None:
+    base = ref / "research/sampling/Qwen3.8-Flash-Next" / REV
+    cal = json.loads((base / "sampling-calibration.json").read_text())
+    hold = json.loads((base / "sampling-holdout.json").read_text())
+    rng = json.loads((base / "sampling-rng-vectors.json").read_text())
+    val = json.loads((base / "sampling-native-validation.json").read_text())
+    doc = {"source": [f"research/sampling/Qwen3.8-Flash-Next/{REV}/{n}" for n in (
+               "sampling-calibration.json", "sampling-holdout.json",
+               "sampling-rng-vectors.json", "sampling-native-validation.json")],
+           "calibration": cal["cases"], "holdout": hold["cases"],
+           "comparison": cal["comparison"],
+           "rng": {k: rng[k] for k in ("algorithm", "cases", "explicit_word_boundaries",
+                                       "uniform_mapping", "comparison_class")},
+           "floating_contract": val["floating_contract"],
+           "categorical_boundaries": val["categorical_boundaries"]}
+    (OUT / "sampling_vectors.json").write_text(json.dumps(doc, indent=0, sort_keys=True))
+
+
 def main() -> None:
     ref = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
     numeric(ref)
@@ -150,6 +175,7 @@ def main() -> None:
     moe(ref)
     routing(ref)
     layer(ref)
+    sampling(ref)
     for p in sorted(OUT.glob("*.json")):
         print(p.name, p.stat().st_size)
 

@@ -181,3 +181,21 @@ def test_execute_matches_reference_f32(shape, down_fmt):
     ref = cfg.execute(f32, x)
     cfg.close()
     same_bits(got, ref)
+
+
+@pytest.mark.parametrize("B,H,rank,seed", [(4, 8, 4, 1), (4, 256, 32, 2), (2, 100, 7, 3),
+                                           (4, 2560, 320, 4)])
+def test_gated_residual_read_bit_exact(B, H, rank, seed):
+    # the reference's src/kq_layer_qwen38.c (kq_layer_gr_read_f32) against
+    # the oracle's kqo_gr_read on F32 projections: every output bit for bit
+    W = B * H
+    key = lambda i: S.stream_key(S.W_MOE + 600 + seed, 90, i)
+    norm = S.normal_f32(key(1), W, 0.1)
+    down = S.normal_f32(key(2), rank * W, 0.05)
+    up = S.normal_f32(key(3), W * rank, 0.05)
+    inject = S.normal_f32(key(4), B * W, 0.01)
+    x = S.normal_f32(key(5), W)
+    want = R.gr_read_f32(x, H, rank, 1e-6, norm, down, up, inject)
+    got = O.gr_read(x, H, rank, 1e-6, norm, (O.F32, down), (O.F32, up), inject)
+    for k in ("normalized", "read_gate", "mixed", "rank", "write_gate"):
+        same_bits(got[k], want[k])
