@@ -338,6 +338,42 @@ def wl_lm_head(ctx, batch, warmup, steps, graph, fmt="Q6_K", V=151936, H=2048):
             "replicas": len(reps)}
 
 
+def wl_sample(ctx, pol, warmup, steps, lm=None):
+    """One synchronous kq_hip_sampling_select_f32 per step on the reference
+    model's 248,320 logits (device resident), or with lm = (fmt, H) the
+    fused LM head + sampler on W[248320][H]. Host wall clock per call: the
+    launches, the device sort and walks, and the result's copy back."""
+    V = kq_hip.QWEN38_VOCAB
+    cfg = kq_hip.SamplingConfig(kq_hip.sampling_policy(**pol))
+    scratch = ctx.alloc(cfg.scratch_bytes)
+    lg = (np.random.default_rng(7).standard_normal(V) * 3).astype(np.float32)
+    dl = ctx.upload(lg)
+    st = kq_hip.rng_seed(1, kq_hip.SAMPLING_DEFAULT_STREAM)
+    bufs = [scratch, dl]
+    if lm is None:
+        step = lambda: ctx.sample(cfg, st, dl, scratch)
+        nbytes = V * 4
+    else:
+        fmt, H = lm
+        t = kq_hip.TYPE_IDS[fmt]
+        w = S.quant_matrix(fmt, S.stream_key(S.W_LM_HEAD, S.R_WEIGHT, 1), V, H)
+        dw, dh = ctx.upload(w), ctx.upload(S.normal_f32(S.stream_key(S.W_LM_HEAD, S.R_HIDDEN), H))
+        bufs += [dw, dh]
+        step = lambda: ctx.lm_head_sample(cfg, st, t, dw, V, H, dh, dl, scratch)
+        nbytes = w.nbytes + H * 4 + V * 4
+    for _ in range(warmup):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    for b in bufs:
+        b.close()
+    cfg.close()
+    return {"ms_per_step": ms, "tokens_per_s": 1e3 / ms, "bytes_per_step": nbytes,
+            "policy": pol, "time_source": "host wall clock per synchronous call"}
+
+
 def wl_copy(ctx, nbytes, warmup, steps, graph):
     """Device-to-device copy of a known size: the reference point that scales
     the FETCH_SIZE / WRITE_SIZE counters to bytes. Not part of `all`."""
@@ -545,6 +581,18 @@ def main() -> int:
             lambda: wl_lm_head(ctx, 4, 10, max(10, K // 2), graph))
         run("lm_head_q8_0_248320x2560_b1",
             lambda: wl_lm_head(ctx, 1, 10, max(10, K // 2), graph, "Q8_0", 248320, 2560))
+        # the token sampler on the reference model's vocabulary: the default
+        # policy (top-k 20, top-p 0.95), the whole vocabulary (top-k off,
+        # top-p 1: every sum walks 248,320 ids), and the fused LM head +
+        # sampler on its Q8_0 248320 x 2560 head
+        run("sample_default_248320",
+            lambda: wl_sample(ctx, {"temperature": 1.0, "top_k": 20, "top_p": 0.95}, 5,
+                              max(10, K // 4)))
+        run("sample_full_vocab_248320",
+            lambda: wl_sample(ctx, {"temperature": 1.0, "top_k": 0, "top_p": 1.0}, 2, 10))
+        run("lm_head_sample_q8_0_248320x2560",
+            lambda: wl_sample(ctx, {"temperature": 1.0, "top_k": 20, "top_p": 0.95}, 5,
+                              max(10, K // 4), lm=("Q8_0", 2560)))
         run("moe_prefill_512", lambda: wl_moe(ctx, 512, 2, max(3, K // 20), graph, cache))
         run("moe_decode_1tok_2560x640",
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))

@@ -621,6 +621,148 @@ kq_status kq_hip_f32_expf(kq_hip_context *context, const float *device_input,
                           uint64_t count, float *device_output,
                           kq_diagnostic *diagnostic);
 
+/* ------------------------------------------------------------------ */
+/* Token sampling on the device. Replaces include/kq_sampling.h (all of
+ * it) and src/kq_sampling.c: the same policy, RNG state record and
+ * result record, field for field; the same PCG-XSH-RR 64/32 stream and
+ * integrity word; the same statuses in the same order; the same selected
+ * id, RNG word and float bits. The logits and the scratch are device
+ * memory; the RNG state and the result stay in host memory, and the state
+ * advances only when a call succeeds. */
+
+#define KQ_HIP_SAMPLING_QWEN38_VOCAB_SIZE UINT32_C(248320)
+#define KQ_HIP_SAMPLING_QWEN38_CANONICAL_TOKEN_COUNT UINT32_C(248077)
+#define KQ_HIP_SAMPLING_QWEN38_EOS_ID UINT32_C(248046)
+#define KQ_HIP_SAMPLING_QWEN38_PAD_ID UINT32_C(248044)
+#define KQ_HIP_SAMPLING_POLICY_VERSION UINT32_C(1)
+#define KQ_HIP_SAMPLING_RNG_STATE_VERSION UINT32_C(1)
+#define KQ_HIP_SAMPLING_DEFAULT_STREAM UINT64_C(0x4b515f53414d504c)
+#define KQ_HIP_SAMPLING_MAX_STREAM UINT64_C(0x7fffffffffffffff)
+
+typedef struct kq_hip_sampling_config kq_hip_sampling_config;
+
+/* kq_sampling_policy (include/kq_sampling.h:23-30): top_k 0 keeps every
+ * id; top_p 1 switches the nucleus cut off. */
+typedef struct kq_hip_sampling_policy {
+    uint32_t version;
+    uint32_t flags;
+    float temperature;
+    float top_p;
+    uint32_t top_k;
+    uint32_t reserved[3];
+} kq_hip_sampling_policy;
+
+/* kq_sampling_rng_state (include/kq_sampling.h:32-41) */
+typedef struct kq_hip_sampling_rng_state {
+    uint32_t version;
+    uint32_t reserved;
+    uint64_t seed;
+    uint64_t stream;
+    uint64_t state;
+    uint64_t increment;
+    uint64_t draws;
+    uint64_t integrity;
+} kq_hip_sampling_rng_state;
+
+/* kq_sampling_result (include/kq_sampling.h:43-55) */
+typedef struct kq_hip_sampling_result {
+    uint32_t selected_token_id;
+    uint32_t top_k_retained_count;
+    uint32_t retained_count;
+    uint32_t rng_word;
+    float selected_probability;
+    float maximum_probability;
+    float normalized_sum_f32;
+    uint32_t reserved;
+    double uniform_value;
+    uint64_t rng_draws_before;
+    uint64_t rng_draws_after;
+} kq_hip_sampling_result;
+
+/* kq_sampling_policy_qwen38_default (src/kq_sampling.c:161-170):
+ * temperature 1, top-p 0.95, top-k 20. */
+void kq_hip_sampling_policy_qwen38_default(kq_hip_sampling_policy *policy);
+
+/* kq_sampling_config_open_qwen38 (src/kq_sampling.c:172-225): the policy
+ * checks and statuses of the reference, for the model's 248,320-entry
+ * vocabulary of which 248,077 ids are canonical. Looks up the device
+ * sort's work size on the current HIP device (DEVICE_FAILURE without
+ * one). */
+kq_status kq_hip_sampling_config_open_qwen38(const kq_hip_sampling_policy *policy,
+                                             kq_hip_sampling_config **output,
+                                             kq_diagnostic *diagnostic);
+/* The same for another vocabulary: 1 <= canonical_token_count <=
+ * vocabulary_size <= 2^24, top_k <= vocabulary_size. No counterpart in
+ * the reference, which fixes the model's vocabulary. */
+kq_status kq_hip_sampling_config_open(const kq_hip_sampling_policy *policy,
+                                      uint32_t vocabulary_size,
+                                      uint32_t canonical_token_count,
+                                      kq_hip_sampling_config **output,
+                                      kq_diagnostic *diagnostic);
+void kq_hip_sampling_config_close(kq_hip_sampling_config *config);
+uint64_t kq_hip_sampling_config_owned_bytes(const kq_hip_sampling_config *config);
+uint32_t kq_hip_sampling_config_vocabulary_size(const kq_hip_sampling_config *config);
+/* Device scratch bytes a select call needs (kq_sampling_required_scratch_
+ * bytes, src/kq_sampling.c:242-244, there host bytes): six arrays of
+ * one entry per vocabulary id, the finiteness flags, the sort's work
+ * area and the device result record. 0 for an invalid config. */
+uint64_t kq_hip_sampling_required_scratch_bytes(const kq_hip_sampling_config *config);
+
+/* The RNG record (src/kq_sampling.c:246-322): host functions, the same
+ * statuses. */
+kq_status kq_hip_sampling_rng_seed(uint64_t seed, uint64_t stream,
+                                   kq_hip_sampling_rng_state *output,
+                                   kq_diagnostic *diagnostic);
+kq_status kq_hip_sampling_rng_reset(kq_hip_sampling_rng_state *state,
+                                    kq_diagnostic *diagnostic);
+kq_status kq_hip_sampling_rng_snapshot(const kq_hip_sampling_rng_state *state,
+                                       kq_hip_sampling_rng_state *output,
+                                       kq_diagnostic *diagnostic);
+kq_status kq_hip_sampling_rng_import(const kq_hip_sampling_rng_state *snapshot,
+                                     kq_hip_sampling_rng_state *output,
+                                     kq_diagnostic *diagnostic);
+kq_status kq_hip_sampling_rng_next_u32(kq_hip_sampling_rng_state *state, uint32_t *word,
+                                       kq_diagnostic *diagnostic);
+
+/* kq_sampling_select_f32 (src/kq_sampling.c:576-772) with device logits
+ * [logit_count == the config's vocabulary] and device scratch of at least
+ * kq_hip_sampling_required_scratch_bytes (any alignment; it must not
+ * overlap the logits). Synchronous: returns once the result is on the
+ * host. On success *state has advanced by one draw; on any failure
+ * neither *state nor *result is written. */
+kq_status kq_hip_sampling_select_f32(kq_hip_context *context,
+                                     const kq_hip_sampling_config *config,
+                                     kq_hip_sampling_rng_state *state,
+                                     const float *device_logits, uint64_t logit_count,
+                                     void *device_scratch, uint64_t scratch_bytes,
+                                     kq_hip_sampling_result *result,
+                                     kq_diagnostic *diagnostic);
+
+/* The LM head and the sampler in one call, the logits never leaving the
+ * device (the sampled counterpart of kq_hip_lm_head_greedy_f32, for one
+ * hidden state): device_logits [vocab] receives W_lm h, then the sampler
+ * runs on it as kq_hip_sampling_select_f32. vocab must equal the
+ * config's vocabulary. */
+kq_status kq_hip_lm_head_sample_f32(kq_hip_context *context,
+                                    const kq_hip_sampling_config *config,
+                                    kq_hip_sampling_rng_state *state,
+                                    uint32_t type_id, const void *device_weights,
+                                    uint64_t vocab, uint64_t columns,
+                                    const float *device_hidden, float *device_logits,
+                                    void *device_scratch, uint64_t scratch_bytes,
+                                    kq_hip_sampling_result *result,
+                                    kq_diagnostic *diagnostic);
+
+/* kq_sampling_copy_work_for_test (src/kq_sampling.c:474-505): the last
+ * select's processed logits (scores) and final probabilities by id, copied
+ * from the device scratch to host arrays of output_capacity >= the
+ * vocabulary entries each. */
+kq_status kq_hip_sampling_copy_work(kq_hip_context *context,
+                                    const kq_hip_sampling_config *config,
+                                    const void *device_scratch, uint64_t scratch_bytes,
+                                    float *scores, float *probabilities,
+                                    uint64_t output_capacity, kq_diagnostic *diagnostic);
+
 #ifdef __cplusplus
 }
 #endif

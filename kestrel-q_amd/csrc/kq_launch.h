@@ -175,6 +175,15 @@ hipError_t kq_launch_moe_route_finish(const float *logits, const float *shared_l
                                       uint32_t *order, float *shared_scale, uint32_t *status,
                                       hipStream_t stream);
 
+/* GDN canonical-order copies (kq_layout.hip): `units` units of unit_bytes
+ * (even) gathered from physical into canonical order; rows (columns == 0):
+ * unit j <- j below prefix, else prefix + grouped_to_tiled(j - prefix,
+ * width); columns: 128-column unit u of each row of units_per_row (48)
+ * <- unit (u % 3) * 16 + u / 3 */
+hipError_t kq_launch_gdn_gather(const void *physical, void *canonical, uint64_t units,
+                                uint32_t unit_bytes, int columns, uint64_t prefix, uint32_t width,
+                                uint32_t units_per_row, hipStream_t s);
+
 /* MoE on F32 expert weights in the reference's order (kq_moe_f32.hip) */
 typedef struct kq_launch_moe_f32_weights {
     const float *router;             /* [experts][hidden] */
@@ -199,6 +208,50 @@ hipError_t kq_launch_moe_f32(const kq_launch_moe_dims *d, const kq_launch_moe_f3
                              const float *hidden, uint32_t tokens,
                              const kq_launch_moe_f32_ws *ws, float *out, uint32_t *status,
                              hipStream_t s);
+
+/* The token sampler (kq_sample.hip). status: the first failure, in the
+ * reference's order of checks: a numeric failure before the RNG draw, one
+ * inside the categorical walk, or a selected id at or past the canonical
+ * token count (the record is filled in that case too). */
+enum {
+    KQ_SAMPLE_OK = 0,
+    KQ_SAMPLE_NUMERIC_BEFORE_DRAW = 1,
+    KQ_SAMPLE_NUMERIC_IN_DRAW = 2,
+    KQ_SAMPLE_INVALID_TOKEN = 3
+};
+
+typedef struct kq_launch_sample_out {
+    uint32_t status;
+    uint32_t selected;
+    uint32_t top_k_retained;
+    uint32_t retained;
+    float selected_probability;
+    float maximum_probability;
+    float normalized_sum;
+    uint32_t reserved;
+    double uniform;
+} kq_launch_sample_out;
+
+typedef struct kq_launch_sample_args {
+    const float *logits; /* [count] */
+    uint32_t count;      /* vocabulary */
+    uint32_t canonical;  /* ids at or past this are padding */
+    uint32_t top_k;      /* 0: off */
+    float temperature;
+    float top_p;
+    uint32_t word;       /* the RNG word of this draw */
+    /* device work arrays of count entries each */
+    float *scores;
+    uint32_t *keys, *ids, *sorted_keys, *sorted_ids;
+    float *probs;
+    uint32_t *bad_per_block; /* ceil(count / 256) */
+    void *sort_temp;
+    size_t sort_bytes;   /* kq_launch_sample_sort_bytes(count) */
+    kq_launch_sample_out *out;
+} kq_launch_sample_args;
+
+hipError_t kq_launch_sample_sort_bytes(uint32_t count, size_t *bytes);
+hipError_t kq_launch_sample(const kq_launch_sample_args *args, hipStream_t s);
 
 #ifdef __cplusplus
 }

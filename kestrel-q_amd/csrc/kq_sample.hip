@@ -1,0 +1,452 @@
+/*
+ * kq_sample.hip — the token sampler on the device: temperature, top-k,
+ * top-p and the categorical draw of src/kq_sampling.c:576-772, with the
+ * same ids, the same RNG word and the same float bits.
+ *
+ * The reference's sums are sequential binary32 (binary64 for the draw) in a
+ * fixed order, so they are replayed here in that order, on one wave: the
+ * lanes load and exponentiate 64 terms at once, then the wave adds them one
+ * after another through v_readlane (every lane holds the same running sum).
+ * Everything that does not depend on the order runs wide:
+ *
+ *   sample_prep   (grid over the vocabulary) scores = logits / temperature,
+ *                 the finiteness flag per workgroup, order-preserving u32
+ *                 keys (-0 folded onto +0, which compares equal), ids, and
+ *                 the by-id probability array cleared;
+ *   sort          rocPRIM's radix sort of (key, id) pairs: LSD radix sort is
+ *                 stable, so equal scores stay in ascending id order, the
+ *                 reference's (score, id) order (src/kq_sampling.c:276-331);
+ *   sample_tail   one workgroup: the top-k threshold by binary search in the
+ *                 sorted keys, the softmax mass in ascending-score order, the
+ *                 top-p walk from the low end, the kept ids' mass again in id
+ *                 order (an LDS sort of the kept ids when they fit, else a
+ *                 walk over the by-id array), the normalisation, and the
+ *                 categorical walk in binary64.
+ *
+ * Adding +0 to a running sum of non-negative terms leaves it unchanged, so
+ * walks over the by-id array may add the zeros of dropped ids: the result
+ * is the reference's sum over the kept ids only.
+ */
+#include <rocprim/device/device_radix_sort.hpp>
+
+#include "kq_device.h"
+#include "kq_launch.h"
+
+namespace {
+
+constexpr int kPrepThreads = 256;
+constexpr int kTailThreads = 1024;
+constexpr uint32_t kKeptCap = 4096; /* kept ids sorted in LDS up to this many */
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ __launch_bounds__(kPrepThreads) void sample_prep(
+    const float *__restrict__ logits, uint32_t count, float temperature, float *__restrict__ scores,
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ ids, float *__restrict__ probs,
+    uint32_t *__restrict__ bad_per_block) {
+    __shared__ uint32_t any;
+    if (threadIdx.x == 0) any = 0u;
+    __syncthreads();
+    const uint32_t i = blockIdx.x * kPrepThreads + threadIdx.x;
+    if (i < count) {
+        float v = logits[i];
+        bool bad = !kq_isfinite(v);
+        if (temperature != 1.0f) {
+            v = v / temperature;
+            bad = bad || !kq_isfinite(v);
+        }
+        scores[i] = v;
+        keys[i] = order_key(v);
+        ids[i] = i;
+        probs[i] = 0.0f;
+        if (bad) any = 1u; /* benign race: every writer stores 1 */
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) bad_per_block[blockIdx.x] = any;
+}
+
+/* the sampler's device result record (host mirror in kq_launch.h) */
+using Out = kq_launch_sample_out;
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+__device__ __forceinline__ double lane_d(double v, int l) {
+    const int64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const int hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)b >> 32), l);
+    return __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+/* s + v[lane 0] + v[lane 1] + ... + v[lane 63], each sum rounded */
+__device__ __forceinline__ float chain_f(float s, float v) {
+#pragma unroll
+    for (int l = 0; l < 64; ++l) s = s + lane_f(v, l);
+    return s;
+}
+
+__device__ __forceinline__ double chain_d(double s, double v) {
+#pragma unroll
+    for (int l = 0; l < 64; ++l) s = s + lane_d(v, l);
+    return s;
+}
+
+/* the categorical draw (src/kq_sampling.c:400-447) on one wave: uniform =
+ * word / 2^32, threshold = uniform * total, the first kept id whose
+ * binary64 running sum exceeds the threshold (walk), else the last kept id
+ * while the threshold is below the total; lane 0 writes the record */
+template <class Walk>
+__device__ __forceinline__ void draw(Out *o, double total, uint32_t last, float last_p,
+                                     uint32_t word, Walk walk, uint32_t top_k_retained,
+                                     uint32_t retained, float maxp, float norm_sum,
+                                     uint32_t canonical) {
+    const uint32_t lane = threadIdx.x % 64u;
+    if (!__builtin_isfinite(total) || !(total > 0.0) || last == 0xffffffffu) {
+        if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_IN_DRAW;
+        return;
+    }
+    const double uniform = (double)word / 4294967296.0;
+    const double thr = uniform * total;
+    uint32_t sel = 0xffffffffu;
+    float selp = 0.0f;
+    walk(thr, sel, selp);
+    if (sel == 0xffffffffu && thr < total) {
+        sel = last;
+        selp = last_p;
+    }
+    if (lane != 0) return;
+    if (sel == 0xffffffffu) {
+        o->status = KQ_SAMPLE_NUMERIC_IN_DRAW;
+        return;
+    }
+    o->selected = sel;
+    o->top_k_retained = top_k_retained;
+    o->retained = retained;
+    o->selected_probability = selp;
+    o->maximum_probability = maxp;
+    o->normalized_sum = norm_sum;
+    o->uniform = uniform;
+    o->status = sel >= canonical ? KQ_SAMPLE_INVALID_TOKEN : KQ_SAMPLE_OK;
+}
+
+struct TailArgs {
+    const float *scores;  /* by id */
+    const uint32_t *skeys; /* ascending */
+    const uint32_t *sids;
+    float *probs; /* by id, cleared by sample_prep */
+    const uint32_t *bad_per_block;
+    uint32_t prep_blocks;
+    uint32_t count;
+    uint32_t canonical;
+    uint32_t top_k;
+    float top_p;
+    uint32_t word;
+    Out *out;
+};
+
+__device__ __forceinline__ void fail(Out *o, uint32_t code) {
+    if (threadIdx.x == 0) o->status = code;
+}
+
+__global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
+    __shared__ uint32_t s_ids[kKeptCap];
+    __shared__ float s_w[kKeptCap];
+    __shared__ uint32_t s_flag;
+    __shared__ float s_max_p[kTailThreads / 64];
+    __shared__ uint32_t s_u[4];
+    __shared__ float s_f[4]; /* [2]: the by-id mass of the wide path */
+    const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;
+    const uint32_t n = a.count;
+    Out *o = a.out;
+
+    if (tid == 0) s_flag = 0u;
+    __syncthreads();
+    for (uint32_t b = tid; b < a.prep_blocks; b += kTailThreads)
+        if (a.bad_per_block[b]) s_flag = 1u;
+    __syncthreads();
+    if (s_flag) return fail(o, KQ_SAMPLE_NUMERIC_BEFORE_DRAW);
+
+    /* top-k: the first sorted position whose key reaches the k-th largest
+     * key (src/kq_sampling.c:660-667) */
+    uint32_t top_start = 0u;
+    if (a.top_k != 0u) {
+        const uint32_t t = a.skeys[n - a.top_k];
+        uint32_t lo = 0u, hi = n - a.top_k; /* first index in [lo, hi] with key >= t */
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2u;
+            if (a.skeys[mid] < t) lo = mid + 1u;
+            else hi = mid;
+        }
+        top_start = lo;
+    }
+    const float maximum = a.scores[a.sids[n - 1u]];
+
+    /* wave 0: the softmax mass over [top_start, n) in ascending order, then
+     * the top-p walk (src/kq_sampling.c:673-697) */
+    if (wave == 0u) {
+        float sum = 0.0f;
+        bool bad = false;
+        for (uint32_t j0 = top_start; j0 < n; j0 += 64u) {
+            const uint32_t j = j0 + lane;
+            float w = 0.0f;
+            if (j < n) {
+                w = kq_expf(a.scores[a.sids[j]] - maximum);
+                bad = bad || !kq_isfinite(w);
+            }
+            sum = chain_f(sum, w);
+        }
+        bad = __ballot(bad) != 0u;
+        uint32_t keep = top_start;
+        if (!bad && kq_isfinite(sum) && sum > 0.0f && a.top_p < 1.0f) {
+            const float cutoff = 1.0f - a.top_p;
+            float c = 0.0f;
+            bool found = false;
+            for (uint32_t j0 = top_start; j0 < n && !found; j0 += 64u) {
+                const uint32_t j = j0 + lane;
+                float p = 0.0f;
+                if (j < n) p = kq_expf(a.scores[a.sids[j]] - maximum) / sum;
+#pragma unroll
+                for (int l = 0; l < 64; ++l) {
+                    c = c + lane_f(p, l);
+                    const uint32_t at = j0 + (uint32_t)l;
+                    if (!found && at < n && (at == n - 1u || c > cutoff)) {
+                        found = true;
+                        keep = at;
+                    }
+                }
+            }
+        }
+        if (lane == 0) {
+            s_u[0] = bad || !kq_isfinite(sum) || !(sum > 0.0f) ? 1u : 0u;
+            s_u[1] = keep;
+        }
+    }
+    __syncthreads();
+    if (s_u[0]) return fail(o, KQ_SAMPLE_NUMERIC_BEFORE_DRAW);
+    const uint32_t keep = s_u[1];
+    const uint32_t kept = n - keep;
+
+    float norm_sum = 0.0f, sum2 = 0.0f;
+    if (kept <= kKeptCap) {
+        /* the kept ids, sorted by id in LDS (bitonic; ids are distinct) */
+        uint32_t m2 = 1u;
+        while (m2 < kept) m2 <<= 1u;
+        for (uint32_t i = tid; i < m2; i += kTailThreads) {
+            if (i < kept) {
+                const uint32_t id = a.sids[keep + i];
+                s_ids[i] = id;
+                s_w[i] = kq_expf(a.scores[id] - maximum);
+            } else {
+                s_ids[i] = 0xffffffffu;
+                s_w[i] = 0.0f;
+            }
+        }
+        __syncthreads();
+        for (uint32_t size = 2u; size <= m2; size <<= 1u) {
+            for (uint32_t stride = size / 2u; stride > 0u; stride >>= 1u) {
+                for (uint32_t i = tid; i < m2 / 2u; i += kTailThreads) {
+                    const uint32_t lo = 2u * i - (i & (stride - 1u));
+                    const uint32_t hi = lo + stride;
+                    const bool up = (lo & size) == 0u;
+                    const uint32_t x = s_ids[lo], y = s_ids[hi];
+                    if ((x > y) == up) {
+                        const float wx = s_w[lo];
+                        s_ids[lo] = y;
+                        s_ids[hi] = x;
+                        s_w[lo] = s_w[hi];
+                        s_w[hi] = wx;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        /* the mass again in id order, the normalisation, and the draw
+         * (src/kq_sampling.c:701-760, :400-447) */
+        if (wave == 0u) {
+            bool bad = false;
+            float maxp = 0.0f;
+            for (uint32_t i0 = 0u; i0 < kept; i0 += 64u) {
+                const uint32_t i = i0 + lane;
+                sum2 = chain_f(sum2, i < kept ? s_w[i] : 0.0f);
+            }
+            if (kq_isfinite(sum2) && sum2 > 0.0f) {
+                for (uint32_t i0 = 0u; i0 < kept; i0 += 64u) {
+                    const uint32_t i = i0 + lane;
+                    float p = 0.0f;
+                    if (i < kept && s_w[i] > 0.0f) {
+                        p = s_w[i] / sum2;
+                        bad = bad || !kq_isfinite(p);
+                        a.probs[s_ids[i]] = p;
+                    }
+                    if (i < kept) s_w[i] = p;
+                    norm_sum = chain_f(norm_sum, p);
+                    maxp = fmaxf(maxp, p);
+                }
+                for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
+                bad = __ballot(bad) != 0u;
+            } else {
+                bad = true;
+            }
+            if (!bad && (!kq_isfinite(norm_sum) || !(norm_sum > 0.0f))) bad = true;
+            if (bad) {
+                if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_BEFORE_DRAW;
+            } else {
+                double total = 0.0;
+                uint32_t last = 0xffffffffu;
+                float last_p = 0.0f;
+                for (uint32_t i0 = 0u; i0 < kept; i0 += 64u) {
+                    const uint32_t i = i0 + lane;
+                    const float p = i < kept ? s_w[i] : 0.0f;
+                    total = chain_d(total, (double)p);
+                    const uint64_t has = __ballot(p > 0.0f);
+                    if (has) {
+                        const int hl = 63 - __builtin_clzll(has);
+                        last = s_ids[i0 + (uint32_t)hl];
+                        last_p = lane_f(p, hl);
+                    }
+                }
+                draw(o, total, last, last_p, a.word, [&](double thr, uint32_t &sel, float &selp) {
+                    double cum = 0.0;
+                    for (uint32_t i0 = 0u; i0 < kept && sel == 0xffffffffu; i0 += 64u) {
+                        const uint32_t i = i0 + lane;
+                        const float p = i < kept ? s_w[i] : 0.0f;
+                        const double pd = (double)p;
+#pragma unroll
+                        for (int l = 0; l < 64; ++l) {
+                            cum = cum + lane_d(pd, l);
+                            const float pl = lane_f(p, l);
+                            if (sel == 0xffffffffu && pl > 0.0f && thr < cum) {
+                                sel = s_ids[i0 + (uint32_t)l];
+                                selp = pl;
+                            }
+                        }
+                    }
+                }, n - top_start, kept, maxp, norm_sum, a.canonical);
+            }
+        }
+        return;
+    }
+
+    /* many kept ids: weights scattered into the by-id array, then walks over
+     * the whole vocabulary in id order */
+    for (uint32_t j = keep + tid; j < n; j += kTailThreads) {
+        const uint32_t id = a.sids[j];
+        a.probs[id] = kq_expf(a.scores[id] - maximum);
+    }
+    __syncthreads();
+    if (wave == 0u) {
+        for (uint32_t i0 = 0u; i0 < n; i0 += 64u) {
+            const uint32_t i = i0 + lane;
+            sum2 = chain_f(sum2, i < n ? a.probs[i] : 0.0f);
+        }
+        if (lane == 0) s_f[2] = sum2;
+    }
+    __syncthreads();
+    sum2 = s_f[2];
+    if (!kq_isfinite(sum2) || !(sum2 > 0.0f)) return fail(o, KQ_SAMPLE_NUMERIC_BEFORE_DRAW);
+    {
+        float maxp = 0.0f;
+        bool bad = false;
+        for (uint32_t i = tid; i < n; i += kTailThreads) {
+            const float w = a.probs[i];
+            if (w > 0.0f) {
+                const float p = w / sum2;
+                bad = bad || !kq_isfinite(p);
+                a.probs[i] = p;
+                maxp = fmaxf(maxp, p);
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
+        bad = __ballot(bad) != 0u;
+        if (lane == 0) s_max_p[wave] = bad ? -1.0f : maxp;
+    }
+    __syncthreads();
+    if (wave == 0u) {
+        float maxp = lane < kTailThreads / 64u ? s_max_p[lane] : 0.0f;
+        bool bad = __ballot(maxp < 0.0f) != 0u;
+        for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
+        for (uint32_t i0 = 0u; i0 < n; i0 += 64u) {
+            const uint32_t i = i0 + lane;
+            norm_sum = chain_f(norm_sum, i < n ? a.probs[i] : 0.0f);
+        }
+        if (bad || !kq_isfinite(norm_sum) || !(norm_sum > 0.0f)) {
+            if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_BEFORE_DRAW;
+            return;
+        }
+        double total = 0.0;
+        uint32_t last = 0xffffffffu;
+        float last_p = 0.0f;
+        for (uint32_t i0 = 0u; i0 < n; i0 += 64u) {
+            const uint32_t i = i0 + lane;
+            const float p = i < n ? a.probs[i] : 0.0f;
+            total = chain_d(total, (double)p);
+            const uint64_t has = __ballot(p > 0.0f);
+            if (has) {
+                const int hl = 63 - __builtin_clzll(has);
+                last = i0 + (uint32_t)hl;
+                last_p = lane_f(p, hl);
+            }
+        }
+        draw(o, total, last, last_p, a.word, [&](double thr, uint32_t &sel, float &selp) {
+            double cum = 0.0;
+            for (uint32_t i0 = 0u; i0 < n && sel == 0xffffffffu; i0 += 64u) {
+                const uint32_t i = i0 + lane;
+                const float p = i < n ? a.probs[i] : 0.0f;
+                const double pd = (double)p;
+#pragma unroll
+                for (int l = 0; l < 64; ++l) {
+                    cum = cum + lane_d(pd, l);
+                    const float pl = lane_f(p, l);
+                    if (sel == 0xffffffffu && pl > 0.0f && thr < cum) {
+                        sel = i0 + (uint32_t)l;
+                        selp = pl;
+                    }
+                }
+            }
+        }, n - top_start, kept, maxp, norm_sum, a.canonical);
+    }
+}
+
+}  // namespace
+
+extern "C" hipError_t kq_launch_sample_sort_bytes(uint32_t count, size_t *bytes) {
+    size_t b = 0;
+    hipError_t e = rocprim::radix_sort_pairs((void *)nullptr, b, (const uint32_t *)nullptr,
+                                             (uint32_t *)nullptr, (const uint32_t *)nullptr,
+                                             (uint32_t *)nullptr, count, 0u, 32u, (hipStream_t)0);
+    *bytes = b;
+    return e;
+}
+
+extern "C" hipError_t kq_launch_sample(const kq_launch_sample_args *p, hipStream_t s) {
+    const uint32_t n = p->count;
+    if (n == 0u || p->top_k > n) return hipErrorInvalidValue;
+    const uint32_t blocks = (n + kPrepThreads - 1u) / kPrepThreads;
+    hipLaunchKernelGGL(sample_prep, dim3(blocks), dim3(kPrepThreads), 0, s, p->logits, n,
+                       p->temperature, p->scores, p->keys, p->ids, p->probs, p->bad_per_block);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    size_t tmp = p->sort_bytes;
+    e = rocprim::radix_sort_pairs(p->sort_temp, tmp, p->keys, p->sorted_keys, p->ids,
+                                  p->sorted_ids, n, 0u, 32u, s);
+    if (e != hipSuccess) return e;
+    TailArgs a;
+    a.scores = p->scores;
+    a.skeys = p->sorted_keys;
+    a.sids = p->sorted_ids;
+    a.probs = p->probs;
+    a.bad_per_block = p->bad_per_block;
+    a.prep_blocks = blocks;
+    a.count = n;
+    a.canonical = p->canonical;
+    a.top_k = p->top_k;
+    a.top_p = p->top_p;
+    a.word = p->word;
+    a.out = p->out;
+    hipLaunchKernelGGL(sample_tail, dim3(1), dim3(kTailThreads), 0, s, a);
+    return hipGetLastError();
+}

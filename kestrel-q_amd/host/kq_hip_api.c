@@ -195,6 +195,19 @@ kq_status kq_hip_context_synchronize(kq_hip_context *c, kq_diagnostic *diag) {
     return drain(c, diag);
 }
 
+kq_status kqi_context_begin(kq_hip_context *c, kq_diagnostic *diag) {
+    if (!ctx_ok(c)) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "valid context is required");
+    return set_device(c, diag);
+}
+
+void *kqi_context_stream_ptr(const kq_hip_context *c) { return (void *)c->stream; }
+
+kq_status kqi_context_drain(kq_hip_context *c, kq_diagnostic *diag) { return drain(c, diag); }
+
+kq_status kqi_hip_fail(kq_diagnostic *diag, int e, const char *what) {
+    return hip_fail(diag, (hipError_t)e, what);
+}
+
 void *kq_hip_context_stream(const kq_hip_context *c) {
     return c == NULL ? NULL : (void *)c->stream;
 }
@@ -861,6 +874,16 @@ static kq_status lm_head(kq_hip_context *c, uint32_t type_id, const void *w, uin
     e = enqueue_matvec(c, type_id, w, vocab, cols, h, batch, logits, pv, pi, nparts);
     if (e == hipSuccess) e = kq_launch_argmax_from_parts(pv, pi, nparts, batch, ids, c->stream);
     return finish(c, e, "lm head launch", diag);
+}
+
+kq_status kqi_enqueue_logits(kq_hip_context *c, uint32_t type_id, const void *w, uint64_t vocab,
+                             uint64_t cols, const float *h, float *logits, kq_diagnostic *diag) {
+    kq_status st = validate_matvec(c, type_id, w, vocab, cols, h, 1u, logits, vocab, diag);
+    if (st != KQ_STATUS_OK) return st;
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    hipError_t e = enqueue_matvec(c, type_id, w, vocab, cols, h, 1u, logits, NULL, NULL, 0u);
+    return e == hipSuccess ? KQ_STATUS_OK : hip_fail(diag, e, "lm head launch");
 }
 
 kq_status kq_hip_lm_head_greedy_f32(kq_hip_context *c, uint32_t type_id, const void *w,

@@ -130,6 +130,29 @@ PHYSICAL_ORDER, CANONICAL_ORDER = 0, 1
 GDN = {"none": 0, "qkv": 1, "gate": 2, "alpha": 3, "beta": 4, "conv": 5, "out": 6}
 
 
+class SamplingPolicy(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("flags", C.c_uint32), ("temperature", C.c_float),
+                ("top_p", C.c_float), ("top_k", C.c_uint32), ("reserved", C.c_uint32 * 3)]
+
+
+class RngState(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("reserved", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("seed", "stream", "state", "increment", "draws", "integrity")]
+
+
+class SamplingResult(C.Structure):
+    _fields_ = [("selected_token_id", C.c_uint32), ("top_k_retained_count", C.c_uint32),
+                ("retained_count", C.c_uint32), ("rng_word", C.c_uint32),
+                ("selected_probability", C.c_float), ("maximum_probability", C.c_float),
+                ("normalized_sum_f32", C.c_float), ("reserved", C.c_uint32),
+                ("uniform_value", C.c_double), ("rng_draws_before", C.c_uint64),
+                ("rng_draws_after", C.c_uint64)]
+
+
+QWEN38_VOCAB, QWEN38_CANONICAL = 248320, 248077
+SAMPLING_DEFAULT_STREAM = 0x4B515F53414D504C
+
+
 class StringView(C.Structure):
     _fields_ = [("data", C.c_void_p), ("length", C.c_uint64)]
 
@@ -276,6 +299,23 @@ SIGNATURES = {
                                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_uint64, C.c_void_p]),
     "kq_hip_f32_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
+    "kq_hip_sampling_policy_qwen38_default": (None, [_P]),
+    "kq_hip_sampling_config_open_qwen38": (C.c_int, [_P, _P, _P]),
+    "kq_hip_sampling_config_open": (C.c_int, [_P, C.c_uint32, C.c_uint32, _P, _P]),
+    "kq_hip_sampling_config_close": (None, [_P]),
+    "kq_hip_sampling_config_owned_bytes": (C.c_uint64, [_P]),
+    "kq_hip_sampling_config_vocabulary_size": (C.c_uint32, [_P]),
+    "kq_hip_sampling_required_scratch_bytes": (C.c_uint64, [_P]),
+    "kq_hip_sampling_rng_seed": (C.c_int, [C.c_uint64, C.c_uint64, _P, _P]),
+    "kq_hip_sampling_rng_reset": (C.c_int, [_P, _P]),
+    "kq_hip_sampling_rng_snapshot": (C.c_int, [_P, _P, _P]),
+    "kq_hip_sampling_rng_import": (C.c_int, [_P, _P, _P]),
+    "kq_hip_sampling_rng_next_u32": (C.c_int, [_P, _P, _P]),
+    "kq_hip_sampling_select_f32": (C.c_int, [_P, _P, _P, _P, C.c_uint64, _P, C.c_uint64, _P,
+                                             _P]),
+    "kq_hip_lm_head_sample_f32": (C.c_int, [_P, _P, _P, C.c_uint32, _P, C.c_uint64, C.c_uint64,
+                                            _P, _P, _P, C.c_uint64, _P, _P]),
+    "kq_hip_sampling_copy_work": (C.c_int, [_P, _P, _P, C.c_uint64, _P, _P, C.c_uint64, _P]),
     "kq_hip_gr_scratch_bytes": (C.c_uint64, [C.c_void_p, C.c_uint64]),
     "kq_hip_gr_read_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                      C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -407,6 +447,63 @@ class MoeConfig:
             pass
 
 
+def sampling_policy(temperature: float = 1.0, top_p: float = 0.95, top_k: int = 20,
+                    version: int = 1, flags: int = 0, reserved=(0, 0, 0)) -> SamplingPolicy:
+    p = SamplingPolicy()
+    p.version, p.flags, p.temperature, p.top_p, p.top_k = version, flags, temperature, top_p, top_k
+    for i, r in enumerate(reserved):
+        p.reserved[i] = r
+    return p
+
+
+def default_policy() -> SamplingPolicy:
+    p = SamplingPolicy()
+    lib().kq_hip_sampling_policy_qwen38_default(C.byref(p))
+    return p
+
+
+def rng_seed(seed: int, stream: int = SAMPLING_DEFAULT_STREAM) -> RngState:
+    st, d = RngState(), Diagnostic()
+    check(lib().kq_hip_sampling_rng_seed(seed, stream, C.byref(st), C.byref(d)), d)
+    return st
+
+
+def rng_next(state: RngState) -> int:
+    w, d = C.c_uint32(), Diagnostic()
+    check(lib().kq_hip_sampling_rng_next_u32(C.byref(state), C.byref(w), C.byref(d)), d)
+    return w.value
+
+
+class SamplingConfig:
+    """kq_hip_sampling_config: the model's vocabulary by default, or another
+    (vocabulary, canonical) pair."""
+
+    def __init__(self, policy: SamplingPolicy, vocabulary: int | None = None,
+                 canonical: int | None = None):
+        h, d = C.c_void_p(), Diagnostic()
+        if vocabulary is None:
+            check(lib().kq_hip_sampling_config_open_qwen38(C.byref(policy), C.byref(h),
+                                                           C.byref(d)), d)
+        else:
+            check(lib().kq_hip_sampling_config_open(C.byref(policy), vocabulary, canonical,
+                                                    C.byref(h), C.byref(d)), d)
+        self.handle = h.value
+        self.vocabulary = lib().kq_hip_sampling_config_vocabulary_size(C.c_void_p(self.handle))
+        self.scratch_bytes = lib().kq_hip_sampling_required_scratch_bytes(
+            C.c_void_p(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().kq_hip_sampling_config_close(C.c_void_p(self.handle))
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Context:
     def __init__(self, device: int = 0):
         h, d = C.c_void_p(), Diagnostic()
@@ -518,6 +615,33 @@ class Context:
             lib().kq_hip_lm_head_greedy_f32
         check(fn(self._h, type_id, self._p(w), vocab, cols, self._p(h), batch, self._p(logits),
                  self._p(ids), C.byref(d)), d)
+
+    def sample(self, cfg: SamplingConfig, state: RngState, logits, scratch,
+               scratch_bytes: int | None = None) -> SamplingResult:
+        r, d = SamplingResult(), Diagnostic()
+        nb = cfg.scratch_bytes if scratch_bytes is None else scratch_bytes
+        check(lib().kq_hip_sampling_select_f32(self._h, C.c_void_p(cfg.handle), C.byref(state),
+                                               self._p(logits), cfg.vocabulary,
+                                               self._p(scratch), nb, C.byref(r), C.byref(d)), d)
+        return r
+
+    def lm_head_sample(self, cfg: SamplingConfig, state: RngState, type_id: int, w, vocab: int,
+                       cols: int, h, logits, scratch) -> SamplingResult:
+        r, d = SamplingResult(), Diagnostic()
+        check(lib().kq_hip_lm_head_sample_f32(self._h, C.c_void_p(cfg.handle), C.byref(state),
+                                              type_id, self._p(w), vocab, cols, self._p(h),
+                                              self._p(logits), self._p(scratch),
+                                              cfg.scratch_bytes, C.byref(r), C.byref(d)), d)
+        return r
+
+    def sampling_work(self, cfg: SamplingConfig, scratch) -> tuple[np.ndarray, np.ndarray]:
+        sc = np.empty(cfg.vocabulary, np.float32)
+        pr = np.empty(cfg.vocabulary, np.float32)
+        d = Diagnostic()
+        check(lib().kq_hip_sampling_copy_work(self._h, C.c_void_p(cfg.handle), self._p(scratch),
+                                              cfg.scratch_bytes, sc.ctypes.data, pr.ctypes.data,
+                                              cfg.vocabulary, C.byref(d)), d)
+        return sc, pr
 
     def expf(self, x, count: int, out) -> None:
         d = Diagnostic()
