@@ -594,6 +594,8 @@ def main() -> int:
             lambda: wl_sample(ctx, {"temperature": 1.0, "top_k": 20, "top_p": 0.95}, 5,
                               max(10, K // 4), lm=("Q8_0", 2560)))
         run("moe_prefill_512", lambda: wl_moe(ctx, 512, 2, max(3, K // 20), graph, cache))
+        run("moe_prefill_512_2560x640",
+            lambda: wl_moe(ctx, 512, 1, max(3, K // 40), graph, cache, "2560x640"))
         run("moe_decode_1tok_2560x640",
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))
         run("moe_block_decode_1tok_4x2560",

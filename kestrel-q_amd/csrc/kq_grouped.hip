@@ -93,7 +93,9 @@ struct Fmt;
  * 64g + 8s .. +7, low nibbles for s < 4, high nibbles for s >= 4. */
 template <>
 struct Fmt<KQ_LAUNCH_Q4_K> {
-    static constexpr uint32_t kBytes = 144u;
+    static constexpr uint32_t kUnit = 256u;       /* columns per pass iteration */
+    static constexpr uint32_t kUnitBytes = 144u;
+    static constexpr bool kSums = true;           /* 32-column activation sums */
     static constexpr bool kK32 = true; /* 16x16x32 steps, b128 activation reads */
     struct Raw {
         uint4 hd, qa, qb;
@@ -118,6 +120,9 @@ struct Fmt<KQ_LAUNCH_Q4_K> {
 template <>
 struct Fmt<KQ_LAUNCH_Q6_K> {
     static constexpr uint32_t kBytes = 210u;
+    static constexpr uint32_t kUnit = 256u;
+    static constexpr uint32_t kUnitBytes = 210u;
+    static constexpr bool kSums = false;
     static constexpr bool kK32 = false;
     struct Raw {
         kq_u32x2 w[4][3]; /* [n * 2 + h][ql A, ql B, qh] */
@@ -146,6 +151,63 @@ struct Fmt<KQ_LAUNCH_Q6_K> {
     }
 };
 
+/* Q8_0: 34 B per 32 columns (f16 d, 32 int8 codes; src/kq_numeric.c:
+ * 176-196). An iteration takes four blocks (128 columns); each block is one
+ * 16x16x32 step, lane k-group g holding its columns 8g .. 8g + 7, i.e. code
+ * bytes 2 + 8g .. 9 + 8g. Blocks start at 2 mod 4 in a unit (34 B apart),
+ * so the codes of even blocks come from a 12-byte window re-aligned by two
+ * bytes; the scale is half of an aligned dword. Rows are whole units of
+ * 136 B, so a unit starts 4-byte aligned. */
+template <>
+struct Fmt<KQ_LAUNCH_Q8_0> {
+    static constexpr uint32_t kUnit = 128u;
+    static constexpr uint32_t kUnitBytes = 136u;
+    static constexpr bool kSums = false;
+    static constexpr bool kK32 = true;
+    struct Raw {
+        kq_u32x3 c[4]; /* code windows of the four blocks */
+        uint32_t d[4]; /* dwords holding the scales */
+    };
+    __device__ static __forceinline__ Raw load(KqBuf w, uint32_t uoff, uint32_t g) {
+        Raw r;
+#pragma unroll
+        for (uint32_t bb = 0; bb < 4u; ++bb) {
+            const uint32_t a = uoff + 34u * bb + 2u + 8u * g; /* codes */
+            r.c[bb] = kq_ld96(w, a & ~3u, 0u);
+            r.d[bb] = kq_ld32(w, (uoff + 34u * bb) & ~3u, 0u);
+        }
+        return r;
+    }
+};
+
+/* Q5_1: 24 B per 32 columns (f16 d, f16 m, 32 high bits qh, 16 bytes of
+ * nibbles: low nibble of byte i = element i, high = element i + 16, bit i
+ * of qh = bit 4 of element i; src/kq_numeric.c:197-222). Four blocks per
+ * iteration (96 B); lane k-group g holds elements 8g .. 8g + 7: nibbles of
+ * bytes 8(g & 1) .. +7 (low for g < 2, high otherwise) and qh byte g. */
+template <>
+struct Fmt<KQ_LAUNCH_Q5_1> {
+    static constexpr uint32_t kUnit = 128u;
+    static constexpr uint32_t kUnitBytes = 96u;
+    static constexpr bool kSums = true;
+    static constexpr bool kK32 = true;
+    struct Raw {
+        kq_u32x2 q[4];
+        uint32_t dm[4], qh[4];
+    };
+    __device__ static __forceinline__ Raw load(KqBuf w, uint32_t uoff, uint32_t g) {
+        Raw r;
+#pragma unroll
+        for (uint32_t bb = 0; bb < 4u; ++bb) {
+            const uint32_t o = uoff + 24u * bb;
+            r.dm[bb] = kq_ld32(w, o, 0u);
+            r.qh[bb] = kq_ld32(w, o + 4u, 0u);
+            r.q[bb] = kq_ld64(w, o + 8u + 8u * (g & 1u), 0u);
+        }
+        return r;
+    }
+};
+
 /* ------------------------------------------------------------------ */
 /* LDS image of one M-chunk of activations */
 
@@ -157,7 +219,7 @@ struct Stage {
     static constexpr uint32_t kPitch = KDIM + (Fmt<FMT>::kK32 ? 8u : 4u);
     static constexpr uint32_t kSub = KDIM / 32u; /* Q4_K sub-blocks per row */
     static constexpr uint32_t kSxPitch = kSub + 8u;
-    static constexpr bool kSums = FMT == KQ_LAUNCH_Q4_K;
+    static constexpr bool kSums = Fmt<FMT>::kSums;
     __align__(16) _Float16 xh[kTile * kPitch];
     __align__(16) _Float16 xl[kTile * kPitch];
     __align__(16) _Float16 sxh[kSums ? kTile * kSxPitch : 4];
@@ -165,26 +227,30 @@ struct Stage {
     int sig[kTile];
 };
 
-/* Stage rows src_row[i] (or zeros where negative) of X [*, KDIM]: scale by
- * 2^sig (largest magnitude into [2^14, 2^15)), split into fp16 hi + lo and,
- * for Q4_K, form the 32-column sums of the scaled row times 2^-5 (so they
- * fit fp16), also split. One wave per row; lane l holds the float4 column
+/* Stage columns col0 .. col0 + KSL - 1 of rows src_row[i] (or zeros where
+ * negative) of X [*, KDIM]: scale by 2^sig (the row's largest magnitude,
+ * over all KDIM columns, into [2^14, 2^15), so every slice of a row gets
+ * the same scale), split into fp16 hi + lo and, for formats with a min
+ * term, form the 32-column sums of the scaled row times 2^-5 (so they fit
+ * fp16), also split. One wave per row; lane l holds the float4 column
  * groups l, l + 64, ..., so that both the global reads and the LDS writes
  * of a wave are contiguous (no bank conflicts). Returns true if a
- * non-finite input was seen. */
-template <uint32_t FMT, uint32_t KDIM>
-__device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
-                           const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
-    using S = Stage<FMT, KDIM>;
-    constexpr uint32_t NQ = KDIM / 256u; /* float4 groups per lane: 1 .. 8 */
+ * non-finite input was seen. col0 and KSL are multiples of 32. */
+template <uint32_t FMT, uint32_t KDIM, uint32_t KSL>
+__device__ bool stage_slice(Stage<FMT, KSL> &st, const float *__restrict__ X, uint32_t col0,
+                            const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
+    using S = Stage<FMT, KSL>;
+    constexpr uint32_t NQ = (KDIM + 255u) / 256u; /* float4 groups per lane: 1 .. 10 */
     bool bad = false;
     for (uint32_t i = wave; i < kTile; i += nwaves) {
         const int src = src_row[i];
         const float4 *p = (const float4 *)(X + (size_t)(src < 0 ? 0 : src) * KDIM) + lane;
         float4 v[NQ];
 #pragma unroll
-        for (uint32_t q = 0; q < NQ; ++q)
-            v[q] = src < 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : p[64u * q];
+        for (uint32_t q = 0; q < NQ; ++q) {
+            const bool in = src >= 0 && 256u * q + 4u * lane < KDIM;
+            v[q] = in ? p[64u * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         float m = 0.0f;
         bool nf = false;
 #pragma unroll
@@ -200,10 +266,10 @@ __device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
         /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) lies in [2^14, 2^15) */
         int sig = 0;
         if (!any_nf && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
-        _Float16 *dh = st.xh + i * S::kPitch + 4u * lane;
-        _Float16 *dl = st.xl + i * S::kPitch + 4u * lane;
 #pragma unroll
         for (uint32_t q = 0; q < NQ; ++q) {
+            const uint32_t col = 256u * q + 4u * lane;
+            const bool mine = col >= col0 && col < col0 + KSL;
             const float a[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
             _Float16 hi[4], lo[4];
             float part = 0.0f;
@@ -214,18 +280,20 @@ __device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
                 lo[c] = (_Float16)(xs - (float)hi[c]);
                 part += xs;
             }
-            *(h4 *)(dh + 256u * q) = h4{hi[0], hi[1], hi[2], hi[3]};
-            *(h4 *)(dl + 256u * q) = h4{lo[0], lo[1], lo[2], lo[3]};
+            if (mine) {
+                *(h4 *)(st.xh + i * S::kPitch + (col - col0)) = h4{hi[0], hi[1], hi[2], hi[3]};
+                *(h4 *)(st.xl + i * S::kPitch + (col - col0)) = h4{lo[0], lo[1], lo[2], lo[3]};
+            }
             if constexpr (S::kSums) {
                 /* 32-column sums: 8 consecutive lanes hold one */
                 part += __shfl_xor(part, 1, KQ_WAVE);
                 part += __shfl_xor(part, 2, KQ_WAVE);
                 part += __shfl_xor(part, 4, KQ_WAVE);
-                if ((lane & 7u) == 0u) {
+                if (mine && (lane & 7u) == 0u) {
                     const float s = part * 0.03125f;
                     const _Float16 sh = (_Float16)s;
                     const _Float16 sl = (_Float16)(s - (float)sh);
-                    const uint32_t jsb = (256u * q + 4u * lane) / 32u;
+                    const uint32_t jsb = (col - col0) / 32u;
                     st.sxh[i * S::kSxPitch + jsb] = sh;
                     st.sxl[i * S::kSxPitch + jsb] = sl;
                 }
@@ -234,6 +302,12 @@ __device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
         if (lane == 0u) st.sig[i] = sig;
     }
     return bad;
+}
+
+template <uint32_t FMT, uint32_t KDIM>
+__device__ bool stage_rows(Stage<FMT, KDIM> &st, const float *__restrict__ X,
+                           const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
+    return stage_slice<FMT, KDIM, KDIM>(st, X, 0u, src_row, wave, nwaves, lane);
 }
 
 /* ------------------------------------------------------------------ */
@@ -401,6 +475,102 @@ struct Tile<KQ_LAUNCH_Q6_K, KDIM, NMAT> {
     }
 };
 
+template <uint32_t KSL, int NMAT>
+struct Tile<KQ_LAUNCH_Q8_0, KSL, NMAT> {
+    using F = Fmt<KQ_LAUNCH_Q8_0>;
+    using S = Stage<KQ_LAUNCH_Q8_0, KSL>;
+    using Raw = F::Raw;
+
+    /* iteration b: blocks 4b .. 4b + 3 of the slice, one step each; the
+     * int8 codes enter as fp16 through the offset-binary byte (q + 128) */
+    __device__ static __forceinline__ void block(const Raw (&r)[NMAT], const S &st, uint32_t b,
+                                                 uint32_t i, uint32_t g, f4 (&acc)[NMAT],
+                                                 bool &malformed) {
+        const _Float16 *xh = st.xh + i * S::kPitch + 128u * b + 8u * g;
+        const _Float16 *xl = st.xl + i * S::kPitch + 128u * b + 8u * g;
+        const h2 bias = h2{(_Float16)-1152.0f, (_Float16)-1152.0f}; /* 1024 + 128 */
+#pragma unroll
+        for (uint32_t bb = 0; bb < 4u; ++bb) {
+            const h8 ah = *(const h8 *)(xh + 32u * bb);
+            const h8 al = *(const h8 *)(xl + 32u * bb);
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                const kq_u32x3 wv = r[m].c[bb];
+                /* codes start 2 bytes into the window of even blocks */
+                uint32_t c0 = (bb & 1u) ? wv.x : kq_align2(wv.y, wv.x, 2u);
+                uint32_t c1 = (bb & 1u) ? wv.y : kq_align2(wv.z, wv.y, 2u);
+                c0 ^= 0x80808080u;
+                c1 ^= 0x80808080u;
+                const h2 w0 = bytes_lo(c0) + bias, w1 = bytes_hi(c0) + bias;
+                const h2 w2 = bytes_lo(c1) + bias, w3 = bytes_hi(c1) + bias;
+                const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+                f4 t = {0.f, 0.f, 0.f, 0.f};
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, t, 0, 0, 0);
+                const float d = f16f((bb & 1u) ? r[m].d[bb] >> 16 : r[m].d[bb]);
+                malformed |= !kq_isfinite(d);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[m][k] = fmaf(d, t[k], acc[m][k]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
+template <uint32_t KSL, int NMAT>
+struct Tile<KQ_LAUNCH_Q5_1, KSL, NMAT> {
+    using F = Fmt<KQ_LAUNCH_Q5_1>;
+    using S = Stage<KQ_LAUNCH_Q5_1, KSL>;
+    using Raw = F::Raw;
+
+    /* bit k of x (k < 4) to bit 8k + 4: the fifth bit of four codes */
+    __device__ static __forceinline__ uint32_t spread4(uint32_t x) {
+        return ((x * 0x00204081u) & 0x01010101u) << 4;
+    }
+
+    /* iteration b: blocks 4b .. 4b + 3 of the slice; codes 0..31 are
+     * exact in fp16, d scales the step and m the block's activation sum */
+    __device__ static __forceinline__ void block(const Raw (&r)[NMAT], const S &st, uint32_t b,
+                                                 uint32_t i, uint32_t g, f4 (&acc)[NMAT],
+                                                 bool &malformed) {
+        const _Float16 *xh = st.xh + i * S::kPitch + 128u * b + 8u * g;
+        const _Float16 *xl = st.xl + i * S::kPitch + 128u * b + 8u * g;
+        const h2 bias = h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+#pragma unroll
+        for (uint32_t bb = 0; bb < 4u; ++bb) {
+            const h8 ah = *(const h8 *)(xh + 32u * bb);
+            const h8 al = *(const h8 *)(xl + 32u * bb);
+            /* this lane's four tokens' sums of the block (times 2^-5) */
+            float sx[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t so = (4u * g + q) * S::kSxPitch + 4u * b + bb;
+                sx[q] = (float)st.sxh[so] + (float)st.sxl[so];
+            }
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                const kq_u32x2 qv = r[m].q[bb];
+                const uint32_t shn = g >= 2u ? 4u : 0u;
+                const uint32_t hb = (r[m].qh[bb] >> (8u * g)) & 0xffu;
+                const uint32_t c0 = ((qv.x >> shn) & 0x0f0f0f0fu) | spread4(hb & 15u);
+                const uint32_t c1 = ((qv.y >> shn) & 0x0f0f0f0fu) | spread4(hb >> 4);
+                const h2 w0 = bytes_lo(c0) + bias, w1 = bytes_hi(c0) + bias;
+                const h2 w2 = bytes_lo(c1) + bias, w3 = bytes_hi(c1) + bias;
+                const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+                f4 t = {0.f, 0.f, 0.f, 0.f};
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, t, 0, 0, 0);
+                const float d = f16f(r[m].dm[bb]), mn = f16f(r[m].dm[bb] >> 16);
+                malformed |= !kq_isfinite(d) || !kq_isfinite(mn);
+                const float m32 = mn * 32.0f; /* the sums carry 2^-5 */
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[m][k] = fmaf(d, t[k], fmaf(m32, sx[k], acc[m][k]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
 /* ------------------------------------------------------------------ */
 /* grouped expert pass */
 
@@ -446,23 +616,32 @@ __device__ __forceinline__ Work work_of(uint32_t y, const uint32_t *offsets, uin
  * hardware drops -- so the memory counters the compiler waits on are the
  * same on every path and a wait never drains the prefetch.
  */
-template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW, int TPW, int PD>
+template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW, int TPW, int PD, int KS>
 __global__ __launch_bounds__(NW * 64) void grouped_pass(
     const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
     const uint8_t *__restrict__ SW0, const uint8_t *__restrict__ SW1,
     const float *__restrict__ X, const uint32_t *__restrict__ offsets,
     const uint32_t *__restrict__ perm_tok, uint32_t experts, uint32_t tokens, uint32_t top_k,
-    uint32_t rows, uint32_t shared_chunks, float *__restrict__ out, uint32_t *status) {
+    uint32_t rows, uint32_t shared_chunks, uint32_t ybase, float *__restrict__ out,
+    uint32_t *status) {
+    /* KS slices of KSL columns: the activation image of one slice is staged
+     * at a time (a 2560-column image would not fit the LDS); the
+     * accumulators carry over (one tile per wave then) */
+    constexpr uint32_t KSL = KDIM / (uint32_t)KS;
+    static_assert(KS == 1 || TPW == 1, "sliced passes run one tile per wave");
     using F = Fmt<GFMT>;
-    using S = Stage<GFMT, KDIM>;
-    using T = Tile<GFMT, KDIM, NMAT>;
+    using S = Stage<GFMT, KSL>;
+    using T = Tile<GFMT, KSL, NMAT>;
     using Raw = typename F::Raw;
-    constexpr uint32_t NB = KDIM / 256u;
-    constexpr uint32_t RB = NB * F::kBytes;
+    constexpr uint32_t NB = KDIM / F::kUnit;       /* units of a row */
+    constexpr uint32_t NBS = NB / (uint32_t)KS;    /* units of a slice */
+    static_assert(NBS * (uint32_t)KS == NB && NB * F::kUnit == KDIM, "whole units per slice");
+    constexpr uint32_t RB = NB * F::kUnitBytes;
     __shared__ S st;
     __shared__ int src_row[kTile];
 
-    const Work wk = work_of(blockIdx.y, offsets, experts, tokens, shared_chunks);
+    const uint32_t e = blockIdx.y + ybase;
+    const Work wk = work_of(e, offsets, experts, tokens, shared_chunks);
     if (wk.count == 0u) return;
     /* the wave index is uniform across the wave; saying so keeps the weight
      * buffer descriptors in scalar registers (no per-lane waterfall) */
@@ -470,7 +649,6 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t j = lane & 15u, g = lane >> 4;
     const uint32_t tk = tokens * top_k;
-    const uint32_t e = blockIdx.y;
     /* tile t of this wave starts at row tile_row(t); tiles past the matrix
      * load nothing and store nothing */
     auto tile_row = [&](uint32_t t) { return ((blockIdx.x * TPW + t) * NW + wave) * kTile; };
@@ -483,11 +661,11 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
                                         : (m == 0 ? W0 : W1) + (size_t)e * rows * RB;
         wb[m] = kq_buf(base, wbytes);
     }
-    /* byte offset of block b of tile t for this lane's row, or the buffer
+    /* byte offset of unit u of tile t for this lane's row, or the buffer
      * size (every field read from there is dropped) */
-    auto boff = [&](uint32_t t, uint32_t b) {
+    auto boff = [&](uint32_t t, uint32_t u) {
         const uint32_t r0 = tile_row(t);
-        return (t < (uint32_t)TPW && r0 < rows) ? (r0 + j) * RB + b * F::kBytes : wbytes;
+        return (t < (uint32_t)TPW && r0 < rows) ? (r0 + j) * RB + u * F::kUnitBytes : wbytes;
     };
     auto load = [&](Raw (&r)[NMAT], uint32_t off) {
 #pragma unroll
@@ -498,15 +676,29 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
     const uint32_t obytes = wk.count * rows * 4u;
     const KqBuf ob = kq_buf(out + (size_t)pos0 * rows, obytes);
 
-    /* the wave's iterations are (tile, block) pairs in order; iteration
-     * `it` reads ring slot it % R, which iteration it - PD filled */
-    constexpr uint32_t NIT = (uint32_t)TPW * NB;
+    /* the wave's iterations are (slice, tile, unit of the slice) in order;
+     * iteration `it` reads ring slot it % R, which iteration it - PD filled */
+    constexpr uint32_t PER = (uint32_t)TPW * NBS; /* iterations per slice */
+    constexpr uint32_t NIT = (uint32_t)KS * PER;
     constexpr uint32_t R = (uint32_t)PD + 1u;
-    auto it_off = [&](uint32_t it) { return it < NIT ? boff(it / NB, it % NB) : wbytes; };
+    auto it_off = [&](uint32_t it) {
+        if (it >= NIT) return wbytes;
+        const uint32_t ks = it / PER, rem = it % PER;
+        return boff(rem / NBS, ks * NBS + rem % NBS);
+    };
 
     bool bad = false, badin = false, malformed = false;
+    auto stage = [&](uint32_t ks) {
+        /* a non-finite hidden state is the caller's input; a non-finite
+         * intermediate activation is a numeric failure of the layer */
+        const bool nf = stage_slice<GFMT, KDIM, KSL>(st, X, ks * KSL, src_row, wave, NW, lane);
+        if (NMAT == 2)
+            badin |= nf;
+        else
+            bad |= nf;
+    };
     for (uint32_t c0 = 0; c0 < wk.count; c0 += kTile) {
-        /* the first PD blocks' weights are requested before the staging */
+        /* the first PD units' weights are requested before the staging */
         Raw ring[R][NMAT];
 #pragma unroll
         for (uint32_t it = 0; it < (uint32_t)PD; ++it) load(ring[it], it_off(it));
@@ -524,13 +716,7 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
             src_row[i] = src;
         }
         __syncthreads();
-        /* a non-finite hidden state is the caller's input; a non-finite
-         * intermediate activation is a numeric failure of the layer */
-        const bool nf = stage_rows<GFMT, KDIM>(st, X, src_row, wave, NW, lane);
-        if (NMAT == 2)
-            badin |= nf;
-        else
-            bad |= nf;
+        stage(0u);
         __syncthreads();
 
         f4 acc[NMAT];
@@ -540,15 +726,22 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
 #pragma unroll
             for (uint32_t r = 0; r < R; ++r) {
                 const uint32_t it = it0 + r;
-                const uint32_t t = it / NB, b = it % NB;
-                if (b == 0u) {
+                const uint32_t ks = it / PER, rem = it % PER;
+                const uint32_t t = rem / NBS, b = rem % NBS;
+                if (KS > 1 && ks > 0u && rem == 0u) {
+                    /* the next slice of the activations */
+                    __syncthreads();
+                    stage(ks);
+                    __syncthreads();
+                }
+                if (b == 0u && ks == 0u) {
 #pragma unroll
                     for (int m = 0; m < NMAT; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
                 }
                 load(ring[(r + PD) % R], it_off(it + PD));
                 T::block(ring[r], st, b, j, g, acc, malformed);
                 __builtin_amdgcn_sched_barrier(0);
-                if (b + 1u < NB) continue;
+                if (b + 1u < NBS || ks + 1u < (uint32_t)KS) continue;
                 /* D[token][row]: this lane holds row `row` of tokens 4g .. 4g+3 */
                 const uint32_t row = tile_row(t) + j;
 #pragma unroll
@@ -712,13 +905,15 @@ constexpr uint32_t kSharedChunks = 2; /* 16-token chunks per shared-expert workg
 #define KQ_DN_TPW 4
 #define KQ_DN_PD 1
 #endif
-template <uint32_t KDIM, int NMAT>
+template <uint32_t GFMT, uint32_t KDIM, int NMAT>
 struct Shape {
     static constexpr int NW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_NW : 8) : KQ_DN_NW;
     static constexpr int TPW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_TPW : 2) : KQ_DN_TPW;
+    /* gate/up rows longer than 2048 columns are staged in two slices */
+    static constexpr int KS = NMAT == 2 && KDIM > 2048u ? 2 : 1;
     /* the ring (PD + 1 slots) is a power of two that divides the wave's
-     * TPW * KDIM / 256 iterations */
-    static constexpr int NIT = TPW * (int)(KDIM / 256u);
+     * KS * TPW * KDIM / unit iterations */
+    static constexpr int NIT = TPW * (int)(KDIM / Fmt<GFMT>::kUnit);
     static constexpr int WANT = (NMAT == 2 ? KQ_GU_PD : KQ_DN_PD) + 1;
     static constexpr int RING = WANT >= 8 && NIT % 8 == 0 ? 8
                                 : WANT >= 4 && NIT % 4 == 0 ? 4
@@ -730,54 +925,103 @@ struct Shape {
 template <uint32_t KDIM>
 hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X,
                            const uint32_t *offsets, uint32_t experts, uint32_t tokens,
-                           uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
-                           hipStream_t s);
+                           uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, float *out,
+                           uint32_t *status, hipStream_t s);
 
+/* Workgroup rows y0 .. y0 + ny - 1 of the pass: experts 0 .. E-1, then the
+ * shared expert's chunk groups. */
 template <uint32_t GFMT, uint32_t KDIM, int NMAT>
 hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
                        const uint8_t *SW1, const float *X, const uint32_t *offsets,
                        const uint32_t *perm_tok, uint32_t experts, uint32_t tokens,
-                       uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
-                       hipStream_t s) {
+                       uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, float *out,
+                       uint32_t *status, hipStream_t s) {
+    if (ny == 0u) return hipSuccess;
     /* (an intermediate of 2048 leaves no LDS beside its activation image
      * for the weight slots) */
     if constexpr (GFMT == KQ_LAUNCH_Q6_K && NMAT == 1 && KDIM <= 1024u)
-        return launch_down_q6k<KDIM>(W0, SW0, X, offsets, experts, tokens, top_k, rows, out,
-                                     status, s);
-    constexpr int NW = Shape<KDIM, NMAT>::NW;
-    constexpr int TPW = Shape<KDIM, NMAT>::TPW;
-    constexpr int PD = Shape<KDIM, NMAT>::PD;
+        return launch_down_q6k<KDIM>(W0, SW0, X, offsets, experts, tokens, top_k, rows, y0, ny,
+                                     out, status, s);
+    constexpr int NW = Shape<GFMT, KDIM, NMAT>::NW;
+    constexpr int TPW = Shape<GFMT, KDIM, NMAT>::TPW;
+    constexpr int PD = Shape<GFMT, KDIM, NMAT>::PD;
+    constexpr int KS = Shape<GFMT, KDIM, NMAT>::KS;
     const uint32_t slab = (uint32_t)(NW * TPW) * kTile;
-    const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
-    const dim3 grid((rows + slab - 1u) / slab, experts + sh_wgs);
-    hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW, TPW, PD>), grid, dim3(NW * 64), 0, s,
-                       W0, W1,
-                       SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, rows,
-                       kSharedChunks, out, status);
+    const dim3 grid((rows + slab - 1u) / slab, ny);
+    hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW, TPW, PD, KS>), grid, dim3(NW * 64), 0,
+                       s, W0, W1, SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, rows,
+                       kSharedChunks, y0, out, status);
     return hipGetLastError();
+}
+
+/* the row lengths each format's pass is built for: whole units, and the
+ * activation image of a slice within the LDS */
+template <uint32_t GFMT, int NMAT>
+constexpr bool pass_dim(uint32_t k) {
+    if (k % Fmt<GFMT>::kUnit != 0u) return false;
+    if (NMAT == 2) return k == 256u || k == 512u || k == 1024u || k == 2048u || k == 2560u;
+    return k == 256u || k == 512u || k == 640u || k == 1024u || k == 2048u;
 }
 
 template <uint32_t GFMT, int NMAT>
 hipError_t pass_cols(uint32_t kdim, const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
                      const uint8_t *SW1, const float *X, const uint32_t *offsets,
                      const uint32_t *perm_tok, uint32_t experts, uint32_t tokens, uint32_t top_k,
-                     uint32_t rows, float *out, uint32_t *status, hipStream_t s) {
-#define KQ_PASS(K)                                                                        \
-    launch_pass<GFMT, K, NMAT>(W0, W1, SW0, SW1, X, offsets, perm_tok, experts, tokens, \
-                               top_k, rows, out, status, s)
+                     uint32_t rows, uint32_t y0, uint32_t ny, float *out, uint32_t *status,
+                     hipStream_t s) {
+#define KQ_PASS(K)                                                                               \
+    if constexpr (pass_dim<GFMT, NMAT>(K))                                                       \
+        return launch_pass<GFMT, K, NMAT>(W0, W1, SW0, SW1, X, offsets, perm_tok, experts,       \
+                                          tokens, top_k, rows, y0, ny, out, status, s);          \
+    return hipErrorInvalidValue
     switch (kdim) {
-    case 256: return KQ_PASS(256u);
-    case 512: return KQ_PASS(512u);
-    case 1024: return KQ_PASS(1024u);
-    case 2048: return KQ_PASS(2048u);
+    case 256: { KQ_PASS(256u); }
+    case 512: { KQ_PASS(512u); }
+    case 640: { KQ_PASS(640u); }
+    case 1024: { KQ_PASS(1024u); }
+    case 2048: { KQ_PASS(2048u); }
+    case 2560: { KQ_PASS(2560u); }
     default: return hipErrorInvalidValue;
     }
 #undef KQ_PASS
 }
 
-bool down_type(uint32_t t) { return t == KQ_LAUNCH_Q4_K || t == KQ_LAUNCH_Q6_K; }
+/* pass_dim for a run-time format */
+bool pass_dim_rt(uint32_t type, int nmat, uint32_t k) {
+    switch (type) {
+    case KQ_LAUNCH_Q4_K: return nmat == 2 ? pass_dim<KQ_LAUNCH_Q4_K, 2>(k) : pass_dim<KQ_LAUNCH_Q4_K, 1>(k);
+    case KQ_LAUNCH_Q6_K: return nmat == 1 && pass_dim<KQ_LAUNCH_Q6_K, 1>(k);
+    case KQ_LAUNCH_Q8_0: return nmat == 2 ? pass_dim<KQ_LAUNCH_Q8_0, 2>(k) : pass_dim<KQ_LAUNCH_Q8_0, 1>(k);
+    case KQ_LAUNCH_Q5_1: return nmat == 1 && pass_dim<KQ_LAUNCH_Q5_1, 1>(k);
+    default: return false;
+    }
+}
 
-bool grouped_dim(uint32_t n) { return n == 256u || n == 512u || n == 1024u || n == 2048u; }
+/* one pass of a role whose routed and shared matrices may differ in
+ * format: one launch when they agree, else the routed workgroups and the
+ * shared ones as two launches */
+template <int NMAT>
+hipError_t pass_any(uint32_t type, uint32_t kdim, const uint8_t *W0, const uint8_t *W1,
+                    const uint8_t *SW0, const uint8_t *SW1, const float *X,
+                    const uint32_t *offsets, const uint32_t *perm_tok, uint32_t experts,
+                    uint32_t tokens, uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny,
+                    float *out, uint32_t *status, hipStream_t s) {
+#define KQ_ANY(F)                                                                              \
+    pass_cols<F, NMAT>(kdim, W0, W1, SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, \
+                       rows, y0, ny, out, status, s)
+    switch (type) {
+    case KQ_LAUNCH_Q4_K: return KQ_ANY(KQ_LAUNCH_Q4_K);
+    case KQ_LAUNCH_Q8_0: return KQ_ANY(KQ_LAUNCH_Q8_0);
+    case KQ_LAUNCH_Q6_K:
+        if constexpr (NMAT == 1) return KQ_ANY(KQ_LAUNCH_Q6_K);
+        return hipErrorInvalidValue;
+    case KQ_LAUNCH_Q5_1:
+        if constexpr (NMAT == 1) return KQ_ANY(KQ_LAUNCH_Q5_1);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+#undef KQ_ANY
+}
 
 /* ------------------------------------------------------------------ */
 /* Batched Q6_K matvec on MFMA: y[b] = W x[b] for 2 .. 4 activation columns
@@ -1067,7 +1311,7 @@ template <uint32_t KDIM, int NW, int TPW>
 __global__ __launch_bounds__(NW * 64) void grouped_down_q6k(
     const uint8_t *__restrict__ W0, const uint8_t *__restrict__ SW0,
     const float *__restrict__ X, const uint32_t *__restrict__ offsets, uint32_t experts,
-    uint32_t tokens, uint32_t top_k, uint32_t rows, uint32_t shared_chunks,
+    uint32_t tokens, uint32_t top_k, uint32_t rows, uint32_t shared_chunks, uint32_t ybase,
     float *__restrict__ out, uint32_t *status) {
     using F = Fmt<KQ_LAUNCH_Q6_K>;
     using S = Stage<KQ_LAUNCH_Q6_K, KDIM>;
@@ -1081,13 +1325,13 @@ __global__ __launch_bounds__(NW * 64) void grouped_down_q6k(
     __shared__ int src_row[kTile];
     __shared__ __align__(16) uint8_t slots[NW][2][kMvSlot];
 
-    const Work wk = work_of(blockIdx.y, offsets, experts, tokens, shared_chunks);
+    const uint32_t e = blockIdx.y + ybase;
+    const Work wk = work_of(e, offsets, experts, tokens, shared_chunks);
     if (wk.count == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t j = lane & 15u, g = lane >> 4;
     const uint32_t tk = tokens * top_k;
-    const uint32_t e = blockIdx.y;
     auto tile_row = [&](uint32_t t) { return ((blockIdx.x * TPW + t) * NW + wave) * kTile; };
     const uint32_t wbytes = rows * RB;
     const KqBuf wb = kq_buf(wk.shared ? SW0 : W0 + (size_t)e * rows * RB, wbytes);
@@ -1204,15 +1448,14 @@ __global__ __launch_bounds__(NW * 64) void grouped_down_q6k(
 template <uint32_t KDIM>
 hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X,
                            const uint32_t *offsets, uint32_t experts, uint32_t tokens,
-                           uint32_t top_k, uint32_t rows, float *out, uint32_t *status,
-                           hipStream_t s) {
-    constexpr int NW = Shape<KDIM, 1>::NW;
-    constexpr int TPW = Shape<KDIM, 1>::TPW;
+                           uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, float *out,
+                           uint32_t *status, hipStream_t s) {
+    constexpr int NW = Shape<KQ_LAUNCH_Q6_K, KDIM, 1>::NW;
+    constexpr int TPW = Shape<KQ_LAUNCH_Q6_K, KDIM, 1>::TPW;
     const uint32_t slab = (uint32_t)(NW * TPW) * kTile;
-    const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
-    const dim3 grid((rows + slab - 1u) / slab, experts + sh_wgs);
+    const dim3 grid((rows + slab - 1u) / slab, ny);
     hipLaunchKernelGGL((grouped_down_q6k<KDIM, NW, TPW>), grid, dim3(NW * 64), 0, s, W0, SW0, X,
-                       offsets, experts, tokens, top_k, rows, kSharedChunks, out, status);
+                       offsets, experts, tokens, top_k, rows, kSharedChunks, y0, out, status);
     return hipGetLastError();
 }
 
@@ -1220,12 +1463,14 @@ hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X
 
 extern "C" int kq_launch_moe_grouped_supported(const kq_launch_moe_dims *d,
                                                const kq_launch_moe_weights *w) {
-    /* gate/up in Q4_K (the 6-bit scales fold into exact fp16 weights); down
-     * in Q4_K or Q6_K */
-    return w->gate_type == KQ_LAUNCH_Q4_K && w->up_type == w->gate_type &&
-           w->shared_gate_type == w->gate_type && w->shared_up_type == w->gate_type &&
-           down_type(w->down_type) && w->shared_down_type == w->down_type &&
-           grouped_dim(d->hidden) && grouped_dim(d->inter) && d->inter == d->shared_inter &&
+    /* gate/up in Q4_K (the 6-bit scales fold into exact fp16 weights) or
+     * Q8_0; down in Q4_K, Q6_K, Q5_1 or Q8_0; routed and shared each of
+     * their own format, at the row lengths each pass is built for */
+    return w->up_type == w->gate_type && w->shared_up_type == w->shared_gate_type &&
+           pass_dim_rt(w->gate_type, 2, d->hidden) &&
+           pass_dim_rt(w->shared_gate_type, 2, d->hidden) &&
+           pass_dim_rt(w->down_type, 1, d->inter) &&
+           pass_dim_rt(w->shared_down_type, 1, d->inter) && d->inter == d->shared_inter &&
            d->experts <= 1023u;
 }
 
@@ -1249,18 +1494,35 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     if (e != hipSuccess) return e;
     const uint8_t *g = (const uint8_t *)w->gate, *u = (const uint8_t *)w->up;
     const uint8_t *sg = (const uint8_t *)w->shared_gate, *su = (const uint8_t *)w->shared_up;
-    e = pass_cols<KQ_LAUNCH_Q4_K, 2>(d->hidden, g, u, sg, su, hidden, ws->offsets, ws->perm_tok,
-                                     d->experts, tokens, d->top_k, d->inter, ws->act, status, s);
+    const uint32_t E = d->experts;
+    const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
+    /* gate/up + SwiGLU, then down: the routed experts' workgroups and the
+     * shared expert's in one launch when their formats agree */
+    if (w->shared_gate_type == w->gate_type) {
+        e = pass_any<2>(w->gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets, ws->perm_tok,
+                        E, tokens, d->top_k, d->inter, 0u, E + sh_wgs, ws->act, status, s);
+    } else {
+        e = pass_any<2>(w->gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets, ws->perm_tok,
+                        E, tokens, d->top_k, d->inter, 0u, E, ws->act, status, s);
+        if (e == hipSuccess)
+            e = pass_any<2>(w->shared_gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets,
+                            ws->perm_tok, E, tokens, d->top_k, d->inter, E, sh_wgs, ws->act,
+                            status, s);
+    }
     if (e != hipSuccess) return e;
     const uint8_t *dn = (const uint8_t *)w->down, *sd = (const uint8_t *)w->shared_down;
-    if (w->down_type == KQ_LAUNCH_Q4_K)
-        e = pass_cols<KQ_LAUNCH_Q4_K, 1>(d->inter, dn, nullptr, sd, nullptr, ws->act,
-                                         ws->offsets, ws->perm_tok, d->experts, tokens, d->top_k,
-                                         d->hidden, ws->outp, status, s);
-    else
-        e = pass_cols<KQ_LAUNCH_Q6_K, 1>(d->inter, dn, nullptr, sd, nullptr, ws->act,
-                                         ws->offsets, ws->perm_tok, d->experts, tokens, d->top_k,
-                                         d->hidden, ws->outp, status, s);
+    if (w->shared_down_type == w->down_type) {
+        e = pass_any<1>(w->down_type, d->inter, dn, nullptr, sd, nullptr, ws->act, ws->offsets,
+                        ws->perm_tok, E, tokens, d->top_k, d->hidden, 0u, E + sh_wgs, ws->outp,
+                        status, s);
+    } else {
+        e = pass_any<1>(w->down_type, d->inter, dn, nullptr, sd, nullptr, ws->act, ws->offsets,
+                        ws->perm_tok, E, tokens, d->top_k, d->hidden, 0u, E, ws->outp, status, s);
+        if (e == hipSuccess)
+            e = pass_any<1>(w->shared_down_type, d->inter, dn, nullptr, sd, nullptr, ws->act,
+                            ws->offsets, ws->perm_tok, E, tokens, d->top_k, d->hidden, E, sh_wgs,
+                            ws->outp, status, s);
+    }
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(moe_combine, dim3((d->hidden + 255u) / 256u, tokens), dim3(256), 0, s,
                        ws->outp, ws->pos, ws->order, ws->weights, ws->shared_scale, tokens,

@@ -130,8 +130,7 @@ typedef struct kq_launch_moe_ws {
     float *outp;          /* [tokens * top_k + tokens][hidden]: down outputs */
     double *bound;        /* [experts + 1][2]: exact product sums and the bound on the
                              CPU's sequential sum (certified one-token routing) */
-    uint32_t *certified;  /* 1 when the certified routing produced the ids */
-    uint32_t *arrive;     /* workgroup arrivals of the one-launch exact route */
+    uint32_t *certified;  /* one-token route: 1 certified, 2 refined, 0 exact */
 } kq_launch_moe_ws;
 
 uint32_t kq_launch_moe_experts_padded(uint32_t experts);
@@ -140,15 +139,16 @@ void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tokens, void *
                             kq_launch_moe_ws *ws);
 int kq_launch_moe_supported(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w);
 /* logits (+ shared gate logit), softmax, partial-selection top-k, weights.
- * certify != 0 (one token, only the ids needed exactly): select from exact
+ * certify != 0 (one token, only the ids needed exactly): selects from exact
  * product sums with a proven error bound when the bound separates the
- * selection, falling back to the exact chains otherwise; the logits and
- * probabilities are then not written and the weights are within fp32
- * tolerance of the CPU's. */
+ * selection, from the exact chains of the contenders when that separates
+ * it, and from every exact chain otherwise; the logits and probabilities
+ * are then not always written and the weights are within fp32 tolerance of
+ * the CPU's. ids_out (optional) also receives the ids. */
 hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
                                const float *shared_gate_weight, const float *hidden,
                                uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t *status,
-                               int certify, hipStream_t stream);
+                               int certify, uint32_t *ids_out, hipStream_t stream);
 /* grouped multi-token path (kq_grouped.hip): stable permutation, per-expert
  * MFMA gate/up + SwiGLU and down over all of an expert's tokens, ordered
  * combine; needs the route results in ws */

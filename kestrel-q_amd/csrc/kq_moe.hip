@@ -392,13 +392,13 @@ __device__ __forceinline__ float wave_max(float v) {
  *   flag that makes the exact router and route finish return at once;
  *   otherwise they run and overwrite everything.
  */
-/* Rows of router_bounds: four logit rows per workgroup of 16 waves, four
- * waves per row, each wave a quarter of the columns. */
-constexpr uint32_t kSelRows = 4;
+/* Rows of route_bounds: one logit row per workgroup of four waves, each
+ * wave a quarter of the columns (E + 1 workgroups spread over the CUs). */
+constexpr uint32_t kSelRows = 1;
 constexpr uint32_t kSelParts = 4;
 
 constexpr uint32_t kMaxTopK = 64;
-constexpr uint32_t kCertCand = 64; /* candidates one wave ranks */
+constexpr uint32_t kCertCand = 128; /* candidates one wave ranks, two per lane */
 
 /* hi - bhi exceeds lo + blo by more than the bounds and 16 units in the
  * last place of the probability terms involved (m: the largest a) */
@@ -456,153 +456,18 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return kq_fold32(v, v);
 }
 
-__global__ __launch_bounds__(1024) void route_certify(
-    const double *__restrict__ bound, uint32_t experts, uint32_t top_k,
-    uint32_t *__restrict__ ids, float *__restrict__ weights, uint32_t *__restrict__ order,
-    float *__restrict__ shared_scale, uint32_t *__restrict__ certified) {
-    __shared__ CertCand cmp[kCertCand];
-    __shared__ double cmp_b[kCertCand];
-    __shared__ CertCand srt[kCertCand];
-    __shared__ double srt_b[kCertCand];
-    __shared__ __align__(16) float w_key[16];
-    __shared__ __align__(16) double w_rest[16];
-    __shared__ __align__(16) uint32_t w_bad[16];
-    __shared__ uint32_t s_count;
-    const uint32_t e = threadIdx.x, lane = e & 63u;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(e >> 6);
-    const double ninf = -__builtin_inf();
-    const bool live = e < experts;
-    double sh_b = 0.0;
-    if (w == 0u) sh_b = bound[2u * experts + 1u];
-    if (w == 15u) {
-        /* the shared gate from the fp64 sum; the exact route finish
-         * overwrites it when the selection is not certified */
-        const double sh_a = bound[2u * experts];
-        if (lane == 0u) *shared_scale = 1.0f / (1.0f + fast_expf(-(float)sh_a));
-    }
-    const double ar = live ? bound[2u * e] : ninf;
-    const double b = live ? bound[2u * e + 1u] : 0.0;
-    /* a NaN total comes with an infinite bound; keep it out of the maxima */
-    const double a = ar == ar ? ar : ninf;
-    const float key = (float)a;
-    const uint32_t need = top_k + 1u < experts ? top_k + 1u : experts;
-    const uint32_t ns = experts >= 64u ? experts / 64u : 1u;
-    const uint32_t per = (need + ns - 1u) / ns;
-    if (e == 0u) s_count = 0u;
-    /* 1. */
-    {
-        float m = __builtin_inff();
-        if (w < ns) {
-            float v = key;
-            for (uint32_t r = 0; r < per; ++r) {
-                m = wave_max(v);
-                const uint64_t hit = __ballot(v == m);
-                if (lane == (uint32_t)__builtin_ctzll(hit)) v = -__builtin_inff();
-            }
-        }
-        if (lane == 0u) w_key[w] = m;
-    }
-    __syncthreads();
-    /* 2. */
-    float t = w_key[0];
-#pragma unroll
-    for (uint32_t k = 1; k < 16u; ++k) t = fminf(t, w_key[k]);
-    /* 3. */
-    {
-        const bool c = live && key >= t;
-        const uint64_t cb = __ballot(c);
-        uint32_t at = 0;
-        if (lane == 0u) at = atomicAdd(&s_count, (uint32_t)__popcll(cb));
-        at = __builtin_amdgcn_readfirstlane(at) + bits_below(cb);
-        if (c && at < kCertCand) {
-            cmp[at] = CertCand{a, e, 0u};
-            cmp_b[at] = b;
-        }
-        const double rest_w = kq_wave_max_f64(live && !c ? a + b : ninf);
-        const bool bad_w = __ballot(live && !(b < __builtin_inf())) != 0ull;
-        if (lane == 0u) {
-            w_rest[w] = rest_w;
-            w_bad[w] = bad_w ? 1u : 0u;
-        }
-    }
-    __syncthreads();
-    if (w != 0u) return;
-    /* 4. */
-    const uint32_t total = s_count;
-    double rest = w_rest[0];
-    uint32_t anybad = w_bad[0];
-#pragma unroll
-    for (uint32_t k = 1; k < 16u; ++k) {
-        rest = fmax(rest, w_rest[k]);
-        anybad |= w_bad[k];
-    }
-    if (anybad != 0u || total > kCertCand || !(sh_b < __builtin_inf())) {
-        if (lane == 0u) *certified = 0u;
-        return;
-    }
-    /* places past the list hold entries that never rank above a candidate */
-    if (lane >= total) {
-        cmp[lane] = CertCand{ninf, 0xffffffffu, 0u};
-        cmp_b[lane] = 0.0;
-    }
-    const CertCand mine = cmp[lane];
-    const double mb = cmp_b[lane];
-    uint32_t rank = 0;
-    for (uint32_t j0 = 0; j0 < total; j0 += 8u) {
-        CertCand o[8];
-#pragma unroll
-        for (uint32_t q = 0; q < 8u; ++q) o[q] = cmp[(j0 + q) & (kCertCand - 1u)];
-#pragma unroll
-        for (uint32_t q = 0; q < 8u; ++q)
-            rank += (uint32_t)(o[q].a > mine.a) |
-                    ((uint32_t)(o[q].a == mine.a) & (uint32_t)(o[q].id < mine.id));
-    }
-    const bool have = lane < total;
-    if (have) {
-        srt[rank] = mine;
-        srt_b[rank] = mb;
-    }
-    rest = fmax(rest, kq_wave_max_f64(have && rank >= top_k ? mine.a + mb : ninf));
-    /* 5. adjacent selected pairs, then the last selected against the rest */
-    const uint32_t l1 = lane + 1u < top_k ? lane + 1u : 0u;
-    const CertCand s0 = srt[lane], s1 = srt[l1];
-    const double b0 = srt_b[lane], b1 = srt_b[l1];
-    const double m = kq_readlane_f64(s0.a, 0);
-    const bool pair_ok = lane + 1u >= top_k || certify_sep(s0.a, b0, s1.a, b1, m);
-    bool ok = __ballot(!pair_ok) == 0ull;
-    if (ok && rest > ninf)
-        ok = certify_sep(kq_readlane_f64(s0.a, (int)(top_k - 1u)),
-                         kq_readlane_f64(b0, (int)(top_k - 1u)), rest, 0.0, m);
-    if (lane == 0u) *certified = ok ? 1u : 0u;
-    if (!ok) return; /* the exact kernels run */
-    /* 6. weights p_r / sum of the selected p, p = exp(a - m) (the softmax
-     * denominator cancels); ascending-id rank of each slot */
-    const float ex = lane < top_k ? fast_expf((float)(s0.a - m)) : 0.0f;
-    const float psel = wave_sum_f32(ex);
-    uint32_t rk = 0;
-    for (uint32_t j = 0; j < top_k; ++j)
-        rk += (uint32_t)((uint32_t)__builtin_amdgcn_readlane((int)s0.id, (int)j) < s0.id);
-    if (lane < top_k) {
-        ids[lane] = s0.id;
-        weights[lane] = ex / psel;
-        order[rk] = lane;
-    }
-}
-
 /*
  * Bounds of all logit rows (the shared gate vector as row E).
- * Wave w of a workgroup takes quarter w % 4 of row 4 * blockIdx.x + w / 4;
+ * Wave w of a workgroup takes quarter w % 4 of row kSelRows * blockIdx.x +
+ * w / 4;
  * its lanes hold C consecutive columns each, so the wave's partial sums are
  * the lane's own running sum plus a wave scan, and the row's are those plus
  * the totals of the quarters before it.
  */
 template <uint32_t HIDDEN>
-__global__ __launch_bounds__(1024) void router_bounds(
+__device__ __forceinline__ void bounds_rows(
     const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
-    const float *__restrict__ x, uint32_t experts, double *__restrict__ bound,
-    uint32_t *__restrict__ arrive) {
-    /* the exact fallback's arrival count starts each call at zero */
-    if (blockIdx.x == 0u && threadIdx.x == 0u) *arrive = 0u;
+    const float *__restrict__ x, uint32_t experts, double *__restrict__ bound) {
     constexpr uint32_t PART = HIDDEN / kSelParts;
     constexpr uint32_t C = PART / 64u; /* 1 .. 8 */
     __shared__ double p_tot[16], p_abs[16];
@@ -969,38 +834,352 @@ __global__ __launch_bounds__(1024) void route_finish(
 }
 
 /*
- * The exact one-token route when the certified selection failed, as one
- * launch: every workgroup runs the chains of 8 logit rows, and the
- * workgroup that arrives last (arrive: zeroed by router_bounds earlier in
- * the same call) runs the route finish over all of them. When the
- * selection was certified every workgroup returns at once. The logits are
- * written by wave 0 of each workgroup, which releases them before thread 0
- * counts the workgroup in.
+ * The one-token route in two launches: route_bounds forms the bounds of
+ * every logit row, four rows per workgroup; route_select (one workgroup)
+ * selects:
+ *
+ *   1. certified: the top-k by the fp64 sums a when the bounds separate
+ *      every adjacent selected pair and the last selected from the rest;
+ *   2. refined: otherwise, with L the least a - b of the top-k by a (each
+ *      of those k experts has an exact logit >= L, so the k-th largest
+ *      exact logit is >= L), every expert not separated from L by its
+ *      bound is a contender; the exact left-to-right chains of the
+ *      contenders (at most 64) replace their bounds, and the selection is
+ *      certified again on them (an expert left out has logit <= a + b,
+ *      which is separated from L, hence from the k-th exact logit);
+ *   3. exact: otherwise (ties, or non-finite products), the chains of all
+ *      rows, then the route finish, as the several-token path does.
+ *
+ * The certified flag reads 1, 2 or 0 after the call for the three cases.
  */
+struct RouteArgs {
+    const float *router, *sgw, *x;
+    uint32_t experts, top_k;
+    double *bound;           /* [E + 1][2] */
+    float *logits, *shared_logit, *probs;
+    uint32_t *ids, *ids_out; /* ids_out: the caller's copy (may be null) */
+    float *weights;
+    uint32_t *order;
+    float *shared_scale;
+    uint32_t *status, *certified;
+};
+
+constexpr uint32_t kExQ = 16;    /* float4 of a row per stage of exact_rows */
+constexpr uint32_t kExDepth = 4; /* stages each thread has in flight */
+
+/* Exact chains of up to 64 logit rows (ids in rows[], `experts` meaning the
+ * shared gate vector) by a workgroup of 1024 threads: stage s takes columns
+ * 64s .. 64s + 63 of every row, each thread one float4 of one row; the
+ * rounded products w*x (as the CPU forms them) go to LDS, and lane r of
+ * wave 0 adds row r's 64 products to its chain, left to right, while the
+ * other threads form the next stage. out[r] gets row r's logit. */
 template <uint32_t HIDDEN>
-__global__ __launch_bounds__(1024) void route_exact(
-    const float *__restrict__ router, const float *__restrict__ shared_gate_weight,
-    const float *__restrict__ x, uint32_t experts, uint32_t top_k, float *logits,
-    float *shared_logit, float *__restrict__ probs, uint32_t *__restrict__ ids,
-    float *__restrict__ weights, uint32_t *__restrict__ order, float *__restrict__ shared_scale,
-    uint32_t *status, const uint32_t *__restrict__ certified, uint32_t *arrive) {
-    if (*certified != 0u) return;
-    __shared__ uint32_t s_last;
-    router_decode_rows<HIDDEN>(router, shared_gate_weight, x, experts, logits, shared_logit,
-                               status, blockIdx.x * kRtRows);
-    if (threadIdx.x < 64u) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        if (threadIdx.x == 0u) {
-            const uint32_t prev =
-                __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = prev == gridDim.x - 1u ? 1u : 0u;
+__device__ __forceinline__ void exact_rows(const float *__restrict__ router,
+                                           const float *__restrict__ sgw,
+                                           const float *__restrict__ x, uint32_t experts,
+                                           const uint32_t *rows, uint32_t n, float *out,
+                                           uint32_t *status) {
+    constexpr uint32_t NS = HIDDEN / 64u;
+    __shared__ float4 tile[2][64][kExQ + 1u];
+    const uint32_t t = threadIdx.x, r = t / kExQ, q = t % kExQ;
+    const bool have = r < n;
+    const uint32_t e = have ? rows[r] : 0u;
+    const float4 *src = (const float4 *)(e < experts ? router + (size_t)e * HIDDEN : sgw);
+    const float4 *xs = (const float4 *)x;
+    float4 wv[kExDepth], xv[kExDepth];
+#pragma unroll
+    for (uint32_t d = 0; d < kExDepth; ++d) {
+        if (have && d < NS) {
+            wv[d] = src[d * kExQ + q];
+            xv[d] = xs[d * kExQ + q];
+        }
+    }
+    bool bad = false;
+    float acc = 0.0f;
+    static_assert(NS % kExDepth == 0u, "stages come in whole rounds of the prefetch depth");
+    for (uint32_t s0 = 0; s0 < NS; s0 += kExDepth) {
+#pragma unroll
+        for (uint32_t d = 0; d < kExDepth; ++d) {
+            const uint32_t s = s0 + d;
+            if (have) {
+                const float4 w = wv[d], xq = xv[d];
+                bad |= !kq_isfinite(w.x) || !kq_isfinite(w.y) || !kq_isfinite(w.z) ||
+                       !kq_isfinite(w.w);
+                float4 p;
+                p.x = w.x * xq.x;
+                p.y = w.y * xq.y;
+                p.z = w.z * xq.z;
+                p.w = w.w * xq.w;
+                tile[s & 1u][r][q] = p;
+                if (s + kExDepth < NS) {
+                    wv[d] = src[(s + kExDepth) * kExQ + q];
+                    xv[d] = xs[(s + kExDepth) * kExQ + q];
+                }
+            }
+            __syncthreads();
+            if (t < n) {
+#pragma unroll 4
+                for (uint32_t j = 0; j < kExQ; ++j) add4(acc, tile[s & 1u][t][j]);
+            }
+        }
+    }
+    if (t < n) out[t] = acc;
+    if (bad) kq_flag(status, KQ_DEV_INPUT);
+    __syncthreads();
+}
+
+/* Ranks (descending value, ascending id) of two entries (m0, i0), (m1, i1)
+ * among the first `count` entries of v/id, in eight-entry runs of LDS
+ * broadcast reads. Entries past count read as (-inf, max id). */
+__device__ __forceinline__ void rank2(const double *v, const uint32_t *id, uint32_t count,
+                                      double m0, uint32_t i0, double m1, uint32_t i1,
+                                      uint32_t &r0, uint32_t &r1) {
+    r0 = 0u;
+    r1 = 0u;
+    for (uint32_t j0 = 0; j0 < count; j0 += 8u) {
+        double o[8];
+        uint32_t oi[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8u; ++q) {
+            const bool in = j0 + q < count;
+            o[q] = in ? v[j0 + q] : -__builtin_inf();
+            oi[q] = in ? id[j0 + q] : 0xffffffffu;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 8u; ++q) {
+            r0 += (uint32_t)(o[q] > m0) | ((uint32_t)(o[q] == m0) & (uint32_t)(oi[q] < i0));
+            r1 += (uint32_t)(o[q] > m1) | ((uint32_t)(o[q] == m1) & (uint32_t)(oi[q] < i1));
+        }
+    }
+}
+
+/* Writes the selection: sorted ids/values in srt_v/srt_id (descending), the
+ * weights p / sum of the selected p with p = exp(v - v_0) (the softmax
+ * denominator cancels; the hardware exponential, compared by tolerance
+ * like the layer output), and the ascending-id rank of each slot. Wave 0. */
+__device__ __forceinline__ void write_selection(const RouteArgs &a, const double *srt_v,
+                                                const uint32_t *srt_id) {
+    const uint32_t lane = threadIdx.x & 63u, k = a.top_k;
+    const double m = srt_v[0];
+    const uint32_t my_id = lane < k ? srt_id[lane] : 0xffffffffu;
+    const float ex = lane < k ? fast_expf((float)(srt_v[lane < k ? lane : 0] - m)) : 0.0f;
+    const float psel = wave_sum_f32(ex);
+    uint32_t rk = 0;
+    for (uint32_t j = 0; j < k; ++j) rk += (uint32_t)(srt_id[j] < my_id);
+    if (lane < k) {
+        a.ids[lane] = my_id;
+        if (a.ids_out) a.ids_out[lane] = my_id;
+        a.weights[lane] = ex / psel;
+        a.order[rk] = lane;
+    }
+}
+
+/* Adjacent selected pairs, and the last selected against `rest` (the
+ * largest upper value outside the selection, -inf if none), separated. */
+__device__ __forceinline__ bool separated(const double *srt_v, const double *srt_b, uint32_t k,
+                                          double rest) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const double m = srt_v[0];
+    const uint32_t l1 = lane + 1u < k ? lane + 1u : 0u;
+    const bool pair_ok =
+        lane + 1u >= k || certify_sep(srt_v[lane < k ? lane : 0], srt_b[lane < k ? lane : 0],
+                                      srt_v[l1], srt_b[l1], m);
+    bool ok = __ballot(!pair_ok) == 0ull;
+    if (ok && rest > -__builtin_inf())
+        ok = certify_sep(srt_v[k - 1u], srt_b[k - 1u], rest, 0.0, m);
+    return ok;
+}
+
+template <uint32_t HIDDEN>
+__device__ __forceinline__ void select_one(const RouteArgs &a) {
+    __shared__ double cv[kCertCand], cb[kCertCand], sv[kCertCand], sb[kCertCand];
+    __shared__ uint32_t cid[kCertCand], sid[kCertCand];
+    __shared__ __align__(16) float w_key[16];
+    __shared__ __align__(16) double w_rest[16];
+    __shared__ __align__(16) uint32_t w_bad[16];
+    __shared__ uint32_t s_count, s_cn, s_state;
+    __shared__ double s_lw, s_m;
+    __shared__ float ex_l[64];
+    const uint32_t experts = a.experts, top_k = a.top_k;
+    const uint32_t e = threadIdx.x, lane = e & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(e >> 6);
+    const double ninf = -__builtin_inf();
+    const bool live = e < experts;
+    if (w == 15u && lane == 0u) {
+        /* the shared gate from the fp64 sum; the exact route overwrites it */
+        const double sh_a = a.bound[2u * experts];
+        *a.shared_scale = 1.0f / (1.0f + fast_expf(-(float)sh_a));
+    }
+    const double sh_b = a.bound[2u * experts + 1u];
+    const double ar = live ? a.bound[2u * e] : ninf;
+    const double b = live ? a.bound[2u * e + 1u] : 0.0;
+    const double av = ar == ar ? ar : ninf; /* a NaN total has an infinite bound */
+    const float key = (float)av;
+    const uint32_t need = top_k + 1u < experts ? top_k + 1u : experts;
+    const uint32_t ns = experts >= 64u ? experts / 64u : 1u;
+    const uint32_t per = (need + ns - 1u) / ns;
+    if (e == 0u) {
+        s_count = 0u;
+        s_cn = 0u;
+    }
+    /* candidates: each full wave's per-th largest key, t the least of them;
+     * every expert with key >= t is listed, the others' a + b maximised */
+    {
+        float m = __builtin_inff();
+        if (w < ns) {
+            float v = key;
+            for (uint32_t r = 0; r < per; ++r) {
+                m = wave_max(v);
+                const uint64_t hit = __ballot(v == m);
+                if (lane == (uint32_t)__builtin_ctzll(hit)) v = -__builtin_inff();
+            }
+        }
+        if (lane == 0u) w_key[w] = m;
+    }
+    __syncthreads();
+    float t = w_key[0];
+#pragma unroll
+    for (uint32_t k = 1; k < 16u; ++k) t = fminf(t, w_key[k]);
+    {
+        const bool c = live && key >= t;
+        const uint64_t cbm = __ballot(c);
+        uint32_t at = 0;
+        if (lane == 0u) at = atomicAdd(&s_count, (uint32_t)__popcll(cbm));
+        at = __builtin_amdgcn_readfirstlane(at) + bits_below(cbm);
+        if (c && at < kCertCand) {
+            cv[at] = av;
+            cb[at] = b;
+            cid[at] = e;
+        }
+        const double rest_w = kq_wave_max_f64(live && !c ? av + b : ninf);
+        const bool bad_w = __ballot(live && !(b < __builtin_inf())) != 0ull;
+        if (lane == 0u) {
+            w_rest[w] = rest_w;
+            w_bad[w] = bad_w ? 1u : 0u;
         }
     }
     __syncthreads();
-    if (s_last == 0u) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    route_finish_body(0u, logits, shared_logit, experts, top_k, probs, ids, weights, order,
-                      shared_scale, status);
+    if (w == 0u) {
+        const uint32_t total = s_count;
+        double rest = w_rest[0];
+        uint32_t anybad = w_bad[0];
+#pragma unroll
+        for (uint32_t k = 1; k < 16u; ++k) {
+            rest = fmax(rest, w_rest[k]);
+            anybad |= w_bad[k];
+        }
+        uint32_t state = 3u;
+        if (anybad == 0u && total <= kCertCand && sh_b < __builtin_inf()) {
+            /* each lane ranks candidates lane and lane + 64; the places
+             * past the list get entries that never rank above one */
+            const uint32_t j1 = lane + 64u;
+            const bool h0 = lane < total, h1 = j1 < total;
+            const double m0 = h0 ? cv[lane] : ninf, m1 = h1 ? cv[j1] : ninf;
+            const uint32_t i0 = h0 ? cid[lane] : 0xffffffffu, i1 = h1 ? cid[j1] : 0xffffffffu;
+            const double b0 = h0 ? cb[lane] : 0.0, b1 = h1 ? cb[j1] : 0.0;
+            uint32_t r0, r1;
+            rank2(cv, cid, total, m0, i0, m1, i1, r0, r1);
+            r0 = h0 ? r0 : lane;
+            r1 = h1 ? r1 : j1;
+            sv[r0] = m0;
+            sb[r0] = b0;
+            sid[r0] = i0;
+            sv[r1] = m1;
+            sb[r1] = b1;
+            sid[r1] = i1;
+            const double o0 = h0 && r0 >= top_k ? m0 + b0 : ninf;
+            const double o1 = h1 && r1 >= top_k ? m1 + b1 : ninf;
+            rest = fmax(rest, kq_wave_max_f64(fmax(o0, o1)));
+            if (separated(sv, sb, top_k, rest)) {
+                write_selection(a, sv, sid);
+                state = 1u;
+            } else {
+                /* L: the least a - b of the top-k by a */
+                const double lo = lane < top_k ? sv[lane] - sb[lane] : __builtin_inf();
+                const double lw = -kq_wave_max_f64(-lo);
+                if (lane == 0u) {
+                    s_lw = lw;
+                    s_m = sv[0];
+                }
+                state = 0u;
+            }
+        }
+        if (lane == 0u) s_state = state;
+    }
+    __syncthreads();
+    uint32_t state = s_state;
+    if (state == 0u) {
+        /* contenders: not separated from L by their bounds */
+        const bool inc = live && !certify_sep(s_lw, 0.0, av, b, s_m);
+        const uint64_t im = __ballot(inc);
+        uint32_t at = 0;
+        if (lane == 0u && im) at = atomicAdd(&s_cn, (uint32_t)__popcll(im));
+        at = __builtin_amdgcn_readfirstlane(at) + bits_below(im);
+        if (inc && at < 64u) cid[at] = e;
+        __syncthreads();
+        const uint32_t n = s_cn;
+        if (n > 64u || n < top_k) {
+            state = 3u;
+        } else {
+            exact_rows<HIDDEN>(a.router, a.sgw, a.x, experts, cid, n, ex_l, a.status);
+            if (w == 0u) {
+                const bool have = lane < n;
+                const double mine = have ? (double)ex_l[lane] : ninf;
+                const uint32_t my_id = have ? cid[lane] : 0xffffffffu;
+                for (uint32_t j = lane; j < n; j += 64u) cv[j] = (double)ex_l[j];
+                uint32_t rank, unused;
+                rank2(cv, cid, n, mine, my_id, ninf, 0xffffffffu, rank, unused);
+                rank = have ? rank : lane;
+                sv[rank] = mine;
+                sb[rank] = 0.0;
+                sid[rank] = my_id;
+                const bool fin = __ballot(have && !kq_isfinite(ex_l[lane])) == 0ull;
+                const double rest = n > top_k ? sv[top_k] : ninf;
+                uint32_t st = 3u;
+                if (fin && separated(sv, sb, top_k, rest)) {
+                    write_selection(a, sv, sid);
+                    st = 2u;
+                }
+                if (lane == 0u) s_state = st;
+            }
+            __syncthreads();
+            state = s_state;
+        }
+    }
+    if (state == 3u) {
+        /* every row's chain, 64 rows at a time, then the route finish */
+        for (uint32_t r0 = 0; r0 <= experts; r0 += 64u) {
+            const uint32_t n = experts + 1u - r0 < 64u ? experts + 1u - r0 : 64u;
+            if (e < n) cid[e] = r0 + e;
+            __syncthreads();
+            exact_rows<HIDDEN>(a.router, a.sgw, a.x, experts, cid, n, ex_l, a.status);
+            if (e < n) {
+                if (r0 + e < experts)
+                    a.logits[r0 + e] = ex_l[e];
+                else
+                    *a.shared_logit = ex_l[e];
+            }
+            __syncthreads();
+        }
+        route_finish_body(0u, a.logits, a.shared_logit, experts, top_k, a.probs, a.ids,
+                          a.weights, a.order, a.shared_scale, a.status);
+        __syncthreads();
+        if (a.ids_out && e < top_k) a.ids_out[e] = a.ids[e];
+    }
+    if (e == 0u) *a.certified = state == 1u ? 1u : (state == 2u ? 2u : 0u);
+}
+
+template <uint32_t HIDDEN>
+__global__ __launch_bounds__(64 * kSelRows * kSelParts) void route_bounds(RouteArgs a) {
+    bounds_rows<HIDDEN>(a.router, a.sgw, a.x, a.experts, a.bound);
+}
+
+/* one workgroup: the bounds are another launch's stores, so they are read
+ * here without any fence (a cross-workgroup hand-off inside one launch
+ * would need an agent-scope release per workgroup, a write-back of its L2) */
+template <uint32_t HIDDEN>
+__global__ __launch_bounds__(1024) void route_select(RouteArgs a) {
+    select_one<HIDDEN>(a);
 }
 
 /* ---------------------- expert gate/up + SwiGLU ---------------------- */
@@ -1396,7 +1575,7 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
     b += align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u); /* outp */
     b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
-    b += 256u;                                           /* certified flag, arrival count */
+    b += 256u;                                           /* certified flag */
     return b;
 }
 
@@ -1420,7 +1599,6 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->outp = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u);
     ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
     ws->certified = (uint32_t *)p;
-    ws->arrive = (uint32_t *)p + 32; /* its own 128-byte line in the same slot */
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
@@ -1444,37 +1622,48 @@ extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
 extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
                                           const float *shared_gate_weight, const float *hidden,
                                           uint32_t tokens, const kq_launch_moe_ws *ws,
-                                          uint32_t *status, int certify, hipStream_t s) {
+                                          uint32_t *status, int certify, uint32_t *ids_out,
+                                          hipStream_t s) {
     const uint32_t ep = pad64(d->experts + 1u);
     const uint32_t groups = (d->experts + 1u + kRtRows - 1u) / kRtRows;
     bool fused = tokens == 1u;
     uint32_t fin = 64u * ((d->experts + 63u) / 64u + 1u);
     if (fin > 1024u) fin = 1024u;
-    /* one token, ids only needed exactly: the certified selection, then the
-     * exact route as one launch that returns at once when it succeeded */
+    /* one token, ids only needed exactly: the bounds, then the selection
+     * (certified, refined or exact) in one workgroup */
     if (fused && certify && d->top_k <= kMaxTopK) {
+        RouteArgs a;
+        a.router = router;
+        a.sgw = shared_gate_weight;
+        a.x = hidden;
+        a.experts = d->experts;
+        a.top_k = d->top_k;
+        a.bound = ws->bound;
+        a.logits = ws->logits;
+        a.shared_logit = ws->shared_logit;
+        a.probs = ws->probs;
+        a.ids = ws->ids;
+        a.ids_out = ids_out;
+        a.weights = ws->weights;
+        a.order = ws->order;
+        a.shared_scale = ws->shared_scale;
+        a.status = status;
+        a.certified = ws->certified;
         const uint32_t bgroups = (d->experts + kSelRows) / kSelRows; /* E + 1 rows */
-        const uint32_t xthreads = fin > (uint32_t)kThreads ? fin : (uint32_t)kThreads;
-#define KQ_CERTIFIED_ROUTE(H)                                                                  \
-    hipLaunchKernelGGL(router_bounds<H>, dim3(bgroups), dim3(1024), 0, s, router,              \
-                       shared_gate_weight, hidden, d->experts, ws->bound, ws->arrive);         \
-    hipLaunchKernelGGL(route_certify, dim3(1), dim3(1024), 0, s, ws->bound, d->experts,        \
-                       d->top_k, ws->ids, ws->weights, ws->order, ws->shared_scale,            \
-                       ws->certified);                                                         \
-    hipLaunchKernelGGL(route_exact<H>, dim3(groups), dim3(xthreads), 0, s, router,             \
-                       shared_gate_weight, hidden, d->experts, d->top_k, ws->logits,           \
-                       ws->shared_logit, ws->probs, ws->ids, ws->weights, ws->order,           \
-                       ws->shared_scale, status, ws->certified, ws->arrive)
         bool have = true;
+#define KQ_ROUTE_ONE(H)                                                                  \
+    hipLaunchKernelGGL(route_bounds<H>, dim3(bgroups), dim3(64u * kSelRows * kSelParts), 0, s, \
+                       a);                                                               \
+    hipLaunchKernelGGL(route_select<H>, dim3(1), dim3(1024), 0, s, a)
         switch (d->hidden) {
-        case 256: KQ_CERTIFIED_ROUTE(256u); break;
-        case 512: KQ_CERTIFIED_ROUTE(512u); break;
-        case 1024: KQ_CERTIFIED_ROUTE(1024u); break;
-        case 2048: KQ_CERTIFIED_ROUTE(2048u); break;
-        case 2560: KQ_CERTIFIED_ROUTE(2560u); break;
+        case 256: KQ_ROUTE_ONE(256u); break;
+        case 512: KQ_ROUTE_ONE(512u); break;
+        case 1024: KQ_ROUTE_ONE(1024u); break;
+        case 2048: KQ_ROUTE_ONE(2048u); break;
+        case 2560: KQ_ROUTE_ONE(2560u); break;
         default: have = false;
         }
-#undef KQ_CERTIFIED_ROUTE
+#undef KQ_ROUTE_ONE
         if (have) return hipGetLastError();
     }
 #define KQ_ROUTER_DECODE(H)                                                                   \
@@ -1515,7 +1704,13 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
     hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, ws->logits, ws->shared_logit,
                        d->experts, d->top_k, ws->probs, ws->ids, ws->weights, ws->order,
                        ws->shared_scale, status);
-    return hipGetLastError();
+    e = hipGetLastError();
+    /* the one-token selection writes the caller's ids itself; here they
+     * are copied (several tokens, or a hidden size without an instance) */
+    if (e == hipSuccess && ids_out != nullptr)
+        e = hipMemcpyAsync(ids_out, ws->ids, (size_t)tokens * d->top_k * 4u,
+                           hipMemcpyDeviceToDevice, s);
+    return e;
 }
 
 extern "C" hipError_t kq_launch_moe_route_finish(const float *logits, const float *shared_logit,

@@ -1020,7 +1020,7 @@ kq_status kq_hip_moe_route_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
     kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
-    e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, 0,
+    e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, 0, NULL,
                             c->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(logits, ws.logits, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
@@ -1101,7 +1101,7 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     /* the layer needs the CPU's expert ids exactly and its weights to fp32
      * tolerance: one token may take the certified routing */
     e = kq_launch_moe_route(&d, w->router, w->shared_gate_weight, hidden, (uint32_t)tokens, &ws,
-                            c->d_status, 1, c->stream);
+                            c->d_status, 1, tokens == 1u ? ids : NULL, c->stream);
     /* several tokens: each expert's weights stream once for all of its
      * tokens (grouped MFMA path); one token: the fused decode kernels */
     if (e == hipSuccess && tokens >= KQ_GROUPED_MIN_TOKENS &&
@@ -1111,7 +1111,8 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     else if (e == hipSuccess)
         e = kq_launch_moe_experts(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status,
                                   c->stream);
-    if (e == hipSuccess && ids != NULL)
+    /* one token: the route kernel wrote the caller's ids itself */
+    if (e == hipSuccess && ids != NULL && tokens > 1u)
         e = hipMemcpyAsync(ids, ws.ids, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice, c->stream);
     return finish(c, e, "MoE execute launch", diag);
 }

@@ -112,7 +112,8 @@ def test_routing_tie_heavy(ctx, pattern):
 
 def certified_flag(ctx, scratch, n):
     # The one-token workspace ends with the certification word (its last
-    # 256-byte slot): 1 when the certified selection produced the ids.
+    # 256-byte slot): 1 when the certified selection produced the ids, 2
+    # when the exact chains of the contenders did, 0 for the exact route.
     return int(ctx.download(scratch.ptr + n - 256, np.uint32, 1)[0])
 
 
@@ -407,7 +408,8 @@ def test_moe_decode_campaign_10000_tokens(ctx, layer):
     scratch, dx, dout, dids = ctx.alloc(n), ctx.alloc(H * 4), ctx.alloc(H * 4), ctx.alloc(K * 4)
     mw = kq_hip.moe_weights(layer.bufs)
     th = oracle_threads()
-    stats = {"certified": 0, "compared": 0, "flag_agree": 0, "tie_certified": 0}
+    stats = {"certified": 0, "refined": 0, "exact": 0, "compared": 0, "flag_agree": 0,
+             "tie_certified": 0, "tie_refined": 0}
     for t in range(n_rand + n_tie):
         x = xs[t] if t < n_rand else near_tie(router, xs[t], K, cs[t - n_rand])
         x = np.ascontiguousarray(x)
@@ -419,13 +421,16 @@ def test_moe_decode_campaign_10000_tokens(ctx, layer):
         cert = certified_flag(ctx, scratch, n)
         _, _, want, _ = kq_oracle.moe_route(dims, (kq_oracle.F32, router), x, threads=th)
         assert np.array_equal(ids, want), (t, ids, want, cert)
-        stats["certified"] += cert
+        stats["certified"] += int(cert == 1)
+        stats["refined"] += int(cert == 2)
+        stats["exact"] += int(cert == 0)
         if t >= n_rand:
-            stats["tie_certified"] += cert
+            stats["tie_certified"] += int(cert == 1)
+            stats["tie_refined"] += int(cert == 2)
         if t >= n_rand or t % 10 == 0:
             c_cpu, c_ids = kq_oracle.route_certify(router, x, K)
             stats["compared"] += 1
-            stats["flag_agree"] += int(bool(cert) == c_cpu)
+            stats["flag_agree"] += int((cert == 1) == c_cpu)
             if c_cpu:
                 assert np.array_equal(c_ids, want), t
         if t % 2000 == 1999:
@@ -433,8 +438,10 @@ def test_moe_decode_campaign_10000_tokens(ctx, layer):
     for b in (scratch, dx, dout, dids):
         b.close()
     record("decode routing campaign", dict(stats, tokens=n_rand + n_tie, nudged=n_tie))
-    # random tokens nearly all certify; nudged ones split around the bound
+    # random tokens nearly all certify and the exact chains of the
+    # contenders settle the rest; nudged ones split around the bound
     assert stats["certified"] - stats["tie_certified"] >= 0.9 * n_rand
+    assert stats["refined"] - stats["tie_refined"] > 0
     assert 0 < stats["tie_certified"] < n_tie
     assert stats["flag_agree"] >= 0.99 * stats["compared"], stats
 
@@ -556,6 +563,56 @@ def test_moe_reference_model_layer(ctx):
 def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
     seed = S.W_MOE + 3000 + H + I + T
     out, ids, ref, tr, ex = run_layer(ctx, H, E, K, I, T, g, d, sg, sd, seed)
+    assert np.array_equal(ids, tr["selected_ids"])
+    assert_close(out, ref, exact=ex)
+
+
+# grouped (MFMA) prefill with every format pair the passes take: Q8_0 and
+# Q4_K gate/up (2560 columns staged in two slices), Q5_1, Q8_0, Q6_K and
+# Q4_K down (640-column rows of 128-column units), routed and shared of
+# different formats (two launches per role)
+@pytest.mark.parametrize("H,E,K,I,T,g,d,sg,sd", [
+    (2560, 64, 8, 640, 40, "Q4_K", "Q5_1", "Q8_0", "Q8_0"),
+    (2560, 32, 4, 640, 37, "Q8_0", "Q8_0", "Q8_0", "Q8_0"),
+    (1024, 24, 3, 640, 37, "Q4_K", "Q5_1", "Q4_K", "Q5_1"),
+    (2048, 24, 3, 512, 37, "Q8_0", "Q6_K", "Q4_K", "Q4_K"),
+    (512, 16, 4, 640, 20, "Q4_K", "Q8_0", "Q8_0", "Q5_1"),
+], ids=["ref-formats-40tok", "q8_0-2560", "q5_1-640", "mixed-q6k-lds", "q8_0-q5_1-down"])
+def test_moe_prefill_grouped_formats(ctx, H, E, K, I, T, g, d, sg, sd):
+    seed = S.W_MOE + 5000 + H + I + T
+    w = S.moe_weights(seed, H, E, I, I, gate_fmt=g, down_fmt=d, shared_gate_fmt=sg,
+                      shared_down_fmt=sd)
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    x = S.normal_f32(S.stream_key(seed, S.R_HIDDEN), T * H).reshape(T, H)
+    x[5] *= 1e-30   # tiny row: the per-token power-of-two scaling keeps it
+    x[6] *= 1e6     # large row
+    n = cfg.scratch_bytes(T)
+    scratch, dx, dout, dids = ctx.alloc(n), ctx.upload(x), ctx.alloc(T * H * 4), ctx.alloc(T * K * 4)
+    t = kq_hip.TYPE_IDS
+    ctx.moe_execute(cfg, kq_hip.moe_weights(bufs, t[g], t[d], t[sg], t[sd]), dx, T, dout, dids,
+                    scratch, n)
+    out = ctx.download(dout, np.float32, T * H).reshape(T, H)
+    ids = ctx.download(dids, np.uint32, T * K).reshape(T, K)
+    roles = {"router": kq_oracle.F32, "gate": t[g], "up": t[g], "down": t[d],
+             "shared_gate": t[sg], "shared_up": t[sg], "shared_down": t[sd],
+             "shared_gate_weight": kq_oracle.F32}
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    ref, tr = kq_oracle.moe_execute(dims, {k: (r, w[k]) for k, r in roles.items()}, x, trace=True,
+                                    threads=oracle_threads())
+    assert np.array_equal(ids, tr["selected_ids"])
+    assert_close(out, ref, exact=exact.moe(dims, roles, w, x, tr["selected_ids"]))
+    for b in list(bufs.values()) + [scratch, dx, dout, dids]:
+        b.close()
+
+
+def test_moe_reference_model_prefill_512(ctx):
+    # The reference model's MoE layer (2560 / 512 experts / top-10 / 640,
+    # Q4_K gate/up, Q5_1 down, Q8_0 shared) over 512 tokens: the grouped
+    # MFMA passes with every expert touched
+    say("reference-model layer prefill, 512 tokens")
+    out, ids, ref, tr, ex = run_layer(ctx, 2560, 512, 10, 640, 512, "Q4_K", "Q5_1", "Q8_0",
+                                      "Q8_0", S.W_MOE + 2561)
     assert np.array_equal(ids, tr["selected_ids"])
     assert_close(out, ref, exact=ex)
 
