@@ -600,6 +600,8 @@ def main() -> int:
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640"))
         run("moe_block_decode_1tok_4x2560",
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640", block=True))
+        run("moe_block_prefill_512_4x2560",
+            lambda: wl_moe(ctx, 512, 1, max(3, K // 40), graph, cache, "2560x640", block=True))
         if "hbm_copy_64mb" in names:
             run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))
     head = work.get(HEADLINE)

@@ -152,26 +152,26 @@ struct Fmt<KQ_LAUNCH_Q6_K> {
 };
 
 /* Q8_0: 34 B per 32 columns (f16 d, 32 int8 codes; src/kq_numeric.c:
- * 176-196). An iteration takes four blocks (128 columns); each block is one
+ * 176-196). An iteration takes two blocks (64 columns); each block is one
  * 16x16x32 step, lane k-group g holding its columns 8g .. 8g + 7, i.e. code
- * bytes 2 + 8g .. 9 + 8g. Blocks start at 2 mod 4 in a unit (34 B apart),
- * so the codes of even blocks come from a 12-byte window re-aligned by two
- * bytes; the scale is half of an aligned dword. Rows are whole units of
- * 136 B, so a unit starts 4-byte aligned. */
+ * bytes 2 + 8g .. 9 + 8g. The first block's codes start at 2 mod 4, so they
+ * come from a 12-byte window re-aligned by two bytes; each scale is half of
+ * an aligned dword. Rows are whole units of 68 B, so a unit starts 4-byte
+ * aligned. */
 template <>
 struct Fmt<KQ_LAUNCH_Q8_0> {
-    static constexpr uint32_t kUnit = 128u;
-    static constexpr uint32_t kUnitBytes = 136u;
+    static constexpr uint32_t kUnit = 64u;
+    static constexpr uint32_t kUnitBytes = 68u;
     static constexpr bool kSums = false;
     static constexpr bool kK32 = true;
     struct Raw {
-        kq_u32x3 c[4]; /* code windows of the four blocks */
-        uint32_t d[4]; /* dwords holding the scales */
+        kq_u32x3 c[2]; /* code windows of the two blocks */
+        uint32_t d[2]; /* dwords holding the scales */
     };
     __device__ static __forceinline__ Raw load(KqBuf w, uint32_t uoff, uint32_t g) {
         Raw r;
 #pragma unroll
-        for (uint32_t bb = 0; bb < 4u; ++bb) {
+        for (uint32_t bb = 0; bb < 2u; ++bb) {
             const uint32_t a = uoff + 34u * bb + 2u + 8u * g; /* codes */
             r.c[bb] = kq_ld96(w, a & ~3u, 0u);
             r.d[bb] = kq_ld32(w, (uoff + 34u * bb) & ~3u, 0u);
@@ -240,37 +240,51 @@ template <uint32_t FMT, uint32_t KDIM, uint32_t KSL>
 __device__ bool stage_slice(Stage<FMT, KSL> &st, const float *__restrict__ X, uint32_t col0,
                             const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
     using S = Stage<FMT, KSL>;
-    constexpr uint32_t NQ = (KDIM + 255u) / 256u; /* float4 groups per lane: 1 .. 10 */
+    constexpr uint32_t NQ = (KDIM + 255u) / 256u;   /* float4 groups per lane, whole row */
+    constexpr uint32_t NQS = (KSL + 255u) / 256u + (KSL % 256u != 0u ? 1u : 0u); /* a slice */
     bool bad = false;
     for (uint32_t i = wave; i < kTile; i += nwaves) {
         const int src = src_row[i];
         const float4 *p = (const float4 *)(X + (size_t)(src < 0 ? 0 : src) * KDIM) + lane;
-        float4 v[NQ];
-#pragma unroll
-        for (uint32_t q = 0; q < NQ; ++q) {
-            const bool in = src >= 0 && 256u * q + 4u * lane < KDIM;
-            v[q] = in ? p[64u * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        int sig;
+        bool any_nf = false;
+        if (col0 == 0u) {
+            /* the scale, from the whole row (later slices of this chunk reuse
+             * it, so every slice gets the same one) */
+            float m = 0.0f;
+            bool nf = false;
+#pragma unroll 8
+            for (uint32_t q = 0; q < NQ; ++q) {
+                const bool in = src >= 0 && 256u * q + 4u * lane < KDIM;
+                const float4 v = in ? p[64u * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+                nf |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                      !kq_isfinite(v.w);
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+            bad |= nf;
+            m = wave_max_abs(m);
+            any_nf = __ballot(nf) != 0ull;
+            /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) lies in [2^14, 2^15) */
+            sig = 0;
+            if (!any_nf && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
+            if (any_nf) sig = 0x7fffffff; /* a row staged as zeros */
+        } else {
+            sig = st.sig[i];
+            any_nf = sig == 0x7fffffff;
         }
-        float m = 0.0f;
-        bool nf = false;
+        const uint32_t q0 = col0 / 256u;
+        float4 v[NQS];
 #pragma unroll
-        for (uint32_t q = 0; q < NQ; ++q) {
-            nf |= !kq_isfinite(v[q].x) || !kq_isfinite(v[q].y) || !kq_isfinite(v[q].z) ||
-                  !kq_isfinite(v[q].w);
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)),
-                               fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
+        for (uint32_t qq = 0; qq < NQS; ++qq) {
+            const uint32_t col = 256u * (q0 + qq) + 4u * lane;
+            const bool in = src >= 0 && col < KDIM;
+            v[qq] = in ? p[64u * (q0 + qq)] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        bad |= nf;
-        m = wave_max_abs(m);
-        const bool any_nf = __ballot(nf) != 0ull;
-        /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) lies in [2^14, 2^15) */
-        int sig = 0;
-        if (!any_nf && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
 #pragma unroll
-        for (uint32_t q = 0; q < NQ; ++q) {
-            const uint32_t col = 256u * q + 4u * lane;
+        for (uint32_t qq = 0; qq < NQS; ++qq) {
+            const uint32_t col = 256u * (q0 + qq) + 4u * lane;
             const bool mine = col >= col0 && col < col0 + KSL;
-            const float a[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+            const float a[4] = {v[qq].x, v[qq].y, v[qq].z, v[qq].w};
             _Float16 hi[4], lo[4];
             float part = 0.0f;
 #pragma unroll
@@ -481,16 +495,16 @@ struct Tile<KQ_LAUNCH_Q8_0, KSL, NMAT> {
     using S = Stage<KQ_LAUNCH_Q8_0, KSL>;
     using Raw = F::Raw;
 
-    /* iteration b: blocks 4b .. 4b + 3 of the slice, one step each; the
+    /* iteration b: blocks 2b, 2b + 1 of the slice, one step each; the
      * int8 codes enter as fp16 through the offset-binary byte (q + 128) */
     __device__ static __forceinline__ void block(const Raw (&r)[NMAT], const S &st, uint32_t b,
                                                  uint32_t i, uint32_t g, f4 (&acc)[NMAT],
                                                  bool &malformed) {
-        const _Float16 *xh = st.xh + i * S::kPitch + 128u * b + 8u * g;
-        const _Float16 *xl = st.xl + i * S::kPitch + 128u * b + 8u * g;
+        const _Float16 *xh = st.xh + i * S::kPitch + 64u * b + 8u * g;
+        const _Float16 *xl = st.xl + i * S::kPitch + 64u * b + 8u * g;
         const h2 bias = h2{(_Float16)-1152.0f, (_Float16)-1152.0f}; /* 1024 + 128 */
 #pragma unroll
-        for (uint32_t bb = 0; bb < 4u; ++bb) {
+        for (uint32_t bb = 0; bb < 2u; ++bb) {
             const h8 ah = *(const h8 *)(xh + 32u * bb);
             const h8 al = *(const h8 *)(xl + 32u * bb);
 #pragma unroll
@@ -905,12 +919,33 @@ constexpr uint32_t kSharedChunks = 2; /* 16-token chunks per shared-expert workg
 #define KQ_DN_TPW 4
 #define KQ_DN_PD 1
 #endif
+#ifndef KQ_GU_KSL
+#define KQ_GU_KSL 2048 /* widest activation slice staged at once */
+#endif
+
+/* slices of a row: the fewest whole-unit slices of at most KQ_GU_KSL
+ * columns */
+template <uint32_t GFMT, uint32_t KDIM>
+constexpr int gu_slices() {
+    for (int ks = 1; ks <= 16; ++ks) {
+        const uint32_t w = KDIM / (uint32_t)ks;
+        if (w * (uint32_t)ks == KDIM && w % Fmt<GFMT>::kUnit == 0u && w <= (uint32_t)KQ_GU_KSL)
+            return ks;
+    }
+    return 0;
+}
 template <uint32_t GFMT, uint32_t KDIM, int NMAT>
 struct Shape {
-    static constexpr int NW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_NW : 8) : KQ_DN_NW;
-    static constexpr int TPW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_TPW : 2) : KQ_DN_TPW;
-    /* gate/up rows longer than 2048 columns are staged in two slices */
-    static constexpr int KS = NMAT == 2 && KDIM > 2048u ? 2 : 1;
+    /* rows longer than KQ_GU_KSL columns are staged in slices, one tile
+     * per wave */
+    static constexpr bool kSliced = KDIM > (uint32_t)KQ_GU_KSL;
+    static constexpr int NW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_NW : 8)
+                                        : (kSliced ? KQ_GU_NW : KQ_DN_NW);
+    static constexpr int TPW = NMAT == 2 ? (KDIM >= 1024u ? KQ_GU_TPW : 2)
+                                         : (kSliced ? 1 : KQ_DN_TPW);
+    static constexpr int KS = gu_slices<GFMT, KDIM>();
+    static_assert(KS >= 1, "no slicing of this row length");
+    static_assert(KS == 1 || TPW == 1, "sliced passes run one tile per wave");
     /* the ring (PD + 1 slots) is a power of two that divides the wave's
      * KS * TPW * KDIM / unit iterations */
     static constexpr int NIT = TPW * (int)(KDIM / Fmt<GFMT>::kUnit);
@@ -925,8 +960,8 @@ struct Shape {
 template <uint32_t KDIM>
 hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X,
                            const uint32_t *offsets, uint32_t experts, uint32_t tokens,
-                           uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, float *out,
-                           uint32_t *status, hipStream_t s);
+                           uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny,
+                           uint32_t chunks, float *out, uint32_t *status, hipStream_t s);
 
 /* Workgroup rows y0 .. y0 + ny - 1 of the pass: experts 0 .. E-1, then the
  * shared expert's chunk groups. */
@@ -934,14 +969,14 @@ template <uint32_t GFMT, uint32_t KDIM, int NMAT>
 hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
                        const uint8_t *SW1, const float *X, const uint32_t *offsets,
                        const uint32_t *perm_tok, uint32_t experts, uint32_t tokens,
-                       uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, float *out,
-                       uint32_t *status, hipStream_t s) {
+                       uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, uint32_t chunks,
+                       float *out, uint32_t *status, hipStream_t s) {
     if (ny == 0u) return hipSuccess;
     /* (an intermediate of 2048 leaves no LDS beside its activation image
      * for the weight slots) */
     if constexpr (GFMT == KQ_LAUNCH_Q6_K && NMAT == 1 && KDIM <= 1024u)
         return launch_down_q6k<KDIM>(W0, SW0, X, offsets, experts, tokens, top_k, rows, y0, ny,
-                                     out, status, s);
+                                     chunks, out, status, s);
     constexpr int NW = Shape<GFMT, KDIM, NMAT>::NW;
     constexpr int TPW = Shape<GFMT, KDIM, NMAT>::TPW;
     constexpr int PD = Shape<GFMT, KDIM, NMAT>::PD;
@@ -950,7 +985,7 @@ hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
     const dim3 grid((rows + slab - 1u) / slab, ny);
     hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW, TPW, PD, KS>), grid, dim3(NW * 64), 0,
                        s, W0, W1, SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, rows,
-                       kSharedChunks, y0, out, status);
+                       chunks, y0, out, status);
     return hipGetLastError();
 }
 
@@ -960,27 +995,30 @@ template <uint32_t GFMT, int NMAT>
 constexpr bool pass_dim(uint32_t k) {
     if (k % Fmt<GFMT>::kUnit != 0u) return false;
     if (NMAT == 2) return k == 256u || k == 512u || k == 1024u || k == 2048u || k == 2560u;
-    return k == 256u || k == 512u || k == 640u || k == 1024u || k == 2048u;
+    return k == 256u || k == 320u || k == 512u || k == 640u || k == 1024u || k == 2048u ||
+           k == 10240u;
 }
 
 template <uint32_t GFMT, int NMAT>
 hipError_t pass_cols(uint32_t kdim, const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
                      const uint8_t *SW1, const float *X, const uint32_t *offsets,
                      const uint32_t *perm_tok, uint32_t experts, uint32_t tokens, uint32_t top_k,
-                     uint32_t rows, uint32_t y0, uint32_t ny, float *out, uint32_t *status,
-                     hipStream_t s) {
+                     uint32_t rows, uint32_t y0, uint32_t ny, uint32_t chunks, float *out,
+                     uint32_t *status, hipStream_t s) {
 #define KQ_PASS(K)                                                                               \
     if constexpr (pass_dim<GFMT, NMAT>(K))                                                       \
         return launch_pass<GFMT, K, NMAT>(W0, W1, SW0, SW1, X, offsets, perm_tok, experts,       \
-                                          tokens, top_k, rows, y0, ny, out, status, s);          \
+                                          tokens, top_k, rows, y0, ny, chunks, out, status, s);  \
     return hipErrorInvalidValue
     switch (kdim) {
     case 256: { KQ_PASS(256u); }
+    case 320: { KQ_PASS(320u); }
     case 512: { KQ_PASS(512u); }
     case 640: { KQ_PASS(640u); }
     case 1024: { KQ_PASS(1024u); }
     case 2048: { KQ_PASS(2048u); }
     case 2560: { KQ_PASS(2560u); }
+    case 10240: { KQ_PASS(10240u); }
     default: return hipErrorInvalidValue;
     }
 #undef KQ_PASS
@@ -1008,7 +1046,7 @@ hipError_t pass_any(uint32_t type, uint32_t kdim, const uint8_t *W0, const uint8
                     float *out, uint32_t *status, hipStream_t s) {
 #define KQ_ANY(F)                                                                              \
     pass_cols<F, NMAT>(kdim, W0, W1, SW0, SW1, X, offsets, perm_tok, experts, tokens, top_k, \
-                       rows, y0, ny, out, status, s)
+                       rows, y0, ny, kSharedChunks, out, status, s)
     switch (type) {
     case KQ_LAUNCH_Q4_K: return KQ_ANY(KQ_LAUNCH_Q4_K);
     case KQ_LAUNCH_Q8_0: return KQ_ANY(KQ_LAUNCH_Q8_0);
@@ -1448,14 +1486,14 @@ __global__ __launch_bounds__(NW * 64) void grouped_down_q6k(
 template <uint32_t KDIM>
 hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X,
                            const uint32_t *offsets, uint32_t experts, uint32_t tokens,
-                           uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny, float *out,
-                           uint32_t *status, hipStream_t s) {
+                           uint32_t top_k, uint32_t rows, uint32_t y0, uint32_t ny,
+                           uint32_t chunks, float *out, uint32_t *status, hipStream_t s) {
     constexpr int NW = Shape<KQ_LAUNCH_Q6_K, KDIM, 1>::NW;
     constexpr int TPW = Shape<KQ_LAUNCH_Q6_K, KDIM, 1>::TPW;
     const uint32_t slab = (uint32_t)(NW * TPW) * kTile;
     const dim3 grid((rows + slab - 1u) / slab, ny);
     hipLaunchKernelGGL((grouped_down_q6k<KDIM, NW, TPW>), grid, dim3(NW * 64), 0, s, W0, SW0, X,
-                       offsets, experts, tokens, top_k, rows, kSharedChunks, y0, out, status);
+                       offsets, experts, tokens, top_k, rows, chunks, y0, out, status);
     return hipGetLastError();
 }
 
@@ -1528,6 +1566,24 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
                        ws->outp, ws->pos, ws->order, ws->weights, ws->shared_scale, tokens,
                        d->top_k, d->hidden, out, status);
     return hipGetLastError();
+}
+
+/* y[t] = W x[t] for every token: a Q8_0 matrix against many activation
+ * rows on MFMA, as the grouped pass runs a shared matrix (16-token chunks,
+ * one per workgroup), so the weights stream once per chunk instead of once
+ * per four tokens */
+extern "C" int kq_launch_gemm_q8_0_supported(uint32_t rows, uint32_t cols) {
+    return rows != 0u && pass_dim<KQ_LAUNCH_Q8_0, 1>(cols);
+}
+
+extern "C" hipError_t kq_launch_gemm_q8_0(const void *W, uint32_t rows, uint32_t cols,
+                                          const float *x, uint32_t tokens, float *y,
+                                          uint32_t *status, hipStream_t s) {
+    if (!kq_launch_gemm_q8_0_supported(rows, cols) || tokens == 0u) return hipErrorInvalidValue;
+    const uint32_t ny = (tokens + kTile - 1u) / kTile;
+    return pass_cols<KQ_LAUNCH_Q8_0, 1>(cols, nullptr, nullptr, (const uint8_t *)W, nullptr, x,
+                                        nullptr, nullptr, 0u, tokens, 0u, rows, 0u, ny, 1u, y,
+                                        status, s);
 }
 
 /* batched Q6_K matvec on MFMA: rows of 256 .. 4096 columns (whole blocks),

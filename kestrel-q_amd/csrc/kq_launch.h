@@ -39,6 +39,11 @@ hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_
                             const float *x, uint32_t batch, float *y, uint32_t *status,
                             float *part_v, uint32_t *part_i, uint32_t part_stride,
                             hipStream_t stream);
+/* y[t] = W x[t] for many tokens, Q8_0 W on MFMA (kq_grouped.hip): row
+ * lengths 256, 320, 512, 640, 1024, 2048 or 10240 */
+int kq_launch_gemm_q8_0_supported(uint32_t rows, uint32_t cols);
+hipError_t kq_launch_gemm_q8_0(const void *W, uint32_t rows, uint32_t cols, const float *x,
+                               uint32_t tokens, float *y, uint32_t *status, hipStream_t stream);
 /* batched Q6_K matvec on MFMA (kq_grouped.hip), used by kq_launch_matvec
  * where supported; same partials contract */
 int kq_launch_matvec_mfma_supported(uint32_t type, uint32_t rows, uint32_t cols, uint32_t batch);

@@ -1450,8 +1450,16 @@ static kq_status gr_proj_ok(uint32_t type, const void *w, uint64_t cols, const c
     return KQ_STATUS_OK;
 }
 
+/* Tokens from which a Q8_0 projection runs on MFMA: its weights then
+ * stream once per 16 tokens instead of once per 4 */
+#define KQ_GR_GEMM_MIN_TOKENS 5u
+
 static hipError_t gr_project(kq_hip_context *c, uint32_t type, const void *w, uint64_t rows,
                              uint64_t cols, const float *x, uint32_t tokens, float *y) {
+    if (type == KQ_HIP_TYPE_Q8_0 && tokens >= KQ_GR_GEMM_MIN_TOKENS &&
+        kq_launch_gemm_q8_0_supported((uint32_t)rows, (uint32_t)cols))
+        return kq_launch_gemm_q8_0(w, (uint32_t)rows, (uint32_t)cols, x, tokens, y, c->d_status,
+                                   c->stream);
     if (type == KQ_HIP_TYPE_F32)
         return kq_launch_matvec_f32w((const float *)w, (uint32_t)rows, (uint32_t)cols, x, tokens,
                                      y, c->d_status, c->stream);

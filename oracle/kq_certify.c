@@ -21,7 +21,7 @@
  *     this order.
  * kqo_route_certify restates that decision step by step, including how the
  * device gathers its candidates (waves of 64 experts, each wave's per-th
- * largest key, at most 64 candidates) so the cases it certifies are the
+ * largest key, at most 128 candidates) so the cases it certifies are the
  * device's. kqo_certify_campaign generates routers and activations from a
  * SplitMix64 stream, optionally plants near ties at gaps around the bound,
  * and counts certified selections whose ids differ from the oracle's exact
@@ -72,7 +72,7 @@ static int cand_before(const cand *p, const cand *q) {
  * margin (1 as on the device). */
 static int certify(const double *ar, const double *b, uint32_t E, uint32_t k, uint32_t *ids,
                    double slack) {
-    enum { kCand = 64 };
+    enum { kCand = 128 };
     double a[1024];
     float key[1024];
     cand list[kCand];

@@ -156,9 +156,10 @@ def gr_model(ctx):
     g.close()
 
 
-@pytest.mark.parametrize("tokens", [1, 3, 6])
+@pytest.mark.parametrize("tokens", [1, 3, 5, 37, 130])
 def test_gated_residual_read_model_dims(ctx, gr_model, tokens):
-    # 6 tokens run the projections as two batches (4 + 2)
+    # up to 4 tokens the rank projections run on the row engine; from 5 on
+    # MFMA in 16-token chunks (37 and 130: partial last chunks)
     g = gr_model
     x = S.normal_f32(S.stream_key(S.W_MOE + 91, tokens), tokens * g.B * g.H).reshape(tokens, -1)
     mixed, wg = g.read(ctx, x)
@@ -184,7 +185,7 @@ MOE_ROLES = ("router", "gate", "up", "down", "shared_gate", "shared_up", "shared
              "shared_gate_weight")
 
 
-@pytest.mark.parametrize("E,K,T", [(64, 8, 1), (64, 8, 3), (512, 10, 1)])
+@pytest.mark.parametrize("E,K,T", [(64, 8, 1), (64, 8, 3), (512, 10, 1), (64, 8, 40)])
 def test_moe_block_model_layer(ctx, gr_model, E, K, T):
     # The reference model's MoE block: hyper-connection read, MoE (hidden
     # 2560, intermediate 640, Q4_K gate/up, Q5_1 routed down, Q8_0 shared
