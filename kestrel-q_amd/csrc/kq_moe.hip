@@ -28,6 +28,8 @@
  * |G ∩ (t0, E)| lowest ids. (Derivation and brute-force check in the
  * oracle tests.) Final order: descending p, ascending id.
  */
+#include <type_traits>
+
 #include "kq_launch.h"
 #include "kq_rowdot.h"
 
@@ -1412,6 +1414,200 @@ __global__ __launch_bounds__(64 * kDownWaves) void expert_down_combine(
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
+/* ------------------- one launch per role: fused segments ------------------- */
+/* Rows of up to two column segments (C0 columns, then C1 from column C0;
+ * C1 = 0 for one) and a shared expert of its own format in one launch per
+ * role: each segment's engine forms its partial dots of the workgroup's
+ * rows into LDS, the segments' sums are added there (first segment, then
+ * second, as the segment launches add them), and the workgroup finishes
+ * the rows. kFuseRows rows per workgroup; a segment's engine takes row
+ * groups of at most that many rows. */
+constexpr uint32_t kFuseRows = 16;
+
+/* passes of RT rows: two while that keeps four groups per workgroup */
+template <uint32_t T, uint32_t C>
+constexpr int fuse_rt() {
+    return (kFuseRows / (64u / kq::lanes_per_row<T>(C))) >= 8u ? 2 : 1;
+}
+
+/* one segment's dots of rows row0 .. row0 + kFuseRows - 1 of matrices M[m]
+ * (NM of them) against x (the segment's own columns), into dst[m][row -
+ * row0] (added when !first) */
+template <uint32_t T, uint32_t C, int NM>
+__device__ __forceinline__ void fuse_segment(const uint8_t *const (&M)[NM], uint32_t stride,
+                                             uint32_t col0, uint32_t rows, uint32_t row0,
+                                             const float *x, float (*dst)[kFuseRows],
+                                             bool first, uint32_t wave, uint32_t nwaves,
+                                             bool &badx, bool &malformed) {
+    constexpr int RT = fuse_rt<T, C>();
+    using R = kq::Rows<T, C, 1, RT>;
+    using Raw = typename R::Raw;
+    static_assert(R::GROUP <= kFuseRows && kFuseRows % R::GROUP == 0u, "groups tile the rows");
+    constexpr uint32_t NG = kFuseRows / R::GROUP;
+    if (wave >= NG) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
+    typename R::Lane ln;
+    ln.setup(l);
+    const uint32_t boff = kq::row_bytes<T>(col0);
+    const uint32_t wbytes = rows * stride - boff;
+    KqBuf wb[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) wb[m] = kq_buf(M[m] + boff, wbytes);
+    const uint32_t gbase = row0 / R::GROUP;
+    Raw ra[NM][RT], rb[NM][RT];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) R::load_group(ln, wb[m], gbase + wave, rows, sub, ra[m], stride);
+    badx |= ln.load_x(kq::XGlobal{x, 0u});
+    auto finish = [&](const Raw (&raw)[NM][RT], uint32_t gi) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            float v[R::N];
+            R::dot_group(ln, raw[m], l, v, malformed);
+#pragma unroll
+            for (int j = 0; j < R::KEEP; ++j) {
+                const int idx = R::value_index(l, j);
+                if (idx >= 0) {
+                    const uint32_t r = gi * R::GROUP + (uint32_t)idx * R::RPW + sub;
+                    dst[m][r] = first ? v[j] : dst[m][r] + v[j];
+                }
+            }
+        }
+    };
+    /* ping-pong over this wave's groups */
+    uint32_t gi = wave;
+    while (gi < NG) {
+        uint32_t gn = gi + nwaves;
+        if (gn < NG) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) R::load_group(ln, wb[m], gbase + gn, rows, sub, rb[m], stride);
+        }
+        finish(ra, gi);
+        gi = gn;
+        if (gi >= NG) break;
+        gn = gi + nwaves;
+        if (gn < NG) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) R::load_group(ln, wb[m], gbase + gn, rows, sub, ra[m], stride);
+        }
+        finish(rb, gi);
+        gi = gn;
+    }
+}
+
+/* grid: x = groups of kFuseRows rows, y = slot (0..K-1 routed by top-k
+ * position, K the shared expert), z = token; 4 waves */
+template <uint32_t TR, uint32_t TS, uint32_t C0, uint32_t C1>
+__global__ __launch_bounds__(kThreads) void expert_gateup_fused(GateupArgs a) {
+    __shared__ float part[2][kFuseRows];
+    const uint32_t slot = blockIdx.y, t = blockIdx.z;
+    const bool shared = slot == a.top_k;
+    const uint32_t rows = shared ? a.shared_inter : a.inter;
+    const uint32_t row0 = blockIdx.x * kFuseRows;
+    if (row0 >= rows) return;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nwaves = kThreads / 64u;
+    const float *x = a.x + (size_t)t * a.hidden;
+    bool badx = false, malformed = false, bad = false;
+    auto run = [&](auto tag) {
+        constexpr uint32_t T = decltype(tag)::value;
+        const uint32_t stride = shared ? a.srstride : a.rstride;
+        const uint8_t *G, *U;
+        if (shared) {
+            G = a.sgate;
+            U = a.sup;
+        } else {
+            const uint32_t e = a.ids[(size_t)t * a.top_k + slot];
+            G = a.gate + (size_t)e * a.inter * stride;
+            U = a.up + (size_t)e * a.inter * stride;
+        }
+        const uint8_t *const M[2] = {G, U};
+        fuse_segment<T, C0, 2>(M, stride, 0u, rows, row0, x, part, true, wave, nwaves, badx,
+                               malformed);
+        if constexpr (C1 != 0u) {
+            __syncthreads();
+            fuse_segment<T, C1, 2>(M, stride, C0, rows, row0, x + C0, part, false, wave, nwaves,
+                                   badx, malformed);
+        }
+    };
+    if (shared)
+        run(std::integral_constant<uint32_t, TS>{});
+    else
+        run(std::integral_constant<uint32_t, TR>{});
+    __syncthreads();
+    if (threadIdx.x < kFuseRows && row0 + threadIdx.x < rows) {
+        const float gv = part[0][threadIdx.x], uv = part[1][threadIdx.x];
+        const float r = kq_swiglu(gv, uv);
+        bad |= !kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(r);
+        a.act[((size_t)t * (a.top_k + 1u) + slot) * a.act_stride + row0 + threadIdx.x] = r;
+    }
+    if (badx) kq_flag(a.status, KQ_DEV_INPUT);
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+}
+
+/* down and the ordered combine: grid x = groups of kFuseRows output rows,
+ * y = token; one wave per slot (K + 1 <= 16), each forming its slot's rows
+ * into LDS over both segments */
+template <uint32_t TR, uint32_t TS, uint32_t C0, uint32_t C1>
+__global__ __launch_bounds__(1024) void expert_down_fused(DownArgs a) {
+    __shared__ float res[16][kFuseRows];
+    __shared__ uint32_t ord_s[16];
+    __shared__ float w_s[16];
+    const uint32_t t = blockIdx.y, row0 = blockIdx.x * kFuseRows;
+    const uint32_t top_k = a.top_k, nslots = top_k + 1u, hidden = a.hidden;
+    const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (threadIdx.x < top_k) {
+        const uint32_t s = a.order[(size_t)t * top_k + threadIdx.x];
+        ord_s[threadIdx.x] = s;
+        w_s[threadIdx.x] = a.weights[(size_t)t * top_k + s];
+    }
+    bool badx = false, malformed = false, bad = false;
+    if (slot < nslots) {
+        const bool shared = slot == top_k;
+        const float *act = a.act + ((size_t)t * nslots + slot) * a.act_stride;
+        float(*dst)[kFuseRows] = &res[slot];
+        auto run = [&](auto tag) {
+            constexpr uint32_t T = decltype(tag)::value;
+            const uint32_t stride = shared ? a.srstride : a.rstride;
+            const uint8_t *D =
+                shared ? a.sdown
+                       : a.down + (size_t)a.ids[(size_t)t * top_k + slot] * hidden * stride;
+            const uint8_t *const M[1] = {D};
+            /* one wave per slot: it owns every row of its slot, so its two
+             * segments need no barrier between them */
+            fuse_segment<T, C0, 1>(M, stride, 0u, hidden, row0, act, dst, true, 0u, 1u, badx,
+                                   malformed);
+            if constexpr (C1 != 0u)
+                fuse_segment<T, C1, 1>(M, stride, C0, hidden, row0, act + C0, dst, false, 0u, 1u,
+                                       badx, malformed);
+        };
+        if (shared)
+            run(std::integral_constant<uint32_t, TS>{});
+        else
+            run(std::integral_constant<uint32_t, TR>{});
+    }
+    __syncthreads();
+    if (threadIdx.x < kFuseRows && row0 + threadIdx.x < hidden) {
+        const uint32_t i = threadIdx.x;
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < top_k; ++j) {
+            const float o = res[ord_s[j]][i];
+            bad |= !kq_isfinite(o);
+            const float weighted = o * w_s[j];
+            sum = sum + weighted;
+        }
+        const float so = res[top_k][i];
+        const float gated = so * a.shared_scale[t];
+        const float v = sum + gated;
+        bad |= !kq_isfinite(so) || !kq_isfinite(sum) || !kq_isfinite(gated) || !kq_isfinite(v);
+        a.out[(size_t)t * hidden + row0 + i] = v;
+    }
+    /* a non-finite activation is the layer's own intermediate */
+    if (badx || bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+}
+
 template <uint32_t TYPE, uint32_t COLS>
 hipError_t launch_gateup(const GateupArgs &a, uint32_t tokens, uint32_t slot0, uint32_t nslot,
                          uint32_t col0, uint32_t seg, hipStream_t s) {
@@ -1503,6 +1699,45 @@ hipError_t down_width(uint32_t width, const DownArgs &a, uint32_t tokens, uint32
         }
     }
     return hipErrorInvalidValue;
+}
+
+/* The fused launches built: the reference model's layer (Q4_K gate/up with
+ * a Q8_0 shared expert over 2048 + 512 columns; Q5_1 down with a Q8_0
+ * shared expert over 512 + 128) and the same with routed and shared of one
+ * format. Returns false (nothing launched) for other formats and widths. */
+bool gateup_fused(uint32_t tr, uint32_t ts, uint32_t ng, const uint32_t (&gw)[16],
+                  const GateupArgs &a, uint32_t tokens, hipError_t &e, hipStream_t s) {
+    if (ng != 2u || gw[0] != 2048u || gw[1] != 512u || tr != KQ_LAUNCH_Q4_K) return false;
+    const uint32_t rows = a.inter > a.shared_inter ? a.inter : a.shared_inter;
+    const dim3 grid((rows + kFuseRows - 1u) / kFuseRows, a.top_k + 1u, tokens);
+    if (ts == KQ_LAUNCH_Q8_0)
+        hipLaunchKernelGGL((expert_gateup_fused<KQ_LAUNCH_Q4_K, KQ_LAUNCH_Q8_0, 2048u, 512u>),
+                           grid, dim3(kThreads), 0, s, a);
+    else if (ts == KQ_LAUNCH_Q4_K)
+        hipLaunchKernelGGL((expert_gateup_fused<KQ_LAUNCH_Q4_K, KQ_LAUNCH_Q4_K, 2048u, 512u>),
+                           grid, dim3(kThreads), 0, s, a);
+    else
+        return false;
+    e = hipGetLastError();
+    return true;
+}
+
+bool down_fused(uint32_t tr, uint32_t ts, uint32_t nd, const uint32_t (&dw)[16],
+                const DownArgs &a, uint32_t tokens, hipError_t &e, hipStream_t s) {
+    if (nd != 2u || dw[0] != 512u || dw[1] != 128u || tr != KQ_LAUNCH_Q5_1 || a.top_k + 1u > 16u)
+        return false;
+    const dim3 grid((a.hidden + kFuseRows - 1u) / kFuseRows, tokens);
+    const dim3 block(64u * (a.top_k + 1u));
+    if (ts == KQ_LAUNCH_Q8_0)
+        hipLaunchKernelGGL((expert_down_fused<KQ_LAUNCH_Q5_1, KQ_LAUNCH_Q8_0, 512u, 128u>), grid,
+                           block, 0, s, a);
+    else if (ts == KQ_LAUNCH_Q5_1)
+        hipLaunchKernelGGL((expert_down_fused<KQ_LAUNCH_Q5_1, KQ_LAUNCH_Q5_1, 512u, 128u>), grid,
+                           block, 0, s, a);
+    else
+        return false;
+    e = hipGetLastError();
+    return true;
 }
 
 #define KQ_TYPE_SWITCH(TYPE_ID, CALL)                                   \
@@ -1756,7 +1991,8 @@ extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
     /* the shared expert rides in the routed launch when its type matches */
     const bool gsame = w->shared_gate_type == w->gate_type;
     hipError_t e = hipSuccess;
-    for (uint32_t k = 0, col = 0; k < ng && e == hipSuccess; col += gw[k], ++k) {
+    const bool gf = gateup_fused(w->gate_type, w->shared_gate_type, ng, gw, ga, tokens, e, s);
+    for (uint32_t k = 0, col = 0; !gf && k < ng && e == hipSuccess; col += gw[k], ++k) {
         const uint32_t seg = (k == 0u ? kSegFirst : 0u) | (k + 1u == ng ? kSegLast : 0u);
         e = gateup_launch(w->gate_type, gw[k], ga, tokens, 0u, gsame ? K + 1u : K, col, seg, s);
         if (e == hipSuccess && !gsame)
@@ -1780,6 +2016,7 @@ extern "C" hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d,
     da.out = out;
     da.status = status;
     const bool dsame = w->shared_down_type == w->down_type;
+    if (down_fused(w->down_type, w->shared_down_type, nd, dw, da, tokens, e, s)) return e;
     /* a shared expert of its own type is finished (into part[t][K]) before
      * the routed launches that combine it */
     if (!dsame) {

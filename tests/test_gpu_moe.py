@@ -559,7 +559,10 @@ def test_moe_reference_model_layer(ctx):
     (1280, 16, 3, 320, 2, "Q4_K", "Q8_0", "Q6_K", "IQ4_NL"),  # 1024+256, 256+64
     (3072, 16, 2, 256, 1, "Q6_K", "Q4_K", "Q4_K", "Q6_K"),    # 2048+1024 gate/up
     (512, 16, 4, 256, 16, "Q4_K", "Q6_K", "Q8_0", "Q6_K"),    # mixed shared, many tokens
-], ids=["real-64e-3tok", "768x384", "640x96", "1280x320", "3072x256", "mixed-16tok"])
+    (2560, 32, 4, 640, 1, "Q4_K", "Q5_1", "Q8_0", "Q8_0"),    # one launch per role
+    (2560, 64, 8, 640, 1, "Q4_K", "Q5_1", "Q4_K", "Q5_1"),    # one launch, one format
+], ids=["real-64e-3tok", "768x384", "640x96", "1280x320", "3072x256", "mixed-16tok",
+        "fused-ref-formats", "fused-same-formats"])
 def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
     seed = S.W_MOE + 3000 + H + I + T
     out, ids, ref, tr, ex = run_layer(ctx, H, E, K, I, T, g, d, sg, sd, seed)
