@@ -704,8 +704,9 @@ uint64_t kq_hip_sampling_config_owned_bytes(const kq_hip_sampling_config *config
 uint32_t kq_hip_sampling_config_vocabulary_size(const kq_hip_sampling_config *config);
 /* Device scratch bytes a select call needs (kq_sampling_required_scratch_
  * bytes, src/kq_sampling.c:242-244, there host bytes): six arrays of
- * one entry per vocabulary id, the finiteness flags, the sort's work
- * area and the device result record. 0 for an invalid config. */
+ * one entry per vocabulary id, two per 256 ids (finiteness flags and
+ * maxima), the sort's work area and the device result record. 0 for an
+ * invalid config. */
 uint64_t kq_hip_sampling_required_scratch_bytes(const kq_hip_sampling_config *config);
 
 /* The RNG record (src/kq_sampling.c:246-322): host functions, the same

@@ -222,7 +222,8 @@ enum {
     KQ_SAMPLE_OK = 0,
     KQ_SAMPLE_NUMERIC_BEFORE_DRAW = 1,
     KQ_SAMPLE_NUMERIC_IN_DRAW = 2,
-    KQ_SAMPLE_INVALID_TOKEN = 3
+    KQ_SAMPLE_INVALID_TOKEN = 3,
+    KQ_SAMPLE_FULL_SORT = 4 /* the fast path's top did not fit: run _full */
 };
 
 typedef struct kq_launch_sample_out {
@@ -250,13 +251,21 @@ typedef struct kq_launch_sample_args {
     uint32_t *keys, *ids, *sorted_keys, *sorted_ids;
     float *probs;
     uint32_t *bad_per_block; /* ceil(count / 256) */
+    uint32_t *max_per_block; /* ceil(count / 256) */
     void *sort_temp;
     size_t sort_bytes;   /* kq_launch_sample_sort_bytes(count) */
     kq_launch_sample_out *out;
 } kq_launch_sample_args;
 
 hipError_t kq_launch_sample_sort_bytes(uint32_t count, size_t *bytes);
+/* prep, then a tail without the full sort where kq_launch_sample_fast is
+ * nonzero (1: top-k 1..64 over at most 1024 prep blocks; 2: nothing cut,
+ * top-k 0 or the whole vocabulary with top-p 1, more than 4096 ids), else
+ * the full sort and its tail */
 hipError_t kq_launch_sample(const kq_launch_sample_args *args, hipStream_t s);
+int kq_launch_sample_fast(uint32_t count, uint32_t top_k, float top_p);
+/* the full sort and the tail on the prep already in the scratch */
+hipError_t kq_launch_sample_full(const kq_launch_sample_args *args, hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,7 @@ namespace {
 constexpr int kPrepThreads = 256;
 constexpr int kTailThreads = 1024;
 constexpr uint32_t kKeptCap = 4096; /* kept ids sorted in LDS up to this many */
+constexpr int kRun = 8;             /* 64-term chunks a serial walk loads at once */
 
 __device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
@@ -46,11 +47,13 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 __global__ __launch_bounds__(kPrepThreads) void sample_prep(
     const float *__restrict__ logits, uint32_t count, float temperature, float *__restrict__ scores,
     uint32_t *__restrict__ keys, uint32_t *__restrict__ ids, float *__restrict__ probs,
-    uint32_t *__restrict__ bad_per_block) {
+    uint32_t *__restrict__ bad_per_block, uint32_t *__restrict__ max_per_block) {
     __shared__ uint32_t any;
+    __shared__ uint32_t wmax[kPrepThreads / 64];
     if (threadIdx.x == 0) any = 0u;
     __syncthreads();
     const uint32_t i = blockIdx.x * kPrepThreads + threadIdx.x;
+    uint32_t key = 0u; /* below every key of a finite score */
     if (i < count) {
         float v = logits[i];
         bool bad = !kq_isfinite(v);
@@ -59,13 +62,21 @@ __global__ __launch_bounds__(kPrepThreads) void sample_prep(
             bad = bad || !kq_isfinite(v);
         }
         scores[i] = v;
-        keys[i] = order_key(v);
+        key = order_key(v);
+        keys[i] = key;
         ids[i] = i;
         probs[i] = 0.0f;
         if (bad) any = 1u; /* benign race: every writer stores 1 */
     }
+    for (int off = 32; off > 0; off >>= 1) key = max(key, (uint32_t)__shfl_xor((int)key, off));
+    if (threadIdx.x % 64u == 0u) wmax[threadIdx.x / 64u] = key;
     __syncthreads();
-    if (threadIdx.x == 0) bad_per_block[blockIdx.x] = any;
+    if (threadIdx.x == 0) {
+        bad_per_block[blockIdx.x] = any;
+        uint32_t m = wmax[0];
+        for (uint32_t w = 1; w < kPrepThreads / 64u; ++w) m = max(m, wmax[w]);
+        max_per_block[blockIdx.x] = m;
+    }
 }
 
 /* the sampler's device result record (host mirror in kq_launch.h) */
@@ -93,6 +104,17 @@ __device__ __forceinline__ double chain_d(double s, double v) {
 #pragma unroll
     for (int l = 0; l < 64; ++l) s = s + lane_d(v, l);
     return s;
+}
+
+/* kRun chunks of 64 consecutive values from p[i0..], zero past n */
+__device__ __forceinline__ void load_run(const float *p, uint32_t i0, uint32_t n,
+                                         float (&w)[kRun]) {
+    const uint32_t lane = threadIdx.x % 64u;
+#pragma unroll
+    for (int u = 0; u < kRun; ++u) {
+        const uint32_t i = i0 + 64u * (uint32_t)u + lane;
+        w[u] = i < n ? p[i] : 0.0f;
+    }
 }
 
 /* the categorical draw (src/kq_sampling.c:400-447) on one wave: uniform =
@@ -135,8 +157,12 @@ __device__ __forceinline__ void draw(Out *o, double total, uint32_t last, float 
 
 struct TailArgs {
     const float *scores;  /* by id */
-    const uint32_t *skeys; /* ascending */
-    const uint32_t *sids;
+    uint32_t *skeys;       /* ascending */
+    uint32_t *sids;
+    const uint32_t *keys;  /* by id (the fast path's source) */
+    const uint32_t *max_per_block;
+    uint32_t fast;         /* 1: build the sorted top from the block maxima;
+                              2: every id kept, no sorted order */
     float *probs; /* by id, cleared by sample_prep */
     const uint32_t *bad_per_block;
     uint32_t prep_blocks;
@@ -148,13 +174,132 @@ struct TailArgs {
     Out *out;
 };
 
+constexpr uint32_t kFastMaxK = 64;      /* top-k the fast path takes */
+constexpr uint32_t kFastBlocks = 128;   /* blocks it gathers at most */
+
+/* The k-th largest of up to 1024 block maxima by an MSB-first radix select
+ * over 8-bit digits (an LDS histogram per digit), then the gather and sort
+ * of the keys >= it. Returns their count, 0 when they do not fit. vals and
+ * cand are LDS arrays of kKeptCap entries. Every thread of the workgroup
+ * calls it. */
+__device__ uint32_t fast_top(const TailArgs &a, uint32_t *ids_lds, uint32_t *keys_lds) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_sel[2];
+    __shared__ uint32_t blk[kFastBlocks];
+    __shared__ uint32_t s_nb, s_nc;
+    const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;
+    const uint32_t nb = a.prep_blocks;
+    const uint32_t v = tid < nb ? a.max_per_block[tid] : 0u;
+    uint32_t prefix = 0u, mask = 0u, krem = a.top_k;
+    for (int pass = 0; pass < 4; ++pass) {
+        const uint32_t shift = 24u - 8u * (uint32_t)pass;
+        if (tid < 256u) hist[tid] = 0u;
+        __syncthreads();
+        if (tid < nb && (v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
+        __syncthreads();
+        if (wave == 0u) {
+            /* lane l holds digits 255 - 4l .. 252 - 4l (largest first) */
+            uint32_t c[4], tot = 0u;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                c[q] = hist[255u - 4u * lane - (uint32_t)q];
+                tot += c[q];
+            }
+            uint32_t incl = tot;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t y = (uint32_t)__shfl_up((int)incl, off);
+                if (lane >= (uint32_t)off) incl += y;
+            }
+            uint32_t before = incl - tot;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (before < krem && krem <= before + c[q]) {
+                    s_sel[0] = 255u - 4u * lane - (uint32_t)q;
+                    s_sel[1] = krem - before;
+                }
+                before += c[q];
+            }
+        }
+        __syncthreads();
+        prefix |= s_sel[0] << shift;
+        mask |= 255u << shift;
+        krem = s_sel[1];
+        __syncthreads();
+    }
+    const uint32_t t0 = prefix;
+    /* the blocks that can hold a key >= t0 */
+    if (tid == 0u) {
+        s_nb = 0u;
+        s_nc = 0u;
+    }
+    __syncthreads();
+    if (tid < nb && v >= t0) {
+        const uint32_t at = atomicAdd(&s_nb, 1u);
+        if (at < kFastBlocks) blk[at] = tid;
+    }
+    __syncthreads();
+    const uint32_t nbl = s_nb;
+    if (nbl > kFastBlocks) return 0u;
+    /* their keys >= t0 */
+    for (uint32_t j = tid; j < nbl * kPrepThreads; j += kTailThreads) {
+        const uint32_t id = blk[j / kPrepThreads] * kPrepThreads + j % kPrepThreads;
+        if (id < a.count) {
+            const uint32_t key = a.keys[id];
+            if (key >= t0) {
+                const uint32_t at = atomicAdd(&s_nc, 1u);
+                if (at < kKeptCap) {
+                    keys_lds[at] = key;
+                    ids_lds[at] = id;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t nc = s_nc;
+    if (nc > kKeptCap) return 0u;
+    /* sort by (key, id) ascending: bitonic on the 64-bit pair */
+    uint32_t m2 = 1u;
+    while (m2 < nc) m2 <<= 1u;
+    for (uint32_t i = nc + tid; i < m2; i += kTailThreads) {
+        keys_lds[i] = 0xffffffffu;
+        ids_lds[i] = 0xffffffffu;
+    }
+    __syncthreads();
+    for (uint32_t size = 2u; size <= m2; size <<= 1u) {
+        for (uint32_t stride = size / 2u; stride > 0u; stride >>= 1u) {
+            for (uint32_t i = tid; i < m2 / 2u; i += kTailThreads) {
+                const uint32_t lo = 2u * i - (i & (stride - 1u));
+                const uint32_t hi = lo + stride;
+                const bool up = (lo & size) == 0u;
+                const uint64_t x = ((uint64_t)keys_lds[lo] << 32) | ids_lds[lo];
+                const uint64_t y = ((uint64_t)keys_lds[hi] << 32) | ids_lds[hi];
+                if ((x > y) == up) {
+                    keys_lds[lo] = (uint32_t)(y >> 32);
+                    ids_lds[lo] = (uint32_t)y;
+                    keys_lds[hi] = (uint32_t)(x >> 32);
+                    ids_lds[hi] = (uint32_t)x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    /* the last nc positions of the sorted order */
+    for (uint32_t i = tid; i < nc; i += kTailThreads) {
+        a.skeys[a.count - nc + i] = keys_lds[i];
+        a.sids[a.count - nc + i] = ids_lds[i];
+    }
+    __syncthreads();
+    return nc;
+}
+
 __device__ __forceinline__ void fail(Out *o, uint32_t code) {
     if (threadIdx.x == 0) o->status = code;
 }
 
 __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
     __shared__ uint32_t s_ids[kKeptCap];
-    __shared__ float s_w[kKeptCap];
+    __shared__ __align__(16) float s_w[kKeptCap];
     __shared__ uint32_t s_flag;
     __shared__ float s_max_p[kTailThreads / 64];
     __shared__ uint32_t s_u[4];
@@ -170,12 +315,26 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
     __syncthreads();
     if (s_flag) return fail(o, KQ_SAMPLE_NUMERIC_BEFORE_DRAW);
 
+    /* The fast path (1 <= k <= 64, at most 1024 prep blocks): t0 = the k-th
+     * largest block maximum; at least k keys reach it, so the k-th largest
+     * key does, and every key >= t0 sits in a block whose maximum is >= t0.
+     * Those blocks' keys >= t0 are gathered and sorted here by (key, id):
+     * they are the top of the whole sorted order, written to its last
+     * positions. Too many blocks or keys: status FULL_SORT, and the caller
+     * sorts everything. */
+    uint32_t lo0 = 0u;
+    if (a.fast == 1u) {
+        const uint32_t got = fast_top(a, s_ids, reinterpret_cast<uint32_t *>(s_w));
+        if (got == 0u) return fail(o, KQ_SAMPLE_FULL_SORT);
+        lo0 = n - got;
+    }
+
     /* top-k: the first sorted position whose key reaches the k-th largest
      * key (src/kq_sampling.c:660-667) */
-    uint32_t top_start = 0u;
-    if (a.top_k != 0u) {
+    uint32_t top_start = lo0;
+    if (a.top_k != 0u && a.fast != 2u) {
         const uint32_t t = a.skeys[n - a.top_k];
-        uint32_t lo = 0u, hi = n - a.top_k; /* first index in [lo, hi] with key >= t */
+        uint32_t lo = lo0, hi = n - a.top_k; /* first index in [lo, hi] with key >= t */
         while (lo < hi) {
             const uint32_t mid = lo + (hi - lo) / 2u;
             if (a.skeys[mid] < t) lo = mid + 1u;
@@ -183,42 +342,81 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
         }
         top_start = lo;
     }
-    const float maximum = a.scores[a.sids[n - 1u]];
+    /* the largest score: the sorted order's last, or, with nothing to cut
+     * (fast == 2, no sort), the largest block maximum's score (keys of -0
+     * and +0 agree, and either gives the same weights) */
+    float maximum;
+    if (a.fast == 2u) {
+        if (wave == 0u) {
+            uint32_t m = 0u;
+            for (uint32_t b = lane; b < a.prep_blocks; b += 64u) m = max(m, a.max_per_block[b]);
+            for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+            if (lane == 0) s_u[2] = m;
+        }
+        __syncthreads();
+        const uint32_t m = s_u[2];
+        maximum = __uint_as_float((m & 0x80000000u) ? (m & 0x7fffffffu) : ~m);
+    } else {
+        maximum = a.scores[a.sids[n - 1u]];
+    }
 
     /* wave 0: the softmax mass over [top_start, n) in ascending order, then
-     * the top-p walk (src/kq_sampling.c:673-697) */
+     * the top-p walk (src/kq_sampling.c:673-697). The mass only feeds the
+     * top-p walk and a validity check that cannot fail (the largest weight
+     * is expf(0) = 1, the others lie in [0, 1]), so without top-p neither
+     * runs. Terms are gathered kRun at a time per lane, so one load latency
+     * serves 64 * kRun serial adds. */
     if (wave == 0u) {
         float sum = 0.0f;
         bool bad = false;
-        for (uint32_t j0 = top_start; j0 < n; j0 += 64u) {
-            const uint32_t j = j0 + lane;
-            float w = 0.0f;
-            if (j < n) {
-                w = kq_expf(a.scores[a.sids[j]] - maximum);
-                bad = bad || !kq_isfinite(w);
-            }
-            sum = chain_f(sum, w);
-        }
-        bad = __ballot(bad) != 0u;
         uint32_t keep = top_start;
-        if (!bad && kq_isfinite(sum) && sum > 0.0f && a.top_p < 1.0f) {
-            const float cutoff = 1.0f - a.top_p;
-            float c = 0.0f;
-            bool found = false;
-            for (uint32_t j0 = top_start; j0 < n && !found; j0 += 64u) {
-                const uint32_t j = j0 + lane;
-                float p = 0.0f;
-                if (j < n) p = kq_expf(a.scores[a.sids[j]] - maximum) / sum;
+        if (a.top_p < 1.0f) {
+            auto weights = [&](uint32_t j0, float (&w)[kRun]) {
+                uint32_t id[kRun];
 #pragma unroll
-                for (int l = 0; l < 64; ++l) {
-                    c = c + lane_f(p, l);
-                    const uint32_t at = j0 + (uint32_t)l;
-                    if (!found && at < n && (at == n - 1u || c > cutoff)) {
-                        found = true;
-                        keep = at;
+                for (int u = 0; u < kRun; ++u) {
+                    const uint32_t j = j0 + 64u * (uint32_t)u + lane;
+                    id[u] = j < n ? a.sids[j] : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < kRun; ++u) {
+                    const uint32_t j = j0 + 64u * (uint32_t)u + lane;
+                    w[u] = j < n ? kq_expf(a.scores[id[u]] - maximum) : 0.0f;
+                    bad = bad || !kq_isfinite(w[u]);
+                }
+            };
+            for (uint32_t j0 = top_start; j0 < n; j0 += 64u * kRun) {
+                float w[kRun];
+                weights(j0, w);
+#pragma unroll
+                for (int u = 0; u < kRun; ++u) sum = chain_f(sum, w[u]);
+            }
+            bad = __ballot(bad) != 0u;
+            if (!bad && kq_isfinite(sum) && sum > 0.0f) {
+                const float cutoff = 1.0f - a.top_p;
+                float c = 0.0f;
+                bool found = false;
+                for (uint32_t j0 = top_start; j0 < n && !found; j0 += 64u * kRun) {
+                    float w[kRun];
+                    weights(j0, w);
+#pragma unroll
+                    for (int u = 0; u < kRun; ++u) {
+                        const float p = w[u] / sum;
+                        const uint32_t b0 = j0 + 64u * (uint32_t)u;
+#pragma unroll
+                        for (int l = 0; l < 64; ++l) {
+                            c = c + lane_f(p, l);
+                            const uint32_t at = b0 + (uint32_t)l;
+                            if (!found && at < n && (at == n - 1u || c > cutoff)) {
+                                found = true;
+                                keep = at;
+                            }
+                        }
                     }
                 }
             }
+        } else {
+            sum = 1.0f;
         }
         if (lane == 0) {
             s_u[0] = bad || !kq_isfinite(sum) || !(sum > 0.0f) ? 1u : 0u;
@@ -331,17 +529,29 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
         return;
     }
 
-    /* many kept ids: weights scattered into the by-id array, then walks over
-     * the whole vocabulary in id order */
-    for (uint32_t j = keep + tid; j < n; j += kTailThreads) {
-        const uint32_t id = a.sids[j];
-        a.probs[id] = kq_expf(a.scores[id] - maximum);
+    /* many kept ids: weights scattered into the by-id array (every id's when
+     * nothing is cut, without the sort), then walks over the whole
+     * vocabulary in id order */
+    if (a.fast == 2u) {
+        for (uint32_t i = tid; i < n; i += kTailThreads) a.probs[i] = kq_expf(a.scores[i] - maximum);
+    } else {
+        for (uint32_t j = keep + tid; j < n; j += kTailThreads) {
+            const uint32_t id = a.sids[j];
+            a.probs[id] = kq_expf(a.scores[id] - maximum);
+        }
     }
     __syncthreads();
+    const uint32_t runs = (n + 64u * kRun - 1u) / (64u * kRun);
     if (wave == 0u) {
-        for (uint32_t i0 = 0u; i0 < n; i0 += 64u) {
-            const uint32_t i = i0 + lane;
-            sum2 = chain_f(sum2, i < n ? a.probs[i] : 0.0f);
+        float w[kRun], nx[kRun];
+        load_run(a.probs, 0u, n, w);
+        for (uint32_t r = 0u; r < runs; ++r) {
+            load_run(a.probs, (r + 1u) * 64u * kRun, n, nx);
+#pragma unroll
+            for (int u = 0; u < kRun; ++u) {
+                sum2 = chain_f(sum2, w[u]);
+                w[u] = nx[u];
+            }
         }
         if (lane == 0) s_f[2] = sum2;
     }
@@ -365,50 +575,76 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
         if (lane == 0) s_max_p[wave] = bad ? -1.0f : maxp;
     }
     __syncthreads();
-    if (wave == 0u) {
-        float maxp = lane < kTailThreads / 64u ? s_max_p[lane] : 0.0f;
-        bool bad = __ballot(maxp < 0.0f) != 0u;
-        for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
-        for (uint32_t i0 = 0u; i0 < n; i0 += 64u) {
-            const uint32_t i = i0 + lane;
-            norm_sum = chain_f(norm_sum, i < n ? a.probs[i] : 0.0f);
-        }
-        if (bad || !kq_isfinite(norm_sum) || !(norm_sum > 0.0f)) {
-            if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_BEFORE_DRAW;
-            return;
-        }
-        double total = 0.0;
-        uint32_t last = 0xffffffffu;
-        float last_p = 0.0f;
-        for (uint32_t i0 = 0u; i0 < n; i0 += 64u) {
-            const uint32_t i = i0 + lane;
-            const float p = i < n ? a.probs[i] : 0.0f;
-            total = chain_d(total, (double)p);
-            const uint64_t has = __ballot(p > 0.0f);
-            if (has) {
-                const int hl = 63 - __builtin_clzll(has);
-                last = i0 + (uint32_t)hl;
-                last_p = lane_f(p, hl);
-            }
-        }
-        draw(o, total, last, last_p, a.word, [&](double thr, uint32_t &sel, float &selp) {
-            double cum = 0.0;
-            for (uint32_t i0 = 0u; i0 < n && sel == 0xffffffffu; i0 += 64u) {
-                const uint32_t i = i0 + lane;
-                const float p = i < n ? a.probs[i] : 0.0f;
-                const double pd = (double)p;
+    if (wave != 0u) return;
+    float maxp = lane < kTailThreads / 64u ? s_max_p[lane] : 0.0f;
+    const bool bad = __ballot(maxp < 0.0f) != 0u;
+    for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
+    /* one pass for the float mass of the normalised values and the binary64
+     * total the draw uses, both in id order; the total's running value at
+     * the end of every group of `every` runs is kept in LDS, so the draw
+     * walks only the group where the running sum first passes its
+     * threshold, starting from the value the full walk would hold there */
+    double *s_cp = reinterpret_cast<double *>(s_w); /* kKeptCap / 2 entries */
+    const uint32_t every = (runs + kKeptCap / 2u - 1u) / (kKeptCap / 2u);
+    double total = 0.0;
+    uint32_t last = 0xffffffffu;
+    float last_p = 0.0f;
+    {
+        float w[kRun], nx[kRun];
+        load_run(a.probs, 0u, n, w);
+        for (uint32_t r = 0u; r < runs; ++r) {
+            load_run(a.probs, (r + 1u) * 64u * kRun, n, nx);
+#pragma unroll
+            for (int u = 0; u < kRun; ++u) {
 #pragma unroll
                 for (int l = 0; l < 64; ++l) {
-                    cum = cum + lane_d(pd, l);
-                    const float pl = lane_f(p, l);
-                    if (sel == 0xffffffffu && pl > 0.0f && thr < cum) {
-                        sel = i0 + (uint32_t)l;
-                        selp = pl;
-                    }
+                    const float pl = lane_f(w[u], l);
+                    norm_sum = norm_sum + pl;
+                    total = total + (double)pl;
+                }
+                const uint64_t has = __ballot(w[u] > 0.0f);
+                if (has) {
+                    const int hl = 63 - __builtin_clzll(has);
+                    last = (r * kRun + (uint32_t)u) * 64u + (uint32_t)hl;
+                    last_p = lane_f(w[u], hl);
+                }
+                w[u] = nx[u];
+            }
+            if ((r + 1u) % every == 0u || r + 1u == runs)
+                if (lane == 0) s_cp[r / every] = total;
+        }
+    }
+    if (bad || !kq_isfinite(norm_sum) || !(norm_sum > 0.0f)) {
+        if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_BEFORE_DRAW;
+        return;
+    }
+    const uint32_t groups = (runs + every - 1u) / every;
+    draw(o, total, last, last_p, a.word, [&](double thr, uint32_t &sel, float &selp) {
+        /* the first group whose end value passes the threshold; running
+         * sums never decrease, so no earlier id can pass it */
+        uint32_t g = groups;
+        for (uint32_t g0 = 0u; g0 < groups && g == groups; g0 += 64u) {
+            const uint32_t gi = g0 + lane;
+            const uint64_t hit = __ballot(gi < groups && thr < s_cp[gi]);
+            if (hit) g = g0 + (uint32_t)__builtin_ctzll(hit);
+        }
+        if (g == groups) return;
+        double cum = g == 0u ? 0.0 : s_cp[g - 1u];
+        const uint32_t end = min(n, (g + 1u) * every * 64u * kRun);
+        for (uint32_t i0 = g * every * 64u * kRun; i0 < end && sel == 0xffffffffu; i0 += 64u) {
+            const uint32_t i = i0 + lane;
+            const float p = i < n ? a.probs[i] : 0.0f;
+#pragma unroll
+            for (int l = 0; l < 64; ++l) {
+                const float pl = lane_f(p, l);
+                cum = cum + (double)pl;
+                if (sel == 0xffffffffu && pl > 0.0f && thr < cum) {
+                    sel = i0 + (uint32_t)l;
+                    selp = pl;
                 }
             }
-        }, n - top_start, kept, maxp, norm_sum, a.canonical);
-    }
+        }
+    }, n - top_start, kept, maxp, norm_sum, a.canonical);
 }
 
 }  // namespace
@@ -422,26 +658,28 @@ extern "C" hipError_t kq_launch_sample_sort_bytes(uint32_t count, size_t *bytes)
     return e;
 }
 
-extern "C" hipError_t kq_launch_sample(const kq_launch_sample_args *p, hipStream_t s) {
-    const uint32_t n = p->count;
-    if (n == 0u || p->top_k > n) return hipErrorInvalidValue;
-    const uint32_t blocks = (n + kPrepThreads - 1u) / kPrepThreads;
-    hipLaunchKernelGGL(sample_prep, dim3(blocks), dim3(kPrepThreads), 0, s, p->logits, n,
-                       p->temperature, p->scores, p->keys, p->ids, p->probs, p->bad_per_block);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    size_t tmp = p->sort_bytes;
-    e = rocprim::radix_sort_pairs(p->sort_temp, tmp, p->keys, p->sorted_keys, p->ids,
-                                  p->sorted_ids, n, 0u, 32u, s);
-    if (e != hipSuccess) return e;
+extern "C" int kq_launch_sample_fast(uint32_t count, uint32_t top_k, float top_p) {
+    const uint32_t blocks = (count + kPrepThreads - 1u) / kPrepThreads;
+    if (top_k >= 1u && top_k <= kFastMaxK && top_k <= blocks && blocks <= 1024u) return 1;
+    if ((top_k == 0u || top_k == count) && !(top_p < 1.0f) && count > kKeptCap) return 2;
+    return 0;
+}
+
+/* full != 0: sort every key (rocPRIM) after the prep; else the fast path,
+ * whose tail reports KQ_SAMPLE_FULL_SORT when its top does not fit (then
+ * kq_launch_sample_full runs the sort and the tail again on the same prep) */
+static hipError_t launch_tail(const kq_launch_sample_args *p, uint32_t fast, hipStream_t s) {
     TailArgs a;
     a.scores = p->scores;
     a.skeys = p->sorted_keys;
     a.sids = p->sorted_ids;
+    a.keys = p->keys;
+    a.max_per_block = p->max_per_block;
+    a.fast = fast;
     a.probs = p->probs;
     a.bad_per_block = p->bad_per_block;
-    a.prep_blocks = blocks;
-    a.count = n;
+    a.prep_blocks = (p->count + kPrepThreads - 1u) / kPrepThreads;
+    a.count = p->count;
     a.canonical = p->canonical;
     a.top_k = p->top_k;
     a.top_p = p->top_p;
@@ -449,4 +687,26 @@ extern "C" hipError_t kq_launch_sample(const kq_launch_sample_args *p, hipStream
     a.out = p->out;
     hipLaunchKernelGGL(sample_tail, dim3(1), dim3(kTailThreads), 0, s, a);
     return hipGetLastError();
+}
+
+extern "C" hipError_t kq_launch_sample(const kq_launch_sample_args *p, hipStream_t s) {
+    const uint32_t n = p->count;
+    if (n == 0u || p->top_k > n) return hipErrorInvalidValue;
+    const uint32_t blocks = (n + kPrepThreads - 1u) / kPrepThreads;
+    hipLaunchKernelGGL(sample_prep, dim3(blocks), dim3(kPrepThreads), 0, s, p->logits, n,
+                       p->temperature, p->scores, p->keys, p->ids, p->probs, p->bad_per_block,
+                       p->max_per_block);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int fast = kq_launch_sample_fast(n, p->top_k, p->top_p);
+    if (fast) return launch_tail(p, (uint32_t)fast, s);
+    return kq_launch_sample_full(p, s);
+}
+
+extern "C" hipError_t kq_launch_sample_full(const kq_launch_sample_args *p, hipStream_t s) {
+    size_t tmp = p->sort_bytes;
+    hipError_t e = rocprim::radix_sort_pairs(p->sort_temp, tmp, p->keys, p->sorted_keys, p->ids,
+                                             p->sorted_ids, p->count, 0u, 32u, s);
+    if (e != hipSuccess) return e;
+    return launch_tail(p, 0u, s);
 }

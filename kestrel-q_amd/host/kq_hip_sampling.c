@@ -42,7 +42,7 @@ typedef struct scratch_layout {
     float *scores;
     uint32_t *keys, *ids, *sorted_keys, *sorted_ids;
     float *probs;
-    uint32_t *bad;
+    uint32_t *bad, *bmax;
     void *sort_temp;
 } scratch_layout;
 
@@ -51,7 +51,7 @@ static uint64_t round256(uint64_t n) { return (n + 255u) & ~(uint64_t)255u; }
 static uint64_t layout_bytes(uint32_t v, uint64_t sort_bytes) {
     const uint64_t arr = round256((uint64_t)v * 4u);
     const uint64_t bad = round256((((uint64_t)v + PREP_THREADS - 1u) / PREP_THREADS) * 4u);
-    return 256u + 6u * arr + bad + round256(sort_bytes);
+    return 256u + 6u * arr + 2u * bad + round256(sort_bytes);
 }
 
 static void carve(const kq_hip_sampling_config *cfg, void *scratch, scratch_layout *l) {
@@ -74,6 +74,8 @@ static void carve(const kq_hip_sampling_config *cfg, void *scratch, scratch_layo
     l->probs = (float *)p;
     p += arr;
     l->bad = (uint32_t *)p;
+    p += bad;
+    l->bmax = (uint32_t *)p;
     p += bad;
     l->sort_temp = p;
 }
@@ -356,6 +358,7 @@ static kq_status run_select(kq_hip_context *ctx, const kq_hip_sampling_config *c
     a.sorted_ids = l.sorted_ids;
     a.probs = l.probs;
     a.bad_per_block = l.bad;
+    a.max_per_block = l.bmax;
     a.sort_temp = l.sort_temp;
     a.sort_bytes = (size_t)cfg->sort_bytes;
     a.out = l.out;
@@ -369,6 +372,19 @@ static kq_status run_select(kq_hip_context *ctx, const kq_hip_sampling_config *c
     }
     st = kqi_context_drain(ctx, diag); /* the LM head's flags, when fused */
     if (st != KQ_STATUS_OK) return st;
+    if (rec.status == KQ_SAMPLE_FULL_SORT) {
+        /* the fast path's top did not fit (ties): sort everything */
+        e = (int)kq_launch_sample_full(&a, (hipStream_t)kqi_context_stream_ptr(ctx));
+        if (e == 0)
+            e = (int)hipMemcpyAsync(&rec, l.out, sizeof(rec), hipMemcpyDeviceToHost,
+                                    (hipStream_t)kqi_context_stream_ptr(ctx));
+        if (e != 0) {
+            (void)kqi_context_drain(ctx, NULL);
+            return kqi_hip_fail(diag, e, "sampler launch");
+        }
+        st = kqi_context_drain(ctx, diag);
+        if (st != KQ_STATUS_OK) return st;
+    }
     switch (rec.status) {
     case KQ_SAMPLE_OK:
     case KQ_SAMPLE_INVALID_TOKEN:

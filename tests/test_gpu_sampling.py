@@ -158,13 +158,15 @@ def test_seeded_logits_full_vocabulary(ctx, pi):
     s.close()
 
 
-# vocabularies around the wave (64), the prep block (256) and the in-LDS
-# kept-id sort's capacity (4096)
+# vocabularies around the wave (64), the prep block (256), the in-LDS
+# kept-id sort's capacity (4096) and the draw's 2048 LDS checkpoints of 512
+# ids each (past 1,048,576 ids a checkpoint covers several runs)
 SMALL = [(1, 1), (2, 1), (63, 60), (64, 64), (65, 65), (1000, 997), (4096, 4096),
-         (4097, 4000), (8191, 8191), (70001, 69000)]
+         (4097, 4000), (8191, 8191), (70001, 69000), (1200007, 1200000)]
 SMALL_POL = [{"temperature": 1.0, "top_k": 0, "top_p": 1.0},
              {"temperature": 0.5, "top_k": 0, "top_p": 0.8},
-             {"temperature": 1.0, "top_k": 3, "top_p": 0.95}]
+             {"temperature": 1.0, "top_k": 3, "top_p": 0.95},
+             {"temperature": 0.9, "top_k": 1 << 30, "top_p": 1.0}]  # top-k = vocabulary
 
 
 @pytest.mark.parametrize("vocab,canonical", SMALL, ids=[f"{v}-{c}" for v, c in SMALL])
