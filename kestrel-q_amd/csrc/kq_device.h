@@ -178,12 +178,18 @@ __device__ __forceinline__ void kq_lds_barrier() {
  * offset lies at or beyond the byte count read as zero without touching
  * memory. Word 3 = 0x00020000 is the raw-buffer format of the gfx9 family.
  */
-struct KqBuf {
+template <int AUX>
+struct KqBufA {
     __amdgpu_buffer_rsrc_t r;
 };
+/* AUX is the loads' cache policy: 0 the default, kKqNt non-temporal (nt:
+ * the lines are marked for early eviction) */
+using KqBuf = KqBufA<0>;
+constexpr int kKqNt = 2;
 
-__device__ __forceinline__ KqBuf kq_buf(const void *base, uint32_t bytes) {
-    KqBuf b;
+template <int AUX = 0>
+__device__ __forceinline__ KqBufA<AUX> kq_buf(const void *base, uint32_t bytes) {
+    KqBufA<AUX> b;
     b.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
                                             0x00020000);
     return b;
@@ -193,21 +199,26 @@ typedef unsigned int kq_u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int kq_u32x3 __attribute__((ext_vector_type(3)));
 typedef unsigned int kq_u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint4 kq_ld128(KqBuf b, uint32_t voff, uint32_t soff) {
-    const kq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)voff, (int)soff, 0);
+template <int A>
+__device__ __forceinline__ uint4 kq_ld128(KqBufA<A> b, uint32_t voff, uint32_t soff) {
+    const kq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)voff, (int)soff, A);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ kq_u32x3 kq_ld96(KqBuf b, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b96(b.r, (int)voff, (int)soff, 0);
+template <int A>
+__device__ __forceinline__ kq_u32x3 kq_ld96(KqBufA<A> b, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b96(b.r, (int)voff, (int)soff, A);
 }
-__device__ __forceinline__ kq_u32x2 kq_ld64(KqBuf b, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)voff, (int)soff, 0);
+template <int A>
+__device__ __forceinline__ kq_u32x2 kq_ld64(KqBufA<A> b, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)voff, (int)soff, A);
 }
-__device__ __forceinline__ uint32_t kq_ld32(KqBuf b, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)voff, (int)soff, 0);
+template <int A>
+__device__ __forceinline__ uint32_t kq_ld32(KqBufA<A> b, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)voff, (int)soff, A);
 }
-__device__ __forceinline__ uint32_t kq_ld16(KqBuf b, uint32_t voff, uint32_t soff) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.r, (int)voff, (int)soff, 0);
+template <int A>
+__device__ __forceinline__ uint32_t kq_ld16(KqBufA<A> b, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.r, (int)voff, (int)soff, A);
 }
 
 /*

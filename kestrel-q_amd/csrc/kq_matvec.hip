@@ -91,7 +91,7 @@ __global__ __launch_bounds__(NT) void matvec_kernel(
     const uint8_t *__restrict__ W, uint32_t rows, uint32_t row_bytes,
     const float *__restrict__ x, uint32_t x_stride, float *y, const float *y_prev,
     uint32_t *status, float *part_v, uint32_t *part_i, uint32_t part_stride) {
-    using R = kq::Rows<TYPE, COLS, B, RT>;
+    using R = kq::Rows<TYPE, COLS, B, RT, typename kq::MatvecLane<TYPE, B>::T>;
     using Raw = typename R::Raw;
     const uint32_t lane = threadIdx.x & 63u;
     /* uniform across the wave: the group loop and the full-group test stay
@@ -105,7 +105,8 @@ __global__ __launch_bounds__(NT) void matvec_kernel(
     typename R::Lane ln;
     ln.setup(l);
     const uint32_t wbytes = (rows - 1u) * row_bytes + R::RB;
-    const KqBuf wb = kq_buf(W, wbytes);
+    /* one group per wave (small matrices): non-temporal weight loads */
+    const auto wb = kq_buf<(RT == 1 ? kKqNt : 0)>(W, wbytes);
     Raw ra[RT], rb[RT];
     uint32_t g = wave;
     /* The workgroup requests its activations (once, into LDS), then every
@@ -113,14 +114,14 @@ __global__ __launch_bounds__(NT) void matvec_kernel(
      * loads complete first, are checked and written to LDS behind an
      * LDS-only barrier while the weights are still in flight. The check is
      * flagged at the end. */
-    using XS = kq::XStage<R, B, NT>;
+    using XS = kq::StageFor<R, B, NT>;
     __shared__ __align__(16) float4 xs[XS::NP];
     XS stage;
     stage.issue(x, x_stride, threadIdx.x);
     R::load_group_oob(ln, wb, g, rows, sub, ra, row_bytes, wbytes + 64u);
     const bool xbad = stage.commit(xs, threadIdx.x);
     kq_lds_barrier();
-    ln.load_x(kq::XLds{xs, l, R::LPR});
+    stage.load(ln, xs, l);
 
     bool bad = false, malformed = false;
     float best_v[B];

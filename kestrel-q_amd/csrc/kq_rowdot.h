@@ -16,6 +16,8 @@
 #ifndef KQ_ROWDOT_H
 #define KQ_ROWDOT_H
 
+#include <type_traits>
+
 #include "kq_device.h"
 
 namespace kq {
@@ -129,7 +131,8 @@ struct LaneQ4K {
         return bad;
     }
     /* row_off: byte offset of the row in the buffer */
-    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
         Raw r;
         r.hd = kq_ld128(b, row_off + off, 0u);
         r.qs = kq_ld128(b, row_off + off + qoff, 0u);
@@ -170,6 +173,119 @@ struct LaneQ4K {
             v = fmaf(-ml, sxl[b], v);
             v = fmaf(dh, sh, v);
             v = fmaf(-mh, sxh[b], v);
+            acc[b] = v;
+        }
+    }
+};
+
+/* ---------- Q4_K with integer dots over activation byte planes ----------
+ * The same lane layout and loads as LaneQ4K. The activations come staged
+ * (XStageI) as integers: per 16 consecutive columns one power of two
+ * pw = 2^-k and X = rint(x * 2^k) with |X| <= 2^22, stored as three byte
+ * planes X = X0 + 2^8 X1 + 2^16 X2 (X0, X1 unsigned, X2 signed), four
+ * columns per 32-bit word. A code word's four 4-bit codes meet each plane in
+ * one v_dot4 (exact integer sums); the 16-column sub-block sum is rebuilt in
+ * int32 (|sum| <= 16 * 15 * 2^22 < 2^31), converted once and scaled by
+ * d * sc * pw; the block minimum uses the staged fp32 column sum. Against
+ * the fp32 products this moves each activation by at most 2^-23 of the
+ * largest magnitude among its 16 columns, below the fp32 summation error
+ * the results are compared with. */
+template <int B>
+struct LaneQ4KI {
+    static constexpr uint32_t kBlockBytes = 144u;
+    static constexpr bool kDigits = true;
+    using Raw = typename LaneQ4K<B>::Raw;
+    uint32_t off, qoff;
+    uint32_t sel_a, sel_b, lo_mask;
+    uint32_t xd[B][2][3][4];     /* [batch][low/high group][plane][word] */
+    float pw[B][2], sx[B][2];
+
+    __device__ __forceinline__ void setup(uint32_t l) {
+        const uint32_t bb = l >> 3, c = l & 7u, h = c & 1u, gq = c >> 1;
+        off = kBlockBytes * bb;
+        qoff = 16u + 32u * gq + 16u * h;
+        /* scale bytes of sub-blocks 2gq, 2gq + 1 (src/kq_numeric.c:214-227):
+         * q[2p], q[2p+1] and q[4+2p], q[5+2p] for p = gq & 1, in one word */
+        const uint32_t p2 = 2u * (gq & 1u);
+        sel_b = p2 | (p2 + 1u) << 8 | (p2 + 4u) << 16 | (p2 + 5u) << 24;
+        sel_a = p2 | (p2 + 1u) << 8 | p2 << 16 | (p2 + 1u) << 24;
+        lo_mask = gq < 2u ? 0xffffffffu : 0u;
+    }
+    /* the staged image (XStageI): slots 0..3 of lane l hold its low group's
+     * record, 4..7 its high group's, at [b][slot][l] */
+    __device__ __forceinline__ void load_digits(const uint4 *img, uint32_t l, uint32_t lpr) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+#pragma unroll
+            for (int hg = 0; hg < 2; ++hg) {
+                const uint4 *r = img + ((uint32_t)b * 8u + 4u * (uint32_t)hg) * lpr + l;
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) {
+                    const uint4 w = r[(uint32_t)pl * lpr];
+                    xd[b][hg][pl][0] = w.x;
+                    xd[b][hg][pl][1] = w.y;
+                    xd[b][hg][pl][2] = w.z;
+                    xd[b][hg][pl][3] = w.w;
+                }
+                const uint4 t = r[3u * lpr];
+                pw[b][hg] = __uint_as_float(t.x);
+                sx[b][hg] = __uint_as_float(t.y);
+            }
+        }
+    }
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
+        Raw r;
+        r.hd = kq_ld128(b, row_off + off, 0u);
+        r.qs = kq_ld128(b, row_off + off + qoff, 0u);
+        return r;
+    }
+    __device__ __forceinline__ Raw zero() const {
+        Raw r;
+        r.hd = make_uint4(0, 0, 0, 0);
+        r.qs = make_uint4(0, 0, 0, 0);
+        return r;
+    }
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const float d = kq_f16_to_f32_hw(r.hd.x);
+        const float dmin = kq_f16_to_f32_hw(r.hd.x >> 16);
+        malformed |= !kq_isfinite(d) || !kq_isfinite(dmin);
+        /* [sc0, sc1, m0, m1] as bytes: 6-bit fields of q[0..7] for
+         * sub-blocks 0..3, else the low/high nibbles of q[8..11] with the
+         * top two bits of q[0..7] */
+        const uint32_t wb = __builtin_amdgcn_perm(r.hd.z, r.hd.y, sel_b);
+        const uint32_t wa = __builtin_amdgcn_perm(r.hd.w, r.hd.w, sel_a);
+        uint32_t hi = (wa & 0x00000f0fu) | ((wa >> 4) & 0x0f0f0000u);
+        hi |= (wb >> 2) & 0x30303030u;
+        const uint32_t sm = ((wb & 0x3f3f3f3fu) & lo_mask) | (hi & ~lo_mask);
+        const float dl = d * (float)(sm & 0xffu), dh = d * (float)((sm >> 8) & 0xffu);
+        const float ml = dmin * (float)((sm >> 16) & 0xffu), mh = dmin * (float)(sm >> 24);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t cl[4], ch[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            cl[w] = q[w] & 0x0f0f0f0fu;
+            ch[w] = (q[w] >> 4) & 0x0f0f0f0fu;
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            uint32_t l0 = 0u, l1 = 0u, h0 = 0u, h1 = 0u;
+            int l2 = 0, h2 = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                l0 = __builtin_amdgcn_udot4(cl[w], xd[b][0][0][w], l0, false);
+                l1 = __builtin_amdgcn_udot4(cl[w], xd[b][0][1][w], l1, false);
+                l2 = __builtin_amdgcn_sdot4((int)cl[w], (int)xd[b][0][2][w], l2, false);
+                h0 = __builtin_amdgcn_udot4(ch[w], xd[b][1][0][w], h0, false);
+                h1 = __builtin_amdgcn_udot4(ch[w], xd[b][1][1][w], h1, false);
+                h2 = __builtin_amdgcn_sdot4((int)ch[w], (int)xd[b][1][2][w], h2, false);
+            }
+            const int sl = (int)(l0 + (l1 << 8) + ((uint32_t)l2 << 16));
+            const int sh = (int)(h0 + (h1 << 8) + ((uint32_t)h2 << 16));
+            float v = (float)sl * (dl * pw[b][0]);
+            v = fmaf(-ml, sx[b][0], v);
+            v = fmaf((float)sh, dh * pw[b][1], v);
+            v = fmaf(-mh, sx[b][1], v);
             acc[b] = v;
         }
     }
@@ -232,7 +348,8 @@ struct LaneQ6K {
         r.y = back ? w.z : kq_align2(w.z, w.y, sh);
         return r;
     }
-    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
         const uint32_t p = row_off + off;
         Raw r;
         r.sh = p & 3u; /* every field of a block shares the block's alignment */
@@ -338,7 +455,8 @@ struct LaneQ8 {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
         const uint32_t bo = row_off + off;
         Raw r;
         r.sh = bo & 3u;
@@ -435,7 +553,8 @@ struct LaneQ5K {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
         Raw r;
         r.hd = kq_ld128(b, row_off + off, 0u);
         r.qh = kq_ld128(b, row_off + off + hoff, 0u);
@@ -528,7 +647,8 @@ struct LaneQ51 {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
         Raw r;
         r.hdr = kq_ld64(b, row_off + off, 0u);
         r.qs = kq_ld128(b, row_off + off + 8u, 0u);
@@ -625,7 +745,8 @@ struct LaneIQ4NL {
         }
         return bad;
     }
-    __device__ __forceinline__ Raw load(KqBuf b, uint32_t row_off) const {
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
         const uint32_t bo = row_off + off;
         Raw r;
         r.sh = bo & 3u;
@@ -719,9 +840,9 @@ __host__ __device__ constexpr uint32_t row_bytes(uint32_t cols) {
  * such passes per group (GROUP = RPW*RT rows). load_group issues every load
  * of a group; groups entirely below `rows` take the unguarded path.
  */
-template <uint32_t TYPE, uint32_t COLS, int B, int RT>
+template <uint32_t TYPE, uint32_t COLS, int B, int RT, class LaneT = typename LaneFor<TYPE, B>::T>
 struct Rows {
-    using Lane = typename LaneFor<TYPE, B>::T;
+    using Lane = LaneT;
     using Raw = typename Lane::Raw;
     static constexpr uint32_t LPR = lanes_per_row<TYPE>(COLS);
     static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "row must fit a wave");
@@ -737,7 +858,8 @@ struct Rows {
 
     /* stride: bytes from one row to the next (RB, or more when the rows
      * are column segments of longer rows) */
-    __device__ static __forceinline__ void load_group(const Lane &ln, KqBuf W, uint32_t g,
+    template <int A>
+    __device__ static __forceinline__ void load_group(const Lane &ln, KqBufA<A> W, uint32_t g,
                                                       uint32_t rows, uint32_t sub,
                                                       Raw (&raw)[RT], uint32_t stride = RB) {
         const uint32_t row0 = g * GROUP + sub;
@@ -757,7 +879,8 @@ struct Rows {
      * `oob` (at least 64 bytes past the buffer's end, so every window of the
      * row lies outside it), which the hardware returns as zeros, the value
      * of zero() */
-    __device__ static __forceinline__ void load_group_oob(const Lane &ln, KqBuf W, uint32_t g,
+    template <int A>
+    __device__ static __forceinline__ void load_group_oob(const Lane &ln, KqBufA<A> W, uint32_t g,
                                                           uint32_t rows, uint32_t sub,
                                                           Raw (&raw)[RT], uint32_t stride,
                                                           uint32_t oob) {
@@ -834,7 +957,118 @@ struct XStage {
         }
         return bad;
     }
+    template <class L>
+    __device__ __forceinline__ void load(L &ln, const float4 *xs, uint32_t l) const {
+        ln.load_x(XLds{xs, l, LPR});
+    }
 };
+
+/* Activation staging for the integer-digit lanes: the same loads, then per
+ * 16 consecutive columns (four threads, one float4 each) the largest
+ * magnitude m, k = min(22 - e, 149) for m = f * 2^e with f in [0.5, 1)
+ * (so |x| * 2^k < 2^22), X = rint(x * 2^k), the byte planes of X and the
+ * fp32 column sum. A group's record is four 16-byte slots: the plane 0, 1
+ * and 2 words of its four column quads, then 2^-k and the sum. Each group
+ * is read by one lane of a row (columns 256bb + 64gq + 16h + 0..15 as its
+ * low group, + 32 as its high one; Q4_K lane 8bb + 2gq + h), so records go
+ * to [b][slot][lane] (slots 0..3 low, 4..7 high) and consecutive lanes read
+ * consecutive 16-byte words. The image has the size of XStage's. */
+template <class R, int B, int NT>
+struct XStageI {
+    static constexpr uint32_t NG = R::kCols / 16u;       /* groups per batch column */
+    static constexpr uint32_t LPR = R::LPR;              /* = kCols / 32 */
+    static constexpr uint32_t NQ = (uint32_t)B * NG * 4u; /* float4 items */
+    static constexpr uint32_t NP = NQ;                  /* float4 words of the image */
+    static constexpr int NX = (int)((NQ + (uint32_t)NT - 1u) / (uint32_t)NT);
+    static_assert(NT % 4 == 0 && R::kCols % 16u == 0u, "column quads of a group share a quad");
+    kq_u32x4 v[NX];
+
+    __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid) {
+        const uint32_t bytes = ((uint32_t)(B - 1) * stride + R::kCols) * 4u;
+        const KqBuf xb = kq_buf(x, bytes);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
+            const uint32_t b = p / (4u * NG), k = (p % (4u * NG)) * 4u;
+            const uint32_t off = p < NQ ? (b * stride + k) * 4u : bytes;
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(xb.r, (int)off, 0, 0);
+        }
+    }
+    __device__ __forceinline__ bool commit(float4 *xs, uint32_t tid) const {
+        uint32_t *img = reinterpret_cast<uint32_t *>(xs);
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
+            /* uniform over a quad: NQ and NT are multiples of 4 */
+            if (NQ % (uint32_t)NT == 0u || p < NQ) {
+                const float f[4] = {__uint_as_float(v[i].x), __uint_as_float(v[i].y),
+                                    __uint_as_float(v[i].z), __uint_as_float(v[i].w)};
+                float m = 0.0f, sum = (f[0] + f[1]) + (f[2] + f[3]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    bad |= !kq_isfinite(f[j]);
+                    m = fmaxf(m, fabsf(f[j]));
+                }
+                m = fmaxf(m, kq_dpp_pair<1>(m));
+                m = fmaxf(m, kq_dpp_pair<2>(m));
+                sum += kq_dpp_pair<1>(sum);
+                sum += kq_dpp_pair<2>(sum);
+                const int e = __builtin_amdgcn_frexp_expf(m);
+                const int k = min(22 - e, 149);
+                uint32_t X[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) X[j] = (uint32_t)(int)rintf(ldexpf(f[j], k));
+                const uint32_t p01 = __builtin_amdgcn_perm(X[1], X[0], 0x05010400u);
+                const uint32_t p23 = __builtin_amdgcn_perm(X[3], X[2], 0x05010400u);
+                const uint32_t w0 = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+                const uint32_t w1 = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
+                const uint32_t w2 = __builtin_amdgcn_perm(X[1], X[0], 0x0c0c0602u) |
+                                    __builtin_amdgcn_perm(X[3], X[2], 0x06020c0cu);
+                const uint32_t gb = p / 4u, qd = p % 4u;
+                const uint32_t b = gb / NG, g = gb % NG, r = g % 16u, t = r % 4u;
+                const uint32_t lane = 8u * (g / 16u) + 2u * (r / 4u) + (t & 1u);
+                /* dword of slot j, component c */
+                const uint32_t base = ((b * 8u + (t < 2u ? 0u : 4u)) * LPR + lane) * 4u;
+                img[base + qd] = w0;
+                img[base + 4u * LPR + qd] = w1;
+                img[base + 8u * LPR + qd] = w2;
+                if (qd == 0u) {
+                    img[base + 12u * LPR] = __float_as_uint(ldexpf(1.0f, -k));
+                    img[base + 12u * LPR + 1u] = __float_as_uint(sum);
+                }
+            }
+        }
+        return bad;
+    }
+    template <class L>
+    __device__ __forceinline__ void load(L &ln, const float4 *xs, uint32_t l) const {
+        ln.load_digits(reinterpret_cast<const uint4 *>(xs), l, LPR);
+    }
+};
+
+/* the lane a matvec uses for a format: integer digit dots for Q4_K */
+template <uint32_t TYPE, int B>
+struct MatvecLane {
+    using T = typename LaneFor<TYPE, B>::T;
+};
+template <int B>
+struct MatvecLane<12u, B> {
+    using T = LaneQ4KI<B>;
+};
+
+/* the staging a lane reads: XStageI for lanes with kDigits, else XStage */
+template <class L, class = void>
+struct DigitLane {
+    static constexpr bool value = false;
+};
+template <class L>
+struct DigitLane<L, std::void_t<decltype(L::kDigits)>> {
+    static constexpr bool value = L::kDigits;
+};
+template <class R, int B, int NT>
+using StageFor = std::conditional_t<DigitLane<typename R::Lane>::value, XStageI<R, B, NT>,
+                                    XStage<R, B, NT>>;
 
 }  // namespace kq
 

@@ -261,6 +261,35 @@ def test_matvec_shapes(ctx, fmt, rows, cols, batch):
     assert_close(got, want, exact=ex)
 
 
+@pytest.mark.parametrize("fmt", ALL_FMTS)
+def test_matvec_activation_magnitudes(ctx, fmt):
+    # activations over many binades, inside 16-column groups too (the Q4_K
+    # matvec scales each group of 16 by one power of two before its integer
+    # dots): N(0,1) * 2^U(-20, 20) per element, then whole groups of zeros,
+    # of subnormals, of one huge value among tiny ones, and at 2^100
+    rows, cols, batch = 257, 2048, 2
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((batch, cols)) *
+         np.exp2(rng.uniform(-20, 20, (batch, cols)))).astype(np.float32)
+    x[0, 0:16] = 0.0
+    x[0, 16:32] = (rng.standard_normal(16) * 1e-40).astype(np.float32)
+    x[0, 32:48] = np.float32(1e-30)
+    x[0, 40] = np.float32(3e20)
+    x[1, 256:272] = (rng.standard_normal(16) * 2.0 ** 100).astype(np.float32)
+    x[1, 512:528] = np.float32(-2.0 ** -126)
+    t = FMTS[fmt]
+    w = S.quant_matrix(fmt, S.stream_key(S.W_MATVEC_Q4K, 31, t), rows, cols)
+    dw, dx = ctx.upload(w), ctx.upload(x)
+    dy = ctx.alloc(rows * batch * 4)
+    ctx.matvec(t, dw, rows, cols, dx, batch, dy)
+    got = ctx.download(dy, np.float32, rows * batch).reshape(batch, rows)
+    want = kq_oracle.matvec(t, w, rows, cols, x, threads=oracle_threads())
+    for b in (dw, dx, dy):
+        b.close()
+    assert np.isfinite(got).all()
+    assert_close(got, want, exact=exact.matvec(t, w, rows, cols, x))
+
+
 @pytest.mark.parametrize("fmt", ["Q8_0", "Q5_1", "IQ4_NL"])
 @pytest.mark.parametrize("cols", [32, 64, 128])
 def test_matvec_short_rows(ctx, fmt, cols):
