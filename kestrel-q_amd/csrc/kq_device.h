@@ -286,9 +286,13 @@ __device__ __forceinline__ uint32_t kq_xor_80(uint32_t a) {
 /* x from lane (l ^ mask) within rows of 16, through DPP: masks 1 and 2 are
  * quad permutes, 7 and 15 are the half-row and row mirrors. */
 template <int MASK>
-__device__ __forceinline__ float kq_dpp_pair(float x) {
+__device__ __forceinline__ uint32_t kq_dpp_pair(uint32_t x) {
     constexpr int ctrl = MASK == 1 ? 0xB1 : MASK == 2 ? 0x4E : MASK == 7 ? 0x141 : 0x140;
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xf, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, 0xf, 0xf, false);
+}
+template <int MASK>
+__device__ __forceinline__ float kq_dpp_pair(float x) {
+    return __uint_as_float(kq_dpp_pair<MASK>(__float_as_uint(x)));
 }
 
 /* a(lane) + a(lane ^ 32) for lanes < 32 and b(lane ^ 32) + b(lane) for

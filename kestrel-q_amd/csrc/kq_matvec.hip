@@ -150,15 +150,23 @@ __global__ __launch_bounds__(NT) void matvec_kernel(
             }
         }
     };
-    /* ping-pong: the next group's loads are in flight while one is reduced */
+    /* ping-pong: the next group's loads are in flight while one is reduced.
+     * They are issued without a branch (rows past the matrix read zeros
+     * from beyond the buffer), so every path has the same loads
+     * outstanding and the waits before a group's use count only its own:
+     * a conditional prefetch makes the compiler wait for all loads. The
+     * scheduling barrier keeps the loads ahead of the reduction. */
+    const uint32_t oob = wbytes + 64u;
     while (g < ngroups) {
         uint32_t gn = g + nwaves;
-        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, rb, row_bytes);
+        R::load_group_oob(ln, wb, gn, rows, sub, rb, row_bytes, oob);
+        __builtin_amdgcn_sched_barrier(0);
         finish(ra, g);
         g = gn;
         if (g >= ngroups) break;
         gn = g + nwaves;
-        if (gn < ngroups) R::load_group(ln, wb, gn, rows, sub, ra, row_bytes);
+        R::load_group_oob(ln, wb, gn, rows, sub, ra, row_bytes, oob);
+        __builtin_amdgcn_sched_barrier(0);
         finish(rb, g);
         g = gn;
     }

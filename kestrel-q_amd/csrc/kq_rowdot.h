@@ -178,28 +178,70 @@ struct LaneQ4K {
     }
 };
 
-/* ---------- Q4_K with integer dots over activation byte planes ----------
- * The same lane layout and loads as LaneQ4K. The activations come staged
- * (XStageI) as integers: per 16 consecutive columns one power of two
- * pw = 2^-k and X = rint(x * 2^k) with |X| <= 2^22, stored as three byte
- * planes X = X0 + 2^8 X1 + 2^16 X2 (X0, X1 unsigned, X2 signed), four
- * columns per 32-bit word. A code word's four 4-bit codes meet each plane in
- * one v_dot4 (exact integer sums); the 16-column sub-block sum is rebuilt in
- * int32 (|sum| <= 16 * 15 * 2^22 < 2^31), converted once and scaled by
- * d * sc * pw; the block minimum uses the staged fp32 column sum. Against
- * the fp32 products this moves each activation by at most 2^-23 of the
- * largest magnitude among its 16 columns, below the fp32 summation error
- * the results are compared with. */
-template <int B>
-struct LaneQ4KI {
-    static constexpr uint32_t kBlockBytes = 144u;
+/* ---------- integer dots over activation byte planes ----------
+ * Digit lanes (LaneQ4KI, LaneQ6KI, LaneQ8I) keep the loads and lane layout
+ * of their fp32 counterparts but take the activations staged as integers
+ * (XStageI): per group of G consecutive columns (G = 16, 8, 32) one power
+ * of two pw = 2^-k and X = rint(x * 2^k) with |X| <= 2^22, as three byte
+ * planes X = D0 + 2^8 D1 + 2^16 D2, four columns per 32-bit word: for
+ * unsigned codes (Q4_K, Q6_K) D0 and D1 are X's low bytes and D2 its
+ * signed third byte; for signed codes (Q8_0) all three are balanced signed
+ * digits in [-128, 127]. A word of four 8-bit codes meets each plane in one
+ * v_dot4 (exact integer sums: u8 x u8 for unsigned digits, i8 x i8
+ * otherwise); a group's sum
+ * is rebuilt from the three plane sums, converted once and scaled by the
+ * block scale times pw. Against fp32 products this moves each activation
+ * by at most 2^-23 of the largest magnitude in its group, below the fp32
+ * summation error the results are compared with. */
+
+/* a lane's eight 16-byte slots per batch column from the staged image
+ * [b][slot][lane] */
+template <int B, int NS, bool BAL, bool ISUM = false>
+struct DigitSlots {
     static constexpr bool kDigits = true;
+    static constexpr bool kBalanced = BAL; /* all three digits signed */
+    static constexpr bool kIntSum = ISUM;  /* the record's sum is that of X, an int */
+    uint4 sl[B][NS];
+    __device__ __forceinline__ void load_digits(const uint4 *img, uint32_t l, uint32_t lpr) {
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int j = 0; j < NS; ++j) sl[b][j] = img[((uint32_t)b * 8u + (uint32_t)j) * lpr + l];
+    }
+    /* dword i of the lane's slots (i a compile-time constant) */
+    __device__ __forceinline__ uint32_t word(int b, int i) const {
+        const uint4 &s = sl[b][i >> 2];
+        return (i & 3) == 0 ? s.x : (i & 3) == 1 ? s.y : (i & 3) == 2 ? s.z : s.w;
+    }
+};
+
+/* sum of codes times X over one group from its three plane sums: exact in
+ * int32 where |sum| < 2^31 */
+__device__ __forceinline__ int digit_sum(int s0, int s1, int s2) {
+    return (int)((uint32_t)s0 + ((uint32_t)s1 << 8) + ((uint32_t)s2 << 16));
+}
+
+/* Q4_K: groups of 16 columns, the low and the high nibbles' 16 columns of
+ * a lane (|sum| <= 16 * 15 * 2^22 < 2^31). Record of a group: plane p word
+ * w at 4p + w, pw at 12, the fp32 column sum at 13; slots 0..3 hold the
+ * lane's low group, 4..7 its high one. */
+template <int B>
+struct LaneQ4KI : DigitSlots<B, 8, false> {
+    static constexpr uint32_t kBlockBytes = 144u;
+    static constexpr uint32_t kGroupCols = 16u;
     using Raw = typename LaneQ4K<B>::Raw;
+    using DigitSlots<B, 8, false>::word;
     uint32_t off, qoff;
     uint32_t sel_a, sel_b, lo_mask;
-    uint32_t xd[B][2][3][4];     /* [batch][low/high group][plane][word] */
-    float pw[B][2], sx[B][2];
 
+    /* the lane of a row that reads column group g, and its first slot:
+     * columns 256bb + 64gq + 16h + 0..15 are lane 8bb + 2gq + h's low
+     * group, + 32 its high one */
+    __device__ static __forceinline__ void home(uint32_t g, uint32_t &lane, uint32_t &slot) {
+        const uint32_t r = g % 16u, t = r % 4u;
+        lane = 8u * (g / 16u) + 2u * (r / 4u) + (t & 1u);
+        slot = t < 2u ? 0u : 4u;
+    }
     __device__ __forceinline__ void setup(uint32_t l) {
         const uint32_t bb = l >> 3, c = l & 7u, h = c & 1u, gq = c >> 1;
         off = kBlockBytes * bb;
@@ -210,28 +252,6 @@ struct LaneQ4KI {
         sel_b = p2 | (p2 + 1u) << 8 | (p2 + 4u) << 16 | (p2 + 5u) << 24;
         sel_a = p2 | (p2 + 1u) << 8 | p2 << 16 | (p2 + 1u) << 24;
         lo_mask = gq < 2u ? 0xffffffffu : 0u;
-    }
-    /* the staged image (XStageI): slots 0..3 of lane l hold its low group's
-     * record, 4..7 its high group's, at [b][slot][l] */
-    __device__ __forceinline__ void load_digits(const uint4 *img, uint32_t l, uint32_t lpr) {
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-#pragma unroll
-            for (int hg = 0; hg < 2; ++hg) {
-                const uint4 *r = img + ((uint32_t)b * 8u + 4u * (uint32_t)hg) * lpr + l;
-#pragma unroll
-                for (int pl = 0; pl < 3; ++pl) {
-                    const uint4 w = r[(uint32_t)pl * lpr];
-                    xd[b][hg][pl][0] = w.x;
-                    xd[b][hg][pl][1] = w.y;
-                    xd[b][hg][pl][2] = w.z;
-                    xd[b][hg][pl][3] = w.w;
-                }
-                const uint4 t = r[3u * lpr];
-                pw[b][hg] = __uint_as_float(t.x);
-                sx[b][hg] = __uint_as_float(t.y);
-            }
-        }
     }
     template <int A>
     __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
@@ -273,19 +293,19 @@ struct LaneQ4KI {
             int l2 = 0, h2 = 0;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                l0 = __builtin_amdgcn_udot4(cl[w], xd[b][0][0][w], l0, false);
-                l1 = __builtin_amdgcn_udot4(cl[w], xd[b][0][1][w], l1, false);
-                l2 = __builtin_amdgcn_sdot4((int)cl[w], (int)xd[b][0][2][w], l2, false);
-                h0 = __builtin_amdgcn_udot4(ch[w], xd[b][1][0][w], h0, false);
-                h1 = __builtin_amdgcn_udot4(ch[w], xd[b][1][1][w], h1, false);
-                h2 = __builtin_amdgcn_sdot4((int)ch[w], (int)xd[b][1][2][w], h2, false);
+                l0 = __builtin_amdgcn_udot4(cl[w], word(b, w), l0, false);
+                l1 = __builtin_amdgcn_udot4(cl[w], word(b, 4 + w), l1, false);
+                l2 = __builtin_amdgcn_sdot4((int)cl[w], (int)word(b, 8 + w), l2, false);
+                h0 = __builtin_amdgcn_udot4(ch[w], word(b, 16 + w), h0, false);
+                h1 = __builtin_amdgcn_udot4(ch[w], word(b, 20 + w), h1, false);
+                h2 = __builtin_amdgcn_sdot4((int)ch[w], (int)word(b, 24 + w), h2, false);
             }
-            const int sl = (int)(l0 + (l1 << 8) + ((uint32_t)l2 << 16));
-            const int sh = (int)(h0 + (h1 << 8) + ((uint32_t)h2 << 16));
-            float v = (float)sl * (dl * pw[b][0]);
-            v = fmaf(-ml, sx[b][0], v);
-            v = fmaf((float)sh, dh * pw[b][1], v);
-            v = fmaf(-mh, sx[b][1], v);
+            const float pwl = __uint_as_float(word(b, 12)), sxl = __uint_as_float(word(b, 13));
+            const float pwh = __uint_as_float(word(b, 28)), sxh = __uint_as_float(word(b, 29));
+            float v = (float)digit_sum((int)l0, (int)l1, l2) * (dl * pwl);
+            v = fmaf(-ml, sxl, v);
+            v = fmaf((float)digit_sum((int)h0, (int)h1, h2), dh * pwh, v);
+            v = fmaf(-mh, sxh, v);
             acc[b] = v;
         }
     }
@@ -492,6 +512,157 @@ struct LaneQ8 {
 #pragma unroll
             for (int j = 0; j < 8; ++j) s = dot4_u8(u[j], &xv[j >> 1][b][4 * (j & 1)], s);
             acc[b] = d * fmaf(-128.0f, xsum[b], s);
+        }
+    }
+};
+
+/* Q6_K digit lane: LaneQ6K's loads; groups of 8 columns, one per quarter
+ * of a lane. The codes carry +32, taken off in integers with the sum of X
+ * (the record's sum), so a code of 32 contributes exactly zero however
+ * large its activation: sum (c - 32) X = sum c X - 32 sum X, with
+ * |sum c X| <= 8 * 63 * 2^22 < 2^31. Record of a group: plane p word w at
+ * 2p + w, pw at 6, sum X at 7, in slots 2q and 2q + 1 for quarter q. */
+template <int B>
+struct LaneQ6KI : DigitSlots<B, 8, false, true> {
+    static constexpr uint32_t kBlockBytes = 210u;
+    static constexpr uint32_t kGroupCols = 8u;
+    using Base = LaneQ6K<B>;
+    using Raw = typename Base::Raw;
+    using DigitSlots<B, 8, false, true>::word;
+    uint32_t off, n, t;
+
+    /* quarter q of lane 8bb + 4n + t holds columns 256bb + 128n + 8t + 32q
+     * + 0..7 */
+    __device__ static __forceinline__ void home(uint32_t g, uint32_t &lane, uint32_t &slot) {
+        const uint32_t r = g % 32u;
+        lane = 8u * (g / 32u) + 4u * (r / 16u) + r % 4u;
+        slot = 2u * ((r % 16u) / 4u);
+    }
+    __device__ __forceinline__ void setup(uint32_t l) {
+        const uint32_t s = l & 7u;
+        n = s >> 2;
+        t = s & 3u;
+        off = kBlockBytes * (l >> 3);
+    }
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
+        const uint32_t p = row_off + off;
+        Raw r;
+        r.sh = p & 3u;
+        r.wa = kq_ld96(b, Base::window(p + 64u * n + 8u * t, false), 0u);
+        r.wb = kq_ld96(b, Base::window(p + 64u * n + 32u + 8u * t, false), 0u);
+        r.wh = kq_ld96(b, Base::window(p + 128u + 32u * n + 8u * t, false), 0u);
+        r.ws = kq_ld96(b, Base::window(p + 192u + 8u * n, n == 1u), 0u);
+        r.d = kq_ld16(b, p + 208u, 0u);
+        return r;
+    }
+    __device__ __forceinline__ Raw zero() const {
+        Raw r;
+        r.wa = r.wb = r.wh = r.ws = kq_u32x3{0u, 0u, 0u};
+        r.d = 0u;
+        r.sh = 0u;
+        return r;
+    }
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const float d = kq_f16_to_f32_hw(r.d);
+        malformed |= !kq_isfinite(d);
+        const uint2 qa = Base::align8(r.wa, r.sh, false), qb = Base::align8(r.wb, r.sh, false);
+        const uint2 qh = Base::align8(r.wh, r.sh, false);
+        const uint2 sc = Base::align8(r.ws, r.sh, n == 1u && r.sh == 0u);
+        const uint32_t sh = (t >> 1) * 8u;
+        const uint32_t sv[4] = {sc.x >> sh, sc.x >> (sh + 16u), sc.y >> sh,
+                                sc.y >> (sh + 16u)};
+        /* codes of quarter q, columns 4h .. 4h + 3 */
+        uint32_t c[4][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t A = h ? qa.y : qa.x, Bq = h ? qb.y : qb.x, H = h ? qh.y : qh.x;
+            c[0][h] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+            c[1][h] = (Bq & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+            c[2][h] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+            c[3][h] = ((Bq >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float v = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t s0 = 0u, s1 = 0u;
+                int s2 = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    s0 = __builtin_amdgcn_udot4(c[q][h], word(b, 8 * q + h), s0, false);
+                    s1 = __builtin_amdgcn_udot4(c[q][h], word(b, 8 * q + 2 + h), s1, false);
+                    s2 = __builtin_amdgcn_sdot4((int)c[q][h], (int)word(b, 8 * q + 4 + h), s2,
+                                                false);
+                }
+                const float pw = __uint_as_float(word(b, 8 * q + 6));
+                const uint32_t sxi = word(b, 8 * q + 7);
+                const float dq = d * (float)(int8_t)(sv[q] & 0xffu);
+                const int sq = (int)((uint32_t)digit_sum((int)s0, (int)s1, s2) - 32u * sxi);
+                v = fmaf(dq, (float)sq * pw, v);
+            }
+            acc[b] = v;
+        }
+    }
+};
+
+/* Q8_0 digit lane: LaneQ8's loads; one group of 32 columns per lane (its
+ * block). The int8 codes meet the planes as they are; the three plane sums
+ * (each within 32 * 127 * 128) are joined in fp32. Record: plane p word w
+ * at 8p + w, pw at 24 (slots 0..6). */
+template <int B>
+struct LaneQ8I : DigitSlots<B, 7, true> {
+    static constexpr uint32_t kBlockBytes = 34u;
+    static constexpr uint32_t kGroupCols = 32u;
+    using Raw = typename LaneQ8<B>::Raw;
+    using DigitSlots<B, 7, true>::word;
+    uint32_t off;
+
+    __device__ static __forceinline__ void home(uint32_t g, uint32_t &lane, uint32_t &slot) {
+        lane = g;
+        slot = 0u;
+    }
+    __device__ __forceinline__ void setup(uint32_t l) { off = kBlockBytes * l; }
+    template <int A>
+    __device__ __forceinline__ Raw load(KqBufA<A> b, uint32_t row_off) const {
+        const uint32_t bo = row_off + off;
+        Raw r;
+        r.sh = bo & 3u;
+        r.w0 = kq_ld128(b, bo - r.sh, 0u);
+        r.w1 = kq_ld128(b, bo - r.sh + 16u, 0u);
+        r.t0 = kq_ld16(b, bo + 30u, 0u);
+        r.t1 = kq_ld16(b, bo + 32u, 0u);
+        return r;
+    }
+    __device__ __forceinline__ Raw zero() const {
+        Raw r;
+        r.w0 = r.w1 = make_uint4(0u, 0u, 0u, 0u);
+        r.t0 = r.t1 = 0u;
+        r.sh = 0u;
+        return r;
+    }
+    __device__ __forceinline__ void dot(const Raw &r, float *acc, bool &malformed) const {
+        const uint32_t w[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+        const float d = kq_f16_to_f32_hw(r.sh ? (w[0] >> 16) : w[0]);
+        malformed |= !kq_isfinite(d);
+        /* code dword k = bytes bo+2+4k .. bo+5+4k of the block at bo */
+        uint32_t u[8];
+#pragma unroll
+        for (int k = 0; k < 7; ++k) u[k] = r.sh ? w[k + 1] : kq_align2(w[k + 1], w[k], 2u);
+        u[7] = r.t0 | (r.t1 << 16);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                s0 = __builtin_amdgcn_sdot4((int)u[j], (int)word(b, j), s0, false);
+                s1 = __builtin_amdgcn_sdot4((int)u[j], (int)word(b, 8 + j), s1, false);
+                s2 = __builtin_amdgcn_sdot4((int)u[j], (int)word(b, 16 + j), s2, false);
+            }
+            const float lo = (float)(s0 + s1 * 256); /* |.| < 2^28: one rounding */
+            const float sum = fmaf((float)s2, 65536.0f, lo);
+            acc[b] = sum * (d * __uint_as_float(word(b, 24)));
         }
     }
 };
@@ -963,24 +1134,33 @@ struct XStage {
     }
 };
 
-/* Activation staging for the integer-digit lanes: the same loads, then per
- * 16 consecutive columns (four threads, one float4 each) the largest
- * magnitude m, k = min(22 - e, 149) for m = f * 2^e with f in [0.5, 1)
- * (so |x| * 2^k < 2^22), X = rint(x * 2^k), the byte planes of X and the
- * fp32 column sum. A group's record is four 16-byte slots: the plane 0, 1
- * and 2 words of its four column quads, then 2^-k and the sum. Each group
- * is read by one lane of a row (columns 256bb + 64gq + 16h + 0..15 as its
- * low group, + 32 as its high one; Q4_K lane 8bb + 2gq + h), so records go
- * to [b][slot][lane] (slots 0..3 low, 4..7 high) and consecutive lanes read
- * consecutive 16-byte words. The image has the size of XStage's. */
+/* Activation staging for the digit lanes: the same loads as XStage, then
+ * per group of G consecutive columns (G = Lane::kGroupCols, G/4 threads of
+ * one float4 each) the largest magnitude m, k = min(22 - e, 149) for
+ * m = f * 2^e with f in [0.5, 1) (so |x| * 2^k < 2^22), X = rint(x * 2^k),
+ * its byte digits and the fp32 column sum (the int32 sum of X for lanes
+ * with kIntSum). Unsigned digits are X's low three
+ * bytes (the third one signed: bits 23..31 of X all equal its sign);
+ * balanced digits are the low three bytes of (X + 0x8080) ^ 0x8080: D0 = X
+ * mod 256 taken in [-128, 127], D1 the same of (X - D0) / 256, D2 of
+ * (X - D0 - 256 D1) / 65536. A group's
+ * record (plane words, then 2^-k and the sum; the lane type fixes the
+ * order) goes to the one lane that reads it (Lane::home), at
+ * [b][slot][lane] in 16-byte slots, so that consecutive lanes read
+ * consecutive words. The image has the size of XStage's. */
 template <class R, int B, int NT>
 struct XStageI {
-    static constexpr uint32_t NG = R::kCols / 16u;       /* groups per batch column */
-    static constexpr uint32_t LPR = R::LPR;              /* = kCols / 32 */
-    static constexpr uint32_t NQ = (uint32_t)B * NG * 4u; /* float4 items */
+    using L = typename R::Lane;
+    static constexpr uint32_t GS = L::kGroupCols;
+    static constexpr uint32_t TPG = GS / 4u;             /* threads per group */
+    static constexpr uint32_t NG = R::kCols / GS;        /* groups per batch column */
+    static constexpr uint32_t LPR = R::LPR;
+    static constexpr uint32_t NQ = (uint32_t)B * R::kCols / 4u; /* float4 items */
     static constexpr uint32_t NP = NQ;                  /* float4 words of the image */
     static constexpr int NX = (int)((NQ + (uint32_t)NT - 1u) / (uint32_t)NT);
-    static_assert(NT % 4 == 0 && R::kCols % 16u == 0u, "column quads of a group share a quad");
+    static_assert(TPG == 2u || TPG == 4u || TPG == 8u, "group of 8, 16 or 32 columns");
+    static_assert(NT % 64 == 0 && R::kCols % GS == 0u, "a group's threads share a wave");
+    static_assert(NP == (uint32_t)B * 8u * LPR, "the image holds 8 slots per lane");
     kq_u32x4 v[NX];
 
     __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid) {
@@ -989,7 +1169,7 @@ struct XStageI {
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
-            const uint32_t b = p / (4u * NG), k = (p % (4u * NG)) * 4u;
+            const uint32_t b = p / (R::kCols / 4u), k = (p % (R::kCols / 4u)) * 4u;
             const uint32_t off = p < NQ ? (b * stride + k) * 4u : bytes;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(xb.r, (int)off, 0, 0);
         }
@@ -1000,7 +1180,7 @@ struct XStageI {
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
-            /* uniform over a quad: NQ and NT are multiples of 4 */
+            /* uniform over a group's threads: NQ and NT are multiples of TPG */
             if (NQ % (uint32_t)NT == 0u || p < NQ) {
                 const float f[4] = {__uint_as_float(v[i].x), __uint_as_float(v[i].y),
                                     __uint_as_float(v[i].z), __uint_as_float(v[i].w)};
@@ -1011,43 +1191,61 @@ struct XStageI {
                     m = fmaxf(m, fabsf(f[j]));
                 }
                 m = fmaxf(m, kq_dpp_pair<1>(m));
-                m = fmaxf(m, kq_dpp_pair<2>(m));
                 sum += kq_dpp_pair<1>(sum);
-                sum += kq_dpp_pair<2>(sum);
+                if constexpr (TPG >= 4u) {
+                    m = fmaxf(m, kq_dpp_pair<2>(m));
+                    sum += kq_dpp_pair<2>(sum);
+                }
+                if constexpr (TPG >= 8u) { /* quads are uniform: the mirror swaps them */
+                    m = fmaxf(m, kq_dpp_pair<7>(m));
+                    sum += kq_dpp_pair<7>(sum);
+                }
                 const int e = __builtin_amdgcn_frexp_expf(m);
                 const int k = min(22 - e, 149);
                 uint32_t X[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) X[j] = (uint32_t)(int)rintf(ldexpf(f[j], k));
+                if constexpr (L::kIntSum) {
+                    uint32_t is = (X[0] + X[1]) + (X[2] + X[3]);
+                    is += kq_dpp_pair<1>(is);
+                    if constexpr (TPG >= 4u) is += kq_dpp_pair<2>(is);
+                    if constexpr (TPG >= 8u) is += kq_dpp_pair<7>(is);
+                    sum = __uint_as_float(is);
+                }
+                if constexpr (L::kBalanced)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) X[j] = (X[j] + 0x8080u) ^ 0x8080u;
                 const uint32_t p01 = __builtin_amdgcn_perm(X[1], X[0], 0x05010400u);
                 const uint32_t p23 = __builtin_amdgcn_perm(X[3], X[2], 0x05010400u);
                 const uint32_t w0 = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
                 const uint32_t w1 = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
                 const uint32_t w2 = __builtin_amdgcn_perm(X[1], X[0], 0x0c0c0602u) |
                                     __builtin_amdgcn_perm(X[3], X[2], 0x06020c0cu);
-                const uint32_t gb = p / 4u, qd = p % 4u;
-                const uint32_t b = gb / NG, g = gb % NG, r = g % 16u, t = r % 4u;
-                const uint32_t lane = 8u * (g / 16u) + 2u * (r / 4u) + (t & 1u);
-                /* dword of slot j, component c */
-                const uint32_t base = ((b * 8u + (t < 2u ? 0u : 4u)) * LPR + lane) * 4u;
-                img[base + qd] = w0;
-                img[base + 4u * LPR + qd] = w1;
-                img[base + 8u * LPR + qd] = w2;
+                const uint32_t gb = p / TPG, qd = p % TPG, b = gb / NG;
+                uint32_t lane, slot;
+                L::home(gb % NG, lane, slot);
+                /* record dword i -> slot + i / 4, component i % 4 */
+                auto put = [&](uint32_t i, uint32_t val) {
+                    img[((b * 8u + slot + i / 4u) * LPR + lane) * 4u + i % 4u] = val;
+                };
+                put(qd, w0);
+                put(TPG + qd, w1);
+                put(2u * TPG + qd, w2);
                 if (qd == 0u) {
-                    img[base + 12u * LPR] = __float_as_uint(ldexpf(1.0f, -k));
-                    img[base + 12u * LPR + 1u] = __float_as_uint(sum);
+                    put(3u * TPG, __float_as_uint(ldexpf(1.0f, -k)));
+                    put(3u * TPG + 1u, __float_as_uint(sum));
                 }
             }
         }
         return bad;
     }
-    template <class L>
-    __device__ __forceinline__ void load(L &ln, const float4 *xs, uint32_t l) const {
+    template <class Ln>
+    __device__ __forceinline__ void load(Ln &ln, const float4 *xs, uint32_t l) const {
         ln.load_digits(reinterpret_cast<const uint4 *>(xs), l, LPR);
     }
 };
 
-/* the lane a matvec uses for a format: integer digit dots for Q4_K */
+/* the lane a matvec uses for a format: digit lanes for Q4_K, Q6_K, Q8_0 */
 template <uint32_t TYPE, int B>
 struct MatvecLane {
     using T = typename LaneFor<TYPE, B>::T;
@@ -1055,6 +1253,14 @@ struct MatvecLane {
 template <int B>
 struct MatvecLane<12u, B> {
     using T = LaneQ4KI<B>;
+};
+template <int B>
+struct MatvecLane<14u, B> {
+    using T = LaneQ6KI<B>;
+};
+template <int B>
+struct MatvecLane<8u, B> {
+    using T = LaneQ8I<B>;
 };
 
 /* the staging a lane reads: XStageI for lanes with kDigits, else XStage */
