@@ -1212,7 +1212,7 @@ enum : uint32_t { kSegFirst = 1u, kSegLast = 2u };
 template <uint32_t TYPE, uint32_t COLS, int RT>
 __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t slot0,
                                                           uint32_t col0, uint32_t seg) {
-    using R = kq::Rows<TYPE, COLS, 1, RT>;
+    using R = kq::Rows<TYPE, COLS, 1, RT, typename kq::MatvecLane<TYPE, 1>::T>;
     using Raw = typename R::Raw;
     const uint32_t slot = blockIdx.y + slot0, t = blockIdx.z;
     const bool shared = slot == a.top_k;
@@ -1244,7 +1244,7 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t
      * then every wave its first gate and up rows without a branch; the
      * hidden state is checked and written to LDS behind an LDS-only barrier
      * while the weights are in flight, and the check is flagged at the end */
-    using XS = kq::XStage<R, 1, kThreads>;
+    using XS = kq::StageFor<R, 1, kThreads>;
     __shared__ __align__(16) float4 xs[XS::NP];
     XS stage;
     stage.issue(a.x + (size_t)t * a.hidden + col0, COLS, threadIdx.x);
@@ -1252,7 +1252,7 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t
     R::load_group_oob(ln, ub, g, rows, sub, ru, stride, wbytes + 64u);
     const bool xbad = stage.commit(xs, threadIdx.x);
     kq_lds_barrier();
-    ln.load_x(kq::XLds{xs, l, R::LPR});
+    stage.load(ln, xs, l);
     bool bad = false, malformed = false;
     const size_t at = (size_t)t * (a.top_k + 1u) + slot;
     float *out = a.act + at * a.act_stride;
