@@ -196,17 +196,26 @@ struct LaneQ4K {
 
 /* a lane's eight 16-byte slots per batch column from the staged image
  * [b][slot][lane] */
-template <int B, int NS, bool BAL, bool ISUM = false>
+template <int B, int NS, bool BAL, bool ISUM = false, uint32_t HALF = 0u>
 struct DigitSlots {
     static constexpr bool kDigits = true;
     static constexpr bool kBalanced = BAL; /* all three digits signed */
     static constexpr bool kIntSum = ISUM;  /* the record's sum is that of X, an int */
     uint4 sl[B][NS];
+    /* slots in HALF (a bit mask) hold two words: only those are read */
     __device__ __forceinline__ void load_digits(const uint4 *img, uint32_t l, uint32_t lpr) {
 #pragma unroll
         for (int b = 0; b < B; ++b)
 #pragma unroll
-            for (int j = 0; j < NS; ++j) sl[b][j] = img[((uint32_t)b * 8u + (uint32_t)j) * lpr + l];
+            for (int j = 0; j < NS; ++j) {
+                const uint4 *p = img + ((uint32_t)b * 8u + (uint32_t)j) * lpr + l;
+                if ((HALF >> j) & 1u) {
+                    const uint2 h = *reinterpret_cast<const uint2 *>(p);
+                    sl[b][j] = make_uint4(h.x, h.y, 0u, 0u);
+                } else {
+                    sl[b][j] = *p;
+                }
+            }
     }
     /* dword i of the lane's slots (i a compile-time constant) */
     __device__ __forceinline__ uint32_t word(int b, int i) const {
@@ -226,11 +235,11 @@ __device__ __forceinline__ int digit_sum(int s0, int s1, int s2) {
  * w at 4p + w, pw at 12, the fp32 column sum at 13; slots 0..3 hold the
  * lane's low group, 4..7 its high one. */
 template <int B>
-struct LaneQ4KI : DigitSlots<B, 8, false> {
+struct LaneQ4KI : DigitSlots<B, 8, false, false, 0x88u> {
     static constexpr uint32_t kBlockBytes = 144u;
     static constexpr uint32_t kGroupCols = 16u;
     using Raw = typename LaneQ4K<B>::Raw;
-    using DigitSlots<B, 8, false>::word;
+    using DigitSlots<B, 8, false, false, 0x88u>::word;
     uint32_t off, qoff;
     uint32_t sel_a, sel_b, lo_mask;
 
@@ -612,11 +621,11 @@ struct LaneQ6KI : DigitSlots<B, 8, false, true> {
  * (each within 32 * 127 * 128) are joined in fp32. Record: plane p word w
  * at 8p + w, pw at 24 (slots 0..6). */
 template <int B>
-struct LaneQ8I : DigitSlots<B, 7, true> {
+struct LaneQ8I : DigitSlots<B, 7, true, false, 0x40u> {
     static constexpr uint32_t kBlockBytes = 34u;
     static constexpr uint32_t kGroupCols = 32u;
     using Raw = typename LaneQ8<B>::Raw;
-    using DigitSlots<B, 7, true>::word;
+    using DigitSlots<B, 7, true, false, 0x40u>::word;
     uint32_t off;
 
     __device__ static __forceinline__ void home(uint32_t g, uint32_t &lane, uint32_t &slot) {
