@@ -174,6 +174,25 @@ struct TailArgs {
     Out *out;
 };
 
+/* ascending bitonic sort of one 64-bit value per lane across a wave (no
+ * barrier: exchanges through ds_bpermute) */
+__device__ __forceinline__ uint64_t wave_sort64(uint64_t v) {
+    const uint32_t lane = threadIdx.x % 64u;
+#pragma unroll
+    for (uint32_t size = 2u; size <= 64u; size <<= 1u) {
+#pragma unroll
+        for (uint32_t stride = size / 2u; stride > 0u; stride >>= 1u) {
+            const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, (int)stride);
+            const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), (int)stride);
+            const uint64_t o = ((uint64_t)hi << 32) | lo;
+            const bool up = (lane & size) == 0u, lower = (lane & stride) == 0u;
+            const uint64_t mn = o < v ? o : v, mx = o < v ? v : o;
+            v = lower == up ? mn : mx;
+        }
+    }
+    return v;
+}
+
 constexpr uint32_t kFastMaxK = 64;      /* top-k the fast path takes */
 constexpr uint32_t kFastBlocks = 128;   /* blocks it gathers at most */
 
@@ -182,14 +201,13 @@ constexpr uint32_t kFastBlocks = 128;   /* blocks it gathers at most */
  * of the keys >= it. Returns their count, 0 when they do not fit. vals and
  * cand are LDS arrays of kKeptCap entries. Every thread of the workgroup
  * calls it. */
-__device__ uint32_t fast_top(const TailArgs &a, uint32_t *ids_lds, uint32_t *keys_lds) {
+__device__ uint32_t fast_top(const TailArgs &a, uint32_t v, uint32_t *ids_lds, uint32_t *keys_lds) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_sel[2];
     __shared__ uint32_t blk[kFastBlocks];
     __shared__ uint32_t s_nb, s_nc;
     const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;
     const uint32_t nb = a.prep_blocks;
-    const uint32_t v = tid < nb ? a.max_per_block[tid] : 0u;
     uint32_t prefix = 0u, mask = 0u, krem = a.top_k;
     for (int pass = 0; pass < 4; ++pass) {
         const uint32_t shift = 24u - 8u * (uint32_t)pass;
@@ -241,16 +259,25 @@ __device__ uint32_t fast_top(const TailArgs &a, uint32_t *ids_lds, uint32_t *key
     __syncthreads();
     const uint32_t nbl = s_nb;
     if (nbl > kFastBlocks) return 0u;
-    /* their keys >= t0 */
-    for (uint32_t j = tid; j < nbl * kPrepThreads; j += kTailThreads) {
-        const uint32_t id = blk[j / kPrepThreads] * kPrepThreads + j % kPrepThreads;
-        if (id < a.count) {
-            const uint32_t key = a.keys[id];
-            if (key >= t0) {
+    /* their keys >= t0, kGather loads in flight per thread */
+    constexpr uint32_t kGather = 8u;
+    for (uint32_t j0 = 0u; j0 < nbl * kPrepThreads; j0 += kGather * kTailThreads) {
+        uint32_t key[kGather], kid[kGather];
+#pragma unroll
+        for (uint32_t u = 0; u < kGather; ++u) {
+            const uint32_t j = j0 + u * kTailThreads + tid;
+            kid[u] = j < nbl * kPrepThreads
+                         ? blk[j / kPrepThreads] * kPrepThreads + j % kPrepThreads
+                         : a.count;
+            key[u] = kid[u] < a.count ? a.keys[kid[u]] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kGather; ++u) {
+            if (kid[u] < a.count && key[u] >= t0) {
                 const uint32_t at = atomicAdd(&s_nc, 1u);
                 if (at < kKeptCap) {
-                    keys_lds[at] = key;
-                    ids_lds[at] = id;
+                    keys_lds[at] = key[u];
+                    ids_lds[at] = kid[u];
                 }
             }
         }
@@ -258,7 +285,20 @@ __device__ uint32_t fast_top(const TailArgs &a, uint32_t *ids_lds, uint32_t *key
     __syncthreads();
     const uint32_t nc = s_nc;
     if (nc > kKeptCap) return 0u;
-    /* sort by (key, id) ascending: bitonic on the 64-bit pair */
+    /* sort by (key, id) ascending: bitonic on the 64-bit pair; up to 64
+     * entries within wave 0 */
+    if (nc <= 64u) {
+        if (wave == 0u) {
+            uint64_t x = lane < nc ? ((uint64_t)keys_lds[lane] << 32) | ids_lds[lane] : ~0ull;
+            x = wave_sort64(x);
+            if (lane < nc) {
+                keys_lds[lane] = (uint32_t)(x >> 32);
+                ids_lds[lane] = (uint32_t)x;
+            }
+        }
+        __syncthreads();
+        return nc;
+    }
     uint32_t m2 = 1u;
     while (m2 < nc) m2 <<= 1u;
     for (uint32_t i = nc + tid; i < m2; i += kTailThreads) {
@@ -284,12 +324,8 @@ __device__ uint32_t fast_top(const TailArgs &a, uint32_t *ids_lds, uint32_t *key
             __syncthreads();
         }
     }
-    /* the last nc positions of the sorted order */
-    for (uint32_t i = tid; i < nc; i += kTailThreads) {
-        a.skeys[a.count - nc + i] = keys_lds[i];
-        a.sids[a.count - nc + i] = ids_lds[i];
-    }
-    __syncthreads();
+    /* keys_lds[0 .. nc) / ids_lds[0 .. nc) are the last nc positions of
+     * the sorted order */
     return nc;
 }
 
@@ -297,9 +333,17 @@ __device__ __forceinline__ void fail(Out *o, uint32_t code) {
     if (threadIdx.x == 0) o->status = code;
 }
 
+/* the score of an order key (order_key's inverse; -0 comes back as +0,
+ * which gives every weight expf(score - maximum) the same value) */
+__device__ __forceinline__ float key_score(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
     __shared__ uint32_t s_ids[kKeptCap];
     __shared__ __align__(16) float s_w[kKeptCap];
+    /* the fast path's top of the sorted order: positions base .. n - 1 */
+    __shared__ uint32_t f_keys[kKeptCap], f_ids[kKeptCap];
     __shared__ uint32_t s_flag;
     __shared__ float s_max_p[kTailThreads / 64];
     __shared__ uint32_t s_u[4];
@@ -310,6 +354,8 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
 
     if (tid == 0) s_flag = 0u;
     __syncthreads();
+    /* the fast path's block maximum is requested with the flags */
+    const uint32_t vmax = a.fast == 1u && tid < a.prep_blocks ? a.max_per_block[tid] : 0u;
     for (uint32_t b = tid; b < a.prep_blocks; b += kTailThreads)
         if (a.bad_per_block[b]) s_flag = 1u;
     __syncthreads();
@@ -319,25 +365,32 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
      * largest block maximum; at least k keys reach it, so the k-th largest
      * key does, and every key >= t0 sits in a block whose maximum is >= t0.
      * Those blocks' keys >= t0 are gathered and sorted here by (key, id):
-     * they are the top of the whole sorted order, written to its last
-     * positions. Too many blocks or keys: status FULL_SORT, and the caller
-     * sorts everything. */
+     * they are the top of the whole sorted order, its positions lo0 .. n-1,
+     * and stay in LDS (a score is its key's inverse). Too many blocks or
+     * keys: status FULL_SORT, and the caller sorts everything. */
     uint32_t lo0 = 0u;
-    if (a.fast == 1u) {
-        const uint32_t got = fast_top(a, s_ids, reinterpret_cast<uint32_t *>(s_w));
+    const bool lds_top = a.fast == 1u;
+    if (lds_top) {
+        const uint32_t got = fast_top(a, vmax, f_ids, f_keys);
         if (got == 0u) return fail(o, KQ_SAMPLE_FULL_SORT);
         lo0 = n - got;
     }
+    /* sorted position j (j >= lo0 on the fast path) */
+    auto key_at = [&](uint32_t j) { return lds_top ? f_keys[j - lo0] : a.skeys[j]; };
+    auto id_at = [&](uint32_t j) { return lds_top ? f_ids[j - lo0] : a.sids[j]; };
+    auto score_at = [&](uint32_t j) {
+        return lds_top ? key_score(f_keys[j - lo0]) : a.scores[a.sids[j]];
+    };
 
     /* top-k: the first sorted position whose key reaches the k-th largest
      * key (src/kq_sampling.c:660-667) */
     uint32_t top_start = lo0;
     if (a.top_k != 0u && a.fast != 2u) {
-        const uint32_t t = a.skeys[n - a.top_k];
+        const uint32_t t = key_at(n - a.top_k);
         uint32_t lo = lo0, hi = n - a.top_k; /* first index in [lo, hi] with key >= t */
         while (lo < hi) {
             const uint32_t mid = lo + (hi - lo) / 2u;
-            if (a.skeys[mid] < t) lo = mid + 1u;
+            if (key_at(mid) < t) lo = mid + 1u;
             else hi = mid;
         }
         top_start = lo;
@@ -357,7 +410,7 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
         const uint32_t m = s_u[2];
         maximum = __uint_as_float((m & 0x80000000u) ? (m & 0x7fffffffu) : ~m);
     } else {
-        maximum = a.scores[a.sids[n - 1u]];
+        maximum = score_at(n - 1u);
     }
 
     /* wave 0: the softmax mass over [top_start, n) in ascending order, then
@@ -372,24 +425,26 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
         uint32_t keep = top_start;
         if (a.top_p < 1.0f) {
             auto weights = [&](uint32_t j0, float (&w)[kRun]) {
-                uint32_t id[kRun];
+                float sc[kRun];
 #pragma unroll
                 for (int u = 0; u < kRun; ++u) {
                     const uint32_t j = j0 + 64u * (uint32_t)u + lane;
-                    id[u] = j < n ? a.sids[j] : 0u;
+                    sc[u] = j < n ? score_at(j) : 0.0f;
                 }
 #pragma unroll
                 for (int u = 0; u < kRun; ++u) {
                     const uint32_t j = j0 + 64u * (uint32_t)u + lane;
-                    w[u] = j < n ? kq_expf(a.scores[id[u]] - maximum) : 0.0f;
+                    w[u] = j < n ? kq_expf(sc[u] - maximum) : 0.0f;
                     bad = bad || !kq_isfinite(w[u]);
                 }
             };
             for (uint32_t j0 = top_start; j0 < n; j0 += 64u * kRun) {
                 float w[kRun];
                 weights(j0, w);
+                /* chunks past n add zeros: skipped */
 #pragma unroll
-                for (int u = 0; u < kRun; ++u) sum = chain_f(sum, w[u]);
+                for (int u = 0; u < kRun; ++u)
+                    if (j0 + 64u * (uint32_t)u < n) sum = chain_f(sum, w[u]);
             }
             bad = __ballot(bad) != 0u;
             if (!bad && kq_isfinite(sum) && sum > 0.0f) {
@@ -403,6 +458,7 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
                     for (int u = 0; u < kRun; ++u) {
                         const float p = w[u] / sum;
                         const uint32_t b0 = j0 + 64u * (uint32_t)u;
+                        if (b0 >= n || found) break; /* uniform over the wave */
 #pragma unroll
                         for (int l = 0; l < 64; ++l) {
                             c = c + lane_f(p, l);
@@ -430,14 +486,26 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
 
     float norm_sum = 0.0f, sum2 = 0.0f;
     if (kept <= kKeptCap) {
-        /* the kept ids, sorted by id in LDS (bitonic; ids are distinct) */
+        /* the kept ids, sorted by id in LDS (bitonic; ids are distinct; up
+         * to 64 within wave 0) */
         uint32_t m2 = 1u;
         while (m2 < kept) m2 <<= 1u;
+        if (kept <= 64u) {
+            if (wave == 0u) {
+                uint64_t x = ~0ull;
+                if (lane < kept)
+                    x = ((uint64_t)id_at(keep + lane) << 32) |
+                        __float_as_uint(kq_expf(score_at(keep + lane) - maximum));
+                x = wave_sort64(x);
+                s_ids[lane] = lane < kept ? (uint32_t)(x >> 32) : 0xffffffffu;
+                s_w[lane] = lane < kept ? __uint_as_float((uint32_t)x) : 0.0f;
+            }
+            m2 = 0u; /* sorted */
+        }
         for (uint32_t i = tid; i < m2; i += kTailThreads) {
             if (i < kept) {
-                const uint32_t id = a.sids[keep + i];
-                s_ids[i] = id;
-                s_w[i] = kq_expf(a.scores[id] - maximum);
+                s_ids[i] = id_at(keep + i);
+                s_w[i] = kq_expf(score_at(keep + i) - maximum);
             } else {
                 s_ids[i] = 0xffffffffu;
                 s_w[i] = 0.0f;
