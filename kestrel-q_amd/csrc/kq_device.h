@@ -77,7 +77,11 @@ __constant__ static const uint64_t kq_exp2_tab[32] = {
     0x3fef3720dcef9069ULL, 0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL,
     0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-__device__ __forceinline__ float kq_expf(float x) {
+/* The table may also be a copy in LDS (kq_expf_tab): a kernel that keeps
+ * its own loads in flight across an activation then reads it without a
+ * global load, and without the wait on every outstanding load that a
+ * global load's use would bring. */
+__device__ __forceinline__ float kq_expf_tab(float x, const uint64_t *tab) {
     uint32_t ux = __float_as_uint(x);
     uint32_t top = (ux >> 20) & 0x7ffu;
     if (top >= 0x42bu) {
@@ -93,7 +97,7 @@ __device__ __forceinline__ float kq_expf(float x) {
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= 0x1.8p+52;
     double r = __fma_rn(inv_ln2_n, xd, -kd);
-    uint64_t t = kq_exp2_tab[ki % 32u] + (ki << 47);
+    uint64_t t = tab[ki % 32u] + (ki << 47);
     double s = __longlong_as_double((long long)t);
     double p = __fma_rn(0x1.c6af84b912394p-5 / 32768.0, r, 0x1.ebfce50fac4f3p-3 / 1024.0);
     double r2 = r * r;
@@ -103,22 +107,26 @@ __device__ __forceinline__ float kq_expf(float x) {
     return (float)y;
 }
 
+__device__ __forceinline__ float kq_expf(float x) { return kq_expf_tab(x, kq_exp2_tab); }
+
 /* src/kq_numeric.c:628-638: sign-stable logistic. */
-__device__ __forceinline__ float kq_sigmoid(float x) {
+__device__ __forceinline__ float kq_sigmoid_tab(float x, const uint64_t *tab) {
     if (x >= 0.0f) {
-        float e = kq_expf(-x);
+        float e = kq_expf_tab(-x, tab);
         return 1.0f / (1.0f + e);
     }
-    float e = kq_expf(x);
+    float e = kq_expf_tab(x, tab);
     return e / (1.0f + e);
 }
+__device__ __forceinline__ float kq_sigmoid(float x) { return kq_sigmoid_tab(x, kq_exp2_tab); }
 
 /* src/kq_numeric.c:690-720: silu(g) = g * sigmoid(g), then * up. */
-__device__ __forceinline__ float kq_swiglu(float g, float u) {
-    float s = kq_sigmoid(g);
+__device__ __forceinline__ float kq_swiglu_tab(float g, float u, const uint64_t *tab) {
+    float s = kq_sigmoid_tab(g, tab);
     float silu = g * s;
     return silu * u;
 }
+__device__ __forceinline__ float kq_swiglu(float g, float u) { return kq_swiglu_tab(g, u, kq_exp2_tab); }
 
 /* Q4_K/Q5_K 6-bit scale and min for sub-block j (src/kq_numeric.c:161-174),
  * from the 12 packed bytes held little-endian in three dwords. */

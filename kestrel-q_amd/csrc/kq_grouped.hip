@@ -1535,8 +1535,28 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     const uint32_t E = d->experts;
     const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
     /* gate/up + SwiGLU, then down: the routed experts' workgroups and the
-     * shared expert's in one launch when their formats agree */
-    if (w->shared_gate_type == w->gate_type) {
+     * shared expert's in one launch when their formats agree. Q4_K gate/up
+     * rows stream through LDS (kq_grouped_gu.hip) from activations split
+     * once per token into the start of outp, which only the down pass
+     * writes later. */
+    const bool lds_routed = w->gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
+    const bool lds_shared =
+        lds_routed && w->shared_gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
+    if (lds_routed) {
+        e = kq_launch_gu_stage(hidden, tokens, d->hidden, ws->outp, status, s);
+        if (e != hipSuccess) return e;
+    }
+    if (lds_routed) {
+        void *gu_items = (uint8_t *)ws->outp +
+                         ((kq_launch_gu_stage_bytes(tokens, d->hidden) + 255u) & ~(uint64_t)255u);
+        e = kq_launch_gu_lds(d->hidden, g, u, sg, su, ws->outp, ws->offsets, ws->perm_tok, E,
+                             tokens, d->top_k, d->inter, lds_shared ? 1 : 0, gu_items, ws->act,
+                             status, s);
+        if (e == hipSuccess && !lds_shared)
+            e = pass_any<2>(w->shared_gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets,
+                            ws->perm_tok, E, tokens, d->top_k, d->inter, E, sh_wgs, ws->act,
+                            status, s);
+    } else if (w->shared_gate_type == w->gate_type) {
         e = pass_any<2>(w->gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets, ws->perm_tok,
                         E, tokens, d->top_k, d->inter, 0u, E + sh_wgs, ws->act, status, s);
     } else {

@@ -163,6 +163,20 @@ hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens, uint32_t 
                                  uint32_t experts, uint32_t *offsets, uint32_t *pair_token,
                                  uint32_t *pos, uint32_t *pair_slot, uint32_t *status,
                                  hipStream_t stream);
+/* prefill gate/up of Q4_K experts through LDS (kq_grouped_gu.hip): the
+ * per-token activation split, then the pass over the routed experts'
+ * 16-token chunks (and the shared expert's, with_shared) on a persistent
+ * grid; items is scratch of kq_launch_gu_items_bytes */
+int kq_launch_gu_lds_supported(uint32_t hidden);
+uint64_t kq_launch_gu_stage_bytes(uint32_t tokens, uint32_t hidden);
+hipError_t kq_launch_gu_stage(const float *hidden_states, uint32_t tokens, uint32_t hidden,
+                              void *staged, uint32_t *status, hipStream_t s);
+uint64_t kq_launch_gu_items_bytes(uint32_t experts, uint32_t tokens, uint32_t top_k);
+hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const void *up,
+                            const void *shared_gate, const void *shared_up, const void *staged,
+                            const uint32_t *offsets, const uint32_t *perm_tok, uint32_t experts,
+                            uint32_t tokens, uint32_t top_k, uint32_t rows, int with_shared,
+                            void *items, float *act, uint32_t *status, hipStream_t s);
 hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                                  const float *hidden, uint32_t tokens,
                                  const kq_launch_moe_ws *ws, float *out, uint32_t *status,

@@ -1797,6 +1797,15 @@ static uint64_t outp_row(const kq_launch_moe_dims *d) {
     return d->hidden > 2u * ai ? d->hidden : 2u * ai;
 }
 
+/* outp also holds the grouped gate/up pass's split activations and work
+ * list before the down pass writes it */
+static uint64_t outp_bytes(const kq_launch_moe_dims *d, uint32_t tokens) {
+    const uint64_t o = align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u);
+    const uint64_t g = align256(kq_launch_gu_stage_bytes(tokens, d->hidden)) +
+                       align256(kq_launch_gu_items_bytes(d->experts, tokens, d->top_k));
+    return o > g ? o : g;
+}
+
 extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t tokens) {
     const uint64_t ep = pad64(d->experts + 1u);
     const uint64_t ai = d->inter > d->shared_inter ? d->inter : d->shared_inter;
@@ -1808,7 +1817,7 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * (d->top_k + 1u) * ai * 4u);    /* act */
     b += align256((uint64_t)(d->experts + 1u) * 4u);                 /* offsets */
     b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
-    b += align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u); /* outp */
+    b += outp_bytes(d, tokens);                                      /* outp */
     b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
     b += 256u;                                           /* certified flag */
     return b;
@@ -1831,7 +1840,7 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->offsets = (uint32_t *)p; p += align256((uint64_t)(d->experts + 1u) * 4u);
     ws->perm_tok = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->pos = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
-    ws->outp = (float *)p; p += align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u);
+    ws->outp = (float *)p; p += outp_bytes(d, tokens);
     ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
     ws->certified = (uint32_t *)p;
 }
