@@ -1538,7 +1538,8 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
      * shared expert's in one launch when their formats agree. Q4_K gate/up
      * rows stream through LDS (kq_grouped_gu.hip) from activations split
      * once per token into the start of outp, which only the down pass
-     * writes later. */
+     * writes later; the work list it builds (gitems) also drives the Q6_K
+     * down pass (kq_grouped_dn.hip). */
     const bool lds_routed = w->gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
     const bool lds_shared =
         lds_routed && w->shared_gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
@@ -1547,10 +1548,8 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
         if (e != hipSuccess) return e;
     }
     if (lds_routed) {
-        void *gu_items = (uint8_t *)ws->outp +
-                         ((kq_launch_gu_stage_bytes(tokens, d->hidden) + 255u) & ~(uint64_t)255u);
         e = kq_launch_gu_lds(d->hidden, g, u, sg, su, ws->outp, ws->offsets, ws->perm_tok, E,
-                             tokens, d->top_k, d->inter, lds_shared ? 1 : 0, gu_items, ws->act,
+                             tokens, d->top_k, d->inter, lds_shared ? 1 : 0, ws->gitems, ws->act,
                              status, s);
         if (e == hipSuccess && !lds_shared)
             e = pass_any<2>(w->shared_gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets,
@@ -1569,7 +1568,12 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     }
     if (e != hipSuccess) return e;
     const uint8_t *dn = (const uint8_t *)w->down, *sd = (const uint8_t *)w->shared_down;
-    if (w->shared_down_type == w->down_type) {
+    if (lds_shared && w->down_type == KQ_LAUNCH_Q6_K && w->shared_down_type == KQ_LAUNCH_Q6_K &&
+        kq_launch_dn_lds_supported(d->inter)) {
+        /* over the gate/up pass's item list (routed and shared chunks) */
+        e = kq_launch_dn_lds(d->inter, d->hidden, dn, sd, ws->act, tokens, d->top_k, ws->gitems,
+                             ws->dstage, ws->outp, status, s);
+    } else if (w->shared_down_type == w->down_type) {
         e = pass_any<1>(w->down_type, d->inter, dn, nullptr, sd, nullptr, ws->act, ws->offsets,
                         ws->perm_tok, E, tokens, d->top_k, d->hidden, 0u, E + sh_wgs, ws->outp,
                         status, s);

@@ -1,0 +1,411 @@
+/*
+ * kq_grouped_dn.hip — the prefill down pass of Q6_K experts, one
+ * independent weight pipeline per wave.
+ *
+ * The reference forms o = Wd a for every (token, selected expert) pair one
+ * token at a time (src/kq_moe_qwen38.c:722-765 via
+ * kq_weight_provider_linear_f32, src/kq_weight_provider.c:378-509). Here
+ * every expert's down rows stream once for all of its tokens:
+ *
+ *   - The work is the gate/up pass's item list (one item per 16-token chunk
+ *     of an expert, kq_grouped_gu.hip), each of ceil(hidden / 16) tiles of
+ *     16 down rows. Every wave of the grid walks its own contiguous range
+ *     of that tile sequence: no barrier, no shared state between waves.
+ *   - A tile's 16 rows of intermediate / 256 Q6_K blocks are one contiguous
+ *     byte range; the wave copies it into a private LDS slot with 16-byte
+ *     LDS-DMA loads (1 KiB per instruction) while it multiplies the tile
+ *     before, and reads the operand pieces from there.
+ *   - The activation operand (16 positions x intermediate, hi + lo) lives
+ *     in the wave's registers for a whole item: rows of the intermediate
+ *     activations are split once per position by dn_stage, in the order
+ *     the lanes read them.
+ *
+ * Arithmetic per 16-column Q6_K sub-block (the grouped pass's): exact codes
+ * q - 32 in fp16, one 16x16x16 MFMA step each for the hi and lo parts of
+ * the activations, the fp32 result scaled by d * sc.
+ *
+ * The LDS-DMA loads are issued from inline assembly and waited for with
+ * s_waitcnt vmcnt(n), counting only this wave's loads issued after the
+ * ones it needs (loads complete in order).
+ */
+#include "kq_launch.h"
+#include "kq_device.h"
+
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kT = 16;
+constexpr uint32_t kShared = 0x80000000u; /* item flag: the shared expert */
+constexpr int kBadRow = 0x7fffffff;
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ h2 byte_pair_lo(uint32_t m) {
+    return as_h2(__builtin_amdgcn_perm(0x64646464u, m, 0x04010400u));
+}
+__device__ __forceinline__ h2 byte_pair_hi(uint32_t m) {
+    return as_h2(__builtin_amdgcn_perm(0x64646464u, m, 0x04030402u));
+}
+__device__ __forceinline__ float half_bits(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+
+__device__ __forceinline__ i4v dma_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    i4v r;
+    r.x = (int)(uint32_t)a;
+    r.y = (int)(uint32_t)(a >> 32);
+    r.z = (int)bytes;
+    r.w = 0x00020000;
+    return r;
+}
+__device__ __forceinline__ void dma16(i4v rsrc, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\t"
+                 "buffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(lds)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+/* s_waitcnt vmcnt(IPT * after) for a run-time after <= PD */
+template <uint32_t IPT, uint32_t PD>
+__device__ __forceinline__ void wait_after(uint32_t after) {
+    if constexpr (PD > 0u) {
+        if (after >= PD) {
+            wait_vm<(int)(IPT * PD)>();
+            return;
+        }
+        wait_after<IPT, PD - 1u>(after);
+    } else {
+        wait_vm<0>();
+    }
+}
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ uint32_t sload(const uint32_t *p) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    /* (readfirstlane returns int: zero-extend each half, never sign-extend) */
+    const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32);
+    uint32_t v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(u) : "memory");
+    return v;
+}
+
+/* ------------------------------------------------------------------ */
+/* per-position activation split, in lane order */
+
+/* Staged rows: xh[p][K], xl[p][K] (fp16) and sig[p]. Column c = 256b +
+ * 128n + 32q + 16h + 4g + e sits at index ((((g KB + b) 2 + n) 2 + h) 4 + q)
+ * 4 + e of its row, so MFMA lane k-group g reads one contiguous run. */
+struct DnStaged {
+    _Float16 *xh, *xl;
+    int *sig;
+};
+__device__ __forceinline__ DnStaged dn_staged_at(void *base, uint32_t npos, uint32_t k) {
+    DnStaged s;
+    uint8_t *p = (uint8_t *)base;
+    s.xh = (_Float16 *)p;
+    p += (size_t)npos * k * 2u;
+    s.xl = (_Float16 *)p;
+    p += (size_t)npos * k * 2u;
+    s.sig = (int *)p;
+    return s;
+}
+__device__ __forceinline__ uint32_t dn_index(uint32_t c, uint32_t kb) {
+    const uint32_t e = c & 3u, g = (c >> 2) & 3u, h = (c >> 4) & 1u, q = (c >> 5) & 3u,
+                   n = (c >> 7) & 1u, b = c >> 8;
+    return ((((g * kb + b) * 2u + n) * 2u + h) * 4u + q) * 4u + e;
+}
+
+/* grid: one wave per position; k a multiple of 256 */
+__global__ __launch_bounds__(64) void dn_stage(const float *__restrict__ X, uint32_t npos,
+                                               uint32_t k, void *staged, uint32_t *status) {
+    const DnStaged sx = dn_staged_at(staged, npos, k);
+    const uint32_t p = blockIdx.x, lane = threadIdx.x;
+    const float4 *row = (const float4 *)(X + (size_t)p * k);
+    const uint32_t ng = k / 4u;
+    float m = 0.0f;
+    bool nf = false;
+    for (uint32_t i = lane; i < ng; i += 64u) {
+        const float4 v = row[i];
+        nf |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) || !kq_isfinite(v.w);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const bool bad = __ballot(nf) != 0ull;
+    /* largest magnitude into [2^14, 2^15) */
+    int sig = 0;
+    if (!bad && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
+    if (bad) sig = kBadRow;
+    for (uint32_t i = lane; i < ng; i += 64u) {
+        const float4 v = row[i];
+        const float a[4] = {v.x, v.y, v.z, v.w};
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float xs = bad ? 0.0f : ldexpf(a[c], sig);
+            hi[c] = (_Float16)xs;
+            lo[c] = (_Float16)(xs - (float)hi[c]);
+        }
+        const size_t o = (size_t)p * k + dn_index(4u * i, k / 256u);
+        *(h4 *)(sx.xh + o) = h4{hi[0], hi[1], hi[2], hi[3]};
+        *(h4 *)(sx.xl + o) = h4{lo[0], lo[1], lo[2], lo[3]};
+    }
+    if (lane == 0u) {
+        sx.sig[p] = sig;
+        /* a non-finite intermediate activation is a numeric failure */
+        if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* the pass */
+
+template <uint32_t KB>
+struct DnShape {
+    static constexpr uint32_t RB = 210u * KB;                /* row bytes */
+    static constexpr uint32_t TB = kT * RB;                  /* tile bytes */
+    static constexpr uint32_t IPT = (TB + 1023u) / 1024u;    /* loads per tile */
+    static constexpr uint32_t SLOT = IPT * 1024u;
+    /* one wave per SIMD: the activation operand alone takes 64 KB registers
+     * per block, so each wave gets the whole register file, and the LDS
+     * holds RING - 1 tiles in flight per wave */
+    static constexpr uint32_t W = 4u;                        /* waves per workgroup */
+    static constexpr uint32_t RING = KB == 1u ? 8u : 5u;     /* slots per wave */
+    static constexpr uint32_t PD = RING - 1u;
+    static_assert(W * RING * SLOT <= 160u * 1024u, "LDS");
+};
+
+struct DnArgs {
+    const uint8_t *down, *sdown;  /* routed stack, shared matrix */
+    const void *staged;           /* dn_stage output, positions 0 .. T*K + T - 1 */
+    const uint32_t *items, *n_items;
+    uint32_t tokens, top_k, hidden, npos;
+    float *out; /* [T*K + T][hidden] */
+    uint32_t *status;
+};
+
+template <uint32_t KB>
+__global__ __launch_bounds__(DnShape<KB>::W * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void dn_q6k(DnArgs a) {
+    using S = DnShape<KB>;
+    constexpr uint32_t KD = 256u * KB;
+    __shared__ __align__(16) uint8_t slots[S::W][S::RING][S::SLOT];
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t gw = blockIdx.x * S::W + w, nw = gridDim.x * S::W;
+    const uint32_t nt = (a.hidden + kT - 1u) / kT; /* tiles per item */
+    const uint64_t total = (uint64_t)(*a.n_items) * nt;
+    const uint32_t lo = (uint32_t)(total * gw / nw), hi = (uint32_t)(total * (gw + 1u) / nw);
+    if (lo >= hi) return;
+
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t wbytes = a.hidden * S::RB;
+    const uint32_t base_lds = lds_addr(&slots[w][0][0]);
+    const uint8_t *myslots = &slots[w][0][0];
+
+    /* the next tile to request */
+    uint32_t iss_it = lo / nt, iss_tile = lo - (lo / nt) * nt, iss_slot = 0u;
+    bool iss_new = true;
+    i4v rw = {0, 0, 0, 0};
+    auto issue = [&]() {
+        if (iss_new) {
+            iss_new = false;
+            const uint32_t ex = sload(a.items + 2u * iss_it);
+            rw = dma_rsrc((ex & kShared) ? a.sdown : a.down + (size_t)ex * wbytes, wbytes);
+        }
+        const uint32_t toff = iss_tile * S::TB;
+#pragma unroll
+        for (uint32_t q = 0; q < S::IPT; ++q) {
+            /* bytes past the tile re-read its start (their slot bytes are
+             * never read) */
+            const uint32_t c = 64u * q + lane;
+            dma16(rw, toff + (16u * c < S::TB ? 16u * c : 0u),
+                  base_lds + iss_slot * S::SLOT + q * 1024u);
+        }
+        iss_slot = iss_slot + 1u == S::RING ? 0u : iss_slot + 1u;
+        if (++iss_tile == nt) {
+            iss_tile = 0u;
+            ++iss_it;
+            iss_new = true;
+        }
+    };
+
+    const DnStaged sx = dn_staged_at(const_cast<void *>(a.staged), a.npos, KD);
+    const KqBuf bxh = kq_buf(sx.xh, a.npos * KD * 2u), bxl = kq_buf(sx.xl, a.npos * KD * 2u);
+    const KqBuf bsg = kq_buf(sx.sig, a.npos * 4u);
+    const uint32_t tk = a.tokens * a.top_k;
+    bool bad = false, malformed = false;
+
+#pragma unroll
+    for (uint32_t t = 0; t < S::PD; ++t)
+        if (lo + t < hi) issue();
+
+    /* the item being multiplied: activation operand of lane (j, g) (token
+     * row j, k-group g), the scales of the four positions this lane's
+     * results belong to */
+    uint4 axh[KB][8], axl[KB][8]; /* 16-byte loads: h4 steps 2v and 2v + 1 */
+    int sg[4];
+    uint32_t cur = 0u, pos0 = 0u, count = 0u;
+    auto enter = [&](uint32_t it) {
+        cur = it;
+        const uint32_t ex = sload(a.items + 2u * it), fc = sload(a.items + 2u * it + 1u);
+        const uint32_t first = fc & 0xffffffu;
+        count = fc >> 24;
+        pos0 = (ex & kShared) ? tk + first : first;
+        /* rows past the chunk read at 2^31, past the buffer */
+        const uint32_t xo = j < count ? ((pos0 + j) * KD + g * (KD / 4u)) * 2u : 0x80000000u;
+#pragma unroll
+        for (uint32_t b = 0; b < KB; ++b)
+#pragma unroll
+            for (uint32_t v = 0; v < 8u; ++v) {
+                axh[b][v] = kq_ld128(bxh, xo + (b * 8u + v) * 16u, 0u);
+                axl[b][v] = kq_ld128(bxl, xo + (b * 8u + v) * 16u, 0u);
+            }
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
+        }
+        wait_vm_all();
+    };
+    uint32_t ctile = lo - (lo / nt) * nt, cslot = 0u;
+    enter(lo / nt);
+
+    const h2 bias = h2{(_Float16)-1056.0f, (_Float16)-1056.0f}; /* 1024 + 32 */
+    for (uint32_t tau = lo; tau < hi; ++tau) {
+        if (ctile == nt) {
+            ctile = 0u;
+            enter(cur + 1u);
+        }
+        if (tau + S::PD < hi) issue();
+        /* tile tau's loads have landed; those of the (at most PD) tiles
+         * issued after it may still be in flight */
+        const uint32_t after = hi - 1u - tau < S::PD ? hi - 1u - tau : S::PD;
+        wait_after<S::IPT, S::PD>(after);
+        const uint8_t *tile = myslots + cslot * S::SLOT;
+        cslot = cslot + 1u == S::RING ? 0u : cslot + 1u;
+        const uint32_t row0 = ctile * kT;
+        ++ctile;
+
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t b = 0; b < KB; ++b) {
+            /* block b of row j: 4-byte aligned windows, re-aligned by sh */
+            const uint32_t o = j * S::RB + b * 210u;
+            const uint32_t sh = o & 3u;
+            const uint32_t *p = (const uint32_t *)(tile + (o - sh));
+            auto win = [&](uint32_t off) { return kq_align2(p[off / 4u + 1u], p[off / 4u], sh); };
+            const float d = half_bits(sh ? (p[52] >> 16) : p[52]);
+            malformed |= !kq_isfinite(d);
+            uint32_t sc[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) sc[k] = win(192u + 4u * k);
+#pragma unroll
+            for (uint32_t nh = 0; nh < 4u; ++nh) {
+                const uint32_t n = nh >> 1, h = nh & 1u;
+                const uint32_t oa = 64u * n + 16u * h + 4u * g;
+                const uint32_t A = win(oa), B = win(oa + 32u);
+                const uint32_t H = win(128u + 32u * n + 16u * h + 4u * g);
+                uint32_t c[4];
+                c[0] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+                c[1] = (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+                c[2] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+                c[3] = ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+#pragma unroll
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const uint32_t s = 8u * n + 2u * q + h; /* sub-block */
+                    const h2 w0 = byte_pair_lo(c[q]) + bias, w1 = byte_pair_hi(c[q]) + bias;
+                    const h4 bw = h4{w0.x, w0.y, w1.x, w1.y};
+                    /* columns 128n + 32q + 16h + 4g .. +3 of block b */
+                    const uint32_t ai = (n * 2u + h) * 4u + q;
+                    const uint4 &xh = axh[b][ai >> 1], &xl = axl[b][ai >> 1];
+                    const h4 ah = __builtin_bit_cast(h4, (ai & 1u) ? make_uint2(xh.z, xh.w) : make_uint2(xh.x, xh.y));
+                    const h4 al = __builtin_bit_cast(h4, (ai & 1u) ? make_uint2(xl.z, xl.w) : make_uint2(xl.x, xl.y));
+                    f4 t = {0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bw, t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bw, t, 0, 0, 0);
+                    const int8_t scv = (int8_t)((sc[s >> 2] >> (8u * (s & 3u))) & 0xffu);
+                    const float ds = d * (float)scv;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc[k] = fmaf(ds, t[k], acc[k]);
+                }
+            }
+        }
+        /* D[token][row]: this lane holds row row0 + j of tokens 4g .. 4g+3 */
+        const uint32_t row = row0 + j;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            const bool valid = i < count && row < a.hidden;
+            const float v = ldexpf(acc[q], -sg[q]);
+            bad |= valid && !kq_isfinite(v);
+            if (valid) a.out[(size_t)(pos0 + i) * a.hidden + row] = v;
+        }
+    }
+    /* no LDS-DMA load may outlive the wave */
+    wait_vm<0>();
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+}
+
+template <uint32_t KB>
+hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus < 1)
+            cus = 256;
+    }
+    /* one workgroup per CU (the slots' LDS) */
+    hipLaunchKernelGGL((dn_q6k<KB>), dim3((uint32_t)cus), dim3(DnShape<KB>::W * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int kq_launch_dn_lds_supported(uint32_t inter) { return inter == 256u || inter == 512u; }
+
+extern "C" uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter) {
+    return (uint64_t)npos * inter * 4u + (uint64_t)npos * 4u;
+}
+
+/* down over the item list the gate/up pass built (items, as written by
+ * kq_launch_gu_lds): the per-position split of act, then the pass */
+extern "C" hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const void *down,
+                                       const void *shared_down, const float *act,
+                                       uint32_t tokens, uint32_t top_k, const void *items,
+                                       void *staged, float *out, uint32_t *status,
+                                       hipStream_t s) {
+    if (!kq_launch_dn_lds_supported(inter)) return hipErrorInvalidValue;
+    const uint32_t npos = tokens * top_k + tokens;
+    hipLaunchKernelGGL(dn_stage, dim3(npos), dim3(64), 0, s, act, npos, inter, staged, status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    DnArgs a;
+    a.down = (const uint8_t *)down;
+    a.sdown = (const uint8_t *)shared_down;
+    a.staged = staged;
+    a.n_items = (const uint32_t *)items;
+    a.items = (const uint32_t *)items + 4;
+    a.tokens = tokens;
+    a.top_k = top_k;
+    a.hidden = hidden;
+    a.npos = npos;
+    a.out = out;
+    a.status = status;
+    return inter == 256u ? launch_dn<1>(a, s) : launch_dn<2>(a, s);
+}

@@ -136,6 +136,8 @@ typedef struct kq_launch_moe_ws {
     double *bound;        /* [experts + 1][2]: exact product sums and the bound on the
                              CPU's sequential sum (certified one-token routing) */
     uint32_t *certified;  /* one-token route: 1 certified, 2 refined, 0 exact */
+    void *dstage;         /* grouped Q6_K down pass: act split per position */
+    void *gitems;         /* grouped passes' work list (kq_launch_gu_lds) */
 } kq_launch_moe_ws;
 
 uint32_t kq_launch_moe_experts_padded(uint32_t experts);
@@ -177,6 +179,13 @@ hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const void *up,
                             const uint32_t *offsets, const uint32_t *perm_tok, uint32_t experts,
                             uint32_t tokens, uint32_t top_k, uint32_t rows, int with_shared,
                             void *items, float *act, uint32_t *status, hipStream_t s);
+/* prefill Q6_K down over the gate/up pass's item list (kq_grouped_dn.hip) */
+int kq_launch_dn_lds_supported(uint32_t inter);
+uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter);
+hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const void *down,
+                            const void *shared_down, const float *act, uint32_t tokens,
+                            uint32_t top_k, const void *items, void *staged, float *out,
+                            uint32_t *status, hipStream_t s);
 hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                                  const float *hidden, uint32_t tokens,
                                  const kq_launch_moe_ws *ws, float *out, uint32_t *status,

@@ -1797,12 +1797,11 @@ static uint64_t outp_row(const kq_launch_moe_dims *d) {
     return d->hidden > 2u * ai ? d->hidden : 2u * ai;
 }
 
-/* outp also holds the grouped gate/up pass's split activations and work
- * list before the down pass writes it */
+/* outp also holds the grouped gate/up pass's split activations before the
+ * down pass writes it */
 static uint64_t outp_bytes(const kq_launch_moe_dims *d, uint32_t tokens) {
     const uint64_t o = align256((uint64_t)tokens * (d->top_k + 1u) * outp_row(d) * 4u);
-    const uint64_t g = align256(kq_launch_gu_stage_bytes(tokens, d->hidden)) +
-                       align256(kq_launch_gu_items_bytes(d->experts, tokens, d->top_k));
+    const uint64_t g = align256(kq_launch_gu_stage_bytes(tokens, d->hidden));
     return o > g ? o : g;
 }
 
@@ -1820,6 +1819,8 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += outp_bytes(d, tokens);                                      /* outp */
     b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
     b += 256u;                                           /* certified flag */
+    b += align256(kq_launch_dn_stage_bytes(tokens * (d->top_k + 1u), ai)); /* dstage */
+    b += align256(kq_launch_gu_items_bytes(d->experts, tokens, d->top_k));  /* gitems */
     return b;
 }
 
@@ -1842,7 +1843,9 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->pos = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->outp = (float *)p; p += outp_bytes(d, tokens);
     ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
-    ws->certified = (uint32_t *)p;
+    ws->certified = (uint32_t *)p; p += 256u;
+    ws->dstage = p; p += align256(kq_launch_dn_stage_bytes(tokens * (d->top_k + 1u), ai));
+    ws->gitems = p;
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
