@@ -981,6 +981,25 @@ hipError_t launch_pass(const uint8_t *W0, const uint8_t *W1, const uint8_t *SW0,
     constexpr int TPW = Shape<GFMT, KDIM, NMAT>::TPW;
     constexpr int PD = Shape<GFMT, KDIM, NMAT>::PD;
     constexpr int KS = Shape<GFMT, KDIM, NMAT>::KS;
+    if (y0 >= experts && ny > 0u) {
+        /* the shared expert alone (its format differs from the routed
+         * one): a few rows for every token, so 64-row slabs and one
+         * 16-token chunk per workgroup, which spreads it over the device */
+        constexpr int NWS = 4;
+        /* the ring (a power of two) must divide the TPW = 1 iterations */
+        constexpr int NIT1 = (int)(KDIM / Fmt<GFMT>::kUnit);
+        constexpr int R1 = (PD + 1) >= 8 && NIT1 % 8 == 0   ? 8
+                           : (PD + 1) >= 4 && NIT1 % 4 == 0 ? 4
+                           : (PD + 1) >= 2 && NIT1 % 2 == 0 ? 2
+                                                            : 1;
+        constexpr int PD1 = R1 - 1;
+        const uint32_t nys = (tokens + kTile - 1u) / kTile;
+        const dim3 grid((rows + NWS * kTile - 1u) / (NWS * kTile), nys);
+        hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NWS, 1, PD1, KS>), grid,
+                           dim3(NWS * 64), 0, s, W0, W1, SW0, SW1, X, offsets, perm_tok, experts,
+                           tokens, top_k, rows, 1u, y0, out, status);
+        return hipGetLastError();
+    }
     const uint32_t slab = (uint32_t)(NW * TPW) * kTile;
     const dim3 grid((rows + slab - 1u) / slab, ny);
     hipLaunchKernelGGL((grouped_pass<GFMT, KDIM, NMAT, NW, TPW, PD, KS>), grid, dim3(NW * 64), 0,

@@ -1818,9 +1818,9 @@ extern "C" uint64_t kq_launch_moe_ws_bytes(const kq_launch_moe_dims *d, uint32_t
     b += align256((uint64_t)tokens * d->top_k * 4u) * 2u;           /* perm_tok, pos */
     b += outp_bytes(d, tokens);                                      /* outp */
     b += align256((uint64_t)(d->experts + 1u) * 16u);                /* bound */
-    b += 256u;                                           /* certified flag */
     b += align256(kq_launch_dn_stage_bytes(tokens * (d->top_k + 1u), ai)); /* dstage */
     b += align256(kq_launch_gu_items_bytes(d->experts, tokens, d->top_k));  /* gitems */
+    b += 256u;                          /* certified flag (the last slot) */
     return b;
 }
 
@@ -1843,9 +1843,9 @@ extern "C" void kq_launch_moe_ws_carve(const kq_launch_moe_dims *d, uint32_t tok
     ws->pos = (uint32_t *)p; p += align256((uint64_t)tokens * d->top_k * 4u);
     ws->outp = (float *)p; p += outp_bytes(d, tokens);
     ws->bound = (double *)p; p += align256((uint64_t)(d->experts + 1u) * 16u);
-    ws->certified = (uint32_t *)p; p += 256u;
     ws->dstage = p; p += align256(kq_launch_dn_stage_bytes(tokens * (d->top_k + 1u), ai));
-    ws->gitems = p;
+    ws->gitems = p; p += align256(kq_launch_gu_items_bytes(d->experts, tokens, d->top_k));
+    ws->certified = (uint32_t *)p;
 }
 
 extern "C" int kq_launch_moe_supported(const kq_launch_moe_dims *d,
