@@ -34,7 +34,7 @@
  * bits) after an exact power-of-two scaling that puts the row's largest
  * magnitude in [2^14, 2^15), so neither part overflows and small rows keep
  * their precision; every MFMA accumulates in fp32. Outputs are compared
- * with the CPU by tolerance (1e-3 relative to the row RMS, 1e-4 absolute).
+ * with the CPU by tolerance (per element, 1e-4 absolute or 1e-3 relative).
  *
  * MFMA operands: A = activations (16 tokens x K), B = weights (K x 16
  * rows); lane l holds token / row l % 16 and a k-group l / 16, and the
