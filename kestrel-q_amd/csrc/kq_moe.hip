@@ -270,89 +270,98 @@ __global__ __launch_bounds__(64) void router_chain(const float *__restrict__ wt,
         shared_logit[t] = acc;
 }
 
-/* Several tokens per lane: lane e of a wave runs the chains of expert e for
- * kChainTB consecutive tokens, so each router value it reads serves that
- * many chains, and the waves of a workgroup (consecutive token groups, the
- * same 64 experts) read the same router columns, which L1 then serves. The
- * workgroup's activations are staged in LDS 256 columns at a time and read
- * as broadcasts. Each chain is still p = w * x rounded, acc = acc + p in
- * column order. */
-/* two chains per lane (enough independent adds to keep the VALU issuing)
- * and two waves per workgroup: small workgroups spread the T * (E + 1)
- * chains evenly over the CUs; the waves of one workgroup share the router
- * columns through L1 */
-constexpr uint32_t kChainTB = 2;
-constexpr uint32_t kChainWaves = 2;
-constexpr uint32_t kChainCols = 256; /* activation columns staged per round */
+/* Many tokens, the router read where it lies (no transposed copy): lane e
+ * of a wave runs the chain of expert e0 + e for one token; the kSxWaves
+ * waves of a workgroup take consecutive tokens and share one copy of their
+ * 64 router rows, which the workgroup moves into LDS 64 columns at a time,
+ * transposed to [q][expert] (one float4 of padding per q line), double
+ * buffered: one barrier per 64 columns. A token's activations are the same
+ * in every lane, so they come through scalar loads into SGPRs and each term
+ * is two VALU instructions, p = w * x rounded, then acc = acc + p, in
+ * column order. One token per wave keeps four waves on every SIMD to cover
+ * the loads' latency (two tokens per wave halve the LDS reads per term but
+ * leave two waves per SIMD, and ran 30% slower at 512 x 512). Rows past the
+ * experts read as zeros and are not stored; the shared gate vector is not a
+ * row here (its logit only feeds the sigmoid gate, compared by tolerance). */
+constexpr uint32_t kSxTW = 1;
+constexpr uint32_t kSxWaves = 8;
+constexpr uint32_t kSxCols = 64;
 
-__global__ __launch_bounds__(64 * kChainWaves) void router_chain_tb(
-    const float *__restrict__ wt, const float *__restrict__ hidden_states, uint32_t tokens,
-    uint32_t experts, uint32_t hidden, uint32_t ep, float *__restrict__ logits,
-    float *__restrict__ shared_logit) {
-    constexpr uint32_t TPG = kChainTB * kChainWaves; /* tokens per workgroup */
-    constexpr uint32_t NQ = kChainCols / 4u;
-    __shared__ float4 xs[TPG][NQ];
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t e = blockIdx.x * 64u + lane;
-    const uint32_t tg = blockIdx.y * TPG;
-    const uint32_t nq = hidden / 4u;
-    /* the 64-expert router column group, transposed: step q of lane l at
-     * (q * ep + l) * 16 bytes */
-    const KqBuf rb = kq_buf(wt + 4u * (blockIdx.x * 64u), (nq - 1u) * ep * 16u + 64u * 16u);
-    float acc[kChainTB];
+__global__ __launch_bounds__(64 * kSxWaves) void router_chain_sx(
+    const float *__restrict__ router, const float *__restrict__ hidden_states, uint32_t tokens,
+    uint32_t experts, uint32_t hidden, float *__restrict__ logits, uint32_t *status) {
+    constexpr uint32_t NQ = kSxCols / 4u;  /* float4 per row per chunk */
+    constexpr uint32_t PITCH = 65u;        /* float4 per q line */
+    constexpr uint32_t LOADS = 64u * NQ / (64u * kSxWaves); /* float4 per thread per chunk */
+    __shared__ float4 tile[2][NQ * PITCH];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t e0 = blockIdx.y * 64u;
+    const uint32_t tb = (blockIdx.x * kSxWaves + wave) * kSxTW;
+    /* loader: float4 q = tid % NQ of rows tid / NQ + (64 * kSxWaves / NQ) * k */
+    const uint32_t lq = tid % NQ, lr = tid / NQ;
+    constexpr uint32_t RSTEP = 64u * kSxWaves / NQ;
+    const float *xr[kSxTW];
 #pragma unroll
-    for (uint32_t b = 0; b < kChainTB; ++b) acc[b] = 0.0f;
-    constexpr uint32_t RUN = 8;
-    uint4 wa[RUN], wb[RUN];
-    auto fetch = [&](uint4 (&w)[RUN], uint32_t q0) {
+    for (uint32_t b = 0; b < kSxTW; ++b) {
+        const uint32_t t = tb + b < tokens ? tb + b : tokens - 1u;
+        xr[b] = hidden_states + (size_t)__builtin_amdgcn_readfirstlane(t) * hidden;
+    }
+    float4 ld[LOADS];
+    bool bad = false;
+    auto gload = [&](uint32_t c) {
 #pragma unroll
-        for (uint32_t k = 0; k < RUN; ++k) w[k] = kq_ld128(rb, ((q0 + k) * ep + lane) * 16u, 0u);
+        for (uint32_t k = 0; k < LOADS; ++k) {
+            const uint32_t e = e0 + lr + RSTEP * k;
+            ld[k] = e < experts
+                        ? *(const float4 *)(router + (size_t)e * hidden + c * kSxCols + 4u * lq)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     };
-    /* column q (global) of this wave's tokens from the staged round */
-    auto run = [&](const uint4 (&w)[RUN], uint32_t q0) {
+    auto lstore = [&](uint32_t buf) {
 #pragma unroll
-        for (uint32_t k = 0; k < RUN; ++k) {
-            const float4 wv = as_f4(w[k]);
-            const uint32_t ql = (q0 + k) % NQ;
+        for (uint32_t k = 0; k < LOADS; ++k) {
+            const float4 v = ld[k];
+            bad |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                   !kq_isfinite(v.w);
+            tile[buf][lq * PITCH + lr + RSTEP * k] = v;
+        }
+    };
+    float acc[kSxTW];
 #pragma unroll
-            for (uint32_t b = 0; b < kChainTB; ++b) {
-                const float4 xv = xs[wave * kChainTB + b][ql];
+    for (uint32_t b = 0; b < kSxTW; ++b) acc[b] = 0.0f;
+    const uint32_t nc = hidden / kSxCols;
+    gload(0u);
+    lstore(0u);
+    __syncthreads();
+    if (nc > 1u) gload(1u);
+    for (uint32_t c = 0; c < nc; ++c) {
+        const float4 *tl = tile[c & 1u] + lane;
+        /* the chunk's 64 columns of the token in SGPRs, one wait per chunk */
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; ++q) {
+            const float4 w = tl[q * PITCH];
+#pragma unroll
+            for (uint32_t b = 0; b < kSxTW; ++b) {
+                const float4 xv = *(const float4 *)(xr[b] + c * kSxCols + 4u * q);
                 float p;
-                p = wv.x * xv.x; acc[b] = acc[b] + p;
-                p = wv.y * xv.y; acc[b] = acc[b] + p;
-                p = wv.z * xv.z; acc[b] = acc[b] + p;
-                p = wv.w * xv.w; acc[b] = acc[b] + p;
+                p = w.x * xv.x; acc[b] = acc[b] + p;
+                p = w.y * xv.y; acc[b] = acc[b] + p;
+                p = w.z * xv.z; acc[b] = acc[b] + p;
+                p = w.w * xv.w; acc[b] = acc[b] + p;
             }
         }
-    };
-    /* nq is a multiple of NQ (and of 2 * RUN) on this path. Every path
-     * issues the same router loads, so no wait drains the run in flight. */
-    fetch(wa, 0u);
-    for (uint32_t c = 0; c < nq; c += NQ) {
-        __syncthreads(); /* the previous round's readers are done */
-        for (uint32_t i = threadIdx.x; i < TPG * NQ; i += 64u * kChainWaves) {
-            const uint32_t tt = i / NQ, qq = i % NQ;
-            const uint32_t t = tg + tt < tokens ? tg + tt : tokens - 1u;
-            xs[tt][qq] = ((const float4 *)(hidden_states + (size_t)t * hidden))[c + qq];
-        }
+        /* the other buffer was last read before the previous barrier */
+        if (c + 1u < nc) lstore((c + 1u) & 1u);
         __syncthreads();
-        for (uint32_t q = c; q < c + NQ; q += 2u * RUN) {
-            fetch(wb, q + RUN);
-            run(wa, q);
-            fetch(wa, q + 2u * RUN < nq ? q + 2u * RUN : q);
-            run(wb, q + RUN);
-        }
+        if (c + 2u < nc) gload(c + 2u);
     }
+    const uint32_t e = e0 + lane;
 #pragma unroll
-    for (uint32_t b = 0; b < kChainTB; ++b) {
-        const uint32_t t = tg + wave * kChainTB + b;
-        if (t >= tokens) continue;
-        if (e < experts)
-            logits[(size_t)t * experts + e] = acc[b];
-        else if (e == experts)
-            shared_logit[t] = acc[b];
+    for (uint32_t b = 0; b < kSxTW; ++b) {
+        if (tb + b < tokens && e < experts) logits[(size_t)(tb + b) * experts + e] = acc[b];
     }
+    if (bad) kq_flag(status, KQ_DEV_INPUT);
 }
 
 /* Maximum over the 64 lanes of a wave, returned in every lane: DPP within
@@ -826,11 +835,42 @@ __device__ __forceinline__ void route_finish_body(
     }
 }
 
+/* One workgroup per token. With sgw given, the token's shared gate logit
+ * is first formed here as sgw . x in any order (it only feeds the sigmoid
+ * gate, compared by tolerance); thread 0 stores it and reads it back in
+ * the body. */
 __global__ __launch_bounds__(1024) void route_finish(
-    const float *__restrict__ logits_all, const float *__restrict__ shared_logit,
+    const float *__restrict__ logits_all, float *__restrict__ shared_logit,
     uint32_t experts, uint32_t top_k, float *__restrict__ probs_all, uint32_t *__restrict__ ids_all,
     float *__restrict__ weights_all, uint32_t *__restrict__ order_all,
-    float *__restrict__ shared_scale, uint32_t *status) {
+    float *__restrict__ shared_scale, uint32_t *status, const float *__restrict__ sgw,
+    const float *__restrict__ hidden_states, uint32_t hidden) {
+    if (sgw != nullptr) {
+        __shared__ float part[16];
+        const uint32_t e = threadIdx.x, lane = e & 63u, nw = blockDim.x >> 6;
+        const float4 *xq = (const float4 *)(hidden_states + (size_t)blockIdx.x * hidden);
+        const float4 *gq = (const float4 *)sgw;
+        float acc = 0.0f;
+        bool bad = false;
+        for (uint32_t q = e; q < hidden / 4u; q += blockDim.x) {
+            const float4 gv = gq[q], xv = xq[q];
+            bad |= !kq_isfinite(gv.x) || !kq_isfinite(gv.y) || !kq_isfinite(gv.z) ||
+                   !kq_isfinite(gv.w);
+            acc = fmaf(gv.x, xv.x, acc);
+            acc = fmaf(gv.y, xv.y, acc);
+            acc = fmaf(gv.z, xv.z, acc);
+            acc = fmaf(gv.w, xv.w, acc);
+        }
+        acc = wave_sum_f32(acc);
+        if (lane == 0u) part[e >> 6] = acc;
+        __syncthreads();
+        if (e == 0u) {
+            float sum = 0.0f;
+            for (uint32_t i = 0; i < nw; ++i) sum += part[i];
+            shared_logit[blockIdx.x] = sum;
+        }
+        if (bad) kq_flag(status, KQ_DEV_INPUT);
+    }
     route_finish_body(blockIdx.x, logits_all, shared_logit, experts, top_k, probs_all, ids_all,
                       weights_all, order_all, shared_scale, status);
 }
@@ -1928,29 +1968,31 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
         }
     }
 #undef KQ_ROUTER_DECODE
-    if (!fused) {
-        /* several tokens, or a hidden size without a fused instance */
+    /* several tokens: the chains read the router in place and the route
+     * finish forms the shared gate's logit */
+    const bool in_place = !fused && d->hidden % kSxCols == 0u;
+    if (in_place) {
+        const uint32_t per_wg = kSxTW * kSxWaves;
+        hipLaunchKernelGGL(router_chain_sx,
+                           dim3((tokens + per_wg - 1u) / per_wg, (d->experts + 63u) / 64u),
+                           dim3(64u * kSxWaves), 0, s, router, hidden, tokens, d->experts,
+                           d->hidden, ws->logits, status);
+    } else if (!fused) {
+        /* a hidden size the chunked chains do not cover */
         const dim3 tgrid(ep / 64u, (d->hidden / 4u + 15u) / 16u);
         hipLaunchKernelGGL(router_transpose, tgrid, dim3(kThreads), 0, s, router,
                            shared_gate_weight, d->experts, d->hidden, ep, ws->router_t, status);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        if (tokens >= kChainTB * kChainWaves && d->hidden % kChainCols == 0u) {
-            const uint32_t per_wg = kChainTB * kChainWaves;
-            hipLaunchKernelGGL(router_chain_tb, dim3(ep / 64u, (tokens + per_wg - 1u) / per_wg),
-                               dim3(64 * kChainWaves), 0, s, ws->router_t, hidden, tokens,
-                               d->experts, d->hidden, ep, ws->logits, ws->shared_logit);
-        } else {
-            hipLaunchKernelGGL(router_chain, dim3(ep / 64u, tokens), dim3(64), 0, s,
-                               ws->router_t, hidden, d->experts, d->hidden, ep, ws->logits,
-                               ws->shared_logit);
-        }
+        hipLaunchKernelGGL(router_chain, dim3(ep / 64u, tokens), dim3(64), 0, s, ws->router_t,
+                           hidden, d->experts, d->hidden, ep, ws->logits, ws->shared_logit);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, ws->logits, ws->shared_logit,
                        d->experts, d->top_k, ws->probs, ws->ids, ws->weights, ws->order,
-                       ws->shared_scale, status);
+                       ws->shared_scale, status, in_place ? shared_gate_weight : nullptr, hidden,
+                       d->hidden);
     e = hipGetLastError();
     /* the one-token selection writes the caller's ids itself; here they
      * are copied (several tokens, or a hidden size without an instance) */
@@ -1969,8 +2011,9 @@ extern "C" hipError_t kq_launch_moe_route_finish(const float *logits, const floa
     const uint32_t fin = 64u * ((experts + 63u) / 64u + 1u);
     if (fin > 1024u || top_k == 0u || top_k > experts || top_k > kMaxTopK)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, logits, shared_logit,
-                       experts, top_k, probs, ids, weights, order, shared_scale, status);
+    hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, logits,
+                       const_cast<float *>(shared_logit), experts, top_k, probs, ids, weights,
+                       order, shared_scale, status, nullptr, nullptr, 0u);
     return hipGetLastError();
 }
 

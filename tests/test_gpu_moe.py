@@ -89,6 +89,19 @@ def test_routing_512x2048_bit_exact(ctx, seed, tokens):
     assert_route_exact(got, oracle_route(H, E, K, router, x))
 
 
+@pytest.mark.parametrize("H,E,K,T", [(320, 100, 6, 9), (2560, 130, 8, 3), (96, 70, 4, 5),
+                                     (64, 512, 10, 2)])
+def test_routing_odd_shapes_bit_exact(ctx, H, E, K, T):
+    # Expert counts off multiples of 64 (partial last expert group), token
+    # counts off the 8-token workgroup, one 64-column chunk, and a hidden
+    # size (96) that is not a whole number of 64-column chunks.
+    rng = np.random.default_rng(H * 1000 + E)
+    router = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    got = device_route(ctx, H, E, K, router, np.zeros(H, np.float32), x)
+    assert_route_exact(got, oracle_route(H, E, K, router, x))
+
+
 @pytest.mark.parametrize("pattern", ["duplicate-rows", "zero-router", "quantised-logits"])
 def test_routing_tie_heavy(ctx, pattern):
     # Exact probability ties at and around the k-th boundary: the partial
