@@ -789,13 +789,21 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
 
 constexpr uint32_t kPermChunk = 256; /* tokens per rank pass */
 
+/* The Q4_K gate/up pass's work list (kq_grouped_gu.hip, gu_items): one
+ * item per kItemRows-token chunk of an expert, routed experts in id order,
+ * then the shared expert's chunks; [0] the count, items from [4] on as
+ * (expert | kItemShared, first | count << 24). */
+constexpr uint32_t kItemRows = 16;
+constexpr uint32_t kItemShared = 0x80000000u;
+
 __global__ __launch_bounds__(1024) void moe_permute(const uint32_t *__restrict__ ids,
                                                     uint32_t tokens, uint32_t top_k,
                                                     uint32_t experts, uint32_t *__restrict__ offsets,
                                                     uint32_t *__restrict__ perm_tok,
                                                     uint32_t *__restrict__ pos,
                                                     uint32_t *__restrict__ pair_slot,
-                                                    uint32_t *status) {
+                                                    uint32_t *status, uint32_t *items,
+                                                    uint32_t with_shared) {
     __shared__ uint32_t cnt[1024];
     __shared__ uint32_t base[1024];
     __shared__ uint32_t bits[1024][kPermChunk / 32u];
@@ -834,6 +842,38 @@ __global__ __launch_bounds__(1024) void moe_permute(const uint32_t *__restrict__
         if (tid == experts) offsets[tid] = ex; /* = pairs */
     }
     __syncthreads();
+    if (items != nullptr) {
+        /* the gate/up work list from the same counts: exclusive scan of
+         * the chunks per expert */
+        __shared__ uint32_t csum[16];
+        const uint32_t c = tid < experts ? cnt[tid] : 0u;
+        const uint32_t nc = (c + kItemRows - 1u) / kItemRows;
+        uint32_t incl = nc;
+#pragma unroll
+        for (uint32_t o = 1; o < 64u; o <<= 1) {
+            const uint32_t n = __shfl_up(incl, o, KQ_WAVE);
+            if (lane >= o) incl += n;
+        }
+        if (lane == 63u) csum[wave] = incl;
+        __syncthreads();
+        uint32_t ib = incl - nc, total = 0u;
+        for (uint32_t w = 0; w < 16u; ++w) {
+            ib += w < wave ? csum[w] : 0u;
+            total += csum[w];
+        }
+        uint32_t *list = items + 4;
+        const uint32_t o0 = base[tid];
+        for (uint32_t k = 0; k < nc; ++k) {
+            list[2u * (ib + k)] = tid;
+            list[2u * (ib + k) + 1u] = (o0 + kItemRows * k) | (min(c - kItemRows * k, kItemRows) << 24);
+        }
+        const uint32_t nsh = with_shared ? (tokens + kItemRows - 1u) / kItemRows : 0u;
+        for (uint32_t k = tid; k < nsh; k += 1024u) {
+            list[2u * (total + k)] = kItemShared | k;
+            list[2u * (total + k) + 1u] = (kItemRows * k) | (min(tokens - kItemRows * k, kItemRows) << 24);
+        }
+        if (tid == 0u) items[0] = total + nsh;
+    }
     for (uint32_t t0 = 0; t0 < tokens; t0 += kPermChunk) {
         const uint32_t nt = min(kPermChunk, tokens - t0);
         for (uint32_t w = tid; w < 1024u * (kPermChunk / 32u); w += 1024u)
@@ -873,30 +913,62 @@ __global__ __launch_bounds__(1024) void moe_permute(const uint32_t *__restrict__
 /* ------------------------------------------------------------------ */
 /* combine, in the reference's order (src/kq_moe_qwen38.c:722-765, :826) */
 
+/* One thread per four consecutive outputs of a token: the slots' rows are
+ * requested together (up to kCombineRun of them before the first add),
+ * then summed in the reference's order with separately rounded products. */
+constexpr uint32_t kCombineRun = 16;
+
 __global__ __launch_bounds__(256) void moe_combine(
     const float *__restrict__ o, const uint32_t *__restrict__ pos,
     const uint32_t *__restrict__ order, const float *__restrict__ weights,
     const float *__restrict__ shared_scale, uint32_t tokens, uint32_t top_k, uint32_t hidden,
     float *__restrict__ out, uint32_t *status) {
     const uint32_t t = blockIdx.y;
-    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
-    if (n >= hidden) return;
+    const uint32_t q = blockIdx.x * 256u + threadIdx.x; /* float4 of the row */
+    const uint32_t hq = hidden / 4u;
+    if (q >= hq) return;
     const uint32_t tk = tokens * top_k;
+    const float4 *o4 = (const float4 *)o;
     bool bad = false;
-    float sum = 0.0f;
-    for (uint32_t j = 0; j < top_k; ++j) {
-        const uint32_t s = order[(size_t)t * top_k + j];
-        const uint32_t p = pos[(size_t)t * top_k + s];
-        const float v = o[(size_t)p * hidden + n];
-        bad |= !kq_isfinite(v);
-        const float weighted = v * weights[(size_t)t * top_k + s];
-        sum = sum + weighted;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](const float4 v, const float w) {
+        bad |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) || !kq_isfinite(v.w);
+        float p;
+        p = v.x * w; sum.x = sum.x + p;
+        p = v.y * w; sum.y = sum.y + p;
+        p = v.z * w; sum.z = sum.z + p;
+        p = v.w * w; sum.w = sum.w + p;
+    };
+    for (uint32_t j0 = 0; j0 < top_k; j0 += kCombineRun) {
+        float4 v[kCombineRun];
+        float wv[kCombineRun];
+#pragma unroll
+        for (uint32_t i = 0; i < kCombineRun; ++i) {
+            if (j0 + i < top_k) {
+                const uint32_t sl = order[(size_t)t * top_k + j0 + i];
+                const uint32_t p = pos[(size_t)t * top_k + sl];
+                wv[i] = weights[(size_t)t * top_k + sl];
+                v[i] = o4[(size_t)p * hq + q];
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kCombineRun; ++i)
+            if (j0 + i < top_k) add(v[i], wv[i]);
     }
-    const float so = o[(size_t)(tk + t) * hidden + n];
-    const float gated = so * shared_scale[t];
-    const float v = sum + gated;
-    bad |= !kq_isfinite(so) || !kq_isfinite(sum) || !kq_isfinite(gated) || !kq_isfinite(v);
-    out[(size_t)t * hidden + n] = v;
+    const float4 so = o4[(size_t)(tk + t) * hq + q];
+    const float sc = shared_scale[t];
+    float4 r;
+    auto fin = [&](float sv, float sm, float &dst) {
+        const float gated = sv * sc;
+        const float val = sm + gated;
+        bad |= !kq_isfinite(sv) || !kq_isfinite(sm) || !kq_isfinite(gated) || !kq_isfinite(val);
+        dst = val;
+    };
+    fin(so.x, sum.x, r.x);
+    fin(so.y, sum.y, r.y);
+    fin(so.z, sum.z, r.z);
+    fin(so.w, sum.w, r.w);
+    ((float4 *)out)[(size_t)t * hq + q] = r;
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
 }
 
@@ -1537,16 +1609,34 @@ extern "C" hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens
                                             uint32_t *pair_slot, uint32_t *status,
                                             hipStream_t s) {
     hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ids, tokens, top_k, experts,
-                       offsets, pair_token, pos, pair_slot, status);
+                       offsets, pair_token, pos, pair_slot, status, nullptr, 0u);
     return hipGetLastError();
+}
+
+static bool gu_lds_routed(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w) {
+    return w->gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
+}
+
+extern "C" void *kq_launch_moe_grouped_stage(const kq_launch_moe_dims *d,
+                                             const kq_launch_moe_weights *w,
+                                             const kq_launch_moe_ws *ws) {
+    return gu_lds_routed(d, w) ? (void *)ws->outp : nullptr;
 }
 
 extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
                                             const kq_launch_moe_weights *w, const float *hidden,
                                             uint32_t tokens, const kq_launch_moe_ws *ws,
-                                            float *out, uint32_t *status, hipStream_t s) {
+                                            int staged, float *out, uint32_t *status,
+                                            hipStream_t s) {
+    /* Q4_K gate/up rows stream through LDS (kq_grouped_gu.hip) from
+     * activations split once per token into the start of outp, which only
+     * the down pass writes later; the work list the permutation builds for
+     * it (gitems) also drives the Q6_K down pass (kq_grouped_dn.hip) */
+    const bool lds_routed = gu_lds_routed(d, w);
+    const bool lds_shared = lds_routed && w->shared_gate_type == KQ_LAUNCH_Q4_K;
     hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ws->ids, tokens, d->top_k,
-                       d->experts, ws->offsets, ws->perm_tok, ws->pos, nullptr, status);
+                       d->experts, ws->offsets, ws->perm_tok, ws->pos, nullptr, status,
+                       lds_routed ? (uint32_t *)ws->gitems : nullptr, lds_shared ? 1u : 0u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint8_t *g = (const uint8_t *)w->gate, *u = (const uint8_t *)w->up;
@@ -1554,22 +1644,15 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     const uint32_t E = d->experts;
     const uint32_t sh_wgs = (tokens + kSharedChunks * kTile - 1u) / (kSharedChunks * kTile);
     /* gate/up + SwiGLU, then down: the routed experts' workgroups and the
-     * shared expert's in one launch when their formats agree. Q4_K gate/up
-     * rows stream through LDS (kq_grouped_gu.hip) from activations split
-     * once per token into the start of outp, which only the down pass
-     * writes later; the work list it builds (gitems) also drives the Q6_K
-     * down pass (kq_grouped_dn.hip). */
-    const bool lds_routed = w->gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
-    const bool lds_shared =
-        lds_routed && w->shared_gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
-    if (lds_routed) {
+     * shared expert's in one launch when their formats agree */
+    if (lds_routed && !staged) {
         e = kq_launch_gu_stage(hidden, tokens, d->hidden, ws->outp, status, s);
         if (e != hipSuccess) return e;
     }
     if (lds_routed) {
         e = kq_launch_gu_lds(d->hidden, g, u, sg, su, ws->outp, ws->offsets, ws->perm_tok, E,
-                             tokens, d->top_k, d->inter, lds_shared ? 1 : 0, ws->gitems, ws->act,
-                             status, s);
+                             tokens, d->top_k, d->inter, lds_shared ? 1 : 0, 1, ws->gitems,
+                             ws->act, status, s);
         if (e == hipSuccess && !lds_shared)
             e = pass_any<2>(w->shared_gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets,
                             ws->perm_tok, E, tokens, d->top_k, d->inter, E, sh_wgs, ws->act,
@@ -1605,7 +1688,7 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
                             ws->outp, status, s);
     }
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(moe_combine, dim3((d->hidden + 255u) / 256u, tokens), dim3(256), 0, s,
+    hipLaunchKernelGGL(moe_combine, dim3((d->hidden / 4u + 255u) / 256u, tokens), dim3(256), 0, s,
                        ws->outp, ws->pos, ws->order, ws->weights, ws->shared_scale, tokens,
                        d->top_k, d->hidden, out, status);
     return hipGetLastError();

@@ -43,6 +43,7 @@
  * number of loads per tile, and waits for all of its loads before it ends.
  */
 #include "kq_launch.h"
+#include "kq_stage.h"
 #include "kq_device.h"
 
 namespace {
@@ -101,91 +102,10 @@ __device__ __forceinline__ uint32_t lds_addr(T *p) {
 /* ------------------------------------------------------------------ */
 /* per-token activation split */
 
-/* Layout of the staged rows (one region, carved by the launcher):
- *   xh[t][K], xl[t][K]   fp16, the scaled row split hi + lo
- *   sx[t][K/128][8]      fp16: sums of sub-blocks 4q .. 4q + 3 (hi), then
- *                        the same four (lo); the sums carry 2^-5
- *   sig[t]               the row's power-of-two scale, or kBadRow */
-constexpr int kBadRow = 0x7fffffff;
-
-struct StagedX {
-    _Float16 *xh, *xl, *sx;
-    int *sig;
-};
-
-__device__ __forceinline__ StagedX staged_at(void *base, uint32_t tokens, uint32_t k) {
-    StagedX s;
-    uint8_t *p = (uint8_t *)base;
-    s.xh = (_Float16 *)p;
-    p += (size_t)tokens * k * 2u;
-    s.xl = (_Float16 *)p;
-    p += (size_t)tokens * k * 2u;
-    s.sx = (_Float16 *)p;
-    p += (size_t)tokens * (k / 128u) * 16u;
-    s.sig = (int *)p;
-    return s;
-}
-
 /* grid: one workgroup of 256 threads per token; k a multiple of 256 */
 __global__ __launch_bounds__(256) void gu_stage(const float *__restrict__ X, uint32_t tokens,
                                                 uint32_t k, void *staged, uint32_t *status) {
-    __shared__ float s_max[4];
-    __shared__ uint32_t s_bad[4];
-    const StagedX sx = staged_at(staged, tokens, k);
-    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-    const float4 *row = (const float4 *)(X + (size_t)t * k);
-    const uint32_t ng = k / 4u; /* float4 groups, a multiple of 64 */
-    float m = 0.0f;
-    bool nf = false;
-    for (uint32_t i = threadIdx.x; i < ng; i += 256u) {
-        const float4 v = row[i];
-        nf |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) || !kq_isfinite(v.w);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    const bool wbad = __ballot(nf) != 0ull;
-    if (lane == 0u) {
-        s_max[w] = m;
-        s_bad[w] = wbad ? 1u : 0u;
-    }
-    __syncthreads();
-    m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
-    const bool bad = (s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3]) != 0u;
-    int sig = 0;
-    if (!bad && m > 0.0f) sig = 15 - __builtin_amdgcn_frexp_expf(m);
-    if (bad) sig = kBadRow;
-    for (uint32_t i = threadIdx.x; i < ng; i += 256u) {
-        const float4 v = row[i];
-        const float a[4] = {v.x, v.y, v.z, v.w};
-        _Float16 hi[4], lo[4];
-        float part = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float xs = bad ? 0.0f : ldexpf(a[c], sig);
-            hi[c] = (_Float16)xs;
-            lo[c] = (_Float16)(xs - (float)hi[c]);
-            part += xs;
-        }
-        *(h4 *)(sx.xh + (size_t)t * k + 4u * i) = h4{hi[0], hi[1], hi[2], hi[3]};
-        *(h4 *)(sx.xl + (size_t)t * k + 4u * i) = h4{lo[0], lo[1], lo[2], lo[3]};
-        /* 32-column sums: groups 8j .. 8j + 7 are eight consecutive lanes */
-        part += __shfl_xor(part, 1, 64);
-        part += __shfl_xor(part, 2, 64);
-        part += __shfl_xor(part, 4, 64);
-        if ((i & 7u) == 0u) {
-            const uint32_t sb = i / 8u;
-            const float s = part * 0.03125f;
-            const _Float16 sh = (_Float16)s;
-            const _Float16 sl = (_Float16)(s - (float)sh);
-            _Float16 *e = sx.sx + ((size_t)t * (k / 128u) + sb / 4u) * 8u;
-            e[sb % 4u] = sh;
-            e[4u + sb % 4u] = sl;
-        }
-    }
-    if (threadIdx.x == 0u) {
-        sx.sig[t] = sig;
-        if (bad) kq_flag(status, KQ_DEV_INPUT);
-    }
+    kq::stage_row(X, blockIdx.x, tokens, k, staged, status);
 }
 
 /* ------------------------------------------------------------------ */
@@ -347,7 +267,7 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_q4k(GuArgs a) {
         }
     };
 
-    const StagedX sx = staged_at(const_cast<void *>(a.staged), a.tokens, KD);
+    const kq::StagedX sx = kq::staged_at(const_cast<void *>(a.staged), a.tokens, KD);
     const KqBuf bxh = kq_buf(sx.xh, a.tokens * KD * 2u), bxl = kq_buf(sx.xl, a.tokens * KD * 2u);
     const KqBuf bsx = kq_buf(sx.sx, a.tokens * (KD / 128u) * 16u);
     const uint32_t tk = a.tokens * a.top_k;
@@ -580,15 +500,17 @@ extern "C" hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const 
                                        const void *staged, const uint32_t *offsets,
                                        const uint32_t *perm_tok, uint32_t experts,
                                        uint32_t tokens, uint32_t top_k, uint32_t rows,
-                                       int with_shared, void *items, float *act,
-                                       uint32_t *status, hipStream_t s) {
+                                       int with_shared, int items_ready, void *items,
+                                       float *act, uint32_t *status, hipStream_t s) {
     if (experts > 1023u) return hipErrorInvalidValue;
     uint32_t *n_items = (uint32_t *)items;
     uint32_t *list = n_items + 4;
-    hipLaunchKernelGGL(gu_items, dim3(1), dim3(1024), 0, s, offsets, experts, tokens,
-                       with_shared ? 1u : 0u, list, n_items);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (!items_ready) {
+        hipLaunchKernelGGL(gu_items, dim3(1), dim3(1024), 0, s, offsets, experts, tokens,
+                           with_shared ? 1u : 0u, list, n_items);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     GuArgs a;
     a.gate = (const uint8_t *)gate;
     a.up = (const uint8_t *)up;

@@ -151,11 +151,14 @@ int kq_launch_moe_supported(const kq_launch_moe_dims *d, const kq_launch_moe_wei
  * selection, from the exact chains of the contenders when that separates
  * it, and from every exact chain otherwise; the logits and probabilities
  * are then not always written and the weights are within fp32 tolerance of
- * the CPU's. ids_out (optional) also receives the ids. */
+ * the CPU's. ids_out (optional) also receives the ids. stage (optional,
+ * several tokens): where the route finish also splits every token's row for
+ * the grouped gate/up pass (kq_launch_moe_grouped_stage). */
 hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const float *router,
                                const float *shared_gate_weight, const float *hidden,
                                uint32_t tokens, const kq_launch_moe_ws *ws, uint32_t *status,
-                               int certify, uint32_t *ids_out, hipStream_t stream);
+                               int certify, uint32_t *ids_out, void *stage,
+                               hipStream_t stream);
 /* grouped multi-token path (kq_grouped.hip): stable permutation, per-expert
  * MFMA gate/up + SwiGLU and down over all of an expert's tokens, ordered
  * combine; needs the route results in ws */
@@ -174,11 +177,13 @@ uint64_t kq_launch_gu_stage_bytes(uint32_t tokens, uint32_t hidden);
 hipError_t kq_launch_gu_stage(const float *hidden_states, uint32_t tokens, uint32_t hidden,
                               void *staged, uint32_t *status, hipStream_t s);
 uint64_t kq_launch_gu_items_bytes(uint32_t experts, uint32_t tokens, uint32_t top_k);
+/* items_ready: the permutation already wrote the item list (moe_permute) */
 hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const void *up,
                             const void *shared_gate, const void *shared_up, const void *staged,
                             const uint32_t *offsets, const uint32_t *perm_tok, uint32_t experts,
                             uint32_t tokens, uint32_t top_k, uint32_t rows, int with_shared,
-                            void *items, float *act, uint32_t *status, hipStream_t s);
+                            int items_ready, void *items, float *act, uint32_t *status,
+                            hipStream_t s);
 /* prefill Q6_K down over the gate/up pass's item list (kq_grouped_dn.hip) */
 int kq_launch_dn_lds_supported(uint32_t inter);
 uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter);
@@ -186,10 +191,15 @@ hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const void *down,
                             const void *shared_down, const float *act, uint32_t tokens,
                             uint32_t top_k, const void *items, void *staged, float *out,
                             uint32_t *status, hipStream_t s);
+/* where the Q4_K gate/up pass reads its per-token activation split (ws's
+ * outp), or NULL when these weights take another pass; the route can form
+ * it (kq_launch_moe_route's stage), and staged tells the grouped path so */
+void *kq_launch_moe_grouped_stage(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
+                                  const kq_launch_moe_ws *ws);
 hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                                  const float *hidden, uint32_t tokens,
-                                 const kq_launch_moe_ws *ws, float *out, uint32_t *status,
-                                 hipStream_t stream);
+                                 const kq_launch_moe_ws *ws, int staged, float *out,
+                                 uint32_t *status, hipStream_t stream);
 hipError_t kq_launch_moe_experts(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,
                                  const float *hidden, uint32_t tokens,
                                  const kq_launch_moe_ws *ws, float *out, uint32_t *status,

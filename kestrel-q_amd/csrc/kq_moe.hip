@@ -32,6 +32,7 @@
 
 #include "kq_launch.h"
 #include "kq_rowdot.h"
+#include "kq_stage.h"
 
 namespace {
 
@@ -838,13 +839,15 @@ __device__ __forceinline__ void route_finish_body(
 /* One workgroup per token. With sgw given, the token's shared gate logit
  * is first formed here as sgw . x in any order (it only feeds the sigmoid
  * gate, compared by tolerance); thread 0 stores it and reads it back in
- * the body. */
+ * the body. With stage given, the workgroup also splits the token's row
+ * for the Q4_K prefill gate/up pass (kq_stage.h). */
 __global__ __launch_bounds__(1024) void route_finish(
     const float *__restrict__ logits_all, float *__restrict__ shared_logit,
     uint32_t experts, uint32_t top_k, float *__restrict__ probs_all, uint32_t *__restrict__ ids_all,
     float *__restrict__ weights_all, uint32_t *__restrict__ order_all,
     float *__restrict__ shared_scale, uint32_t *status, const float *__restrict__ sgw,
-    const float *__restrict__ hidden_states, uint32_t hidden) {
+    const float *__restrict__ hidden_states, uint32_t hidden, void *stage) {
+    if (stage != nullptr) kq::stage_row(hidden_states, blockIdx.x, gridDim.x, hidden, stage, status);
     if (sgw != nullptr) {
         __shared__ float part[16];
         const uint32_t e = threadIdx.x, lane = e & 63u, nw = blockDim.x >> 6;
@@ -1910,7 +1913,7 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
                                           const float *shared_gate_weight, const float *hidden,
                                           uint32_t tokens, const kq_launch_moe_ws *ws,
                                           uint32_t *status, int certify, uint32_t *ids_out,
-                                          hipStream_t s) {
+                                          void *stage, hipStream_t s) {
     const uint32_t ep = pad64(d->experts + 1u);
     const uint32_t groups = (d->experts + 1u + kRtRows - 1u) / kRtRows;
     bool fused = tokens == 1u;
@@ -1992,7 +1995,7 @@ extern "C" hipError_t kq_launch_moe_route(const kq_launch_moe_dims *d, const flo
     hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, ws->logits, ws->shared_logit,
                        d->experts, d->top_k, ws->probs, ws->ids, ws->weights, ws->order,
                        ws->shared_scale, status, in_place ? shared_gate_weight : nullptr, hidden,
-                       d->hidden);
+                       d->hidden, stage);
     e = hipGetLastError();
     /* the one-token selection writes the caller's ids itself; here they
      * are copied (several tokens, or a hidden size without an instance) */
@@ -2013,7 +2016,7 @@ extern "C" hipError_t kq_launch_moe_route_finish(const float *logits, const floa
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(route_finish, dim3(tokens), dim3(fin), 0, s, logits,
                        const_cast<float *>(shared_logit), experts, top_k, probs, ids, weights,
-                       order, shared_scale, status, nullptr, nullptr, 0u);
+                       order, shared_scale, status, nullptr, nullptr, 0u, nullptr);
     return hipGetLastError();
 }
 

@@ -1021,7 +1021,7 @@ kq_status kq_hip_moe_route_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
     e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, 0, NULL,
-                            c->stream);
+                            NULL, c->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(logits, ws.logits, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
                            c->stream);
@@ -1046,6 +1046,8 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
     kq_launch_moe_ws ws;
     hipError_t e;
     kq_status st;
+    int grouped;
+    void *stage;
     kq_diagnostic_clear(diag);
     if (w == NULL || out == NULL)
         return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE execution arguments are required");
@@ -1093,21 +1095,24 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
                        "reads them, equal intermediates");
     if (!aligned(w->routed_gate, 16u) || !aligned(w->routed_up, 16u) ||
         !aligned(w->routed_down, 16u) || !aligned(w->shared_gate, 16u) ||
-        !aligned(w->shared_up, 16u) || !aligned(w->shared_down, 16u) || !aligned(out, 4u))
-        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "MoE weights must be 16-byte aligned");
+        !aligned(w->shared_up, 16u) || !aligned(w->shared_down, 16u) || !aligned(out, 16u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT,
+                       "MoE weights and output must be 16-byte aligned");
     kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
+    /* several tokens: each expert's weights stream once for all of its
+     * tokens (grouped MFMA path), whose activation split the route finish
+     * forms; one token: the fused decode kernels */
+    grouped = tokens >= KQ_GROUPED_MIN_TOKENS && kq_launch_moe_grouped_supported(&d, &lw);
+    stage = grouped ? kq_launch_moe_grouped_stage(&d, &lw, &ws) : NULL;
     /* the layer needs the CPU's expert ids exactly and its weights to fp32
      * tolerance: one token may take the certified routing */
     e = kq_launch_moe_route(&d, w->router, w->shared_gate_weight, hidden, (uint32_t)tokens, &ws,
-                            c->d_status, 1, tokens == 1u ? ids : NULL, c->stream);
-    /* several tokens: each expert's weights stream once for all of its
-     * tokens (grouped MFMA path); one token: the fused decode kernels */
-    if (e == hipSuccess && tokens >= KQ_GROUPED_MIN_TOKENS &&
-        kq_launch_moe_grouped_supported(&d, &lw))
-        e = kq_launch_moe_grouped(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status,
-                                  c->stream);
+                            c->d_status, 1, tokens == 1u ? ids : NULL, stage, c->stream);
+    if (e == hipSuccess && grouped)
+        e = kq_launch_moe_grouped(&d, &lw, hidden, (uint32_t)tokens, &ws, stage != NULL, out,
+                                  c->d_status, c->stream);
     else if (e == hipSuccess)
         e = kq_launch_moe_experts(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status,
                                   c->stream);
