@@ -78,12 +78,21 @@ __global__ __launch_bounds__(kNormThreads) void gr_norm(const float *__restrict_
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);
 }
 
-/* rank[i] = silu(raw[i] / B), in place over T * r values */
+/* rank[i] = silu(raw[i] / B) over T * r values: raw in place, or (parts)
+ * the sum of nparts slices of a split projection, in slice order */
 __global__ __launch_bounds__(kThreads) void gr_rank(float *__restrict__ v, uint32_t n, uint32_t B,
-                                                    uint32_t *status) {
+                                                    const float *__restrict__ parts,
+                                                    uint32_t nparts, uint32_t *status) {
     bool bad = false;
     for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
-        const float a = v[i] / (float)B;
+        float raw;
+        if (parts != nullptr) {
+            raw = parts[i];
+            for (uint32_t k = 1; k < nparts; ++k) raw = raw + parts[(size_t)k * n + i];
+        } else {
+            raw = v[i];
+        }
+        const float a = raw / (float)B;
         const float s = kq_sigmoid(a);
         const float r = a * s;
         bad |= !kq_isfinite(r);
@@ -283,9 +292,10 @@ extern "C" hipError_t kq_launch_gr_norm(const float *x, const float *norm, uint3
 }
 
 extern "C" hipError_t kq_launch_gr_rank(float *rank, uint32_t n, uint32_t branches,
-                                        uint32_t *status, hipStream_t s) {
+                                        const float *parts, uint32_t nparts, uint32_t *status,
+                                        hipStream_t s) {
     hipLaunchKernelGGL(gr_rank, dim3(grid_for(n)), dim3(kThreads), 0, s, rank, n, branches,
-                       status);
+                       parts, nparts, status);
     return hipGetLastError();
 }
 

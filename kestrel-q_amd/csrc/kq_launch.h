@@ -42,6 +42,12 @@ hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_
 /* y[t] = W x[t] for many tokens, Q8_0 W on MFMA (kq_grouped.hip): row
  * lengths 256, 320, 512, 640, 1024, 2048 or 10240 */
 int kq_launch_gemm_q8_0_supported(uint32_t rows, uint32_t cols);
+/* column slices of a Q8_0 product row (1: staged whole), and the product
+ * split over them: parts [slices][tokens][rows], summed by the caller */
+uint32_t kq_launch_gemm_q8_0_slices(uint32_t cols);
+hipError_t kq_launch_gemm_q8_0_split(const void *W, uint32_t rows, uint32_t cols, const float *x,
+                                     uint32_t tokens, float *parts, uint32_t *status,
+                                     hipStream_t s);
 hipError_t kq_launch_gemm_q8_0(const void *W, uint32_t rows, uint32_t cols, const float *x,
                                uint32_t tokens, float *y, uint32_t *status, hipStream_t stream);
 /* batched Q6_K matvec on MFMA (kq_grouped.hip), used by kq_launch_matvec
@@ -69,8 +75,8 @@ hipError_t kq_launch_noalloc_scratch_init(int device, void **out);
 hipError_t kq_launch_gr_norm(const float *x, const float *norm, uint32_t tokens,
                              uint32_t branches, uint32_t hidden, float eps, float *normalized,
                              uint32_t *status, hipStream_t stream);
-hipError_t kq_launch_gr_rank(float *rank, uint32_t n, uint32_t branches, uint32_t *status,
-                             hipStream_t stream);
+hipError_t kq_launch_gr_rank(float *rank, uint32_t n, uint32_t branches, const float *parts,
+                             uint32_t nparts, uint32_t *status, hipStream_t s);
 hipError_t kq_launch_gr_mix(const float *read_raw, const float *normalized, const float *inject,
                             uint32_t tokens, uint32_t branches, uint32_t hidden, float *mixed,
                             float *write_gate, uint32_t *status, hipStream_t stream);

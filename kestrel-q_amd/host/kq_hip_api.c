@@ -1480,6 +1480,7 @@ kq_status kq_hip_gr_read_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
                              uint64_t scratch_bytes, kq_diagnostic *diag) {
     uint64_t W, need;
     float *normalized, *rank, *read_raw;
+    uint32_t slices;
     hipError_t e;
     kq_status st;
     kq_diagnostic_clear(diag);
@@ -1516,11 +1517,22 @@ kq_status kq_hip_gr_read_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
     if (st != KQ_STATUS_OK) return st;
     e = kq_launch_gr_norm(x, w->norm, (uint32_t)tokens, d->branch_count, d->hidden_size,
                           d->rms_epsilon, normalized, c->d_status, c->stream);
-    if (e == hipSuccess)
+    /* a Q8_0 rank projection whose rows are staged in several slices runs
+     * split over them, into the read projection's region (free until the
+     * up projection), and the rank step sums the slices in order */
+    slices = 1u;
+    if (w->down_type == KQ_HIP_TYPE_Q8_0 && tokens >= KQ_GR_GEMM_MIN_TOKENS &&
+        kq_launch_gemm_q8_0_supported(d->rank, (uint32_t)W))
+        slices = kq_launch_gemm_q8_0_slices((uint32_t)W);
+    if (slices > 1u && (uint64_t)slices * d->rank > W) slices = 1u;
+    if (e == hipSuccess && slices > 1u)
+        e = kq_launch_gemm_q8_0_split(w->down, d->rank, (uint32_t)W, normalized, (uint32_t)tokens,
+                                      read_raw, c->d_status, c->stream);
+    else if (e == hipSuccess)
         e = gr_project(c, w->down_type, w->down, d->rank, W, normalized, (uint32_t)tokens, rank);
     if (e == hipSuccess)
-        e = kq_launch_gr_rank(rank, (uint32_t)(tokens * d->rank), d->branch_count, c->d_status,
-                              c->stream);
+        e = kq_launch_gr_rank(rank, (uint32_t)(tokens * d->rank), d->branch_count,
+                              slices > 1u ? read_raw : NULL, slices, c->d_status, c->stream);
     if (e == hipSuccess)
         e = gr_project(c, w->up_type, w->up, W, d->rank, rank, (uint32_t)tokens, read_raw);
     if (e == hipSuccess)
