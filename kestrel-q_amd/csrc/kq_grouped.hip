@@ -236,7 +236,7 @@ struct Stage {
  * groups l, l + 64, ..., so that both the global reads and the LDS writes
  * of a wave are contiguous (no bank conflicts). Returns true if a
  * non-finite input was seen. col0 and KSL are multiples of 32. */
-template <uint32_t FMT, uint32_t KDIM, uint32_t KSL, bool OWN = false>
+template <uint32_t FMT, uint32_t KDIM, uint32_t KSL>
 __device__ bool stage_slice(Stage<FMT, KSL> &st, const float *__restrict__ X, uint32_t col0,
                             const int *src_row, uint32_t wave, uint32_t nwaves, uint32_t lane) {
     using S = Stage<FMT, KSL>;
@@ -248,18 +248,14 @@ __device__ bool stage_slice(Stage<FMT, KSL> &st, const float *__restrict__ X, ui
         const float4 *p = (const float4 *)(X + (size_t)(src < 0 ? 0 : src) * KDIM) + lane;
         int sig;
         bool any_nf = false;
-        if (col0 == 0u || OWN) {
+        if (col0 == 0u) {
             /* the scale, from the whole row (later slices of this chunk reuse
-             * it, so every slice gets the same one), or with OWN from this
-             * slice alone (a split pass, whose slices are summed unscaled) */
+             * it, so every slice gets the same one) */
             float m = 0.0f;
             bool nf = false;
-            constexpr uint32_t QN = OWN ? NQS : NQ;
-            const uint32_t qb = OWN ? col0 / 256u : 0u;
 #pragma unroll 8
-            for (uint32_t q = qb; q < qb + QN; ++q) {
-                const uint32_t c4 = 256u * q + 4u * lane;
-                const bool in = src >= 0 && c4 < KDIM && (!OWN || (c4 >= col0 && c4 < col0 + KSL));
+            for (uint32_t q = 0; q < NQ; ++q) {
+                const bool in = src >= 0 && 256u * q + 4u * lane < KDIM;
                 const float4 v = in ? p[64u * q] : make_float4(0.f, 0.f, 0.f, 0.f);
                 nf |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
                       !kq_isfinite(v.w);
@@ -634,8 +630,7 @@ __device__ __forceinline__ Work work_of(uint32_t y, const uint32_t *offsets, uin
  * hardware drops -- so the memory counters the compiler waits on are the
  * same on every path and a wait never drains the prefetch.
  */
-template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW, int TPW, int PD, int KS,
-          bool SPLIT = false>
+template <uint32_t GFMT, uint32_t KDIM, int NMAT, int NW, int TPW, int PD, int KS>
 __global__ __launch_bounds__(NW * 64) void grouped_pass(
     const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
     const uint8_t *__restrict__ SW0, const uint8_t *__restrict__ SW1,
@@ -691,25 +686,18 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
         for (int m = 0; m < NMAT; ++m) r[m] = F::load(wb[m], off, g);
     };
     /* results go through a buffer over this workgroup's output rows */
-    const uint32_t kz = SPLIT ? blockIdx.z : 0u; /* slice of a split pass */
     const uint32_t pos0 = wk.shared ? tk + wk.first : wk.first;
     const uint32_t obytes = wk.count * rows * 4u;
-    const size_t zbase = SPLIT ? (size_t)kz * (tk + tokens) * rows : 0u;
-    const KqBuf ob = kq_buf(out + zbase + (size_t)pos0 * rows, obytes);
+    const KqBuf ob = kq_buf(out + (size_t)pos0 * rows, obytes);
 
     /* the wave's iterations are (slice, tile, unit of the slice) in order;
      * iteration `it` reads ring slot it % R, which iteration it - PD filled */
-    /* SPLIT (NMAT = 1, one tile per wave): workgroup z takes slice z alone,
-     * staged at its own scale, and stores its unscaled partial products in
-     * slice z of out ([KS][positions][rows]); the caller sums the slices */
-    static_assert(!SPLIT || (NMAT == 1 && TPW == 1), "split passes: down, one tile per wave");
     constexpr uint32_t PER = (uint32_t)TPW * NBS; /* iterations per slice */
-    constexpr uint32_t NIT = SPLIT ? PER : (uint32_t)KS * PER;
+    constexpr uint32_t NIT = (uint32_t)KS * PER;
     constexpr uint32_t R = (uint32_t)PD + 1u;
-    auto ks_of = [&](uint32_t it) { return SPLIT ? kz : it / PER; };
     auto it_off = [&](uint32_t it) {
         if (it >= NIT) return wbytes;
-        const uint32_t ks = ks_of(it), rem = it % PER;
+        const uint32_t ks = it / PER, rem = it % PER;
         return boff(rem / NBS, ks * NBS + rem % NBS);
     };
 
@@ -717,7 +705,7 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
     auto stage = [&](uint32_t ks) {
         /* a non-finite hidden state is the caller's input; a non-finite
          * intermediate activation is a numeric failure of the layer */
-        const bool nf = stage_slice<GFMT, KDIM, KSL, SPLIT>(st, X, ks * KSL, src_row, wave, NW, lane);
+        const bool nf = stage_slice<GFMT, KDIM, KSL>(st, X, ks * KSL, src_row, wave, NW, lane);
         if (NMAT == 2)
             badin |= nf;
         else
@@ -742,7 +730,7 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
             src_row[i] = src;
         }
         __syncthreads();
-        stage(kz);
+        stage(0u);
         __syncthreads();
 
         f4 acc[NMAT];
@@ -752,22 +740,22 @@ __global__ __launch_bounds__(NW * 64) void grouped_pass(
 #pragma unroll
             for (uint32_t r = 0; r < R; ++r) {
                 const uint32_t it = it0 + r;
-                const uint32_t ks = ks_of(it), rem = it % PER;
+                const uint32_t ks = it / PER, rem = it % PER;
                 const uint32_t t = rem / NBS, b = rem % NBS;
-                if (!SPLIT && KS > 1 && ks > 0u && rem == 0u) {
+                if (KS > 1 && ks > 0u && rem == 0u) {
                     /* the next slice of the activations */
                     __syncthreads();
                     stage(ks);
                     __syncthreads();
                 }
-                if (b == 0u && (SPLIT || ks == 0u)) {
+                if (b == 0u && ks == 0u) {
 #pragma unroll
                     for (int m = 0; m < NMAT; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
                 }
                 load(ring[(r + PD) % R], it_off(it + PD));
                 T::block(ring[r], st, b, j, g, acc, malformed);
                 __builtin_amdgcn_sched_barrier(0);
-                if (b + 1u < NBS || (!SPLIT && ks + 1u < (uint32_t)KS)) continue;
+                if (b + 1u < NBS || ks + 1u < (uint32_t)KS) continue;
                 /* D[token][row]: this lane holds row `row` of tokens 4g .. 4g+3 */
                 const uint32_t row = tile_row(t) + j;
 #pragma unroll
@@ -1665,10 +1653,23 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
         e = kq_launch_gu_lds(d->hidden, g, u, sg, su, ws->outp, ws->offsets, ws->perm_tok, E,
                              tokens, d->top_k, d->inter, lds_shared ? 1 : 0, 1, ws->gitems,
                              ws->act, status, s);
-        if (e == hipSuccess && !lds_shared)
+        if (e == hipSuccess && !lds_shared && w->shared_gate_type == KQ_LAUNCH_Q8_0 &&
+            kq_launch_dense_q8_supported(d->inter, d->hidden, tokens)) {
+            /* a Q8_0 shared expert sees every token: the dense product on
+             * the same per-token split (kq_stage.h: xh [T][H], xl [T][H],
+             * the 32-column sums [T][H/128][8] fp16, sig [T]), its rows
+             * after the routed pairs' */
+            const uint8_t *st = (const uint8_t *)ws->outp;
+            const size_t th = (size_t)tokens * d->hidden;
+            e = kq_launch_dense_q8(sg, su, d->inter, d->hidden, st, st + th * 2u,
+                                   (const int *)(st + th * 4u + (size_t)tokens * (d->hidden / 128u) * 16u),
+                                   tokens, 1u, ws->act + (size_t)tokens * d->top_k * d->inter,
+                                   status, s);
+        } else if (e == hipSuccess && !lds_shared) {
             e = pass_any<2>(w->shared_gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets,
                             ws->perm_tok, E, tokens, d->top_k, d->inter, E, sh_wgs, ws->act,
                             status, s);
+        }
     } else if (w->shared_gate_type == w->gate_type) {
         e = pass_any<2>(w->gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets, ws->perm_tok,
                         E, tokens, d->top_k, d->inter, 0u, E + sh_wgs, ws->act, status, s);
@@ -1722,54 +1723,6 @@ extern "C" hipError_t kq_launch_gemm_q8_0(const void *W, uint32_t rows, uint32_t
     return pass_cols<KQ_LAUNCH_Q8_0, 1>(cols, nullptr, nullptr, (const uint8_t *)W, nullptr, x,
                                         nullptr, nullptr, 0u, tokens, 0u, rows, 0u, ny, 1u, y,
                                         status, s);
-}
-
-/* The same product split over the column slices the activations are
- * staged in (a row too long for one LDS image): slice z of `parts`
- * ([slices][tokens][rows]) receives the products over slice z's columns,
- * each slice staged at its own scale, and the caller sums the slices in
- * order. KS workgroups per (row slab, chunk) instead of one: the long row
- * no longer runs as one serial chain of loads per wave. */
-template <uint32_t KDIM>
-hipError_t launch_gemm_split(const uint8_t *W, uint32_t rows, const float *x, uint32_t tokens,
-                             float *parts, uint32_t *status, hipStream_t s) {
-    using Sh = Shape<KQ_LAUNCH_Q8_0, KDIM, 1>;
-    constexpr int KS = Sh::KS;
-    if constexpr (KS < 2) {
-        return hipErrorInvalidValue;
-    } else {
-        constexpr int NWS = 4;
-        constexpr int NBS = (int)(KDIM / (uint32_t)KS / Fmt<KQ_LAUNCH_Q8_0>::kUnit);
-        constexpr int R1 = (Sh::PD + 1) >= 8 && NBS % 8 == 0   ? 8
-                           : (Sh::PD + 1) >= 4 && NBS % 4 == 0 ? 4
-                           : (Sh::PD + 1) >= 2 && NBS % 2 == 0 ? 2
-                                                               : 1;
-        const dim3 grid((rows + NWS * kTile - 1u) / (NWS * kTile), (tokens + kTile - 1u) / kTile,
-                        (uint32_t)KS);
-        hipLaunchKernelGGL((grouped_pass<KQ_LAUNCH_Q8_0, KDIM, 1, NWS, 1, R1 - 1, KS, true>), grid,
-                           dim3(NWS * 64), 0, s, nullptr, nullptr, W, nullptr, x, nullptr, nullptr,
-                           0u, tokens, 0u, rows, 1u, 0u, parts, status);
-        return hipGetLastError();
-    }
-}
-
-extern "C" uint32_t kq_launch_gemm_q8_0_slices(uint32_t cols) {
-    switch (cols) {
-    case 2560: return (uint32_t)Shape<KQ_LAUNCH_Q8_0, 2560u, 1>::KS;
-    case 10240: return (uint32_t)Shape<KQ_LAUNCH_Q8_0, 10240u, 1>::KS;
-    default: return 1u;
-    }
-}
-
-extern "C" hipError_t kq_launch_gemm_q8_0_split(const void *W, uint32_t rows, uint32_t cols,
-                                                const float *x, uint32_t tokens, float *parts,
-                                                uint32_t *status, hipStream_t s) {
-    if (!kq_launch_gemm_q8_0_supported(rows, cols) || tokens == 0u) return hipErrorInvalidValue;
-    switch (cols) {
-    case 2560: return launch_gemm_split<2560u>((const uint8_t *)W, rows, x, tokens, parts, status, s);
-    case 10240: return launch_gemm_split<10240u>((const uint8_t *)W, rows, x, tokens, parts, status, s);
-    default: return hipErrorInvalidValue;
-    }
 }
 
 /* batched Q6_K matvec on MFMA: rows of 256 .. 4096 columns (whole blocks),

@@ -42,12 +42,18 @@ hipError_t kq_launch_matvec(uint32_t type, const void *W, uint32_t rows, uint32_
 /* y[t] = W x[t] for many tokens, Q8_0 W on MFMA (kq_grouped.hip): row
  * lengths 256, 320, 512, 640, 1024, 2048 or 10240 */
 int kq_launch_gemm_q8_0_supported(uint32_t rows, uint32_t cols);
-/* column slices of a Q8_0 product row (1: staged whole), and the product
- * split over them: parts [slices][tokens][rows], summed by the caller */
-uint32_t kq_launch_gemm_q8_0_slices(uint32_t cols);
-hipError_t kq_launch_gemm_q8_0_split(const void *W, uint32_t rows, uint32_t cols, const float *x,
-                                     uint32_t tokens, float *parts, uint32_t *status,
-                                     hipStream_t s);
+/* one Q8_0 matrix (w1: also the up matrix of a gate/up pair, SwiGLU'd)
+ * against many split activation rows on MFMA (kq_dense.hip): out
+ * [splits][tokens][rows], the splits summed by the caller;
+ * kq_launch_dense_split forms xh, xl [tokens][k] and sig [tokens] (a
+ * non-finite row flags the input (input != 0) or a numeric failure) */
+int kq_launch_dense_q8_supported(uint32_t rows, uint32_t k, uint32_t tokens);
+uint32_t kq_launch_dense_q8_splits(uint32_t k, uint32_t splits);
+hipError_t kq_launch_dense_split(const float *x, uint32_t tokens, uint32_t k, void *xh, void *xl,
+                                 int *sig, int input, uint32_t *status, hipStream_t s);
+hipError_t kq_launch_dense_q8(const void *w0, const void *w1, uint32_t rows, uint32_t k,
+                              const void *xh, const void *xl, const int *sig, uint32_t tokens,
+                              uint32_t splits, float *out, uint32_t *status, hipStream_t s);
 hipError_t kq_launch_gemm_q8_0(const void *W, uint32_t rows, uint32_t cols, const float *x,
                                uint32_t tokens, float *y, uint32_t *status, hipStream_t stream);
 /* batched Q6_K matvec on MFMA (kq_grouped.hip), used by kq_launch_matvec

@@ -1414,11 +1414,18 @@ kq_status kq_hip_moe_token_permutation(kq_hip_context *c, const kq_hip_moe_confi
 /* gated residual around a layer block */
 
 /* scratch of a gr read: normalized [T][W], rank [T][r], read gates [T][W] */
+/* column splits of the dense rank projection (kq_launch_dense_q8) */
+#define KQ_GR_SPLITS 8u
+
+/* normalized [T][W], rank [T][r], read_raw [T][W], then the dense
+ * projections' room: the rank projection's split partials [S][T][r] (later
+ * the split rank rows, hi + lo), and two rows of T scales */
 uint64_t kq_hip_gr_scratch_bytes(const kq_hip_gr_dimensions *d, uint64_t tokens) {
     uint64_t w;
     if (d == NULL) return 0u;
     w = (uint64_t)d->branch_count * d->hidden_size;
-    return 2u * align256(tokens * w * 4u) + align256(tokens * d->rank * 4u);
+    return 2u * align256(tokens * w * 4u) + align256(tokens * d->rank * 4u) +
+           align256(KQ_GR_SPLITS * tokens * d->rank * 4u) + 2u * align256(tokens * 4u);
 }
 
 static kq_status gr_dims_ok(const kq_hip_gr_dimensions *d, uint64_t tokens,
@@ -1479,7 +1486,9 @@ kq_status kq_hip_gr_read_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
                              float *mixed, float *write_gate, void *scratch,
                              uint64_t scratch_bytes, kq_diagnostic *diag) {
     uint64_t W, need;
-    float *normalized, *rank, *read_raw;
+    float *normalized, *rank, *read_raw, *parts;
+    int *sig_dn, *sig_up;
+    int dense_dn, dense_up;
     uint32_t slices;
     hipError_t e;
     kq_status st;
@@ -1513,28 +1522,49 @@ kq_status kq_hip_gr_read_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
     normalized = (float *)scratch;
     rank = (float *)((char *)scratch + align256(tokens * W * 4u));
     read_raw = (float *)((char *)rank + align256(tokens * d->rank * 4u));
+    parts = (float *)((char *)read_raw + align256(tokens * W * 4u));
+    sig_dn = (int *)((char *)parts + align256(KQ_GR_SPLITS * tokens * d->rank * 4u));
+    sig_up = (int *)((char *)sig_dn + align256(tokens * 4u));
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
     e = kq_launch_gr_norm(x, w->norm, (uint32_t)tokens, d->branch_count, d->hidden_size,
                           d->rms_epsilon, normalized, c->d_status, c->stream);
-    /* a Q8_0 rank projection whose rows are staged in several slices runs
-     * split over them, into the read projection's region (free until the
-     * up projection), and the rank step sums the slices in order */
-    slices = 1u;
-    if (w->down_type == KQ_HIP_TYPE_Q8_0 && tokens >= KQ_GR_GEMM_MIN_TOKENS &&
-        kq_launch_gemm_q8_0_supported(d->rank, (uint32_t)W))
-        slices = kq_launch_gemm_q8_0_slices((uint32_t)W);
-    if (slices > 1u && (uint64_t)slices * d->rank > W) slices = 1u;
-    if (e == hipSuccess && slices > 1u)
-        e = kq_launch_gemm_q8_0_split(w->down, d->rank, (uint32_t)W, normalized, (uint32_t)tokens,
-                                      read_raw, c->d_status, c->stream);
-    else if (e == hipSuccess)
+    /* Many tokens and Q8_0 projections: the dense MFMA products
+     * (kq_launch_dense_q8) on rows split once into fp16 hi + lo. The rank
+     * projection's split sits in the read projection's region (free until
+     * the up projection writes it), its column splits' partials in `parts`,
+     * summed in order by the rank step; the rank rows' split then reuses
+     * `parts`. */
+    dense_dn = w->down_type == KQ_HIP_TYPE_Q8_0 && tokens >= KQ_GR_GEMM_MIN_TOKENS &&
+               kq_launch_dense_q8_supported(d->rank, (uint32_t)W, (uint32_t)tokens);
+    dense_up = w->up_type == KQ_HIP_TYPE_Q8_0 && tokens >= KQ_GR_GEMM_MIN_TOKENS &&
+               kq_launch_dense_q8_supported((uint32_t)W, d->rank, (uint32_t)tokens);
+    slices = dense_dn ? kq_launch_dense_q8_splits((uint32_t)W, KQ_GR_SPLITS) : 1u;
+    if (e == hipSuccess && dense_dn) {
+        e = kq_launch_dense_split(normalized, (uint32_t)tokens, (uint32_t)W, read_raw,
+                                  (char *)read_raw + tokens * W * 2u, sig_dn, 0, c->d_status,
+                                  c->stream);
+        if (e == hipSuccess)
+            e = kq_launch_dense_q8(w->down, NULL, d->rank, (uint32_t)W, read_raw,
+                                   (char *)read_raw + tokens * W * 2u, sig_dn, (uint32_t)tokens,
+                                   KQ_GR_SPLITS, parts, c->d_status, c->stream);
+    } else if (e == hipSuccess) {
         e = gr_project(c, w->down_type, w->down, d->rank, W, normalized, (uint32_t)tokens, rank);
+    }
     if (e == hipSuccess)
         e = kq_launch_gr_rank(rank, (uint32_t)(tokens * d->rank), d->branch_count,
-                              slices > 1u ? read_raw : NULL, slices, c->d_status, c->stream);
-    if (e == hipSuccess)
+                              dense_dn ? parts : NULL, slices, c->d_status, c->stream);
+    if (e == hipSuccess && dense_up) {
+        e = kq_launch_dense_split(rank, (uint32_t)tokens, d->rank, parts,
+                                  (char *)parts + tokens * d->rank * 2u, sig_up, 0, c->d_status,
+                                  c->stream);
+        if (e == hipSuccess)
+            e = kq_launch_dense_q8(w->up, NULL, (uint32_t)W, d->rank, parts,
+                                   (char *)parts + tokens * d->rank * 2u, sig_up,
+                                   (uint32_t)tokens, 1u, read_raw, c->d_status, c->stream);
+    } else if (e == hipSuccess) {
         e = gr_project(c, w->up_type, w->up, W, d->rank, rank, (uint32_t)tokens, read_raw);
+    }
     if (e == hipSuccess)
         e = kq_launch_gr_mix(read_raw, normalized, w->inject, (uint32_t)tokens, d->branch_count,
                              d->hidden_size, mixed, write_gate, c->d_status, c->stream);
