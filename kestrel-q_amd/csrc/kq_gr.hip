@@ -27,7 +27,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kNormThreads = 1024; /* a branch's H values in one or few loads per thread */
+constexpr int kNormThreads = 256; /* a branch of H values, float4 per thread where H % 4 == 0 */
 
 /* sum over the workgroup (NT threads), returned to every thread */
 template <int NT>
@@ -55,24 +55,49 @@ __global__ __launch_bounds__(kNormThreads) void gr_norm(const float *__restrict_
     const float *w = norm + (size_t)b * H;
     bool badin = false, bad = false;
     float s = 0.0f;
-#pragma unroll 4
-    for (uint32_t i = threadIdx.x; i < H; i += kNormThreads) {
-        const float v = x[base + i];
-        badin |= !kq_isfinite(v) || !kq_isfinite(w[i]);
-        const float sq = v * v;
-        s += sq;
+    /* (the state is 16-byte aligned; the norm weights may be only 4) */
+    const bool v4 = H % 4u == 0u && ((uintptr_t)w & 15u) == 0u;
+    if (v4) {
+        const float4 *x4 = (const float4 *)(x + base), *w4 = (const float4 *)w;
+        for (uint32_t i = threadIdx.x; i < H / 4u; i += kNormThreads) {
+            const float4 v = x4[i], wv = w4[i];
+            badin |= !kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                     !kq_isfinite(v.w) || !kq_isfinite(wv.x) || !kq_isfinite(wv.y) ||
+                     !kq_isfinite(wv.z) || !kq_isfinite(wv.w);
+            float sq;
+            sq = v.x * v.x; s += sq;
+            sq = v.y * v.y; s += sq;
+            sq = v.z * v.z; s += sq;
+            sq = v.w * v.w; s += sq;
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < H; i += kNormThreads) {
+            const float v = x[base + i];
+            badin |= !kq_isfinite(v) || !kq_isfinite(w[i]);
+            const float sq = v * v;
+            s += sq;
+        }
     }
     s = block_sum<kNormThreads>(s, red);
     const float mean = s / (float)H;
     const float inv = 1.0f / sqrtf(mean + eps);
     bad |= !kq_isfinite(inv);
-#pragma unroll 4
-    for (uint32_t i = threadIdx.x; i < H; i += kNormThreads) {
-        const float nv = x[base + i] * inv;
-        const float wt = 1.0f + w[i];
+    auto one = [&](float xv, float wv) {
+        const float nv = xv * inv;
+        const float wt = 1.0f + wv;
         const float r = nv * wt;
         bad |= !kq_isfinite(r);
-        out[base + i] = r;
+        return r;
+    };
+    if (v4) {
+        const float4 *x4 = (const float4 *)(x + base), *w4 = (const float4 *)w;
+        float4 *o4 = (float4 *)(out + base);
+        for (uint32_t i = threadIdx.x; i < H / 4u; i += kNormThreads) {
+            const float4 v = x4[i], wv = w4[i];
+            o4[i] = make_float4(one(v.x, wv.x), one(v.y, wv.y), one(v.z, wv.z), one(v.w, wv.w));
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < H; i += kNormThreads) out[base + i] = one(x[base + i], w[i]);
     }
     if (badin) kq_flag(status, KQ_DEV_INPUT);
     if (bad) kq_flag(status, KQ_DEV_NUMERIC);

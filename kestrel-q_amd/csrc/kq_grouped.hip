@@ -1695,10 +1695,25 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     } else {
         e = pass_any<1>(w->down_type, d->inter, dn, nullptr, sd, nullptr, ws->act, ws->offsets,
                         ws->perm_tok, E, tokens, d->top_k, d->hidden, 0u, E, ws->outp, status, s);
-        if (e == hipSuccess)
+        const size_t tk = (size_t)tokens * d->top_k;
+        if (e == hipSuccess && w->shared_down_type == KQ_LAUNCH_Q8_0 &&
+            kq_launch_dense_q8_supported(d->hidden, d->inter, tokens)) {
+            /* a Q8_0 shared expert's down on the dense product: its T
+             * activation rows (after the routed pairs') split into dstage,
+             * which only the LDS down pass uses */
+            uint8_t *xs = (uint8_t *)ws->dstage;
+            const size_t ti = (size_t)tokens * d->inter;
+            e = kq_launch_dense_split(ws->act + tk * d->inter, tokens, d->inter, xs, xs + ti * 2u,
+                                      (int *)(xs + ti * 4u), 0, status, s);
+            if (e == hipSuccess)
+                e = kq_launch_dense_q8(sd, nullptr, d->hidden, d->inter, xs, xs + ti * 2u,
+                                       (const int *)(xs + ti * 4u), tokens, 1u,
+                                       ws->outp + tk * d->hidden, status, s);
+        } else if (e == hipSuccess) {
             e = pass_any<1>(w->shared_down_type, d->inter, dn, nullptr, sd, nullptr, ws->act,
                             ws->offsets, ws->perm_tok, E, tokens, d->top_k, d->hidden, E, sh_wgs,
                             ws->outp, status, s);
+        }
     }
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(moe_combine, dim3((d->hidden / 4u + 255u) / 256u, tokens), dim3(256), 0, s,
