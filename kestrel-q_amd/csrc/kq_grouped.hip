@@ -1688,6 +1688,29 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
         /* over the gate/up pass's item list (routed and shared chunks) */
         e = kq_launch_dn_lds(d->inter, d->hidden, dn, sd, ws->act, tokens, d->top_k, ws->gitems,
                              ws->dstage, ws->outp, status, s);
+    } else if (lds_routed && w->down_type == KQ_LAUNCH_Q5_1 &&
+               (!lds_shared || w->shared_down_type == KQ_LAUNCH_Q5_1) &&
+               kq_launch_dn51_supported(d->inter)) {
+        /* Q5_1 rows through the same per-wave LDS-DMA pipeline, over the
+         * item list (the shared expert's chunks are in it when its gate/up
+         * ran in the Q4_K pass; otherwise it runs below) */
+        e = kq_launch_dn51(d->inter, d->hidden, dn, sd, ws->act, tokens, d->top_k, ws->gitems,
+                           ws->dstage, ws->outp, status, s);
+        const size_t tk = (size_t)tokens * d->top_k;
+        if (e == hipSuccess && !lds_shared && w->shared_down_type == KQ_LAUNCH_Q8_0 &&
+            kq_launch_dense_q8_supported(d->hidden, d->inter, tokens)) {
+            /* the dstage split above holds every position in natural order,
+             * the shared expert's rows last */
+            uint8_t *xs = (uint8_t *)ws->dstage;
+            const size_t npos = tk + tokens, xb = npos * d->inter * 2u;
+            e = kq_launch_dense_q8(sd, nullptr, d->hidden, d->inter, xs + tk * d->inter * 2u,
+                                   xs + xb + tk * d->inter * 2u, (const int *)(xs + 2u * xb) + tk,
+                                   tokens, 1u, ws->outp + tk * d->hidden, status, s);
+        } else if (e == hipSuccess && !lds_shared) {
+            e = pass_any<1>(w->shared_down_type, d->inter, dn, nullptr, sd, nullptr, ws->act,
+                            ws->offsets, ws->perm_tok, E, tokens, d->top_k, d->hidden, E, sh_wgs,
+                            ws->outp, status, s);
+        }
     } else if (w->shared_down_type == w->down_type) {
         e = pass_any<1>(w->down_type, d->inter, dn, nullptr, sd, nullptr, ws->act, ws->offsets,
                         ws->perm_tok, E, tokens, d->top_k, d->hidden, 0u, E + sh_wgs, ws->outp,

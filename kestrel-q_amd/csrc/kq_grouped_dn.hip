@@ -34,6 +34,7 @@
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4v __attribute__((ext_vector_type(4)));
@@ -360,6 +361,173 @@ void dn_q6k(DnArgs a) {
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
+/* ------------------------------------------------------------------ */
+/* the same pipeline for Q5_1 rows (the reference model's routed down):
+ * 24 B per 32 columns (f16 d, f16 m, 32 high bits, 16 bytes of nibbles;
+ * src/kq_numeric.c:197-222), every block 4-byte aligned. The activations
+ * are split in natural column order (dense_split), so lane (j, g) reads
+ * columns 32b + 8g .. + 7 of block b as one 16-byte run. Per block and
+ * tile: the 5-bit codes enter fp16 exactly, one 16x16x32 step each for hi
+ * and lo scaled by d; the min term m * sum(x) is two more steps against m
+ * repeated over the block's columns, added unscaled. */
+template <uint32_t KD>
+struct Dn51Shape {
+    static constexpr uint32_t NBK = KD / 32u;                /* blocks per row */
+    static constexpr uint32_t RB = 24u * NBK;                /* row bytes */
+    static constexpr uint32_t TB = kT * RB;                  /* tile bytes */
+    static constexpr uint32_t IPT = (TB + 1023u) / 1024u;    /* loads per tile */
+    static constexpr uint32_t SLOT = IPT * 1024u;
+    static constexpr uint32_t W = 4u;
+    static constexpr uint32_t RING0 = 160u * 1024u / (W * SLOT);
+    static constexpr uint32_t RING = RING0 > 8u ? 8u : RING0;
+    static constexpr uint32_t PD = RING - 1u;
+    static_assert(RING >= 2u, "LDS");
+    static_assert(W * RING * SLOT <= 160u * 1024u, "LDS");
+};
+
+__device__ __forceinline__ uint32_t spread4(uint32_t x) {
+    return ((x * 0x00204081u) & 0x01010101u) << 4;
+}
+
+template <uint32_t KD>
+__global__ __launch_bounds__(Dn51Shape<KD>::W * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void dn_q51(DnArgs a) {
+    using S = Dn51Shape<KD>;
+    constexpr uint32_t NBK = S::NBK;
+    __shared__ __align__(16) uint8_t slots[S::W][S::RING][S::SLOT];
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t gw = blockIdx.x * S::W + w, nw = gridDim.x * S::W;
+    const uint32_t nt = (a.hidden + kT - 1u) / kT; /* tiles per item */
+    const uint64_t total = (uint64_t)(*a.n_items) * nt;
+    const uint32_t lo = (uint32_t)(total * gw / nw), hi = (uint32_t)(total * (gw + 1u) / nw);
+    if (lo >= hi) return;
+
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t wbytes = a.hidden * S::RB;
+    const uint32_t base_lds = lds_addr(&slots[w][0][0]);
+    const uint8_t *myslots = &slots[w][0][0];
+
+    uint32_t iss_it = lo / nt, iss_tile = lo - (lo / nt) * nt, iss_slot = 0u;
+    bool iss_new = true;
+    i4v rw = {0, 0, 0, 0};
+    auto issue = [&]() {
+        if (iss_new) {
+            iss_new = false;
+            const uint32_t ex = sload(a.items + 2u * iss_it);
+            rw = dma_rsrc((ex & kShared) ? a.sdown : a.down + (size_t)ex * wbytes, wbytes);
+        }
+        const uint32_t toff = iss_tile * S::TB;
+#pragma unroll
+        for (uint32_t q = 0; q < S::IPT; ++q) {
+            const uint32_t c = 64u * q + lane;
+            dma16(rw, toff + (16u * c < S::TB ? 16u * c : 0u),
+                  base_lds + iss_slot * S::SLOT + q * 1024u);
+        }
+        iss_slot = iss_slot + 1u == S::RING ? 0u : iss_slot + 1u;
+        if (++iss_tile == nt) {
+            iss_tile = 0u;
+            ++iss_it;
+            iss_new = true;
+        }
+    };
+
+    /* dense_split layout: xh [npos][KD], xl [npos][KD], sig [npos] */
+    const uint8_t *st = (const uint8_t *)a.staged;
+    const uint32_t xbytes = a.npos * KD * 2u;
+    const KqBuf bxh = kq_buf(st, xbytes), bxl = kq_buf(st + xbytes, xbytes);
+    const KqBuf bsg = kq_buf(st + 2u * (size_t)xbytes, a.npos * 4u);
+    const uint32_t tk = a.tokens * a.top_k;
+    bool bad = false, malformed = false;
+
+#pragma unroll
+    for (uint32_t t = 0; t < S::PD; ++t)
+        if (lo + t < hi) issue();
+
+    uint4 axh[NBK], axl[NBK];
+    int sg[4];
+    uint32_t cur = 0u, pos0 = 0u, count = 0u;
+    auto enter = [&](uint32_t it) {
+        cur = it;
+        const uint32_t ex = sload(a.items + 2u * it), fc = sload(a.items + 2u * it + 1u);
+        const uint32_t first = fc & 0xffffffu;
+        count = fc >> 24;
+        pos0 = (ex & kShared) ? tk + first : first;
+        /* rows past the chunk read at 2^31, past the buffer */
+        const uint32_t xo = j < count ? ((pos0 + j) * KD + 8u * g) * 2u : 0x80000000u;
+#pragma unroll
+        for (uint32_t b = 0; b < NBK; ++b) {
+            axh[b] = kq_ld128(bxh, xo + 64u * b, 0u);
+            axl[b] = kq_ld128(bxl, xo + 64u * b, 0u);
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
+        }
+        wait_vm_all();
+    };
+    uint32_t ctile = lo - (lo / nt) * nt, cslot = 0u;
+    enter(lo / nt);
+
+    const h2 bias = h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const uint32_t shn = g >= 2u ? 4u : 0u;
+    for (uint32_t tau = lo; tau < hi; ++tau) {
+        if (ctile == nt) {
+            ctile = 0u;
+            enter(cur + 1u);
+        }
+        if (tau + S::PD < hi) issue();
+        const uint32_t after = hi - 1u - tau < S::PD ? hi - 1u - tau : S::PD;
+        wait_after<S::IPT, S::PD>(after);
+        const uint32_t *row = (const uint32_t *)(myslots + cslot * S::SLOT + j * S::RB);
+        cslot = cslot + 1u == S::RING ? 0u : cslot + 1u;
+        const uint32_t row0 = ctile * kT;
+        ++ctile;
+
+        f4 acc = {0.f, 0.f, 0.f, 0.f}, macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t b = 0; b < NBK; ++b) {
+            const uint32_t *blk = row + 6u * b;
+            const uint32_t dm = blk[0];
+            const uint32_t hb = (blk[1] >> (8u * g)) & 0xffu;
+            const uint2 qv = *(const uint2 *)(blk + 2u + 2u * (g & 1u));
+            const uint32_t c0 = ((qv.x >> shn) & 0x0f0f0f0fu) | spread4(hb & 15u);
+            const uint32_t c1 = ((qv.y >> shn) & 0x0f0f0f0fu) | spread4(hb >> 4);
+            const h2 w0 = byte_pair_lo(c0) + bias, w1 = byte_pair_hi(c0) + bias;
+            const h2 w2 = byte_pair_lo(c1) + bias, w3 = byte_pair_hi(c1) + bias;
+            const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+            const h8 ah = __builtin_bit_cast(h8, axh[b]), al = __builtin_bit_cast(h8, axl[b]);
+            f4 t = {0.f, 0.f, 0.f, 0.f};
+            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, t, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, t, 0, 0, 0);
+            const float d = half_bits(dm), mn = half_bits(dm >> 16);
+            malformed |= !kq_isfinite(d) || !kq_isfinite(mn);
+            /* the block's min, exact in fp16, on every column */
+            const h2 m2 = __builtin_bit_cast(h2, (dm >> 16) | (dm & 0xffff0000u));
+            const h8 mw = h8{m2.x, m2.y, m2.x, m2.y, m2.x, m2.y, m2.x, m2.y};
+            macc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, mw, macc, 0, 0, 0);
+            macc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, mw, macc, 0, 0, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = fmaf(d, t[k], acc[k]);
+        }
+        /* D[token][row]: this lane holds row row0 + j of tokens 4g .. 4g+3 */
+        const uint32_t r = row0 + j;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            const bool valid = i < count && r < a.hidden;
+            const float v = ldexpf(acc[q] + macc[q], -sg[q]);
+            bad |= valid && !kq_isfinite(v);
+            if (valid) a.out[(size_t)(pos0 + i) * a.hidden + r] = v;
+        }
+    }
+    wait_vm<0>();
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+}
+
 template <uint32_t KB>
 hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
     static int cus = 0;
@@ -378,6 +546,48 @@ hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
 }  // namespace
 
 extern "C" int kq_launch_dn_lds_supported(uint32_t inter) { return inter == 256u || inter == 512u; }
+
+extern "C" int kq_launch_dn51_supported(uint32_t inter) { return inter == 640u || inter == 512u; }
+
+/* Q5_1 down over the item list the permutation built: the activation rows
+ * split in natural order (dense_split) into staged, then dn_q51 */
+extern "C" hipError_t kq_launch_dn51(uint32_t inter, uint32_t hidden, const void *down,
+                                     const void *shared_down, const float *act, uint32_t tokens,
+                                     uint32_t top_k, const void *items, void *staged, float *out,
+                                     uint32_t *status, hipStream_t s) {
+    if (!kq_launch_dn51_supported(inter)) return hipErrorInvalidValue;
+    const uint32_t npos = tokens * top_k + tokens;
+    uint8_t *st = (uint8_t *)staged;
+    const size_t xb = (size_t)npos * inter * 2u;
+    hipError_t e = kq_launch_dense_split(act, npos, inter, st, st + xb, (int *)(st + 2u * xb), 0,
+                                         status, s);
+    if (e != hipSuccess) return e;
+    DnArgs a;
+    a.down = (const uint8_t *)down;
+    a.sdown = (const uint8_t *)shared_down;
+    a.staged = staged;
+    a.n_items = (const uint32_t *)items;
+    a.items = (const uint32_t *)items + 4;
+    a.tokens = tokens;
+    a.top_k = top_k;
+    a.hidden = hidden;
+    a.npos = npos;
+    a.out = out;
+    a.status = status;
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus < 1)
+            cus = 256;
+    }
+    if (inter == 640u)
+        hipLaunchKernelGGL((dn_q51<640u>), dim3((uint32_t)cus), dim3(Dn51Shape<640u>::W * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((dn_q51<512u>), dim3((uint32_t)cus), dim3(Dn51Shape<512u>::W * 64), 0, s, a);
+    return hipGetLastError();
+}
 
 extern "C" uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter) {
     return (uint64_t)npos * inter * 4u + (uint64_t)npos * 4u;
