@@ -368,8 +368,9 @@ void dn_q6k(DnArgs a) {
  * are split in natural column order (dense_split), so lane (j, g) reads
  * columns 32b + 8g .. + 7 of block b as one 16-byte run. Per block and
  * tile: the 5-bit codes enter fp16 exactly, one 16x16x32 step each for hi
- * and lo scaled by d; the min term m * sum(x) is two more steps against m
- * repeated over the block's columns, added unscaled. */
+ * and lo scaled by d; the min term m * sum(x) is one small step per 16
+ * blocks of the mins against the token's block sums (formed once per
+ * item from the activation registers), added unscaled. */
 template <uint32_t KD>
 struct Dn51Shape {
     static constexpr uint32_t NBK = KD / 32u;                /* blocks per row */
@@ -446,6 +447,8 @@ void dn_q51(DnArgs a) {
         if (lo + t < hi) issue();
 
     uint4 axh[NBK], axl[NBK];
+    constexpr uint32_t NMS = (NBK + 15u) / 16u; /* 16-block steps of the min term */
+    h4 sxh[NMS], sxl[NMS];
     int sg[4];
     uint32_t cur = 0u, pos0 = 0u, count = 0u;
     auto enter = [&](uint32_t it) {
@@ -467,6 +470,38 @@ void dn_q51(DnArgs a) {
             sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
         }
         wait_vm_all();
+        /* the min term's operand: each block's column sum of token row j
+         * (the four lanes of row j hold 8 columns each), times 2^-5 so
+         * it fits fp16, split hi + lo; lane (j, g) keeps blocks 4g .. 4g+3
+         * and 16 + 4g .. (the blocks past NBK are zero) */
+        float bs[NMS * 16u];
+#pragma unroll
+        for (uint32_t b = 0; b < NMS * 16u; ++b) bs[b] = 0.0f;
+#pragma unroll
+        for (uint32_t b = 0; b < NBK; ++b) {
+            const h8 hh = __builtin_bit_cast(h8, axh[b]), ll = __builtin_bit_cast(h8, axl[b]);
+            float p = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) p += (float)hh[e] + (float)ll[e];
+            p += __shfl_xor(p, 16, 64);
+            p += __shfl_xor(p, 32, 64);
+            bs[b] = p * 0.03125f;
+        }
+#pragma unroll
+        for (uint32_t st4 = 0; st4 < NMS; ++st4) {
+            _Float16 hv[4], lv[4];
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                float v = 0.0f;
+#pragma unroll
+                for (uint32_t gg = 0; gg < 4u; ++gg)
+                    if (gg == g) v = bs[16u * st4 + 4u * gg + e];
+                hv[e] = (_Float16)v;
+                lv[e] = (_Float16)(v - (float)hv[e]);
+            }
+            sxh[st4] = h4{hv[0], hv[1], hv[2], hv[3]};
+            sxl[st4] = h4{lv[0], lv[1], lv[2], lv[3]};
+        }
     };
     uint32_t ctile = lo - (lo / nt) * nt, cslot = 0u;
     enter(lo / nt);
@@ -504,13 +539,23 @@ void dn_q51(DnArgs a) {
             t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, t, 0, 0, 0);
             const float d = half_bits(dm), mn = half_bits(dm >> 16);
             malformed |= !kq_isfinite(d) || !kq_isfinite(mn);
-            /* the block's min, exact in fp16, on every column */
-            const h2 m2 = __builtin_bit_cast(h2, (dm >> 16) | (dm & 0xffff0000u));
-            const h8 mw = h8{m2.x, m2.y, m2.x, m2.y, m2.x, m2.y, m2.x, m2.y};
-            macc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, mw, macc, 0, 0, 0);
-            macc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, mw, macc, 0, 0, 0);
 #pragma unroll
             for (int k = 0; k < 4; ++k) acc[k] = fmaf(d, t[k], acc[k]);
+        }
+        /* the min term: sum over blocks of m times the token's block sum,
+         * as 16x16x16 steps over 16 blocks each (m exact in fp16) */
+#pragma unroll
+        for (uint32_t st4 = 0; st4 < NMS; ++st4) {
+            _Float16 mv[4];
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                const uint32_t b = 16u * st4 + 4u * g + e;
+                mv[e] = b < NBK ? __builtin_bit_cast(_Float16, (uint16_t)(row[6u * b] >> 16))
+                                : (_Float16)0.0f;
+            }
+            const h4 mb = h4{mv[0], mv[1], mv[2], mv[3]};
+            macc = __builtin_amdgcn_mfma_f32_16x16x16f16(sxh[st4], mb, macc, 0, 0, 0);
+            macc = __builtin_amdgcn_mfma_f32_16x16x16f16(sxl[st4], mb, macc, 0, 0, 0);
         }
         /* D[token][row]: this lane holds row row0 + j of tokens 4g .. 4g+3 */
         const uint32_t r = row0 + j;
@@ -518,7 +563,7 @@ void dn_q51(DnArgs a) {
         for (uint32_t q = 0; q < 4u; ++q) {
             const uint32_t i = 4u * g + q;
             const bool valid = i < count && r < a.hidden;
-            const float v = ldexpf(acc[q] + macc[q], -sg[q]);
+            const float v = ldexpf(fmaf(32.0f, macc[q], acc[q]), -sg[q]);
             bad |= valid && !kq_isfinite(v);
             if (valid) a.out[(size_t)(pos0 + i) * a.hidden + r] = v;
         }
