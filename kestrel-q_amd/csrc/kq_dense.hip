@@ -229,7 +229,11 @@ __global__ __launch_bounds__(kWaves * 64) void dense_q8(DenseArgs a) {
     /* D[token][row]: this lane holds row r0 + 16 i + j of tokens
      * t0 + 4 g .. + 3 */
     bool bad = false;
-    float *out = a.out + (size_t)blockIdx.z * a.tokens * a.rows;
+    /* a split gate/up pair stores its gate and up partials ([z][tokens]
+     * [2 rows]) for dense_swiglu; one matrix stores [z][tokens][rows] */
+    const bool parts2 = NMAT == 2 && gridDim.z > 1u;
+    const uint32_t ostride = parts2 ? 2u * a.rows : a.rows;
+    float *out = a.out + (size_t)blockIdx.z * a.tokens * ostride;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t t = t0 + 4u * g + (uint32_t)q;
@@ -242,20 +246,59 @@ __global__ __launch_bounds__(kWaves * 64) void dense_q8(DenseArgs a) {
             float v;
             if constexpr (NMAT == 2) {
                 const float gv = ldexpf(acc[0][i][q], -sg), uv = ldexpf(acc[1][i][q], -sg);
+                if (parts2) {
+                    out[(size_t)t * ostride + row] = gv;
+                    out[(size_t)t * ostride + a.rows + row] = uv;
+                    continue;
+                }
                 v = kq_swiglu(gv, uv);
                 bad |= !kq_isfinite(gv) || !kq_isfinite(uv);
             } else {
                 v = ldexpf(acc[0][i][q], -sg);
             }
             bad |= !kq_isfinite(v);
-            out[(size_t)t * a.rows + row] = v;
+            out[(size_t)t * ostride + row] = v;
         }
     }
     if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
+/* act[t][r] = swiglu(sum of the gate partials, sum of the up partials),
+ * the splits summed in order (parts [splits][tokens][2 rows]) */
+__global__ __launch_bounds__(256) void dense_swiglu(const float *__restrict__ parts,
+                                                    uint32_t splits, uint32_t tokens,
+                                                    uint32_t rows, float *__restrict__ out,
+                                                    uint32_t *status) {
+    const uint32_t n = tokens * rows;
+    bool bad = false;
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
+        const uint32_t t = i / rows, r = i - t * rows;
+        const size_t o = (size_t)t * 2u * rows + r, zs = (size_t)tokens * 2u * rows;
+        float gv = parts[o], uv = parts[o + rows];
+        for (uint32_t z = 1; z < splits; ++z) {
+            gv = gv + parts[z * zs + o];
+            uv = uv + parts[z * zs + o + rows];
+        }
+        const float v = kq_swiglu(gv, uv);
+        bad |= !kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(v);
+        out[i] = v;
+    }
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+}
+
 }  // namespace
+
+extern "C" hipError_t kq_launch_dense_swiglu(const float *parts, uint32_t splits,
+                                             uint32_t tokens, uint32_t rows, float *out,
+                                             uint32_t *status, hipStream_t s) {
+    const uint32_t n = tokens * rows;
+    uint32_t g = (n + 255u) / 256u;
+    if (g > 4096u) g = 4096u;
+    hipLaunchKernelGGL(dense_swiglu, dim3(g), dim3(256), 0, s, parts, splits, tokens, rows, out,
+                       status);
+    return hipGetLastError();
+}
 
 extern "C" int kq_launch_dense_q8_supported(uint32_t rows, uint32_t k, uint32_t tokens) {
     return rows != 0u && tokens != 0u && k % 64u == 0u && k != 0u &&

@@ -1661,10 +1661,25 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
              * after the routed pairs' */
             const uint8_t *st = (const uint8_t *)ws->outp;
             const size_t th = (size_t)tokens * d->hidden;
-            e = kq_launch_dense_q8(sg, su, d->inter, d->hidden, st, st + th * 2u,
-                                   (const int *)(st + th * 4u + (size_t)tokens * (d->hidden / 128u) * 16u),
-                                   tokens, 1u, ws->act + (size_t)tokens * d->top_k * d->inter,
-                                   status, s);
+            const int *sig =
+                (const int *)(st + th * 4u + (size_t)tokens * (d->hidden / 128u) * 16u);
+            float *sact = ws->act + (size_t)tokens * d->top_k * d->inter;
+            /* the columns in up to four runs (more workgroups for the few
+             * rows), their gate/up partials in dstage (free until the down
+             * pass), summed in order with the SwiGLU */
+            const uint32_t sp = kq_launch_dense_q8_splits(d->hidden, 4u);
+            const uint64_t need = (uint64_t)sp * tokens * 2u * d->inter * 4u;
+            const uint32_t ai = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+            if (sp > 1u && need <= kq_launch_dn_stage_bytes(tokens * (d->top_k + 1u), ai)) {
+                e = kq_launch_dense_q8(sg, su, d->inter, d->hidden, st, st + th * 2u, sig, tokens,
+                                       4u, (float *)ws->dstage, status, s);
+                if (e == hipSuccess)
+                    e = kq_launch_dense_swiglu((const float *)ws->dstage, sp, tokens, d->inter,
+                                               sact, status, s);
+            } else {
+                e = kq_launch_dense_q8(sg, su, d->inter, d->hidden, st, st + th * 2u, sig, tokens,
+                                       1u, sact, status, s);
+            }
         } else if (e == hipSuccess && !lds_shared) {
             e = pass_any<2>(w->shared_gate_type, d->hidden, g, u, sg, su, hidden, ws->offsets,
                             ws->perm_tok, E, tokens, d->top_k, d->inter, E, sh_wgs, ws->act,

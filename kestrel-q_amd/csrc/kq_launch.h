@@ -51,6 +51,11 @@ int kq_launch_dense_q8_supported(uint32_t rows, uint32_t k, uint32_t tokens);
 uint32_t kq_launch_dense_q8_splits(uint32_t k, uint32_t splits);
 hipError_t kq_launch_dense_split(const float *x, uint32_t tokens, uint32_t k, void *xh, void *xl,
                                  int *sig, int input, uint32_t *status, hipStream_t s);
+/* a gate/up pair launched with splits > 1 leaves gate and up partials
+ * [splits][tokens][2 rows]; kq_launch_dense_swiglu sums them in order and
+ * writes swiglu(gate, up) [tokens][rows] */
+hipError_t kq_launch_dense_swiglu(const float *parts, uint32_t splits, uint32_t tokens,
+                                  uint32_t rows, float *out, uint32_t *status, hipStream_t s);
 hipError_t kq_launch_dense_q8(const void *w0, const void *w1, uint32_t rows, uint32_t k,
                               const void *xh, const void *xl, const int *sig, uint32_t tokens,
                               uint32_t splits, float *out, uint32_t *status, hipStream_t s);
