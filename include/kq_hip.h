@@ -21,9 +21,18 @@
  * failures (non-finite block scales -> KQ_STATUS_MALFORMED_QUANTIZED_DATA,
  * non-finite inputs/results -> KQ_STATUS_NUMERIC_DOMAIN). In asynchronous
  * mode calls return after enqueueing and kq_hip_context_synchronize reports
- * them. Device outputs of a call that fails are unspecified (the reference
- * stages host outputs and commits on success; device results are written in
- * place and the status tells the caller not to use them).
+ * them.
+ *
+ * Commit on success: the reference stages its outputs and copies them only
+ * when a call succeeds (src/kq_weight_provider.c:420, :480,
+ * src/kq_moe_qwen38.c:562-565). A synchronous call here does the same for
+ * device outputs: it copies their prior contents aside before its first
+ * launch (one device-to-device copy of the outputs) and copies them back if
+ * the call fails, so a failed call leaves its outputs as they were
+ * (kq_hip_context_set_commit_on_success turns this off). Asynchronous calls
+ * and kq_hip_lm_head_greedy_f32_noalloc (which may not allocate the copy)
+ * write in place: their outputs are unspecified when the status reports a
+ * failure.
  */
 #ifndef KQ_HIP_H
 #define KQ_HIP_H
@@ -59,6 +68,10 @@ void kq_hip_context_destroy(kq_hip_context *context);
 /* 0 = synchronous (default), 1 = asynchronous. */
 kq_status kq_hip_context_set_async(kq_hip_context *context, int async,
                                    kq_diagnostic *diagnostic);
+/* 1 = synchronous calls restore their device outputs when they fail
+ * (default), 0 = outputs of a failed call are unspecified. */
+kq_status kq_hip_context_set_commit_on_success(kq_hip_context *context, int commit,
+                                               kq_diagnostic *diagnostic);
 /* Waits for enqueued work; reports and clears device-detected failures. */
 kq_status kq_hip_context_synchronize(kq_hip_context *context,
                                      kq_diagnostic *diagnostic);
@@ -388,19 +401,68 @@ typedef struct kq_hip_moe_weights {
 /* Replaces kq_moe_route_f32 (include/kq_moe.h:128-141,
  * src/kq_moe_qwen38.c:276-376) for token_count tokens: logits, softmax
  * probabilities, top-k ids (bit-identical to the CPU partial selection)
- * and renormalised weights, each [tokens][...] in device memory. */
+ * and renormalised weights, each [tokens][...] in device memory.
+ * router_weight_count must be experts x hidden (DIMENSION_MISMATCH); each
+ * capacity counts values and must hold tokens x experts (logits,
+ * probabilities) or tokens x top_k (ids, weights), else BUFFER_TOO_SMALL
+ * with the required counts in the message; outputs that overlap each other
+ * or an input fail with ALIASING_VIOLATION. The results are formed in
+ * scratch and written to the outputs only once the call has succeeded (in
+ * a synchronous call). device_shared_gate_weight [hidden] is read for the
+ * layer's shared gate logit, which the route leaves in scratch. */
 kq_status kq_hip_moe_route_f32(kq_hip_context *context,
                                const kq_hip_moe_config *config,
                                const float *device_router_weight,
+                               uint64_t router_weight_count,
                                const float *device_shared_gate_weight,
                                const float *device_hidden,
                                uint64_t token_count,
                                float *device_router_logits,
+                               uint64_t router_logits_capacity,
                                float *device_router_probabilities,
+                               uint64_t router_probabilities_capacity,
                                uint32_t *device_selected_ids,
+                               uint64_t selected_ids_capacity,
                                float *device_selected_weights,
+                               uint64_t selected_weights_capacity,
                                void *device_scratch, uint64_t scratch_bytes,
                                kq_diagnostic *diagnostic);
+
+/* Mirrors kq_moe_routed_expert_weights_f32 (include/kq_moe.h:91-98): one
+ * routed expert's member matrices, gate/up [routed_inter][hidden] and down
+ * [hidden][routed_inter], with element counts. */
+typedef struct kq_hip_moe_routed_expert_weights_f32 {
+    const float *gate;
+    uint64_t gate_count;
+    const float *up;
+    uint64_t up_count;
+    const float *down;
+    uint64_t down_count;
+} kq_hip_moe_routed_expert_weights_f32;
+
+/* Device scratch of kq_hip_moe_execute_routed_expert_f32: gate, up,
+ * activated [routed_inter] and the expert's output [hidden] (the
+ * reference's one-expert workspace, src/kq_moe.c). */
+uint64_t kq_hip_moe_config_one_expert_scratch_bytes(const kq_hip_moe_config *config);
+
+/* Replaces kq_moe_execute_routed_expert_f32 (include/kq_moe.h:143-152,
+ * src/kq_moe_qwen38.c:461-566): output_token [hidden] = down .
+ * swiglu(gate . x, up . x) for one expert's member matrices, every dot the
+ * reference's left-to-right binary32 chain (bit-identical). expert_id only
+ * names the member (INVALID_ARGUMENT past the config's experts). Checks in
+ * the reference's order: arguments, expert id, output and scratch sizes
+ * (BUFFER_TOO_SMALL), member counts (DIMENSION_MISMATCH), overlaps
+ * (ALIASING_VIOLATION); non-finite weights, input or results give
+ * NUMERIC_DOMAIN. The output is written only when the call succeeds. */
+kq_status kq_hip_moe_execute_routed_expert_f32(kq_hip_context *context,
+                                               const kq_hip_moe_config *config,
+                                               const kq_hip_moe_routed_expert_weights_f32 *weights,
+                                               uint32_t expert_id,
+                                               const float *device_hidden_token,
+                                               float *device_output_token,
+                                               uint64_t output_capacity,
+                                               void *device_scratch, uint64_t scratch_bytes,
+                                               kq_diagnostic *diagnostic);
 
 /* Replaces kq_moe_execute_quantized (src/kq_moe_internal.h:56-64,
  * src/kq_moe_qwen38.c:882-901) / kq_moe_execute_f32 (include/kq_moe.h:154-166):

@@ -82,11 +82,20 @@ __device__ __forceinline__ i4v dma_rsrc(const void *base, uint32_t bytes) {
 
 /* 16 bytes per lane from rsrc + voff into LDS at lds + 16 * lane */
 __device__ __forceinline__ void dma16(i4v rsrc, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\t"
-                 "buffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :
-                 : "v"(voff), "s"(rsrc), "s"(lds)
-                 : "memory", "m0");
+    /* m0 carries the LDS address; it leaves the statement as it entered
+       (saved and restored here), and one wait state separates each write of
+       m0 from the next instruction that may read it (the LDS-DMA load, or
+       the compiler's own code after the statement) */
+    uint32_t save;
+    asm volatile("s_mov_b32 %[sv], m0\n\t"
+                 "s_mov_b32 m0, %[lds]\n\t"
+                 "s_nop 0\n\t"
+                 "buffer_load_dwordx4 %[v], %[r], 0 offen lds\n\t"
+                 "s_mov_b32 m0, %[sv]\n\t"
+                 "s_nop 0"
+                 : [sv] "=&s"(save)
+                 : [v] "v"(voff), [r] "s"(rsrc), [lds] "s"(lds)
+                 : "memory");
 }
 
 template <int N>

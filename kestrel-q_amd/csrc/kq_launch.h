@@ -266,6 +266,13 @@ typedef struct kq_launch_moe_f32_ws {
 } kq_launch_moe_f32_ws;
 
 hipError_t kq_launch_f32_scan(const float *p, uint64_t n, uint32_t *status, hipStream_t s);
+/* one routed expert on F32 member matrices (gate/up [I][H], down [H][I]):
+ * gate, up, activated [I] and the output [H], every dot the reference's
+ * left-to-right binary32 chain */
+hipError_t kq_launch_routed_expert_f32(const float *gate_w, const float *up_w,
+                                       const float *down_w, const float *x, uint32_t hidden,
+                                       uint32_t inter, float *gate, float *up, float *act,
+                                       float *out, uint32_t *status, hipStream_t s);
 hipError_t kq_launch_moe_f32(const kq_launch_moe_dims *d, const kq_launch_moe_f32_weights *w,
                              const float *hidden, uint32_t tokens,
                              const kq_launch_moe_f32_ws *ws, float *out, uint32_t *status,

@@ -146,9 +146,51 @@ __global__ __launch_bounds__(kF32Threads) void f32_combine(F32Args a) {
     a.y[(size_t)t * H + h] = y;
 }
 
+/* one routed expert (src/kq_moe_qwen38.c:436-459): gate and up rows, then
+ * SwiGLU, one thread per row */
+__global__ __launch_bounds__(kF32Threads) void f32_member_gateup(
+    const float *__restrict__ gw, const float *__restrict__ uw, const float *__restrict__ x,
+    uint32_t hidden, uint32_t inter, float *__restrict__ gate, float *__restrict__ up,
+    float *__restrict__ act, uint32_t *status) {
+    const uint32_t r = blockIdx.x * kF32Threads + threadIdx.x;
+    if (r >= inter) return;
+    const float gv = chain_dot(gw + (size_t)r * hidden, x, hidden);
+    const float uv = chain_dot(uw + (size_t)r * hidden, x, hidden);
+    const float av = kq_swiglu(gv, uv);
+    if (!kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(av)) kq_flag(status, KQ_DEV_NUMERIC);
+    gate[r] = gv;
+    up[r] = uv;
+    act[r] = av;
+}
+
+/* its down rows over the activated vector */
+__global__ __launch_bounds__(kF32Threads) void f32_member_down(
+    const float *__restrict__ dw, const float *__restrict__ act, uint32_t hidden, uint32_t inter,
+    float *__restrict__ out, uint32_t *status) {
+    const uint32_t h = blockIdx.x * kF32Threads + threadIdx.x;
+    if (h >= hidden) return;
+    const float o = chain_dot(dw + (size_t)h * inter, act, inter);
+    if (!kq_isfinite(o)) kq_flag(status, KQ_DEV_NUMERIC);
+    out[h] = o;
+}
+
 uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kF32Threads - 1u) / kF32Threads); }
 
 }  // namespace
+
+extern "C" hipError_t kq_launch_routed_expert_f32(const float *gate_w, const float *up_w,
+                                                  const float *down_w, const float *x,
+                                                  uint32_t hidden, uint32_t inter, float *gate,
+                                                  float *up, float *act, float *out,
+                                                  uint32_t *status, hipStream_t s) {
+    hipLaunchKernelGGL(f32_member_gateup, dim3(blocks_for(inter)), dim3(kF32Threads), 0, s,
+                       gate_w, up_w, x, hidden, inter, gate, up, act, status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(f32_member_down, dim3(blocks_for(hidden)), dim3(kF32Threads), 0, s,
+                       down_w, act, hidden, inter, out, status);
+    return hipGetLastError();
+}
 
 extern "C" hipError_t kq_launch_f32_scan(const float *p, uint64_t n, uint32_t *status,
                                          hipStream_t s) {

@@ -27,6 +27,8 @@
 #define KQ_DEV_NUMERIC 2u
 #define KQ_DEV_INPUT 4u
 #define KQ_DEV_RANGE 8u
+/* output ranges one call can restore */
+#define KQ_SNAP_RANGES 4u
 
 struct kq_hip_context {
     int device;
@@ -43,6 +45,14 @@ struct kq_hip_context {
     void *stage_dev;    /* aligned device copy of a view span that starts off
                            the decoder's alignment, grown on demand */
     uint64_t stage_dev_cap;
+    /* commit-on-success of synchronous calls: the outputs' prior contents,
+     * copied aside before the call's launches and copied back when it fails */
+    int commit;
+    void *snap;
+    uint64_t snap_cap;
+    uint32_t snap_n;
+    void *snap_dst[KQ_SNAP_RANGES];
+    uint64_t snap_len[KQ_SNAP_RANGES];
 };
 
 struct kq_hip_moe_config {
@@ -51,6 +61,8 @@ struct kq_hip_moe_config {
 };
 
 /* ------------------------------------------------------------------ */
+
+static uint64_t align256(uint64_t n) { return (n + 255u) & ~(uint64_t)255u; }
 
 static kq_status hip_fail(kq_diagnostic *diag, hipError_t e, const char *what) {
     return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "%s: %s", what, hipGetErrorString(e));
@@ -95,11 +107,92 @@ static kq_status drain(kq_hip_context *c, kq_diagnostic *diag) {
     return KQ_STATUS_OK;
 }
 
+/* Copies the outputs of a synchronous call aside before its first launch
+ * (commit-on-success, the reference's staged outputs: src/kq_weight_provider.c
+ * :420, :480, src/kq_moe_qwen38.c:562-565). n ranges (pointer, bytes); empty
+ * or NULL ranges are skipped. Asynchronous calls, and contexts with the
+ * commit switched off, take no copy. On an allocation failure nothing has
+ * been launched and the outputs are untouched. */
+static kq_status snapshot(kq_hip_context *c, uint32_t n, void *const *p, const uint64_t *len,
+                          kq_diagnostic *diag) {
+    uint64_t total = 0u, off = 0u;
+    hipError_t e = hipSuccess;
+    /* a call enqueued by another call (the MoE block's stages) runs
+     * asynchronously and leaves the outer call's copies in place */
+    if (c->async || !c->commit) return KQ_STATUS_OK;
+    c->snap_n = 0u;
+    for (uint32_t i = 0; i < n; ++i)
+        if (p[i] != NULL) total += align256(len[i]);
+    if (total == 0u) return KQ_STATUS_OK;
+    if (c->snap_cap < total) {
+        if (c->snap) {
+            (void)hipStreamSynchronize(c->stream);
+            (void)hipFree(c->snap);
+            c->snap = NULL;
+            c->snap_cap = 0u;
+        }
+        e = hipMalloc(&c->snap, (size_t)total);
+        if (e != hipSuccess)
+            return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY,
+                           "commit-on-success copy of the outputs (%llu bytes): %s",
+                           (unsigned long long)total, hipGetErrorString(e));
+        c->snap_cap = total;
+    }
+    for (uint32_t i = 0; i < n && e == hipSuccess; ++i) {
+        if (p[i] == NULL || len[i] == 0u) continue;
+        e = hipMemcpyAsync((char *)c->snap + off, p[i], (size_t)len[i], hipMemcpyDeviceToDevice,
+                           c->stream);
+        c->snap_dst[c->snap_n] = p[i];
+        c->snap_len[c->snap_n] = len[i];
+        c->snap_n++;
+        off += align256(len[i]);
+    }
+    if (e != hipSuccess) {
+        c->snap_n = 0u;
+        return hip_fail(diag, e, "commit-on-success copy");
+    }
+    return KQ_STATUS_OK;
+}
+
+static kq_status snapshot1(kq_hip_context *c, void *p, uint64_t len, kq_diagnostic *diag) {
+    return snapshot(c, 1u, &p, &len, diag);
+}
+
+/* A failed synchronous call: its outputs get their prior contents back
+ * (the work it enqueued has drained, or the stream is broken and the copies
+ * fail with it). */
+static void restore(kq_hip_context *c) {
+    uint64_t off = 0u;
+    for (uint32_t i = 0; i < c->snap_n; ++i) {
+        (void)hipMemcpyAsync(c->snap_dst[i], (char *)c->snap + off, (size_t)c->snap_len[i],
+                             hipMemcpyDeviceToDevice, c->stream);
+        off += align256(c->snap_len[i]);
+    }
+    if (c->snap_n != 0u) (void)hipStreamSynchronize(c->stream);
+    c->snap_n = 0u;
+}
+
+/* The end of a call: asynchronous calls return after enqueueing;
+ * synchronous ones drain the stream, report the device status word and, on
+ * any failure, restore the outputs copied aside by snapshot(). */
 static kq_status finish(kq_hip_context *c, hipError_t launch, const char *what,
                         kq_diagnostic *diag) {
-    if (launch != hipSuccess) return hip_fail(diag, launch, what);
-    if (c->async) return KQ_STATUS_OK;
-    return drain(c, diag);
+    kq_status st;
+    if (c->async && launch == hipSuccess) return KQ_STATUS_OK;
+    if (launch != hipSuccess) {
+        st = hip_fail(diag, launch, what);
+        if (!c->async) {
+            (void)hipStreamSynchronize(c->stream);
+            restore(c);
+        }
+        return st;
+    }
+    st = drain(c, diag);
+    if (st != KQ_STATUS_OK)
+        restore(c);
+    else
+        c->snap_n = 0u;
+    return st;
 }
 
 static int ranges_overlap(const void *a, uint64_t an, const void *b, uint64_t bn) {
@@ -110,7 +203,6 @@ static int ranges_overlap(const void *a, uint64_t an, const void *b, uint64_t bn
 
 static int aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0u; }
 
-static uint64_t align256(uint64_t n) { return (n + 255u) & ~(uint64_t)255u; }
 
 static int u64_mul(uint64_t a, uint64_t b, uint64_t *out) {
     if (a != 0u && b > UINT64_MAX / a) return 0;
@@ -143,6 +235,7 @@ kq_status kq_hip_context_create(int device, kq_hip_context **out, kq_diagnostic 
     c = (kq_hip_context *)calloc(1, sizeof(*c));
     if (c == NULL) return kq_fail(diag, KQ_STATUS_OUT_OF_MEMORY, "context allocation failed");
     c->device = device;
+    c->commit = 1;
     e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc((void **)&c->d_status, sizeof(uint32_t));
@@ -169,6 +262,7 @@ void kq_hip_context_destroy(kq_hip_context *c) {
     if (c->part_v) (void)hipFree(c->part_v);
     if (c->part_i) (void)hipFree(c->part_i);
     if (c->stage_dev) (void)hipFree(c->stage_dev);
+    if (c->snap) (void)hipFree(c->snap);
     if (c->d_status) (void)hipFree(c->d_status);
     if (c->h_status) (void)hipHostFree(c->h_status);
     for (int k = 0; k < 2; ++k) {
@@ -183,6 +277,14 @@ kq_status kq_hip_context_set_async(kq_hip_context *c, int async, kq_diagnostic *
     kq_diagnostic_clear(diag);
     if (!ctx_ok(c)) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "valid context is required");
     c->async = async ? 1 : 0;
+    return KQ_STATUS_OK;
+}
+
+kq_status kq_hip_context_set_commit_on_success(kq_hip_context *c, int commit,
+                                               kq_diagnostic *diag) {
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c)) return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "valid context is required");
+    c->commit = commit ? 1 : 0;
     return KQ_STATUS_OK;
 }
 
@@ -439,6 +541,7 @@ kq_status kq_hip_dequantize_blocks_f32(kq_hip_context *c, uint32_t type_id, cons
                        "packed input must be 16-byte (Q4_K, Q5_K), 2-byte (BF16) or 4-byte "
                        "aligned, output 16-byte");
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) st = snapshot1(c, output, out_bytes, diag);
     if (st != KQ_STATUS_OK) return st;
     return finish(c, kq_launch_dequant(type_id, packed, blocks, output, c->d_status, c->stream),
                   "dequant launch", diag);
@@ -678,15 +781,16 @@ kq_status kq_hip_gdn_canonicalize(kq_hip_context *c, uint32_t layout, uint32_t t
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "the two matrices overlap");
     if (!aligned(phys, 2u) || !aligned(canon, 2u) || bb % 2u != 0u)
         return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "matrices must be 2-byte aligned");
+    units = columns ? rows * KQ_GDN_UNITS : rows;
+    unit_bytes = columns ? 128u / be * bb : row_bytes;
+    if (layout != KQ_HIP_GDN_NONE && (units > 0x7fffffffu || unit_bytes > 0x7fffffffu))
+        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "matrix too large for one gather");
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) st = snapshot1(c, canon, bytes, diag);
     if (st != KQ_STATUS_OK) return st;
     if (layout == KQ_HIP_GDN_NONE)
         return finish(c, hipMemcpyAsync(canon, phys, (size_t)bytes, hipMemcpyDeviceToDevice,
                                         c->stream), "canonical copy", diag);
-    units = columns ? rows * KQ_GDN_UNITS : rows;
-    unit_bytes = columns ? 128u / be * bb : row_bytes;
-    if (units > 0x7fffffffu || unit_bytes > 0x7fffffffu)
-        return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED, "matrix too large for one gather");
     return finish(c, kq_launch_gdn_gather(phys, canon, units, (uint32_t)unit_bytes, columns, prefix,
                                           (uint32_t)width, KQ_GDN_UNITS, c->stream),
                   "GDN gather launch", diag);
@@ -776,6 +880,7 @@ kq_status kq_hip_quantized_matvec_f32(kq_hip_context *c, uint32_t type_id, const
     st = validate_matvec(c, type_id, w, rows, cols, x, batch, y, capacity, diag);
     if (st != KQ_STATUS_OK) return st;
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) st = snapshot1(c, y, rows * batch * 4u, diag);
     if (st != KQ_STATUS_OK) return st;
     return finish(c, enqueue_matvec(c, type_id, w, rows, cols, x, batch, y, NULL, NULL, 0u),
                   "matvec launch", diag);
@@ -819,6 +924,7 @@ kq_status kq_hip_greedy_argmax_f32(kq_hip_context *c, const float *logits, uint6
     if (st != KQ_STATUS_OK) return st;
     parts = kq_launch_argmax_parts((uint32_t)count);
     st = ensure_parts(c, (uint64_t)parts * batch, diag);
+    if (st == KQ_STATUS_OK) st = snapshot1(c, ids, (uint64_t)batch * 4u, diag);
     if (st != KQ_STATUS_OK) return st;
     return finish(c, kq_launch_argmax(logits, (uint32_t)count, batch, c->part_v, c->part_i, ids,
                                       c->d_status, c->stream),
@@ -866,7 +972,10 @@ static kq_status lm_head(kq_hip_context *c, uint32_t type_id, const void *w, uin
         pv = (float *)c->noalloc;
         pi = (uint32_t *)((char *)c->noalloc + cap * sizeof(float));
     } else {
+        void *const outs[2] = {logits, ids};
+        const uint64_t lens[2] = {vocab * batch * 4u, (uint64_t)batch * 4u};
         st = ensure_parts(c, (uint64_t)nparts * batch, diag);
+        if (st == KQ_STATUS_OK) st = snapshot(c, 2u, outs, lens, diag);
         if (st != KQ_STATUS_OK) return st;
         pv = c->part_v;
         pi = c->part_i;
@@ -909,6 +1018,7 @@ kq_status kq_hip_f32_expf(kq_hip_context *c, const float *in, uint64_t n, float 
     if (ranges_overlap(in, n * 4u, out, n * 4u) && in != out)
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "input and output overlap");
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) st = snapshot1(c, out, n * 4u, diag);
     if (st != KQ_STATUS_OK) return st;
     return finish(c, kq_launch_expf(in, n, out, c->stream), "expf launch", diag);
 }
@@ -1003,37 +1113,153 @@ static kq_status moe_common(const kq_hip_context *c, const kq_hip_moe_config *cf
 }
 
 kq_status kq_hip_moe_route_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
-                               const float *router, const float *sgw, const float *hidden,
-                               uint64_t tokens, float *logits, float *probs, uint32_t *ids,
-                               float *weights, void *scratch, uint64_t scratch_bytes,
+                               const float *router, uint64_t router_count, const float *sgw,
+                               const float *hidden, uint64_t tokens, float *logits,
+                               uint64_t logits_cap, float *probs, uint64_t probs_cap,
+                               uint32_t *ids, uint64_t ids_cap, float *weights,
+                               uint64_t weights_cap, void *scratch, uint64_t scratch_bytes,
                                kq_diagnostic *diag) {
     kq_launch_moe_dims d;
     kq_launch_moe_ws ws;
+    uint64_t need_e, need_k, eb, kb, rb;
     hipError_t e;
     kq_status st;
     kq_diagnostic_clear(diag);
-    st = moe_common(c, cfg, router, sgw, hidden, tokens, scratch, scratch_bytes, diag);
-    if (st != KQ_STATUS_OK) return st;
+    /* the reference's order of checks (src/kq_moe_qwen38.c:293-349):
+     * arguments, shape, output capacities, overlaps */
     if (logits == NULL || probs == NULL || ids == NULL || weights == NULL)
         return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete MoE route arguments are required");
+    st = moe_common(c, cfg, router, sgw, hidden, tokens, scratch, scratch_bytes, diag);
+    if (st != KQ_STATUS_OK) return st;
     d = launch_dims(cfg);
+    if (router_count != (uint64_t)d.experts * d.hidden)
+        return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH,
+                       "MoE router weight shape mismatch: %llu values for %u x %u",
+                       (unsigned long long)router_count, d.experts, d.hidden);
+    need_e = tokens * d.experts;
+    need_k = tokens * d.top_k;
+    if (logits_cap < need_e || probs_cap < need_e || ids_cap < need_k || weights_cap < need_k)
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL,
+                       "MoE route output capacity is too small: logits and probabilities need "
+                       "%llu values, ids and weights %llu",
+                       (unsigned long long)need_e, (unsigned long long)need_k);
+    eb = need_e * 4u;
+    kb = need_k * 4u;
+    rb = router_count * 4u;
+    {
+        const void *outs[4] = {logits, probs, ids, weights};
+        const uint64_t lens[4] = {eb, eb, kb, kb};
+        for (int i = 0; i < 4; ++i) {
+            int bad = ranges_overlap(router, rb, outs[i], lens[i]) ||
+                      ranges_overlap(hidden, tokens * d.hidden * 4u, outs[i], lens[i]) ||
+                      ranges_overlap(sgw, (uint64_t)d.hidden * 4u, outs[i], lens[i]) ||
+                      ranges_overlap(scratch, scratch_bytes, outs[i], lens[i]);
+            for (int j = i + 1; j < 4; ++j) bad |= ranges_overlap(outs[i], lens[i], outs[j], lens[j]);
+            if (bad)
+                return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                               "MoE route inputs and outputs must not overlap");
+        }
+    }
     kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
     st = set_device(c, diag);
     if (st != KQ_STATUS_OK) return st;
+    /* the results land in scratch; the outputs are written from there, in a
+     * synchronous call only once the device reported success (the
+     * reference's commit-on-success) */
     e = kq_launch_moe_route(&d, router, sgw, hidden, (uint32_t)tokens, &ws, c->d_status, 0, NULL,
                             NULL, c->stream);
+    if (!c->async) {
+        st = finish(c, e, "MoE route launch", diag);
+        if (st != KQ_STATUS_OK) return st;
+    } else if (e != hipSuccess) {
+        return hip_fail(diag, e, "MoE route launch");
+    }
+    e = hipMemcpyAsync(logits, ws.logits, eb, hipMemcpyDeviceToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(probs, ws.probs, eb, hipMemcpyDeviceToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(ids, ws.ids, kb, hipMemcpyDeviceToDevice, c->stream);
     if (e == hipSuccess)
-        e = hipMemcpyAsync(logits, ws.logits, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
-                           c->stream);
+        e = hipMemcpyAsync(weights, ws.weights, kb, hipMemcpyDeviceToDevice, c->stream);
+    return finish(c, e, "MoE route copy", diag);
+}
+
+/* kq_moe_execute_routed_expert_f32 (src/kq_moe_qwen38.c:461-566): gate,
+ * up, activated and the expert's output in scratch, the output copied to
+ * the caller's buffer on success */
+uint64_t kq_hip_moe_config_one_expert_scratch_bytes(const kq_hip_moe_config *cfg) {
+    if (!moe_ok(cfg)) return 0u;
+    return 3u * align256((uint64_t)cfg->dims.routed_intermediate_size * 4u) +
+           align256((uint64_t)cfg->dims.hidden_size * 4u);
+}
+
+kq_status kq_hip_moe_execute_routed_expert_f32(kq_hip_context *c, const kq_hip_moe_config *cfg,
+                                               const kq_hip_moe_routed_expert_weights_f32 *w,
+                                               uint32_t expert_id, const float *hidden,
+                                               float *out, uint64_t capacity, void *scratch,
+                                               uint64_t scratch_bytes, kq_diagnostic *diag) {
+    uint64_t H, I, member, hb, ib;
+    float *gate, *up, *act, *tmp;
+    hipError_t e;
+    kq_status st;
+    kq_diagnostic_clear(diag);
+    if (!ctx_ok(c) || !moe_ok(cfg) || w == NULL || hidden == NULL || out == NULL ||
+        scratch == NULL)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "complete routed-expert arguments are required");
+    H = cfg->dims.hidden_size;
+    I = cfg->dims.routed_intermediate_size;
+    if (expert_id >= cfg->dims.expert_count)
+        return kq_fail(diag, KQ_STATUS_INVALID_ARGUMENT, "routed expert ID is out of range");
+    if (capacity < H || scratch_bytes < kq_hip_moe_config_one_expert_scratch_bytes(cfg) ||
+        !aligned(scratch, 4u))
+        return kq_fail(diag, KQ_STATUS_BUFFER_TOO_SMALL,
+                       "routed expert output or scratch is too small (output %llu values, scratch "
+                       "%llu bytes)",
+                       (unsigned long long)H,
+                       (unsigned long long)kq_hip_moe_config_one_expert_scratch_bytes(cfg));
+    if (H > UINT32_MAX / 4u || I > UINT32_MAX / 4u || !u64_mul(H, I, &member))
+        return kq_fail(diag, KQ_STATUS_ARITHMETIC_OVERFLOW, "routed expert member geometry overflows");
+    if (w->gate == NULL || w->up == NULL || w->down == NULL || w->gate_count != member ||
+        w->up_count != member || w->down_count != member)
+        return kq_fail(diag, KQ_STATUS_DIMENSION_MISMATCH,
+                       "MoE routed member gate/up/down shape mismatch: %llu values each",
+                       (unsigned long long)member);
+    if (!aligned(hidden, 4u) || !aligned(out, 4u) || !aligned(w->gate, 4u) ||
+        !aligned(w->up, 4u) || !aligned(w->down, 4u))
+        return kq_fail(diag, KQ_STATUS_INVALID_ALIGNMENT, "routed expert buffers need 4-byte alignment");
+    hb = H * 4u;
+    if (ranges_overlap(hidden, hb, out, hb) || ranges_overlap(hidden, hb, scratch, scratch_bytes) ||
+        ranges_overlap(out, hb, scratch, scratch_bytes))
+        return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "routed expert buffers must not overlap");
+    {
+        const void *wp[3] = {w->gate, w->up, w->down};
+        for (int i = 0; i < 3; ++i)
+            if (ranges_overlap(wp[i], member * 4u, out, hb) ||
+                ranges_overlap(wp[i], member * 4u, scratch, scratch_bytes))
+                return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
+                               "MoE weights must not overlap writable expert buffers");
+    }
+    ib = align256(I * 4u);
+    gate = (float *)scratch;
+    up = (float *)((char *)scratch + ib);
+    act = (float *)((char *)scratch + 2u * ib);
+    tmp = (float *)((char *)scratch + 3u * ib);
+    st = set_device(c, diag);
+    if (st != KQ_STATUS_OK) return st;
+    /* the reference validates gate, up, down, then the input, for finiteness */
+    e = kq_launch_f32_scan(w->gate, member, c->d_status, c->stream);
+    if (e == hipSuccess) e = kq_launch_f32_scan(w->up, member, c->d_status, c->stream);
+    if (e == hipSuccess) e = kq_launch_f32_scan(w->down, member, c->d_status, c->stream);
+    if (e == hipSuccess) e = kq_launch_f32_scan(hidden, H, c->d_status, c->stream);
     if (e == hipSuccess)
-        e = hipMemcpyAsync(probs, ws.probs, tokens * d.experts * 4u, hipMemcpyDeviceToDevice,
-                           c->stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(ids, ws.ids, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice, c->stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(weights, ws.weights, tokens * d.top_k * 4u, hipMemcpyDeviceToDevice,
-                           c->stream);
-    return finish(c, e, "MoE route launch", diag);
+        e = kq_launch_routed_expert_f32(w->gate, w->up, w->down, hidden, (uint32_t)H,
+                                        (uint32_t)I, gate, up, act, tmp, c->d_status, c->stream);
+    if (!c->async) {
+        st = finish(c, e, "routed expert launch", diag);
+        if (st != KQ_STATUS_OK) return st;
+    } else if (e != hipSuccess) {
+        return hip_fail(diag, e, "routed expert launch");
+    }
+    return finish(c, hipMemcpyAsync(out, tmp, hb, hipMemcpyDeviceToDevice, c->stream),
+                  "routed expert copy", diag);
 }
 
 kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_config *cfg,
@@ -1100,6 +1326,11 @@ kq_status kq_hip_moe_execute_quantized(kq_hip_context *c, const kq_hip_moe_confi
                        "MoE weights and output must be 16-byte aligned");
     kq_launch_moe_ws_carve(&d, (uint32_t)tokens, scratch, &ws);
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) {
+        void *const outs[2] = {out, ids};
+        const uint64_t lens[2] = {tokens * d.hidden * 4u, tokens * d.top_k * 4u};
+        st = snapshot(c, 2u, outs, lens, diag);
+    }
     if (st != KQ_STATUS_OK) return st;
     /* several tokens: each expert's weights stream once for all of its
      * tokens (grouped MFMA path), whose activation split the route finish
@@ -1345,6 +1576,7 @@ kq_status kq_hip_moe_execute_f32(kq_hip_context *c, const kq_hip_moe_config *cfg
                                "MoE weights must not overlap writable execution buffers");
         }
         st = set_device(c, diag);
+        if (st == KQ_STATUS_OK) st = snapshot1(c, out, vbytes, diag);
         if (st != KQ_STATUS_OK) return st;
         /* the reference validates the input, then every weight, for finiteness */
         e = kq_launch_f32_scan(hidden, vals, c->d_status, c->stream);
@@ -1362,8 +1594,14 @@ kq_status kq_hip_moe_execute_f32(kq_hip_context *c, const kq_hip_moe_config *cfg
     lw.shared_gate_weight = w->shared_gate_weight;
     if (e == hipSuccess)
         e = kq_launch_moe_f32(&d, &lw, hidden, (uint32_t)tokens, &ws, out, c->d_status, c->stream);
-    if (e != hipSuccess) return hip_fail(diag, e, "F32 MoE launch");
-    st = drain(c, diag); /* always synchronous: the observers read the results */
+    /* always synchronous: the observers read the results */
+    if (!c->async) {
+        st = finish(c, e, "F32 MoE launch", diag);
+    } else if (e != hipSuccess) {
+        st = hip_fail(diag, e, "F32 MoE launch");
+    } else {
+        st = drain(c, diag);
+    }
     if (st != KQ_STATUS_OK) return st;
     if (ro == NULL && co == NULL) return KQ_STATUS_OK;
     return f32_observe(c, &d, tokens, &ws, out, ro, co, user, diag);
@@ -1402,6 +1640,11 @@ kq_status kq_hip_moe_token_permutation(kq_hip_context *c, const kq_hip_moe_confi
         ranges_overlap(scratch, pairs * 4u, ids, pairs * 4u))
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION, "permutation buffers overlap");
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) {
+        void *const outs[3] = {offsets, pair_token, pair_slot};
+        const uint64_t lens[3] = {(d.experts + 1u) * 4u, pairs * 4u, pairs * 4u};
+        st = snapshot(c, 3u, outs, lens, diag);
+    }
     if (st != KQ_STATUS_OK) return st;
     return finish(c,
                   kq_launch_moe_permute(ids, (uint32_t)tokens, d.top_k, d.experts, offsets,
@@ -1526,6 +1769,11 @@ kq_status kq_hip_gr_read_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
     sig_dn = (int *)((char *)parts + align256(KQ_GR_SPLITS * tokens * d->rank * 4u));
     sig_up = (int *)((char *)sig_dn + align256(tokens * 4u));
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) {
+        void *const outs[2] = {mixed, write_gate};
+        const uint64_t lens[2] = {tokens * d->hidden_size * 4u, tokens * d->branch_count * 4u};
+        st = snapshot(c, 2u, outs, lens, diag);
+    }
     if (st != KQ_STATUS_OK) return st;
     e = kq_launch_gr_norm(x, w->norm, (uint32_t)tokens, d->branch_count, d->hidden_size,
                           d->rms_epsilon, normalized, c->d_status, c->stream);
@@ -1592,6 +1840,7 @@ kq_status kq_hip_gr_write_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
         return kq_fail(diag, KQ_STATUS_ALIASING_VIOLATION,
                        "gated residual output may only be the branches themselves");
     st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) st = snapshot1(c, out, tokens * W * 4u, diag);
     if (st != KQ_STATUS_OK) return st;
     return finish(c, kq_launch_gr_write(x, block_output, write_gate, (uint32_t)tokens,
                                         d->branch_count, d->hidden_size, out, c->d_status,
@@ -1658,6 +1907,13 @@ kq_status kq_hip_moe_block_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
     p += hb;
     wg = (float *)p;
     p += align256(tokens * d->branch_count * 4u);
+    st = set_device(c, diag);
+    if (st == KQ_STATUS_OK) {
+        void *const outs[2] = {out, ids};
+        const uint64_t lens[2] = {tokens * W * 4u, tokens * cfg->dims.top_k * 4u};
+        st = snapshot(c, 2u, outs, lens, diag);
+    }
+    if (st != KQ_STATUS_OK) return st;
     /* one synchronisation for the whole step: the three stages enqueue */
     prev = c->async;
     c->async = 1;
@@ -1675,6 +1931,7 @@ kq_status kq_hip_moe_block_f32(kq_hip_context *c, const kq_hip_gr_dimensions *d,
         if (!prev) {
             kq_diagnostic ignored;
             (void)drain(c, &ignored);
+            restore(c);
         }
         return st;
     }

@@ -86,6 +86,11 @@ class MoeWeightsF32(C.Structure):
                 for n, t in ((role, C.c_void_p), (role + "_count", C.c_uint64))]
 
 
+class RoutedExpertWeightsF32(C.Structure):
+    _fields_ = [(n, t) for role in ("gate", "up", "down")
+                for n, t in ((role, C.c_void_p), (role + "_count", C.c_uint64))]
+
+
 class MoeCheckpoint(C.Structure):
     _fields_ = [("kind", C.c_int), ("token_index", C.c_uint64), ("expert_id", C.c_uint32),
                 ("top_k_position", C.c_uint32), ("rank", C.c_uint32),
@@ -238,6 +243,7 @@ SIGNATURES = {
     "kq_hip_context_create": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
     "kq_hip_context_destroy": (None, [C.c_void_p]),
     "kq_hip_context_set_async": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
+    "kq_hip_context_set_commit_on_success": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
     "kq_hip_context_synchronize": (C.c_int, [C.c_void_p, C.c_void_p]),
     "kq_hip_context_stream": (C.c_void_p, [C.c_void_p]),
     "kq_hip_malloc": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
@@ -283,10 +289,16 @@ SIGNATURES = {
     "kq_hip_moe_config_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "kq_hip_moe_config_close": (None, [C.c_void_p]),
     "kq_hip_moe_config_scratch_bytes": (C.c_uint64, [C.c_void_p, C.c_uint64]),
-    "kq_hip_moe_route_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-                                       C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p,
-                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
-                                       C.c_void_p]),
+    "kq_hip_moe_route_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
+                                       C.c_void_p, C.c_void_p, C.c_uint64,
+                                       C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
+                                       C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
+                                       C.c_void_p, C.c_uint64, C.c_void_p]),
+    "kq_hip_moe_config_one_expert_scratch_bytes": (C.c_uint64, [C.c_void_p]),
+    "kq_hip_moe_execute_routed_expert_f32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p,
+                                                       C.c_uint32, C.c_void_p, C.c_void_p,
+                                                       C.c_uint64, C.c_void_p, C.c_uint64,
+                                                       C.c_void_p]),
     "kq_hip_moe_execute_quantized": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p,
                                                C.c_void_p, C.c_uint64, C.c_void_p]),
@@ -432,6 +444,9 @@ class MoeConfig:
     def scratch_bytes(self, tokens: int) -> int:
         return lib().kq_hip_moe_config_scratch_bytes(C.c_void_p(self.handle), tokens)
 
+    def one_expert_scratch_bytes(self) -> int:
+        return lib().kq_hip_moe_config_one_expert_scratch_bytes(C.c_void_p(self.handle))
+
     def f32_scratch_bytes(self, tokens: int) -> int:
         return lib().kq_hip_moe_config_f32_scratch_bytes(C.c_void_p(self.handle), tokens)
 
@@ -533,6 +548,11 @@ class Context:
     def set_async(self, on: bool) -> None:
         d = Diagnostic()
         check(lib().kq_hip_context_set_async(C.c_void_p(self.handle), int(on), C.byref(d)), d)
+
+    def set_commit_on_success(self, on: bool) -> None:
+        d = Diagnostic()
+        check(lib().kq_hip_context_set_commit_on_success(C.c_void_p(self.handle), int(on),
+                                                         C.byref(d)), d)
 
     def synchronize(self) -> None:
         d = Diagnostic()
@@ -649,13 +669,33 @@ class Context:
 
     # ---- MoE ----
     def moe_route(self, cfg: MoeConfig, router, shared_gate_weight, hidden, tokens: int,
-                  logits, probs, ids, weights, scratch, scratch_bytes: int) -> None:
+                  logits, probs, ids, weights, scratch, scratch_bytes: int,
+                  router_count: int | None = None, caps: tuple | None = None) -> None:
+        """caps: (logits, probabilities, ids, weights) capacities in values;
+        by default exactly what the tokens need."""
         d = Diagnostic()
-        check(lib().kq_hip_moe_route_f32(self._h, C.c_void_p(cfg.handle), self._p(router),
+        ne, nk = tokens * cfg.experts, tokens * cfg.top_k
+        cl, cp, ci, cw = caps if caps is not None else (ne, ne, nk, nk)
+        rc = cfg.experts * cfg.hidden if router_count is None else router_count
+        check(lib().kq_hip_moe_route_f32(self._h, C.c_void_p(cfg.handle), self._p(router), rc,
                                          self._p(shared_gate_weight), self._p(hidden), tokens,
-                                         self._p(logits), self._p(probs), self._p(ids),
-                                         self._p(weights), self._p(scratch), scratch_bytes,
-                                         C.byref(d)), d)
+                                         self._p(logits), cl, self._p(probs), cp,
+                                         self._p(ids), ci, self._p(weights), cw,
+                                         self._p(scratch), scratch_bytes, C.byref(d)), d)
+
+    def moe_routed_expert_f32(self, cfg: MoeConfig, gate, up, down, expert_id: int, hidden,
+                              out, scratch, scratch_bytes: int, capacity: int | None = None,
+                              counts: tuple | None = None) -> None:
+        """One routed expert on F32 member matrices (device pointers);
+        counts: (gate, up, down) element counts, by default the config's."""
+        d = Diagnostic()
+        m = cfg.inter * cfg.hidden
+        gc, uc, dc = counts if counts is not None else (m, m, m)
+        w = RoutedExpertWeightsF32(self._p(gate), gc, self._p(up), uc, self._p(down), dc)
+        cap = cfg.hidden if capacity is None else capacity
+        check(lib().kq_hip_moe_execute_routed_expert_f32(
+            self._h, C.c_void_p(cfg.handle), C.byref(w), expert_id, self._p(hidden),
+            self._p(out), cap, self._p(scratch), scratch_bytes, C.byref(d)), d)
 
     def moe_execute(self, cfg: MoeConfig, weights: MoeWeights, hidden, tokens: int, out,
                     ids, scratch, scratch_bytes: int, capacity: int | None = None) -> None:

@@ -622,6 +622,32 @@ int kqo_f32_swiglu(const float *g, const float *u, uint64_t n, float *out) {
     return KQO_OK;
 }
 
+/* src/kq_moe_qwen38.c:436-459 (kq_moe_expert_member) as called by
+ * kq_moe_execute_routed_expert_f32 (:461-566): gate and up rows as
+ * left-to-right dots (kq_moe_project, :198-209), SwiGLU, the down rows over
+ * the activated vector; the output is written only on success. */
+int kqo_moe_routed_expert_f32(uint32_t hidden, uint32_t inter, const float *gate,
+                              const float *up, const float *down, const float *x, float *out) {
+    float *g = (float *)malloc((size_t)inter * 3u * sizeof(float) + (size_t)hidden * sizeof(float));
+    float *u, *a, *o;
+    int st = KQO_OK;
+    uint32_t r;
+    if (g == NULL) return KQO_INVALID_ARGUMENT;
+    u = g + inter;
+    a = u + inter;
+    o = a + inter;
+    for (r = 0U; r < inter && st == KQO_OK; ++r)
+        st = kqo_f32_dot(gate + (size_t)r * hidden, x, hidden, &g[r]);
+    for (r = 0U; r < inter && st == KQO_OK; ++r)
+        st = kqo_f32_dot(up + (size_t)r * hidden, x, hidden, &u[r]);
+    if (st == KQO_OK) st = kqo_f32_swiglu(g, u, inter, a);
+    for (r = 0U; r < hidden && st == KQO_OK; ++r)
+        st = kqo_f32_dot(down + (size_t)r * inter, a, inter, &o[r]);
+    if (st == KQO_OK) memcpy(out, o, (size_t)hidden * sizeof(float));
+    free(g);
+    return st;
+}
+
 int kqo_f32_rms_norm(const float *a, const float *w, uint64_t n, float eps,
                      float *out) {
     float sum = 0.0f, mean, inv;

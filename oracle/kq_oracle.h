@@ -76,6 +76,9 @@ int kqo_f32_dot(const float *a, const float *b, uint64_t n, float *out);
 int kqo_f32_sigmoid(const float *a, uint64_t n, float *out);
 int kqo_f32_silu(const float *a, uint64_t n, float *out);
 int kqo_f32_swiglu(const float *g, const float *u, uint64_t n, float *out);
+/* one routed expert on F32 member matrices (src/kq_moe_qwen38.c:436-566) */
+int kqo_moe_routed_expert_f32(uint32_t hidden, uint32_t inter, const float *gate,
+                              const float *up, const float *down, const float *x, float *out);
 int kqo_f32_rms_norm(const float *a, const float *w, uint64_t n, float eps,
                      float *out);
 int kqo_f32_softmax(const float *a, uint64_t n, float *out);

@@ -108,6 +108,7 @@ def _declare(l: C.CDLL) -> None:
     l.kqo_moe_execute.argtypes = [C.POINTER(MoeDims), C.POINTER(MoeWeights), P, U64, P,
                                   C.POINTER(MoeTrace), I]
     l.kqo_moe_permutation.argtypes = [P, U64, U32, U32, P, P, P]
+    l.kqo_moe_routed_expert_f32.argtypes = [U32, U32, P, P, P, P, P]
     l.kqo_gdn_physical_row.argtypes = [U32, U64]
     l.kqo_gdn_physical_row.restype = U64
     l.kqo_gdn_physical_column.argtypes = [U32, U64]
@@ -401,6 +402,21 @@ def certify_campaign(seed: int, trials: int, experts: int, hidden: int, top_k: i
     keys = ("trials", "certified", "certified_mismatch", "rounding_decided",
             "first_mismatch_plus_1", "route_failures")
     return {k: int(v) for k, v in zip(keys, st_arr)}
+
+
+def moe_routed_expert(gate: np.ndarray, up: np.ndarray, down: np.ndarray,
+                      x: np.ndarray) -> np.ndarray:
+    """One routed expert on F32 member matrices gate/up [I][H], down [H][I]
+    (kq_moe_execute_routed_expert_f32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    H = x.size
+    g, u, d = (np.ascontiguousarray(a, np.float32) for a in (gate, up, down))
+    inter = g.size // H
+    out = np.empty(H, np.float32)
+    st = lib().kqo_moe_routed_expert_f32(H, inter, _p(g), _p(u), _p(d), _p(x), _p(out))
+    if st != 0:
+        raise OracleError(st)
+    return out
 
 
 def moe_permutation(ids: np.ndarray, experts: int):

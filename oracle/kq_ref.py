@@ -43,6 +43,12 @@ class MoeWeightsF32(C.Structure):
                 for n, t in ((role, C.c_void_p), (role + "_count", C.c_uint64))]
 
 
+class RoutedExpertWeightsF32(C.Structure):
+    # include/kq_moe.h:91-98
+    _fields_ = [(n, t) for role in ("gate", "up", "down")
+                for n, t in ((role, C.c_void_p), (role + "_count", C.c_uint64))]
+
+
 class QuantBlockSpan(C.Structure):
     # include/kq_tensor_view.h:39-48
     _fields_ = [(n, C.c_uint64) for n in (
@@ -87,6 +93,8 @@ def lib() -> C.CDLL:
             "kq_moe_route_f32": [vp, vp, u64, vp, vp, u64, vp, u64, vp, u64, vp, u64, dp],
             "kq_moe_execute_f32": [vp, C.POINTER(MoeWeightsF32), vp, u64, vp, u64, vp, u64,
                                    vp, vp, vp, dp],
+            "kq_moe_execute_routed_expert_f32": [vp, C.POINTER(RoutedExpertWeightsF32), u32, vp,
+                                                 vp, u64, vp, u64, dp],
             "kq_quant_element_to_block": [u32, u64, u64, C.POINTER(u64), C.POINTER(u64), dp],
             "kq_quant_range_to_blocks": [u32, u64, u64, u64, C.POINTER(QuantBlockSpan), dp],
         }
@@ -95,6 +103,8 @@ def lib() -> C.CDLL:
             fn.argtypes = args
             fn.restype = C.c_int
         l.kq_moe_config_scratch_bytes.restype = C.c_uint64
+        l.kq_moe_config_one_expert_workspace_bytes.argtypes = [vp]
+        l.kq_moe_config_one_expert_workspace_bytes.restype = C.c_uint64
         l.kq_moe_config_close.argtypes = [vp]
         l.kq_moe_config_close.restype = None
         _lib = l
@@ -244,6 +254,24 @@ class MoeConfig:
         d = Diagnostic()
         _check(lib().kq_moe_execute_f32(self.h, C.byref(mw), _p(hidden), T, _p(out), out.size,
                                         _p(scratch), nbytes, None, None, None, C.byref(d)), d)
+        return out
+
+
+    def routed_expert(self, gate: np.ndarray, up: np.ndarray, down: np.ndarray, expert_id: int,
+                      x: np.ndarray) -> np.ndarray:
+        """kq_moe_execute_routed_expert_f32 on one expert's member matrices."""
+        H = self.dims[0]
+        keep = [np.ascontiguousarray(a, dtype=np.float32) for a in (gate, up, down)]
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = RoutedExpertWeightsF32(keep[0].ctypes.data, keep[0].size, keep[1].ctypes.data,
+                                   keep[1].size, keep[2].ctypes.data, keep[2].size)
+        out = np.empty(H, np.float32)
+        nbytes = lib().kq_moe_config_one_expert_workspace_bytes(self.h)
+        scratch = np.empty(max(1, nbytes), np.float32)
+        d = Diagnostic()
+        _check(lib().kq_moe_execute_routed_expert_f32(self.h, C.byref(w), expert_id, _p(x),
+                                                      _p(out), H, _p(scratch), nbytes,
+                                                      C.byref(d)), d)
         return out
 
 

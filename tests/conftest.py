@@ -49,11 +49,20 @@ TOL_RECORDS: list = []
 
 
 # Third stage of assert_close: the error against the binary64 value at most
-# this fraction of the element's term magnitude S (tests/exact.py).
-COND_TOL = 2.0 ** -20
+# this fraction of the element's term magnitude S (tests/exact.py): 2^-23 is
+# 2 u (u = 2^-24, binary32's unit roundoff), about 16 times the largest
+# ratio measured on the device over the GPU suite (7.5e-9).
+COND_TOL = 2.0 ** -23
+# Ceiling on the elements one call may pass through the second and third
+# stages together, as a fraction of its elements (at least FALLBACK_MIN):
+# the fallbacks are for the few elements where the oracle's own binary32
+# sum is off, not a second bar for a whole output.
+FALLBACK_FRAC = 0.005
+FALLBACK_MIN = 4
 
 
-def assert_close(got, ref, rtol=RTOL, atol=ATOL, exact=None, what=""):
+def assert_close(got, ref, rtol=RTOL, atol=ATOL, exact=None, what="", max_fallback=None,
+                 cond_tol=COND_TOL):
     """fp32-accumulated outputs, per element: |got - ref| <= atol OR
     |got - ref| <= rtol * |ref| (the reference's validator rule,
     tools/validate-native-moe.py:186-189, with the contract's 1e-4 absolute
@@ -66,13 +75,16 @@ def assert_close(got, ref, rtol=RTOL, atol=ATOL, exact=None, what=""):
       2. within the same bar of the exact value: the reference's own
          left-to-right binary32 sum is off there (a 2048-term row whose
          partial sums reach ~100 rounds each step by ~1e-6);
-      3. otherwise, where S is given: |got - exact| <= 2^-20 * S. At these
+      3. otherwise, where S is given: |got - exact| <= 2^-23 * S. At these
          elements the output is a near-cancellation of terms many times its
          size, where no binary32 evaluation meets the bar (the reference's
          own error against the exact value is recorded beside the device's).
          Binary32 rounding in any order stays near u * S (u = 2^-24); a
          wrong, missing or transposed term moves the element by about one
          term, above 1e-4 * S.
+    `cond_tol` replaces COND_TOL where a test states why its bar differs.
+    At most `max_fallback` elements (default: FALLBACK_FRAC of the elements,
+    at least FALLBACK_MIN) may take stages 2 and 3 together.
     Counts and the largest ratios of each stage are recorded."""
     import numpy as np
     got = np.asarray(got, np.float64)
@@ -91,6 +103,15 @@ def assert_close(got, ref, rtol=RTOL, atol=ATOL, exact=None, what=""):
     if ok.all():
         return rec
     bad = np.flatnonzero(~ok)
+    ceiling = max_fallback if max_fallback is not None else max(
+        FALLBACK_MIN, int(np.ceil(FALLBACK_FRAC * err.size)))
+    rec["fallback_ceiling"] = int(ceiling)
+    if bad.size > ceiling:
+        i = bad[:5]
+        raise AssertionError(
+            f"{bad.size} elements beyond 1e-4 abs / 1e-3 rel of the reference, more than the "
+            f"{ceiling} the exact-value fallbacks may take; first {i.tolist()}: got "
+            f"{got.flat[i]}, ref {ref.flat[i]}, err {err.flat[i]}")
     if exact is None:
         i = bad[:5]
         raise AssertionError(
@@ -120,11 +141,12 @@ def assert_close(got, ref, rtol=RTOL, atol=ATOL, exact=None, what=""):
                 "max_err_vs_exact_stage3": float(eg[~ok2].max()),
                 "ref_err_vs_exact_stage3": float(er[~ok2].max()),
                 "min_S_over_abs_exact": float((S3 / np.maximum(np.abs(ex[~ok2]), 1e-300)).min())})
-    if not (r3 <= COND_TOL).all():
-        j = np.flatnonzero(r3 > COND_TOL)[:5]
+    rec["cond_tol"] = float(cond_tol)
+    if not (r3 <= cond_tol).all():
+        j = np.flatnonzero(r3 > cond_tol)[:5]
         raise AssertionError(
-            f"{int((r3 > COND_TOL).sum())} elements beyond the bar against the reference and "
-            f"the exact value, and beyond 2^-20 of their term magnitude: indices "
+            f"{int((r3 > cond_tol).sum())} elements beyond the bar against the reference and "
+            f"the exact value, and beyond {cond_tol:.3g} of their term magnitude: indices "
             f"{b3[j].tolist()}, got {got.flat[b3[j]]}, exact {ex[~ok2][j]}, S {S3[j]}")
     return rec
 

@@ -202,8 +202,9 @@ def test_moe_repeated_calls_identical(ctx, layer):
                                                   ("Q5_K", "Q5_1", 3), ("IQ4_NL", "Q8_0", 1),
                                                   ("Q4_K", "IQ4_NL", 2), ("Q5_1", "Q5_K", 1)])
 def test_moe_small_formats(ctx, gate_fmt, down_fmt, T):
-    # Other gate/up and down formats at reduced dims, among them the
-    # reference model's own pair (Q5_K gate/up, Q5_1 routed down).
+    # Other gate/up and down formats at reduced dims. The reference model's
+    # layers use Q4_K gate/up with a Q5_1 routed down, and in layer 2 Q5_K
+    # gate/up with a Q8_0 routed down; the pairs here mix those formats.
     H, E, K, I = 512, 32, 4, 256
     seed = S.W_MOE + 7 + kq_hip.TYPE_IDS[gate_fmt] * 64 + kq_hip.TYPE_IDS[down_fmt]
     w = S.moe_weights(seed, H, E, I, I, gate_fmt=gate_fmt, down_fmt=down_fmt)

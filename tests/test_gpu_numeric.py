@@ -182,7 +182,14 @@ def test_matvec_f16_scale_every_finite_pattern(ctx):
     ctx.matvec(kq_hip.TYPE_Q8_0, dw, rows, cols, dx, 2, dy)
     got = ctx.download(dy, np.float32, rows * 2).reshape(2, rows)
     want = kq_oracle.matvec(kq_oracle.Q8_0, w, rows, cols, x)
-    assert_close(got, want, exact=exact.matvec(kq_oracle.Q8_0, w, rows, cols, x))
+    # The integer-dot lane stages each activation as a 22-bit integer of its
+    # 16-column group's largest magnitude m (error <= 2^-22 m), so at a
+    # near-cancellation the error is bounded by 2^-22 sum|w| m rather than
+    # by a multiple of u sum|w x|: 1.7e-7 S measured on this sweep of every
+    # binary16 scale, against 7.5e-9 S at most anywhere else. The stage-3
+    # bar here is 2^-21 S (a missing 32-column term is about S / 32).
+    assert_close(got, want, exact=exact.matvec(kq_oracle.Q8_0, w, rows, cols, x),
+                 cond_tol=2.0 ** -21)
     for b in (dw, dx, dy):
         b.close()
 

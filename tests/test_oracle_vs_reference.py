@@ -199,3 +199,18 @@ def test_gated_residual_read_bit_exact(B, H, rank, seed):
     got = O.gr_read(x, H, rank, 1e-6, norm, (O.F32, down), (O.F32, up), inject)
     for k in ("normalized", "read_gate", "mixed", "rank", "write_gate"):
         same_bits(got[k], want[k])
+
+
+@pytest.mark.parametrize("H,I,scale", [(2048, 512, 1.0), (96, 40, 3.0), (7, 3, 0.01)])
+def test_routed_expert_matches_reference(H, I, scale):
+    # kq_moe_execute_routed_expert_f32 (src/kq_moe_qwen38.c:461-566): the
+    # oracle's restatement bit for bit against the reference's own function
+    rng = np.random.default_rng(H + I)
+    g = (rng.standard_normal((I, H)) * 0.05 * scale).astype(np.float32)
+    u = (rng.standard_normal((I, H)) * 0.05 * scale).astype(np.float32)
+    d = (rng.standard_normal((H, I)) * 0.05 * scale).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    cfg = R.MoeConfig(H, 8, 2, I, 4)
+    want = cfg.routed_expert(g, u, d, 5, x)
+    cfg.close()
+    same_bits(O.moe_routed_expert(g, u, d, x), want)
