@@ -168,6 +168,34 @@ def time_steps(ctx, step, warmup: int, steps: int, graph: bool, flush: bool = Tr
     return ms / steps
 
 
+def time_each(ctx, step, warmup: int, steps: int) -> float:
+    """Mean duration of one launch on its own, in ms: a pair of HIP events
+    brackets every launch of `steps` consecutive ones (the same sequence as
+    time_steps, behind the same flush and hold). Each pair times the
+    dispatch with its start and completion, as a kernel trace does; the
+    spacing of back-to-back launches (time_steps) is shorter for short
+    kernels, whose start and end overheads overlap their neighbours'."""
+    stream = C.c_void_p(ctx.stream)
+    ctx.set_async(True)
+    for i in range(warmup):
+        step(i)
+    ctx.synchronize()
+    hcheck(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+    evs = [Events() for _ in range(steps)]
+    lead_in(ctx, True, steps)
+    for i in range(steps):
+        hcheck(hip().hipEventRecord(evs[i].a, stream), "hipEventRecord")
+        step(warmup + i)
+        hcheck(hip().hipEventRecord(evs[i].b, stream), "hipEventRecord")
+    ms = [e.ms() for e in evs]
+    hcheck(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+    for e in evs:
+        e.close()
+    ctx.synchronize()
+    ctx.set_async(False)
+    return float(np.mean(ms))
+
+
 def replicas(ctx, host: np.ndarray, want_bytes: int, cap: int = 256):
     """Bit-identical device copies of `host` at distinct addresses."""
     n = max(1, min(cap, -(-want_bytes // max(1, host.nbytes))))
@@ -191,23 +219,28 @@ def reuse_bytes(nrep: int, nbytes: int, steps: int, warm: bool = False):
 
 
 # ---------------------------------------------------------------- workloads
-def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph, warm=False):
+def wl_matvec(ctx, fmt, rows, cols, batch, warmup, steps, graph, warm=False, each=False):
     """warm: one weight copy, re-read every step from the caches (a
-    single-call latency with a warm cache, not an HBM rate)."""
+    single-call latency with a warm cache, not an HBM rate). each: also the
+    mean duration of one launch on its own (time_each)."""
     t = kq_hip.TYPE_IDS[fmt]
     w = S.quant_matrix(fmt, S.stream_key(S.W_MATVEC_Q4K, S.R_WEIGHT), rows, cols)
     x = S.normal_f32(S.stream_key(S.W_MATVEC_Q4K, S.R_X), batch * cols)
     reps = replicas(ctx, w, 0 if warm else MALL_DEFEAT_BYTES, cap=1 if warm else 256)
     dx, dy = ctx.upload(x), ctx.alloc(rows * batch * 4)
-    ms = time_steps(ctx, lambda i: ctx.matvec(t, reps[i % len(reps)], rows, cols, dx, batch, dy),
-                    warmup, steps, graph, flush=not warm)
+    step = lambda i: ctx.matvec(t, reps[i % len(reps)], rows, cols, dx, batch, dy)  # noqa: E731
+    ms = time_steps(ctx, step, warmup, steps, graph, flush=not warm)
     nbytes = w.nbytes + x.nbytes + rows * batch * 4
+    out = {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
+           "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "replicas": len(reps),
+           "bytes_between_reuse": reuse_bytes(len(reps), w.nbytes, steps, warm),
+           "flops_per_step": 2 * rows * cols * batch}
+    if each:
+        one = time_each(ctx, step, warmup, steps)
+        out.update({"dispatch_ms": one, "dispatch_GBps": nbytes / one / 1e6})
     for b in reps + [dx, dy]:
         b.close()
-    return {"ms_per_step": ms, "bytes_per_step": nbytes, "GBps": nbytes / ms / 1e6,
-            "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "replicas": len(reps),
-            "bytes_between_reuse": reuse_bytes(len(reps), w.nbytes, steps, warm),
-            "flops_per_step": 2 * rows * cols * batch}
+    return out
 
 
 def wl_dequant(ctx, fmt, warmup, steps, graph):
@@ -541,7 +574,7 @@ def main() -> int:
                 print(f"[bench] {name}: {json.dumps(work[name])}", file=sys.stderr, flush=True)
 
         HEADLINE = "q4k_matvec_4096x2048_b1"
-        run(HEADLINE, lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph))
+        run(HEADLINE, lambda: wl_matvec(ctx, "Q4_K", 4096, 2048, 1, W, K, graph, each=True))
         # what any launch costs, and a plain read of the headline's weight
         # bytes in one launch
         run("floor_empty_launch", lambda: wl_floor_empty(ctx, W, K, graph))
@@ -558,7 +591,8 @@ def main() -> int:
         # launch and the first-load latency (151 MB per step): the rate the
         # Q4_K row engine sustains
         run("q4k_matvec_131072x2048_b1",
-            lambda: wl_matvec(ctx, "Q4_K", 131072, 2048, 1, 10, max(10, K // 2), graph))
+            lambda: wl_matvec(ctx, "Q4_K", 131072, 2048, 1, 10, max(10, K // 2), graph,
+                              each=True))
         run("floor_read_150994944b",
             lambda: wl_floor_read(ctx, 150994944, (2, 4, 8), 10, max(10, K // 2), graph))
         run("floor_read_255252480b",
@@ -638,22 +672,32 @@ def main() -> int:
         "workloads": work,
     }
     if head:
-        # achieved: algorithmic bytes per launch / the launch's time from HIP
-        # events around the timed replay on the library's stream (the same
-        # figure as ms_per_step); traffic: FETCH_SIZE + WRITE_SIZE per
-        # dispatch from the committed counter runs
-        line["roofline"] = {"bound": "hbm", "achieved": round(head["GBps"], 2),
+        # achieved: algorithmic bytes per launch / the kernel's traced mean
+        # duration in the committed profile of this command (rocprofv3
+        # --kernel-trace); traffic: FETCH_SIZE + WRITE_SIZE per dispatch from
+        # the counter runs of the same profile. The HIP-event figures of this
+        # run sit beside it: the spacing of back-to-back launches (the
+        # throughput `value` reports) and the duration of one launch between
+        # its own pair of events.
+        prof = profile_figures(HEADLINE)
+        traced_us = prof.get("traced_avg_ns", 0) / 1e3 if prof else 0.0
+        kern_us = traced_us if traced_us > 0 else head["ms_per_step"] * 1e3
+        achieved = head["bytes_per_step"] / (kern_us * 1e3)
+        line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 2),
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(head["GBps"] / HBM_PEAK_GBS, 4),
-                            "traffic": traffic_from_profiles(HEADLINE),
-                            "kernel_us": round(head["ms_per_step"] * 1e3, 3),
-                            "time_source": "hip events around the timed replay of the K "
-                                           "launches, enqueued behind a hold kernel "
-                                           "(authoritative); "
-                                           "rocprofv3 durations in profiles/ include the "
-                                           "profiler's per-dispatch completion signal",
-                            "traffic_source": "profiles/traffic.json (rocprofv3 --pmc "
-                                              "FETCH_SIZE, WRITE_SIZE, scaled by a 64 MiB copy)"}
+                            "frac": round(achieved / HBM_PEAK_GBS, 4),
+                            "traffic": prof.get("hbm_bytes_per_launch") if prof else None,
+                            "kernel_us": round(kern_us, 3),
+                            "time_source": ("rocprofv3 kernel trace, mean duration of the kernel "
+                                            "(profiles/q4k_matvec_4096x2048_b1.md)"
+                                            if traced_us > 0 else
+                                            "hip events (no committed trace)"),
+                            "traffic_source": "the same profile's rocprofv3 --pmc FETCH_SIZE and "
+                                              "WRITE_SIZE runs, scaled by a 64 MiB copy",
+                            "hip_events": {
+                                "back_to_back_us": round(head["ms_per_step"] * 1e3, 3),
+                                "frac_back_to_back": round(head["hbm_frac"], 4),
+                                "one_launch_us": round(head.get("dispatch_ms", 0.0) * 1e3, 3)}}
         floors = {k: work[k]["ms_per_step"] * 1e3 for k in ("floor_empty_launch",
                                                              "floor_read_4718592b") if k in work}
         if floors:
@@ -680,14 +724,16 @@ def main() -> int:
     return 0
 
 
-def traffic_from_profiles(workload: str):
+def profile_figures(workload: str) -> dict:
+    """The committed profile figures of a workload (profiles/traffic.json):
+    traced mean kernel duration and HBM bytes per launch."""
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
-        return None
+        return {}
     try:
-        return json.loads(p.read_text()).get(workload, {}).get("hbm_bytes_per_launch")
+        return json.loads(p.read_text()).get(workload, {})
     except (ValueError, OSError):
-        return None
+        return {}
 
 
 if __name__ == "__main__":

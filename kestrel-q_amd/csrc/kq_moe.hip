@@ -1249,19 +1249,97 @@ struct GateupArgs {
 
 enum : uint32_t { kSegFirst = 1u, kSegLast = 2u };
 
+/* Gate/up + SwiGLU rows of one slot (matrices G and U: `rows` rows of
+ * `stride` bytes, columns [col0, col0 + COLS)) for one token, by wave
+ * `wave` of the `nwaves` working on the slot, in workgroups of NT threads.
+ * The caller has requested the token's activations into `stage` (issue());
+ * here every wave requests its first gate and up rows without a branch,
+ * then the activations are checked and written to the workgroup's LDS
+ * image behind an LDS-only barrier while the weights are in flight, and
+ * the check is flagged at the end. */
+template <uint32_t TYPE, uint32_t COLS, int RT, int NT>
+struct GateupEngine {
+    using R = kq::Rows<TYPE, COLS, 1, RT, typename kq::MatvecLane<TYPE, 1>::T>;
+    using Raw = typename R::Raw;
+    using XS = kq::StageFor<R, 1, NT>;
+    static constexpr uint32_t kImage = XS::NP; /* float4 words of the LDS image */
+
+    __device__ static __forceinline__ void run(const GateupArgs &a, const XS &stage, float4 *xs,
+                                               uint32_t slot, uint32_t t, const uint8_t *G,
+                                               const uint8_t *U, uint32_t rows, uint32_t stride,
+                                               uint32_t wave, uint32_t nwaves, uint32_t col0,
+                                               uint32_t seg) {
+        const uint32_t boff = kq::row_bytes<TYPE>(col0);
+        const uint32_t lane = threadIdx.x & 63u;
+        const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
+        const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
+        typename R::Lane ln;
+        ln.setup(l);
+        Raw rg[RT], ru[RT];
+        uint32_t g = wave;
+        const uint32_t wbytes = rows * stride - boff;
+        const KqBuf gb = kq_buf(G + boff, wbytes), ub = kq_buf(U + boff, wbytes);
+        R::load_group_oob(ln, gb, g, rows, sub, rg, stride, wbytes + 64u);
+        R::load_group_oob(ln, ub, g, rows, sub, ru, stride, wbytes + 64u);
+        const bool xbad = stage.commit(xs, threadIdx.x);
+        kq_lds_barrier();
+        stage.load(ln, xs, l);
+        bool bad = false, malformed = false;
+        const size_t at = (size_t)t * (a.top_k + 1u) + slot;
+        float *out = a.act + at * a.act_stride;
+        float *pg = a.part + at * 2u * a.act_stride, *pu = pg + a.act_stride;
+        for (; g < ngroups; g += nwaves) {
+            if (g != wave) {
+                R::load_group(ln, gb, g, rows, sub, rg, stride);
+                R::load_group(ln, ub, g, rows, sub, ru, stride);
+            }
+            float vg[R::N], vu[R::N];
+            R::dot_group(ln, rg, l, vg, malformed);
+            R::dot_group(ln, ru, l, vu, malformed);
+#pragma unroll
+            for (int j = 0; j < R::KEEP; ++j) {
+                const int idx = R::value_index(l, j);
+                if (idx >= 0) {
+                    const uint32_t row = g * R::GROUP + (uint32_t)idx * R::RPW + sub;
+                    if (row < rows) {
+                        float gv = vg[j], uv = vu[j];
+                        if (!(seg & kSegFirst)) {
+                            gv = pg[row] + gv;
+                            uv = pu[row] + uv;
+                        }
+                        if (seg & kSegLast) {
+                            const float r = kq_swiglu(gv, uv);
+                            bad |= !kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(r);
+                            out[row] = r;
+                        } else {
+                            pg[row] = gv;
+                            pu[row] = uv;
+                        }
+                    }
+                }
+            }
+        }
+        if (xbad) kq_flag(a.status, KQ_DEV_INPUT);
+        if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+        if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+    }
+};
+
 /* grid: x = row groups, y = slot - slot0 (slots 0..K-1 routed by top-k
  * position, K the shared expert), z = token. This launch covers columns
- * [col0, col0 + COLS) of every row. */
+ * [col0, col0 + COLS) of every row. The activations are requested before
+ * the routed expert's id is read. */
 template <uint32_t TYPE, uint32_t COLS, int RT>
 __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t slot0,
                                                           uint32_t col0, uint32_t seg) {
-    using R = kq::Rows<TYPE, COLS, 1, RT, typename kq::MatvecLane<TYPE, 1>::T>;
-    using Raw = typename R::Raw;
+    using E = GateupEngine<TYPE, COLS, RT, kThreads>;
+    __shared__ __align__(16) float4 xs[E::kImage];
     const uint32_t slot = blockIdx.y + slot0, t = blockIdx.z;
+    typename E::XS stage;
+    stage.issue(a.x + (size_t)t * a.hidden + col0, COLS, threadIdx.x);
     const bool shared = slot == a.top_k;
     const uint32_t rows = shared ? a.shared_inter : a.inter;
     const uint32_t stride = shared ? a.srstride : a.rstride;
-    const uint32_t boff = kq::row_bytes<TYPE>(col0);
     const uint8_t *G, *U;
     if (shared) {
         G = a.sgate;
@@ -1271,69 +1349,10 @@ __global__ __launch_bounds__(kThreads) void expert_gateup(GateupArgs a, uint32_t
         G = a.gate + (size_t)e * a.inter * stride;
         U = a.up + (size_t)e * a.inter * stride;
     }
-    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave =
         __builtin_amdgcn_readfirstlane((blockIdx.x * kThreads + threadIdx.x) >> 6);
     const uint32_t nwaves = (gridDim.x * kThreads) >> 6;
-    const uint32_t sub = lane / R::LPR, l = lane % R::LPR;
-    const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
-    typename R::Lane ln;
-    ln.setup(l);
-    Raw rg[RT], ru[RT];
-    uint32_t g = wave;
-    const uint32_t wbytes = rows * stride - boff;
-    const KqBuf gb = kq_buf(G + boff, wbytes), ub = kq_buf(U + boff, wbytes);
-    /* the workgroup requests the token's hidden state (once, into LDS),
-     * then every wave its first gate and up rows without a branch; the
-     * hidden state is checked and written to LDS behind an LDS-only barrier
-     * while the weights are in flight, and the check is flagged at the end */
-    using XS = kq::StageFor<R, 1, kThreads>;
-    __shared__ __align__(16) float4 xs[XS::NP];
-    XS stage;
-    stage.issue(a.x + (size_t)t * a.hidden + col0, COLS, threadIdx.x);
-    R::load_group_oob(ln, gb, g, rows, sub, rg, stride, wbytes + 64u);
-    R::load_group_oob(ln, ub, g, rows, sub, ru, stride, wbytes + 64u);
-    const bool xbad = stage.commit(xs, threadIdx.x);
-    kq_lds_barrier();
-    stage.load(ln, xs, l);
-    bool bad = false, malformed = false;
-    const size_t at = (size_t)t * (a.top_k + 1u) + slot;
-    float *out = a.act + at * a.act_stride;
-    float *pg = a.part + at * 2u * a.act_stride, *pu = pg + a.act_stride;
-    for (; g < ngroups; g += nwaves) {
-        if (g != wave) {
-            R::load_group(ln, gb, g, rows, sub, rg, stride);
-            R::load_group(ln, ub, g, rows, sub, ru, stride);
-        }
-        float vg[R::N], vu[R::N];
-        R::dot_group(ln, rg, l, vg, malformed);
-        R::dot_group(ln, ru, l, vu, malformed);
-#pragma unroll
-        for (int j = 0; j < R::KEEP; ++j) {
-            const int idx = R::value_index(l, j);
-            if (idx >= 0) {
-                const uint32_t row = g * R::GROUP + (uint32_t)idx * R::RPW + sub;
-                if (row < rows) {
-                    float gv = vg[j], uv = vu[j];
-                    if (!(seg & kSegFirst)) {
-                        gv = pg[row] + gv;
-                        uv = pu[row] + uv;
-                    }
-                    if (seg & kSegLast) {
-                        const float r = kq_swiglu(gv, uv);
-                        bad |= !kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(r);
-                        out[row] = r;
-                    } else {
-                        pg[row] = gv;
-                        pu[row] = uv;
-                    }
-                }
-            }
-        }
-    }
-    if (xbad) kq_flag(a.status, KQ_DEV_INPUT);
-    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
-    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+    E::run(a, stage, xs, slot, t, G, U, rows, stride, wave, nwaves, col0, seg);
 }
 
 /* -------------------------- down + combine -------------------------- */
