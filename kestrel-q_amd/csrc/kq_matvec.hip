@@ -193,6 +193,141 @@ __global__ __launch_bounds__(NT) void matvec_kernel(
     }
 }
 
+/* Rows wider than one engine width in one launch. A row of `cols` columns
+ * is NCH chunks of 2048 (the last one `tail` columns, a whole number of
+ * blocks). The workgroup stages every chunk's activations once (one LDS
+ * image per chunk); each wave keeps its lanes' partial dots of RT rows in
+ * registers while it walks the chunks, the next chunk's weights in flight
+ * while one is dotted, and reduces across the lanes once per row group.
+ * In the last chunk the lanes past `tail` read outside the buffer (zeros,
+ * whose scale is zero) against zero activations. The per-lane sums
+ * accumulate chunk by chunk, so the fp32 order differs from the
+ * per-segment launches (compared by tolerance like every row sum). */
+constexpr uint32_t kWideCols = 2048u;
+
+template <uint32_t TYPE, int B, int RT, int NT, uint32_t NCH>
+__global__ __launch_bounds__(NT) void matvec_wide(
+    const uint8_t *__restrict__ W, uint32_t rows, uint32_t row_bytes, uint32_t tail,
+    const float *__restrict__ x, uint32_t x_stride, float *y, uint32_t *status, float *part_v,
+    uint32_t *part_i, uint32_t part_stride) {
+    using R = kq::Rows<TYPE, kWideCols, B, RT, typename kq::MatvecLane<TYPE, B>::T>;
+    using Raw = typename R::Raw;
+    static_assert(R::LPR == 64u && R::RPW == 1u, "a 2048-column chunk takes the whole wave");
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave =
+        __builtin_amdgcn_readfirstlane((blockIdx.x * NT + threadIdx.x) >> 6);
+    const uint32_t nwaves = (gridDim.x * NT) >> 6;
+    const uint32_t ngroups = (rows + R::GROUP - 1u) / R::GROUP;
+    const uint32_t wbytes = (rows - 1u) * row_bytes + (NCH - 1u) * R::RB +
+                            kq::row_bytes<TYPE>(tail);
+    const uint32_t oob = wbytes + 64u;
+    const auto wb = kq_buf<(RT == 1 ? kKqNt : 0)>(W, wbytes);
+    /* lanes of the last chunk that hold columns */
+    const bool tail_lane = lane < tail / 32u;
+
+    typename R::Lane ln;
+    ln.setup(lane);
+    using XS = kq::StageFor<R, B, NT>;
+    __shared__ __align__(16) float4 xs[NCH][XS::NP];
+    /* chunk c of row group g: its RT rows, lanes past the tail outside */
+    auto load = [&](uint32_t g, uint32_t c, Raw (&raw)[RT]) {
+        const bool live = c + 1u < NCH || tail_lane;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint32_t row = g * R::GROUP + (uint32_t)r;
+            raw[r] = ln.load(wb, live && row < rows ? row * row_bytes + c * R::RB : oob);
+        }
+    };
+    Raw ra[RT], rb[RT];
+    uint32_t g = wave;
+    load(g, 0u, ra);
+    /* every chunk's activations requested before any is written to LDS */
+    XS stage[NCH];
+#pragma unroll
+    for (uint32_t c = 0; c < NCH; ++c)
+        stage[c].issue(x + c * kWideCols, x_stride, threadIdx.x,
+                       c + 1u < NCH ? kWideCols : tail);
+    bool xbad = false;
+#pragma unroll
+    for (uint32_t c = 0; c < NCH; ++c) xbad |= stage[c].commit(xs[c], threadIdx.x);
+    kq_lds_barrier();
+
+    bool bad = false, malformed = false;
+    float best_v[B];
+    uint32_t best_i[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        best_v[b] = -__builtin_inff();
+        best_i[b] = 0xffffffffu;
+    }
+    while (g < ngroups) {
+        float acc[R::N];
+#pragma unroll
+        for (int i = 0; i < R::N; ++i) acc[i] = 0.0f;
+        /* chunk c from ra (even) or rb (odd); chunk c + 1, or the next
+         * group's chunk 0, in flight meanwhile */
+#pragma unroll
+        for (uint32_t c = 0; c < NCH; ++c) {
+            Raw(&cur)[RT] = (c & 1u) ? rb : ra;
+            Raw(&nxt)[RT] = (c & 1u) ? ra : rb;
+            if (c + 1u < NCH)
+                load(g, c + 1u, nxt);
+            else
+                load(g + nwaves, 0u, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            stage[c].load(ln, xs[c], lane);
+            float v[R::NV];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) ln.dot(cur[r], &v[r * B], malformed);
+#pragma unroll
+            for (int i = 0; i < R::NV; ++i) acc[i] += v[i];
+        }
+        /* the next group's chunk 0 is in the register set chunk NCH used
+         * for its successor: move it to ra when NCH is odd (a wait for
+         * those loads; odd chunk counts are the narrow-row shapes, one
+         * group per wave) */
+        if constexpr (NCH % 2u == 1u) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) ra[r] = rb[r];
+        }
+        kq_group_reduce<64, R::N>(acc, lane);
+#pragma unroll
+        for (int j = 0; j < R::KEEP; ++j) {
+            const int idx = R::value_index(lane, j);
+            if (idx >= 0) {
+                const uint32_t r = (uint32_t)idx / B, b = (uint32_t)idx % B;
+                const uint32_t row = g * R::GROUP + r;
+                if (row < rows) {
+                    const float s = acc[j];
+                    y[(size_t)b * rows + row] = s;
+                    bad |= !kq_isfinite(s);
+                    argmax_merge(best_v[b], best_i[b], s, row);
+                }
+            }
+        }
+        g += nwaves;
+    }
+    if (xbad) kq_flag(status, KQ_DEV_INPUT);
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(status, KQ_DEV_NUMERIC);
+    if (part_v != nullptr) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float bv = best_v[b];
+            uint32_t bi = best_i[b];
+            wave_argmax(bv, bi);
+            if (lane == 0) {
+                part_v[(size_t)b * part_stride + wave] = bv;
+                part_i[(size_t)b * part_stride + wave] = bi;
+                for (uint32_t sl = wave + nwaves; sl < part_stride; sl += nwaves) {
+                    part_v[(size_t)b * part_stride + sl] = -__builtin_inff();
+                    part_i[(size_t)b * part_stride + sl] = 0xffffffffu;
+                }
+            }
+        }
+    }
+}
+
 /* ---- argmax over rows of logits (two stages) ---- */
 __global__ __launch_bounds__(kThreads) void argmax_partial(const float *__restrict__ logits,
                                                            uint32_t count, float *part_v,
@@ -364,6 +499,86 @@ hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t row
     }
 }
 
+/* One launch of matvec_wide over all rows (or, with waves set, only its
+ * wave count): like launch_one, one row group per wave for RT = 1, a
+ * resident striding grid for RT = 4. */
+template <uint32_t TYPE, int B, uint32_t NCH>
+hipError_t launch_wide_n(const uint8_t *W, uint32_t rows, uint32_t row_bytes, uint32_t tail,
+                         const float *x, uint32_t x_stride, float *y, uint32_t *st, float *pv,
+                         uint32_t *pi, uint32_t ps, hipStream_t s, uint32_t *waves) {
+    const uint32_t rt = pick_rt(rows, kWideCols);
+    const uint32_t threads = rt == 4u ? (uint32_t)kThreadsRt4 : (uint32_t)kThreadsRt1;
+    const uint32_t waves_per_block = threads / 64u;
+    const uint32_t groups = (rows + rt - 1u) / rt;
+    uint32_t blocks = (groups + waves_per_block - 1u) / waves_per_block;
+    if (rt == 4u) {
+        static const uint32_t resident =
+            resident_blocks(matvec_wide<TYPE, B, 4, kThreadsRt4, NCH>);
+        if (blocks > resident) blocks = resident;
+    }
+    if (blocks < 1u) blocks = 1u;
+    if (waves != nullptr) {
+        *waves = blocks * waves_per_block;
+        return hipSuccess;
+    }
+    if (rt == 4u)
+        hipLaunchKernelGGL((matvec_wide<TYPE, B, 4, kThreadsRt4, NCH>), dim3(blocks),
+                           dim3(threads), 0, s, W, rows, row_bytes, tail, x, x_stride, y, st, pv,
+                           pi, ps);
+    else
+        hipLaunchKernelGGL((matvec_wide<TYPE, B, 1, kThreadsRt1, NCH>), dim3(blocks),
+                           dim3(threads), 0, s, W, rows, row_bytes, tail, x, x_stride, y, st, pv,
+                           pi, ps);
+    return hipGetLastError();
+}
+
+/* chunk counts with an instance: 2 .. 5 at one batch column, 2 .. 3 at two,
+ * 2 at three (the LDS holds one activation image per chunk and column) */
+constexpr bool wide_shape(uint32_t nch, uint32_t batch) {
+    return batch == 1u ? (nch >= 2u && nch <= 5u)
+                       : batch == 2u ? (nch == 2u || nch == 3u) : batch == 3u && nch == 2u;
+}
+
+template <uint32_t TYPE>
+hipError_t launch_wide_t(uint32_t nch, uint32_t batch, const uint8_t *W, uint32_t rows,
+                         uint32_t row_bytes, uint32_t tail, const float *x, uint32_t x_stride,
+                         float *y, uint32_t *st, float *pv, uint32_t *pi, uint32_t ps,
+                         hipStream_t s, uint32_t *wv) {
+#define KQ_WIDE(BB, N)                                                                        \
+    if (batch == BB && nch == N)                                                              \
+    return launch_wide_n<TYPE, BB, N>(W, rows, row_bytes, tail, x, x_stride, y, st, pv, pi, ps, \
+                                      s, wv)
+    KQ_WIDE(1, 2u);
+    KQ_WIDE(1, 3u);
+    KQ_WIDE(1, 4u);
+    KQ_WIDE(1, 5u);
+    KQ_WIDE(2, 2u);
+    KQ_WIDE(2, 3u);
+    KQ_WIDE(3, 2u);
+#undef KQ_WIDE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_wide(uint32_t type, uint32_t nch, uint32_t batch, const uint8_t *W,
+                       uint32_t rows, uint32_t row_bytes, uint32_t tail, const float *x,
+                       uint32_t x_stride, float *y, uint32_t *st, float *pv, uint32_t *pi,
+                       uint32_t ps, hipStream_t s, uint32_t *wv) {
+    switch (type) {
+#define KQ_WIDE_T(T)                                                                          \
+    case T:                                                                                   \
+        return launch_wide_t<T>(nch, batch, W, rows, row_bytes, tail, x, x_stride, y, st, pv, \
+                                pi, ps, s, wv)
+        KQ_WIDE_T(KQ_LAUNCH_Q4_K);
+        KQ_WIDE_T(KQ_LAUNCH_Q6_K);
+        KQ_WIDE_T(KQ_LAUNCH_Q8_0);
+        KQ_WIDE_T(KQ_LAUNCH_Q5_K);
+        KQ_WIDE_T(KQ_LAUNCH_Q5_1);
+        KQ_WIDE_T(KQ_LAUNCH_IQ4_NL);
+#undef KQ_WIDE_T
+    default: return hipErrorInvalidValue;
+    }
+}
+
 /* block elements and bytes of the product formats (0 for others) */
 void block_geometry(uint32_t type, uint32_t &be, uint32_t &bb) {
     switch (type) {
@@ -410,6 +625,12 @@ hipError_t dispatch(uint32_t type, const void *W, uint32_t rows, uint32_t cols, 
     if (be == 0u || cols == 0u || cols % be != 0u) return hipErrorInvalidValue;
     const uint8_t *w = (const uint8_t *)W;
     const uint32_t row_bytes = cols / be * bb;
+    /* rows wider than one engine width: one launch when a chunk count has
+     * an instance */
+    const uint32_t nch = (cols + kWideCols - 1u) / kWideCols;
+    if (cols > kWideCols && wide_shape(nch, batch))
+        return launch_wide(type, nch, batch, w, rows, row_bytes, cols - (nch - 1u) * kWideCols, x,
+                           cols, y, status, pv, pi, ps, stream, wv);
     uint32_t off = 0u;
     while (off < cols) {
         const uint32_t seg = segment_cols(be, cols - off);

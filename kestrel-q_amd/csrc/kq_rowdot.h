@@ -1110,15 +1110,18 @@ struct XStage {
     static constexpr int NX = (int)((NP + (uint32_t)NT - 1u) / (uint32_t)NT);
     kq_u32x4 v[NX];
 
-    __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid) {
-        const uint32_t bytes = ((uint32_t)(B - 1) * stride + R::kCols) * 4u;
+    /* valid: the columns that exist (a row's last chunk may be shorter
+     * than kCols); the others stage as zeros */
+    __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid,
+                                          uint32_t valid = R::kCols) {
+        const uint32_t bytes = ((uint32_t)(B - 1) * stride + valid) * 4u;
         const KqBuf xb = kq_buf(x, bytes);
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
             const uint32_t b = p / (8u * LPR), c = (p / LPR) & 7u, l = p % LPR;
             const uint32_t k = R::Lane::xk(l, (int)c);
-            const uint32_t off = p < NP ? (b * stride + k) * 4u : bytes;
+            const uint32_t off = p < NP && k < valid ? (b * stride + k) * 4u : bytes;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(xb.r, (int)off, 0, 0);
         }
     }
@@ -1172,14 +1175,15 @@ struct XStageI {
     static_assert(NP == (uint32_t)B * 8u * LPR, "the image holds 8 slots per lane");
     kq_u32x4 v[NX];
 
-    __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid) {
-        const uint32_t bytes = ((uint32_t)(B - 1) * stride + R::kCols) * 4u;
+    __device__ __forceinline__ void issue(const float *x, uint32_t stride, uint32_t tid,
+                                          uint32_t valid = R::kCols) {
+        const uint32_t bytes = ((uint32_t)(B - 1) * stride + valid) * 4u;
         const KqBuf xb = kq_buf(x, bytes);
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             const uint32_t p = tid + (uint32_t)i * (uint32_t)NT;
             const uint32_t b = p / (R::kCols / 4u), k = (p % (R::kCols / 4u)) * 4u;
-            const uint32_t off = p < NQ ? (b * stride + k) * 4u : bytes;
+            const uint32_t off = p < NQ && k < valid ? (b * stride + k) * 4u : bytes;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(xb.r, (int)off, 0, 0);
         }
     }

@@ -269,6 +269,40 @@ def test_matvec_shapes(ctx, fmt, rows, cols, batch):
 
 
 @pytest.mark.parametrize("fmt", ALL_FMTS)
+@pytest.mark.parametrize("rows,cols,batch", [(37, 2304, 1), (300, 2560, 2), (5, 4096, 1),
+                                             (129, 6144, 1), (64, 10240, 1), (17, 6144, 2),
+                                             (9, 4352, 3), (4100, 2560, 1), (3, 12288, 1),
+                                             (16500, 2560, 1)])
+def test_matvec_wide_rows(ctx, fmt, rows, cols, batch):
+    # Rows wider than 2048 columns run as one launch over 2048-column chunks
+    # (the last one shorter: 256 .. 2048 columns), or as column segments
+    # where no chunk count has an instance (12288 columns, 3 x 4352):
+    # every format against the oracle
+    got, want, ex = matvec_case(ctx, fmt, rows, cols, batch,
+                                S.stream_key(S.W_MATVEC_Q6K, 77, rows * 64 + batch, cols // 256))
+    assert_close(got, want, exact=ex)
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K"])
+def test_lm_head_wide_rows_argmax(ctx, fmt):
+    # the LM head's argmax partials from the one-launch wide path
+    rows, cols, batch = 9000, 2560, 2
+    t = FMTS[fmt]
+    w = S.quant_matrix(fmt, S.stream_key(S.W_LM_HEAD, 78, t), rows, cols)
+    h = S.normal_f32(S.stream_key(S.W_LM_HEAD, 79, t), batch * cols).reshape(batch, cols)
+    dw, dh, dl, di = ctx.upload(w), ctx.upload(h), ctx.alloc(rows * batch * 4), ctx.alloc(batch * 4)
+    ctx.lm_head(t, dw, rows, cols, dh, batch, dl, di)
+    logits = ctx.download(dl, np.float32, rows * batch).reshape(batch, rows)
+    ids = ctx.download(di, np.uint32, batch)
+    want = kq_oracle.matvec(t, w, rows, cols, h, threads=oracle_threads())
+    assert_close(logits, want, exact=exact.matvec(t, w, rows, cols, h))
+    for b in range(batch):
+        assert ids[b] == kq_oracle.argmax(logits[b])
+    for buf in (dw, dh, dl, di):
+        buf.close()
+
+
+@pytest.mark.parametrize("fmt", ALL_FMTS)
 def test_matvec_activation_magnitudes(ctx, fmt):
     # activations over many binades, inside 16-column groups too (the Q4_K
     # matvec scales each group of 16 by one power of two before its integer
