@@ -261,19 +261,44 @@ def wl_dequant(ctx, fmt, warmup, steps, graph):
 
 
 # MoE layers measured: the configuration the headline MoE figures are quoted
-# on, and the reference model's own layer (hidden 2560, intermediate 640,
-# Q4_K gate/up, Q5_1 routed down, Q8_0 shared expert).
+# on, and the reference model's own layers (hidden 2560, intermediate 640,
+# Q4_K gate/up, Q5_1 routed down, Q8_0 shared expert; its layer 2 with Q5_K
+# gate/up and a Q8_0 routed down).
 MOE_LAYERS = {
     "2048x512": dict(H=2048, E=512, K=10, I=512, gate="Q4_K", down="Q6_K", sgate="Q4_K",
                      sdown="Q6_K", seed=S.W_MOE),
     "2560x640": dict(H=2560, E=512, K=10, I=640, gate="Q4_K", down="Q5_1", sgate="Q8_0",
                      sdown="Q8_0", seed=S.W_MOE + 2560),
+    "2560x640_l2": dict(H=2560, E=512, K=10, I=640, gate="Q5_K", down="Q8_0", sgate="Q8_0",
+                        sdown="Q8_0", seed=S.W_MOE + 2562),
 }
 
 
-def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512", block=False):
+def near_tie(router, x, K, c):
+    """x moved (least-norm, binary64) so that the K-th and (K+1)-th logits
+    by binary64 value are c times the sum of their certification bounds
+    apart (1.001 * 2^-24 * sum of |prefix sums| each)."""
+    r64, x64 = router.astype(np.float64), x.astype(np.float64)
+    a = r64 @ x64
+    order = np.argsort(-a, kind="stable")
+    hi, lo = order[K - 1], order[K]
+
+    def bound(e):
+        return 1.001 * 2.0 ** -24 * np.abs(np.cumsum((router[e] * x).astype(np.float64))).sum()
+    d = r64[hi] - r64[lo]
+    g = c * (bound(hi) + bound(lo))
+    return (x64 - ((a[hi] - a[lo] - g) / (d @ d)) * d).astype(np.float32)
+
+
+def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512", block=False,
+           inputs="random"):
     """block: the MoE block (4 residual branches, hyper-connection read with
-    rank-320 Q8_0 projections, MoE, write) instead of the bare MoE."""
+    rank-320 Q8_0 projections, MoE, write) instead of the bare MoE.
+    inputs (one token): "random" ~N(0,1) activations; "near_tie" the same
+    moved so that the selection's boundary pair is 1/4 of its certification
+    bounds apart (the refined route: exact chains of the contenders);
+    "all_tie" zero activations, every logit equal (the exact route: every
+    row's chain, then the route finish)."""
     L = MOE_LAYERS[layer]
     H, E, K, I = L["H"], L["E"], L["K"], L["I"]
     if layer_cache.get("layer") != layer:
@@ -326,6 +351,11 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512", blo
     ntok_inputs = 16
     x = S.normal_f32(S.stream_key(L["seed"], S.R_HIDDEN, 1000 + tokens),
                      ntok_inputs * tokens * width).reshape(ntok_inputs, tokens * width)
+    if inputs == "near_tie":
+        router = w["router"].reshape(E, H)
+        x = np.stack([near_tie(router, x[j], K, 0.25) for j in range(ntok_inputs)])
+    elif inputs == "all_tie":
+        x = np.zeros_like(x)
     dxs = [ctx.upload(x[j]) for j in range(ntok_inputs)]
     n = kq_hip.moe_block_scratch_bytes(gdims, cfg, tokens) if block else cfg.scratch_bytes(tokens)
     scratch = ctx.alloc(n)
@@ -343,6 +373,16 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512", blo
             ctx.moe_execute(cfg, mw[i % nrep], dxs[i % ntok_inputs], tokens, out, None, scratch,
                             n)
 
+    paths = None
+    if tokens == 1 and not block:
+        # the certification word (the workspace's last 256-byte slot): 1
+        # certified, 2 refined, 0 exact route
+        paths = {"certified": 0, "refined": 0, "exact": 0}
+        for j in range(ntok_inputs):
+            step(j)
+            ctx.synchronize()
+            f = int(ctx.download(scratch.ptr + n - 256, np.uint32, 1)[0])
+            paths[{1: "certified", 2: "refined"}.get(f, "exact")] += 1
     ms = time_steps(ctx, step, warmup, steps, graph)
     for bufs in layers:
         for b in bufs.values():
@@ -352,7 +392,8 @@ def wl_moe(ctx, tokens, warmup, steps, graph, layer_cache, layer="2048x512", blo
     nbytes = touched + 2 * tokens * width * 4
     return {"ms_per_step": ms, "tokens_per_s": tokens / ms * 1e3, "bytes_per_step": nbytes,
             "GBps": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-            "layer_replicas": nrep, "tokens": tokens, "layer": layer + ("+gr" if block else "")}
+            "layer_replicas": nrep, "tokens": tokens, "layer": layer + ("+gr" if block else ""),
+            **({"inputs": inputs, "route_paths": paths} if paths else {})}
 
 
 def wl_lm_head(ctx, batch, warmup, steps, graph, fmt="Q6_K", V=151936, H=2048):
@@ -607,6 +648,12 @@ def main() -> int:
                 lambda f=f: wl_dequant(ctx, f, 5, max(10, K // 4), graph))
         cache = {}
         run("moe_decode_1tok", lambda: wl_moe(ctx, 1, W, K, graph, cache))
+        # the same layer on tokens the bounds cannot certify: the refined
+        # route and the exact route
+        run("moe_decode_1tok_near_tie",
+            lambda: wl_moe(ctx, 1, W, K, graph, cache, inputs="near_tie"))
+        run("moe_decode_1tok_all_tie",
+            lambda: wl_moe(ctx, 1, W, K, graph, cache, inputs="all_tie"))
         # the large workloads run 100 / 10 timed steps (several ms): shorter
         # timed regions read up to 10% slower per step
         run("lm_head_q6k_151936x2048_b1",
@@ -636,6 +683,11 @@ def main() -> int:
             lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640", block=True))
         run("moe_block_prefill_512_4x2560",
             lambda: wl_moe(ctx, 512, 1, max(3, K // 40), graph, cache, "2560x640", block=True))
+        # the reference model's layer 2 (Q5_K gate/up, Q8_0 routed down)
+        run("moe_prefill_512_2560x640_l2",
+            lambda: wl_moe(ctx, 512, 1, max(3, K // 40), graph, cache, "2560x640_l2"))
+        run("moe_decode_1tok_2560x640_l2",
+            lambda: wl_moe(ctx, 1, W, K, graph, cache, "2560x640_l2"))
         if "hbm_copy_64mb" in names:
             run("hbm_copy_64mb", lambda: wl_copy(ctx, 64 << 20, W, K, graph))
     head = work.get(HEADLINE)

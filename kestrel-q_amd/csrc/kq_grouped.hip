@@ -1593,11 +1593,16 @@ hipError_t launch_down_q6k(const uint8_t *W0, const uint8_t *SW0, const float *X
 extern "C" int kq_launch_moe_grouped_supported(const kq_launch_moe_dims *d,
                                                const kq_launch_moe_weights *w) {
     /* gate/up in Q4_K (the 6-bit scales fold into exact fp16 weights) or
-     * Q8_0; down in Q4_K, Q6_K, Q5_1 or Q8_0; routed and shared each of
-     * their own format, at the row lengths each pass is built for */
+     * Q8_0, or Q5_K through the LDS pass (a Q5_K shared expert only with
+     * Q5_K routed experts, in the same pass); down in Q4_K, Q6_K, Q5_1 or
+     * Q8_0; routed and shared each of their own format, at the row lengths
+     * each pass is built for */
+    const bool q5 = w->gate_type == KQ_LAUNCH_Q5_K &&
+                    kq_launch_gu_lds_supported(KQ_LAUNCH_Q5_K, d->hidden);
     return w->up_type == w->gate_type && w->shared_up_type == w->shared_gate_type &&
-           pass_dim_rt(w->gate_type, 2, d->hidden) &&
-           pass_dim_rt(w->shared_gate_type, 2, d->hidden) &&
+           (pass_dim_rt(w->gate_type, 2, d->hidden) || q5) &&
+           (pass_dim_rt(w->shared_gate_type, 2, d->hidden) ||
+            (q5 && w->shared_gate_type == KQ_LAUNCH_Q5_K)) &&
            pass_dim_rt(w->down_type, 1, d->inter) &&
            pass_dim_rt(w->shared_down_type, 1, d->inter) && d->inter == d->shared_inter &&
            d->experts <= 1023u;
@@ -1614,7 +1619,7 @@ extern "C" hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens
 }
 
 static bool gu_lds_routed(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w) {
-    return w->gate_type == KQ_LAUNCH_Q4_K && kq_launch_gu_lds_supported(d->hidden);
+    return kq_launch_gu_lds_supported(w->gate_type, d->hidden) != 0;
 }
 
 extern "C" void *kq_launch_moe_grouped_stage(const kq_launch_moe_dims *d,
@@ -1628,12 +1633,12 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
                                             uint32_t tokens, const kq_launch_moe_ws *ws,
                                             int staged, float *out, uint32_t *status,
                                             hipStream_t s) {
-    /* Q4_K gate/up rows stream through LDS (kq_grouped_gu.hip) from
+    /* Q4_K and Q5_K gate/up rows stream through LDS (kq_grouped_gu.hip) from
      * activations split once per token into the start of outp, which only
      * the down pass writes later; the work list the permutation builds for
      * it (gitems) also drives the Q6_K down pass (kq_grouped_dn.hip) */
     const bool lds_routed = gu_lds_routed(d, w);
-    const bool lds_shared = lds_routed && w->shared_gate_type == KQ_LAUNCH_Q4_K;
+    const bool lds_shared = lds_routed && w->shared_gate_type == w->gate_type;
     hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ws->ids, tokens, d->top_k,
                        d->experts, ws->offsets, ws->perm_tok, ws->pos, nullptr, status,
                        lds_routed ? (uint32_t *)ws->gitems : nullptr, lds_shared ? 1u : 0u);
@@ -1650,9 +1655,9 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
         if (e != hipSuccess) return e;
     }
     if (lds_routed) {
-        e = kq_launch_gu_lds(d->hidden, g, u, sg, su, ws->outp, ws->offsets, ws->perm_tok, E,
-                             tokens, d->top_k, d->inter, lds_shared ? 1 : 0, 1, ws->gitems,
-                             ws->act, status, s);
+        e = kq_launch_gu_lds(w->gate_type, d->hidden, g, u, sg, su, ws->outp, ws->offsets,
+                             ws->perm_tok, E, tokens, d->top_k, d->inter, lds_shared ? 1 : 0, 1,
+                             ws->gitems, ws->act, status, s);
         if (e == hipSuccess && !lds_shared && w->shared_gate_type == KQ_LAUNCH_Q8_0 &&
             kq_launch_dense_q8_supported(d->inter, d->hidden, tokens)) {
             /* a Q8_0 shared expert sees every token: the dense product on

@@ -1,6 +1,7 @@
 /*
- * kq_grouped_gu.hip — the prefill gate/up + SwiGLU pass of Q4_K experts with
- * the weights streamed into LDS by direct (LDS-DMA) buffer loads.
+ * kq_grouped_gu.hip — the prefill gate/up + SwiGLU pass of Q4_K and Q5_K
+ * experts with the weights streamed into LDS by direct (LDS-DMA) buffer
+ * loads.
  *
  * The reference computes g = Wg x, u = Wu x and a = swiglu(g, u) for every
  * (token, selected expert) pair one token at a time
@@ -31,10 +32,18 @@
  *
  * Activations come pre-split from gu_stage: per token, the row scaled by
  * 2^sig (largest magnitude in [2^14, 2^15)), as fp16 hi + lo, and the
- * 32-column sums of the scaled row times 2^-5 (also hi + lo) for the Q4_K
+ * 32-column sums of the scaled row times 2^-5 (also hi + lo) for the
  * min term. The arithmetic per block is the grouped pass's: the 6-bit
  * sub-block scale folds into exact fp16 weights, d scales the fp32 MFMA
  * result, dmin * m is a small MFMA against the sums.
+ *
+ * Q5_K (176-byte blocks: d, dmin, the same 12 scale bytes, 32 bytes qh of
+ * fifth bits, 128 bytes qs of low nibbles; src/kq_numeric.c) differs from
+ * Q4_K (144 bytes: d, dmin, scales, qs) only in the code: byte l of the
+ * 32-byte qs run of sub-block pair p holds weights 64 p + l (low nibble)
+ * and 64 p + 32 + l (high nibble), whose fifth bits are bits 2 p and
+ * 2 p + 1 of qh[l] (src/kq_numeric.c:223-270). The five-bit code q <= 31
+ * times the scale s <= 63 is at most 1953, still exact in fp16.
  *
  * The LDS-DMA loads are issued from inline assembly, so the compiler's
  * memory-counter bookkeeping never waits on them; the pass waits for them
@@ -120,22 +129,29 @@ __global__ __launch_bounds__(256) void gu_stage(const float *__restrict__ X, uin
 /* ------------------------------------------------------------------ */
 /* the pass */
 
-/* LDS shape for rows of NB Q4_K blocks, WPB waves per block (2: one
- * matrix per wave; 1: gate and up in one wave) */
-template <uint32_t NB, uint32_t WPB>
+/* LDS shape for rows of NB blocks of format FMT (Q4_K or Q5_K), WPB waves
+ * per block (2: one matrix per wave; 1: gate and up in one wave) */
+template <uint32_t FMT, uint32_t NB, uint32_t WPB>
 struct GuShape {
+    static_assert(FMT == KQ_LAUNCH_Q4_K || FMT == KQ_LAUNCH_Q5_K, "format");
+    static constexpr bool Q5 = FMT == KQ_LAUNCH_Q5_K;
+    static constexpr uint32_t BB = Q5 ? 176u : 144u;         /* block bytes */
+    static constexpr uint32_t CB = BB / 16u;                /* 16-byte chunks per block */
+    static constexpr uint32_t QS = Q5 ? 48u : 16u;          /* offset of qs in a block */
     static constexpr uint32_t W = NB * WPB;                 /* waves */
-    static constexpr uint32_t RB = 144u * NB;               /* row bytes */
+    static constexpr uint32_t RB = BB * NB;                 /* row bytes */
     static constexpr uint32_t CH = RB / 16u;                /* 16-byte chunks per row */
     static constexpr uint32_t PITCH = (CH & 1u) ? CH : CH + 1u; /* odd: conflict-free rows */
     static constexpr uint32_t SLOTS = kT * PITCH;           /* chunk slots per matrix tile */
     static constexpr uint32_t IM = (SLOTS + 63u) / 64u;     /* instructions per matrix tile */
     static constexpr uint32_t LPW = (2u * IM + W - 1u) / W; /* loads per wave per tile */
     static constexpr uint32_t ENTRY = 2u * IM * 1024u;      /* bytes per ring entry */
-    static constexpr uint32_t RING = NB <= 8u ? 3u : 2u;
-    static constexpr uint32_t PD = RING - 1u;                /* tiles in flight ahead */
     static constexpr uint32_t PART = NB * 2u * 4u * 64u;     /* floats per partial buffer */
-    static constexpr uint32_t LDS = RING * ENTRY + 1024u + 2u * PART * 4u;
+    static constexpr uint32_t FIXED = 1024u + 2u * PART * 4u;
+    /* three tiles in the ring where they fit, else two */
+    static constexpr uint32_t RING = 3u * ENTRY + FIXED <= 160u * 1024u ? 3u : 2u;
+    static constexpr uint32_t PD = RING - 1u;                /* tiles in flight ahead */
+    static constexpr uint32_t LDS = RING * ENTRY + FIXED;
     static_assert(LDS <= 160u * 1024u, "LDS");
     static_assert(W <= 16u, "workgroup size");
 };
@@ -211,9 +227,9 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0f7
  * N = items x tiles-per-item sequence, so every workgroup streams the same
  * number of tiles, and its ring keeps running across item boundaries; only
  * the activation operand is reloaded when the item changes. */
-template <uint32_t NB, uint32_t WPB>
-__global__ __launch_bounds__(NB * WPB * 64) void gu_q4k(GuArgs a) {
-    using S = GuShape<NB, WPB>;
+template <uint32_t FMT, uint32_t NB, uint32_t WPB>
+__global__ __launch_bounds__(NB * WPB * 64) void gu_kq(GuArgs a) {
+    using S = GuShape<FMT, NB, WPB>;
     constexpr uint32_t KD = 256u * NB;
     __shared__ __align__(16) uint8_t ring[S::RING * S::ENTRY];
     __shared__ __align__(16) uint8_t trash[1024]; /* landing place of the padding loads */
@@ -374,14 +390,20 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_q4k(GuArgs a) {
         const uint8_t *ent = ring + cslot * S::ENTRY;
         rtile = ctile++;
         cslot = cslot + 1u == S::RING ? 0u : cslot + 1u;
-            uint4 hd[NM], qa[NM], qb[NM];
+            uint4 hd[NM], qa[NM], qb[NM], ha[NM], hb[NM];
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
                 const uint32_t mat = WPB == 2u ? mw : (uint32_t)m;
-                const uint8_t *rowp = ent + mat * S::IM * 1024u + (j * S::PITCH + 9u * b) * 16u;
+                const uint8_t *rowp =
+                    ent + mat * S::IM * 1024u + (j * S::PITCH + S::CB * b) * 16u;
                 hd[m] = *(const uint4 *)rowp;
-                qa[m] = *(const uint4 *)(rowp + 16u + 32u * g);
-                qb[m] = *(const uint4 *)(rowp + 32u + 32u * g);
+                qa[m] = *(const uint4 *)(rowp + S::QS + 32u * g);
+                qb[m] = *(const uint4 *)(rowp + S::QS + 16u + 32u * g);
+                if constexpr (S::Q5) {
+                    /* qh[0..15], qh[16..31]: the fifth bits of every qs byte */
+                    ha[m] = *(const uint4 *)(rowp + 16u);
+                    hb[m] = *(const uint4 *)(rowp + 32u);
+                }
             }
             float d[NM], dm[NM];
             h2 S0[NM], C0[NM], S1[NM], C1[NM];
@@ -401,8 +423,15 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_q4k(GuArgs a) {
                 const _Float16 fs0 = (_Float16)(float)s0, fs1 = (_Float16)(float)s1;
                 S0[m] = h2{fs0, fs0};
                 C0[m] = S0[m] * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
-                S1[m] = h2{fs1, fs1} * h2{(_Float16)0.0625f, (_Float16)0.0625f};
-                C1[m] = h2{fs1, fs1} * h2{(_Float16)-64.0f, (_Float16)-64.0f};
+                if constexpr (S::Q5) {
+                    /* both halves as whole five-bit codes: (1024 + q) s - 1024 s */
+                    S1[m] = h2{fs1, fs1};
+                    C1[m] = S1[m] * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+                } else {
+                    /* high nibbles as 16 q: (1024 + 16 q) s / 16 - 64 s */
+                    S1[m] = h2{fs1, fs1} * h2{(_Float16)0.0625f, (_Float16)0.0625f};
+                    C1[m] = h2{fs1, fs1} * h2{(_Float16)-64.0f, (_Float16)-64.0f};
+                }
                 /* mins m_4g .. m_4g+3 for g < 2; zero for g >= 2 */
                 const uint32_t mq = g == 0u ? (hd[m].z & 0x3f3f3f3fu)
                                             : (((hd[m].w >> 4) & 0x0f0f0f0fu) |
@@ -423,8 +452,22 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_q4k(GuArgs a) {
                 for (int m = 0; m < NM; ++m) {
                     const uint4 &qd = (s & 2u) ? qb[m] : qa[m];
                     const uint32_t raw0 = (s & 1u) ? qd.z : qd.x, raw1 = (s & 1u) ? qd.w : qd.y;
-                    const uint32_t m0 = s < 4u ? kq_and_0f(raw0) : kq_and_f0(raw0);
-                    const uint32_t m1 = s < 4u ? kq_and_0f(raw1) : kq_and_f0(raw1);
+                    uint32_t m0, m1;
+                    if constexpr (S::Q5) {
+                        /* nibble | fifth bit << 4 per byte: the bit of qh[l]
+                         * for sub-block 2 g (low nibbles) or 2 g + 1 (high),
+                         * moved to bit 4 */
+                        const uint4 &hq = (s & 2u) ? hb[m] : ha[m];
+                        const uint32_t h0 = (s & 1u) ? hq.z : hq.x, h1 = (s & 1u) ? hq.w : hq.y;
+                        const uint32_t sh = s < 4u ? 2u * g : 2u * g + 1u;
+                        const uint32_t n0 = s < 4u ? raw0 : raw0 >> 4;
+                        const uint32_t n1 = s < 4u ? raw1 : raw1 >> 4;
+                        m0 = (n0 & 0x0f0f0f0fu) | (((h0 >> sh) & 0x01010101u) << 4);
+                        m1 = (n1 & 0x0f0f0f0fu) | (((h1 >> sh) & 0x01010101u) << 4);
+                    } else {
+                        m0 = s < 4u ? kq_and_0f(raw0) : kq_and_f0(raw0);
+                        m1 = s < 4u ? kq_and_0f(raw1) : kq_and_f0(raw1);
+                    }
                     const h2 Sc = s < 4u ? S0[m] : S1[m], Cc = s < 4u ? C0[m] : C1[m];
                     const h2 w0 = fma2(byte_pair_lo(m0), Sc, Cc), w1 = fma2(byte_pair_hi(m0), Sc, Cc);
                     const h2 w2 = fma2(byte_pair_lo(m1), Sc, Cc), w3 = fma2(byte_pair_hi(m1), Sc, Cc);
@@ -451,14 +494,13 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_q4k(GuArgs a) {
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
-/* waves per block: one per matrix where the workgroup stays within 16
- * waves and the registers within 128 */
+/* waves per block: one (gate and up in one wave) */
 template <uint32_t NB>
 constexpr uint32_t gu_wpb() {
     return 1u;
 }
 
-template <uint32_t NB>
+template <uint32_t FMT, uint32_t NB>
 hipError_t launch_gu(const GuArgs &a, hipStream_t s) {
     constexpr uint32_t WPB = gu_wpb<NB>();
     static int cus = 0;
@@ -470,15 +512,16 @@ hipError_t launch_gu(const GuArgs &a, hipStream_t s) {
             cus = 256;
     }
     /* one workgroup per CU: the LDS ring holds one */
-    hipLaunchKernelGGL((gu_q4k<NB, WPB>), dim3((uint32_t)cus), dim3(NB * WPB * 64), 0, s, a);
+    hipLaunchKernelGGL((gu_kq<FMT, NB, WPB>), dim3((uint32_t)cus), dim3(NB * WPB * 64), 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
-extern "C" int kq_launch_gu_lds_supported(uint32_t hidden) {
-    return hidden == 256u || hidden == 512u || hidden == 1024u || hidden == 2048u ||
-           hidden == 2560u;
+extern "C" int kq_launch_gu_lds_supported(uint32_t type, uint32_t hidden) {
+    return (type == KQ_LAUNCH_Q4_K || type == KQ_LAUNCH_Q5_K) &&
+           (hidden == 256u || hidden == 512u || hidden == 1024u || hidden == 2048u ||
+            hidden == 2560u);
 }
 
 extern "C" uint64_t kq_launch_gu_stage_bytes(uint32_t tokens, uint32_t hidden) {
@@ -504,14 +547,15 @@ extern "C" uint64_t kq_launch_gu_items_bytes(uint32_t experts, uint32_t tokens,
 /* the routed experts' chunks (and the shared expert's when with_shared)
  * of a permutation (offsets) as the pass's work list, then the pass over
  * it; items holds kq_launch_gu_items_bytes */
-extern "C" hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const void *up,
+extern "C" hipError_t kq_launch_gu_lds(uint32_t type, uint32_t hidden, const void *gate,
+                                       const void *up,
                                        const void *shared_gate, const void *shared_up,
                                        const void *staged, const uint32_t *offsets,
                                        const uint32_t *perm_tok, uint32_t experts,
                                        uint32_t tokens, uint32_t top_k, uint32_t rows,
                                        int with_shared, int items_ready, void *items,
                                        float *act, uint32_t *status, hipStream_t s) {
-    if (experts > 1023u) return hipErrorInvalidValue;
+    if (experts > 1023u || !kq_launch_gu_lds_supported(type, hidden)) return hipErrorInvalidValue;
     uint32_t *n_items = (uint32_t *)items;
     uint32_t *list = n_items + 4;
     if (!items_ready) {
@@ -534,12 +578,18 @@ extern "C" hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const 
     a.rows = rows;
     a.act = act;
     a.status = status;
-    switch (hidden) {
-    case 256: return launch_gu<1>(a, s);
-    case 512: return launch_gu<2>(a, s);
-    case 1024: return launch_gu<4>(a, s);
-    case 2048: return launch_gu<8>(a, s);
-    case 2560: return launch_gu<10>(a, s);
-    default: return hipErrorInvalidValue;
+#define KQ_GU_HIDDEN(F)                               \
+    switch (hidden) {                                 \
+    case 256: return launch_gu<F, 1>(a, s);           \
+    case 512: return launch_gu<F, 2>(a, s);           \
+    case 1024: return launch_gu<F, 4>(a, s);          \
+    case 2048: return launch_gu<F, 8>(a, s);          \
+    case 2560: return launch_gu<F, 10>(a, s);         \
+    default: return hipErrorInvalidValue;             \
     }
+    if (type == KQ_LAUNCH_Q5_K) {
+        KQ_GU_HIDDEN(KQ_LAUNCH_Q5_K)
+    }
+    KQ_GU_HIDDEN(KQ_LAUNCH_Q4_K)
+#undef KQ_GU_HIDDEN
 }

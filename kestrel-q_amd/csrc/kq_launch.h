@@ -185,17 +185,18 @@ hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens, uint32_t 
                                  uint32_t experts, uint32_t *offsets, uint32_t *pair_token,
                                  uint32_t *pos, uint32_t *pair_slot, uint32_t *status,
                                  hipStream_t stream);
-/* prefill gate/up of Q4_K experts through LDS (kq_grouped_gu.hip): the
- * per-token activation split, then the pass over the routed experts'
- * 16-token chunks (and the shared expert's, with_shared) on a persistent
- * grid; items is scratch of kq_launch_gu_items_bytes */
-int kq_launch_gu_lds_supported(uint32_t hidden);
+/* prefill gate/up of Q4_K or Q5_K experts (type) through LDS
+ * (kq_grouped_gu.hip): the per-token activation split, then the pass over
+ * the routed experts' 16-token chunks (and the shared expert's,
+ * with_shared, in the same format) on a persistent grid; items is scratch
+ * of kq_launch_gu_items_bytes */
+int kq_launch_gu_lds_supported(uint32_t type, uint32_t hidden);
 uint64_t kq_launch_gu_stage_bytes(uint32_t tokens, uint32_t hidden);
 hipError_t kq_launch_gu_stage(const float *hidden_states, uint32_t tokens, uint32_t hidden,
                               void *staged, uint32_t *status, hipStream_t s);
 uint64_t kq_launch_gu_items_bytes(uint32_t experts, uint32_t tokens, uint32_t top_k);
 /* items_ready: the permutation already wrote the item list (moe_permute) */
-hipError_t kq_launch_gu_lds(uint32_t hidden, const void *gate, const void *up,
+hipError_t kq_launch_gu_lds(uint32_t type, uint32_t hidden, const void *gate, const void *up,
                             const void *shared_gate, const void *shared_up, const void *staged,
                             const uint32_t *offsets, const uint32_t *perm_tok, uint32_t experts,
                             uint32_t tokens, uint32_t top_k, uint32_t rows, int with_shared,
@@ -215,7 +216,7 @@ hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const void *down,
                             const void *shared_down, const float *act, uint32_t tokens,
                             uint32_t top_k, const void *items, void *staged, float *out,
                             uint32_t *status, hipStream_t s);
-/* where the Q4_K gate/up pass reads its per-token activation split (ws's
+/* where the Q4_K / Q5_K gate/up pass reads its per-token activation split (ws's
  * outp), or NULL when these weights take another pass; the route can form
  * it (kq_launch_moe_route's stage), and staged tells the grouped path so */
 void *kq_launch_moe_grouped_stage(const kq_launch_moe_dims *d, const kq_launch_moe_weights *w,

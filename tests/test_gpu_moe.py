@@ -584,17 +584,23 @@ def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
     assert_close(out, ref, exact=ex)
 
 
-# grouped (MFMA) prefill with every format pair the passes take: Q8_0 and
-# Q4_K gate/up (2560 columns staged in two slices), Q5_1, Q8_0, Q6_K and
-# Q4_K down (640-column rows of 128-column units), routed and shared of
-# different formats (two launches per role)
+# grouped (MFMA) prefill with every format pair the passes take: Q8_0,
+# Q4_K and Q5_K gate/up (2560 columns staged in two slices, or streamed
+# through LDS), Q5_1, Q8_0, Q6_K and Q4_K down (640-column rows of
+# 128-column units), routed and shared of different formats (two launches
+# per role)
 @pytest.mark.parametrize("H,E,K,I,T,g,d,sg,sd", [
     (2560, 64, 8, 640, 40, "Q4_K", "Q5_1", "Q8_0", "Q8_0"),
     (2560, 32, 4, 640, 37, "Q8_0", "Q8_0", "Q8_0", "Q8_0"),
     (1024, 24, 3, 640, 37, "Q4_K", "Q5_1", "Q4_K", "Q5_1"),
     (2048, 24, 3, 512, 37, "Q8_0", "Q6_K", "Q4_K", "Q4_K"),
     (512, 16, 4, 640, 20, "Q4_K", "Q8_0", "Q8_0", "Q5_1"),
-], ids=["ref-formats-40tok", "q8_0-2560", "q5_1-640", "mixed-q6k-lds", "q8_0-q5_1-down"])
+    (2560, 64, 8, 640, 40, "Q5_K", "Q8_0", "Q8_0", "Q8_0"),
+    (2048, 24, 3, 512, 37, "Q5_K", "Q6_K", "Q5_K", "Q6_K"),
+    (1024, 24, 3, 640, 37, "Q5_K", "Q5_1", "Q4_K", "Q5_1"),
+    (256, 16, 4, 256, 33, "Q5_K", "Q4_K", "Q5_K", "Q8_0"),
+], ids=["ref-formats-40tok", "q8_0-2560", "q5_1-640", "mixed-q6k-lds", "q8_0-q5_1-down",
+        "layer2-formats-40tok", "q5k-q6k-lds", "q5k-q4k-shared", "q5k-256"])
 def test_moe_prefill_grouped_formats(ctx, H, E, K, I, T, g, d, sg, sd):
     seed = S.W_MOE + 5000 + H + I + T
     w = S.moe_weights(seed, H, E, I, I, gate_fmt=g, down_fmt=d, shared_gate_fmt=sg,
@@ -630,6 +636,17 @@ def test_moe_reference_model_prefill_512(ctx):
     say("reference-model layer prefill, 512 tokens")
     out, ids, ref, tr, ex = run_layer(ctx, 2560, 512, 10, 640, 512, "Q4_K", "Q5_1", "Q8_0",
                                       "Q8_0", S.W_MOE + 2561)
+    assert np.array_equal(ids, tr["selected_ids"])
+    assert_close(out, ref, exact=ex)
+
+
+def test_moe_reference_model_layer2_prefill_512(ctx):
+    # The reference model's layer 2 (blk.2: Q5_K gate/up, Q8_0 routed down,
+    # Q8_0 shared expert; 2560 / 512 experts / top-10 / 640) over 512
+    # tokens: the Q5_K rows through the LDS gate/up pass
+    say("reference-model layer 2 prefill, 512 tokens")
+    out, ids, ref, tr, ex = run_layer(ctx, 2560, 512, 10, 640, 512, "Q5_K", "Q8_0", "Q8_0",
+                                      "Q8_0", S.W_MOE + 2562)
     assert np.array_equal(ids, tr["selected_ids"])
     assert_close(out, ref, exact=ex)
 
