@@ -399,6 +399,38 @@ uint32_t pick_rt(uint32_t rows, uint32_t cols) {
 constexpr int kThreadsRt1 = 512;
 constexpr int kThreadsRt4 = 256;
 
+/* Between the two, for one activation column: two rows per wave on a grid
+ * of two 256-thread workgroups per CU, each wave striding over row pairs
+ * with the next pair's loads in flight. It serves matrices too small for
+ * the RT = 4 grid whose rows carry many bytes per 2048 columns (Q8_0,
+ * Q6_K, Q5_1: one row per wave leaves too few bytes in flight), and every
+ * row wider than 2048 columns. Measured against one row per wave: Q8_0
+ * 4096 x 2048 5.17 -> 4.23 us, Q6_K 4.85 -> 4.55 us, the 10240 x 2560,
+ * 6144 x 2560 and 2560 x 6144 Q8_0 projections 13.4 -> 8.5, 8.8 -> 6.6 and
+ * 10.4 -> 7.1 us; Q4_K (1,152 bytes per 2048 columns) is slower this way
+ * (3.39 -> 3.8 us) and keeps one row per wave. */
+constexpr int kThreadsRt2 = 256;
+constexpr uint32_t kRt2MinChunkBytes = 1536u;
+constexpr uint32_t kRt2BlocksPerCu = 2u;
+
+uint32_t rt2_blocks(uint32_t rows) {
+    static uint32_t cus = 0u;
+    if (cus == 0u) {
+        int dev = 0, n = 0;
+        cus = hipGetDevice(&dev) == hipSuccess &&
+                      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                          hipSuccess &&
+                      n > 0
+                  ? (uint32_t)n
+                  : 256u;
+    }
+    const uint32_t per_block = (uint32_t)kThreadsRt2 / 64u * 2u; /* rows */
+    uint32_t blocks = (rows + per_block - 1u) / per_block;
+    if (blocks > kRt2BlocksPerCu * cus) blocks = kRt2BlocksPerCu * cus;
+    return blocks < 1u ? 1u : blocks;
+}
+
+
 /* workgroups of `kernel` (kThreadsRt4 threads) that fit on the device at once */
 template <class K>
 uint32_t resident_blocks(K kernel) {
@@ -429,6 +461,19 @@ hipError_t launch_one(const uint8_t *W, uint32_t rows, Seg sg, const float *x, f
                       uint32_t *st, float *pv, uint32_t *pi, uint32_t ps, hipStream_t s,
                       uint32_t *waves) {
     const uint32_t rt = pick_rt(rows, COLS);
+    if constexpr (COLS == 2048u && B == 1 && kq::row_bytes<TYPE>(2048u) >= kRt2MinChunkBytes) {
+        if (rt == 1u) {
+            const uint32_t blocks = rt2_blocks(rows);
+            if (waves != nullptr) {
+                *waves = blocks * ((uint32_t)kThreadsRt2 / 64u);
+                return hipSuccess;
+            }
+            hipLaunchKernelGGL((matvec_kernel<TYPE, COLS, B, 2, kThreadsRt2>), dim3(blocks),
+                               dim3(kThreadsRt2), 0, s, W, rows, sg.row_bytes, x, sg.x_stride, y,
+                               sg.y_prev, st, pv, pi, ps);
+            return hipGetLastError();
+        }
+    }
     const uint32_t threads = rt == 4u ? (uint32_t)kThreadsRt4 : (uint32_t)kThreadsRt1;
     const uint32_t waves_per_block = threads / 64u;
     const uint32_t groups = (rows + group_rows(COLS, rt) - 1u) / group_rows(COLS, rt);
@@ -500,13 +545,27 @@ hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t row
 }
 
 /* One launch of matvec_wide over all rows (or, with waves set, only its
- * wave count): like launch_one, one row group per wave for RT = 1, a
- * resident striding grid for RT = 4. */
+ * wave count): like launch_one, a resident striding grid for RT = 4;
+ * below that size two rows per wave on the RT = 2 grid at one activation
+ * column, one row group per wave otherwise. */
 template <uint32_t TYPE, int B, uint32_t NCH>
 hipError_t launch_wide_n(const uint8_t *W, uint32_t rows, uint32_t row_bytes, uint32_t tail,
                          const float *x, uint32_t x_stride, float *y, uint32_t *st, float *pv,
                          uint32_t *pi, uint32_t ps, hipStream_t s, uint32_t *waves) {
     const uint32_t rt = pick_rt(rows, kWideCols);
+    if constexpr (B == 1) {
+        if (rt == 1u) {
+            const uint32_t blocks = rt2_blocks(rows);
+            if (waves != nullptr) {
+                *waves = blocks * ((uint32_t)kThreadsRt2 / 64u);
+                return hipSuccess;
+            }
+            hipLaunchKernelGGL((matvec_wide<TYPE, B, 2, kThreadsRt2, NCH>), dim3(blocks),
+                               dim3(kThreadsRt2), 0, s, W, rows, row_bytes, tail, x, x_stride, y,
+                               st, pv, pi, ps);
+            return hipGetLastError();
+        }
+    }
     const uint32_t threads = rt == 4u ? (uint32_t)kThreadsRt4 : (uint32_t)kThreadsRt1;
     const uint32_t waves_per_block = threads / 64u;
     const uint32_t groups = (rows + rt - 1u) / rt;
