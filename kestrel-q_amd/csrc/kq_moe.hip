@@ -1763,41 +1763,64 @@ hipError_t down_width(uint32_t width, const DownArgs &a, uint32_t tokens, uint32
     return hipErrorInvalidValue;
 }
 
-/* The fused launches built: the reference model's layer (Q4_K gate/up with
- * a Q8_0 shared expert over 2048 + 512 columns; Q5_1 down with a Q8_0
- * shared expert over 512 + 128) and the same with routed and shared of one
- * format. Returns false (nothing launched) for other formats and widths. */
-bool gateup_fused(uint32_t tr, uint32_t ts, uint32_t ng, const uint32_t (&gw)[16],
-                  const GateupArgs &a, uint32_t tokens, hipError_t &e, hipStream_t s) {
-    if (ng != 2u || gw[0] != 2048u || gw[1] != 512u || tr != KQ_LAUNCH_Q4_K) return false;
-    const uint32_t rows = a.inter > a.shared_inter ? a.inter : a.shared_inter;
-    const dim3 grid((rows + kFuseRows - 1u) / kFuseRows, a.top_k + 1u, tokens);
+/* The fused launches built: the reference model's layers (hidden 2560 =
+ * 2048 + 512 columns of Q4_K gate/up, or Q5_K in its layer 2; intermediate
+ * 640 = 512 + 128 columns of Q5_1 down, or Q8_0 in its layers 2, 4, 30, 46
+ * and 47; a Q8_0 shared expert throughout) and the same with routed and
+ * shared of one format. Returns false (nothing launched) for other formats
+ * and widths. */
+template <uint32_t TR>
+bool gateup_fused_tr(uint32_t ts, const dim3 &grid, const GateupArgs &a, hipStream_t s) {
     if (ts == KQ_LAUNCH_Q8_0)
-        hipLaunchKernelGGL((expert_gateup_fused<KQ_LAUNCH_Q4_K, KQ_LAUNCH_Q8_0, 2048u, 512u>),
-                           grid, dim3(kThreads), 0, s, a);
-    else if (ts == KQ_LAUNCH_Q4_K)
-        hipLaunchKernelGGL((expert_gateup_fused<KQ_LAUNCH_Q4_K, KQ_LAUNCH_Q4_K, 2048u, 512u>),
-                           grid, dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL((expert_gateup_fused<TR, KQ_LAUNCH_Q8_0, 2048u, 512u>), grid,
+                           dim3(kThreads), 0, s, a);
+    else if (ts == TR)
+        hipLaunchKernelGGL((expert_gateup_fused<TR, TR, 2048u, 512u>), grid, dim3(kThreads), 0, s,
+                           a);
     else
         return false;
+    return true;
+}
+
+bool gateup_fused(uint32_t tr, uint32_t ts, uint32_t ng, const uint32_t (&gw)[16],
+                  const GateupArgs &a, uint32_t tokens, hipError_t &e, hipStream_t s) {
+    if (ng != 2u || gw[0] != 2048u || gw[1] != 512u) return false;
+    const uint32_t rows = a.inter > a.shared_inter ? a.inter : a.shared_inter;
+    const dim3 grid((rows + kFuseRows - 1u) / kFuseRows, a.top_k + 1u, tokens);
+    bool launched = false;
+    if (tr == KQ_LAUNCH_Q4_K)
+        launched = gateup_fused_tr<KQ_LAUNCH_Q4_K>(ts, grid, a, s);
+    else if (tr == KQ_LAUNCH_Q5_K)
+        launched = gateup_fused_tr<KQ_LAUNCH_Q5_K>(ts, grid, a, s);
+    if (!launched) return false;
     e = hipGetLastError();
+    return true;
+}
+
+template <uint32_t TR>
+bool down_fused_tr(uint32_t ts, const dim3 &grid, const dim3 &block, const DownArgs &a,
+                   hipStream_t s) {
+    if (ts == KQ_LAUNCH_Q8_0)
+        hipLaunchKernelGGL((expert_down_fused<TR, KQ_LAUNCH_Q8_0, 512u, 128u>), grid, block, 0,
+                           s, a);
+    else if (ts == TR)
+        hipLaunchKernelGGL((expert_down_fused<TR, TR, 512u, 128u>), grid, block, 0, s, a);
+    else
+        return false;
     return true;
 }
 
 bool down_fused(uint32_t tr, uint32_t ts, uint32_t nd, const uint32_t (&dw)[16],
                 const DownArgs &a, uint32_t tokens, hipError_t &e, hipStream_t s) {
-    if (nd != 2u || dw[0] != 512u || dw[1] != 128u || tr != KQ_LAUNCH_Q5_1 || a.top_k + 1u > 16u)
-        return false;
+    if (nd != 2u || dw[0] != 512u || dw[1] != 128u || a.top_k + 1u > 16u) return false;
     const dim3 grid((a.hidden + kFuseRows - 1u) / kFuseRows, tokens);
     const dim3 block(64u * (a.top_k + 1u));
-    if (ts == KQ_LAUNCH_Q8_0)
-        hipLaunchKernelGGL((expert_down_fused<KQ_LAUNCH_Q5_1, KQ_LAUNCH_Q8_0, 512u, 128u>), grid,
-                           block, 0, s, a);
-    else if (ts == KQ_LAUNCH_Q5_1)
-        hipLaunchKernelGGL((expert_down_fused<KQ_LAUNCH_Q5_1, KQ_LAUNCH_Q5_1, 512u, 128u>), grid,
-                           block, 0, s, a);
-    else
-        return false;
+    bool launched = false;
+    if (tr == KQ_LAUNCH_Q5_1)
+        launched = down_fused_tr<KQ_LAUNCH_Q5_1>(ts, grid, block, a, s);
+    else if (tr == KQ_LAUNCH_Q8_0)
+        launched = down_fused_tr<KQ_LAUNCH_Q8_0>(ts, grid, block, a, s);
+    if (!launched) return false;
     e = hipGetLastError();
     return true;
 }

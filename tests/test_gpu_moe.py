@@ -575,8 +575,12 @@ def test_moe_reference_model_layer(ctx):
     (512, 16, 4, 256, 16, "Q4_K", "Q6_K", "Q8_0", "Q6_K"),    # mixed shared, many tokens
     (2560, 32, 4, 640, 1, "Q4_K", "Q5_1", "Q8_0", "Q8_0"),    # one launch per role
     (2560, 64, 8, 640, 1, "Q4_K", "Q5_1", "Q4_K", "Q5_1"),    # one launch, one format
+    (2560, 64, 8, 640, 1, "Q5_K", "Q8_0", "Q8_0", "Q8_0"),    # layer 2's formats
+    (2560, 64, 8, 640, 1, "Q4_K", "Q8_0", "Q8_0", "Q8_0"),    # layers 4, 30, 46, 47
+    (2560, 32, 4, 640, 1, "Q5_K", "Q8_0", "Q5_K", "Q8_0"),    # Q5_K routed and shared
 ], ids=["real-64e-3tok", "768x384", "640x96", "1280x320", "3072x256", "mixed-16tok",
-        "fused-ref-formats", "fused-same-formats"])
+        "fused-ref-formats", "fused-same-formats", "fused-layer2", "fused-q8-down",
+        "fused-q5k-shared"])
 def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
     seed = S.W_MOE + 3000 + H + I + T
     out, ids, ref, tr, ex = run_layer(ctx, H, E, K, I, T, g, d, sg, sd, seed)
