@@ -961,6 +961,11 @@ static kq_status lm_head(kq_hip_context *c, uint32_t type_id, const void *w, uin
     if (nparts == 0u)
         return kq_fail(diag, KQ_STATUS_DEVICE_FAILURE, "lm head: no launch configuration");
     if (noalloc) {
+        /* The launch shapes keep every call within the array: one row group
+         * per wave only below 4 x 4096 groups (at most 16,384 waves in
+         * 512-thread workgroups), resident grids above, so 8 columns need
+         * at most 131,072 partials. The check stays as the guard should a
+         * launch shape change. */
         const uint64_t cap = kq_launch_noalloc_parts();
         if ((uint64_t)nparts * batch > cap)
             return kq_fail(diag, KQ_STATUS_LIMIT_EXCEEDED,
