@@ -1708,14 +1708,13 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
         /* over the gate/up pass's item list (routed and shared chunks) */
         e = kq_launch_dn_lds(d->inter, d->hidden, dn, sd, ws->act, tokens, d->top_k, ws->gitems,
                              ws->dstage, ws->outp, status, s);
-    } else if (lds_routed && w->down_type == KQ_LAUNCH_Q5_1 &&
-               (!lds_shared || w->shared_down_type == KQ_LAUNCH_Q5_1) &&
-               kq_launch_dn51_supported(d->inter)) {
-        /* Q5_1 rows through the same per-wave LDS-DMA pipeline, over the
-         * item list (the shared expert's chunks are in it when its gate/up
-         * ran in the Q4_K pass; otherwise it runs below) */
-        e = kq_launch_dn51(d->inter, d->hidden, dn, sd, ws->act, tokens, d->top_k, ws->gitems,
-                           ws->dstage, ws->outp, status, s);
+    } else if (lds_routed && kq_launch_dn_small_supported(w->down_type, d->inter) &&
+               (!lds_shared || w->shared_down_type == w->down_type)) {
+        /* Q5_1 or Q8_0 rows through the same per-wave LDS-DMA pipeline,
+         * over the item list (the shared expert's chunks are in it when its
+         * gate/up ran in the LDS gate/up pass; otherwise it runs below) */
+        e = kq_launch_dn_small(w->down_type, d->inter, d->hidden, dn, sd, ws->act, tokens,
+                               d->top_k, ws->gitems, ws->dstage, ws->outp, status, s);
         const size_t tk = (size_t)tokens * d->top_k;
         if (e == hipSuccess && !lds_shared && w->shared_down_type == KQ_LAUNCH_Q8_0 &&
             kq_launch_dense_q8_supported(d->hidden, d->inter, tokens)) {

@@ -371,19 +371,26 @@ void dn_q6k(DnArgs a) {
 }
 
 /* ------------------------------------------------------------------ */
-/* the same pipeline for Q5_1 rows (the reference model's routed down):
- * 24 B per 32 columns (f16 d, f16 m, 32 high bits, 16 bytes of nibbles;
- * src/kq_numeric.c:197-222), every block 4-byte aligned. The activations
- * are split in natural column order (dense_split), so lane (j, g) reads
- * columns 32b + 8g .. + 7 of block b as one 16-byte run. Per block and
- * tile: the 5-bit codes enter fp16 exactly, one 16x16x32 step each for hi
- * and lo scaled by d; the min term m * sum(x) is one small step per 16
- * blocks of the mins against the token's block sums (formed once per
- * item from the activation registers), added unscaled. */
-template <uint32_t KD>
-struct Dn51Shape {
+/* the same pipeline for rows of 32-weight blocks: Q5_1 (the reference
+ * model's routed down: 24 B per block, f16 d, f16 m, 32 high bits, 16
+ * bytes of nibbles; src/kq_numeric.c:197-222, every block 4-byte aligned)
+ * and Q8_0 (its layers 2, 4, 30, 46 and 47: 34 B per block, f16 d and 32
+ * int8 codes; src/kq_numeric.c:208-221, blocks alternately at 0 and 2 mod
+ * 4 in a row). The activations are split in natural column order
+ * (dense_split), so lane (j, g) reads columns 32b + 8g .. + 7 of block b
+ * as one 16-byte run. Per block and tile: the codes enter fp16 exactly,
+ * one 16x16x32 step each for hi and lo scaled by d; for Q5_1 the min term
+ * m * sum(x) is one small step per 16 blocks of the mins against the
+ * token's block sums (formed once per item from the activation
+ * registers), added unscaled. */
+template <uint32_t FMT, uint32_t KD>
+struct DnSmallShape {
+    static_assert(FMT == KQ_LAUNCH_Q5_1 || FMT == KQ_LAUNCH_Q8_0, "format");
+    static constexpr bool Q51 = FMT == KQ_LAUNCH_Q5_1;
+    static constexpr uint32_t BB = Q51 ? 24u : 34u;          /* block bytes */
     static constexpr uint32_t NBK = KD / 32u;                /* blocks per row */
-    static constexpr uint32_t RB = 24u * NBK;                /* row bytes */
+    static constexpr uint32_t RB = BB * NBK;                 /* row bytes */
+    static_assert(RB % 4u == 0u, "rows start 4-byte aligned in the slot");
     static constexpr uint32_t TB = kT * RB;                  /* tile bytes */
     static constexpr uint32_t IPT = (TB + 1023u) / 1024u;    /* loads per tile */
     static constexpr uint32_t SLOT = IPT * 1024u;
@@ -399,10 +406,10 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) {
     return ((x * 0x00204081u) & 0x01010101u) << 4;
 }
 
-template <uint32_t KD>
-__global__ __launch_bounds__(Dn51Shape<KD>::W * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void dn_q51(DnArgs a) {
-    using S = Dn51Shape<KD>;
+template <uint32_t FMT, uint32_t KD>
+__global__ __launch_bounds__((DnSmallShape<FMT, KD>::W * 64))
+__attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
+    using S = DnSmallShape<FMT, KD>;
     constexpr uint32_t NBK = S::NBK;
     __shared__ __align__(16) uint8_t slots[S::W][S::RING][S::SLOT];
 
@@ -479,6 +486,7 @@ void dn_q51(DnArgs a) {
             sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
         }
         wait_vm_all();
+        if constexpr (!S::Q51) return;
         /* the min term's operand: each block's column sum of token row j
          * (the four lanes of row j hold 8 columns each), times 2^-5 so
          * it fits fp16, split hi + lo; lane (j, g) keeps blocks 4g .. 4g+3
@@ -515,7 +523,9 @@ void dn_q51(DnArgs a) {
     uint32_t ctile = lo - (lo / nt) * nt, cslot = 0u;
     enter(lo / nt);
 
-    const h2 bias = h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    /* fp16 1024 + code: Q5_1 codes are unsigned, Q8_0 ones offset by 128 */
+    const h2 bias = S::Q51 ? h2{(_Float16)-1024.0f, (_Float16)-1024.0f}
+                           : h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
     const uint32_t shn = g >= 2u ? 4u : 0u;
     for (uint32_t tau = lo; tau < hi; ++tau) {
         if (ctile == nt) {
@@ -533,12 +543,39 @@ void dn_q51(DnArgs a) {
         f4 acc = {0.f, 0.f, 0.f, 0.f}, macc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t b = 0; b < NBK; ++b) {
-            const uint32_t *blk = row + 6u * b;
-            const uint32_t dm = blk[0];
-            const uint32_t hb = (blk[1] >> (8u * g)) & 0xffu;
-            const uint2 qv = *(const uint2 *)(blk + 2u + 2u * (g & 1u));
-            const uint32_t c0 = ((qv.x >> shn) & 0x0f0f0f0fu) | spread4(hb & 15u);
-            const uint32_t c1 = ((qv.y >> shn) & 0x0f0f0f0fu) | spread4(hb >> 4);
+            uint32_t c0, c1;
+            float d;
+            if constexpr (S::Q51) {
+                const uint32_t *blk = row + 6u * b;
+                const uint32_t dm = blk[0];
+                const uint32_t hb = (blk[1] >> (8u * g)) & 0xffu;
+                const uint2 qv = *(const uint2 *)(blk + 2u + 2u * (g & 1u));
+                c0 = ((qv.x >> shn) & 0x0f0f0f0fu) | spread4(hb & 15u);
+                c1 = ((qv.y >> shn) & 0x0f0f0f0fu) | spread4(hb >> 4);
+                d = half_bits(dm);
+                const float mn = half_bits(dm >> 16);
+                malformed |= !kq_isfinite(d) || !kq_isfinite(mn);
+            } else {
+                /* block b at byte 34 b of the row: d in the low half of
+                 * dword 17 b / 2 (b even) or the high half of dword
+                 * (34 b - 2) / 4 (b odd); lane g's eight codes at byte
+                 * 34 b + 2 + 8 g, 2 mod 4 (b even) or 0 mod 4 (b odd).
+                 * The codes, offset by 128, become fp16 1024 + c + 128. */
+                if (b % 2u == 0u) {
+                    const uint32_t *blk = row + 17u * (b / 2u);
+                    d = half_bits(blk[0]);
+                    const uint32_t q0 = blk[2u * g], q1 = blk[2u * g + 1u],
+                                   q2 = blk[2u * g + 2u];
+                    c0 = kq_align2(q1, q0, 2u) ^ 0x80808080u;
+                    c1 = kq_align2(q2, q1, 2u) ^ 0x80808080u;
+                } else {
+                    const uint32_t *blk = row + (34u * b - 2u) / 4u;
+                    d = half_bits(blk[0] >> 16);
+                    c0 = blk[1u + 2u * g] ^ 0x80808080u;
+                    c1 = blk[2u + 2u * g] ^ 0x80808080u;
+                }
+                malformed |= !kq_isfinite(d);
+            }
             const h2 w0 = byte_pair_lo(c0) + bias, w1 = byte_pair_hi(c0) + bias;
             const h2 w2 = byte_pair_lo(c1) + bias, w3 = byte_pair_hi(c1) + bias;
             const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
@@ -546,15 +583,13 @@ void dn_q51(DnArgs a) {
             f4 t = {0.f, 0.f, 0.f, 0.f};
             t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, t, 0, 0, 0);
             t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, t, 0, 0, 0);
-            const float d = half_bits(dm), mn = half_bits(dm >> 16);
-            malformed |= !kq_isfinite(d) || !kq_isfinite(mn);
 #pragma unroll
             for (int k = 0; k < 4; ++k) acc[k] = fmaf(d, t[k], acc[k]);
         }
         /* the min term: sum over blocks of m times the token's block sum,
          * as 16x16x16 steps over 16 blocks each (m exact in fp16) */
 #pragma unroll
-        for (uint32_t st4 = 0; st4 < NMS; ++st4) {
+        for (uint32_t st4 = 0; st4 < (S::Q51 ? NMS : 0u); ++st4) {
             _Float16 mv[4];
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) {
@@ -601,15 +636,19 @@ hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
 
 extern "C" int kq_launch_dn_lds_supported(uint32_t inter) { return inter == 256u || inter == 512u; }
 
-extern "C" int kq_launch_dn51_supported(uint32_t inter) { return inter == 640u || inter == 512u; }
+extern "C" int kq_launch_dn_small_supported(uint32_t type, uint32_t inter) {
+    return (type == KQ_LAUNCH_Q5_1 || type == KQ_LAUNCH_Q8_0) && (inter == 640u || inter == 512u);
+}
 
-/* Q5_1 down over the item list the permutation built: the activation rows
- * split in natural order (dense_split) into staged, then dn_q51 */
-extern "C" hipError_t kq_launch_dn51(uint32_t inter, uint32_t hidden, const void *down,
-                                     const void *shared_down, const float *act, uint32_t tokens,
-                                     uint32_t top_k, const void *items, void *staged, float *out,
-                                     uint32_t *status, hipStream_t s) {
-    if (!kq_launch_dn51_supported(inter)) return hipErrorInvalidValue;
+/* Q5_1 or Q8_0 down over the item list the permutation built: the
+ * activation rows split in natural order (dense_split) into staged, then
+ * dn_small */
+extern "C" hipError_t kq_launch_dn_small(uint32_t type, uint32_t inter, uint32_t hidden,
+                                         const void *down, const void *shared_down,
+                                         const float *act, uint32_t tokens, uint32_t top_k,
+                                         const void *items, void *staged, float *out,
+                                         uint32_t *status, hipStream_t s) {
+    if (!kq_launch_dn_small_supported(type, inter)) return hipErrorInvalidValue;
     const uint32_t npos = tokens * top_k + tokens;
     uint8_t *st = (uint8_t *)staged;
     const size_t xb = (size_t)npos * inter * 2u;
@@ -636,10 +675,21 @@ extern "C" hipError_t kq_launch_dn51(uint32_t inter, uint32_t hidden, const void
             cus < 1)
             cus = 256;
     }
-    if (inter == 640u)
-        hipLaunchKernelGGL((dn_q51<640u>), dim3((uint32_t)cus), dim3(Dn51Shape<640u>::W * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((dn_q51<512u>), dim3((uint32_t)cus), dim3(Dn51Shape<512u>::W * 64), 0, s, a);
+#define KQ_DN_SMALL(F, K)                                                                   \
+    hipLaunchKernelGGL((dn_small<F, K>), dim3((uint32_t)cus),                               \
+                       dim3(DnSmallShape<F, K>::W * 64), 0, s, a)
+    if (type == KQ_LAUNCH_Q5_1) {
+        if (inter == 640u)
+            KQ_DN_SMALL(KQ_LAUNCH_Q5_1, 640u);
+        else
+            KQ_DN_SMALL(KQ_LAUNCH_Q5_1, 512u);
+    } else {
+        if (inter == 640u)
+            KQ_DN_SMALL(KQ_LAUNCH_Q8_0, 640u);
+        else
+            KQ_DN_SMALL(KQ_LAUNCH_Q8_0, 512u);
+    }
+#undef KQ_DN_SMALL
     return hipGetLastError();
 }
 

@@ -202,13 +202,13 @@ hipError_t kq_launch_gu_lds(uint32_t type, uint32_t hidden, const void *gate, co
                             uint32_t tokens, uint32_t top_k, uint32_t rows, int with_shared,
                             int items_ready, void *items, float *act, uint32_t *status,
                             hipStream_t s);
-/* prefill Q5_1 down over the same item list (kq_grouped_dn.hip); staged
- * is scratch of kq_launch_dn_stage_bytes */
-int kq_launch_dn51_supported(uint32_t inter);
-hipError_t kq_launch_dn51(uint32_t inter, uint32_t hidden, const void *down,
-                          const void *shared_down, const float *act, uint32_t tokens,
-                          uint32_t top_k, const void *items, void *staged, float *out,
-                          uint32_t *status, hipStream_t s);
+/* prefill Q5_1 or Q8_0 down (type) over the same item list
+ * (kq_grouped_dn.hip); staged is scratch of kq_launch_dn_stage_bytes */
+int kq_launch_dn_small_supported(uint32_t type, uint32_t inter);
+hipError_t kq_launch_dn_small(uint32_t type, uint32_t inter, uint32_t hidden, const void *down,
+                              const void *shared_down, const float *act, uint32_t tokens,
+                              uint32_t top_k, const void *items, void *staged, float *out,
+                              uint32_t *status, hipStream_t s);
 /* prefill Q6_K down over the gate/up pass's item list (kq_grouped_dn.hip) */
 int kq_launch_dn_lds_supported(uint32_t inter);
 uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter);

@@ -591,8 +591,8 @@ def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
 # grouped (MFMA) prefill with every format pair the passes take: Q8_0,
 # Q4_K and Q5_K gate/up (2560 columns staged in two slices, or streamed
 # through LDS), Q5_1, Q8_0, Q6_K and Q4_K down (640-column rows of
-# 128-column units), routed and shared of different formats (two launches
-# per role)
+# 128-column units, or streamed through LDS per wave), routed and shared of
+# different formats (two launches per role)
 @pytest.mark.parametrize("H,E,K,I,T,g,d,sg,sd", [
     (2560, 64, 8, 640, 40, "Q4_K", "Q5_1", "Q8_0", "Q8_0"),
     (2560, 32, 4, 640, 37, "Q8_0", "Q8_0", "Q8_0", "Q8_0"),
@@ -603,8 +603,11 @@ def test_moe_segments_and_shared_types(ctx, H, E, K, I, T, g, d, sg, sd):
     (2048, 24, 3, 512, 37, "Q5_K", "Q6_K", "Q5_K", "Q6_K"),
     (1024, 24, 3, 640, 37, "Q5_K", "Q5_1", "Q4_K", "Q5_1"),
     (256, 16, 4, 256, 33, "Q5_K", "Q4_K", "Q5_K", "Q8_0"),
+    (1024, 24, 3, 512, 37, "Q4_K", "Q8_0", "Q4_K", "Q8_0"),
+    (2560, 48, 6, 640, 29, "Q4_K", "Q8_0", "Q8_0", "Q8_0"),
 ], ids=["ref-formats-40tok", "q8_0-2560", "q5_1-640", "mixed-q6k-lds", "q8_0-q5_1-down",
-        "layer2-formats-40tok", "q5k-q6k-lds", "q5k-q4k-shared", "q5k-256"])
+        "layer2-formats-40tok", "q5k-q6k-lds", "q5k-q4k-shared", "q5k-256", "q8_0-down-lds-512",
+        "q8_0-down-layers"])
 def test_moe_prefill_grouped_formats(ctx, H, E, K, I, T, g, d, sg, sd):
     seed = S.W_MOE + 5000 + H + I + T
     w = S.moe_weights(seed, H, E, I, I, gate_fmt=g, down_fmt=d, shared_gate_fmt=sg,
