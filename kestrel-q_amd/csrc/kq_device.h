@@ -229,6 +229,15 @@ __device__ __forceinline__ uint32_t kq_ld16(KqBufA<A> b, uint32_t voff, uint32_t
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.r, (int)voff, (int)soff, A);
 }
 
+/* a * b for operands below 2^24 with the full-rate 24-bit multiply: the
+ * compiler emits the quarter-rate 32-bit one for a plain product (and for
+ * __umul24) even when the operands are known to be small */
+__device__ __forceinline__ uint32_t kq_mul_u24(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 /*
  * Byte loads from addresses that are only 2-byte aligned (Q8_0 blocks are
  * 34 B and Q6_K blocks 210 B, so a block can start at 2 mod 4). The dwords

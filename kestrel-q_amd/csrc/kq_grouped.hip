@@ -539,7 +539,7 @@ struct Tile<KQ_LAUNCH_Q5_1, KSL, NMAT> {
 
     /* bit k of x (k < 4) to bit 8k + 4: the fifth bit of four codes */
     __device__ static __forceinline__ uint32_t spread4(uint32_t x) {
-        return ((x * 0x00204081u) & 0x01010101u) << 4;
+        return (kq_mul_u24(x, 0x00204081u) & 0x01010101u) << 4;
     }
 
     /* iteration b: blocks 4b .. 4b + 3 of the slice; codes 0..31 are

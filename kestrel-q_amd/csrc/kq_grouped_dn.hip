@@ -402,8 +402,9 @@ struct DnSmallShape {
     static_assert(W * RING * SLOT <= 160u * 1024u, "LDS");
 };
 
+/* bits 0..3 of x (x < 16) to bit 4 of bytes 0..3 */
 __device__ __forceinline__ uint32_t spread4(uint32_t x) {
-    return ((x * 0x00204081u) & 0x01010101u) << 4;
+    return (kq_mul_u24(x, 0x00204081u) & 0x01010101u) << 4;
 }
 
 template <uint32_t FMT, uint32_t KD>

@@ -402,15 +402,16 @@ constexpr int kThreadsRt4 = 256;
 /* Between the two, for one activation column: two rows per wave on a grid
  * of two 256-thread workgroups per CU, each wave striding over row pairs
  * with the next pair's loads in flight. It serves matrices too small for
- * the RT = 4 grid whose rows carry many bytes per 2048 columns (Q8_0,
- * Q6_K, Q5_1: one row per wave leaves too few bytes in flight), and every
- * row wider than 2048 columns. Measured against one row per wave: Q8_0
- * 4096 x 2048 5.17 -> 4.23 us, Q6_K 4.85 -> 4.55 us, the 10240 x 2560,
- * 6144 x 2560 and 2560 x 6144 Q8_0 projections 13.4 -> 8.5, 8.8 -> 6.6 and
- * 10.4 -> 7.1 us; Q4_K (1,152 bytes per 2048 columns) is slower this way
- * (3.39 -> 3.8 us) and keeps one row per wave. */
+ * the RT = 4 grid whose rows carry the most bytes per 2048 columns (Q8_0
+ * 2,176, Q6_K 1,680: one row per wave leaves too few bytes in flight), in
+ * one chunk or several. Measured against one row per wave: Q8_0 4096 x
+ * 2048 5.17 -> 4.23 us, Q6_K 4.85 -> 4.55 us, the 10240 x 2560, 6144 x
+ * 2560 and 2560 x 6144 Q8_0 projections 13.4 -> 8.5, 8.8 -> 6.6 and
+ * 10.4 -> 7.1 us. Q5_1 (1,536 bytes) and Q4_K (1,152) are slower this way
+ * (4096 x 2048: 3.61 -> 4.08 and 3.39 -> 3.8 us) and keep one row per
+ * wave. */
 constexpr int kThreadsRt2 = 256;
-constexpr uint32_t kRt2MinChunkBytes = 1536u;
+constexpr uint32_t kRt2MinChunkBytes = 1680u;
 constexpr uint32_t kRt2BlocksPerCu = 2u;
 
 uint32_t rt2_blocks(uint32_t rows) {
@@ -546,14 +547,14 @@ hipError_t launch_b(uint32_t type, uint32_t cols, const uint8_t *W, uint32_t row
 
 /* One launch of matvec_wide over all rows (or, with waves set, only its
  * wave count): like launch_one, a resident striding grid for RT = 4;
- * below that size two rows per wave on the RT = 2 grid at one activation
- * column, one row group per wave otherwise. */
+ * below that size two rows per wave on the RT = 2 grid for the formats
+ * above at one activation column, one row group per wave otherwise. */
 template <uint32_t TYPE, int B, uint32_t NCH>
 hipError_t launch_wide_n(const uint8_t *W, uint32_t rows, uint32_t row_bytes, uint32_t tail,
                          const float *x, uint32_t x_stride, float *y, uint32_t *st, float *pv,
                          uint32_t *pi, uint32_t ps, hipStream_t s, uint32_t *waves) {
     const uint32_t rt = pick_rt(rows, kWideCols);
-    if constexpr (B == 1) {
+    if constexpr (B == 1 && kq::row_bytes<TYPE>(kWideCols) >= kRt2MinChunkBytes) {
         if (rt == 1u) {
             const uint32_t blocks = rt2_blocks(rows);
             if (waves != nullptr) {

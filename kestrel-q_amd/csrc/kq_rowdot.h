@@ -782,7 +782,7 @@ struct LaneQ5K {
 
 /* bit j of the low 4 bits of n into bit 8j (bits 0, 8, 16, 24) */
 __device__ __forceinline__ uint32_t spread4(uint32_t n) {
-    return ((n & 15u) * 0x00204081u) & 0x01010101u;
+    return kq_mul_u24(n & 15u, 0x00204081u) & 0x01010101u;
 }
 
 /* ---------------- Q5_1: 24 B blocks of 32 ---------------- */
