@@ -1214,39 +1214,59 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
     const uint32_t ntiles = (rows + kTile - 1u) / kTile;
     uint8_t *myslot = slots + wave * 2u * kMvSlot;
 
-    /* Work item it = block it % nb of tile gw + nwaves * (it / nb). Its
-     * loads: unit e = i * 64 + lane of the 224 = 16 rows x 14 covers bytes
-     * [16u, 16u + 16) of row e / 14's window (the block's start rounded
-     * down to 4 bytes); rows past the matrix, and the 32 spare units, read
-     * far past the buffer (zeros). */
+    /* Work item it = block it % nb of tile gw + nwaves * (it / nb), walked
+     * with counters (t, b) and the tile's byte offset tb = 16 t rb (no
+     * division or 32-bit multiply per item; tb is used only while
+     * t < ntiles, where it stays below wbytes). Its loads: unit
+     * e = i * 64 + lane of the 224 = 16 rows x 14 covers bytes [16u, 16u +
+     * 16) of row e / 14's window (the block's start rounded down to 4
+     * bytes); rows past the matrix, and the 32 spare units, read far past
+     * the buffer (zeros). */
+    struct Pos {
+        uint32_t t, b, tb;
+    };
+    const uint32_t tstep = nwaves * kTile * rb;
+    auto advance = [&](Pos &q) {
+        if (++q.b == nb) {
+            q.b = 0u;
+            q.t += nwaves;
+            q.tb += tstep;
+        }
+    };
+    uint32_t ld_r[kMvLoads], ld_rb[kMvLoads], ld_u[kMvLoads];
+#pragma unroll
+    for (int i = 0; i < kMvLoads; ++i) {
+        const uint32_t e = (uint32_t)i * 64u + lane;
+        ld_r[i] = e < kMvUnits ? e / 14u : 0xffffu; /* spare units: no row */
+        ld_u[i] = 16u * (e - 14u * (e / 14u));
+        ld_rb[i] = (e / 14u) * rb;
+    }
     typedef kq_u32x4 MvLd[kMvLoads];
-    auto load_item = [&](uint32_t it, MvLd &v) {
-        const uint32_t t = gw + nwaves * (it / nb), b = it % nb;
+    auto load_item = [&](const Pos &q, MvLd &v) {
 #pragma unroll
         for (int i = 0; i < kMvLoads; ++i) {
-            const uint32_t e = (uint32_t)i * 64u + lane;
-            const uint32_t r = e / 14u, u = e - 14u * r;
-            const uint32_t row = t * kTile + r;
-            const uint32_t o = row * rb + b * F::kBytes;
+            const uint32_t row = q.t * kTile + ld_r[i];
+            const uint32_t o = q.tb + ld_rb[i] + q.b * F::kBytes;
             const uint32_t off =
-                (e < kMvUnits && t < ntiles && row < rows) ? (o & ~3u) + 16u * u : wbytes + 256u;
+                (ld_r[i] < kTile && q.t < ntiles && row < rows) ? (o & ~3u) + ld_u[i]
+                                                                 : wbytes + 256u;
             v[i] = __builtin_amdgcn_raw_buffer_load_b128(wb.r, (int)off, 0, 0);
         }
     };
     auto store_item = [&](uint32_t slot, const MvLd &v) {
 #pragma unroll
-        for (int i = 0; i < kMvLoads; ++i) {
-            const uint32_t e = (uint32_t)i * 64u + lane;
-            const uint32_t r = e / 14u, u = e - 14u * r;
-            if (e < kMvUnits)
-                *(kq_u32x4 *)(myslot + slot * kMvSlot + r * kMvPitch + 16u * u) = v[i];
-        }
+        for (int i = 0; i < kMvLoads; ++i)
+            if (ld_r[i] < kTile)
+                *(kq_u32x4 *)(myslot + slot * kMvSlot + ld_r[i] * kMvPitch + ld_u[i]) = v[i];
     };
 
     /* the first two items are requested before the staging */
     MvLd va, vb;
-    load_item(0u, va);
-    load_item(1u, vb);
+    Pos ld = {gw, 0u, gw * kTile * rb}, pr = ld;
+    load_item(ld, va);
+    advance(ld);
+    load_item(ld, vb);
+    advance(ld);
 
     /* stage column i (one wave each): scale by 2^sig[i], split into hi + lo */
     bool bad = false;
@@ -1282,7 +1302,8 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
         if (lane == 0u) sig[i] = e;
     }
     store_item(0u, va);
-    load_item(2u, va);
+    load_item(ld, va);
+    advance(ld);
     kq_lds_barrier();
     int unscale[4];
 #pragma unroll
@@ -1308,10 +1329,11 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
 
     /* item it from its slot: 16 sub-block steps into acc; at the tile's
      * last block lanes 0..15 write row t*16 + j of columns 0 .. batch-1 */
-    auto process = [&](uint32_t it, uint32_t slot) {
-        const uint32_t tt = gw + nwaves * (it / nb), bb = it % nb;
-        const uint32_t row = tt * kTile + j;
-        const uint32_t sh = (row * rb + bb * F::kBytes) & 3u;
+    const uint32_t jrb = j * rb;
+    auto process = [&](const Pos &q, uint32_t slot) {
+        const uint32_t bb = q.b;
+        const uint32_t row = q.t * kTile + j;
+        const uint32_t sh = (q.tb + jrb + bb * F::kBytes) & 3u;
         const uint8_t *p = myslot + slot * kMvSlot + j * kMvPitch;
         auto w32 = [&](uint32_t o) { return *(const uint32_t *)(p + o); };
         const float d = (float)*(const _Float16 *)(p + sh + 208u);
@@ -1386,13 +1408,17 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
      * the other slot and it + 3 is requested. */
     const uint32_t nitems = ntiles > gw ? ((ntiles - gw + nwaves - 1u) / nwaves) * nb : 0u;
     for (uint32_t it = 0u; it < nitems; it += 2u) {
-        process(it, 0u);
+        process(pr, 0u);
+        advance(pr);
         store_item(1u, vb);
-        load_item(it + 3u, vb);
+        load_item(ld, vb);
+        advance(ld);
         if (it + 1u >= nitems) break;
-        process(it + 1u, 1u);
+        process(pr, 1u);
+        advance(pr);
         store_item(0u, va);
-        load_item(it + 4u, va);
+        load_item(ld, va);
+        advance(ld);
     }
     if (bad) kq_flag(status, KQ_DEV_INPUT);
     if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
