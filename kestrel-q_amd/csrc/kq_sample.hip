@@ -117,6 +117,53 @@ __device__ __forceinline__ void load_run(const float *p, uint32_t i0, uint32_t n
     }
 }
 
+/* s + p[0] + p[1] + ... + p[n - 1] (zeros past n), each sum rounded, on one
+ * wave whose lanes all hold the running sum. The terms go through LDS 64 x
+ * kRun at a time (stage: 2 x 64 x kRun floats) and come back as broadcast
+ * reads (every lane the same address), so each term is one dependent add
+ * with no lane extraction; the next run's global loads are in flight
+ * meanwhile. LDS operations of one wave complete in order, so the wave
+ * reads back what its lanes wrote without a barrier. */
+__device__ __forceinline__ float serial_sum(const float *p, uint32_t n, float *stage, float s) {
+    const uint32_t lane = threadIdx.x % 64u;
+    const uint32_t runs = (n + 64u * kRun - 1u) / (64u * kRun);
+    float w[kRun], nx[kRun];
+    load_run(p, 0u, n, w);
+    for (uint32_t r = 0u; r < runs; ++r) {
+        load_run(p, (r + 1u) * 64u * kRun, n, nx);
+        float *buf = stage + (r & 1u) * 64u * kRun;
+#pragma unroll
+        for (int u = 0; u < kRun; ++u) buf[64u * (uint32_t)u + lane] = w[u];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float4 *b4 = reinterpret_cast<const float4 *>(buf);
+#pragma unroll
+        for (uint32_t j = 0; j < 16u * kRun; ++j) {
+            const float4 t = b4[j];
+            s = s + t.x;
+            s = s + t.y;
+            s = s + t.z;
+            s = s + t.w;
+        }
+#pragma unroll
+        for (int u = 0; u < kRun; ++u) w[u] = nx[u];
+    }
+    return s;
+}
+
+/* inclusive prefix sums of one int64 per lane across the wave */
+__device__ __forceinline__ int64_t wave_scan_i64(int64_t v) {
+    const uint32_t lane = threadIdx.x % 64u;
+#pragma unroll
+    for (uint32_t o = 1u; o < 64u; o <<= 1) {
+        const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, o, 64);
+        const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)((uint64_t)v >> 32), o, 64);
+        if (lane >= o) v += (int64_t)(((uint64_t)hi << 32) | lo);
+    }
+    return v;
+}
+
 /* the categorical draw (src/kq_sampling.c:400-447) on one wave: uniform =
  * word / 2^32, threshold = uniform * total, the first kept id whose
  * binary64 running sum exceeds the threshold (walk), else the last kept id
@@ -348,6 +395,10 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
     __shared__ float s_max_p[kTailThreads / 64];
     __shared__ uint32_t s_u[4];
     __shared__ float s_f[4]; /* [2]: the by-id mass of the wide path */
+    __shared__ __align__(16) float s_stage[2 * 64 * kRun];
+    __shared__ int64_t s_qsum[kTailThreads / 64];
+    __shared__ double s_dsum[kTailThreads / 64];
+    __shared__ uint32_t s_ok[kTailThreads / 64], s_last[kTailThreads / 64];
     const uint32_t tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;
     const uint32_t n = a.count;
     Out *o = a.out;
@@ -611,52 +662,196 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
     __syncthreads();
     const uint32_t runs = (n + 64u * kRun - 1u) / (64u * kRun);
     if (wave == 0u) {
-        float w[kRun], nx[kRun];
-        load_run(a.probs, 0u, n, w);
-        for (uint32_t r = 0u; r < runs; ++r) {
-            load_run(a.probs, (r + 1u) * 64u * kRun, n, nx);
-#pragma unroll
-            for (int u = 0; u < kRun; ++u) {
-                sum2 = chain_f(sum2, w[u]);
-                w[u] = nx[u];
-            }
-        }
+        sum2 = serial_sum(a.probs, n, s_stage, sum2);
         if (lane == 0) s_f[2] = sum2;
     }
     __syncthreads();
     sum2 = s_f[2];
     if (!kq_isfinite(sum2) || !(sum2 > 0.0f)) return fail(o, KQ_SAMPLE_NUMERIC_BEFORE_DRAW);
+    /* The normalisation, by contiguous segments of whole 64-id chunks, one
+     * per wave. Each wave also forms what decides whether the draw's
+     * binary64 running sum is exact: when every p is a multiple of 2^-52
+     * and their total is at most 2, every running sum is a multiple of
+     * 2^-52 below 2, which binary64 holds exactly, so the sequential sums
+     * equal the exact prefix sums q = p * 2^52 summed as integers (in any
+     * order). Beside it: the segment's integer total and its last id with
+     * p > 0. */
+    const uint32_t nchunk = (n + 63u) / 64u;
+    const uint32_t per_wave = (nchunk + kTailThreads / 64u - 1u) / (kTailThreads / 64u);
+    const uint32_t seg0 = wave * per_wave * 64u, seg1 = min(n, (wave + 1u) * per_wave * 64u);
     {
         float maxp = 0.0f;
-        bool bad = false;
-        for (uint32_t i = tid; i < n; i += kTailThreads) {
-            const float w = a.probs[i];
-            if (w > 0.0f) {
-                const float p = w / sum2;
-                bad = bad || !kq_isfinite(p);
-                a.probs[i] = p;
-                maxp = fmaxf(maxp, p);
+        bool bad = false, exact = true;
+        int64_t qs = 0;
+        double ds = 0.0;
+        uint32_t lastw = 0xffffffffu;
+        for (uint32_t i0 = seg0; i0 < seg1; i0 += 64u) {
+            const uint32_t i = i0 + lane;
+            float p = 0.0f;
+            if (i < seg1) {
+                const float w = a.probs[i];
+                if (w > 0.0f) {
+                    p = w / sum2;
+                    bad = bad || !kq_isfinite(p);
+                    a.probs[i] = p;
+                    maxp = fmaxf(maxp, p);
+                }
             }
+            const double q = (double)p * 0x1p52;
+            exact = exact && q == __builtin_trunc(q);
+            qs += (int64_t)q;
+            ds += (double)p;
+            const uint64_t has = __ballot(p > 0.0f);
+            if (has) lastw = i0 + 63u - (uint32_t)__builtin_clzll(has);
         }
         for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)qs, off);
+            const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)((uint64_t)qs >> 32), off);
+            qs += (int64_t)(((uint64_t)hi << 32) | lo);
+        }
+        for (int off = 32; off > 0; off >>= 1) ds += __shfl_xor(ds, off);
         bad = __ballot(bad) != 0u;
-        if (lane == 0) s_max_p[wave] = bad ? -1.0f : maxp;
+        exact = __ballot(!exact) == 0u;
+        if (lane == 0) {
+            s_max_p[wave] = bad ? -1.0f : maxp;
+            s_qsum[wave] = qs;
+            s_dsum[wave] = ds;
+            s_ok[wave] = exact ? 1u : 0u;
+            s_last[wave] = lastw;
+        }
     }
     __syncthreads();
     if (wave != 0u) return;
     float maxp = lane < kTailThreads / 64u ? s_max_p[lane] : 0.0f;
     const bool bad = __ballot(maxp < 0.0f) != 0u;
     for (int off = 32; off > 0; off >>= 1) maxp = fmaxf(maxp, __shfl_xor(maxp, off));
-    /* one pass for the float mass of the normalised values and the binary64
-     * total the draw uses, both in id order; the total's running value at
-     * the end of every group of `every` runs is kept in LDS, so the draw
-     * walks only the group where the running sum first passes its
-     * threshold, starting from the value the full walk would hold there */
+    int64_t qtotal = 0;
+    bool exact = true;
+    uint32_t last = 0xffffffffu;
+    for (uint32_t wv = 0; wv < kTailThreads / 64u; ++wv) {
+        qtotal += s_qsum[wv];
+        exact = exact && s_ok[wv] != 0u;
+        if (s_last[wv] != 0xffffffffu) last = s_last[wv];
+    }
+    exact = exact && qtotal <= ((int64_t)1 << 53);
+    if (exact) {
+        /* the float mass of the normalised values, in id order, and the
+         * draw from the exact prefix sums */
+        norm_sum = serial_sum(a.probs, n, s_stage, norm_sum);
+        if (bad || !kq_isfinite(norm_sum) || !(norm_sum > 0.0f)) {
+            if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_BEFORE_DRAW;
+            return;
+        }
+        const double total = (double)qtotal * 0x1p-52;
+        const float last_p = last != 0xffffffffu ? a.probs[last] : 0.0f;
+        draw(o, total, last, last_p, a.word, [&](double thr, uint32_t &sel, float &selp) {
+            /* the first id whose prefix sum passes thr (it has p > 0: the
+             * prefix sums never decrease): the segment, then its chunk */
+            const double t52 = thr * 0x1p52;
+            int64_t base = 0;
+            uint32_t wv = 0;
+            for (; wv < kTailThreads / 64u; ++wv) {
+                if ((double)(base + s_qsum[wv]) > t52) break;
+                base += s_qsum[wv];
+            }
+            if (wv == kTailThreads / 64u) return;
+            const uint32_t b0 = wv * per_wave * 64u, b1 = min(n, (wv + 1u) * per_wave * 64u);
+            for (uint32_t i0 = b0; i0 < b1; i0 += 64u) {
+                const uint32_t i = i0 + lane;
+                const float p = i < b1 ? a.probs[i] : 0.0f;
+                const int64_t run = base + wave_scan_i64((int64_t)((double)p * 0x1p52));
+                const uint64_t hit = __ballot(i < b1 && (double)run > t52);
+                if (hit) {
+                    const int hl = __builtin_ctzll(hit);
+                    sel = i0 + (uint32_t)hl;
+                    selp = lane_f(p, hl);
+                    return;
+                }
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)run, 63);
+                const uint32_t hi =
+                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)run >> 32), 63);
+                base = (int64_t)(((uint64_t)hi << 32) | lo);
+            }
+        }, n - top_start, kept, maxp, norm_sum, a.canonical);
+        return;
+    }
+    /* Otherwise the sequential binary64 sums carry rounding, but for
+     * non-negative terms every running sum of the walk (and the total its
+     * threshold comes from) is within n u total of the exact prefix sum
+     * (u = 2^-53, recursive summation), and prefix sums formed here in any
+     * order are within the same bound. So when the threshold from these sums
+     * lies farther than M = (8 n + 8) u total from the sums just before and
+     * at the first id whose sum passes it, the walk selects that id too:
+     * the sums before it stay at or below its threshold, the one at it
+     * above. Any closer call takes the sequential walk below. */
+    if (!bad) {
+        double dtotal = 0.0;
+        for (uint32_t wv = 0; wv < kTailThreads / 64u; ++wv) dtotal += s_dsum[wv];
+        const double uniform = (double)a.word / 4294967296.0;
+        const double thr = uniform * dtotal;
+        const double margin = (8.0 * (double)n + 8.0) * 0x1p-53 * dtotal;
+        uint32_t cand = 0xffffffffu;
+        float cand_p = 0.0f;
+        bool sure = false;
+        if (kq_isfinite(dtotal) && dtotal > 0.0 && last != 0xffffffffu) {
+            double base = 0.0;
+            uint32_t wv = 0;
+            for (; wv < kTailThreads / 64u; ++wv) {
+                if (base + s_dsum[wv] > thr) break;
+                base += s_dsum[wv];
+            }
+            if (wv < kTailThreads / 64u) {
+                const uint32_t b0 = wv * per_wave * 64u, b1 = min(n, (wv + 1u) * per_wave * 64u);
+                for (uint32_t i0 = b0; i0 < b1; i0 += 64u) {
+                    const uint32_t i = i0 + lane;
+                    const float p = i < b1 ? a.probs[i] : 0.0f;
+                    double run = (double)p;
+#pragma unroll
+                    for (uint32_t o = 1u; o < 64u; o <<= 1) {
+                        const double v = __shfl_up(run, o, 64);
+                        if (lane >= o) run += v;
+                    }
+                    run += base;
+                    const uint64_t hit = __ballot(i < b1 && run > thr);
+                    if (hit) {
+                        const int hl = __builtin_ctzll(hit);
+                        const double at = lane_d(run, hl);
+                        const double before = hl > 0 ? lane_d(run, hl - 1) : base;
+                        cand = i0 + (uint32_t)hl;
+                        cand_p = lane_f(p, hl);
+                        sure = at - thr > margin && thr - before > margin;
+                        break;
+                    }
+                    base = lane_d(run, 63);
+                }
+            }
+        }
+        if (sure) {
+            norm_sum = serial_sum(a.probs, n, s_stage, norm_sum);
+            if (!kq_isfinite(norm_sum) || !(norm_sum > 0.0f)) {
+                if (lane == 0) o->status = KQ_SAMPLE_NUMERIC_BEFORE_DRAW;
+                return;
+            }
+            const float last_p = a.probs[last];
+            draw(o, dtotal, last, last_p, a.word, [&](double, uint32_t &sel, float &selp) {
+                sel = cand;
+                selp = cand_p;
+            }, n - top_start, kept, maxp, norm_sum, a.canonical);
+            return;
+        }
+    }
+    /* otherwise one pass for the float mass of the normalised values and
+     * the binary64 total the draw uses, both in id order; the total's
+     * running value at the end of every group of `every` runs is kept in
+     * LDS, so the draw walks only the group where the running sum first
+     * passes its threshold, starting from the value the full walk would
+     * hold there */
     double *s_cp = reinterpret_cast<double *>(s_w); /* kKeptCap / 2 entries */
     const uint32_t every = (runs + kKeptCap / 2u - 1u) / (kKeptCap / 2u);
     double total = 0.0;
-    uint32_t last = 0xffffffffu;
     float last_p = 0.0f;
+    last = 0xffffffffu;
     {
         float w[kRun], nx[kRun];
         load_run(a.probs, 0u, n, w);
