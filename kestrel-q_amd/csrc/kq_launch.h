@@ -320,6 +320,8 @@ typedef struct kq_launch_sample_args {
     void *sort_temp;
     size_t sort_bytes;   /* kq_launch_sample_sort_bytes(count) */
     kq_launch_sample_out *out;
+    uint32_t sequential_draw; /* nonzero: over many kept ids, always the
+                                 sequential binary64 walk (diagnostic) */
 } kq_launch_sample_args;
 
 hipError_t kq_launch_sample_sort_bytes(uint32_t count, size_t *bytes);

@@ -219,6 +219,7 @@ struct TailArgs {
     float top_p;
     uint32_t word;
     Out *out;
+    uint32_t sequential; /* the sequential walk even where a shortcut is certified */
 };
 
 /* ascending bitonic sort of one 64-bit value per lane across a wave (no
@@ -734,7 +735,7 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
         exact = exact && s_ok[wv] != 0u;
         if (s_last[wv] != 0xffffffffu) last = s_last[wv];
     }
-    exact = exact && qtotal <= ((int64_t)1 << 53);
+    exact = exact && qtotal <= ((int64_t)1 << 53) && !a.sequential;
     if (exact) {
         /* the float mass of the normalised values, in id order, and the
          * draw from the exact prefix sums */
@@ -785,7 +786,7 @@ __global__ __launch_bounds__(kTailThreads) void sample_tail(TailArgs a) {
      * at the first id whose sum passes it, the walk selects that id too:
      * the sums before it stay at or below its threshold, the one at it
      * above. Any closer call takes the sequential walk below. */
-    if (!bad) {
+    if (!bad && !a.sequential) {
         double dtotal = 0.0;
         for (uint32_t wv = 0; wv < kTailThreads / 64u; ++wv) dtotal += s_dsum[wv];
         const double uniform = (double)a.word / 4294967296.0;
@@ -948,6 +949,7 @@ static hipError_t launch_tail(const kq_launch_sample_args *p, uint32_t fast, hip
     a.top_p = p->top_p;
     a.word = p->word;
     a.out = p->out;
+    a.sequential = p->sequential_draw;
     hipLaunchKernelGGL(sample_tail, dim3(1), dim3(kTailThreads), 0, s, a);
     return hipGetLastError();
 }

@@ -362,6 +362,14 @@ static kq_status run_select(kq_hip_context *ctx, const kq_hip_sampling_config *c
     a.sort_temp = l.sort_temp;
     a.sort_bytes = (size_t)cfg->sort_bytes;
     a.out = l.out;
+    /* KQ_HIP_SAMPLE_SEQUENTIAL=1: every draw over many kept ids takes the
+     * sequential binary64 walk rather than the parallel prefix sums that
+     * are certified to select the same id (a diagnostic: the tests run the
+     * two and compare them with the oracle) */
+    {
+        const char *seq = getenv("KQ_HIP_SAMPLE_SEQUENTIAL");
+        a.sequential_draw = seq != NULL && seq[0] == '1' ? 1u : 0u;
+    }
     e = (int)kq_launch_sample(&a, (hipStream_t)kqi_context_stream_ptr(ctx));
     if (e == 0)
         e = (int)hipMemcpyAsync(&rec, l.out, sizeof(rec), hipMemcpyDeviceToHost,

@@ -158,6 +158,32 @@ def test_seeded_logits_full_vocabulary(ctx, pi):
     s.close()
 
 
+@pytest.mark.parametrize("sequential", [False, True], ids=["certified", "sequential"])
+def test_many_kept_draw_paths(ctx, monkeypatch, sequential):
+    # Over more kept ids than the LDS sort holds, the draw's binary64 walk
+    # is replaced by parallel prefix sums when they are exact or when the
+    # threshold clears the summation error bound; KQ_HIP_SAMPLE_SEQUENTIAL=1
+    # forces the sequential walk. Both must give the oracle's draw, on
+    # spreads where the prefix sums are exact (all probabilities multiples
+    # of 2^-52: equal logits) and where they are not (N(0, s) logits, and
+    # weights down to underflow).
+    if sequential:
+        monkeypatch.setenv("KQ_HIP_SAMPLE_SEQUENTIAL", "1")
+    rng = np.random.default_rng(4242)
+    cases = [np.full(VOCAB, 0.25, np.float32)]
+    cases += [(rng.standard_normal(VOCAB) * sd).astype(np.float32) for sd in (0.5, 1.0, 3.0)]
+    under = -np.linspace(0.0, 120.0, VOCAB, dtype=np.float32)
+    rng.shuffle(under)
+    cases.append(under)
+    for pol in ({"temperature": 1.0, "top_k": 0, "top_p": 1.0},
+                {"temperature": 0.8, "top_k": 0, "top_p": 0.7}):
+        s = Sampler(ctx, pol)
+        for ci, lg in enumerate(cases):
+            for seed in range(4):
+                check_against_oracle(s, lg, 31 * ci + seed, 9, work=seed == 0)
+        s.close()
+
+
 # vocabularies around the wave (64), the prep block (256), the in-LDS
 # kept-id sort's capacity (4096) and the draw's 2048 LDS checkpoints of 512
 # ids each (past 1,048,576 ids a checkpoint covers several runs)
