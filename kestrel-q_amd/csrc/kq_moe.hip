@@ -973,6 +973,102 @@ __device__ __forceinline__ void exact_rows(const float *__restrict__ router,
     __syncthreads();
 }
 
+/* Exact chains of every logit row (experts rows, then the shared gate
+ * vector as row `experts`; experts + 1 <= 1024) by a workgroup of 1024
+ * threads, each row's chain on its own lane: stage s forms the rounded
+ * products w * x (as the CPU forms them) of columns C s .. C s + C - 1 of
+ * every row into LDS (a float4 of up to K rows per thread, the next
+ * stage's loads in flight; the activations from an LDS copy), and thread r
+ * adds its row's C products to its chain, left to right, one barrier per
+ * stage. C = 16 while two stages of rows fit kAllFloats, else 8. The
+ * chains of the rows run side by side, so the route costs one row's chain
+ * (HIDDEN dependent adds) plus the staging, instead of one per 64 rows.
+ * logits[r] (r < experts) and *shared_logit get the results. */
+constexpr uint32_t kAllFloats = 2u * 1024u * 9u; /* LDS floats of the stages */
+
+template <uint32_t HIDDEN, uint32_t C>
+__device__ __forceinline__ void exact_all_rows_c(const float *__restrict__ router,
+                                                 const float *__restrict__ sgw,
+                                                 const float *__restrict__ x, uint32_t experts,
+                                                 float *stage, const float *xs, float *logits,
+                                                 float *shared_logit, uint32_t *status) {
+    static_assert(HIDDEN % C == 0u && C % 8u == 0u, "whole stages of float4 pairs");
+    constexpr uint32_t NS = HIDDEN / C, P = C + 1u; /* odd pitch: conflict-free chain reads */
+    constexpr uint32_t Q = C / 4u;                  /* float4 per row and stage */
+    /* thread t stages float4 q = t % Q of rows t / Q + k (1024 / Q), k < K:
+     * rows <= 542 at C = 16, <= 1024 at C = 8 */
+    constexpr uint32_t RPP = 1024u / Q;
+    constexpr uint32_t MAXR = C == 16u ? 542u : 1024u;
+    constexpr uint32_t K = (MAXR + RPP - 1u) / RPP;
+    const uint32_t t = threadIdx.x, rows = experts + 1u;
+    const uint32_t half = (uint32_t)kAllFloats / 2u;
+    const uint32_t q = t % Q, r0 = t / Q;
+    bool bad = false;
+    float4 wv[K];
+    auto load = [&](uint32_t s) {
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            const uint32_t r = r0 + k * RPP;
+            if (r < rows) {
+                const float *row = r < experts ? router + (size_t)r * HIDDEN : sgw;
+                wv[k] = *(const float4 *)(row + C * s + 4u * q);
+            }
+        }
+    };
+    float acc = 0.0f;
+    load(0u);
+    for (uint32_t s = 0; s < NS; ++s) {
+        float *buf = stage + (s & 1u) * half;
+        const float4 xv = *(const float4 *)(xs + C * s + 4u * q);
+#pragma unroll
+        for (uint32_t k = 0; k < K; ++k) {
+            const uint32_t r = r0 + k * RPP;
+            if (r < rows) {
+                const float4 w = wv[k];
+                bad |= !kq_isfinite(w.x) || !kq_isfinite(w.y) || !kq_isfinite(w.z) ||
+                       !kq_isfinite(w.w);
+                float *d = buf + r * P + 4u * q;
+                d[0] = w.x * xv.x;
+                d[1] = w.y * xv.y;
+                d[2] = w.z * xv.z;
+                d[3] = w.w * xv.w;
+            }
+        }
+        if (s + 1u < NS) load(s + 1u);
+        __syncthreads();
+        if (t < rows) {
+            const float *src = buf + t * P;
+#pragma unroll
+            for (uint32_t j = 0; j < C; ++j) acc = acc + src[j];
+        }
+    }
+    if (t < experts)
+        logits[t] = acc;
+    else if (t == experts)
+        *shared_logit = acc;
+    if (bad) kq_flag(status, KQ_DEV_INPUT);
+    __syncthreads();
+}
+
+template <uint32_t HIDDEN>
+__device__ __forceinline__ void exact_all_rows(const float *__restrict__ router,
+                                               const float *__restrict__ sgw,
+                                               const float *__restrict__ x, uint32_t experts,
+                                               float *logits, float *shared_logit,
+                                               uint32_t *status) {
+    __shared__ float stage[kAllFloats];
+    __shared__ __align__(16) float xs[HIDDEN];
+    for (uint32_t i = threadIdx.x; i < HIDDEN / 4u; i += blockDim.x)
+        reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(x)[i];
+    __syncthreads();
+    if (2u * (experts + 1u) * 17u <= kAllFloats)
+        exact_all_rows_c<HIDDEN, 16u>(router, sgw, x, experts, stage, xs, logits, shared_logit,
+                                      status);
+    else
+        exact_all_rows_c<HIDDEN, 8u>(router, sgw, x, experts, stage, xs, logits, shared_logit,
+                                     status);
+}
+
 /* Ranks (descending value, ascending id) of two entries (m0, i0), (m1, i1)
  * among the first `count` entries of v/id, in eight-entry runs of LDS
  * broadcast reads. Entries past count read as (-inf, max id). */
@@ -1192,20 +1288,9 @@ __device__ __forceinline__ void select_one(const RouteArgs &a) {
         }
     }
     if (state == 3u) {
-        /* every row's chain, 64 rows at a time, then the route finish */
-        for (uint32_t r0 = 0; r0 <= experts; r0 += 64u) {
-            const uint32_t n = experts + 1u - r0 < 64u ? experts + 1u - r0 : 64u;
-            if (e < n) cid[e] = r0 + e;
-            __syncthreads();
-            exact_rows<HIDDEN>(a.router, a.sgw, a.x, experts, cid, n, ex_l, a.status);
-            if (e < n) {
-                if (r0 + e < experts)
-                    a.logits[r0 + e] = ex_l[e];
-                else
-                    *a.shared_logit = ex_l[e];
-            }
-            __syncthreads();
-        }
+        /* every row's chain, all rows side by side, then the route finish */
+        exact_all_rows<HIDDEN>(a.router, a.sgw, a.x, experts, a.logits, a.shared_logit,
+                               a.status);
         route_finish_body(0u, a.logits, a.shared_logit, experts, top_k, a.probs, a.ids,
                           a.weights, a.order, a.shared_scale, a.status);
         __syncthreads();
