@@ -45,6 +45,7 @@
  */
 #include "kq_launch.h"
 #include "kq_device.h"
+#include "kq_dma.h"
 
 namespace {
 
@@ -1157,20 +1158,28 @@ hipError_t pass_any(uint32_t type, uint32_t kdim, const uint8_t *W0, const uint8
  *
  * The row engine keeps every lane's activations in registers, 32 per batch
  * column; at 4 columns that leaves no room for the weights in flight. Here
- * the columns ride on the token dimension of the same 16x16x16 steps as the
- * grouped down pass (Tile<Q6_K>): they are staged once per workgroup as
- * fp16 hi + lo after an exact power-of-two scaling (an LDS image of
- * kMvCols rows), and lane l keeps row l % 16 of a 16-row tile for columns
- * 4 (l / 16) .. + 3 -- lanes 0..15 hold every real column.
+ * the columns ride on the token dimension of 16x16x32 matrix steps: they are
+ * staged once per workgroup as fp16 hi + lo after an exact power-of-two
+ * scaling (an LDS image of kMvCols rows). The four columns' hi and lo parts
+ * fill 8 token rows, so one step carries two 16-column sub-blocks of the
+ * block: token rows 0..7 hold the first sub-block's activations on k 0..15
+ * (zeros on k 16..31) and rows 8..15 the second's on k 16..31. Each product
+ * row then belongs to one sub-block, and lane l keeps row l % 16 of a
+ * 16-row tile for the four token rows 4 (l / 16) .. + 3: its sub-block's
+ * scale applies to all four.
  *
- * Weights: the MFMA operand wants twelve scattered 4-byte pieces of a block
- * per lane, which as global loads would touch 16 rows per instruction. So
- * each wave streams one block of its tile's 16 rows (16 windows of 224
- * bytes from the block's aligned start) with four contiguous 16-byte loads
- * per lane, two blocks ahead of the one it multiplies, into a private LDS
- * slot, and reads the operand pieces from there. The per-row fp32 sums are
- * compared with the CPU by tolerance; the argmax partials (largest value,
- * lowest row on ties) are exact over them. */
+ * Weights: the MFMA operand wants scattered 4-byte pieces of a block per
+ * lane, which as global loads would touch 16 rows per instruction. So each
+ * wave streams one block of its tile's 16 rows at a time (16 windows of 224
+ * bytes from the block's aligned start) with four LDS-DMA loads straight
+ * into a ring of NS private LDS slots, NS - 1 blocks ahead of the one it
+ * multiplies, and reads the operand pieces from there. Eight waves with a
+ * four-slot ring fill the LDS beside the activation image at 2,048 columns;
+ * on the 151936 x 2048 LM head at 4 columns this was faster than 4, 6, 10,
+ * 12 or 16 waves with the rings that fit them (92.7, 84.2, 77.6, 81.3 and
+ * 82.1 us against 70.9-75.6 us). The per-row fp32 sums are compared with
+ * the CPU by tolerance; the argmax partials (largest value, lowest row on
+ * ties) are exact over them. */
 
 constexpr uint32_t kMvCols = 4;      /* staged activation columns */
 constexpr int kMvWaves = 8;          /* waves per workgroup */
@@ -1180,6 +1189,11 @@ constexpr uint32_t kMvPitch = 240u;  /* slot row pitch: lanes (j, g) hit distinc
 constexpr uint32_t kMvSlot = kTile * kMvPitch;
 constexpr uint32_t kMvUnits = kTile * (kMvWin / 16u); /* 16-byte loads per block: 224 */
 constexpr int kMvLoads = (int)((kMvUnits + 63u) / 64u); /* per lane: 4 */
+constexpr uint32_t kMvUnitsPerRow = kMvPitch / 16u; /* 15: 14 window units + 1 gap */
+constexpr int kMvDma = (int)((kMvSlot / 16u + 63u) / 64u); /* DMA loads per block: 4 */
+constexpr uint32_t kMvZero = 256u; /* fp16 zeros: k 8 g + 128 n + 32 q .. + 7 < 256 */
+constexpr uint32_t kMvLdsMax = 160u * 1024u;
+constexpr uint32_t kMvMaxSlots = 4u; /* block slots per wave, at most */
 
 __device__ __forceinline__ void mv_argmax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
     if (v > bv || (v == bv && i < bi)) {
@@ -1192,6 +1206,14 @@ __device__ __forceinline__ void mv_argmax_merge(float &bv, uint32_t &bi, float v
  * reads of a step on distinct banks) */
 __host__ __device__ __forceinline__ uint32_t mv_xpitch(uint32_t nb) { return nb * 256u + 16u; }
 
+__host__ __device__ __forceinline__ uint32_t mv_lds_bytes(uint32_t nb, uint32_t ns) {
+    return 2u * kMvCols * mv_xpitch(nb) * 2u + kMvCols * 4u + kMvZero * 2u +
+           (uint32_t)kMvWaves * ns * kMvSlot;
+}
+
+/* NS block slots per wave: block it is multiplied from slot it % NS while
+ * blocks it + 1 .. it + NS - 1 are in flight */
+template <uint32_t NS>
 __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
     const uint8_t *__restrict__ W, uint32_t rows, uint32_t nb, const float *__restrict__ x,
     uint32_t batch, float *__restrict__ y, uint32_t *status, float *part_v, uint32_t *part_i,
@@ -1201,7 +1223,11 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
     const uint32_t K = nb * 256u, pitch = mv_xpitch(nb);
     _Float16 *xh = mv_lds, *xl = mv_lds + kMvCols * pitch;
     int *sig = (int *)(xl + kMvCols * pitch);
-    uint8_t *slots = (uint8_t *)(sig + kMvCols);
+    /* the zero operand of the token rows off their sub-block (16 bytes past
+     * a 32-byte boundary of the x image, so its broadcast reads sit on the
+     * banks the live rows leave free) */
+    _Float16 *xz = (_Float16 *)(sig + kMvCols);
+    uint8_t *slots = (uint8_t *)(xz + kMvZero);
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1210,18 +1236,15 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
     const uint32_t nwaves = gridDim.x * (uint32_t)kMvWaves;
     const uint32_t rb = nb * F::kBytes;
     const uint32_t wbytes = rows * rb;
-    const KqBuf wb = kq_buf(W, wbytes);
+    const kq_i4v wr = dma_rsrc(W, wbytes);
     const uint32_t ntiles = (rows + kTile - 1u) / kTile;
-    uint8_t *myslot = slots + wave * 2u * kMvSlot;
+    uint8_t *myslot = slots + wave * NS * kMvSlot;
+    const uint32_t myslot_lds = lds_addr(myslot);
 
     /* Work item it = block it % nb of tile gw + nwaves * (it / nb), walked
      * with counters (t, b) and the tile's byte offset tb = 16 t rb (no
      * division or 32-bit multiply per item; tb is used only while
-     * t < ntiles, where it stays below wbytes). Its loads: unit
-     * e = i * 64 + lane of the 224 = 16 rows x 14 covers bytes [16u, 16u +
-     * 16) of row e / 14's window (the block's start rounded down to 4
-     * bytes); rows past the matrix, and the 32 spare units, read far past
-     * the buffer (zeros). */
+     * t < ntiles, where it stays below wbytes). */
     struct Pos {
         uint32_t t, b, tb;
     };
@@ -1233,40 +1256,47 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
             q.tb += tstep;
         }
     };
-    uint32_t ld_r[kMvLoads], ld_rb[kMvLoads], ld_u[kMvLoads];
+    /* A block's DMA: load i, lane l writes slot bytes [16 p, 16 p + 16) with
+     * p = 64 i + l, which is unit p % 15 of row p / 15 (row pitch 240: 14
+     * units of the row's window -- the block's start rounded down to 4
+     * bytes -- and a gap). Gap units and rows past the matrix read the
+     * matrix's first bytes instead (whatever lands there is never a result:
+     * gap bytes are not read, and rows past the matrix are not stored); the
+     * last load runs on the 48 lanes that reach the slot's 3,840 bytes. */
+    uint32_t ld_r[kMvDma], ld_rb[kMvDma], ld_u[kMvDma];
 #pragma unroll
-    for (int i = 0; i < kMvLoads; ++i) {
-        const uint32_t e = (uint32_t)i * 64u + lane;
-        ld_r[i] = e < kMvUnits ? e / 14u : 0xffffu; /* spare units: no row */
-        ld_u[i] = 16u * (e - 14u * (e / 14u));
-        ld_rb[i] = (e / 14u) * rb;
+    for (int i = 0; i < kMvDma; ++i) {
+        const uint32_t p = (uint32_t)i * 64u + lane;
+        const uint32_t r = p / kMvUnitsPerRow, u = p - kMvUnitsPerRow * r;
+        ld_r[i] = (r < kTile && u * 16u < kMvWin) ? r : 0xffffu;
+        ld_u[i] = 16u * u;
+        ld_rb[i] = r * rb;
     }
-    typedef kq_u32x4 MvLd[kMvLoads];
-    auto load_item = [&](const Pos &q, MvLd &v) {
+    auto dma_item = [&](const Pos &q, uint32_t slot) {
+        const uint32_t dst = myslot_lds + slot * kMvSlot;
 #pragma unroll
-        for (int i = 0; i < kMvLoads; ++i) {
+        for (int i = 0; i < kMvDma; ++i) {
             const uint32_t row = q.t * kTile + ld_r[i];
             const uint32_t o = q.tb + ld_rb[i] + q.b * F::kBytes;
             const uint32_t off =
-                (ld_r[i] < kTile && q.t < ntiles && row < rows) ? (o & ~3u) + ld_u[i]
-                                                                 : wbytes + 256u;
-            v[i] = __builtin_amdgcn_raw_buffer_load_b128(wb.r, (int)off, 0, 0);
+                (ld_r[i] < kTile && q.t < ntiles && row < rows) ? (o & ~3u) + ld_u[i] : ld_u[i];
+            if ((uint32_t)i * 64u + 64u <= kMvSlot / 16u) {
+                dma16(wr, off, dst + 1024u * (uint32_t)i);
+            } else if ((uint32_t)i * 64u + lane < kMvSlot / 16u) {
+                dma16(wr, off, dst + 1024u * (uint32_t)i);
+            }
         }
     };
-    auto store_item = [&](uint32_t slot, const MvLd &v) {
-#pragma unroll
-        for (int i = 0; i < kMvLoads; ++i)
-            if (ld_r[i] < kTile)
-                *(kq_u32x4 *)(myslot + slot * kMvSlot + ld_r[i] * kMvPitch + ld_u[i]) = v[i];
-    };
 
-    /* the first two items are requested before the staging */
-    MvLd va, vb;
+    /* the first block is requested before the staging, the next NS - 1
+     * after it (the staging's own loads wait for every load issued before
+     * theirs) */
+    const uint32_t nitems = ntiles > gw ? ((ntiles - gw + nwaves - 1u) / nwaves) * nb : 0u;
     Pos ld = {gw, 0u, gw * kTile * rb}, pr = ld;
-    load_item(ld, va);
-    advance(ld);
-    load_item(ld, vb);
-    advance(ld);
+    if (nitems > 0u) {
+        dma_item(ld, 0u);
+        advance(ld);
+    }
 
     /* stage column i (one wave each): scale by 2^sig[i], split into hi + lo */
     bool bad = false;
@@ -1301,9 +1331,14 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
         }
         if (lane == 0u) sig[i] = e;
     }
-    store_item(0u, va);
-    load_item(ld, va);
-    advance(ld);
+    if (threadIdx.x < kMvZero / 8u) *(h8 *)(xz + 8u * threadIdx.x) = h8{};
+#pragma unroll
+    for (uint32_t sl = 1u; sl < NS; ++sl) {
+        if (sl < nitems) {
+            dma_item(ld, sl);
+            advance(ld);
+        }
+    }
     kq_lds_barrier();
     int unscale[4];
 #pragma unroll
@@ -1317,83 +1352,114 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
         best_v[k] = -__builtin_inff();
         best_i[k] = 0xffffffffu;
     }
-    /* Lane l supplies token row j = l % 16 of the A operand: rows 0..3 are
-     * the hi parts of columns 0..3, rows 4..7 their lo parts, and rows
-     * 8..15 repeat rows 0..7. Row t of a product depends on row t of A
-     * only, so one step gives the hi products to lanes 0..15 and the lo
-     * products to lanes 16..31 (both scaled and summed per row); lanes
-     * 32..63 are never used and need no zero fill. */
-    const _Float16 *xa = ((j & 4u) ? xl : xh) + (j & 3u) * pitch;
+    /* Lane l supplies token row j = l % 16 of the A operand on k 8 (l / 16)
+     * .. + 7: rows 0..3 are the hi parts of columns 0..3, rows 4..7 their lo
+     * parts, rows 8..15 repeat them for the step's second sub-block. Lanes
+     * whose k range belongs to the other sub-block read zeros. Product rows
+     * 4 (l / 16) .. + 3 in lane l are then: l / 16 = 0 hi and 1 lo of the
+     * first sub-block, 2 hi and 3 lo of the second. */
+    const bool live = (j >> 3) == (g >> 1);
+    const _Float16 *xa = live ? ((j & 4u) ? xl : xh) + (j & 3u) * pitch + 8u * g : xz + 8u * g;
+    const uint32_t xstep = live ? 256u : 0u;
+    const uint32_t hsh = 8u * (g >> 1); /* this lane's scale byte within a pair */
     const h2 bias = h2{(_Float16)-1056.0f, (_Float16)-1056.0f}; /* 1024 + 32 */
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 
-    /* item it from its slot: 16 sub-block steps into acc; at the tile's
-     * last block lanes 0..15 write row t*16 + j of columns 0 .. batch-1 */
+    /* item from its slot: 8 two-sub-block steps into acc; at the tile's last
+     * block lanes 0..15 write row t*16 + j of columns 0 .. batch-1. Every LDS
+     * read of the item is issued before its first product. */
     const uint32_t jrb = j * rb;
-    auto process = [&](const Pos &q, uint32_t slot) {
+    auto process = [&](const Pos &q, const uint8_t *sp, auto &&refill) {
         const uint32_t bb = q.b;
         const uint32_t row = q.t * kTile + j;
         const uint32_t sh = (q.tb + jrb + bb * F::kBytes) & 3u;
-        const uint8_t *p = myslot + slot * kMvSlot + j * kMvPitch;
+        const uint8_t *p = sp + j * kMvPitch;
         auto w32 = [&](uint32_t o) { return *(const uint32_t *)(p + o); };
-        const float d = (float)*(const _Float16 *)(p + sh + 208u);
-        malformed |= !kq_isfinite(d);
-        uint32_t sc[4];
-        {
-            const uint32_t s0 = w32(192u), s1 = w32(196u), s2 = w32(200u), s3 = w32(204u),
-                           s4 = w32(208u);
-            sc[0] = kq_align2(s1, s0, sh);
-            sc[1] = kq_align2(s2, s1, sh);
-            sc[2] = kq_align2(s3, s2, sh);
-            sc[3] = kq_align2(s4, s3, sh);
-        }
-        const _Float16 *pa = xa + 256u * bb + 4u * g;
+        /* columns 128 n + 32 q + 8 g .. + 7 of step (n, q): ql bytes 64 n +
+         * 8 g (q = 0, 2) and + 32 (q = 1, 3), qh bytes 128 + 32 n + 8 g; the
+         * scales at 192 and d at 208 (the window starts up to 3 bytes early) */
+        uint32_t wa[2][3], wbv[2][3], wq[2][3], ws[6];
 #pragma unroll
-        for (uint32_t nh = 0; nh < 4u; ++nh) {
-            const uint32_t n = nh >> 1, h = nh & 1u;
-            const uint32_t oa = 64u * n + 16u * h + 4u * g;
-            const uint32_t oq = 128u + 32u * n + 16u * h + 4u * g;
-            const uint32_t A = kq_align2(w32(oa + 4u), w32(oa), sh);
-            const uint32_t B = kq_align2(w32(oa + 36u), w32(oa + 32u), sh);
-            const uint32_t H = kq_align2(w32(oq + 4u), w32(oq), sh);
-            uint32_t c[4];
-            c[0] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
-            c[1] = (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
-            c[2] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
-            c[3] = ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
-            /* the group's four steps are independent products: all four
-             * are issued before any result is scaled, so the matrix core's
-             * latency overlaps the next products and the scaling */
+        for (uint32_t n = 0; n < 2u; ++n) {
+            const uint32_t oa = 64u * n + 8u * g, oq = 128u + 32u * n + 8u * g;
+#pragma unroll
+            for (uint32_t e = 0; e < 3u; ++e) {
+                wa[n][e] = w32(oa + 4u * e);
+                wbv[n][e] = w32(oa + 32u + 4u * e);
+                wq[n][e] = w32(oq + 4u * e);
+            }
+        }
+#pragma unroll
+        for (uint32_t e = 0; e < 6u; ++e) ws[e] = w32(192u + 4u * e);
+        const _Float16 *pa = xa + xstep * bb;
+        h8 av[2][4];
+#pragma unroll
+        for (uint32_t n = 0; n < 2u; ++n)
+#pragma unroll
+            for (uint32_t qq = 0; qq < 4u; ++qq) av[n][qq] = *(const h8 *)(pa + 128u * n + 32u * qq);
+        /* every read of the slot has landed: its next block can be requested
+         * before the products */
+        wait_lgkm0();
+        refill();
+        __builtin_amdgcn_sched_barrier(0);
+
+        const float d = f16f(kq_align2(ws[5], ws[4], sh)); /* block bytes 208, 209 */
+        malformed |= row < rows && !kq_isfinite(d);
+        uint32_t sc[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) sc[e] = kq_align2(ws[e + 1u], ws[e], sh) >> hsh;
+#pragma unroll
+        for (uint32_t n = 0; n < 2u; ++n) {
+            const uint32_t A[2] = {kq_align2(wa[n][1], wa[n][0], sh),
+                                   kq_align2(wa[n][2], wa[n][1], sh)};
+            const uint32_t B[2] = {kq_align2(wbv[n][1], wbv[n][0], sh),
+                                   kq_align2(wbv[n][2], wbv[n][1], sh)};
+            const uint32_t H[2] = {kq_align2(wq[n][1], wq[n][0], sh),
+                                   kq_align2(wq[n][2], wq[n][1], sh)};
+            uint32_t c[4][2];
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                c[0][w] = (A[w] & 0x0f0f0f0fu) | ((H[w] << 4) & 0x30303030u);
+                c[1][w] = (B[w] & 0x0f0f0f0fu) | ((H[w] << 2) & 0x30303030u);
+                c[2][w] = ((A[w] >> 4) & 0x0f0f0f0fu) | (H[w] & 0x30303030u);
+                c[3][w] = ((B[w] >> 4) & 0x0f0f0f0fu) | ((H[w] >> 2) & 0x30303030u);
+            }
+            /* the four steps are independent products: all are issued
+             * before any result is scaled, so the matrix core's latency
+             * overlaps the next products and the scaling */
             f4 tm[4];
 #pragma unroll
-            for (uint32_t q = 0; q < 4u; ++q) {
-                const uint32_t ko = 128u * n + 32u * q + 16u * h;
-                const h4 av = *(const h4 *)(pa + ko);
-                const h2 w0 = bytes_lo(c[q]) + bias, w1 = bytes_hi(c[q]) + bias;
-                const h4 bw = h4{w0.x, w0.y, w1.x, w1.y};
-                tm[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bw, f4{0.f, 0.f, 0.f, 0.f}, 0,
-                                                             0, 0);
+            for (uint32_t qq = 0; qq < 4u; ++qq) {
+                const h2 w0 = bytes_lo(c[qq][0]) + bias, w1 = bytes_hi(c[qq][0]) + bias;
+                const h2 w2 = bytes_lo(c[qq][1]) + bias, w3 = bytes_hi(c[qq][1]) + bias;
+                const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+                tm[qq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[n][qq], bw,
+                                                                f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             }
 #pragma unroll
-            for (uint32_t q = 0; q < 4u; ++q) {
-                const uint32_t s = 8u * n + 2u * q + h;
-                const int8_t scv = (int8_t)((sc[s >> 2] >> (8u * (s & 3u))) & 0xffu);
+            for (uint32_t qq = 0; qq < 4u; ++qq) {
+                /* sub-block 8 n + 2 qq + (g >> 1): byte (2 qq) & 3 of word
+                 * 2 n + qq / 2, pre-shifted by this lane's half */
+                const int8_t scv = (int8_t)((sc[2u * n + (qq >> 1)] >> (16u * (qq & 1u))) & 0xffu);
                 const float ds = d * (float)scv;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] = fmaf(ds, tm[q][k], acc[k]);
+                for (int k = 0; k < 4; ++k) acc[k] = fmaf(ds, tm[qq][k], acc[k]);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
         if (bb + 1u == nb) {
-            /* column k of row j = hi sum (lane j) + lo sum (lane j + 16) */
-            f4 lo;
+            /* column k of row j = the four lanes j + 16 G: hi and lo of both
+             * sub-block halves */
+            f4 o;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) lo[k] = __shfl_down(acc[k], 16, KQ_WAVE);
+            for (int k = 0; k < 4; ++k) o[k] = acc[k] + __shfl_down(acc[k], 32, KQ_WAVE);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] += __shfl_down(o[k], 16, KQ_WAVE);
             if (g == 0u && row < rows) {
 #pragma unroll
                 for (uint32_t k = 0; k < 4u; ++k) {
                     if (k < batch) {
-                        const float v = ldexpf(acc[k] + lo[k], unscale[k]);
+                        const float v = ldexpf(o[k], unscale[k]);
                         nonfinite |= !kq_isfinite(v);
                         y[(size_t)k * rows + row] = v;
                         mv_argmax_merge(best_v[k], best_i[k], v, row);
@@ -1403,22 +1469,22 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
             acc = f4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    /* Item it is multiplied from slot it % 2 while items it + 1 and it + 2
-     * are in flight (registers vb and va for even it); then it + 1 goes to
-     * the other slot and it + 3 is requested. */
-    const uint32_t nitems = ntiles > gw ? ((ntiles - gw + nwaves - 1u) / nwaves) * nb : 0u;
-    for (uint32_t it = 0u; it < nitems; it += 2u) {
-        process(pr, 0u);
+    /* Before block it: every DMA issued after its own has not necessarily
+     * landed, and there are min(NS - 1, nitems - 1 - it) of them (kMvDma
+     * loads each; the y stores between are not loads). Once its reads are
+     * in registers, its slot takes block it + NS. */
+    uint32_t slot = 0u;
+    for (uint32_t it = 0u; it < nitems; ++it) {
+        const uint32_t after = nitems - 1u - it;
+        wait_after<(uint32_t)kMvDma, NS - 1u>(after);
+        process(pr, myslot + slot * kMvSlot, [&]() {
+            if (it + NS < nitems) {
+                dma_item(ld, slot);
+                advance(ld);
+            }
+        });
         advance(pr);
-        store_item(1u, vb);
-        load_item(ld, vb);
-        advance(ld);
-        if (it + 1u >= nitems) break;
-        process(pr, 1u);
-        advance(pr);
-        store_item(0u, va);
-        load_item(ld, va);
-        advance(ld);
+        slot = slot + 1u == NS ? 0u : slot + 1u;
     }
     if (bad) kq_flag(status, KQ_DEV_INPUT);
     if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
@@ -1445,11 +1511,6 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
             }
         }
     }
-}
-
-size_t mv_lds_bytes(uint32_t nb) {
-    return (size_t)2u * kMvCols * mv_xpitch(nb) * sizeof(_Float16) + kMvCols * sizeof(int) +
-           (size_t)kMvWaves * 2u * kMvSlot;
 }
 
 /* ------------------------------------------------------------------ */
@@ -1820,20 +1881,41 @@ extern "C" int kq_launch_matvec_mfma_supported(uint32_t type, uint32_t rows, uin
            cols >= 256u && cols <= kMvMaxK && rows >= 65536u && bytes <= 0xfffff000ull;
 }
 
+/* block slots per wave: as many (2 .. kMvMaxSlots) as fit beside the
+ * activation image */
+static uint32_t mv_ns(uint32_t nb) {
+    uint32_t ns = kMvMaxSlots;
+    while (ns > 2u && mv_lds_bytes(nb, ns) > kMvLdsMax) --ns;
+    return ns;
+}
+/* f(std::integral_constant<uint32_t, ns>) for ns in 2 .. kMvMaxSlots */
+template <uint32_t NS = 2u, typename Fn>
+static void kq_mv_ns_dispatch(uint32_t ns, Fn &&f) {
+    if constexpr (NS <= kMvMaxSlots) {
+        if (ns == NS) f(std::integral_constant<uint32_t, NS>{});
+        else kq_mv_ns_dispatch<NS + 1u>(ns, f);
+    }
+}
+template <uint32_t NS>
+static hipError_t mv_occupancy(int *n, uint32_t nb) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, matvec_mfma_q6k<NS>, kMvWaves * 64,
+                                                         mv_lds_bytes(nb, NS));
+}
+
 /* a resident grid (workgroups that fit at once), capped by the tile count */
 static uint32_t mv_blocks(uint32_t rows, uint32_t nb) {
     static uint32_t per_cu_cache[kMvMaxK / 256u + 1u];
     uint32_t &per = per_cu_cache[nb];
     if (per == 0u) {
         int dev = 0, cus = 0, n = 0;
+        const uint32_t ns = mv_ns(nb);
+        hipError_t oe = hipErrorInvalidValue;
+        kq_mv_ns_dispatch(ns, [&](auto c) { oe = mv_occupancy<decltype(c)::value>(&n, nb); });
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             cus < 1)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_mfma_q6k, kMvWaves * 64,
-                                                         mv_lds_bytes(nb)) != hipSuccess ||
-            n < 1)
-            n = 1;
+        if (oe != hipSuccess || n < 1) n = 1;
         per = (uint32_t)(n * cus);
     }
     const uint32_t tiles = (rows + kTile - 1u) / kTile;
@@ -1851,8 +1933,13 @@ extern "C" hipError_t kq_launch_matvec_mfma(const void *W, uint32_t rows, uint32
                                             uint32_t *status, float *part_v, uint32_t *part_i,
                                             uint32_t part_stride, hipStream_t stream) {
     const uint32_t nb = cols / 256u;
-    hipLaunchKernelGGL(matvec_mfma_q6k, dim3(mv_blocks(rows, nb)), dim3(kMvWaves * 64),
-                       mv_lds_bytes(nb), stream, (const uint8_t *)W, rows, nb, x, batch, y,
-                       status, part_v, part_i, part_stride);
+    const uint32_t ns = mv_ns(nb);
+    const dim3 grid(mv_blocks(rows, nb)), block(kMvWaves * 64);
+#define KQ_MV(NS)                                                                              \
+    hipLaunchKernelGGL(matvec_mfma_q6k<NS>, grid, block, mv_lds_bytes(nb, NS), stream,         \
+                       (const uint8_t *)W, rows, nb, x, batch, y, status, part_v, part_i,      \
+                       part_stride)
+    kq_mv_ns_dispatch(ns, [&](auto c) { KQ_MV(decltype(c)::value); });
+#undef KQ_MV
     return hipGetLastError();
 }

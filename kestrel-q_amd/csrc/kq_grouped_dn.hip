@@ -30,6 +30,7 @@
  */
 #include "kq_launch.h"
 #include "kq_device.h"
+#include "kq_dma.h"
 
 namespace {
 
@@ -37,7 +38,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef int i4v __attribute__((ext_vector_type(4)));
+typedef kq_i4v i4v;
 
 constexpr uint32_t kT = 16;
 constexpr uint32_t kShared = 0x80000000u; /* item flag: the shared expert */
@@ -54,53 +55,6 @@ __device__ __forceinline__ float half_bits(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
 }
 
-__device__ __forceinline__ i4v dma_rsrc(const void *base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    i4v r;
-    r.x = (int)(uint32_t)a;
-    r.y = (int)(uint32_t)(a >> 32);
-    r.z = (int)bytes;
-    r.w = 0x00020000;
-    return r;
-}
-__device__ __forceinline__ void dma16(i4v rsrc, uint32_t voff, uint32_t lds) {
-    /* m0 carries the LDS address; it leaves the statement as it entered
-       (saved and restored here), and one wait state separates each write of
-       m0 from the next instruction that may read it (the LDS-DMA load, or
-       the compiler's own code after the statement) */
-    uint32_t save;
-    asm volatile("s_mov_b32 %[sv], m0\n\t"
-                 "s_mov_b32 m0, %[lds]\n\t"
-                 "s_nop 0\n\t"
-                 "buffer_load_dwordx4 %[v], %[r], 0 offen lds\n\t"
-                 "s_mov_b32 m0, %[sv]\n\t"
-                 "s_nop 0"
-                 : [sv] "=&s"(save)
-                 : [v] "v"(voff), [r] "s"(rsrc), [lds] "s"(lds)
-                 : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-/* s_waitcnt vmcnt(IPT * after) for a run-time after <= PD */
-template <uint32_t IPT, uint32_t PD>
-__device__ __forceinline__ void wait_after(uint32_t after) {
-    if constexpr (PD > 0u) {
-        if (after >= PD) {
-            wait_vm<(int)(IPT * PD)>();
-            return;
-        }
-        wait_after<IPT, PD - 1u>(after);
-    } else {
-        wait_vm<0>();
-    }
-}
-__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }
-template <typename T>
-__device__ __forceinline__ uint32_t lds_addr(T *p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)p;
-}
 __device__ __forceinline__ uint32_t sload(const uint32_t *p) {
     const uint64_t a = (uint64_t)(uintptr_t)p;
     /* (readfirstlane returns int: zero-extend each half, never sign-extend) */
