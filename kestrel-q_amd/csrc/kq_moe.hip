@@ -396,7 +396,8 @@ __device__ __forceinline__ float wave_max(float v) {
  * Certification: with a_e = S_n and bounds b_e, the top-k by a_e is the
  *   CPU's selection in the CPU's order if every adjacent pair in it, and
  *   its last member against every unselected expert, is separated by more
- *   than the two bounds plus a margin: the margin keeps the rounded
+ *   than the two bounds plus a margin, and the higher member's probability
+ *   is a normal binary32 number: the margin keeps the rounded
  *   probabilities fl(fl(exp(fl(l - max))) / s) strictly ordered too, so no
  *   tie (and no tie-break) can occur. It then writes the ids, the weights
  *   p / sum(p) from the fp64 values (compared by tolerance like the layer
@@ -413,11 +414,15 @@ constexpr uint32_t kMaxTopK = 64;
 constexpr uint32_t kCertCand = 128; /* candidates one wave ranks, two per lane */
 
 /* hi - bhi exceeds lo + blo by more than the bounds and 16 units in the
- * last place of the probability terms involved (m: the largest a) */
+ * last place of the probability terms involved (m: the largest a), and the
+ * higher one's probability exp(hi - max) / sum is a normal binary32 number
+ * (sum <= 1024 terms of at most 1): a lower probability may round to a
+ * subnormal or to zero, but not up to it. Two probabilities that both
+ * underflow tie on the CPU, which then orders them by id. */
 __device__ __forceinline__ bool certify_sep(double hi, double bhi, double lo, double blo,
                                             double m) {
     const double margin = 0x1p-20 * (4.0 + fabs(hi - m) + fabs(lo - m));
-    return (hi - bhi) - (lo + blo) > margin;
+    return (hi - bhi) - m > -75.0 && (hi - bhi) - (lo + blo) > margin;
 }
 
 __device__ __forceinline__ float rdl_f32(float v, uint32_t lane) {

@@ -15,7 +15,10 @@
  *   - the top k by a (larger first, lower id among equals) is certified if
  *     each adjacent pair of it, and its last member against the largest
  *     a + b outside it, are separated by more than both bounds plus
- *     2^-20 * (4 + |hi - max a| + |lo - max a|). Then the CPU's softmax
+ *     2^-20 * (4 + |hi - max a| + |lo - max a|), and the higher member of
+ *     each pair has hi - b - max a > -75 (its probability a normal binary32
+ *     number: two probabilities that underflow tie, and the CPU orders
+ *     ties by id). Then the CPU's softmax
  *     probabilities are strictly ordered the same way, and its partial
  *     selection (src/kq_moe_qwen38.c:211-274) returns exactly these ids in
  *     this order.
@@ -52,9 +55,11 @@ static void row_bound(const float *w, const float *x, uint32_t n, double *a, dou
     *b = bad || !(sab < 0x1p126) ? INFINITY : 1.001 * 0x1p-24 * sab;
 }
 
+/* slack < 0: |slack| as below, without the normal-probability rule (a
+ * planted unsound certification for scaled activations) */
 static int certify_sep(double hi, double bhi, double lo, double blo, double m, double slack) {
-    const double margin = slack * 0x1p-20 * (4.0 + fabs(hi - m) + fabs(lo - m));
-    return (hi - bhi) - (lo + blo) > margin;
+    const double margin = fabs(slack) * 0x1p-20 * (4.0 + fabs(hi - m) + fabs(lo - m));
+    return (slack < 0.0 || (hi - bhi) - m > -75.0) && (hi - bhi) - (lo + blo) > margin;
 }
 
 typedef struct cand {
@@ -219,16 +224,20 @@ static void plant_tie(float *router, const float *x, uint32_t H, uint32_t hi, ui
  *         [2^-6, 2^6];
  * mode 2: as 1 for a pair inside the selection (positions j, j+1 < k);
  * mode 3: as 1 with c log-uniform in [2^-16, 2^-2]: ties far below the
- *         bound, where the chains' rounding decides.
+ *         bound, where the chains' rounding decides;
+ * mode 4: as 0 with x scaled by 2^s, s uniform in [0, 28]: logits so far
+ *         apart that the lower selected probabilities underflow and tie.
  * slack multiplies every bound and the margin: 1 restates the device; a
  * smaller value plants an unsound certification, which the campaign must
- * catch (certified selections that differ from the exact route).
+ * catch (certified selections that differ from the exact route); a
+ * negative one also drops the rule that a pair's higher probability be a
+ * normal number.
  */
 int kqo_certify_campaign(uint64_t seed, uint64_t trials, uint32_t E, uint32_t H, uint32_t K,
                          int mode, float sigma, double slack, int threads,
                          uint64_t *stats) {
     if (stats == NULL || E == 0 || E > 1024 || H == 0 || K == 0 || K >= E || K > 64 || mode < 0 ||
-        mode > 3)
+        mode > 4)
         return KQO_INVALID_ARGUMENT;
     memset(stats, 0, 6 * sizeof(uint64_t));
     const uint64_t per_router = 64;
@@ -258,8 +267,12 @@ int kqo_certify_campaign(uint64_t seed, uint64_t trials, uint32_t E, uint32_t H,
             const uint64_t trial = (uint64_t)g * per_router + tt;
             if (trial >= trials) break;
             for (uint32_t i = 0; i < H; ++i) x[i] = normal(&r, 1.0f);
+            if (mode == 4) {
+                const float sc = ldexpf(1.0f, (int)(next64(&r) % 29u));
+                for (uint32_t i = 0; i < H; ++i) x[i] *= sc;
+            }
             uint32_t planted = UINT32_MAX;
-            if (mode != 0) {
+            if (mode != 0 && mode != 4) {
                 /* rank by binary64 logit, then plant the tie */
                 for (uint32_t e = 0; e < E; ++e) row_bound(router + (uint64_t)e * H, x, H, &a[e], &b[e]);
                 for (uint32_t e = 0; e < E; ++e) ord[e] = e;

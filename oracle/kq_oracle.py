@@ -383,7 +383,8 @@ def route_certify(router: np.ndarray, x: np.ndarray, top_k: int):
     return bool(cert.value), ids
 
 
-CAMPAIGN_MODES = {"random": 0, "tie-at-boundary": 1, "tie-inside": 2, "tie-below-bound": 3}
+CAMPAIGN_MODES = {"random": 0, "tie-at-boundary": 1, "tie-inside": 2, "tie-below-bound": 3,
+                  "large-activations": 4}
 
 
 def certify_campaign(seed: int, trials: int, experts: int, hidden: int, top_k: int,
@@ -392,7 +393,7 @@ def certify_campaign(seed: int, trials: int, experts: int, hidden: int, top_k: i
     """Certified selections against the exact route on generated cases
     (kq_certify.c kqo_certify_campaign). slack < 1 scales the bounds and the
     margin down: a planted unsound certification, which the campaign must
-    catch."""
+    catch; a negative slack also drops the normal-probability rule."""
     st_arr = np.zeros(6, np.uint64)
     st = lib().kqo_certify_campaign(seed, trials, experts, hidden, top_k,
                                     CAMPAIGN_MODES[mode], sigma, slack, threads,

@@ -494,6 +494,41 @@ def test_moe_decode_certified_shapes(ctx, H, E, K):
         b.close()
 
 
+@pytest.mark.parametrize("scale", [1e6, 3e4])
+def test_moe_decode_underflowing_probabilities(ctx, scale):
+    # Activations scaled so that the selection's lower softmax probabilities
+    # underflow to zero: they tie on the CPU, which keeps the lowest ids
+    # among them, whatever their logits' order. Certification must not
+    # claim such a selection (it requires the higher probability of every
+    # certified pair to be a normal number); the ids are the CPU's.
+    H, E, K, I = 256, 24, 3, 256
+    w = S.moe_weights(S.W_MOE + 77, H, E, I, I)
+    bufs = {k: ctx.upload(v) for k, v in w.items()}
+    cfg = kq_hip.MoeConfig(H, E, K, I, I)
+    dims = dict(hidden=H, experts=E, top_k=K, inter=I, shared_inter=I)
+    n = cfg.scratch_bytes(1)
+    scratch, dout, dids = ctx.alloc(n), ctx.alloc(H * 4), ctx.alloc(K * 4)
+    xs = S.normal_f32(S.stream_key(S.W_MOE + 77, S.R_HIDDEN), 4 * H).reshape(4, H) * scale
+    underflow = 0
+    for t in range(xs.shape[0]):
+        x = np.ascontiguousarray(xs[t:t + 1], dtype=np.float32)
+        dx = ctx.upload(x)
+        ctx.moe_execute(cfg, kq_hip.moe_weights(bufs), dx, 1, dout, dids, scratch, n)
+        ref, tr = kq_oracle.moe_execute(dims, {k: (r, w[k]) for k, r in ROLES.items()}, x,
+                                        trace=True)
+        got = ctx.download(dids, np.uint32, K)[None, :]
+        assert np.array_equal(got, tr["selected_ids"]), (t, got, tr["selected_ids"])
+        logits = w["router"].reshape(E, H).astype(np.float64) @ x[0].astype(np.float64)
+        top = np.sort(logits)[::-1][:K]
+        if top[0] - top[-1] > 200.0:
+            underflow += 1
+            assert certified_flag(ctx, scratch, n) != 1, t
+        dx.close()
+    assert underflow >= 1
+    for b in (scratch, dout, dids):
+        b.close()
+
+
 @pytest.mark.parametrize("pattern", ["zero-router", "duplicate-rows", "near-tie"])
 def test_moe_decode_ties_fall_back_to_exact_chains(ctx, pattern):
     # Exactly tied or almost tied logits cannot be certified: the exact

@@ -63,6 +63,22 @@ def test_campaign_catches_unsound_certification(slack):
     assert r["first_mismatch_plus_1"] > 0
 
 
+def test_certified_selection_large_activations():
+    # activations scaled by up to 2^28: the lower selected probabilities
+    # underflow to zero and tie, and the CPU orders ties by id. The rule
+    # that a pair's higher probability be a normal binary32 number keeps
+    # certification sound there; without it the campaign finds certified
+    # selections that are not the exact route's.
+    n = 20_000
+    r = kq_oracle.certify_campaign(0x5CA1E, n, 64, 128, 4, "large-activations", threads=THREADS)
+    assert r["route_failures"] == 0
+    assert r["certified_mismatch"] == 0, r
+    assert 0 < r["certified"] < n, r
+    r = kq_oracle.certify_campaign(0x5CA1E, n, 64, 128, 4, "large-activations", threads=THREADS,
+                                   slack=-1.0)
+    assert r["certified_mismatch"] > 0, r
+
+
 def test_restatement_entry_matches_campaign_rule():
     # kqo_route_certify on one planted-free case: certified, ids equal to
     # the exact route's
