@@ -1,6 +1,8 @@
 /*
- * kq_grouped_dn.hip — the prefill down pass of Q6_K experts, one
- * independent weight pipeline per wave.
+ * kq_grouped_dn.hip — the prefill down pass of Q6_K experts: one
+ * independent weight pipeline per wave at intermediate 256 (dn_q6k), one
+ * per pair of waves at intermediate 512 (dn_q6k_pair, below), and the Q5_1
+ * and Q8_0 down passes (dn_small).
  *
  * The reference forms o = Wd a for every (token, selected expert) pair one
  * token at a time (src/kq_moe_qwen38.c:722-765 via
@@ -325,6 +327,238 @@ void dn_q6k(DnArgs a) {
 }
 
 /* ------------------------------------------------------------------ */
+/* intermediate 512: the two blocks of a row on a pair of waves */
+
+/* With both blocks' activation operand (128 registers) in one wave, the
+ * MFMA results spill into accumulation registers and one wave per SIMD
+ * pays every latency itself. Here wave h of a pair multiplies block h of
+ * each tile: its operand is 64 registers and two waves share each SIMD.
+ *   - A workgroup of W waves (W / 2 pairs) owns a contiguous range of the
+ *     (item, 16-row tile) sequence; pair p takes tiles lo + p, lo + p +
+ *     W / 2, ..., one per round.
+ *   - A tile (16 rows x 420 bytes, one contiguous range) goes into a ring
+ *     slot of its pair by 16-byte LDS-DMA loads, 1 KiB per instruction:
+ *     wave 0 of the pair issues instructions 0-3, wave 1 instructions 4-6
+ *     and one that lands in a scratch area. PD tiles stay in flight.
+ *   - Round k: each wave waits for its own loads of tile k, then one
+ *     barrier makes both halves visible and frees the slot of round k - 1,
+ *     which then takes the request for tile k + PD. The block-1 wave leaves
+ *     its partial sums in an exchange slot of the round's parity; the
+ *     block-0 wave adds them after the next barrier, scales and stores. */
+struct DnPair {
+    static constexpr uint32_t W = 2u;        /* waves per workgroup: one pair */
+    static constexpr uint32_t NP = W / 2u;   /* pairs */
+    static constexpr uint32_t TB = kT * 420u;               /* tile bytes */
+    static constexpr uint32_t IPT = (TB + 1023u) / 1024u;   /* instructions per tile: 7 */
+    static constexpr uint32_t IPW = (IPT + 1u) / 2u;        /* per wave: 4 */
+    static constexpr uint32_t SLOT = IPT * 1024u;
+    static constexpr uint32_t RING = 5u;     /* slots per pair */
+    static constexpr uint32_t PD = RING - 1u;
+    static_assert(NP * RING * SLOT + 1024u + 2u * NP * 64u * 16u <= 40u * 1024u,
+                  "four workgroups per CU");
+};
+
+__global__ __launch_bounds__(DnPair::W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void dn_q6k_pair(DnArgs a) {
+    using S = DnPair;
+    constexpr uint32_t KD = 512u, RB = 420u;
+    __shared__ __align__(16) uint8_t slots[S::NP][S::RING][S::SLOT];
+    __shared__ __align__(16) uint8_t trash[1024];
+    __shared__ __align__(16) f4 xch[2][S::NP][64];
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t p = w % S::NP, h = w / S::NP; /* pair, block */
+    const uint32_t nt = (a.hidden + kT - 1u) / kT; /* tiles per item (>= 16) */
+    const uint64_t total = (uint64_t)(*a.n_items) * nt;
+    const uint32_t lo = (uint32_t)(total * blockIdx.x / gridDim.x);
+    const uint32_t hi = (uint32_t)(total * (blockIdx.x + 1u) / gridDim.x);
+    if (lo >= hi) return; /* the whole workgroup */
+    const uint32_t rounds = (hi - lo + S::NP - 1u) / S::NP;
+    const uint32_t first = lo + p;
+
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t wbytes = a.hidden * RB;
+    const uint8_t *pslots = &slots[p][0][0];
+    const uint32_t pair_lds = lds_addr(pslots);
+
+    /* this wave's instructions of a tile: n = h * IPW + q; past IPT, a
+     * re-read of the tile's start into the scratch area */
+    uint32_t rel[S::IPW];
+#pragma unroll
+    for (uint32_t q = 0; q < S::IPW; ++q) {
+        const uint32_t c = 64u * (h * S::IPW + q) + lane;
+        /* bytes past the tile re-read its start (their slot bytes are
+         * never read) */
+        rel[q] = 16u * c < S::TB ? 16u * c : 0u;
+    }
+
+    /* the next tile to request (stride NP), as item and tile within it */
+    uint32_t iss_it = first / nt, iss_in = first - (first / nt) * nt, iss_slot = 0u;
+    bool iss_new = true;
+    i4v rw = {0, 0, 0, 0};
+    auto issue = [&]() {
+        if (iss_new) {
+            iss_new = false;
+            const uint32_t ex = sload(a.items + 2u * iss_it);
+            rw = dma_rsrc((ex & kShared) ? a.sdown : a.down + (size_t)ex * wbytes, wbytes);
+        }
+        const uint32_t toff = iss_in * S::TB;
+#pragma unroll
+        for (uint32_t q = 0; q < S::IPW; ++q) {
+            const uint32_t n = h * S::IPW + q; /* wave-uniform */
+            dma16(rw, toff + rel[q],
+                  n < S::IPT ? pair_lds + iss_slot * S::SLOT + n * 1024u : lds_addr(trash));
+        }
+        iss_slot = iss_slot + 1u == S::RING ? 0u : iss_slot + 1u;
+        iss_in += S::NP;
+        if (iss_in >= nt) {
+            iss_in -= nt;
+            ++iss_it;
+            iss_new = true;
+        }
+    };
+
+    const DnStaged sx = dn_staged_at(const_cast<void *>(a.staged), a.npos, KD);
+    const KqBuf bxh = kq_buf(sx.xh, a.npos * KD * 2u), bxl = kq_buf(sx.xl, a.npos * KD * 2u);
+    const KqBuf bsg = kq_buf(sx.sig, a.npos * 4u);
+    const uint32_t tk = a.tokens * a.top_k;
+    bool bad = false, malformed = false;
+
+#pragma unroll
+    for (uint32_t t = 0; t < S::PD; ++t)
+        if (first + t * S::NP < hi) issue();
+
+    /* the item being multiplied: block h of the activation operand of lane
+     * (j, g), the scales of the four positions of this lane's results */
+    uint4 axh[8], axl[8];
+    int sg[4];
+    uint32_t cur = 0xffffffffu, pos0 = 0u, count = 0u;
+    auto enter = [&](uint32_t it) {
+        cur = it;
+        const uint32_t ex = sload(a.items + 2u * it), fc = sload(a.items + 2u * it + 1u);
+        const uint32_t f0 = fc & 0xffffffu;
+        count = fc >> 24;
+        pos0 = (ex & kShared) ? tk + f0 : f0;
+        /* rows past the chunk read at 2^31, past the buffer */
+        const uint32_t xo = j < count ? ((pos0 + j) * KD + g * (KD / 4u) + h * 64u) * 2u
+                                      : 0x80000000u;
+#pragma unroll
+        for (uint32_t v = 0; v < 8u; ++v) {
+            axh[v] = kq_ld128(bxh, xo + v * 16u, 0u);
+            axl[v] = kq_ld128(bxl, xo + v * 16u, 0u);
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
+        }
+        wait_vm_all();
+    };
+
+    /* block 0's sums of the previous round plus block 1's: D[token][row],
+     * this lane holds row row0 + j of tokens 4g .. 4g + 3 */
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    uint32_t prow0 = 0u, ppos0 = 0u, pcount = 0u;
+    int psg[4] = {0, 0, 0, 0};
+    auto finish = [&](uint32_t k) {
+        const f4 o = xch[k & 1u][p][lane];
+        const uint32_t row = prow0 + j;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            const bool valid = i < pcount && row < a.hidden;
+            const float v = ldexpf(acc[q] + o[q], -psg[q]);
+            bad |= valid && !kq_isfinite(v);
+            if (valid) a.out[(size_t)(ppos0 + i) * a.hidden + row] = v;
+        }
+    };
+
+    const h2 bias = h2{(_Float16)-1056.0f, (_Float16)-1056.0f}; /* 1024 + 32 */
+    uint32_t c_it = first / nt, c_in = first - (first / nt) * nt, cslot = 0u;
+    uint32_t tau = first;
+    bool prev = false;
+    for (uint32_t k = 0; k < rounds; ++k, tau += S::NP) {
+        const bool live = tau < hi; /* uniform over the pair */
+        if (live) {
+            if (c_it != cur) enter(c_it);
+            /* this wave's loads of tile tau have landed; those of the later
+             * tiles requested so far (at most PD - 1) may be in flight */
+            const uint32_t later = (hi - 1u - tau) / S::NP;
+            wait_after<S::IPW, S::PD - 1u>(later < S::PD - 1u ? later : S::PD - 1u);
+        }
+        /* both halves of tile tau are in LDS, the slot of the previous
+         * round is free, the previous round's exchange slot is written */
+        kq_lds_barrier();
+        if (live && tau + S::NP * S::PD < hi) issue();
+        if (prev && h == 0u) finish(k - 1u);
+        prev = live;
+        if (live) {
+            const uint8_t *tile = pslots + cslot * S::SLOT;
+            cslot = cslot + 1u == S::RING ? 0u : cslot + 1u;
+            prow0 = c_in * kT;
+            ppos0 = pos0;
+            pcount = count;
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) psg[q] = sg[q];
+            c_in += S::NP;
+            if (c_in >= nt) {
+                c_in -= nt;
+                ++c_it;
+            }
+            /* block h of row j: 4-byte aligned windows, re-aligned by sh */
+            const uint32_t o = j * RB + h * 210u;
+            const uint32_t sh = o & 3u;
+            const uint32_t *pw = (const uint32_t *)(tile + (o - sh));
+            auto win = [&](uint32_t off) { return kq_align2(pw[off / 4u + 1u], pw[off / 4u], sh); };
+            const float d = half_bits(sh ? (pw[52] >> 16) : pw[52]);
+            malformed |= !kq_isfinite(d);
+            uint32_t sc[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) sc[q] = win(192u + 4u * q);
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (uint32_t nh = 0; nh < 4u; ++nh) {
+                const uint32_t n = nh >> 1, hh = nh & 1u;
+                const uint32_t oa = 64u * n + 16u * hh + 4u * g;
+                const uint32_t A = win(oa), B = win(oa + 32u);
+                const uint32_t H = win(128u + 32u * n + 16u * hh + 4u * g);
+                uint32_t c[4];
+                c[0] = (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+                c[1] = (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+                c[2] = ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+                c[3] = ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+#pragma unroll
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const uint32_t s = 8u * n + 2u * q + hh; /* sub-block */
+                    const h2 w0 = byte_pair_lo(c[q]) + bias, w1 = byte_pair_hi(c[q]) + bias;
+                    const h4 bw = h4{w0.x, w0.y, w1.x, w1.y};
+                    /* columns 128n + 32q + 16hh + 4g .. +3 of block h */
+                    const uint32_t ai = (n * 2u + hh) * 4u + q;
+                    const uint4 &xh = axh[ai >> 1], &xl = axl[ai >> 1];
+                    const h4 ah = __builtin_bit_cast(h4, (ai & 1u) ? make_uint2(xh.z, xh.w) : make_uint2(xh.x, xh.y));
+                    const h4 al = __builtin_bit_cast(h4, (ai & 1u) ? make_uint2(xl.z, xl.w) : make_uint2(xl.x, xl.y));
+                    f4 t = {0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bw, t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bw, t, 0, 0, 0);
+                    const int8_t scv = (int8_t)((sc[s >> 2] >> (8u * (s & 3u))) & 0xffu);
+                    const float ds = d * (float)scv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] = fmaf(ds, t[e], acc[e]);
+                }
+            }
+            if (h == 1u) xch[k & 1u][p][lane] = acc;
+        }
+    }
+    kq_lds_barrier();
+    if (prev && h == 0u) finish(rounds - 1u);
+    /* no LDS-DMA load may outlive the wave */
+    wait_vm<0>();
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+}
+
+/* ------------------------------------------------------------------ */
 /* the same pipeline for rows of 32-weight blocks: Q5_1 (the reference
  * model's routed down: 24 B per block, f16 d, f16 m, 32 high bits, 16
  * bytes of nibbles; src/kq_numeric.c:197-222, every block 4-byte aligned)
@@ -582,8 +816,13 @@ hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
             cus < 1)
             cus = 256;
     }
-    /* one workgroup per CU (the slots' LDS) */
-    hipLaunchKernelGGL((dn_q6k<KB>), dim3((uint32_t)cus), dim3(DnShape<KB>::W * 64), 0, s, a);
+    if constexpr (KB == 2u) {
+        /* four workgroups per CU: two waves per SIMD */
+        hipLaunchKernelGGL(dn_q6k_pair, dim3(4u * (uint32_t)cus), dim3(DnPair::W * 64), 0, s, a);
+    } else {
+        /* one workgroup per CU (the slots' LDS) */
+        hipLaunchKernelGGL((dn_q6k<KB>), dim3((uint32_t)cus), dim3(DnShape<KB>::W * 64), 0, s, a);
+    }
     return hipGetLastError();
 }
 
