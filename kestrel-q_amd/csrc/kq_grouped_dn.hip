@@ -332,14 +332,18 @@ void dn_q6k(DnArgs a) {
 /* With both blocks' activation operand (128 registers) in one wave, the
  * MFMA results spill into accumulation registers and one wave per SIMD
  * pays every latency itself. Here wave h of a pair multiplies block h of
- * each tile: its operand is 64 registers and two waves share each SIMD.
+ * each tile: its operand is 64 registers, and eight one-pair workgroups per
+ * CU put four waves on each SIMD (measured on the 512-expert T = 512
+ * layer: 161.6 us with one wave per SIMD, 134.5 with two and a ring of
+ * five tiles, 125.5 with three and three, 123.3 with four and two).
  *   - A workgroup of W waves (W / 2 pairs) owns a contiguous range of the
  *     (item, 16-row tile) sequence; pair p takes tiles lo + p, lo + p +
  *     W / 2, ..., one per round.
  *   - A tile (16 rows x 420 bytes, one contiguous range) goes into a ring
  *     slot of its pair by 16-byte LDS-DMA loads, 1 KiB per instruction:
  *     wave 0 of the pair issues instructions 0-3, wave 1 instructions 4-6
- *     and one that lands in a scratch area. PD tiles stay in flight.
+ *     and one that lands in a scratch area. PD tiles stay in flight while
+ *     one is multiplied.
  *   - Round k: each wave waits for its own loads of tile k, then one
  *     barrier makes both halves visible and frees the slot of round k - 1,
  *     which then takes the request for tile k + PD. The block-1 wave leaves
@@ -352,13 +356,13 @@ struct DnPair {
     static constexpr uint32_t IPT = (TB + 1023u) / 1024u;   /* instructions per tile: 7 */
     static constexpr uint32_t IPW = (IPT + 1u) / 2u;        /* per wave: 4 */
     static constexpr uint32_t SLOT = IPT * 1024u;
-    static constexpr uint32_t RING = 5u;     /* slots per pair */
+    static constexpr uint32_t RING = 2u;     /* slots per pair */
     static constexpr uint32_t PD = RING - 1u;
-    static_assert(NP * RING * SLOT + 1024u + 2u * NP * 64u * 16u <= 40u * 1024u,
-                  "four workgroups per CU");
+    static_assert(NP * RING * SLOT + 1024u + 2u * NP * 64u * 16u <= 20u * 1024u,
+                  "eight workgroups per CU");
 };
 
-__global__ __launch_bounds__(DnPair::W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(DnPair::W * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void dn_q6k_pair(DnArgs a) {
     using S = DnPair;
     constexpr uint32_t KD = 512u, RB = 420u;
@@ -817,8 +821,8 @@ hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
             cus = 256;
     }
     if constexpr (KB == 2u) {
-        /* four workgroups per CU: two waves per SIMD */
-        hipLaunchKernelGGL(dn_q6k_pair, dim3(4u * (uint32_t)cus), dim3(DnPair::W * 64), 0, s, a);
+        /* eight workgroups per CU: four waves per SIMD */
+        hipLaunchKernelGGL(dn_q6k_pair, dim3(8u * (uint32_t)cus), dim3(DnPair::W * 64), 0, s, a);
     } else {
         /* one workgroup per CU (the slots' LDS) */
         hipLaunchKernelGGL((dn_q6k<KB>), dim3((uint32_t)cus), dim3(DnShape<KB>::W * 64), 0, s, a);
