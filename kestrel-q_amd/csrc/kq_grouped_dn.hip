@@ -2,7 +2,7 @@
  * kq_grouped_dn.hip — the prefill down pass of Q6_K experts: one
  * independent weight pipeline per wave at intermediate 256 (dn_q6k), one
  * per pair of waves at intermediate 512 (dn_q6k_pair, below), and the Q5_1
- * and Q8_0 down passes (dn_small).
+ * and Q8_0 down passes (dn_small_pair).
  *
  * The reference forms o = Wd a for every (token, selected expert) pair one
  * token at a time (src/kq_moe_qwen38.c:722-765 via
@@ -563,7 +563,7 @@ void dn_q6k_pair(DnArgs a) {
 }
 
 /* ------------------------------------------------------------------ */
-/* the same pipeline for rows of 32-weight blocks: Q5_1 (the reference
+/* rows of 32-weight blocks: Q5_1 (the reference
  * model's routed down: 24 B per block, f16 d, f16 m, 32 high bits, 16
  * bytes of nibbles; src/kq_numeric.c:197-222, every block 4-byte aligned)
  * and Q8_0 (its layers 2, 4, 30, 46 and 47: 34 B per block, f16 d and 32
@@ -584,14 +584,6 @@ struct DnSmallShape {
     static constexpr uint32_t RB = BB * NBK;                 /* row bytes */
     static_assert(RB % 4u == 0u, "rows start 4-byte aligned in the slot");
     static constexpr uint32_t TB = kT * RB;                  /* tile bytes */
-    static constexpr uint32_t IPT = (TB + 1023u) / 1024u;    /* loads per tile */
-    static constexpr uint32_t SLOT = IPT * 1024u;
-    static constexpr uint32_t W = 4u;
-    static constexpr uint32_t RING0 = 160u * 1024u / (W * SLOT);
-    static constexpr uint32_t RING = RING0 > 8u ? 8u : RING0;
-    static constexpr uint32_t PD = RING - 1u;
-    static_assert(RING >= 2u, "LDS");
-    static_assert(W * RING * SLOT <= 160u * 1024u, "LDS");
 };
 
 /* bits 0..3 of x (x < 16) to bit 4 of bytes 0..3 */
@@ -599,27 +591,64 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) {
     return (kq_mul_u24(x, 0x00204081u) & 0x01010101u) << 4;
 }
 
+/* The Q5_1 / Q8_0 down pass on pairs of waves, as dn_q6k_pair: wave h of a
+ * pair multiplies blocks h NH .. h NH + NH - 1 of every row (NH = blocks per
+ * row / 2), so its activation operand is half a row (80 registers at
+ * intermediate 640) and two or three waves share a SIMD; the pair's tiles go
+ * through a two-slot ring it shares, and the block-1 wave's partial sums
+ * (min term included) reach the block-0 wave through LDS once per tile. */
 template <uint32_t FMT, uint32_t KD>
-__global__ __launch_bounds__((DnSmallShape<FMT, KD>::W * 64))
-__attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
-    using S = DnSmallShape<FMT, KD>;
-    constexpr uint32_t NBK = S::NBK;
-    __shared__ __align__(16) uint8_t slots[S::W][S::RING][S::SLOT];
+struct DnSmallPair {
+    using B = DnSmallShape<FMT, KD>;
+    static constexpr uint32_t NH = B::NBK / 2u;             /* blocks per wave */
+    static_assert(B::NBK % 4u == 0u, "an even number of blocks per wave");
+    static constexpr uint32_t IPT = (B::TB + 1023u) / 1024u; /* instructions per tile */
+    static constexpr uint32_t IPW = (IPT + 1u) / 2u;         /* per wave */
+    static constexpr uint32_t SLOT = IPT * 1024u;
+    static constexpr uint32_t RING = 2u;
+    static constexpr uint32_t PD = RING - 1u;
+    static constexpr uint32_t LDS = RING * SLOT + 1024u + 2u * 64u * 16u;
+    /* waves per SIMD: three for Q8_0 (six one-pair workgroups per CU),
+     * two for Q5_1, whose decode and min term need more than the 168
+     * registers of three at intermediate 640 */
+    static constexpr uint32_t WPE = B::Q51 ? 2u : 3u;
+    static constexpr uint32_t WGS = 2u * WPE;
+    static_assert(WGS * LDS <= 160u * 1024u, "LDS");
+};
+
+template <uint32_t FMT, uint32_t KD>
+__global__ __launch_bounds__(128)
+__attribute__((amdgpu_waves_per_eu(DnSmallPair<FMT, KD>::WPE, DnSmallPair<FMT, KD>::WPE)))
+void dn_small_pair(DnArgs a) {
+    using S = DnSmallPair<FMT, KD>;
+    using B = typename S::B;
+    constexpr uint32_t NH = S::NH;
+    __shared__ __align__(16) uint8_t slots[S::RING][S::SLOT];
+    __shared__ __align__(16) uint8_t trash[1024];
+    __shared__ __align__(16) f4 xch[2][64];
 
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t gw = blockIdx.x * S::W + w, nw = gridDim.x * S::W;
+    const uint32_t h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* block half */
     const uint32_t nt = (a.hidden + kT - 1u) / kT; /* tiles per item */
     const uint64_t total = (uint64_t)(*a.n_items) * nt;
-    const uint32_t lo = (uint32_t)(total * gw / nw), hi = (uint32_t)(total * (gw + 1u) / nw);
-    if (lo >= hi) return;
+    const uint32_t lo = (uint32_t)(total * blockIdx.x / gridDim.x);
+    const uint32_t hi = (uint32_t)(total * (blockIdx.x + 1u) / gridDim.x);
+    if (lo >= hi) return; /* the whole workgroup */
 
     const uint32_t j = lane & 15u, g = lane >> 4;
-    const uint32_t wbytes = a.hidden * S::RB;
-    const uint32_t base_lds = lds_addr(&slots[w][0][0]);
-    const uint8_t *myslots = &slots[w][0][0];
+    const uint32_t wbytes = a.hidden * B::RB;
+    const uint32_t pair_lds = lds_addr(&slots[0][0]);
 
-    uint32_t iss_it = lo / nt, iss_tile = lo - (lo / nt) * nt, iss_slot = 0u;
+    /* this wave's instructions of a tile: n = h * IPW + q; past IPT, a
+     * re-read of the tile's start into the scratch area */
+    uint32_t rel[S::IPW];
+#pragma unroll
+    for (uint32_t q = 0; q < S::IPW; ++q) {
+        const uint32_t c = 64u * (h * S::IPW + q) + lane;
+        rel[q] = 16u * c < B::TB ? 16u * c : 0u;
+    }
+
+    uint32_t iss_it = lo / nt, iss_in = lo - (lo / nt) * nt, iss_slot = 0u;
     bool iss_new = true;
     i4v rw = {0, 0, 0, 0};
     auto issue = [&]() {
@@ -628,16 +657,16 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
             const uint32_t ex = sload(a.items + 2u * iss_it);
             rw = dma_rsrc((ex & kShared) ? a.sdown : a.down + (size_t)ex * wbytes, wbytes);
         }
-        const uint32_t toff = iss_tile * S::TB;
+        const uint32_t toff = iss_in * B::TB;
 #pragma unroll
-        for (uint32_t q = 0; q < S::IPT; ++q) {
-            const uint32_t c = 64u * q + lane;
-            dma16(rw, toff + (16u * c < S::TB ? 16u * c : 0u),
-                  base_lds + iss_slot * S::SLOT + q * 1024u);
+        for (uint32_t q = 0; q < S::IPW; ++q) {
+            const uint32_t n = h * S::IPW + q; /* wave-uniform */
+            dma16(rw, toff + rel[q],
+                  n < S::IPT ? pair_lds + iss_slot * S::SLOT + n * 1024u : lds_addr(trash));
         }
         iss_slot = iss_slot + 1u == S::RING ? 0u : iss_slot + 1u;
-        if (++iss_tile == nt) {
-            iss_tile = 0u;
+        if (++iss_in == nt) {
+            iss_in = 0u;
             ++iss_it;
             iss_new = true;
         }
@@ -655,11 +684,11 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
     for (uint32_t t = 0; t < S::PD; ++t)
         if (lo + t < hi) issue();
 
-    uint4 axh[NBK], axl[NBK];
-    constexpr uint32_t NMS = (NBK + 15u) / 16u; /* 16-block steps of the min term */
+    uint4 axh[NH], axl[NH];
+    constexpr uint32_t NMS = (NH + 15u) / 16u; /* 16-block steps of the min term */
     h4 sxh[NMS], sxl[NMS];
     int sg[4];
-    uint32_t cur = 0u, pos0 = 0u, count = 0u;
+    uint32_t cur = 0xffffffffu, pos0 = 0u, count = 0u;
     auto enter = [&](uint32_t it) {
         cur = it;
         const uint32_t ex = sload(a.items + 2u * it), fc = sload(a.items + 2u * it + 1u);
@@ -667,9 +696,10 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
         count = fc >> 24;
         pos0 = (ex & kShared) ? tk + first : first;
         /* rows past the chunk read at 2^31, past the buffer */
-        const uint32_t xo = j < count ? ((pos0 + j) * KD + 8u * g) * 2u : 0x80000000u;
+        const uint32_t xo =
+            j < count ? ((pos0 + j) * KD + 8u * g + 32u * NH * h) * 2u : 0x80000000u;
 #pragma unroll
-        for (uint32_t b = 0; b < NBK; ++b) {
+        for (uint32_t b = 0; b < NH; ++b) {
             axh[b] = kq_ld128(bxh, xo + 64u * b, 0u);
             axl[b] = kq_ld128(bxl, xo + 64u * b, 0u);
         }
@@ -679,16 +709,16 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
             sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
         }
         wait_vm_all();
-        if constexpr (!S::Q51) return;
-        /* the min term's operand: each block's column sum of token row j
-         * (the four lanes of row j hold 8 columns each), times 2^-5 so
-         * it fits fp16, split hi + lo; lane (j, g) keeps blocks 4g .. 4g+3
-         * and 16 + 4g .. (the blocks past NBK are zero) */
+        if constexpr (!B::Q51) return;
+        /* the min term's operand: each of this wave's blocks' column sum
+         * of token row j (the four lanes of row j hold 8 columns each),
+         * times 2^-5 so it fits fp16, split hi + lo; lane (j, g) keeps
+         * blocks 4g .. 4g+3 and 16 + 4g .. (the blocks past NH are zero) */
         float bs[NMS * 16u];
 #pragma unroll
         for (uint32_t b = 0; b < NMS * 16u; ++b) bs[b] = 0.0f;
 #pragma unroll
-        for (uint32_t b = 0; b < NBK; ++b) {
+        for (uint32_t b = 0; b < NH; ++b) {
             const h8 hh = __builtin_bit_cast(h8, axh[b]), ll = __builtin_bit_cast(h8, axl[b]);
             float p = 0.0f;
 #pragma unroll
@@ -713,32 +743,62 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
             sxl[st4] = h4{lv[0], lv[1], lv[2], lv[3]};
         }
     };
-    uint32_t ctile = lo - (lo / nt) * nt, cslot = 0u;
-    enter(lo / nt);
+
+    /* the previous round's block-0 sums and where they go */
+    f4 part = {0.f, 0.f, 0.f, 0.f};
+    uint32_t prow0 = 0u, ppos0 = 0u, pcount = 0u;
+    int psg[4] = {0, 0, 0, 0};
+    auto finish = [&](uint32_t k) {
+        const f4 o = xch[k & 1u][lane];
+        const uint32_t r = prow0 + j;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t i = 4u * g + q;
+            const bool valid = i < pcount && r < a.hidden;
+            const float v = ldexpf(part[q] + o[q], -psg[q]);
+            bad |= valid && !kq_isfinite(v);
+            if (valid) a.out[(size_t)(ppos0 + i) * a.hidden + r] = v;
+        }
+    };
 
     /* fp16 1024 + code: Q5_1 codes are unsigned, Q8_0 ones offset by 128 */
-    const h2 bias = S::Q51 ? h2{(_Float16)-1024.0f, (_Float16)-1024.0f}
+    const h2 bias = B::Q51 ? h2{(_Float16)-1024.0f, (_Float16)-1024.0f}
                            : h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
     const uint32_t shn = g >= 2u ? 4u : 0u;
-    for (uint32_t tau = lo; tau < hi; ++tau) {
-        if (ctile == nt) {
-            ctile = 0u;
-            enter(cur + 1u);
+    uint32_t c_it = lo / nt, c_in = lo - (lo / nt) * nt, cslot = 0u;
+    const uint32_t rounds = hi - lo;
+    for (uint32_t k = 0; k < rounds; ++k) {
+        const uint32_t tau = lo + k;
+        if (c_it != cur) enter(c_it);
+        {
+            /* this wave's loads of tile tau have landed; the later tile
+             * requested so far (at most PD - 1 = 0) may be in flight */
+            wait_vm<0>();
         }
+        /* both halves of tile tau are in LDS, the slot of the previous
+         * round is free, the previous round's exchange slot is written */
+        kq_lds_barrier();
         if (tau + S::PD < hi) issue();
-        const uint32_t after = hi - 1u - tau < S::PD ? hi - 1u - tau : S::PD;
-        wait_after<S::IPT, S::PD>(after);
-        const uint32_t *row = (const uint32_t *)(myslots + cslot * S::SLOT + j * S::RB);
+        if (k > 0u && h == 0u) finish(k - 1u);
+        const uint8_t *tile = &slots[cslot][0];
         cslot = cslot + 1u == S::RING ? 0u : cslot + 1u;
-        const uint32_t row0 = ctile * kT;
-        ++ctile;
-
+        prow0 = c_in * kT;
+        ppos0 = pos0;
+        pcount = count;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) psg[q] = sg[q];
+        if (++c_in == nt) {
+            c_in = 0u;
+            ++c_it;
+        }
+        /* this wave's blocks of row j (h NH B::BB is a multiple of 4) */
+        const uint32_t *row = (const uint32_t *)(tile + j * B::RB + h * NH * B::BB);
         f4 acc = {0.f, 0.f, 0.f, 0.f}, macc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (uint32_t b = 0; b < NBK; ++b) {
+        for (uint32_t b = 0; b < NH; ++b) {
             uint32_t c0, c1;
             float d;
-            if constexpr (S::Q51) {
+            if constexpr (B::Q51) {
                 const uint32_t *blk = row + 6u * b;
                 const uint32_t dm = blk[0];
                 const uint32_t hb = (blk[1] >> (8u * g)) & 0xffu;
@@ -749,11 +809,13 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
                 const float mn = half_bits(dm >> 16);
                 malformed |= !kq_isfinite(d) || !kq_isfinite(mn);
             } else {
-                /* block b at byte 34 b of the row: d in the low half of
-                 * dword 17 b / 2 (b even) or the high half of dword
-                 * (34 b - 2) / 4 (b odd); lane g's eight codes at byte
-                 * 34 b + 2 + 8 g, 2 mod 4 (b even) or 0 mod 4 (b odd).
-                 * The codes, offset by 128, become fp16 1024 + c + 128. */
+                /* block b at byte 34 b of the half row (NH is even, so
+                 * it has the parity of the block in the whole row): d in
+                 * the low half of dword 17 b / 2 (b even) or the high half
+                 * of dword (34 b - 2) / 4 (b odd); lane g's eight codes at
+                 * byte 34 b + 2 + 8 g, 2 mod 4 (b even) or 0 mod 4 (b
+                 * odd). The codes, offset by 128, become fp16 1024 + c +
+                 * 128. */
                 if (b % 2u == 0u) {
                     const uint32_t *blk = row + 17u * (b / 2u);
                     d = half_bits(blk[0]);
@@ -777,34 +839,28 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void dn_small(DnArgs a) {
             t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, t, 0, 0, 0);
             t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, t, 0, 0, 0);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) acc[k] = fmaf(d, t[k], acc[k]);
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(d, t[e], acc[e]);
         }
-        /* the min term: sum over blocks of m times the token's block sum,
-         * as 16x16x16 steps over 16 blocks each (m exact in fp16) */
 #pragma unroll
-        for (uint32_t st4 = 0; st4 < (S::Q51 ? NMS : 0u); ++st4) {
+        for (uint32_t st4 = 0; st4 < (B::Q51 ? NMS : 0u); ++st4) {
             _Float16 mv[4];
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) {
                 const uint32_t b = 16u * st4 + 4u * g + e;
-                mv[e] = b < NBK ? __builtin_bit_cast(_Float16, (uint16_t)(row[6u * b] >> 16))
-                                : (_Float16)0.0f;
+                mv[e] = b < NH ? __builtin_bit_cast(_Float16, (uint16_t)(row[6u * b] >> 16))
+                               : (_Float16)0.0f;
             }
             const h4 mb = h4{mv[0], mv[1], mv[2], mv[3]};
             macc = __builtin_amdgcn_mfma_f32_16x16x16f16(sxh[st4], mb, macc, 0, 0, 0);
             macc = __builtin_amdgcn_mfma_f32_16x16x16f16(sxl[st4], mb, macc, 0, 0, 0);
         }
-        /* D[token][row]: this lane holds row row0 + j of tokens 4g .. 4g+3 */
-        const uint32_t r = row0 + j;
 #pragma unroll
-        for (uint32_t q = 0; q < 4u; ++q) {
-            const uint32_t i = 4u * g + q;
-            const bool valid = i < count && r < a.hidden;
-            const float v = ldexpf(fmaf(32.0f, macc[q], acc[q]), -sg[q]);
-            bad |= valid && !kq_isfinite(v);
-            if (valid) a.out[(size_t)(pos0 + i) * a.hidden + r] = v;
-        }
+        for (uint32_t q = 0; q < 4u; ++q) part[q] = fmaf(32.0f, macc[q], acc[q]);
+        if (h == 1u) xch[k & 1u][lane] = part;
     }
+    kq_lds_barrier();
+    if (h == 0u) finish(rounds - 1u);
+    /* no LDS-DMA load may outlive the wave */
     wait_vm<0>();
     if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
@@ -840,7 +896,7 @@ extern "C" int kq_launch_dn_small_supported(uint32_t type, uint32_t inter) {
 
 /* Q5_1 or Q8_0 down over the item list the permutation built: the
  * activation rows split in natural order (dense_split) into staged, then
- * dn_small */
+ * dn_small_pair */
 extern "C" hipError_t kq_launch_dn_small(uint32_t type, uint32_t inter, uint32_t hidden,
                                          const void *down, const void *shared_down,
                                          const float *act, uint32_t tokens, uint32_t top_k,
@@ -874,8 +930,8 @@ extern "C" hipError_t kq_launch_dn_small(uint32_t type, uint32_t inter, uint32_t
             cus = 256;
     }
 #define KQ_DN_SMALL(F, K)                                                                   \
-    hipLaunchKernelGGL((dn_small<F, K>), dim3((uint32_t)cus),                               \
-                       dim3(DnSmallShape<F, K>::W * 64), 0, s, a)
+    hipLaunchKernelGGL((dn_small_pair<F, K>), dim3(DnSmallPair<F, K>::WGS * (uint32_t)cus),  \
+                       dim3(128), 0, s, a)
     if (type == KQ_LAUNCH_Q5_1) {
         if (inter == 640u)
             KQ_DN_SMALL(KQ_LAUNCH_Q5_1, 640u);
