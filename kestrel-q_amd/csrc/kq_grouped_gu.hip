@@ -375,12 +375,10 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_kq(GuArgs a) {
                 const float dmin = half_bits(hd[m].x >> 16);
                 malformed |= !kq_isfinite(d[m]) || !kq_isfinite(dmin);
                 dm[m] = dmin * 32.0f; /* the sums carry 2^-5 */
-                /* scales of sub-blocks 2g and 2g + 1 (src/kq_numeric.c:161-174) */
-                const uint32_t u = hd[m].y >> (16u * (g & 1u));
-                const uint32_t v = hd[m].w >> (16u * (g & 1u));
-                const uint32_t s0 = g < 2u ? (u & 63u) : ((v & 15u) | ((u >> 2) & 0x30u));
-                const uint32_t s1 =
-                    g < 2u ? ((u >> 8) & 63u) : (((v >> 8) & 15u) | ((u >> 10) & 0x30u));
+                /* scales of sub-blocks 2g and 2g + 1 (src/kq_numeric.c:161-174),
+                 * bitwise selects (a ?: on g becomes a divergent branch) */
+                uint32_t s0, s1, m0u, m1u;
+                kq_k_scale_pair(g, hd[m].y, hd[m].z, hd[m].w, &s0, &m0u, &s1, &m1u);
                 const _Float16 fs0 = (_Float16)(float)s0, fs1 = (_Float16)(float)s1;
                 S0[m] = h2{fs0, fs0};
                 C0[m] = S0[m] * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
@@ -394,15 +392,14 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_kq(GuArgs a) {
                     C1[m] = h2{fs1, fs1} * h2{(_Float16)-64.0f, (_Float16)-64.0f};
                 }
                 /* mins m_4g .. m_4g+3 for g < 2; zero for g >= 2 */
-                const uint32_t mq = g == 0u ? (hd[m].z & 0x3f3f3f3fu)
-                                            : (((hd[m].w >> 4) & 0x0f0f0f0fu) |
-                                               ((hd[m].z >> 2) & 0x30303030u));
+                const uint32_t k0 = 0u - (uint32_t)(g == 0u), k01 = 0u - (uint32_t)(g < 2u);
+                const uint32_t mq = ((hd[m].z & 0x3f3f3f3fu) & k0) |
+                                    ((((hd[m].w >> 4) & 0x0f0f0f0fu) | ((hd[m].z >> 2) & 0x30303030u)) & ~k0);
                 const h2 one = h2{(_Float16)1.0f, (_Float16)1.0f};
                 const h2 neg = h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
-                const h2 zero = h2{(_Float16)0.0f, (_Float16)0.0f};
-                const h2 mlo = g < 2u ? fma2(byte_pair_lo(mq), one, neg) : zero;
-                const h2 mhi = g < 2u ? fma2(byte_pair_hi(mq), one, neg) : zero;
-                bm[m] = h4{mlo.x, mlo.y, mhi.x, mhi.y};
+                const uint32_t mlo = __builtin_bit_cast(uint32_t, fma2(byte_pair_lo(mq), one, neg)) & k01;
+                const uint32_t mhi = __builtin_bit_cast(uint32_t, fma2(byte_pair_hi(mq), one, neg)) & k01;
+                bm[m] = __builtin_bit_cast(h4, make_uint2(mlo, mhi));
             }
             f4 qacc[NM];
 #pragma unroll
@@ -455,6 +452,262 @@ __global__ __launch_bounds__(NB * WPB * 64) void gu_kq(GuArgs a) {
     if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
 }
 
+/* ------------------------------------------------------------------ */
+/* the pass on mixed tiles: 8 gate rows and the same 8 up rows per tile */
+
+/* With 16 gate and 16 up rows per tile a workgroup's ring and partial sums
+ * need one CU's LDS, so the CU runs one workgroup whose waves meet at a
+ * barrier every tile. Here one 16-row MFMA operand holds rows r0 .. r0 + 7
+ * of gate (operand rows 0-7) and the same rows of up (8-15): a tile is half
+ * the bytes, two workgroups share a CU, and their barriers are independent.
+ * The arithmetic per block and row is gu_kq's; the SwiGLU pairs result
+ * column j (gate) with column j + 8 (up). */
+template <uint32_t FMT, uint32_t NB>
+struct GuMixShape {
+    static_assert(FMT == KQ_LAUNCH_Q4_K || FMT == KQ_LAUNCH_Q5_K, "format");
+    static constexpr bool Q5 = FMT == KQ_LAUNCH_Q5_K;
+    static constexpr uint32_t MR = 8u;                      /* rows per matrix and tile */
+    static constexpr uint32_t BB = Q5 ? 176u : 144u;        /* block bytes */
+    static constexpr uint32_t CB = BB / 16u;
+    static constexpr uint32_t QS = Q5 ? 48u : 16u;
+    static constexpr uint32_t W = NB;                       /* waves: one per block */
+    static constexpr uint32_t RB = BB * NB;                 /* row bytes */
+    static constexpr uint32_t CH = RB / 16u;
+    static constexpr uint32_t PITCH = (CH & 1u) ? CH : CH + 1u; /* odd: conflict-free rows */
+    static constexpr uint32_t SLOTS = MR * PITCH;           /* chunk slots per matrix half */
+    static constexpr uint32_t IM = (SLOTS + 63u) / 64u;     /* instructions per half */
+    static constexpr uint32_t LPW = (2u * IM + W - 1u) / W; /* loads per wave per tile */
+    static constexpr uint32_t ENTRY = 2u * IM * 1024u;
+    static constexpr uint32_t PART = NB * 4u * 64u;         /* floats per partial buffer */
+    static constexpr uint32_t FIXED = 1024u + 2u * PART * 4u + 2u * kT * 4u;
+    static constexpr uint32_t BUDGET = 80u * 1024u;         /* two workgroups per CU */
+    static constexpr uint32_t RING = 3u * ENTRY + FIXED <= BUDGET ? 3u : 2u;
+    static constexpr uint32_t PD = RING - 1u;
+    static_assert(RING * ENTRY + FIXED <= BUDGET, "LDS");
+    static_assert(W <= 16u, "workgroup size");
+};
+
+template <uint32_t FMT, uint32_t NB>
+__global__ __launch_bounds__(NB * 64) void gu_mix(GuArgs a) {
+    using S = GuMixShape<FMT, NB>;
+    constexpr uint32_t KD = 256u * NB;
+    __shared__ __align__(16) uint8_t ring[S::RING * S::ENTRY];
+    __shared__ __align__(16) uint8_t trash[1024]; /* landing place of the padding loads */
+    __shared__ __align__(16) float part[2][S::PART];
+    __shared__ int s_sig[2][kT]; /* by item parity */
+
+    const uint32_t nt = (a.rows + S::MR - 1u) / S::MR; /* tiles per item */
+    const uint64_t total = (uint64_t)(*a.n_items) * nt;
+    const uint32_t lo = (uint32_t)(total * blockIdx.x / gridDim.x);
+    const uint32_t hi = (uint32_t)(total * (blockIdx.x + 1u) / gridDim.x);
+    if (lo >= hi) return;
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t b = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* this wave's block */
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t wbytes = a.rows * S::RB;
+
+    /* this wave's LPW instructions of a tile (instruction n = b * LPW + q:
+     * gate rows for n < IM, up rows for n < 2 IM, padding after): the
+     * lane's byte offset relative to the tile's first row */
+    uint32_t rel[S::LPW];
+#pragma unroll
+    for (uint32_t q = 0; q < S::LPW; ++q) {
+        const uint32_t n = b * S::LPW + q;
+        const uint32_t s = (n < S::IM ? n : n - S::IM) * 64u + lane;
+        const uint32_t jj = s / S::PITCH, c = s % S::PITCH;
+        /* a pad slot (c == CH) holds the next row's first chunk; slots past
+         * the tile and the padding instructions re-read the tile's start */
+        rel[q] = (n < 2u * S::IM && s < S::SLOTS) ? 16u * (jj * S::CH + c) : 0u;
+    }
+    uint32_t iss_it = lo / nt, iss_tile = lo - (lo / nt) * nt, iss_slot = 0u;
+    bool iss_new = true;
+    i4v rg = {0, 0, 0, 0}, ru = {0, 0, 0, 0};
+    auto issue = [&]() {
+        if (iss_new) {
+            iss_new = false;
+            const uint32_t ex = sload(a.items + 2u * iss_it);
+            const uint8_t *gb = (ex & kShared) ? a.sgate : a.gate + (size_t)ex * wbytes;
+            const uint8_t *ub = (ex & kShared) ? a.sup : a.up + (size_t)ex * wbytes;
+            rg = dma_rsrc(gb, wbytes);
+            ru = dma_rsrc(ub, wbytes);
+        }
+        const uint32_t toff = iss_tile * S::MR * S::RB;
+        const uint32_t slot = lds_addr(ring) + iss_slot * S::ENTRY;
+#pragma unroll
+        for (uint32_t q = 0; q < S::LPW; ++q) {
+            const uint32_t n = b * S::LPW + q; /* wave-uniform */
+            const bool up = n >= S::IM && n < 2u * S::IM;
+            dma16(up ? ru : rg, toff + rel[q], n < 2u * S::IM ? slot + n * 1024u : lds_addr(trash));
+        }
+        iss_slot = iss_slot + 1u == S::RING ? 0u : iss_slot + 1u;
+        if (++iss_tile == nt) {
+            iss_tile = 0u;
+            ++iss_it;
+            iss_new = true;
+        }
+    };
+
+    const kq::StagedX sx = kq::staged_at(const_cast<void *>(a.staged), a.tokens, KD);
+    const KqBuf bxh = kq_buf(sx.xh, a.tokens * KD * 2u), bxl = kq_buf(sx.xl, a.tokens * KD * 2u);
+    const KqBuf bsx = kq_buf(sx.sx, a.tokens * (KD / 128u) * 16u);
+    const uint32_t tk = a.tokens * a.top_k;
+    float *out = a.act;
+    bool bad = false, malformed = false;
+
+#pragma unroll
+    for (uint32_t t = 0; t < S::PD; ++t)
+        if (lo + t < hi) issue();
+
+    h8 ah[8], al[8];
+    h4 sh4, sl4;
+    uint32_t cur = 0xffffffffu, pos0 = 0u, count = 0u, par = 1u;
+    uint32_t ctile = lo - (lo / nt) * nt, cslot = 0u, rtile = 0u;
+    auto enter = [&](uint32_t it) {
+        cur = it;
+        par ^= 1u;
+        const uint32_t ex = sload(a.items + 2u * it), fc = sload(a.items + 2u * it + 1u);
+        const uint32_t first = fc & 0xffffffu;
+        count = fc >> 24;
+        const bool sh = (ex & kShared) != 0u;
+        pos0 = sh ? tk + first : first;
+        uint32_t tok = 0xffffffffu;
+        if (j < count) tok = sh ? first + j : a.perm_tok[first + j];
+        const int sg = tok < a.tokens ? sx.sig[tok] : 0;
+        const uint32_t xo = tok < a.tokens ? (tok * KD + 256u * b + 64u * g) * 2u : 0x80000000u;
+#pragma unroll
+        for (uint32_t s = 0; s < 8u; ++s) {
+            ah[s] = __builtin_bit_cast(h8, kq_ld128(bxh, xo + 16u * s, 0u));
+            al[s] = __builtin_bit_cast(h8, kq_ld128(bxl, xo + 16u * s, 0u));
+        }
+        const uint32_t so =
+            tok < a.tokens ? ((tok * (KD / 128u)) + 2u * b + (g & 1u)) * 16u : 0x80000000u;
+        const uint4 sums = kq_ld128(bsx, so, 0u);
+        sh4 = __builtin_bit_cast(h4, make_uint2(sums.x, sums.y));
+        sl4 = __builtin_bit_cast(h4, make_uint2(sums.z, sums.w));
+        if (threadIdx.x < kT) s_sig[par][threadIdx.x] = sg;
+        wait_vm_all();
+    };
+    enter(lo / nt);
+
+    /* lane (j, g)'s operand row: gate (j < 8) or up row r0 + (j & 7) */
+    const uint32_t half = j >> 3, jr = j & 7u;
+    for (uint32_t tau = lo;; ++tau) {
+        if (tau + S::PD - 1u < hi && S::PD >= 2u)
+            wait_vm<(int)S::LPW * (S::PD >= 2u ? (int)S::PD - 1 : 0)>();
+        else
+            wait_vm<0>();
+        kq_lds_barrier();
+        if (tau > lo) {
+            /* tile tau - 1 (of item cur): sum the blocks' partials in
+             * order, SwiGLU: result (token 4g + q, gate row r) sits in
+             * column r of the lanes of k-group g, the up row in column
+             * r + 8 */
+            const float *pp = part[(tau - 1u) & 1u];
+            const uint32_t row0 = rtile * S::MR;
+            for (uint32_t t4 = threadIdx.x; t4 < kT * S::MR; t4 += S::W * 64u) {
+                const uint32_t r = t4 & 7u, i = t4 >> 3, q = i & 3u, lg = (i >> 2) * 16u + r;
+                float gs = 0.0f, us = 0.0f;
+#pragma unroll
+                for (uint32_t bb = 0; bb < NB; ++bb) {
+                    gs += pp[(bb * 4u + q) * 64u + lg];
+                    us += pp[(bb * 4u + q) * 64u + lg + 8u];
+                }
+                const uint32_t row = row0 + r;
+                const bool valid = i < count && row < a.rows;
+                const int sg = s_sig[par][i];
+                const float gv = ldexpf(gs, -sg), uv = ldexpf(us, -sg);
+                /* silu(g) u with the hardware exponential: the activations
+                 * are compared by tolerance like every accumulated output */
+                const float v = gv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv * 1.44269504088896341f)) * uv;
+                bad |= valid && (!kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(v));
+                if (valid) out[(size_t)(pos0 + i) * a.rows + row] = v;
+            }
+        }
+        if (tau == hi) break;
+        if (ctile == nt) {
+            ctile = 0u;
+            enter(cur + 1u);
+        }
+        if (tau + S::PD < hi) issue();
+
+        const uint8_t *ent = ring + cslot * S::ENTRY;
+        rtile = ctile++;
+        cslot = cslot + 1u == S::RING ? 0u : cslot + 1u;
+        const uint8_t *rowp = ent + half * S::IM * 1024u + (jr * S::PITCH + S::CB * b) * 16u;
+        const uint4 hd = *(const uint4 *)rowp;
+        const uint4 qa = *(const uint4 *)(rowp + S::QS + 32u * g);
+        const uint4 qb = *(const uint4 *)(rowp + S::QS + 16u + 32u * g);
+        uint4 ha = {0u, 0u, 0u, 0u}, hb = {0u, 0u, 0u, 0u};
+        if constexpr (S::Q5) {
+            ha = *(const uint4 *)(rowp + 16u);
+            hb = *(const uint4 *)(rowp + 32u);
+        }
+        const float d = half_bits(hd.x);
+        const float dmin = half_bits(hd.x >> 16);
+        malformed |= !kq_isfinite(d) || !kq_isfinite(dmin);
+        const float dm = dmin * 32.0f; /* the sums carry 2^-5 */
+        /* scales of sub-blocks 2g and 2g + 1 (src/kq_numeric.c:161-174),
+         * bitwise selects (a ?: on g becomes a divergent branch) */
+        uint32_t s0, s1, m0u, m1u;
+        kq_k_scale_pair(g, hd.y, hd.z, hd.w, &s0, &m0u, &s1, &m1u);
+        const _Float16 fs0 = (_Float16)(float)s0, fs1 = (_Float16)(float)s1;
+        const h2 S0 = h2{fs0, fs0};
+        const h2 C0 = S0 * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+        h2 S1, C1;
+        if constexpr (S::Q5) {
+            S1 = h2{fs1, fs1};
+            C1 = S1 * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+        } else {
+            S1 = h2{fs1, fs1} * h2{(_Float16)0.0625f, (_Float16)0.0625f};
+            C1 = h2{fs1, fs1} * h2{(_Float16)-64.0f, (_Float16)-64.0f};
+        }
+        /* mins m_4g .. m_4g+3 for g < 2; zero for g >= 2 */
+        const uint32_t k0 = 0u - (uint32_t)(g == 0u), k01 = 0u - (uint32_t)(g < 2u);
+        const uint32_t mq = ((hd.z & 0x3f3f3f3fu) & k0) |
+                            ((((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)) & ~k0);
+        const h2 one = h2{(_Float16)1.0f, (_Float16)1.0f};
+        const h2 neg = h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+        const uint32_t mlo = __builtin_bit_cast(uint32_t, fma2(byte_pair_lo(mq), one, neg)) & k01;
+        const uint32_t mhi = __builtin_bit_cast(uint32_t, fma2(byte_pair_hi(mq), one, neg)) & k01;
+        const h4 bm = __builtin_bit_cast(h4, make_uint2(mlo, mhi));
+        f4 qacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t s = 0; s < 8u; ++s) {
+            const uint4 &qd = (s & 2u) ? qb : qa;
+            const uint32_t raw0 = (s & 1u) ? qd.z : qd.x, raw1 = (s & 1u) ? qd.w : qd.y;
+            uint32_t m0, m1;
+            if constexpr (S::Q5) {
+                const uint4 &hq = (s & 2u) ? hb : ha;
+                const uint32_t h0 = (s & 1u) ? hq.z : hq.x, h1 = (s & 1u) ? hq.w : hq.y;
+                const uint32_t sh = s < 4u ? 2u * g : 2u * g + 1u;
+                const uint32_t n0 = s < 4u ? raw0 : raw0 >> 4;
+                const uint32_t n1 = s < 4u ? raw1 : raw1 >> 4;
+                m0 = (n0 & 0x0f0f0f0fu) | (((h0 >> sh) & 0x01010101u) << 4);
+                m1 = (n1 & 0x0f0f0f0fu) | (((h1 >> sh) & 0x01010101u) << 4);
+            } else {
+                m0 = s < 4u ? kq_and_0f(raw0) : kq_and_f0(raw0);
+                m1 = s < 4u ? kq_and_0f(raw1) : kq_and_f0(raw1);
+            }
+            const h2 Sc = s < 4u ? S0 : S1, Cc = s < 4u ? C0 : C1;
+            const h2 w0 = fma2(byte_pair_lo(m0), Sc, Cc), w1 = fma2(byte_pair_hi(m0), Sc, Cc);
+            const h2 w2 = fma2(byte_pair_lo(m1), Sc, Cc), w3 = fma2(byte_pair_hi(m1), Sc, Cc);
+            const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+            qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s], bw, qacc, 0, 0, 0);
+            qacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s], bw, qacc, 0, 0, 0);
+        }
+        f4 mm = {0.f, 0.f, 0.f, 0.f};
+        mm = __builtin_amdgcn_mfma_f32_16x16x16f16(sh4, bm, mm, 0, 0, 0);
+        mm = __builtin_amdgcn_mfma_f32_16x16x16f16(sl4, bm, mm, 0, 0, 0);
+        float *pw = part[tau & 1u];
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) pw[(b * 4u + q) * 64u + lane] = fmaf(d, qacc[q], -dm * mm[q]);
+    }
+    wait_vm<0>();
+    if (malformed) kq_flag(a.status, KQ_DEV_MALFORMED);
+    if (bad) kq_flag(a.status, KQ_DEV_NUMERIC);
+}
+
 /* waves per block: one (gate and up in one wave) */
 template <uint32_t NB>
 constexpr uint32_t gu_wpb() {
@@ -472,8 +725,14 @@ hipError_t launch_gu(const GuArgs &a, hipStream_t s) {
             cus < 1)
             cus = 256;
     }
-    /* one workgroup per CU: the LDS ring holds one */
-    hipLaunchKernelGGL((gu_kq<FMT, NB, WPB>), dim3((uint32_t)cus), dim3(NB * WPB * 64), 0, s, a);
+    if constexpr (NB == 8u) {
+        /* mixed tiles: two workgroups of eight waves per CU */
+        hipLaunchKernelGGL((gu_mix<FMT, NB>), dim3(2u * (uint32_t)cus), dim3(NB * 64), 0, s, a);
+    } else {
+        /* one workgroup per CU: the LDS ring holds one */
+        hipLaunchKernelGGL((gu_kq<FMT, NB, WPB>), dim3((uint32_t)cus), dim3(NB * WPB * 64), 0, s,
+                           a);
+    }
     return hipGetLastError();
 }
 
