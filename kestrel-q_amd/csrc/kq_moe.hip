@@ -1110,8 +1110,11 @@ __device__ __forceinline__ void write_selection(const RouteArgs &a, const double
     const uint32_t my_id = lane < k ? srt_id[lane] : 0xffffffffu;
     const float ex = lane < k ? fast_expf((float)(srt_v[lane < k ? lane : 0] - m)) : 0.0f;
     const float psel = wave_sum_f32(ex);
+    /* the slot's place in ascending id order, from the other lanes' ids
+     * (register reads, not an LDS round trip per slot) */
     uint32_t rk = 0;
-    for (uint32_t j = 0; j < k; ++j) rk += (uint32_t)(srt_id[j] < my_id);
+    for (uint32_t j = 0; j < k; ++j)
+        rk += (uint32_t)((uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)j) < my_id);
     if (lane < k) {
         a.ids[lane] = my_id;
         if (a.ids_out) a.ids_out[lane] = my_id;
@@ -1205,8 +1208,37 @@ __device__ __forceinline__ void select_one(const RouteArgs &a) {
         }
     }
     __syncthreads();
+    const uint32_t total = s_count;
+    if (total <= kCertCand) {
+        /* every thread: candidate c = e / 8 against candidates e % 8,
+         * e % 8 + 8, ... (descending a, ascending id); the eight partial
+         * counts of lanes 8c .. 8c + 7 summed give its rank, and lane 8c
+         * places it. A lone wave ranking all of them paid an LDS round
+         * trip per eight candidates. */
+        const uint32_t c = e >> 3, sl = e & 7u;
+        uint32_t r = 0u;
+        double mc = 0.0;
+        uint32_t ic = 0u;
+        if (c < total) {
+            mc = cv[c];
+            ic = cid[c];
+            for (uint32_t j = sl; j < total; j += 8u) {
+                const double o = cv[j];
+                const uint32_t oi = cid[j];
+                r += (uint32_t)(o > mc) | ((uint32_t)(o == mc) & (uint32_t)(oi < ic));
+            }
+        }
+        r += __shfl_xor(r, 1, 64);
+        r += __shfl_xor(r, 2, 64);
+        r += __shfl_xor(r, 4, 64);
+        if (c < total && sl == 0u) {
+            sv[r] = mc;
+            sb[r] = cb[c];
+            sid[r] = ic;
+        }
+    }
+    __syncthreads();
     if (w == 0u) {
-        const uint32_t total = s_count;
         double rest = w_rest[0];
         uint32_t anybad = w_bad[0];
 #pragma unroll
@@ -1216,25 +1248,10 @@ __device__ __forceinline__ void select_one(const RouteArgs &a) {
         }
         uint32_t state = 3u;
         if (anybad == 0u && total <= kCertCand && sh_b < __builtin_inf()) {
-            /* each lane ranks candidates lane and lane + 64; the places
-             * past the list get entries that never rank above one */
+            /* the candidates ranked k and after join the rest */
             const uint32_t j1 = lane + 64u;
-            const bool h0 = lane < total, h1 = j1 < total;
-            const double m0 = h0 ? cv[lane] : ninf, m1 = h1 ? cv[j1] : ninf;
-            const uint32_t i0 = h0 ? cid[lane] : 0xffffffffu, i1 = h1 ? cid[j1] : 0xffffffffu;
-            const double b0 = h0 ? cb[lane] : 0.0, b1 = h1 ? cb[j1] : 0.0;
-            uint32_t r0, r1;
-            rank2(cv, cid, total, m0, i0, m1, i1, r0, r1);
-            r0 = h0 ? r0 : lane;
-            r1 = h1 ? r1 : j1;
-            sv[r0] = m0;
-            sb[r0] = b0;
-            sid[r0] = i0;
-            sv[r1] = m1;
-            sb[r1] = b1;
-            sid[r1] = i1;
-            const double o0 = h0 && r0 >= top_k ? m0 + b0 : ninf;
-            const double o1 = h1 && r1 >= top_k ? m1 + b1 : ninf;
+            const double o0 = lane >= top_k && lane < total ? sv[lane] + sb[lane] : ninf;
+            const double o1 = j1 >= top_k && j1 < total ? sv[j1] + sb[j1] : ninf;
             rest = fmax(rest, kq_wave_max_f64(fmax(o0, o1)));
             if (separated(sv, sb, top_k, rest)) {
                 write_selection(a, sv, sid);
