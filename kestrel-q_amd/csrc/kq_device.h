@@ -172,9 +172,14 @@ __device__ __forceinline__ void kq_k_scale_pair(uint32_t p, uint32_t w0, uint32_
 }
 
 /* Workgroup barrier that orders LDS accesses only: global loads issued
- * before it stay in flight across it. */
+ * before it stay in flight across it. The LDS-only release fence does not
+ * make the compiler wait for the wave's own LDS writes (it takes LDS
+ * operations as ordered across waves), and without the wait the last
+ * ds_write before the barrier has been read stale by other waves: the
+ * explicit lgkmcnt(0) completes them first. */
 __device__ __forceinline__ void kq_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
