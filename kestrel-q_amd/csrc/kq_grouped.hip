@@ -804,7 +804,8 @@ __global__ __launch_bounds__(1024) void moe_permute(const uint32_t *__restrict__
                                                     uint32_t *__restrict__ pos,
                                                     uint32_t *__restrict__ pair_slot,
                                                     uint32_t *status, uint32_t *items,
-                                                    uint32_t with_shared) {
+                                                    uint32_t with_shared, uint32_t *zero,
+                                                    uint32_t nzero) {
     __shared__ uint32_t cnt[1024];
     __shared__ uint32_t base[1024];
     __shared__ uint32_t bits[1024][kPermChunk / 32u];
@@ -813,6 +814,8 @@ __global__ __launch_bounds__(1024) void moe_permute(const uint32_t *__restrict__
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const uint32_t pairs = tokens * top_k;
     cnt[tid] = 0u;
+    /* words a later pass accumulates into (atomic maxima) start at zero */
+    for (uint32_t i = tid; i < nzero; i += 1024u) zero[i] = 0u;
     __syncthreads();
     bool bad = false;
     for (uint32_t p = tid; p < pairs; p += 1024u) {
@@ -1701,7 +1704,7 @@ extern "C" hipError_t kq_launch_moe_permute(const uint32_t *ids, uint32_t tokens
                                             uint32_t *pair_slot, uint32_t *status,
                                             hipStream_t s) {
     hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ids, tokens, top_k, experts,
-                       offsets, pair_token, pos, pair_slot, status, nullptr, 0u);
+                       offsets, pair_token, pos, pair_slot, status, nullptr, 0u, nullptr, 0u);
     return hipGetLastError();
 }
 
@@ -1726,9 +1729,18 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
      * it (gitems) also drives the Q6_K down pass (kq_grouped_dn.hip) */
     const bool lds_routed = gu_lds_routed(d, w);
     const bool lds_shared = lds_routed && w->shared_gate_type == w->gate_type;
+    /* the mixed-tile gate/up pass (hidden 2048) records each position's
+     * largest activation, and the Q6_K pair down pass (intermediate 512)
+     * then splits its own operand: no dn_stage. The maxima live in dstage,
+     * which only dn_stage and the dense shared expert use otherwise. */
+    const bool fused_split = lds_shared && d->hidden == 2048u && d->inter == 512u &&
+                             w->down_type == KQ_LAUNCH_Q6_K &&
+                             w->shared_down_type == KQ_LAUNCH_Q6_K;
+    uint32_t *posmax = fused_split ? (uint32_t *)ws->dstage : nullptr;
     hipLaunchKernelGGL(moe_permute, dim3(1), dim3(1024), 0, s, ws->ids, tokens, d->top_k,
                        d->experts, ws->offsets, ws->perm_tok, ws->pos, nullptr, status,
-                       lds_routed ? (uint32_t *)ws->gitems : nullptr, lds_shared ? 1u : 0u);
+                       lds_routed ? (uint32_t *)ws->gitems : nullptr, lds_shared ? 1u : 0u,
+                       posmax, posmax != nullptr ? tokens * (d->top_k + 1u) : 0u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint8_t *g = (const uint8_t *)w->gate, *u = (const uint8_t *)w->up;
@@ -1744,7 +1756,7 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
     if (lds_routed) {
         e = kq_launch_gu_lds(w->gate_type, d->hidden, g, u, sg, su, ws->outp, ws->offsets,
                              ws->perm_tok, E, tokens, d->top_k, d->inter, lds_shared ? 1 : 0, 1,
-                             ws->gitems, ws->act, status, s);
+                             ws->gitems, ws->act, posmax, status, s);
         if (e == hipSuccess && !lds_shared && w->shared_gate_type == KQ_LAUNCH_Q8_0 &&
             kq_launch_dense_q8_supported(d->inter, d->hidden, tokens)) {
             /* a Q8_0 shared expert sees every token: the dense product on
@@ -1794,7 +1806,7 @@ extern "C" hipError_t kq_launch_moe_grouped(const kq_launch_moe_dims *d,
         kq_launch_dn_lds_supported(d->inter)) {
         /* over the gate/up pass's item list (routed and shared chunks) */
         e = kq_launch_dn_lds(d->inter, d->hidden, dn, sd, ws->act, tokens, d->top_k, ws->gitems,
-                             ws->dstage, ws->outp, status, s);
+                             ws->dstage, posmax, ws->outp, status, s);
     } else if (lds_routed && kq_launch_dn_small_supported(w->down_type, d->inter) &&
                (!lds_shared || w->shared_down_type == w->down_type)) {
         /* Q5_1 or Q8_0 rows through the same per-wave LDS-DMA pipeline,

@@ -155,6 +155,8 @@ struct DnShape {
 struct DnArgs {
     const uint8_t *down, *sdown;  /* routed stack, shared matrix */
     const void *staged;           /* dn_stage output, positions 0 .. T*K + T - 1 */
+    const float *act;             /* fused split: the activations [T*K + T][inter] */
+    const uint32_t *posmax;       /* and each position's largest |act| (float bits) */
     const uint32_t *items, *n_items;
     uint32_t tokens, top_k, hidden, npos;
     float *out; /* [T*K + T][hidden] */
@@ -362,6 +364,7 @@ struct DnPair {
                   "eight workgroups per CU");
 };
 
+template <bool FUSED>
 __global__ __launch_bounds__(DnPair::W * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void dn_q6k_pair(DnArgs a) {
     using S = DnPair;
@@ -444,20 +447,76 @@ void dn_q6k_pair(DnArgs a) {
         const uint32_t f0 = fc & 0xffffffu;
         count = fc >> 24;
         pos0 = (ex & kShared) ? tk + f0 : f0;
-        /* rows past the chunk read at 2^31, past the buffer */
-        const uint32_t xo = j < count ? ((pos0 + j) * KD + g * (KD / 4u) + h * 64u) * 2u
-                                      : 0x80000000u;
+        if constexpr (FUSED) {
+            /* the operand split here from the fp32 activations, scaled by
+             * each position's largest magnitude exactly as dn_stage does:
+             * sub-block s of block h holds columns 256h + 16s .. + 15, of
+             * which lane group g takes 4g .. 4g + 3; operand entry ai =
+             * (2n + hh) 4 + q is sub-block 8n + 2q + hh */
+            const KqBuf bact = kq_buf(a.act, a.npos * KD * 4u);
+            const KqBuf bpm = kq_buf(a.posmax, a.npos * 4u);
+            const uint32_t fo = j < count ? ((pos0 + j) * KD + 256u * h + 4u * g) * 4u
+                                          : 0x80000000u;
+            uint4 raw[16];
 #pragma unroll
-        for (uint32_t v = 0; v < 8u; ++v) {
-            axh[v] = kq_ld128(bxh, xo + v * 16u, 0u);
-            axl[v] = kq_ld128(bxl, xo + v * 16u, 0u);
-        }
+            for (uint32_t ai = 0; ai < 16u; ++ai) {
+                const uint32_t sb = 8u * (ai >> 3) + 2u * (ai & 3u) + ((ai >> 2) & 1u);
+                raw[ai] = kq_ld128(bact, fo + 64u * sb, 0u);
+            }
+            const uint32_t mj = kq_ld32(bpm, j < count ? (pos0 + j) * 4u : 0x80000000u, 0u);
+            uint32_t mq[4];
 #pragma unroll
-        for (uint32_t q = 0; q < 4u; ++q) {
-            const uint32_t i = 4u * g + q;
-            sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t i = 4u * g + q;
+                mq[q] = kq_ld32(bpm, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
+            }
+            wait_vm_all();
+            auto sig_of = [](uint32_t bits) {
+                const float m = __builtin_bit_cast(float, bits);
+                return m > 0.0f && kq_isfinite(m) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+            };
+            const int sj = sig_of(mj);
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) sg[q] = sig_of(mq[q]);
+#pragma unroll
+            for (uint32_t ai = 0; ai < 16u; ++ai) {
+                const float v[4] = {__builtin_bit_cast(float, raw[ai].x),
+                                    __builtin_bit_cast(float, raw[ai].y),
+                                    __builtin_bit_cast(float, raw[ai].z),
+                                    __builtin_bit_cast(float, raw[ai].w)};
+                _Float16 hi[4], lo[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float xs = ldexpf(v[c], sj);
+                    hi[c] = (_Float16)xs;
+                    lo[c] = (_Float16)(xs - (float)hi[c]);
+                }
+                const uint2 hv = __builtin_bit_cast(uint2, h4{hi[0], hi[1], hi[2], hi[3]});
+                const uint2 lv = __builtin_bit_cast(uint2, h4{lo[0], lo[1], lo[2], lo[3]});
+                if (ai & 1u) {
+                    axh[ai >> 1].z = hv.x, axh[ai >> 1].w = hv.y;
+                    axl[ai >> 1].z = lv.x, axl[ai >> 1].w = lv.y;
+                } else {
+                    axh[ai >> 1].x = hv.x, axh[ai >> 1].y = hv.y;
+                    axl[ai >> 1].x = lv.x, axl[ai >> 1].y = lv.y;
+                }
+            }
+        } else {
+            /* rows past the chunk read at 2^31, past the buffer */
+            const uint32_t xo = j < count ? ((pos0 + j) * KD + g * (KD / 4u) + h * 64u) * 2u
+                                          : 0x80000000u;
+#pragma unroll
+            for (uint32_t v = 0; v < 8u; ++v) {
+                axh[v] = kq_ld128(bxh, xo + v * 16u, 0u);
+                axl[v] = kq_ld128(bxl, xo + v * 16u, 0u);
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint32_t i = 4u * g + q;
+                sg[q] = (int)kq_ld32(bsg, i < count ? (pos0 + i) * 4u : 0x80000000u, 0u);
+            }
+            wait_vm_all();
         }
-        wait_vm_all();
     };
 
     /* block 0's sums of the previous round plus block 1's: D[token][row],
@@ -867,7 +926,7 @@ void dn_small_pair(DnArgs a) {
 }
 
 template <uint32_t KB>
-hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
+hipError_t launch_dn(const DnArgs &a, hipStream_t s, bool fused) {
     static int cus = 0;
     if (cus == 0) {
         int dev = 0;
@@ -878,7 +937,12 @@ hipError_t launch_dn(const DnArgs &a, hipStream_t s) {
     }
     if constexpr (KB == 2u) {
         /* eight workgroups per CU: four waves per SIMD */
-        hipLaunchKernelGGL(dn_q6k_pair, dim3(8u * (uint32_t)cus), dim3(DnPair::W * 64), 0, s, a);
+        if (fused)
+            hipLaunchKernelGGL(dn_q6k_pair<true>, dim3(8u * (uint32_t)cus), dim3(DnPair::W * 64), 0,
+                               s, a);
+        else
+            hipLaunchKernelGGL(dn_q6k_pair<false>, dim3(8u * (uint32_t)cus), dim3(DnPair::W * 64),
+                               0, s, a);
     } else {
         /* one workgroup per CU (the slots' LDS) */
         hipLaunchKernelGGL((dn_q6k<KB>), dim3((uint32_t)cus), dim3(DnShape<KB>::W * 64), 0, s, a);
@@ -913,6 +977,8 @@ extern "C" hipError_t kq_launch_dn_small(uint32_t type, uint32_t inter, uint32_t
     a.down = (const uint8_t *)down;
     a.sdown = (const uint8_t *)shared_down;
     a.staged = staged;
+    a.act = nullptr;
+    a.posmax = nullptr;
     a.n_items = (const uint32_t *)items;
     a.items = (const uint32_t *)items + 4;
     a.tokens = tokens;
@@ -952,21 +1018,29 @@ extern "C" uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter) {
 }
 
 /* down over the item list the gate/up pass built (items, as written by
- * kq_launch_gu_lds): the per-position split of act, then the pass */
+ * kq_launch_gu_lds): the per-position split of act, then the pass; with
+ * posmax (each position's largest |act|, recorded by the mixed-tile gate/up
+ * pass; intermediate 512 only) the pass splits its operand itself */
 extern "C" hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const void *down,
                                        const void *shared_down, const float *act,
                                        uint32_t tokens, uint32_t top_k, const void *items,
-                                       void *staged, float *out, uint32_t *status,
-                                       hipStream_t s) {
-    if (!kq_launch_dn_lds_supported(inter)) return hipErrorInvalidValue;
+                                       void *staged, const uint32_t *posmax, float *out,
+                                       uint32_t *status, hipStream_t s) {
+    if (!kq_launch_dn_lds_supported(inter) || (posmax != nullptr && inter != 512u))
+        return hipErrorInvalidValue;
     const uint32_t npos = tokens * top_k + tokens;
-    hipLaunchKernelGGL(dn_stage, dim3(npos), dim3(64), 0, s, act, npos, inter, staged, status);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (posmax == nullptr) {
+        hipLaunchKernelGGL(dn_stage, dim3(npos), dim3(64), 0, s, act, npos, inter, staged,
+                           status);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     DnArgs a;
     a.down = (const uint8_t *)down;
     a.sdown = (const uint8_t *)shared_down;
     a.staged = staged;
+    a.act = act;
+    a.posmax = posmax;
     a.n_items = (const uint32_t *)items;
     a.items = (const uint32_t *)items + 4;
     a.tokens = tokens;
@@ -975,5 +1049,5 @@ extern "C" hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const vo
     a.npos = npos;
     a.out = out;
     a.status = status;
-    return inter == 256u ? launch_dn<1>(a, s) : launch_dn<2>(a, s);
+    return inter == 256u ? launch_dn<1>(a, s, false) : launch_dn<2>(a, s, posmax != nullptr);
 }

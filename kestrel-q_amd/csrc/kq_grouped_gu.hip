@@ -126,6 +126,7 @@ struct GuArgs {
     const uint32_t *n_items;
     uint32_t tokens, top_k, rows;
     float *act; /* [T*K + T][rows] */
+    uint32_t *posmax; /* [T*K + T] or null: each position's largest |act| (float bits) */
     uint32_t *status;
 };
 
@@ -622,6 +623,17 @@ __global__ __launch_bounds__(NB * 64) void gu_mix(GuArgs a) {
                 const float v = gv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv * 1.44269504088896341f)) * uv;
                 bad |= valid && (!kq_isfinite(gv) || !kq_isfinite(uv) || !kq_isfinite(v));
                 if (valid) out[(size_t)(pos0 + i) * a.rows + row] = v;
+                if (a.posmax != nullptr) {
+                    /* the position's largest magnitude over the tile's 8
+                     * rows (lanes 8i .. 8i + 7), then over all tiles: float
+                     * bits of non-negative values order as integers */
+                    float mv = valid && kq_isfinite(v) ? fabsf(v) : 0.0f;
+                    mv = fmaxf(mv, __shfl_xor(mv, 1, 64));
+                    mv = fmaxf(mv, __shfl_xor(mv, 2, 64));
+                    mv = fmaxf(mv, __shfl_xor(mv, 4, 64));
+                    if (r == 0u && i < count && mv > 0.0f)
+                        atomicMax(a.posmax + pos0 + i, __builtin_bit_cast(uint32_t, mv));
+                }
             }
         }
         if (tau == hi) break;
@@ -774,7 +786,8 @@ extern "C" hipError_t kq_launch_gu_lds(uint32_t type, uint32_t hidden, const voi
                                        const uint32_t *perm_tok, uint32_t experts,
                                        uint32_t tokens, uint32_t top_k, uint32_t rows,
                                        int with_shared, int items_ready, void *items,
-                                       float *act, uint32_t *status, hipStream_t s) {
+                                       float *act, uint32_t *posmax, uint32_t *status,
+                                       hipStream_t s) {
     if (experts > 1023u || !kq_launch_gu_lds_supported(type, hidden)) return hipErrorInvalidValue;
     uint32_t *n_items = (uint32_t *)items;
     uint32_t *list = n_items + 4;
@@ -797,6 +810,9 @@ extern "C" hipError_t kq_launch_gu_lds(uint32_t type, uint32_t hidden, const voi
     a.top_k = top_k;
     a.rows = rows;
     a.act = act;
+    /* the positions' maxima come from the mixed-tile pass only */
+    if (posmax != nullptr && hidden != 2048u) return hipErrorInvalidValue;
+    a.posmax = posmax;
     a.status = status;
 #define KQ_GU_HIDDEN(F)                               \
     switch (hidden) {                                 \

@@ -195,13 +195,15 @@ uint64_t kq_launch_gu_stage_bytes(uint32_t tokens, uint32_t hidden);
 hipError_t kq_launch_gu_stage(const float *hidden_states, uint32_t tokens, uint32_t hidden,
                               void *staged, uint32_t *status, hipStream_t s);
 uint64_t kq_launch_gu_items_bytes(uint32_t experts, uint32_t tokens, uint32_t top_k);
-/* items_ready: the permutation already wrote the item list (moe_permute) */
+/* items_ready: the permutation already wrote the item list (moe_permute);
+ * posmax (hidden 2048 only, zeroed beforehand, or NULL): each position's
+ * largest |act| as float bits, for kq_launch_dn_lds */
 hipError_t kq_launch_gu_lds(uint32_t type, uint32_t hidden, const void *gate, const void *up,
                             const void *shared_gate, const void *shared_up, const void *staged,
                             const uint32_t *offsets, const uint32_t *perm_tok, uint32_t experts,
                             uint32_t tokens, uint32_t top_k, uint32_t rows, int with_shared,
-                            int items_ready, void *items, float *act, uint32_t *status,
-                            hipStream_t s);
+                            int items_ready, void *items, float *act, uint32_t *posmax,
+                            uint32_t *status, hipStream_t s);
 /* prefill Q5_1 or Q8_0 down (type) over the same item list
  * (kq_grouped_dn.hip); staged is scratch of kq_launch_dn_stage_bytes */
 int kq_launch_dn_small_supported(uint32_t type, uint32_t inter);
@@ -214,8 +216,9 @@ int kq_launch_dn_lds_supported(uint32_t inter);
 uint64_t kq_launch_dn_stage_bytes(uint32_t npos, uint32_t inter);
 hipError_t kq_launch_dn_lds(uint32_t inter, uint32_t hidden, const void *down,
                             const void *shared_down, const float *act, uint32_t tokens,
-                            uint32_t top_k, const void *items, void *staged, float *out,
-                            uint32_t *status, hipStream_t s);
+                            uint32_t top_k, const void *items, void *staged,
+                            const uint32_t *posmax, float *out, uint32_t *status,
+                            hipStream_t s);
 /* where the Q4_K / Q5_K gate/up pass reads its per-token activation split (ws's
  * outp), or NULL when these weights take another pass; the route can form
  * it (kq_launch_moe_route's stage), and staged tells the grouped path so */
