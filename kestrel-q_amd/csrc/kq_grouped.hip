@@ -1517,6 +1517,266 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_mfma_q6k(
 }
 
 /* ------------------------------------------------------------------ */
+/* The same product at 2,048 columns on whole tiles shared by a workgroup
+ *
+ * matvec_mfma_q6k gives every wave its own ring of block slots and its own
+ * tiles, so the weights in flight grow with the waves and two waves per
+ * SIMD fill the LDS. Here a workgroup of eight waves owns a contiguous run
+ * of 16-row tiles; a tile (16 rows x 1,680 contiguous bytes) is copied into
+ * a two-slot LDS ring by 1 KiB LDS-DMA instructions spread over the waves,
+ * one tile ahead of the one being multiplied, and wave b multiplies Q6_K
+ * block b of every row of it. Its activation operand (the block's 256
+ * columns of the four columns, hi and lo, laid out as above) is 32
+ * registers held for the whole run, so nothing but the tile is read from
+ * LDS and two workgroups share a CU (four waves per SIMD). Each wave sums
+ * its product rows across lanes and leaves 16 rows x 4 columns in LDS;
+ * after the next barrier wave 0 adds the eight blocks in order, unscales,
+ * stores and keeps the argmax partials: one per workgroup and column. */
+
+constexpr uint32_t kLtWaves = 8u;                      /* one per 256-column block */
+constexpr uint32_t kLtRow = 8u * 210u;                 /* row bytes at 2,048 columns */
+constexpr uint32_t kLtTile = kTile * kLtRow;           /* 26,880 */
+constexpr uint32_t kLtIns = (kLtTile + 1023u) / 1024u; /* DMA instructions per tile: 27 */
+constexpr uint32_t kLtSlot = kLtIns * 1024u;
+constexpr uint32_t kLtIpw = (kLtIns + kLtWaves - 1u) / kLtWaves; /* per wave, at most 4 */
+
+__global__ __launch_bounds__(kLtWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void lm_q6k_tiles(const uint8_t *__restrict__ W, uint32_t rows, const float *__restrict__ x,
+                  uint32_t batch, float *__restrict__ y, uint32_t *status, float *part_v,
+                  uint32_t *part_i, uint32_t part_stride) {
+    constexpr uint32_t K = 2048u;
+    __shared__ __align__(16) uint8_t ring[2][kLtSlot];
+    __shared__ __align__(16) float part[2][kLtWaves][64];
+    __shared__ float smax[kLtWaves][kMvCols];
+    __shared__ uint32_t snf[kLtWaves][kMvCols];
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t b = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* block of the row */
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t ntiles = (rows + kTile - 1u) / kTile;
+    const uint32_t lo = (uint32_t)((uint64_t)ntiles * blockIdx.x / gridDim.x);
+    const uint32_t hi = (uint32_t)((uint64_t)ntiles * (blockIdx.x + 1u) / gridDim.x);
+    const kq_i4v wr = dma_rsrc(W, rows * kLtRow);
+
+    /* instruction n = b + 8 q of a tile: lane l copies tile bytes
+     * [16 (64 n + l), + 16) to the same place in the slot; units past the
+     * tile re-read its first bytes (never used) */
+    uint32_t rel[kLtIpw];
+#pragma unroll
+    for (uint32_t q = 0; q < kLtIpw; ++q) {
+        const uint32_t u = (b + kLtWaves * q) * 64u + lane;
+        rel[q] = u * 16u < kLtTile ? u * 16u : 0u;
+    }
+    auto issue = [&](uint32_t t, uint32_t s) {
+        const uint32_t toff = t * kLtTile, dst = lds_addr(&ring[s][0]);
+#pragma unroll
+        for (uint32_t q = 0; q < kLtIpw; ++q) {
+            const uint32_t n = b + kLtWaves * q; /* wave-uniform */
+            if (n < kLtIns) dma16(wr, toff + rel[q], dst + 1024u * n);
+        }
+    };
+    if (lo < hi) issue(lo, 0u);
+
+    /* column k's power of two from its largest magnitude: wave b scans its
+     * block's 256 columns of the four (16 per lane), the workgroup merges */
+    bool bad = false;
+    {
+        const uint32_t k = lane >> 4, c0 = 256u * b + 16u * (lane & 15u);
+        float m = 0.0f;
+        uint32_t nf = 0u;
+        if (k < batch) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const float4 v = *(const float4 *)(x + (size_t)k * K + c0 + 4u * i);
+                nf |= (!kq_isfinite(v.x) || !kq_isfinite(v.y) || !kq_isfinite(v.z) ||
+                       !kq_isfinite(v.w)) ? 1u : 0u;
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+        }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+            m = fmaxf(m, __shfl_xor(m, o, KQ_WAVE));
+            nf |= __shfl_xor(nf, o, KQ_WAVE);
+        }
+        bad = nf != 0u;
+        if ((lane & 15u) == 0u) {
+            smax[b][k] = m;
+            snf[b][k] = nf;
+        }
+    }
+    __syncthreads();
+    int sig[kMvCols];
+    bool zero[kMvCols];
+#pragma unroll
+    for (uint32_t k = 0; k < kMvCols; ++k) {
+        float m = 0.0f;
+        uint32_t nf = 0u;
+#pragma unroll
+        for (uint32_t w = 0; w < kLtWaves; ++w) {
+            m = fmaxf(m, smax[w][k]);
+            nf |= snf[w][k];
+        }
+        zero[k] = nf != 0u;
+        sig[k] = (nf == 0u && m > 0.0f) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+    }
+
+    /* lane (j, g): token row j of the A operand on k 8 g .. + 7 of step
+     * (n, qq) = columns 256 b + 128 n + 32 qq + 8 g ..; rows 0..3 the hi
+     * parts of columns 0..3, 4..7 their lo parts, 8..15 the same for the
+     * step's second sub-block; lanes off their sub-block hold zeros */
+    h8 av[2][4];
+    {
+        const uint32_t c = j & 3u;
+        const bool live = (j >> 3) == (g >> 1) && c < batch && !zero[c];
+        const bool want_lo = (j & 4u) != 0u;
+        int e = sig[0];
+#pragma unroll
+        for (uint32_t k = 1; k < kMvCols; ++k) e = c == k ? sig[k] : e;
+        const float *xp = x + (size_t)(live ? c : 0u) * K + 256u * b + 8u * g;
+#pragma unroll
+        for (uint32_t n = 0; n < 2u; ++n)
+#pragma unroll
+            for (uint32_t qq = 0; qq < 4u; ++qq) {
+                float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                if (live) {
+                    const float4 p0 = *(const float4 *)(xp + 128u * n + 32u * qq);
+                    const float4 p1 = *(const float4 *)(xp + 128u * n + 32u * qq + 4u);
+                    v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+                    v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+                }
+                h8 h;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float xs = ldexpf(v[i], e);
+                    const _Float16 hv = (_Float16)xs;
+                    h[i] = want_lo ? (_Float16)(xs - (float)hv) : hv;
+                }
+                av[n][qq] = h;
+            }
+    }
+
+    const uint32_t hsh = 8u * (g >> 1); /* this lane's scale byte within a pair */
+    const h2 bias = h2{(_Float16)-1056.0f, (_Float16)-1056.0f}; /* 1024 + 32 */
+    /* row j's block b in a slot: from its 4-byte aligned start, sh bytes in */
+    const uint32_t boff = j * kLtRow + 210u * b;
+    const uint32_t sh = boff & 3u, wbase = boff & ~3u;
+    bool malformed = false, nonfinite = false;
+    float best_v = -__builtin_inff();
+    uint32_t best_i = 0xffffffffu;
+    const uint32_t rk = lane >> 4, rr = lane & 15u; /* wave 0's output: column, row */
+
+    for (uint32_t tau = lo; tau < hi + 1u; ++tau) {
+        wait_vm<0>();
+        kq_lds_barrier();
+        if (tau + 1u < hi) issue(tau + 1u, (tau + 1u - lo) & 1u);
+        if (tau > lo && b == 0u) {
+            /* tile tau - 1: the eight blocks' sums in order */
+            const uint32_t pb = (tau - 1u - lo) & 1u;
+            float s = 0.0f;
+#pragma unroll
+            for (uint32_t w = 0; w < kLtWaves; ++w) s += part[pb][w][lane];
+            const uint32_t row = (tau - 1u) * kTile + rr;
+            if (row < rows && rk < batch) {
+                const float v = ldexpf(s, -sig[rk]);
+                nonfinite |= !kq_isfinite(v);
+                y[(size_t)rk * rows + row] = v;
+                mv_argmax_merge(best_v, best_i, v, row);
+            }
+        }
+        if (tau == hi) break;
+
+        const uint8_t *p = &ring[(tau - lo) & 1u][wbase];
+        auto w32 = [&](uint32_t o) { return *(const uint32_t *)(p + o); };
+        uint32_t wa[2][3], wbv[2][3], wq[2][3], ws[6];
+#pragma unroll
+        for (uint32_t n = 0; n < 2u; ++n) {
+            const uint32_t oa = 64u * n + 8u * g, oq = 128u + 32u * n + 8u * g;
+#pragma unroll
+            for (uint32_t e = 0; e < 3u; ++e) {
+                wa[n][e] = w32(oa + 4u * e);
+                wbv[n][e] = w32(oa + 32u + 4u * e);
+                wq[n][e] = w32(oq + 4u * e);
+            }
+        }
+#pragma unroll
+        for (uint32_t e = 0; e < 6u; ++e) ws[e] = w32(192u + 4u * e);
+        const uint32_t row = tau * kTile + j;
+        const float d = f16f(kq_align2(ws[5], ws[4], sh)); /* block bytes 208, 209 */
+        malformed |= row < rows && !kq_isfinite(d);
+        uint32_t sc[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) sc[e] = kq_align2(ws[e + 1u], ws[e], sh) >> hsh;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t n = 0; n < 2u; ++n) {
+            const uint32_t A[2] = {kq_align2(wa[n][1], wa[n][0], sh),
+                                   kq_align2(wa[n][2], wa[n][1], sh)};
+            const uint32_t B[2] = {kq_align2(wbv[n][1], wbv[n][0], sh),
+                                   kq_align2(wbv[n][2], wbv[n][1], sh)};
+            const uint32_t H[2] = {kq_align2(wq[n][1], wq[n][0], sh),
+                                   kq_align2(wq[n][2], wq[n][1], sh)};
+            uint32_t c[4][2];
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                c[0][w] = (A[w] & 0x0f0f0f0fu) | ((H[w] << 4) & 0x30303030u);
+                c[1][w] = (B[w] & 0x0f0f0f0fu) | ((H[w] << 2) & 0x30303030u);
+                c[2][w] = ((A[w] >> 4) & 0x0f0f0f0fu) | (H[w] & 0x30303030u);
+                c[3][w] = ((B[w] >> 4) & 0x0f0f0f0fu) | ((H[w] >> 2) & 0x30303030u);
+            }
+            f4 tm[4];
+#pragma unroll
+            for (uint32_t qq = 0; qq < 4u; ++qq) {
+                const h2 w0 = bytes_lo(c[qq][0]) + bias, w1 = bytes_hi(c[qq][0]) + bias;
+                const h2 w2 = bytes_lo(c[qq][1]) + bias, w3 = bytes_hi(c[qq][1]) + bias;
+                const h8 bw = h8{w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+                tm[qq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[n][qq], bw,
+                                                                f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t qq = 0; qq < 4u; ++qq) {
+                const int8_t scv = (int8_t)((sc[2u * n + (qq >> 1)] >> (16u * (qq & 1u))) & 0xffu);
+                const float ds = d * (float)scv;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] = fmaf(ds, tm[qq][k], acc[k]);
+            }
+        }
+        /* column k of row j = the four lanes j + 16 G: hi and lo of both
+         * sub-block halves */
+        f4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = acc[k] + __shfl_down(acc[k], 32, KQ_WAVE);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] += __shfl_down(o[k], 16, KQ_WAVE);
+        if (g == 0u) {
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) part[(tau - lo) & 1u][b][16u * k + j] = o[k];
+        }
+    }
+    /* no LDS-DMA load may outlive the workgroup */
+    wait_vm<0>();
+    if (bad) kq_flag(status, KQ_DEV_INPUT);
+    if (malformed) kq_flag(status, KQ_DEV_MALFORMED);
+    if (nonfinite) kq_flag(status, KQ_DEV_NUMERIC);
+    if (part_v != nullptr && b == 0u) {
+        /* wave 0's lanes 16 k .. 16 k + 15 hold column k's candidates */
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best_v, o, KQ_WAVE);
+            const uint32_t oi = __shfl_xor(best_i, o, KQ_WAVE);
+            mv_argmax_merge(best_v, best_i, ov, oi);
+        }
+        if (rr == 0u && rk < batch) {
+            part_v[(size_t)rk * part_stride + blockIdx.x] = best_v;
+            part_i[(size_t)rk * part_stride + blockIdx.x] = best_i;
+            for (uint32_t sl = blockIdx.x + gridDim.x; sl < part_stride; sl += gridDim.x) {
+                part_v[(size_t)rk * part_stride + sl] = -__builtin_inff();
+                part_i[(size_t)rk * part_stride + sl] = 0xffffffffu;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
 /* grouped Q6_K down pass with its weights streamed through LDS
  *
  * The same work split, staging and Tile<Q6_K> steps as grouped_pass, but
@@ -1936,7 +2196,24 @@ static uint32_t mv_blocks(uint32_t rows, uint32_t nb) {
     return blocks < 1u ? 1u : blocks;
 }
 
+/* lm_q6k_tiles (2,048 columns): two workgroups per CU */
+static uint32_t lt_blocks() {
+    static uint32_t blocks = 0u;
+    if (blocks == 0u) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus < 1)
+            cus = 256;
+        blocks = 2u * (uint32_t)cus;
+    }
+    return blocks;
+}
+
+/* argmax partials per column: one per wave (matvec_mfma_q6k) or per
+ * workgroup (lm_q6k_tiles) */
 extern "C" uint32_t kq_launch_matvec_mfma_waves(uint32_t rows, uint32_t cols) {
+    if (cols == 2048u) return lt_blocks();
     return mv_blocks(rows, cols / 256u) * (uint32_t)kMvWaves;
 }
 
@@ -1945,6 +2222,12 @@ extern "C" hipError_t kq_launch_matvec_mfma(const void *W, uint32_t rows, uint32
                                             uint32_t *status, float *part_v, uint32_t *part_i,
                                             uint32_t part_stride, hipStream_t stream) {
     const uint32_t nb = cols / 256u;
+    if (nb == 8u) {
+        hipLaunchKernelGGL(lm_q6k_tiles, dim3(lt_blocks()), dim3(kLtWaves * 64), 0, stream,
+                           (const uint8_t *)W, rows, x, batch, y, status, part_v, part_i,
+                           part_stride);
+        return hipGetLastError();
+    }
     const uint32_t ns = mv_ns(nb);
     const dim3 grid(mv_blocks(rows, nb)), block(kMvWaves * 64);
 #define KQ_MV(NS)                                                                              \

@@ -423,8 +423,11 @@ def test_matvec_q6k_batched_mfma(ctx, rows, cols, batch, scale):
         b.close()
 
 
-def test_matvec_q6k_batched_mfma_fails_closed(ctx):
-    rows, cols = 65536, 256
+@pytest.mark.parametrize("cols", [256, 2048])
+def test_matvec_q6k_batched_mfma_fails_closed(ctx, cols):
+    # 2,048 columns run on the tile-shared kernel, the other widths on the
+    # per-wave block rings
+    rows = 65536
     w = S.quant_matrix("Q6_K", S.stream_key(S.W_MATVEC_Q6K, 91), rows, cols)
     x = S.normal_f32(S.stream_key(S.W_MATVEC_Q6K, 92), 2 * cols).reshape(2, cols)
     x_bad = x.copy()
